@@ -1,0 +1,105 @@
+/* macai_gdr.h -- C ABI of the MI355X (gfx950) chunked gated delta rule.
+ *
+ * The drop-in boundary of the reference's hot path (macai.gated_delta).  The reference launches four Metal kernels per
+ * training step through torch.mps compiled shaders, `lib.<kernel>(*tensors, *uint_scalars, threads=..., group_size=...)`
+ * (reference src/macai/gated_delta/op.py:71, 159, 217, 234, 241-242), plus the query/key prologue (_norm.py:97, 113).
+ * Each entry point below replaces one of those passes; the caller (PyTorch, through ctypes) owns every buffer,
+ * including the per-chunk scratch, and passes raw device pointers, sizes and the HIP stream (hipStream_t as void*).
+ * The library allocates nothing and keeps no state between calls; every call only enqueues work on `stream`.
+ *
+ * Layouts (all contiguous, row-major):
+ *   q, k        [B, T, H, DK]   dtype (float32 or bfloat16; raw, or already normalised when use_l2norm = 0)
+ *   v, o, dO    [B, T, H, DV]   dtype
+ *   g, beta     [B, T, H]       float32   (g = log decay <= 0)
+ *   states      [B, H, DK, DV]  float32   (initial_state, final state, their gradients)
+ *   per chunk   NT = ceil(T / 64) chunks of 64 tokens, padding rows zero:
+ *     W   [B, H, NT, 64, DK] dtype     W = A diag(beta gamma) K^
+ *     U   [B, H, NT, 64, DV] float32   U = A diag(beta) V
+ *     M   [B, H, NT, 64, 64] dtype     M = (Q^ K^T) * exp(G_i - G_j), lower with the diagonal;  Mt = M^T
+ *     A   [B, H, NT, 64, 64] float32   A = (I + L)^-1;  At = A^T
+ *     Sc, dSn [B, H, NT, DK, DV] float32   state entering each chunk; dLoss/dS_{c+1}
+ *     Vn, dVn [B, H, NT, 64, DV] float32   per-token corrections U - W S_c and their gradient
+ * With use_l2norm = 1 the kernels apply the reference prologue (_norm.py:1-10) themselves: q^ = q * rsqrt(|q|^2 + 1e-6)
+ * * q_scale, k^ = k * rsqrt(|k|^2 + 1e-6), and the backward returns gradients w.r.t. the raw q and k.
+ * Supported widths: DK in {32, 64, 128}; DV a multiple of 32 up to 512.  Pointers must be 16-byte aligned.
+ *
+ * Return value: 0 on success, else an error code below; macai_gdr_last_error() describes the last failure of the
+ * calling thread.  Argument checks run before any launch, so they are testable without a GPU.
+ */
+#ifndef MACAI_GDR_H
+#define MACAI_GDR_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MACAI_GDR_ABI_VERSION 1
+
+/* dtype codes */
+#define MACAI_GDR_F32 0
+#define MACAI_GDR_BF16 1
+
+/* error codes */
+#define MACAI_GDR_OK 0
+#define MACAI_GDR_EINVAL 1  /* bad shape, null or misaligned pointer, inconsistent flags */
+#define MACAI_GDR_EUNSUP 2  /* unsupported head width or dtype */
+#define MACAI_GDR_ELAUNCH 3 /* HIP launch error (hipGetLastError) */
+
+/* state-pass flags (the reference's gdc_fwd flags, _chunked.py:335-338) */
+#define MACAI_GDR_STORE_STATES 1 /* store Sc and Vn for the backward */
+#define MACAI_GDR_NO_OUTPUT 8    /* write neither o nor the final state */
+
+const char* macai_gdr_last_error(void);
+int macai_gdr_abi_version(void);
+
+/* Per-chunk preparation (north star (1), the intra-chunk kernel): G, L, A = (I + L)^-1, W, U, and M and/or Mt when
+ * given, A and At when given.  Replaces `lib.gdc_prep(q, k, g, beta, gc, a, m, kg, T, H, ...)` (reference
+ * op.py:63-72; kernel _chunked.py:220-313) and the fused prologue l2n_fwd (_norm.py:97). */
+int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, const float* beta, void* W, float* U,
+                   void* M, void* Mt, float* A, float* At, int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV,
+                   int32_t dtype, int32_t use_l2norm, float q_scale, void* stream);
+
+/* The sequential state pass (north star (2) + (3)): S <- exp(G_last) S + K^T diag(e) (U - W S) over the chunks from
+ * s0 (NULL = zeros), with the output O = diag(gamma) Q S + M Vn written to o (dtype) unless MACAI_GDR_NO_OUTPUT, the
+ * final state to sT when sT != NULL, and Sc / Vn when MACAI_GDR_STORE_STATES.  split = workgroups per head-row's
+ * value columns (a divisor of DV / 16; 0 = automatic).  Replaces `lib.gdc_fwd(q, k, v, beta, s0, gc, a, m, o, sT, sc,
+ * vn, xu, ckpt, T, H, DV, flags, ...)` (reference op.py:159, 217; kernel _chunked.py:315-659). */
+int macai_gdr_state_fwd(const void* q, const void* k, const float* g, const void* W, const float* U, const void* M,
+                        const float* s0, void* o, float* sT, float* Sc, float* Vn, int64_t B, int64_t T, int64_t H,
+                        int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, int32_t flags,
+                        int32_t split, void* stream);
+
+/* The reverse state pass (north star (4)): from dS_NT = dsT (NULL = zeros) back over the chunks, dVn = M^T dO +
+ * diag(e) K dS, dS <- exp(G_last) dS + (diag(gamma) Q)^T dO - W^T dVn; stores dSn (= dS_{c+1}) and dVn per chunk and
+ * writes ds0 = dLoss/d initial_state.  Replaces `lib.gdc_bwd_state(q, k, beta, do, dsT, gc, a, m, dsn, dvn, ds0, T,
+ * H, DV, ...)` (reference op.py:234; kernel _chunked.py:661-903). */
+int macai_gdr_state_bwd(const void* q, const void* k, const float* g, const void* W, const void* Mt, const void* dO,
+                        const float* dsT, float* dSn, float* dVn, float* ds0, int64_t B, int64_t T, int64_t H,
+                        int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, int32_t split,
+                        void* stream);
+
+/* The per-chunk backward (north star (4)): dq, dk (w.r.t. the raw inputs when use_l2norm), dv in dtype; dg, dbeta in
+ * float32; one writer per element (bitwise deterministic).  Replaces `lib.gdc_bwd_chunk(q, k, beta, do, gc, a, kg, m,
+ * sc, dsn, vn, xu, dvn, dq, dk, dv, dg, dbeta, T, H, DV, ...)` (reference op.py:241-242; kernel
+ * _chunked.py:905-1177) and the prologue's backward l2n_bwd (_norm.py:113). */
+int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float* g, const float* beta, const void* dO,
+                        const float* A, const float* At, const float* Sc, const float* dSn, const float* Vn,
+                        const float* dVn, void* dq, void* dk, void* dv, float* dg, float* dbeta, int64_t B, int64_t T,
+                        int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale,
+                        void* stream);
+
+/* One recurrent step per sequence (T = 1): q, k [B, 1, H, DK], v [B, 1, H, DV] dtype; g, beta [B, 1, H] float32;
+ * s_in, s_out [B, H, DK, DV] float32 (s_out may equal s_in).  S' = e^g S + k beta (v - e^g S^T k)^T, o = S'^T q.  The
+ * math of the reference's recurrence (op.py:308-313) and of transformers' torch_recurrent_gated_delta_rule
+ * (modeling_qwen3_5.py:330-380), which the reference leaves unpatched (patch.py:27-29).  (DK, DV) in {64, 128}^2. */
+int macai_gdr_decode(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                     const float* s_in, void* o, float* s_out, int64_t B, int64_t H, int64_t DK, int64_t DV,
+                     int32_t dtype, int32_t use_l2norm, float q_scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MACAI_GDR_H */

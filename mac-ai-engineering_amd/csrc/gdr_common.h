@@ -1,0 +1,204 @@
+// Device helpers shared by the gated-delta-rule kernels (gfx950 / CDNA4, wave64).
+//
+// MFMA tiles.  Every product is built from 16 x 16 output tiles accumulated in fp32 over 32-deep k-blocks:
+//   * fp32 operands: 8 x v_mfma_f32_16x16x4_f32 per k-block;
+//   * bf16 operands: 1 x v_mfma_f32_16x16x32_bf16 per k-block.
+// Lane l (j = l / 16) holds, for an A operand, row l % 16 and the 8 k-values kmap(j, 0..7); for a B operand, column
+// l % 16 and the same 8 k-values.  kmap(j, r) = 4j + r for r < 4 and 16 + 4j + (r - 4) for r >= 4: the same bijection
+// of the k-block is used for A and B, so any of them gives the product.  It is chosen so that the fp32 accumulator of
+// a 16 x 16 tile (lane l, register r holds D[4j + r][l % 16]) -- two tiles stacked along k -- IS a B-operand fragment
+// (rows = k) and an A-operand fragment of the transpose, with no data movement: the state S and the per-token
+// corrections stay in registers across the sequential chunk loop.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gdr {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int C = 64;          // chunk length (tokens); one wave lane per chunk row in the scans
+constexpr float L2_EPS = 1e-6f; // l2norm epsilon of the reference prologue (_norm.py:17)
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+// ---- scalar conversions -------------------------------------------------------------------------------------------
+__device__ __forceinline__ float to_f(float x) { return x; }
+__device__ __forceinline__ float to_f(bf16 x) { return (float)x; }
+template <typename T> __device__ __forceinline__ T from_f(float x);
+template <> __device__ __forceinline__ float from_f<float>(float x) { return x; }
+template <> __device__ __forceinline__ bf16 from_f<bf16>(float x) { return (bf16)x; }
+
+// ---- fragments ----------------------------------------------------------------------------------------------------
+__device__ __forceinline__ int kmap(int j, int r) { return r < 4 ? 4 * j + r : 12 + 4 * j + r; }
+
+template <typename MT> struct Frag;
+template <> struct Frag<float> {
+  float v[8];
+  __device__ __forceinline__ void set(int r, float x) { v[r] = x; }
+  __device__ __forceinline__ float get(int r) const { return v[r]; }
+};
+template <> struct Frag<bf16> {
+  bf16x8 v;
+  __device__ __forceinline__ void set(int r, float x) { v[r] = (bf16)x; }
+  __device__ __forceinline__ float get(int r) const { return (float)v[r]; }
+};
+
+__device__ __forceinline__ void mma(f4& acc, const Frag<float>& a, const Frag<float>& b) {
+#pragma unroll
+  for (int r = 0; r < 8; ++r) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[r], b.v[r], acc, 0, 0, 0);
+}
+__device__ __forceinline__ void mma(f4& acc, const Frag<bf16>& a, const Frag<bf16>& b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc, 0, 0, 0);
+}
+
+// 4 contiguous values from memory (global or LDS) as floats
+__device__ __forceinline__ f4 load4(const float* p) { return *reinterpret_cast<const f4*>(p); }
+__device__ __forceinline__ f4 load4(const bf16* p) {
+  bf16x4 x = *reinterpret_cast<const bf16x4*>(p);
+  return f4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
+}
+
+// Fragment of a k-contiguous ("row-major along k") matrix X: lane takes row `row0 + l % 16`, k-block at k0.  For an A
+// operand X = A ([m][k]); for a B operand X = B^T ([n][k]).  `scale` multiplies the values before rounding to MT.
+template <typename MT, typename ST>
+__device__ __forceinline__ Frag<MT> frag_k(const ST* base, int pitch, int row0, int k0, float scale = 1.0f) {
+  const int l = lane_id(), j = l >> 4;
+  const ST* p = base + (size_t)(row0 + (l & 15)) * pitch + k0 + 4 * j;
+  f4 lo = load4(p), hi = load4(p + 16);
+  Frag<MT> f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    f.set(r, lo[r] * scale);
+    f.set(r + 4, hi[r] * scale);
+  }
+  return f;
+}
+
+// Specialisation for bf16 LDS/global data feeding bf16 MFMA without a scale: plain 8-byte moves.
+__device__ __forceinline__ Frag<bf16> frag_k_raw(const bf16* base, int pitch, int row0, int k0) {
+  const int l = lane_id(), j = l >> 4;
+  const bf16* p = base + (size_t)(row0 + (l & 15)) * pitch + k0 + 4 * j;
+  bf16x4 lo = *reinterpret_cast<const bf16x4*>(p), hi = *reinterpret_cast<const bf16x4*>(p + 16);
+  Frag<bf16> f;
+  f.v = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return f;
+}
+__device__ __forceinline__ Frag<float> frag_k_raw(const float* base, int pitch, int row0, int k0) {
+  return frag_k<float, float>(base, pitch, row0, k0);
+}
+
+// Fragment from two stacked accumulator tiles (rows 0-15 in `lo`, rows 16-31 in `hi`): B operand with k = the tiles'
+// rows, or A operand of their transpose.
+template <typename MT>
+__device__ __forceinline__ Frag<MT> frag_acc(const f4& lo, const f4& hi, float scale = 1.0f) {
+  Frag<MT> f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    f.set(r, lo[r] * scale);
+    f.set(r + 4, hi[r] * scale);
+  }
+  return f;
+}
+
+// hi/lo split of fp32 values for bf16 MFMA: x = hi + lo with both representable in bf16 (relative residual ~2^-16)
+template <typename MT>
+__device__ __forceinline__ void frag_split(const Frag<float>& x, Frag<MT>& hi, Frag<MT>& lo) {
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    float h = (float)from_f<MT>(x.v[r]);
+    hi.set(r, h);
+    lo.set(r, x.v[r] - h);
+  }
+}
+
+// fp32 fragment of a k-contiguous fp32 matrix (no rounding), for split products
+__device__ __forceinline__ Frag<float> frag_k_f32(const float* base, int pitch, int row0, int k0) {
+  return frag_k<float, float>(base, pitch, row0, k0);
+}
+
+// ---- wave-level scans and reductions -------------------------------------------------------------------------------
+__device__ __forceinline__ float wave_incl_scan(float x) {
+  const int l = lane_id();
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    float y = __shfl_up(x, off, 64);
+    if (l >= off) x += y;
+  }
+  return x;
+}
+// sum over the 16 lanes of a lane group (lanes with equal l / 16), result in every lane of the group
+__device__ __forceinline__ float group16_sum(float x) {
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+// sum over lanes with equal l % 16 (the 4 lane groups), result in every lane
+__device__ __forceinline__ float across_groups_sum(float x) {
+  x += __shfl_xor(x, 16, 64);
+  x += __shfl_xor(x, 32, 64);
+  return x;
+}
+
+// ---- chunk scalars ------------------------------------------------------------------------------------------------
+// One wave: lane t = chunk row t.  g is the log decay (0 on padding rows).  Writes G (in-chunk cumulative log decay),
+// gam = exp(G), e = exp(G_last - G) for the 64 rows into LDS; G_last = G[63] (padding rows add 0).
+struct ChunkScalars {
+  float G[C];
+  float gam[C];
+  float e[C];
+  float beta[C];
+};
+
+__device__ __forceinline__ void chunk_scalars(ChunkScalars& cs, const float* g, const float* beta, size_t row_base,
+                                              size_t row_stride, int t0, int T) {
+  const int l = lane_id();
+  const int t = t0 + l;
+  float gv = 0.f, bv = 0.f;
+  if (t < T) {
+    gv = g[row_base + (size_t)t * row_stride];
+    if (beta) bv = beta[row_base + (size_t)t * row_stride];
+  }
+  float G = wave_incl_scan(gv);
+  float Gl = __shfl(G, 63, 64);
+  cs.G[l] = G;
+  cs.gam[l] = expf(G);
+  cs.e[l] = expf(Gl - G);
+  cs.beta[l] = bv;
+}
+
+// ---- row norms ----------------------------------------------------------------------------------------------------
+// Inverse l2 norm of chunk rows: rinv = 1 / sqrt(sum x^2 + eps).  Every kernel computes it with this one routine: a row
+// is summed by the 16 lanes of a lane group, each over D/16 consecutive elements in order, then a fixed butterfly, so
+// all kernels produce the same bits.  A wave handles rows w*4 + (l/16), stepping by 4 * nwaves.
+template <typename IT, int D>
+__device__ __forceinline__ void row_rnorms(float* out, const IT* x, size_t row_base, size_t row_stride, int t0, int T,
+                                           int nwaves) {
+  const int l = lane_id(), w = wave_id();
+  constexpr int PER = D / 16;
+  for (int r0 = w * 4; r0 < C; r0 += 4 * nwaves) {
+    const int r = r0 + (l >> 4);
+    const int t = t0 + r;
+    float ss = 0.f;
+    if (t < T) {
+      const IT* p = x + row_base + (size_t)t * row_stride + (l & 15) * PER;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        float v = to_f(p[i]);
+        ss = fmaf(v, v, ss);
+      }
+    }
+    ss = group16_sum(ss);
+    if ((l & 15) == 0) out[r] = (t < T) ? 1.0f / sqrtf(ss + L2_EPS) : 0.f;
+  }
+}
+
+// ---- global I/O helpers -------------------------------------------------------------------------------------------
+template <typename T> __device__ __forceinline__ void store(T* p, float x) { *p = from_f<T>(x); }
+
+}  // namespace gdr

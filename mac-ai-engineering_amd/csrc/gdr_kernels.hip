@@ -1,0 +1,1174 @@
+// The chunked gated delta rule for MI355X (gfx950): forward, backward and the one-token decode step.
+//
+// Kernels (one launch each; C = 64-token chunks; MT = MFMA operand type: fp32 for fp32 inputs, bf16 for bf16 inputs;
+// accumulation, the state, decays and the triangular inverse always fp32):
+//   prep_kernel       one workgroup per (chunk, head, batch row), all independent.  G (in-chunk cumulative log decay),
+//                     L = strictLower(diag(beta) (K K^T) * exp(G_i - G_j)), A = (I + L)^-1 by substitution on 16 x 16
+//                     diagonal blocks and block products, W = A diag(beta gamma) K, U = A diag(beta) V, and
+//                     M = (Q K^T) * exp(G_i - G_j) (lower with the diagonal).  Replaces the reference's gdc_prep
+//                     (/root/reference/src/macai/gated_delta/_chunked.py:220-313), which keeps A and forms no W/U.
+//   state_fwd_kernel  one wave per 16 value columns of a head-row, sequential over chunks, the fp32 state S in MFMA
+//                     accumulators: Vn = U - W S; O = diag(gamma) Q S + M Vn; S <- exp(G_last) S + K^T diag(e) Vn.
+//                     Optionally stores S_c and Vn for the backward (the recompute pass).  Replaces gdc_fwd
+//                     (_chunked.py:315-659, flags 1 / 8).
+//   state_bwd_kernel  the reverse pass on the same grid, dS in accumulators: dVn = M^T dO + diag(e) K dS;
+//                     dS <- exp(G_last) dS + (diag(gamma) Q)^T dO - W^T dVn; stores dS_{c+1}, dVn; writes dS_0.
+//                     Replaces gdc_bwd_state (_chunked.py:661-903).
+//   chunk_bwd_kernel  one workgroup per (chunk, head, batch row): dq, dk, dv, dg, dbeta with one writer per element
+//                     (no atomics), dg in the no-cancellation form, the l2norm prologue's backward fused.  Replaces
+//                     gdc_bwd_chunk (_chunked.py:905-1177) and l2n_bwd (_norm.py:44-57).
+//   decode_kernel     one token per sequence (T = 1): S' = e^g S + k beta (v - e^g k^T S)^T, o = S'^T q, one
+//                     workgroup per head-row streaming the fp32 state once.  The math of op.py:308-313.
+// Equations: _chunked.py:1-35; docs/prior_art_gated_delta.md:132-195 of the reference.
+#include <hip/hip_runtime.h>
+#include <stdio.h>
+#include <string.h>
+#include <stdarg.h>
+
+#include "gdr_common.h"
+#include "gdr_stage.h"
+#include "macai_gdr.h"
+
+namespace gdr {
+
+// ---------------------------------------------------------------------------------------------------------------------
+// argument blocks (device side)
+// ---------------------------------------------------------------------------------------------------------------------
+struct PrepArgs {
+  const void *q, *k, *v;
+  const float *g, *beta;
+  void* W;       // [B,H,NT,C,DK] MT   W = A diag(beta gamma) K^
+  float* U;      // [B,H,NT,C,DV] fp32 U = A diag(beta) V
+  void* M;       // [B,H,NT,C,C]  MT   M (row-major [t][s]) or null
+  void* Mt;      // [B,H,NT,C,C]  MT   M^T ([s][t]) or null
+  float* A;      // [B,H,NT,C,C]  fp32 A or null
+  float* At;     // [B,H,NT,C,C]  fp32 A^T or null
+  int B, T, H, DV, NT;
+  int l2norm;
+  float q_scale;
+};
+
+struct StateFwdArgs {
+  const void *q, *k;
+  const float* g;
+  const void* W;
+  const float* U;
+  const void* M;
+  const float* s0;
+  void* o;
+  float* sT;
+  float* Sc;     // [B,H,NT,DK,DV]
+  float* Vn;     // [B,H,NT,C,DV]
+  int B, T, H, DV, NT;
+  int l2norm;
+  float q_scale;
+  int nslice;    // workgroups per head-row
+};
+
+struct StateBwdArgs {
+  const void *q, *k;
+  const float* g;
+  const void* W;
+  const void* Mt;
+  const void* dO;
+  const float* dsT;
+  float* dSn;    // [B,H,NT,DK,DV]  dS_{c+1}
+  float* dVn;    // [B,H,NT,C,DV]
+  float* ds0;    // [B,H,DK,DV]
+  int B, T, H, DV, NT;
+  int l2norm;
+  float q_scale;
+  int nslice;
+};
+
+struct ChunkBwdArgs {
+  const void *q, *k, *v;
+  const float *g, *beta;
+  const void* dO;
+  const float *A, *At, *Sc, *dSn, *Vn, *dVn;
+  void *dq, *dk, *dv;
+  float *dg, *dbeta;
+  int B, T, H, DV, NT;
+  int l2norm;
+  float q_scale;
+};
+
+struct DecodeArgs {
+  const void *q, *k, *v;
+  const float *g, *beta, *s_in;
+  void* o;
+  float* s_out;
+  int B, H;
+  int l2norm;
+  float q_scale;
+};
+
+template <typename MT>
+__device__ __forceinline__ Frag<MT> cvt(const Frag<float>& x, float s = 1.0f) {
+  Frag<MT> f;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) f.set(r, x.v[r] * s);
+  return f;
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// prep: G, L, A = (I + L)^-1, W, U, M per chunk
+// ---------------------------------------------------------------------------------------------------------------------
+template <typename IT, typename MT, int DK>
+__global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
+  constexpr int KP = DK + 8;   // pitch of [C][DK] tiles (elements)
+  constexpr int CP = C + 8;    // pitch of [*][C] MT tiles
+  constexpr int FP = C + 4;    // pitch of fp32 [C][C] tiles
+  constexpr int QSZ = (C * KP > DK * CP) ? C * KP : DK * CP;
+  constexpr int KSZ = (C * KP > C * CP) ? C * KP : C * CP;
+  __shared__ __attribute__((aligned(16))) MT sK[KSZ];    // K^ rows; then (beta V)^T column blocks
+  __shared__ __attribute__((aligned(16))) MT sQ[QSZ];    // Q^ rows; then (beta gamma K^)^T
+  __shared__ __attribute__((aligned(16))) float sL[C * FP];
+  __shared__ __attribute__((aligned(16))) float sA[C * FP];
+  __shared__ ChunkScalars cs;
+  __shared__ float rk[C], rq[C];
+
+  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int T = a.T, H = a.H, DV = a.DV, NT = a.NT;
+  const int t0 = c * C;
+  const int l = lane_id(), w = wave_id(), j = l >> 4;
+  const size_t qk_base = ((size_t)b * T * H + h) * DK, qk_pitch = (size_t)H * DK;
+  const size_t v_base = ((size_t)b * T * H + h) * DV, v_pitch = (size_t)H * DV;
+  const size_t s_base = (size_t)b * T * H + h;
+  const size_t bhc = ((size_t)b * H + h) * NT + c;
+  const IT* q = (const IT*)a.q + qk_base;
+  const IT* k = (const IT*)a.k + qk_base;
+  const IT* v = (const IT*)a.v + v_base;
+  const bool wantM = a.M != nullptr || a.Mt != nullptr;
+
+  if (w == 0) chunk_scalars(cs, a.g, a.beta, s_base, H, t0, T);
+  if (a.l2norm) {
+    row_rnorms<IT, DK>(rk, (const IT*)a.k, qk_base, qk_pitch, t0, T, 4);
+    if (wantM) row_rnorms<IT, DK>(rq, (const IT*)a.q, qk_base, qk_pitch, t0, T, 4);
+  } else if (threadIdx.x < C) {
+    rk[threadIdx.x] = 1.f;
+    rq[threadIdx.x] = 1.f;
+  }
+  __syncthreads();
+  stage_rows<MT, IT>(sK, KP, k, qk_pitch, t0, T, DK, [&](int r) { return rk[r]; });
+  if (wantM) stage_rows<MT, IT>(sQ, KP, q, qk_pitch, t0, T, DK, [&](int r) { return rq[r] * a.q_scale; });
+  __syncthreads();
+
+  // K K^T and Q K^T on the lower 16 x 16 tiles: wave w owns row block w.  L (strictly lower, fp32) into LDS; M out.
+  {
+    const int mi = w;
+    for (int ni = 0; ni < 4; ++ni) {
+      f4 kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
+      if (ni <= mi) {
+#pragma unroll
+        for (int p = 0; p < DK / 32; ++p) {
+          Frag<MT> bk = frag_k_raw(sK, KP, 16 * ni, 32 * p);
+          Frag<MT> ak = frag_k_raw(sK, KP, 16 * mi, 32 * p);
+          mma(kk, ak, bk);
+          if (wantM) {
+            Frag<MT> aq = frag_k_raw(sQ, KP, 16 * mi, 32 * p);
+            mma(qk, aq, bk);
+          }
+        }
+      }
+      const int col = 16 * ni + (l & 15);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * mi + 4 * j + r;
+        const float gm = (row >= col) ? expf(cs.G[row] - cs.G[col]) : 0.f;   // mask before the exponent
+        sL[row * FP + col] = (row > col) ? cs.beta[row] * kk[r] * gm : 0.f;
+        if (wantM) {
+          const MT mv = from_f<MT>((row >= col) ? qk[r] * gm : 0.f);
+          if (a.M) ((MT*)a.M)[bhc * C * C + row * C + col] = mv;
+          if (a.Mt) ((MT*)a.Mt)[bhc * C * C + col * C + row] = mv;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // (beta gamma K^)^T for W, from the raw keys (one rounding)
+  stage_rows_T<MT, IT>(sQ, CP, k, qk_pitch, t0, T, DK, [&](int r) { return rk[r] * cs.beta[r] * cs.gam[r]; });
+
+  // A = (I + L)^-1.  Diagonal 16 x 16 blocks by forward substitution: wave 0, lane = (block l/16, column l%16).
+  if (w == 0) {
+    const int bb = l >> 4, cc = l & 15;
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float s = (i == cc) ? 1.f : 0.f;
+      const float* Lr = sL + (16 * bb + i) * FP + 16 * bb;
+#pragma unroll
+      for (int m = 0; m < i; ++m) s = fmaf(-Lr[m], x[m], s);
+      x[i] = s;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sA[(16 * bb + i) * FP + 16 * bb + cc] = x[i];
+  }
+  for (int i = threadIdx.x; i < C * C; i += blockDim.x) {
+    const int row = i / C, col = i % C;
+    if ((col >> 4) > (row >> 4)) sA[row * FP + col] = 0.f;
+  }
+  __syncthreads();
+  // blocks below the diagonal, one block-distance at a time: A_ij = -A_ii sum_{m=j}^{i-1} L_im A_mj (fp32 MFMA)
+  for (int dist = 1; dist < 4; ++dist) {
+    if (w < 4 - dist) {
+      const int bi = w + dist, bj = w;
+      f4 t = {0.f, 0.f, 0.f, 0.f};
+      for (int m = bj; m < bi; ++m) {
+#pragma unroll
+        for (int kk = 0; kk < 16; kk += 4)
+          t = __builtin_amdgcn_mfma_f32_16x16x4f32(sL[(16 * bi + (l & 15)) * FP + 16 * m + kk + j],
+                                                   sA[(16 * m + kk + j) * FP + 16 * bj + (l & 15)], t, 0, 0, 0);
+      }
+      f4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        o = __builtin_amdgcn_mfma_f32_16x16x4f32(sA[(16 * bi + (l & 15)) * FP + 16 * bi + 4 * j + r], t[r], o, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sA[(16 * bi + 4 * j + r) * FP + 16 * bj + (l & 15)] = -o[r];
+    }
+    __syncthreads();
+  }
+
+  // W = A (beta gamma K^): wave w owns row block w; A is lower triangular, so k-blocks above the row block are zero
+  {
+    Frag<MT> af[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) af[p] = cvt<MT>(frag_k_f32(sA, FP, 16 * w, 32 * p));
+    const int np = (16 * w + 15) / 32 + 1;
+    MT* Wc = (MT*)a.W + bhc * C * DK;
+    for (int ni = 0; ni < DK / 16; ++ni) {
+      f4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int p = 0; p < np; ++p) mma(acc, af[p], frag_k_raw(sQ, CP, 16 * ni, 32 * p));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Wc[(16 * w + 4 * j + r) * DK + 16 * ni + (l & 15)] = from_f<MT>(acc[r]);
+    }
+    // U = A (beta V), 64 value columns at a time staged transposed in sK
+    float* Uc = a.U + bhc * C * DV;
+    for (int vb = 0; vb < DV; vb += 64) {
+      const int nv = (DV - vb < 64) ? DV - vb : 64;
+      __syncthreads();
+      stage_rows_T<MT, IT>(sK, CP, v + vb, v_pitch, t0, T, nv, [&](int r) { return cs.beta[r]; });
+      __syncthreads();
+      for (int ni = 0; ni < nv / 16; ++ni) {
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int p = 0; p < np; ++p) mma(acc, af[p], frag_k_raw(sK, CP, 16 * ni, 32 * p));
+#pragma unroll
+        for (int r = 0; r < 4; ++r) Uc[(16 * w + 4 * j + r) * DV + vb + 16 * ni + (l & 15)] = acc[r];
+      }
+    }
+  }
+  if (a.A) {
+    float* Ag = a.A + bhc * C * C;
+    float* Atg = a.At + bhc * C * C;
+    for (int i = threadIdx.x; i < C * C; i += blockDim.x) {
+      const int row = i / C, col = i % C;
+      const float x = sA[row * FP + col];
+      Ag[row * C + col] = x;
+      Atg[col * C + row] = x;
+    }
+  }
+}
+
+// XCD-aware map of a flat workgroup id to (head-row, column slice): the slices of one head-row share an XCD (and its
+// L2), since consecutive workgroup ids go to consecutive XCDs.  Returns false for the padding workgroups.
+__device__ __forceinline__ bool state_map(int nslice, int HR, int& hr, int& slice) {
+  const int f = blockIdx.x, xcd = f & 7, kx = f >> 3;
+  hr = (kx / nslice) * 8 + xcd;
+  slice = kx % nslice;
+  return hr < HR;
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// the forward state pass (+ output), sequential over chunks
+// ---------------------------------------------------------------------------------------------------------------------
+template <typename IT, typename MT, int DK, bool OUT, bool STORE>
+__global__ void __launch_bounds__(512) state_fwd_kernel(StateFwdArgs a) {
+  constexpr int KP = DK + 8, CP = C + 8, ND = DK / 16;
+  __shared__ __attribute__((aligned(16))) MT sW[C * KP];
+  __shared__ __attribute__((aligned(16))) MT sKeT[DK * CP];
+  __shared__ __attribute__((aligned(16))) MT sQg[OUT ? C * KP : 8];
+  __shared__ __attribute__((aligned(16))) MT sM[OUT ? C * CP : 8];
+  __shared__ ChunkScalars cs;
+  __shared__ float rk[C], rq[C];
+
+  const int T = a.T, H = a.H, DV = a.DV, NT = a.NT;
+  int hr, slice;
+  if (!state_map(a.nslice, a.B * H, hr, slice)) return;
+  const int b = hr / H, h = hr % H;
+  const int nw = blockDim.x >> 6;
+  const int l = lane_id(), w = wave_id(), j = l >> 4;
+  const int v0 = (slice * nw + w) * 16;
+  const int col = v0 + (l & 15);
+  const size_t qk_base = ((size_t)b * T * H + h) * DK, qk_pitch = (size_t)H * DK;
+  const size_t o_base = ((size_t)b * T * H + h) * DV, o_pitch = (size_t)H * DV;
+  const size_t s_base = (size_t)b * T * H + h;
+  const IT* q = (const IT*)a.q + qk_base;
+  const IT* k = (const IT*)a.k + qk_base;
+
+  f4 S[ND];
+#pragma unroll
+  for (int di = 0; di < ND; ++di)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      S[di][r] = a.s0 ? a.s0[(size_t)hr * DK * DV + (16 * di + 4 * j + r) * DV + col] : 0.f;
+
+  for (int c = 0; c < NT; ++c) {
+    const int t0 = c * C;
+    const size_t bhc = (size_t)hr * NT + c;
+    if (w == 0) chunk_scalars(cs, a.g, nullptr, s_base, H, t0, T);
+    if (a.l2norm) {
+      row_rnorms<IT, DK>(rk, (const IT*)a.k, qk_base, qk_pitch, t0, T, nw);
+      if (OUT) row_rnorms<IT, DK>(rq, (const IT*)a.q, qk_base, qk_pitch, t0, T, nw);
+    } else if (threadIdx.x < C) {
+      rk[threadIdx.x] = 1.f;
+      rq[threadIdx.x] = 1.f;
+    }
+    __syncthreads();
+    stage_copy<MT>(sW, KP, (const MT*)a.W + bhc * C * DK, C, DK);
+    stage_rows_T<MT, IT>(sKeT, CP, k, qk_pitch, t0, T, DK, [&](int r) { return rk[r] * cs.e[r]; });
+    if (OUT) {
+      stage_rows<MT, IT>(sQg, KP, q, qk_pitch, t0, T, DK, [&](int r) { return rq[r] * a.q_scale * cs.gam[r]; });
+      stage_copy<MT>(sM, CP, (const MT*)a.M + bhc * C * C, C, C);
+    }
+    __syncthreads();
+
+    // S as the B operand (k = state rows)
+    Frag<MT> Sf[ND / 2];
+#pragma unroll
+    for (int p = 0; p < ND / 2; ++p) Sf[p] = frag_acc<MT>(S[2 * p], S[2 * p + 1]);
+    // Vn = U - W S
+    f4 Vn[4];
+    const float* Uc = a.U + bhc * C * DV;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p = 0; p < ND / 2; ++p) mma(acc, frag_k_raw(sW, KP, 16 * mi, 32 * p), Sf[p]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Vn[mi][r] = Uc[(16 * mi + 4 * j + r) * DV + col] - acc[r];
+    }
+    if (STORE) {
+      float* Scc = a.Sc + bhc * DK * DV;
+#pragma unroll
+      for (int di = 0; di < ND; ++di)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) Scc[(16 * di + 4 * j + r) * DV + col] = S[di][r];
+      float* Vnc = a.Vn + bhc * C * DV;
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) Vnc[(16 * mi + 4 * j + r) * DV + col] = Vn[mi][r];
+    }
+    Frag<MT> Vf[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) Vf[p] = frag_acc<MT>(Vn[2 * p], Vn[2 * p + 1]);
+    if (OUT) {
+      // O = diag(gamma) Q S + M Vn (M lower triangular: k-blocks past the row block are zero)
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int p = 0; p < ND / 2; ++p) mma(acc, frag_k_raw(sQg, KP, 16 * mi, 32 * p), Sf[p]);
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+          if (32 * p <= 16 * mi + 15) mma(acc, frag_k_raw(sM, CP, 16 * mi, 32 * p), Vf[p]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = t0 + 16 * mi + 4 * j + r;
+          if (t < T) ((IT*)a.o)[o_base + (size_t)t * o_pitch + col] = from_f<IT>(acc[r]);
+        }
+      }
+    }
+    // S <- exp(G_last) S + (diag(e) K)^T Vn
+    const float gl = cs.gam[C - 1];
+#pragma unroll
+    for (int di = 0; di < ND; ++di) {
+      f4 acc = S[di] * gl;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) mma(acc, frag_k_raw(sKeT, CP, 16 * di, 32 * p), Vf[p]);
+      S[di] = acc;
+    }
+    __syncthreads();
+  }
+  if (a.sT) {
+#pragma unroll
+    for (int di = 0; di < ND; ++di)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) a.sT[(size_t)hr * DK * DV + (16 * di + 4 * j + r) * DV + col] = S[di][r];
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// the reverse state pass
+// ---------------------------------------------------------------------------------------------------------------------
+template <typename IT, typename MT, int DK>
+__global__ void __launch_bounds__(512) state_bwd_kernel(StateBwdArgs a) {
+  constexpr int KP = DK + 8, CP = C + 8, ND = DK / 16;
+  __shared__ __attribute__((aligned(16))) MT sKe[C * KP];     // diag(e) K^ rows
+  __shared__ __attribute__((aligned(16))) MT sQgT[DK * CP];   // (diag(gamma) Q^)^T
+  __shared__ __attribute__((aligned(16))) MT sWT[DK * CP];    // W^T
+  __shared__ __attribute__((aligned(16))) MT sMT[C * CP];     // M^T
+  __shared__ ChunkScalars cs;
+  __shared__ float rk[C], rq[C];
+
+  const int T = a.T, H = a.H, DV = a.DV, NT = a.NT;
+  int hr, slice;
+  if (!state_map(a.nslice, a.B * H, hr, slice)) return;
+  const int b = hr / H, h = hr % H;
+  const int nw = blockDim.x >> 6;
+  const int l = lane_id(), w = wave_id(), j = l >> 4;
+  const int v0 = (slice * nw + w) * 16;
+  const int col = v0 + (l & 15);
+  const size_t qk_base = ((size_t)b * T * H + h) * DK, qk_pitch = (size_t)H * DK;
+  const size_t o_base = ((size_t)b * T * H + h) * DV, o_pitch = (size_t)H * DV;
+  const size_t s_base = (size_t)b * T * H + h;
+  const IT* q = (const IT*)a.q + qk_base;
+  const IT* k = (const IT*)a.k + qk_base;
+  const IT* dO = (const IT*)a.dO + o_base;
+
+  f4 dS[ND];
+#pragma unroll
+  for (int di = 0; di < ND; ++di)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      dS[di][r] = a.dsT ? a.dsT[(size_t)hr * DK * DV + (16 * di + 4 * j + r) * DV + col] : 0.f;
+
+  for (int c = NT - 1; c >= 0; --c) {
+    const int t0 = c * C;
+    const size_t bhc = (size_t)hr * NT + c;
+    if (w == 0) chunk_scalars(cs, a.g, nullptr, s_base, H, t0, T);
+    if (a.l2norm) {
+      row_rnorms<IT, DK>(rk, (const IT*)a.k, qk_base, qk_pitch, t0, T, nw);
+      row_rnorms<IT, DK>(rq, (const IT*)a.q, qk_base, qk_pitch, t0, T, nw);
+    } else if (threadIdx.x < C) {
+      rk[threadIdx.x] = 1.f;
+      rq[threadIdx.x] = 1.f;
+    }
+    __syncthreads();
+    stage_rows<MT, IT>(sKe, KP, k, qk_pitch, t0, T, DK, [&](int r) { return rk[r] * cs.e[r]; });
+    stage_rows_T<MT, IT>(sQgT, CP, q, qk_pitch, t0, T, DK, [&](int r) { return rq[r] * a.q_scale * cs.gam[r]; });
+    stage_copy_T<MT>(sWT, CP, (const MT*)a.W + bhc * C * DK, C, DK);
+    stage_copy<MT>(sMT, CP, (const MT*)a.Mt + bhc * C * C, C, C);
+    __syncthreads();
+
+    Frag<MT> Of[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) Of[p] = frag_rows<MT, IT>(dO, o_pitch, t0, T, 32 * p, col, One());
+    Frag<MT> Sf[ND / 2];
+#pragma unroll
+    for (int p = 0; p < ND / 2; ++p) Sf[p] = frag_acc<MT>(dS[2 * p], dS[2 * p + 1]);
+    // dVn = M^T dO + diag(e) K^ dS   (M^T upper triangular: k-blocks before the row block are zero)
+    f4 dV[4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+        if (32 * p + 31 >= 16 * mi) mma(acc, frag_k_raw(sMT, CP, 16 * mi, 32 * p), Of[p]);
+#pragma unroll
+      for (int p = 0; p < ND / 2; ++p) mma(acc, frag_k_raw(sKe, KP, 16 * mi, 32 * p), Sf[p]);
+      dV[mi] = acc;
+    }
+    {
+      float* dSc = a.dSn + bhc * DK * DV;
+#pragma unroll
+      for (int di = 0; di < ND; ++di)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dSc[(16 * di + 4 * j + r) * DV + col] = dS[di][r];
+      float* dVc = a.dVn + bhc * C * DV;
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dVc[(16 * mi + 4 * j + r) * DV + col] = dV[mi][r];
+    }
+    Frag<MT> Vf[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) Vf[p] = frag_acc<MT>(dV[2 * p], dV[2 * p + 1], -1.f);
+    // dS <- exp(G_last) dS + (diag(gamma) Q^)^T dO - W^T dVn
+    const float gl = cs.gam[C - 1];
+#pragma unroll
+    for (int di = 0; di < ND; ++di) {
+      f4 acc = dS[di] * gl;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        mma(acc, frag_k_raw(sQgT, CP, 16 * di, 32 * p), Of[p]);
+        mma(acc, frag_k_raw(sWT, CP, 16 * di, 32 * p), Vf[p]);
+      }
+      dS[di] = acc;
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int di = 0; di < ND; ++di)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) a.ds0[(size_t)hr * DK * DV + (16 * di + 4 * j + r) * DV + col] = dS[di][r];
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// the per-chunk backward: dq, dk, dv, dg, dbeta
+// ---------------------------------------------------------------------------------------------------------------------
+enum { P_QD = 0, P_E, P_KX, P_R1, P_R2, P_VY, P_DQ, P_DK, NPART };
+
+template <typename IT, typename MT, int DK>
+__global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
+  constexpr int KP = DK + 8, CP = C + 8, FP = C + 4;
+  constexpr int NBD = DK / 16;            // 16-column blocks of the key width
+  constexpr int NBW = (NBD + 3) / 4;      // most blocks a wave owns
+  __shared__ __attribute__((aligned(16))) MT sdW[C * KP];   // dW = -dVn S_c^T
+  __shared__ __attribute__((aligned(16))) MT sdM[C * CP];   // dM = Gamma * (dO Vn^T)
+  __shared__ __attribute__((aligned(16))) MT sdMT[C * CP];  // dM^T
+  __shared__ __attribute__((aligned(16))) MT sZ[C * CP];    // Z = diag(beta) P + (diag(beta) P)^T
+  __shared__ __attribute__((aligned(16))) float sdA[C * FP];
+  __shared__ ChunkScalars cs;
+  __shared__ float rk[C], rq[C];
+  __shared__ float part[NPART][4][C];
+  __shared__ float partS[4];
+  __shared__ float colR1[C], colR2b[C];
+
+  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int T = a.T, H = a.H, DV = a.DV, NT = a.NT;
+  const int t0 = c * C;
+  const int l = lane_id(), w = wave_id(), j = l >> 4;
+  const size_t qk_base = ((size_t)b * T * H + h) * DK, qk_pitch = (size_t)H * DK;
+  const size_t v_base = ((size_t)b * T * H + h) * DV, v_pitch = (size_t)H * DV;
+  const size_t s_base = (size_t)b * T * H + h;
+  const size_t bhc = ((size_t)b * H + h) * NT + c;
+  const IT* q = (const IT*)a.q + qk_base;
+  const IT* k = (const IT*)a.k + qk_base;
+  const IT* v = (const IT*)a.v + v_base;
+  const IT* dO = (const IT*)a.dO + v_base;
+  const float* Scc = a.Sc + bhc * DK * DV;
+  const float* dSc = a.dSn + bhc * DK * DV;
+  const float* Vnc = a.Vn + bhc * C * DV;
+  const float* dVc = a.dVn + bhc * C * DV;
+  const float* Ac = a.A + bhc * C * C;
+  const float* Atc = a.At + bhc * C * C;
+  const float qs = a.q_scale;
+
+  if (w == 0) chunk_scalars(cs, a.g, a.beta, s_base, H, t0, T);
+  if (a.l2norm) {
+    row_rnorms<IT, DK>(rk, (const IT*)a.k, qk_base, qk_pitch, t0, T, 4);
+    row_rnorms<IT, DK>(rq, (const IT*)a.q, qk_base, qk_pitch, t0, T, 4);
+  } else if (threadIdx.x < C) {
+    rk[threadIdx.x] = 1.f;
+    rq[threadIdx.x] = 1.f;
+  }
+  __syncthreads();
+  auto qrow = [&](int r) { return rq[r] * qs; };
+  auto krow = [&](int r) { return rk[r]; };
+
+  // ---- B: products with the chunk states; wave w owns key-column blocks w, w + 4, ...
+  f4 dQ[NBW][4], dK[NBW][4];
+  float pQD[4][4], pE[4][4], pKX[4][4];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pQD[mi][r] = pE[mi][r] = pKX[mi][r] = 0.f;
+  float sds = 0.f;
+#pragma unroll
+  for (int ib = 0; ib < NBW; ++ib) {
+    const int nb = w + 4 * ib;
+    if (nb >= NBD) break;
+    const int d0 = 16 * nb, d = d0 + (l & 15);
+    f4 aO[4], aV[4], aD[4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) aO[mi] = aV[mi] = aD[mi] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb < DV / 32; ++kb) {
+      const Frag<float> s32 = frag_k_f32(Scc, DV, d0, 32 * kb);
+      const Frag<float> d32 = frag_k_f32(dSc, DV, d0, 32 * kb);
+#pragma unroll
+      for (int r = 0; r < 8; ++r) sds = fmaf(s32.v[r], d32.v[r], sds);
+      const Frag<MT> bS = cvt<MT>(s32), bD = cvt<MT>(d32);
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+        mma(aO[mi], frag_k_seq<MT, IT>(dO, v_pitch, t0, T, 16 * mi, 32 * kb, One()), bS);
+        mma(aV[mi], frag_k<MT, float>(Vnc, DV, 16 * mi, 32 * kb), bD);
+        mma(aD[mi], frag_k<MT, float>(dVc, DV, 16 * mi, 32 * kb), bS);
+      }
+    }
+    float kv[4][4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * mi + 4 * j + r, t = t0 + row;
+        const float qv = (t < T) ? to_f(q[(size_t)t * qk_pitch + d]) * rq[row] * qs : 0.f;
+        kv[mi][r] = (t < T) ? to_f(k[(size_t)t * qk_pitch + d]) * rk[row] : 0.f;
+        const float oq = aO[mi][r] * cs.gam[row];
+        dQ[ib][mi][r] = oq;
+        pQD[mi][r] = fmaf(qv, oq, pQD[mi][r]);
+        const float ve = aV[mi][r] * cs.e[row];
+        dK[ib][mi][r] = ve;
+        pE[mi][r] = fmaf(kv[mi][r], ve, pE[mi][r]);
+        sdW[row * KP + d] = from_f<MT>(-aD[mi][r]);
+      }
+    // X = A^T dW = -A^T (dVn S_c^T)   (A^T upper triangular)
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      f4 x = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+        if (32 * p + 31 >= 16 * mi)
+          mma(x, frag_k<MT, float>(Atc, C, 16 * mi, 32 * p), frag_acc<MT>(aD[2 * p], aD[2 * p + 1], -1.f));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * mi + 4 * j + r;
+        dK[ib][mi][r] = fmaf(cs.beta[row] * cs.gam[row], x[r], dK[ib][mi][r]);
+        pKX[mi][r] = fmaf(kv[mi][r], x[r], pKX[mi][r]);
+      }
+    }
+  }
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float s1 = group16_sum(pQD[mi][r]), s2 = group16_sum(pE[mi][r]), s3 = group16_sum(pKX[mi][r]);
+      if ((l & 15) == 0) {
+        const int row = 16 * mi + 4 * j + r;
+        part[P_QD][w][row] = s1;
+        part[P_E][w][row] = s2;
+        part[P_KX][w][row] = s3;
+      }
+    }
+  sds = across_groups_sum(group16_sum(sds));
+  if (l == 0) partS[w] = sds;
+  __syncthreads();
+
+  // ---- C: the C x C products; wave w owns column block cb = w of every C x C matrix
+  const int cb = w, s = 16 * cb + (l & 15);
+  f4 QK[4], KK[4], dOV[4], Ta[4], Tb[4];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) QK[mi] = KK[mi] = dOV[mi] = Ta[mi] = Tb[mi] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int p = 0; p < DK / 32; ++p) {
+    const Frag<MT> bk = frag_k_seq<MT, IT>(k, qk_pitch, t0, T, 16 * cb, 32 * p, krow);
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      mma(QK[mi], frag_k_seq<MT, IT>(q, qk_pitch, t0, T, 16 * mi, 32 * p, qrow), bk);
+      mma(KK[mi], frag_k_seq<MT, IT>(k, qk_pitch, t0, T, 16 * mi, 32 * p, krow), bk);
+      mma(Ta[mi], frag_k_raw(sdW, KP, 16 * mi, 32 * p), bk);
+    }
+  }
+  for (int kb = 0; kb < DV / 32; ++kb) {
+    const Frag<MT> bvn = frag_k<MT, float>(Vnc, DV, 16 * cb, 32 * kb);
+    const Frag<MT> bv = frag_k_seq<MT, IT>(v, v_pitch, t0, T, 16 * cb, 32 * kb, One());
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      mma(dOV[mi], frag_k_seq<MT, IT>(dO, v_pitch, t0, T, 16 * mi, 32 * kb, One()), bvn);
+      mma(Tb[mi], frag_k<MT, float>(dVc, DV, 16 * mi, 32 * kb), bv);
+    }
+  }
+  float KG[4][4];
+  {
+    float cR1 = 0.f;
+    float pR1[4][4];
+    const float bs = cs.beta[s], bgs = cs.beta[s] * cs.gam[s];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * mi + 4 * j + r;
+        const float gm = (row >= s) ? expf(cs.G[row] - cs.G[s]) : 0.f;
+        const float Mv = QK[mi][r] * gm;
+        const float dMv = dOV[mi][r] * gm;
+        sdM[row * CP + s] = from_f<MT>(dMv);
+        sdMT[s * CP + row] = from_f<MT>(dMv);
+        const float r1 = (row > s) ? dOV[mi][r] * Mv : 0.f;
+        pR1[mi][r] = r1;
+        cR1 += r1;
+        sdA[row * FP + s] = (row > s) ? fmaf(Ta[mi][r], bgs, Tb[mi][r] * bs) : 0.f;
+        KG[mi][r] = (row > s) ? KK[mi][r] * gm : 0.f;
+      }
+    cR1 = across_groups_sum(cR1);
+    if (j == 0) colR1[s] = cR1;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float t = group16_sum(pR1[mi][r]);
+        if ((l & 15) == 0) part[P_R1][w][16 * mi + 4 * j + r] = t;
+      }
+  }
+  __syncthreads();
+  // T1 = dA A^T (column block cb of T1), then dL = strictLower(-A^T T1)
+  f4 T1[4], dL[4];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+    T1[mi] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+      if (32 * p <= 16 * mi + 15 && 32 * p <= 16 * cb + 15)
+        mma(T1[mi], frag_k<MT, float>(sdA, FP, 16 * mi, 32 * p), frag_k<MT, float>(Ac, C, 16 * cb, 32 * p));
+  }
+  Frag<MT> T1f[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) T1f[p] = frag_acc<MT>(T1[2 * p], T1[2 * p + 1]);
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+      if (32 * p + 31 >= 16 * mi) mma(acc, frag_k<MT, float>(Atc, C, 16 * mi, 32 * p), T1f[p]);
+    dL[mi] = acc;
+  }
+  {
+    float cR2 = 0.f;
+    float pR2[4][4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * mi + 4 * j + r;
+        const float dl = (row > s) ? -dL[mi][r] : 0.f;
+        const float gm = (row > s) ? expf(cs.G[row] - cs.G[s]) : 0.f;
+        const float Pv = dl * gm;
+        const float r2 = dl * KG[mi][r];
+        pR2[mi][r] = r2;
+        cR2 = fmaf(cs.beta[row], r2, cR2);
+        const float z = cs.beta[row] * Pv;
+        if (row > s) {
+          sZ[row * CP + s] = from_f<MT>(z);
+          sZ[s * CP + row] = from_f<MT>(z);
+        } else if (row == s) {
+          sZ[row * CP + s] = from_f<MT>(0.f);
+        }
+      }
+    cR2 = across_groups_sum(cR2);
+    if (j == 0) colR2b[s] = cR2;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float t = group16_sum(pR2[mi][r]);
+        if ((l & 15) == 0) part[P_R2][w][16 * mi + 4 * j + r] = t;
+      }
+  }
+  __syncthreads();
+
+  // ---- D: dQ^ += dM K^; dK^ += dM^T Q^ + Z K^   (own key-column blocks)
+  float pDQ[4][4], pDK[4][4];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pDQ[mi][r] = pDK[mi][r] = 0.f;
+#pragma unroll
+  for (int ib = 0; ib < NBW; ++ib) {
+    const int nb = w + 4 * ib;
+    if (nb >= NBD) break;
+    const int d = 16 * nb + (l & 15);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const Frag<MT> bK = frag_rows<MT, IT>(k, qk_pitch, t0, T, 32 * p, d, krow);
+      const Frag<MT> bQ = frag_rows<MT, IT>(q, qk_pitch, t0, T, 32 * p, d, qrow);
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+        if (32 * p <= 16 * mi + 15) mma(dQ[ib][mi], frag_k_raw(sdM, CP, 16 * mi, 32 * p), bK);
+        if (32 * p + 31 >= 16 * mi) mma(dK[ib][mi], frag_k_raw(sdMT, CP, 16 * mi, 32 * p), bQ);
+        mma(dK[ib][mi], frag_k_raw(sZ, CP, 16 * mi, 32 * p), bK);
+      }
+    }
+    if (a.l2norm) {
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 16 * mi + 4 * j + r, t = t0 + row;
+          if (t < T) {
+            pDQ[mi][r] = fmaf(to_f(q[(size_t)t * qk_pitch + d]) * rq[row], dQ[ib][mi][r], pDQ[mi][r]);
+            pDK[mi][r] = fmaf(to_f(k[(size_t)t * qk_pitch + d]) * rk[row], dK[ib][mi][r], pDK[mi][r]);
+          }
+        }
+    }
+  }
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float s1 = group16_sum(pDQ[mi][r]), s2 = group16_sum(pDK[mi][r]);
+      if ((l & 15) == 0) {
+        part[P_DQ][w][16 * mi + 4 * j + r] = s1;
+        part[P_DK][w][16 * mi + 4 * j + r] = s2;
+      }
+    }
+
+  // ---- E: Y = A^T dVn, dV = diag(beta) Y; v . Y row sums  (value-column blocks w, w + 4, ...)
+  {
+    float pVY[4][4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pVY[mi][r] = 0.f;
+    for (int vb = w; vb < DV / 16; vb += 4) {
+      const int vc = 16 * vb + (l & 15);
+      Frag<MT> bdv[2];
+#pragma unroll
+      for (int p = 0; p < 2; ++p) bdv[p] = frag_rows<MT, float>(dVc, DV, 0, C, 32 * p, vc, One());
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+        f4 y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+          if (32 * p + 31 >= 16 * mi) mma(y, frag_k<MT, float>(Atc, C, 16 * mi, 32 * p), bdv[p]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 16 * mi + 4 * j + r, t = t0 + row;
+          if (t < T) {
+            ((IT*)a.dv)[v_base + (size_t)t * v_pitch + vc] = from_f<IT>(cs.beta[row] * y[r]);
+            pVY[mi][r] = fmaf(to_f(v[(size_t)t * v_pitch + vc]), y[r], pVY[mi][r]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float t = group16_sum(pVY[mi][r]);
+        if ((l & 15) == 0) part[P_VY][w][16 * mi + 4 * j + r] = t;
+      }
+  }
+  __syncthreads();
+
+  // ---- F: dbeta and dg (wave 0, lane = chunk row), fixed-order sums of the per-wave partials
+  if (w == 0) {
+    const int r = l, t = t0 + r;
+    auto sum4 = [&](int pi) { return ((part[pi][0][r] + part[pi][1][r]) + part[pi][2][r]) + part[pi][3][r]; };
+    const float kx = sum4(P_KX), qd = sum4(P_QD), E = sum4(P_E), r1 = sum4(P_R1), r2 = sum4(P_R2), vy = sum4(P_VY);
+    const float gm = cs.gam[r], bt = cs.beta[r];
+    const float db = fmaf(gm, kx, vy) + r2;
+    float dG = qd + bt * gm * kx + (r1 - colR1[r]) + (bt * r2 - colR2b[r]);
+    if (r == C - 1) dG += cs.gam[C - 1] * (((partS[0] + partS[1]) + partS[2]) + partS[3]);
+    // dg_t = sum_{s >= t} dG_s + sum_{r < t} E_r
+    const float rev = __shfl(dG, C - 1 - r, 64);
+    const float suf = __shfl(wave_incl_scan(rev), C - 1 - r, 64);
+    const float pre = wave_incl_scan(E) - E;
+    if (t < T) {
+      a.dg[s_base + (size_t)t * H] = suf + pre;
+      a.dbeta[s_base + (size_t)t * H] = db;
+    }
+  }
+
+  // ---- G: the prologue's backward, dq and dk out (own key-column blocks)
+#pragma unroll
+  for (int ib = 0; ib < NBW; ++ib) {
+    const int nb = w + 4 * ib;
+    if (nb >= NBD) break;
+    const int d = 16 * nb + (l & 15);
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * mi + 4 * j + r, t = t0 + row;
+        if (t >= T) continue;
+        float gq = dQ[ib][mi][r], gk = dK[ib][mi][r];
+        if (a.l2norm) {
+          const float dq_dot = ((part[P_DQ][0][row] + part[P_DQ][1][row]) + part[P_DQ][2][row]) + part[P_DQ][3][row];
+          const float dk_dot = ((part[P_DK][0][row] + part[P_DK][1][row]) + part[P_DK][2][row]) + part[P_DK][3][row];
+          const float xq = to_f(q[(size_t)t * qk_pitch + d]) * rq[row];
+          const float xk = to_f(k[(size_t)t * qk_pitch + d]) * rk[row];
+          gq = qs * rq[row] * fmaf(-xq, dq_dot, gq);
+          gk = rk[row] * fmaf(-xk, dk_dot, gk);
+        } else {
+          gq = qs * gq;
+        }
+        ((IT*)a.dq)[qk_base + (size_t)t * qk_pitch + d] = from_f<IT>(gq);
+        ((IT*)a.dk)[qk_base + (size_t)t * qk_pitch + d] = from_f<IT>(gk);
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
+// decode: one token per head-row
+// ---------------------------------------------------------------------------------------------------------------------
+template <typename IT, int DK, int DV>
+__global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
+  constexpr int NCQ = DV / 4;       // column quads
+  constexpr int RG = 256 / NCQ;     // row groups
+  constexpr int RPG = DK / RG;      // rows per group
+  static_assert(RG * NCQ == 256 && RPG * RG == DK, "decode tiling");
+  __shared__ float sq[DK], sk[DK], sd[DV];
+  __shared__ float red_k[RG][DV], red_q[RG][DV];
+  __shared__ float sc[2];
+  const int bh = blockIdx.x;
+  const int l = lane_id(), w = wave_id();
+  const IT* q = (const IT*)a.q + (size_t)bh * DK;
+  const IT* k = (const IT*)a.k + (size_t)bh * DK;
+  if (w == 0) {
+    float qq = 0.f, kk = 0.f;
+    for (int i = l; i < DK; i += 64) {
+      const float x = to_f(q[i]), y = to_f(k[i]);
+      qq = fmaf(x, x, qq);
+      kk = fmaf(y, y, kk);
+    }
+    qq = across_groups_sum(group16_sum(qq));
+    kk = across_groups_sum(group16_sum(kk));
+    const float rq = a.l2norm ? 1.0f / sqrtf(qq + L2_EPS) : 1.f;
+    const float rk = a.l2norm ? 1.0f / sqrtf(kk + L2_EPS) : 1.f;
+    float qk = 0.f;
+    for (int i = l; i < DK; i += 64) {
+      const float x = to_f(q[i]) * rq * a.q_scale, y = to_f(k[i]) * rk;
+      sq[i] = x;
+      sk[i] = y;
+      qk = fmaf(x, y, qk);
+    }
+    qk = across_groups_sum(group16_sum(qk));
+    if (l == 0) sc[0] = qk;
+  }
+  __syncthreads();
+  const int cq = threadIdx.x % NCQ, rg = threadIdx.x / NCQ;
+  const float* sin = a.s_in + (size_t)bh * DK * DV;
+  f4 st[RPG];
+  f4 pk = {0.f, 0.f, 0.f, 0.f}, pq = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < RPG; ++i) {
+    const int row = rg * RPG + i;
+    st[i] = *reinterpret_cast<const f4*>(sin + (size_t)row * DV + 4 * cq);
+    pk += sk[row] * st[i];
+    pq += sq[row] * st[i];
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    red_k[rg][4 * cq + e] = pk[e];
+    red_q[rg][4 * cq + e] = pq[e];
+  }
+  __syncthreads();
+  const float eg = expf(a.g[bh]);
+  if (threadIdx.x < DV) {
+    const int cc = threadIdx.x;
+    float u = 0.f, oq = 0.f;
+    for (int g2 = 0; g2 < RG; ++g2) {
+      u += red_k[g2][cc];
+      oq += red_q[g2][cc];
+    }
+    const float dd = a.beta[bh] * (to_f(((const IT*)a.v)[(size_t)bh * DV + cc]) - eg * u);
+    sd[cc] = dd;
+    ((IT*)a.o)[(size_t)bh * DV + cc] = from_f<IT>(fmaf(eg, oq, sc[0] * dd));
+  }
+  __syncthreads();
+  const f4 d4 = *reinterpret_cast<const f4*>(sd + 4 * cq);
+  float* so = a.s_out + (size_t)bh * DK * DV;
+#pragma unroll
+  for (int i = 0; i < RPG; ++i) {
+    const int row = rg * RPG + i;
+    *reinterpret_cast<f4*>(so + (size_t)row * DV + 4 * cq) = eg * st[i] + sk[row] * d4;
+  }
+}
+
+}  // namespace gdr
+
+// =====================================================================================================================
+// C ABI
+// =====================================================================================================================
+using namespace gdr;
+
+static thread_local char g_err[512] = "";
+
+static int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+static int launched(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(MACAI_GDR_ELAUNCH, "%s: HIP launch failed: %s", what, hipGetErrorString(e));
+  g_err[0] = 0;
+  return MACAI_GDR_OK;
+}
+
+static bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
+
+static int check_common(const char* what, int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV, int dtype) {
+  if (B < 1 || T < 1 || H < 1) return fail(MACAI_GDR_EINVAL, "%s: B, T, H must be >= 1 (got %lld, %lld, %lld)", what,
+                                           (long long)B, (long long)T, (long long)H);
+  if (DK != 32 && DK != 64 && DK != 128)
+    return fail(MACAI_GDR_EUNSUP, "%s: key head width must be 32, 64 or 128 (got %lld)", what, (long long)DK);
+  if (DV < 32 || DV % 32 != 0 || DV > 512)
+    return fail(MACAI_GDR_EUNSUP, "%s: value head width must be a multiple of 32 in [32, 512] (got %lld)", what,
+                (long long)DV);
+  if (dtype != MACAI_GDR_F32 && dtype != MACAI_GDR_BF16)
+    return fail(MACAI_GDR_EUNSUP, "%s: dtype code must be 0 (float32) or 1 (bfloat16), got %d", what, dtype);
+  if (B * T * H * (DK > DV ? DK : DV) >= ((int64_t)1 << 31) * 4)
+    return fail(MACAI_GDR_EINVAL, "%s: tensor too large", what);
+  return MACAI_GDR_OK;
+}
+
+#define DISPATCH_DK(DK, ...)                                   \
+  switch (DK) {                                                \
+    case 32: { constexpr int DKC = 32; __VA_ARGS__; } break;   \
+    case 64: { constexpr int DKC = 64; __VA_ARGS__; } break;   \
+    default: { constexpr int DKC = 128; __VA_ARGS__; } break;  \
+  }
+
+static int pick_waves(int64_t DV, int split, const char* what, int* nw_out, int* nslice_out) {
+  const int ncb = (int)(DV / 16);   // 16-column slices of the value width
+  int s = split;
+  if (s <= 0) s = -1;
+  int nw;
+  if (s < 0) {
+    nw = ncb >= 8 ? 8 : ncb;        // default: one workgroup of up to 8 waves per head-row
+    while (ncb % nw) --nw;
+  } else {
+    if (ncb % s) return fail(MACAI_GDR_EINVAL, "%s: split %d does not divide the %d value-column slices", what, s, ncb);
+    nw = ncb / s;
+    if (nw > 8) return fail(MACAI_GDR_EINVAL, "%s: split %d leaves %d waves per workgroup (max 8)", what, s, nw);
+  }
+  *nw_out = nw;
+  *nslice_out = ncb / nw;
+  return MACAI_GDR_OK;
+}
+
+extern "C" {
+
+const char* macai_gdr_last_error(void) { return g_err; }
+
+int macai_gdr_abi_version(void) { return MACAI_GDR_ABI_VERSION; }
+
+int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, const float* beta, void* W, float* U,
+                   void* M, void* Mt, float* A, float* At, int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV,
+                   int32_t dtype, int32_t use_l2norm, float q_scale, void* stream) {
+  const char* what = "macai_gdr_prep";
+  int rc = check_common(what, B, T, H, DK, DV, dtype);
+  if (rc) return rc;
+  if (!k || !v || !g || !beta || !W || !U) return fail(MACAI_GDR_EINVAL, "%s: null input or output pointer", what);
+  if ((M || Mt) && !q) return fail(MACAI_GDR_EINVAL, "%s: M needs q", what);
+  if ((A == nullptr) != (At == nullptr)) return fail(MACAI_GDR_EINVAL, "%s: A and At go together", what);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(W) || !aligned16(U) || !aligned16(M) ||
+      !aligned16(Mt) || !aligned16(A) || !aligned16(At))
+    return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
+  PrepArgs a{q, k, v, g, beta, W, U, M, Mt, A, At, (int)B, (int)T, (int)H, (int)DV, (int)((T + C - 1) / C),
+             use_l2norm, q_scale};
+  dim3 grid(a.NT, (unsigned)H, (unsigned)B);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == MACAI_GDR_F32) {
+    DISPATCH_DK(DK, hipLaunchKernelGGL((prep_kernel<float, float, DKC>), grid, dim3(256), 0, st, a));
+  } else {
+    DISPATCH_DK(DK, hipLaunchKernelGGL((prep_kernel<bf16, bf16, DKC>), grid, dim3(256), 0, st, a));
+  }
+  return launched(what);
+}
+
+int macai_gdr_state_fwd(const void* q, const void* k, const float* g, const void* W, const float* U, const void* M,
+                        const float* s0, void* o, float* sT, float* Sc, float* Vn, int64_t B, int64_t T, int64_t H,
+                        int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, int32_t flags,
+                        int32_t split, void* stream) {
+  const char* what = "macai_gdr_state_fwd";
+  int rc = check_common(what, B, T, H, DK, DV, dtype);
+  if (rc) return rc;
+  const bool store = flags & MACAI_GDR_STORE_STATES, out = !(flags & MACAI_GDR_NO_OUTPUT);
+  if (!k || !g || !W || !U) return fail(MACAI_GDR_EINVAL, "%s: null input pointer", what);
+  if (out && (!q || !M || !o)) return fail(MACAI_GDR_EINVAL, "%s: the output needs q, M and o", what);
+  if (store && (!Sc || !Vn)) return fail(MACAI_GDR_EINVAL, "%s: storing states needs Sc and Vn", what);
+  if (!out && !store) return fail(MACAI_GDR_EINVAL, "%s: flags ask for nothing", what);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(W) || !aligned16(M) || !aligned16(U))
+    return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
+  int nw, nslice;
+  if ((rc = pick_waves(DV, split, what, &nw, &nslice))) return rc;
+  StateFwdArgs a{q, k, g, W, U, M, s0, o, out ? sT : nullptr, Sc, Vn, (int)B, (int)T, (int)H, (int)DV,
+                 (int)((T + C - 1) / C), use_l2norm, q_scale, nslice};
+  const int HR = (int)(B * H);
+  dim3 grid((unsigned)(8 * nslice * ((HR + 7) / 8)));
+  dim3 block(64 * nw);
+  hipStream_t st = (hipStream_t)stream;
+#define LAUNCH_SF(IT, MT, O, S) \
+  DISPATCH_DK(DK, hipLaunchKernelGGL((state_fwd_kernel<IT, MT, DKC, O, S>), grid, block, 0, st, a))
+  if (dtype == MACAI_GDR_F32) {
+    if (out && store) { LAUNCH_SF(float, float, true, true); }
+    else if (out) { LAUNCH_SF(float, float, true, false); }
+    else { LAUNCH_SF(float, float, false, true); }
+  } else {
+    if (out && store) { LAUNCH_SF(bf16, bf16, true, true); }
+    else if (out) { LAUNCH_SF(bf16, bf16, true, false); }
+    else { LAUNCH_SF(bf16, bf16, false, true); }
+  }
+#undef LAUNCH_SF
+  return launched(what);
+}
+
+int macai_gdr_state_bwd(const void* q, const void* k, const float* g, const void* W, const void* Mt, const void* dO,
+                        const float* dsT, float* dSn, float* dVn, float* ds0, int64_t B, int64_t T, int64_t H,
+                        int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, int32_t split,
+                        void* stream) {
+  const char* what = "macai_gdr_state_bwd";
+  int rc = check_common(what, B, T, H, DK, DV, dtype);
+  if (rc) return rc;
+  if (!q || !k || !g || !W || !Mt || !dO || !dSn || !dVn || !ds0)
+    return fail(MACAI_GDR_EINVAL, "%s: null pointer", what);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(W) || !aligned16(Mt))
+    return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
+  int nw, nslice;
+  if ((rc = pick_waves(DV, split, what, &nw, &nslice))) return rc;
+  StateBwdArgs a{q, k, g, W, Mt, dO, dsT, dSn, dVn, ds0, (int)B, (int)T, (int)H, (int)DV, (int)((T + C - 1) / C),
+                 use_l2norm, q_scale, nslice};
+  const int HR = (int)(B * H);
+  dim3 grid((unsigned)(8 * nslice * ((HR + 7) / 8)));
+  dim3 block(64 * nw);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == MACAI_GDR_F32) {
+    DISPATCH_DK(DK, hipLaunchKernelGGL((state_bwd_kernel<float, float, DKC>), grid, block, 0, st, a));
+  } else {
+    DISPATCH_DK(DK, hipLaunchKernelGGL((state_bwd_kernel<bf16, bf16, DKC>), grid, block, 0, st, a));
+  }
+  return launched(what);
+}
+
+int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float* g, const float* beta, const void* dO,
+                        const float* A, const float* At, const float* Sc, const float* dSn, const float* Vn,
+                        const float* dVn, void* dq, void* dk, void* dv, float* dg, float* dbeta, int64_t B, int64_t T,
+                        int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale,
+                        void* stream) {
+  const char* what = "macai_gdr_chunk_bwd";
+  int rc = check_common(what, B, T, H, DK, DV, dtype);
+  if (rc) return rc;
+  if (!q || !k || !v || !g || !beta || !dO || !A || !At || !Sc || !dSn || !Vn || !dVn || !dq || !dk || !dv || !dg ||
+      !dbeta)
+    return fail(MACAI_GDR_EINVAL, "%s: null pointer", what);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(A) || !aligned16(At) ||
+      !aligned16(Sc) || !aligned16(dSn) || !aligned16(Vn) || !aligned16(dVn))
+    return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
+  ChunkBwdArgs a{q, k, v, g, beta, dO, A, At, Sc, dSn, Vn, dVn, dq, dk, dv, dg, dbeta, (int)B, (int)T, (int)H,
+                 (int)DV, (int)((T + C - 1) / C), use_l2norm, q_scale};
+  dim3 grid(a.NT, (unsigned)H, (unsigned)B);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == MACAI_GDR_F32) {
+    DISPATCH_DK(DK, hipLaunchKernelGGL((chunk_bwd_kernel<float, float, DKC>), grid, dim3(256), 0, st, a));
+  } else {
+    DISPATCH_DK(DK, hipLaunchKernelGGL((chunk_bwd_kernel<bf16, bf16, DKC>), grid, dim3(256), 0, st, a));
+  }
+  return launched(what);
+}
+
+int macai_gdr_decode(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                     const float* s_in, void* o, float* s_out, int64_t B, int64_t H, int64_t DK, int64_t DV,
+                     int32_t dtype, int32_t use_l2norm, float q_scale, void* stream) {
+  const char* what = "macai_gdr_decode";
+  if (B < 1 || H < 1) return fail(MACAI_GDR_EINVAL, "%s: B and H must be >= 1", what);
+  if (!((DK == 128 && DV == 128) || (DK == 64 && DV == 64) || (DK == 128 && DV == 64) || (DK == 64 && DV == 128)))
+    return fail(MACAI_GDR_EUNSUP, "%s: head widths (DK, DV) must be 64 or 128 each (got %lld, %lld)", what,
+                (long long)DK, (long long)DV);
+  if (dtype != MACAI_GDR_F32 && dtype != MACAI_GDR_BF16)
+    return fail(MACAI_GDR_EUNSUP, "%s: dtype code must be 0 or 1, got %d", what, dtype);
+  if (!q || !k || !v || !g || !beta || !s_in || !o || !s_out) return fail(MACAI_GDR_EINVAL, "%s: null pointer", what);
+  if (!aligned16(s_in) || !aligned16(s_out)) return fail(MACAI_GDR_EINVAL, "%s: states must be 16-byte aligned", what);
+  DecodeArgs a{q, k, v, g, beta, s_in, o, s_out, (int)B, (int)H, use_l2norm, q_scale};
+  dim3 grid((unsigned)(B * H));
+  hipStream_t st = (hipStream_t)stream;
+#define LAUNCH_DEC(IT)                                                                                           \
+  if (DK == 128 && DV == 128) hipLaunchKernelGGL((decode_kernel<IT, 128, 128>), grid, dim3(256), 0, st, a);    \
+  else if (DK == 64 && DV == 64) hipLaunchKernelGGL((decode_kernel<IT, 64, 64>), grid, dim3(256), 0, st, a);   \
+  else if (DK == 128) hipLaunchKernelGGL((decode_kernel<IT, 128, 64>), grid, dim3(256), 0, st, a);             \
+  else hipLaunchKernelGGL((decode_kernel<IT, 64, 128>), grid, dim3(256), 0, st, a);
+  if (dtype == MACAI_GDR_F32) {
+    LAUNCH_DEC(float)
+  } else {
+    LAUNCH_DEC(bf16)
+  }
+#undef LAUNCH_DEC
+  return launched(what);
+}
+
+}  // extern "C"

@@ -1,0 +1,84 @@
+"""ctypes binding of libmacai_gdr.so (the C ABI declared in include/macai_gdr.h).
+
+The library is built in-tree by mac-ai-engineering_amd/build.py (hipcc, gfx950) next to this file.  There is no
+fallback: if it is missing or fails to load, every call raises.
+"""
+import ctypes
+import os
+
+import torch
+
+LIB_NAME = "libmacai_gdr.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+F32, BF16 = 0, 1
+OK, EINVAL, EUNSUP, ELAUNCH = 0, 1, 2, 3
+STORE_STATES, NO_OUTPUT = 1, 8
+ABI_VERSION = 1
+
+_p, _i64, _i32, _f = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
+# name -> argument types (the order of include/macai_gdr.h)
+SIGNATURES = {
+    "macai_gdr_prep": [_p] * 11 + [_i64] * 5 + [_i32, _i32, _f, _p],
+    "macai_gdr_state_fwd": [_p] * 11 + [_i64] * 5 + [_i32, _i32, _f, _i32, _i32, _p],
+    "macai_gdr_state_bwd": [_p] * 10 + [_i64] * 5 + [_i32, _i32, _f, _i32, _p],
+    "macai_gdr_chunk_bwd": [_p] * 17 + [_i64] * 5 + [_i32, _i32, _f, _p],
+    "macai_gdr_decode": [_p] * 8 + [_i64] * 4 + [_i32, _i32, _f, _p],
+}
+
+_lib = None
+
+
+class NativeError(RuntimeError):
+    """A HIP launch failure reported by the library."""
+
+
+def lib():
+    """The loaded library (loaded once); raises RuntimeError when it is not built or does not load."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built: run `python -c 'import __graft_entry__ as g; g.build()'` "
+                               "(or mac-ai-engineering_amd/build.py) first")
+        L = ctypes.CDLL(LIB_PATH)
+        L.macai_gdr_last_error.restype = ctypes.c_char_p
+        L.macai_gdr_last_error.argtypes = []
+        L.macai_gdr_abi_version.restype = ctypes.c_int
+        L.macai_gdr_abi_version.argtypes = []
+        for name, args in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = args
+        if L.macai_gdr_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH}: ABI version {L.macai_gdr_abi_version()}, expected {ABI_VERSION}")
+        _lib = L
+    return _lib
+
+
+def ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def dtype_code(dt):
+    if dt == torch.float32:
+        return F32
+    if dt == torch.bfloat16:
+        return BF16
+    raise NotImplementedError(f"the HIP kernels take float32 or bfloat16, got {dt}")
+
+
+def stream_of(t):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def call(name, *args):
+    """Call entry point `name`; raise on a non-zero return (ValueError for bad arguments, NotImplementedError for an
+    unsupported shape or dtype, NativeError for a launch failure)."""
+    rc = getattr(lib(), name)(*args)
+    if rc != OK:
+        msg = lib().macai_gdr_last_error().decode()
+        if rc == EINVAL:
+            raise ValueError(msg)
+        if rc == EUNSUP:
+            raise NotImplementedError(msg)
+        raise NativeError(msg)

@@ -1,0 +1,246 @@
+"""The gated delta rule on MI355X: autograd functions over the HIP kernels, and a drop-in for transformers'
+torch_chunk_gated_delta_rule (same arguments, same returns).
+
+Mirrors the reference's src/macai/gated_delta/op.py: `GatedDeltaRule` keeps its autograd contract (op.py:116-257),
+`chunk_gated_delta_rule` its drop-in signature and behaviour (op.py:264-298), `l2norm` and `recurrent_reference` its
+helpers (op.py:260-261, 301-314).  The per-call passes (op.py:63-113, 159, 217, 234, 241-242) become the C-ABI calls of
+include/macai_gdr.h on the current HIP stream.  The training forward keeps only its inputs and the backward recomputes
+the per-chunk matrices and chunk states (the reference's RECOMPUTE_STATES default, op.py:27-33).
+"""
+import collections
+import math
+
+import torch
+
+from . import _native as N
+
+CHUNK = 64   # chunk length of the kernels; the drop-in's chunk_size is accepted and not used (as op.py:266-269)
+# VALUE_SPLIT: workgroups a head-row's value columns are split over in the state passes (each owns DV / VALUE_SPLIT
+# columns as DV / 16 / VALUE_SPLIT waves of 16 columns): "auto" (split_for) or 1, 2, 4, 8, ...
+VALUE_SPLIT = "auto"
+# the passes' calls by what they ran, "fwd s<split>" / "bwd s<split>" (counted at every call; no GPU work)
+CALLS = collections.Counter()
+
+
+def split_for(rows: int, T: int, dv: int) -> int:
+    """VALUE_SPLIT's choice for `rows` head-rows (B x H) of value width dv: "auto" takes the smallest split (a divisor of
+    dv / 16) that gives at least 256 workgroups, one per CU, or every 16-column slice its own workgroup; an int setting
+    is rounded down to a divisor."""
+    slices = dv // 16
+    if VALUE_SPLIT == "auto":
+        s = 1
+        while s < slices and rows * s < 256:
+            s *= 2
+    else:
+        s = int(VALUE_SPLIT)
+    s = max(1, min(s, slices))
+    while slices % s:
+        s -= 1
+    return s
+
+
+def _check(q, k, v, g, beta, s0):
+    if not q.is_cuda:
+        raise RuntimeError("macai's gated delta rule runs on a HIP device (MI355X); got tensors on " + str(q.device))
+    if q.dim() != 4 or k.shape != q.shape or v.dim() != 4 or v.shape[:3] != q.shape[:3]:
+        raise ValueError(f"q, k [B, T, H, DK] and v [B, T, H, DV] expected, got {tuple(q.shape)}, {tuple(k.shape)}, "
+                         f"{tuple(v.shape)}")
+    B, T, H, DK = q.shape
+    if g.shape != (B, T, H) or beta.shape != (B, T, H):
+        raise ValueError(f"g and beta must be [B, T, H] = {(B, T, H)}, got {tuple(g.shape)}, {tuple(beta.shape)}")
+    if s0 is not None and s0.shape != (B, H, DK, v.shape[-1]):
+        raise ValueError(f"initial_state must be [B, H, DK, DV] = {(B, H, DK, v.shape[-1])}, got {tuple(s0.shape)}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError(f"q, k, v must share a dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
+    if g.dtype != torch.float32 or beta.dtype != torch.float32 or (s0 is not None and s0.dtype != torch.float32):
+        raise ValueError("g, beta and the state must be float32")
+
+
+def _dims(q, v):
+    B, T, H, DK = q.shape
+    return B, T, H, DK, v.shape[-1], math.ceil(T / CHUNK)
+
+
+def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool):
+    """prep (W, U, M) then the state pass with the output: returns (o in q's dtype, sT or None)."""
+    B, T, H, DK, DV, NT = _dims(q, v)
+    dev, dt = q.device, q.dtype
+    code, stream = N.dtype_code(dt), N.stream_of(q)
+    W = torch.empty(B, H, NT, CHUNK, DK, device=dev, dtype=dt)
+    U = torch.empty(B, H, NT, CHUNK, DV, device=dev, dtype=torch.float32)
+    M = torch.empty(B, H, NT, CHUNK, CHUNK, device=dev, dtype=dt)
+    N.call("macai_gdr_prep", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(g), N.ptr(beta), N.ptr(W), N.ptr(U), N.ptr(M), None,
+           None, None, B, T, H, DK, DV, code, int(l2norm), q_scale, stream)
+    o = torch.empty(B, T, H, DV, device=dev, dtype=dt)
+    sT = torch.empty(B, H, DK, DV, device=dev, dtype=torch.float32) if want_sT else None
+    split = split_for(B * H, T, DV)
+    N.call("macai_gdr_state_fwd", N.ptr(q), N.ptr(k), N.ptr(g), N.ptr(W), N.ptr(U), N.ptr(M), N.ptr(s0), N.ptr(o),
+           N.ptr(sT), None, None, B, T, H, DK, DV, code, int(l2norm), q_scale, 0, split, stream)
+    CALLS[f"fwd s{split}"] += 1
+    return o, sT
+
+
+def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float):
+    """Recompute (prep with M^T, A, A^T; the state pass storing S_c and Vn), the reverse state pass, the per-chunk
+    backward.  Returns (dq, dk, dv in q's dtype; dg, dbeta, ds0 float32)."""
+    B, T, H, DK, DV, NT = _dims(q, v)
+    dev, dt = q.device, q.dtype
+    code, stream = N.dtype_code(dt), N.stream_of(q)
+    f32 = torch.float32
+    W = torch.empty(B, H, NT, CHUNK, DK, device=dev, dtype=dt)
+    U = torch.empty(B, H, NT, CHUNK, DV, device=dev, dtype=f32)
+    Mt = torch.empty(B, H, NT, CHUNK, CHUNK, device=dev, dtype=dt)
+    A = torch.empty(B, H, NT, CHUNK, CHUNK, device=dev, dtype=f32)
+    At = torch.empty_like(A)
+    N.call("macai_gdr_prep", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(g), N.ptr(beta), N.ptr(W), N.ptr(U), None, N.ptr(Mt),
+           N.ptr(A), N.ptr(At), B, T, H, DK, DV, code, int(l2norm), q_scale, stream)
+    split = split_for(B * H, T, DV)
+    Sc = torch.empty(B, H, NT, DK, DV, device=dev, dtype=f32)
+    Vn = torch.empty(B, H, NT, CHUNK, DV, device=dev, dtype=f32)
+    N.call("macai_gdr_state_fwd", N.ptr(q), N.ptr(k), N.ptr(g), N.ptr(W), N.ptr(U), None, N.ptr(s0), None, None,
+           N.ptr(Sc), N.ptr(Vn), B, T, H, DK, DV, code, int(l2norm), q_scale, N.STORE_STATES | N.NO_OUTPUT, split,
+           stream)
+    dSn = torch.empty_like(Sc)
+    dVn = torch.empty_like(Vn)
+    ds0 = torch.empty(B, H, DK, DV, device=dev, dtype=f32)
+    N.call("macai_gdr_state_bwd", N.ptr(q), N.ptr(k), N.ptr(g), N.ptr(W), N.ptr(Mt), N.ptr(do), N.ptr(dsT), N.ptr(dSn),
+           N.ptr(dVn), N.ptr(ds0), B, T, H, DK, DV, code, int(l2norm), q_scale, split, stream)
+    CALLS[f"bwd s{split}"] += 1
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dg, dbeta = torch.empty_like(g), torch.empty_like(beta)
+    N.call("macai_gdr_chunk_bwd", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(g), N.ptr(beta), N.ptr(do), N.ptr(A), N.ptr(At),
+           N.ptr(Sc), N.ptr(dSn), N.ptr(Vn), N.ptr(dVn), N.ptr(dq), N.ptr(dk), N.ptr(dv), N.ptr(dg), N.ptr(dbeta),
+           B, T, H, DK, DV, code, int(l2norm), q_scale, stream)
+    return dq, dk, dv, dg, dbeta, ds0
+
+
+def _grad_in(x, like_shape, dtype, dev):
+    return None if x is None else x.to(dtype).contiguous()
+
+
+class GatedDeltaRule(torch.autograd.Function):
+    """o, S_T = recurrence(q, k, v, g, beta, S_0) on [B, T, H, D] tensors (q already normalised and scaled): the
+    reference's contract (op.py:116-257).  q, k, v float32 or bfloat16 (o in that dtype), g, beta, s0 float32.
+    backward -> (dq, dk, dv, dg, dbeta, ds0, None); None upstream gradients count as zeros (op.py:194-200)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, s0, save: bool):
+        _check(q, k, v, g, beta, s0)
+        q, k, v, g, beta, s0 = (t.contiguous() for t in (q, k, v, g, beta, s0))
+        with torch.cuda.device(q.device):
+            o, sT = _forward(q, k, v, g, beta, s0, False, 1.0, True)
+        if save:
+            ctx.save_for_backward(q, k, v, g, beta, s0)
+        return o, sT
+
+    @staticmethod
+    def backward(ctx, do, dsT):
+        q, k, v, g, beta, s0 = ctx.saved_tensors
+        do = torch.zeros_like(v) if do is None else do.to(v.dtype).contiguous()
+        dsT = None if dsT is None else dsT.to(torch.float32).contiguous()
+        with torch.cuda.device(q.device):
+            dq, dk, dv, dg, dbeta, ds0 = _backward(q, k, v, g, beta, s0, do, dsT, False, 1.0)
+        return dq, dk, dv, dg, dbeta, ds0, None
+
+
+class _DropIn(torch.autograd.Function):
+    """The drop-in's rule on the raw query / key: the l2norm prologue (and q's DK^-1/2 scale) is applied inside the
+    kernels and its backward fused into the per-chunk backward (the reference runs it as separate L2NormScale passes,
+    _norm.py:81-114).  s0 may be None (zeros); sT is returned only when want_sT."""
+
+    @staticmethod
+    def forward(ctx, query, key, value, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, save: bool):
+        with torch.cuda.device(query.device):
+            o, sT = _forward(query, key, value, g, beta, s0, l2norm, q_scale, want_sT)
+        if save:
+            ctx.save_for_backward(query, key, value, g, beta, s0)
+            ctx.cfg = (l2norm, q_scale, s0 is not None)
+        if sT is None:
+            return o
+        return o, sT
+
+    @staticmethod
+    def backward(ctx, do, dsT=None):
+        query, key, value, g, beta, s0 = ctx.saved_tensors
+        l2norm, q_scale, has_s0 = ctx.cfg
+        do = torch.zeros_like(value) if do is None else do.to(value.dtype).contiguous()
+        dsT = None if dsT is None else dsT.to(torch.float32).contiguous()
+        with torch.cuda.device(query.device):
+            dq, dk, dv, dg, dbeta, ds0 = _backward(query, key, value, g, beta, s0, do, dsT, l2norm, q_scale)
+        return dq, dk, dv, dg, dbeta, (ds0 if has_s0 else None), None, None, None, None
+
+
+def l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    return x * torch.rsqrt((x * x).sum(dim=-1, keepdim=True) + eps)
+
+
+def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size: int = 64, initial_state=None,
+                           output_final_state: bool = False, use_qk_l2norm_in_kernel: bool = False, **kwargs):
+    """Drop-in for transformers' torch_chunk_gated_delta_rule: query, key [B, T, H, DK]; value [B, T, H, DV]; g (log
+    decay, <= 0) and beta [B, T, H]; initial_state [B, H, DK, DV] or None.  Returns the output [B, T, H, DV] in the
+    query's dtype and the final state (float32) when output_final_state, else None.  chunk_size is accepted and unused
+    (the kernels use 64-token chunks).  bfloat16 inputs run on bf16 MFMA with fp32 accumulation and an fp32 state;
+    float32 inputs on fp32 MFMA; float16 inputs are computed as float32."""
+    if kwargs.get("cu_seqlens") is not None:
+        # packed rows (several sequences in one row): the state must restart at each boundary; not implemented, and
+        # running without it would silently carry state across sequences (op.py:270-273)
+        raise NotImplementedError("macai's gated delta rule does not take packed rows (cu_seqlens) yet")
+    dtype = query.dtype
+    cdt = torch.bfloat16 if dtype == torch.bfloat16 else torch.float32
+    q, k, v = (x.to(cdt).contiguous() for x in (query, key, value))
+    gf, bf = g.to(torch.float32).contiguous(), beta.to(torch.float32).contiguous()
+    s0 = None if initial_state is None else initial_state.to(torch.float32).contiguous()
+    _check(q, k, v, gf, bf, s0)
+    tensors = (q, k, v, gf, bf) + (() if s0 is None else (s0,))
+    save = torch.is_grad_enabled() and any(t.requires_grad for t in tensors)
+    res = _DropIn.apply(q, k, v, gf, bf, s0, bool(use_qk_l2norm_in_kernel), q.shape[-1] ** -0.5,
+                        bool(output_final_state), save)
+    out, sT = (res, None) if not output_final_state else res
+    return out.to(dtype), sT
+
+
+def recurrent_gated_delta_rule(query, key, value, g, beta, initial_state=None, output_final_state: bool = False,
+                               use_qk_l2norm_in_kernel: bool = False, **kwargs):
+    """Drop-in for transformers' torch_recurrent_gated_delta_rule (modeling_qwen3_5.py:330-380), the decode path the
+    reference leaves to PyTorch (patch.py:27-29).  One token (T = 1) without autograd runs the decode kernel (one
+    streaming pass over the fp32 state); longer inputs, or inputs that need gradients, run the chunked kernels, which
+    compute the same recurrence."""
+    T = query.shape[1]
+    needs_grad = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (query, key, value, g, beta, initial_state))
+    if T != 1 or needs_grad:
+        return chunk_gated_delta_rule(query, key, value, g, beta, initial_state=initial_state,
+                                      output_final_state=output_final_state,
+                                      use_qk_l2norm_in_kernel=use_qk_l2norm_in_kernel)
+    dtype = query.dtype
+    cdt = torch.bfloat16 if dtype == torch.bfloat16 else torch.float32
+    q, k, v = (x.to(cdt).contiguous() for x in (query, key, value))
+    gf, bf = g.to(torch.float32).contiguous(), beta.to(torch.float32).contiguous()
+    B, _, H, DK = q.shape
+    DV = v.shape[-1]
+    s_in = (torch.zeros(B, H, DK, DV, device=q.device, dtype=torch.float32) if initial_state is None
+            else initial_state.to(torch.float32).contiguous())
+    _check(q, k, v, gf, bf, s_in)
+    o = torch.empty(B, 1, H, DV, device=q.device, dtype=cdt)
+    s_out = torch.empty_like(s_in)
+    with torch.cuda.device(q.device):
+        N.call("macai_gdr_decode", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gf), N.ptr(bf), N.ptr(s_in), N.ptr(o),
+               N.ptr(s_out), B, H, DK, DV, N.dtype_code(cdt), int(bool(use_qk_l2norm_in_kernel)), DK ** -0.5,
+               N.stream_of(q))
+    return o.to(dtype), (s_out if output_final_state else None)
+
+
+def recurrent_reference(q, k, v, g, beta, s0):
+    """The recurrence step by step in plain PyTorch ([B, T, H, D] inputs, q already normalised and scaled): the
+    reference's parity helper (op.py:301-314), kept for API compatibility.  No kernel path calls it."""
+    B, T, H, DK = q.shape
+    s = s0.clone()
+    outs = []
+    for t in range(T):
+        a = g[:, t].exp()[..., None, None]
+        st = s * a
+        u = (st * k[:, t, :, :, None]).sum(-2)
+        d = beta[:, t, :, None] * (v[:, t] - u)
+        s = st + k[:, t, :, :, None] * d[:, :, None, :]
+        outs.append((s * q[:, t, :, :, None]).sum(-2))
+    return torch.stack(outs, 1), s

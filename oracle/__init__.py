@@ -1,0 +1,19 @@
+"""CPU oracle for the chunked gated delta rule -- TEST INFRASTRUCTURE ONLY.
+
+This package restates, in float64 PyTorch on the CPU, the algorithm of the reference's hot path
+(`macai.gated_delta`, /root/reference/src/macai/gated_delta/op.py and _chunked.py) so that the HIP kernels can be
+checked against it.  Only `tests/`, `__graft_entry__.smoke()` and the `cpu_baseline` leg of `bench.py` may import it,
+and only as the checker (or, for `cpu_baseline`, as the timed CPU restatement of the reference's torch path).  The
+product (`mac-ai-engineering_amd/macai`) never imports it and has no CPU fallback.
+
+Pinning (each function's checks live in tests/test_oracle.py):
+  recurrence            -- the token recurrence; pinned by hand-computed closed forms (beta = 0 decay-only, exact
+                           delta-rule recall with orthonormal keys, one-step by hand) and by gradcheck.
+  chunked_forward       -- F1-F5; pinned against `recurrence` (< 1e-12, float64) on ragged shapes, chunk-size
+                           invariance, A (I + L) = I.
+  chunked_backward      -- B1-B6 with the no-cancellation dg form; pinned against torch.autograd through
+                           `recurrence` (< 1e-12) including strong decay (g = -20) where the naive dg form fails.
+  torch_chunk_gated_delta_rule -- restatement of transformers' reference (the error anchor of the parity bar);
+                           pinned against the installed transformers function and against `recurrence`.
+  decode_step           -- one token of the recurrence; pinned against `recurrence` with T = 1 and by hand.
+"""
