@@ -1,0 +1,251 @@
+"""Benchmark of the MI355X gated delta rule: the drop-in's forward + backward at BASELINE config 1.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--config 1|2]
+
+A step = one call of macai.gated_delta.chunk_gated_delta_rule (use_qk_l2norm_in_kernel=True, bf16 q/k/v, fp32 g and
+beta) followed by its backward for a seeded upstream gradient dO (torch.autograd.grad, so no gradient accumulation),
+on synthetic inputs already resident in HBM.  Prints ONE JSON line (rank 0).  Beside the step time it times every
+kernel of the step alone with HIP events on the launch stream (the roofline of the dominant kernel), and the
+reference's torch path on the host CPU (the oracle's restatement of transformers' torch_chunk_gated_delta_rule,
+float32, autograd backward) on a bounded sample, as a reported baseline.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "mac-ai-engineering_amd"))
+
+import torch  # noqa: E402
+
+METRIC = "gated-delta fwd+bwd tokens/s (B4×T1024,H16,d128 bf16); % HBM/MFMA roofline"
+HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
+MFMA_PEAK = {"bf16": 2.5e15, "f32": 157.3e12}
+PUBLISHED = 401.1e3        # reference's own fwd+bwd tokens/s at this config (M3 Max)
+C = 64
+# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (profiles/), scaled by the copy-kernel factor;
+# None until measured for a kernel at this workload
+TRAFFIC = {}
+
+CONFIGS = {
+    1: dict(B=4, T=1024, Hk=16, Hv=16, DK=128, DV=128, s0=False),
+    2: dict(B=2, T=1024, Hk=16, Hv=32, DK=128, DV=128, s0=True),
+}
+
+
+def make_inputs(cfg, seed, dev):
+    """The measurement plan's synthetic inputs (q, k, v, u_g, x_g, x_beta, s0, dO drawn in that order in float64)."""
+    c = CONFIGS[cfg]
+    gen = torch.Generator().manual_seed(seed)
+    B, T, Hk, Hv, DK, DV = c["B"], c["T"], c["Hk"], c["Hv"], c["DK"], c["DV"]
+    rep = Hv // Hk
+    f64 = torch.float64
+    q = torch.randn(B, T, Hk, DK, generator=gen, dtype=f64).repeat_interleave(rep, 2)
+    k = torch.randn(B, T, Hk, DK, generator=gen, dtype=f64).repeat_interleave(rep, 2)
+    v = torch.randn(B, T, Hv, DV, generator=gen, dtype=f64)
+    u = torch.rand(Hv, generator=gen, dtype=f64) * math.log(16.0)
+    xg = torch.randn(B, T, Hv, generator=gen, dtype=f64)
+    xb = torch.randn(B, T, Hv, generator=gen, dtype=f64)
+    g = -torch.exp(u) * torch.nn.functional.softplus(xg)
+    beta = torch.sigmoid(xb)
+    s0 = torch.randn(B, Hv, DK, DV, generator=gen, dtype=f64) * 0.02 if c["s0"] else None
+    do = torch.randn(B, T, Hv, DV, generator=gen, dtype=f64)
+    bf = torch.bfloat16
+    out = dict(query=q.to(dev, bf), key=k.to(dev, bf), value=v.to(dev, bf), g=g.to(dev, torch.float32),
+               beta=beta.to(dev, torch.float32), initial_state=None if s0 is None else s0.to(dev, torch.float32),
+               do=do.to(dev, bf))
+    return out, c
+
+
+def kernel_costs(B, T, H, DK, DV, es=2):
+    """Algorithmic bytes (each declared input read once, each output written once, from argument sizes) and dense
+    FLOPs (2 per multiply-add, triangular products counted dense) per launch of each kernel of the training step."""
+    NT = math.ceil(T / C)
+    n = B * H * NT                       # chunk-heads
+    tok = B * T * H
+    io_k, io_v = tok * DK * es, tok * DV * es
+    gb = tok * 4 * 2                     # g and beta
+    cdk, cdv, cc = C * DK, C * DV, C * C
+    cost = {}
+    # the forward
+    cost["prep_fwd"] = dict(bytes=2 * io_k + io_v + gb + n * (cdk * es + cdv * 4 + cc * es),
+                            flops=n * (2 * 2 * cc * DK + cc * C / 3 + 2 * cc * DK + 2 * cc * DV))
+    cost["state_fwd_out"] = dict(bytes=2 * io_k + tok * 4 + n * (cdk * es + cdv * 4 + cc * es) + io_v,
+                                 flops=n * (3 * 2 * C * DK * DV + 2 * cc * DV))
+    # the backward
+    cost["prep_bwd"] = dict(bytes=io_k + io_v + gb + n * (cdk * es + cdv * 4 + cc * es + 2 * cc * 4),
+                            flops=n * (2 * cc * DK + cc * C / 3 + 2 * cc * DK + 2 * cc * DV))
+    cost["state_fwd_store"] = dict(bytes=io_k + tok * 4 + n * (cdk * es + cdv * 4 + DK * DV * 4 + cdv * 4),
+                                   flops=n * (2 * 2 * C * DK * DV))
+    cost["state_bwd"] = dict(bytes=2 * io_k + tok * 4 + io_v + n * (cdk * es + cc * es + DK * DV * 4 + cdv * 4),
+                             flops=n * (3 * 2 * C * DK * DV + 2 * cc * DV))
+    cost["chunk_bwd"] = dict(bytes=2 * io_k + 2 * io_v + gb + n * (2 * cc * 4 + 2 * DK * DV * 4 + 2 * cdv * 4)
+                             + 2 * io_k + io_v + gb,
+                             flops=n * (3 * 2 * C * DK * DV + 2 * cc * DK + 3 * 2 * cc * DK + 2 * 2 * cc * DV
+                                        + 2 * 2 * cc * C + 3 * 2 * cc * DK + 2 * cc * DV))
+    return cost
+
+
+def time_kernels(inp, reps=20):
+    """Each pass of the step alone: HIP events on the current (launch) stream around `reps` back-to-back launches."""
+    from macai.gated_delta import _native as N
+    from macai.gated_delta import op
+    q, k, v, g, beta, do = (inp[n] for n in ("query", "key", "value", "g", "beta", "do"))
+    s0 = inp["initial_state"]
+    B, T, H, DK = q.shape
+    DV = v.shape[-1]
+    NT = math.ceil(T / C)
+    dev, dt = q.device, q.dtype
+    f32 = torch.float32
+    code, st = N.dtype_code(dt), N.stream_of(q)
+    sc = DK ** -0.5
+    split = op.split_for(B * H, T, DV)
+    W = torch.empty(B, H, NT, C, DK, device=dev, dtype=dt)
+    U = torch.empty(B, H, NT, C, DV, device=dev, dtype=f32)
+    M = torch.empty(B, H, NT, C, C, device=dev, dtype=dt)
+    Mt, A, At = torch.empty_like(M), torch.empty(B, H, NT, C, C, device=dev, dtype=f32), None
+    At = torch.empty_like(A)
+    o = torch.empty_like(v)
+    Sc = torch.empty(B, H, NT, DK, DV, device=dev, dtype=f32)
+    Vn = torch.empty(B, H, NT, C, DV, device=dev, dtype=f32)
+    dSn, dVn = torch.empty_like(Sc), torch.empty_like(Vn)
+    ds0 = torch.empty(B, H, DK, DV, device=dev, dtype=f32)
+    dq, dk, dv, dg, db = (torch.empty_like(x) for x in (q, k, v, g, beta))
+    P = N.ptr
+    calls = {
+        "prep_fwd": ("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), P(M), None, None, None,
+                     B, T, H, DK, DV, code, 1, sc, st),
+        "state_fwd_out": ("macai_gdr_state_fwd", P(q), P(k), P(g), P(W), P(U), P(M), P(s0), P(o), None, None, None,
+                          B, T, H, DK, DV, code, 1, sc, 0, split, st),
+        "prep_bwd": ("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), None, P(Mt), P(A), P(At),
+                     B, T, H, DK, DV, code, 1, sc, st),
+        "state_fwd_store": ("macai_gdr_state_fwd", P(q), P(k), P(g), P(W), P(U), None, P(s0), None, None, P(Sc), P(Vn),
+                            B, T, H, DK, DV, code, 1, sc, N.STORE_STATES | N.NO_OUTPUT, split, st),
+        "state_bwd": ("macai_gdr_state_bwd", P(q), P(k), P(g), P(W), P(Mt), P(do), None, P(dSn), P(dVn), P(ds0),
+                      B, T, H, DK, DV, code, 1, sc, split, st),
+        "chunk_bwd": ("macai_gdr_chunk_bwd", P(q), P(k), P(v), P(g), P(beta), P(do), P(A), P(At), P(Sc), P(dSn),
+                      P(Vn), P(dVn), P(dq), P(dk), P(dv), P(dg), P(db), B, T, H, DK, DV, code, 1, sc, st),
+    }
+    order = ["prep_fwd", "state_fwd_out", "prep_bwd", "state_fwd_store", "state_bwd", "chunk_bwd"]
+    for name in order:                   # warm, and produce every input of the later passes
+        N.call(*calls[name])
+    torch.cuda.synchronize()
+    out = {}
+    for name in order:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            N.call(*calls[name])
+        e1.record()
+        e1.synchronize()
+        out[name] = e0.elapsed_time(e1) / reps * 1e-3     # seconds per launch
+    return out, split
+
+
+def cpu_baseline(cfg, threads):
+    """The reference's torch path (transformers' algorithm, float32, autograd backward) on the host CPU: B = 1 of the
+    config's rows (a bounded sample), 2 warm-up calls, then the median of 3."""
+    sys.path.insert(0, ROOT)
+    from oracle import gdr
+    torch.set_num_threads(threads)
+    c = dict(CONFIGS[cfg])
+    inp = gdr.make_inputs(1, c["T"], c["Hk"], c["Hv"], c["DK"], c["DV"], torch.float32, c["s0"], seed=1000 + cfg)
+    leaves = [inp[n].clone().requires_grad_(True) for n in ("query", "key", "value", "g", "beta")]
+
+    def step():
+        o, _ = gdr.torch_chunk_gated_delta_rule(*leaves, initial_state=inp["initial_state"], output_final_state=True,
+                                                use_qk_l2norm_in_kernel=True, inverse="solve")
+        torch.autograd.grad(o, leaves, inp["do"].float())
+
+    for _ in range(2):
+        step()
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        step()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    dt = ts[1]
+    return {"value": c["T"] / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"B=1 of config {cfg} (T={c['T']}, H={c['Hv']}, D={c['DK']}), fp32 fwd+bwd, median of 3 "
+                      f"after 2 warm-ups ({dt * 1e3:.0f} ms/call)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the gated delta rule has no cross-GPU step in this build "
+              "(head/batch sharding needs no collective); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    from macai.gated_delta import chunk_gated_delta_rule
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    inp, c = make_inputs(args.config, 1000 + args.config, dev)
+    leaves = [inp[n].requires_grad_(True) for n in ("query", "key", "value", "g", "beta")]
+    s0 = inp["initial_state"]
+    if s0 is not None:
+        s0.requires_grad_(True)
+        leaves.append(s0)
+    do = inp["do"]
+
+    def step():
+        o, _ = chunk_gated_delta_rule(*leaves[:5], initial_state=s0, output_final_state=False,
+                                      use_qk_l2norm_in_kernel=True)
+        return torch.autograd.grad(o, leaves, do)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu = e0.elapsed_time(e1) * 1e-3
+    elapsed = max(wall, gpu)
+    B, T, H, DK, DV = c["B"], c["T"], c["Hv"], c["DK"], c["DV"]
+    tokens = B * T
+    ms = elapsed / args.steps * 1e3
+
+    ktime, split = time_kernels(inp)
+    cost = kernel_costs(B, T, H, DK, DV)
+    kernels = {}
+    for name, t in ktime.items():
+        bw = cost[name]["bytes"] / t
+        fl = cost[name]["flops"] / t
+        kernels[name] = {"us": round(t * 1e6, 2), "GB/s": round(bw / 1e9, 1), "hbm_frac": round(bw / HBM_PEAK, 4),
+                         "TFLOP/s": round(fl / 1e12, 2), "mfma_frac": round(fl / MFMA_PEAK["bf16"], 4)}
+    dom = max(ktime, key=ktime.get)
+    bw = cost[dom]["bytes"] / ktime[dom]
+    roof = {"kernel": dom, "bound": "hbm", "achieved": round(bw / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+            "frac": round(bw / HBM_PEAK, 4), "traffic": TRAFFIC.get(dom)}
+    line = {"metric": METRIC, "value": round(tokens / (elapsed / args.steps), 1), "unit": "tokens/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": round(tokens / (elapsed / args.steps) / PUBLISHED, 2)
+            if args.config == 1 else None,
+            "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": f"gated-delta drop-in fwd+bwd, BASELINE config {args.config}", "B": B, "T": T,
+                       "Hk": c["Hk"], "Hv": H, "DK": DK, "DV": DV, "chunk": C, "l2norm_in_kernel": True,
+                       "initial_state": c["s0"], "value_split": split},
+            "roofline": roof, "kernels": kernels}
+    if not args.no_cpu:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        line["cpu_baseline"] = cpu_baseline(args.config, threads)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

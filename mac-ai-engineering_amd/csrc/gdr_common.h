@@ -146,29 +146,45 @@ __device__ __forceinline__ float across_groups_sum(float x) {
 }
 
 // ---- chunk scalars ------------------------------------------------------------------------------------------------
-// One wave: lane t = chunk row t.  g is the log decay (0 on padding rows).  Writes G (in-chunk cumulative log decay),
-// gam = exp(G), e = exp(G_last - G) for the 64 rows into LDS; G_last = G[63] (padding rows add 0).
+// One wave: lane t = chunk row t.  g is the log decay (0 on padding rows).  G (the in-chunk cumulative log decay) is
+// scanned in double: under strong decay |G| reaches ~1e3 within a chunk, where one fp32 ulp (6e-5) would become a
+// relative error of exp(G_i - G_j) -- the decays are formed from the double differences.  G_last is G of the last
+// valid row exactly (padding rows copy it), so e = exp(G_last - G) is exactly 1 on that row.
 struct ChunkScalars {
-  float G[C];
-  float gam[C];
-  float e[C];
+  double G[C];
+  float gam[C];    // exp(G_r)
+  float e[C];      // exp(G_last - G_r)
   float beta[C];
+  // exp(G_i - G_j) for i >= j (masked before the exponent by the caller)
+  __device__ __forceinline__ float decay(int i, int j) const { return expf((float)(G[i] - G[j])); }
 };
+
+__device__ __forceinline__ double wave_incl_scan_d(double x) {
+  const int l = lane_id();
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    double y = __shfl_up(x, off, 64);
+    if (l >= off) x += y;
+  }
+  return x;
+}
 
 __device__ __forceinline__ void chunk_scalars(ChunkScalars& cs, const float* g, const float* beta, size_t row_base,
                                               size_t row_stride, int t0, int T) {
   const int l = lane_id();
   const int t = t0 + l;
+  const int last = (T - t0 < C ? T - t0 : C) - 1;
   float gv = 0.f, bv = 0.f;
   if (t < T) {
     gv = g[row_base + (size_t)t * row_stride];
     if (beta) bv = beta[row_base + (size_t)t * row_stride];
   }
-  float G = wave_incl_scan(gv);
-  float Gl = __shfl(G, 63, 64);
+  double G = wave_incl_scan_d((double)gv);
+  const double Gl = __shfl(G, last, 64);
+  if (l > last) G = Gl;
   cs.G[l] = G;
-  cs.gam[l] = expf(G);
-  cs.e[l] = expf(Gl - G);
+  cs.gam[l] = (float)exp(G);
+  cs.e[l] = (float)exp(Gl - G);
   cs.beta[l] = bv;
 }
 

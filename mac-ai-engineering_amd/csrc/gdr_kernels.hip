@@ -175,7 +175,7 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * mi + 4 * j + r;
-        const float gm = (row >= col) ? expf(cs.G[row] - cs.G[col]) : 0.f;   // mask before the exponent
+        const float gm = (row >= col) ? cs.decay(row, col) : 0.f;   // mask before the exponent
         sL[row * FP + col] = (row > col) ? cs.beta[row] * kk[r] * gm : 0.f;
         if (wantM) {
           const MT mv = from_f<MT>((row >= col) ? qk[r] * gm : 0.f);
@@ -670,7 +670,7 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * mi + 4 * j + r;
-        const float gm = (row >= s) ? expf(cs.G[row] - cs.G[s]) : 0.f;
+        const float gm = (row >= s) ? cs.decay(row, s) : 0.f;
         const float Mv = QK[mi][r] * gm;
         const float dMv = dOV[mi][r] * gm;
         sdM[row * CP + s] = from_f<MT>(dMv);
@@ -722,7 +722,7 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * mi + 4 * j + r;
         const float dl = (row > s) ? -dL[mi][r] : 0.f;
-        const float gm = (row > s) ? expf(cs.G[row] - cs.G[s]) : 0.f;
+        const float gm = (row > s) ? cs.decay(row, s) : 0.f;
         const float Pv = dl * gm;
         const float r2 = dl * KG[mi][r];
         pR2[mi][r] = r2;
@@ -843,7 +843,11 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
     // dg_t = sum_{s >= t} dG_s + sum_{r < t} E_r
     const float rev = __shfl(dG, C - 1 - r, 64);
     const float suf = __shfl(wave_incl_scan(rev), C - 1 - r, 64);
-    const float pre = wave_incl_scan(E) - E;
+    // exclusive prefix by a shift, not incl - E: E on the last valid row is O(1) while the earlier ones carry
+    // exp(G_last - G_r) and can be ~1e-9 of it; the subtraction would cancel them away
+    float Esh = __shfl_up(E, 1, 64);
+    if (r == 0) Esh = 0.f;
+    const float pre = wave_incl_scan(Esh);
     if (t < T) {
       a.dg[s_base + (size_t)t * H] = suf + pre;
       a.dbeta[s_base + (size_t)t * H] = db;

@@ -117,6 +117,18 @@ def chunked_forward(q, k, v, g, beta, s0, C=64):
     return _unchunk(torch.stack(O, 2), T), S, P
 
 
+def chunked_forward_segments(q, k, v, g, beta, s0, C=64, seg=4096):
+    """chunked_forward over segments of `seg` tokens (a multiple of C), the state carried between them: the same
+    arithmetic chunk by chunk with bounded memory, for long sequences.  Returns (o, sT)."""
+    assert seg % C == 0
+    S, outs = s0, []
+    for t0 in range(0, q.shape[1], seg):
+        sl = slice(t0, t0 + seg)
+        o, S, _ = chunked_forward(q[:, sl], k[:, sl], v[:, sl], g[:, sl], beta[:, sl], S, C)
+        outs.append(o)
+    return torch.cat(outs, 1), S
+
+
 def chunked_backward(q, k, v, g, beta, s0, do, dsT, C=64, P=None):
     """B1-B6 (q already normalised and scaled), dg in the reference's no-cancellation form (_chunked.py:1138-1176).
     Returns (dq, dk, dv, dg, dbeta, ds0) and the intermediates dict (adds dSn = dS_{c+1} per chunk and dVn)."""
@@ -166,7 +178,10 @@ def chunked_backward(q, k, v, g, beta, s0, do, dsT, C=64, P=None):
     dG = dG + bc * R2.sum(-1) - (bc[..., :, None] * R2).sum(-2)
     dG[..., -1] = dG[..., -1] + gam[..., -1] * (Sc * dSn).sum((-1, -2))
     E = e * (K * VndSt).sum(-1)
-    dg = torch.flip(torch.cumsum(torch.flip(dG, [-1]), -1), [-1]) + (torch.cumsum(E, -1) - E)
+    # exclusive prefix by shifting first: cumsum(E) - E would cancel E_t (O(1) on the last row) against the O(e^g)
+    # earlier terms under strong decay
+    Ex = torch.cat([torch.zeros_like(E[..., :1]), E[..., :-1]], -1)
+    dg = torch.flip(torch.cumsum(torch.flip(dG, [-1]), -1), [-1]) + torch.cumsum(Ex, -1)
     P = dict(P, dSn=dSn, dVn=dVn)
     return (_unchunk(dQ, T), _unchunk(dK, T), _unchunk(dV, T), _unchunk(dg, T), _unchunk(dbeta, T), dS), P
 
@@ -235,7 +250,7 @@ def torch_chunk_gated_delta_rule(query, key, value, g, beta, chunk_size=64, init
     g = g.reshape(B, H, -1, C)
     upper0 = torch.triu(torch.ones(C, C, dtype=torch.bool), diagonal=0)
     g = g.cumsum(dim=-1)
-    decay = ((g.unsqueeze(-1) - g.unsqueeze(-2)).tril().exp().float()).tril().to(compute_dtype)
+    decay = ((g.unsqueeze(-1) - g.unsqueeze(-2)).tril().exp()).tril()   # transformers' .float() is a no-op here
     attn = -((k_beta @ key.transpose(-1, -2)) * decay).masked_fill(upper0, 0)
     if inverse == "rowloop":
         for i in range(1, C):

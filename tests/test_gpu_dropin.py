@@ -1,0 +1,271 @@
+"""GPU parity of the drop-in and the autograd contract against the float64 oracle (reference tests/test_harness.py,
+test_gated_delta.py, test_chunking.py, test_layer.py:48-85 patterns).
+
+Bars (error = max|a - r| / max|r| per tensor, r = float64 on the same dtype-representable values):
+  * float32 inputs through the drop-in: every output and gradient <= 2 x the reference torch path's own float32 error
+    (transformers' algorithm in float32 on the CPU, oracle.torch_chunk_gated_delta_rule) -- the north-star bar;
+  * bfloat16 inputs: every output and gradient <= 1e-2 (the north star; the reference's own bf16 bar was 2e-2);
+  * the GatedDeltaRule contract on the harness cases: 2e-4, stress and nearly parallel keys 5e-4, long 1e-3
+    (reference tests/test_harness.py:34-97).
+"""
+import pytest
+import torch
+
+from macai.gated_delta import GatedDeltaRule, chunk_gated_delta_rule, op, recurrent_gated_delta_rule
+from oracle import gdr
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+NAMES = ("dquery", "dkey", "dvalue", "dg", "dbeta", "dstate")
+BF16_BAR = 1e-2
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def run_dropin(inp, grads=True, dsT=None, final=True):
+    """The drop-in on the GPU from the CPU inputs dict; returns (o, sT, grads dict) on the CPU."""
+    names = ("query", "key", "value", "g", "beta")
+    leaves = [inp[n].to(DEV).requires_grad_(grads) for n in names]
+    s0 = inp["initial_state"]
+    if s0 is not None:
+        s0 = s0.to(DEV).requires_grad_(grads)
+    o, sT = chunk_gated_delta_rule(*leaves, initial_state=s0, output_final_state=final, use_qk_l2norm_in_kernel=True)
+    g = {}
+    if grads:
+        outs, gos = [o], [inp["do"].to(DEV)]
+        if dsT is not None:
+            outs.append(sT)
+            gos.append(dsT.to(DEV))
+        torch.autograd.backward(outs, gos)
+        for n, x in zip(NAMES, leaves + ([s0] if s0 is not None else [])):
+            g[n] = x.grad.cpu()
+    torch.cuda.synchronize()
+    return o.detach().cpu(), (None if sT is None else sT.detach().cpu()), g
+
+
+def torch_path_errors(inp, ro, rsT, rg, dsT=None):
+    """The reference torch path's own float32 errors against float64 (the anchor of the 2x bar)."""
+    names = ("query", "key", "value", "g", "beta")
+    leaves = [inp[n].float().clone().requires_grad_(True) for n in names]
+    s0 = inp["initial_state"]
+    if s0 is not None:
+        s0 = s0.clone().requires_grad_(True)
+    o, sT = gdr.torch_chunk_gated_delta_rule(*leaves, initial_state=s0, output_final_state=True,
+                                             use_qk_l2norm_in_kernel=True, inverse="solve")
+    outs, gos = [o], [inp["do"].float()]
+    if dsT is not None:
+        outs.append(sT)
+        gos.append(dsT)
+    torch.autograd.backward(outs, gos)
+    e = {"o": gdr.rel(o, ro), "sT": gdr.rel(sT, rsT)}
+    for n, x in zip(NAMES, leaves + ([s0] if s0 is not None else [])):
+        e[n] = gdr.rel(x.grad, rg[n])
+    return e
+
+
+def check_dropin(inp, bar=None, anchor=False, dsT=None, grads=True):
+    ro, rsT, rg = gdr.dropin_f64(*(inp[n] for n in ("query", "key", "value", "g", "beta", "initial_state")),
+                                 do=inp["do"] if grads else None, dsT=dsT)
+    o, sT, g = run_dropin(inp, grads=grads, dsT=dsT)
+    errs = {"o": gdr.rel(o, ro), "sT": gdr.rel(sT, rsT)}
+    for n, x in g.items():
+        errs[n] = gdr.rel(x, rg[n])
+    bars = {n: bar for n in errs}
+    if anchor:
+        ref = torch_path_errors(inp, ro, rsT, rg, dsT)
+        bars = {n: 2 * ref[n] for n in errs}
+        _say("torch-path fp32 errors:", {k: f"{v:.2e}" for k, v in ref.items()})
+    _say("errors:", {k: f"{v:.2e}" for k, v in errs.items()})
+    bad = {n: (errs[n], bars[n]) for n in errs if not errs[n] <= bars[n]}
+    assert not bad, f"(error, bar) over the bar: {bad}"
+    return errs
+
+
+# ---- BASELINE configs ------------------------------------------------------------------------------------------------
+def test_config0_fp32_forward():
+    """Config 0: fp32, forward only, o and sT within 2x the torch path's fp32 error."""
+    _say("case config0")
+    inp = gdr.config_inputs(0)
+    ro, rsT, _ = gdr.dropin_f64(*(inp[n] for n in ("query", "key", "value", "g", "beta", "initial_state")))
+    with torch.no_grad():
+        o, sT, _ = run_dropin(inp, grads=False)
+        to, tsT = gdr.torch_chunk_gated_delta_rule(*(inp[n] for n in ("query", "key", "value", "g", "beta")),
+                                                   output_final_state=True, use_qk_l2norm_in_kernel=True)
+    e, a = (gdr.rel(o, ro), gdr.rel(sT, rsT)), (gdr.rel(to, ro), gdr.rel(tsT, rsT))
+    _say("errors", e, "torch path", a)
+    assert e[0] <= 2 * a[0] and e[1] <= 2 * a[1]
+
+
+@pytest.mark.parametrize("cfg", [1, 2])
+def test_config_bf16_fwd_bwd(cfg):
+    """Configs 1 and 2 at full size: bf16 q/k/v/dO, fp32 g/beta (config 2: Hk=16 repeated to Hv=32, an initial state
+    and its gradient, the final state used): every output and gradient within 1e-2."""
+    _say(f"case config{cfg}")
+    inp = gdr.config_inputs(cfg)
+    dsT = torch.randn(inp["value"].shape[0], inp["value"].shape[2], 128, 128,
+                      generator=torch.Generator().manual_seed(77)) if cfg == 2 else None
+    check_dropin(inp, bar=BF16_BAR, dsT=dsT)
+
+
+@pytest.mark.parametrize("Hv", [16, 32])
+def test_config3_long_prefill_forward(Hv):
+    """Config 3: one row of 32,768 tokens (512 sequential chunks), bf16, forward only, the final state returned."""
+    _say(f"case config3 Hv={Hv}")
+    inp = gdr.config_inputs(3, Hv=Hv)
+    names = ("query", "key", "value", "g", "beta")
+    with torch.no_grad():
+        o, sT = chunk_gated_delta_rule(*(inp[n].to(DEV) for n in names), output_final_state=True,
+                                       use_qk_l2norm_in_kernel=True)
+        torch.cuda.synchronize()
+    q, k = gdr.prologue(inp["query"].double(), inp["key"].double())
+    ro, rsT = gdr.chunked_forward_segments(q, k, inp["value"].double(), inp["g"].double(), inp["beta"].double(),
+                                           torch.zeros(1, Hv, 128, 128, dtype=torch.float64))
+    errs = (gdr.rel(o.cpu(), ro), gdr.rel(sT.cpu(), rsT))
+    _say("errors", errs)
+    assert max(errs) <= BF16_BAR
+
+
+def test_config4_decode_step():
+    """Config 4: one decode step per sequence (64 x 32 heads, fp32 state) through the recurrent drop-in, against the
+    oracle's one-step recurrence; the state's error is small enough to also hold at the fp32 2e-4 bar."""
+    _say("case config4")
+    inp = gdr.config_inputs(4)
+    names = ("query", "key", "value", "g", "beta")
+    with torch.no_grad():
+        o, sT = recurrent_gated_delta_rule(*(inp[n].to(DEV) for n in names), initial_state=inp["initial_state"].to(DEV),
+                                           output_final_state=True, use_qk_l2norm_in_kernel=True)
+        torch.cuda.synchronize()
+    q, k = gdr.prologue(inp["query"].double(), inp["key"].double())
+    ro, rs = gdr.decode_step(q[:, 0], k[:, 0], inp["value"].double()[:, 0], inp["g"].double()[:, 0],
+                             inp["beta"].double()[:, 0], inp["initial_state"].double())
+    errs = (gdr.rel(o.cpu()[:, 0], ro), gdr.rel(sT.cpu(), rs))
+    _say("errors", errs)
+    assert o.dtype == torch.bfloat16 and errs[0] <= BF16_BAR and errs[1] <= 2e-4
+
+
+# ---- float32 drop-in at the north-star bar ---------------------------------------------------------------------------
+@pytest.mark.parametrize("shape,s0", [((2, 100, 4, 128), True), ((1, 256, 4, 64), False), ((2, 512, 16, 128), False),
+                                      ((1, 45, 3, 128), True)])
+def test_dropin_fp32_within_twice_the_torch_path(shape, s0):
+    """Every output and gradient (final-state gradient included) <= 2 x the torch path's own fp32 error vs float64
+    (reference tests/test_gated_delta.py:37-56 shape first; test_layer.py:48-85 bar)."""
+    B, T, H, D = shape
+    _say(f"case dropin_fp32 {shape} s0={s0}")
+    inp = gdr.make_inputs(B, T, H, H, D, D, torch.float32, s0=s0, seed=1)
+    dsT = torch.randn(B, H, D, D, generator=torch.Generator().manual_seed(9))
+    check_dropin(inp, anchor=True, dsT=dsT)
+
+
+@pytest.mark.parametrize("shape", [(2, 50, 3, 128), (2, 45, 3, 128), (1, 1, 2, 64), (3, 130, 2, 32)])
+def test_dropin_bf16_small(shape):
+    """bf16 drop-in end to end with a starting state and the final state used (reference test_harness.py:139-166)."""
+    B, T, H, D = shape
+    _say(f"case dropin_bf16 {shape}")
+    inp = gdr.make_inputs(B, T, H, H, D, D, torch.bfloat16, s0=True, seed=8)
+    dsT = torch.randn(B, H, D, D, generator=torch.Generator().manual_seed(9))
+    check_dropin(inp, bar=BF16_BAR, dsT=dsT)
+
+
+def test_golden_fixture():
+    """The committed fixture (autograd through the recurrence in float64): the bf16 drop-in within 1e-2."""
+    import os
+
+    import numpy as np
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "dropin_small.npz"))
+    t = {n: torch.from_numpy(z[n]) for n in z.files}
+    inp = {n: t[n].to(torch.bfloat16) for n in ("query", "key", "value", "do")}
+    inp.update(g=t["g"], beta=t["beta"], initial_state=t["initial_state"])
+    o, sT, g = run_dropin(inp, dsT=t["dsT"])
+    errs = {"o": gdr.rel(o, t["o"]), "sT": gdr.rel(sT, t["sT"])}
+    errs.update({n: gdr.rel(x, t[n]) for n, x in g.items()})
+    _say("errors:", errs)
+    assert max(errs.values()) <= BF16_BAR
+
+
+# ---- the GatedDeltaRule contract on the reference harness cases ------------------------------------------------------
+def check_rule(xs64, rtol, dtype=torch.float32):
+    gen = torch.Generator().manual_seed(9)
+    xs = [x.to(dtype if i < 3 else torch.float32).to(DEV).requires_grad_(True) for i, x in enumerate(xs64)]
+    o, sT = GatedDeltaRule.apply(*xs, True)
+    ref = [x.to(dtype if i < 3 else torch.float32).double() for i, x in enumerate(xs64)]
+    w_o = torch.randn(o.shape, generator=gen, dtype=torch.float64)
+    w_s = torch.randn(sT.shape, generator=gen, dtype=torch.float64)
+    torch.autograd.backward([o, sT], [w_o.to(DEV, o.dtype), w_s.float().to(DEV)])
+    ro, rsT, P = gdr.chunked_forward(*ref)
+    rg, _ = gdr.chunked_backward(*ref, w_o.to(o.dtype).double(), w_s.float().double(), P=P)
+    errs = {"o": gdr.rel(o.cpu(), ro), "sT": gdr.rel(sT.cpu(), rsT)}
+    for n, a, r in zip(("dq", "dk", "dv", "dg", "dbeta", "ds0"), xs, rg):
+        errs[n] = gdr.rel(a.grad.cpu(), r)
+    _say("errors:", {k: f"{v:.2e}" for k, v in errs.items()})
+    bad = {k: v for k, v in errs.items() if not v <= rtol}
+    assert not bad, f"relative errors over {rtol}: {bad}"
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1, 128, 128), (1, 2, 1, 128, 128), (2, 7, 3, 128, 128), (1, 8, 2, 128, 128),
+                                   (1, 9, 2, 128, 128), (3, 63, 2, 128, 128), (1, 64, 1, 128, 128), (2, 65, 2, 128, 64),
+                                   (1, 100, 5, 64, 64), (1, 31, 2, 64, 32)])
+def test_rule_shapes(shape):
+    _say(f"case rule_shapes {shape}")
+    check_rule(gdr.harness_inputs(*shape), 2e-4)
+
+
+def test_rule_no_starting_state():
+    _say("case rule_no_state")
+    check_rule(gdr.harness_inputs(2, 40, 2, 128, 128, state=False), 2e-4)
+
+
+@pytest.mark.parametrize("beta,g", [(0.0, None), (1.0 - 1e-6, None), (None, 0.0), (None, -20.0), (1.0 - 1e-6, 0.0)])
+def test_rule_stress(beta, g):
+    _say(f"case rule_stress beta={beta} g={g}")
+    check_rule(gdr.harness_inputs(1, 48, 2, 128, 128, beta=beta, g=g), 5e-4)
+
+
+@pytest.mark.parametrize("beta,g", [(None, None), (1.0 - 1e-6, 0.0), (1.0 - 1e-6, None)])
+def test_rule_correlated_keys(beta, g):
+    _say(f"case rule_corr beta={beta} g={g}")
+    xs = gdr.harness_inputs(1, 96, 2, 128, 128, beta=beta, g=g, corr=0.9, seed=6)
+    assert (xs[1][0, 1:, 0] * xs[1][0, :-1, 0]).sum(-1).min() > 0.95
+    check_rule(xs, 5e-4)
+
+
+@pytest.mark.parametrize("T", [2048, 4096])
+def test_rule_long_sequence(T):
+    _say(f"case rule_long T={T}")
+    check_rule(gdr.harness_inputs(1, T, 1, 128, 128, seed=3), 1e-3)
+
+
+def test_rule_bf16_operands():
+    """The contract with bf16 q/k/v (bf16 MFMA operands, fp32 accumulation): within 1e-2."""
+    _say("case rule_bf16")
+    check_rule(gdr.harness_inputs(2, 100, 2, 128, 128, seed=4), BF16_BAR, dtype=torch.bfloat16)
+
+
+# ---- determinism and launch-policy invariance ------------------------------------------------------------------------
+def _grads_once(inp, split=None):
+    old = op.VALUE_SPLIT
+    try:
+        if split is not None:
+            op.VALUE_SPLIT = split
+        o, sT, g = run_dropin(inp, dsT=torch.ones(inp["value"].shape[0], inp["value"].shape[2], 128, 128))
+    finally:
+        op.VALUE_SPLIT = old
+    return [o, sT] + [g[n] for n in sorted(g)]
+
+
+def test_backward_is_bitwise_deterministic():
+    """One writer per gradient element, no atomics: three runs give identical bits (reference test_harness.py:196-211)."""
+    _say("case determinism")
+    inp = gdr.make_inputs(2, 100, 2, 2, 128, 128, torch.bfloat16, s0=True, seed=5)
+    runs = [_grads_once(inp) for _ in range(3)]
+    assert all(torch.equal(a, b) for r in runs[1:] for a, b in zip(runs[0], r))
+
+
+def test_value_split_changes_no_bits():
+    """Splitting a head-row's value columns over 1, 2, 4 or 8 workgroups changes no arithmetic: identical bits
+    (reference test_chunking.py:108-128)."""
+    _say("case split bits")
+    inp = gdr.make_inputs(1, 150, 3, 3, 128, 128, torch.bfloat16, s0=True, seed=6)
+    runs = [_grads_once(inp, s) for s in (1, 2, 4, 8)]
+    assert all(torch.equal(a, b) for r in runs[1:] for a, b in zip(runs[0], r))

@@ -1,0 +1,136 @@
+"""Host-side checks that need no GPU: the C-ABI library loads and exports every symbol include/macai_gdr.h declares
+with the argument counts the binding uses, rejects bad arguments with the documented codes before any launch, and the
+Python layer's refusals, launch policy and installer (reference tests/test_harness.py:169-173, test_chunking.py:176-199,
+patch.py:33-98)."""
+import os
+import re
+
+import pytest
+import torch
+
+from macai.gated_delta import _native as N
+from macai.gated_delta import chunk_gated_delta_rule, op
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "macai_gdr.h")
+
+
+def _declared():
+    """(name, number of parameters) of every function the header declares."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(?:int|const char\s*\*)\s+(macai_gdr_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = [p for p in m.group(2).split(",") if p.strip() and p.strip() != "void"]
+        out[m.group(1)] = len(params)
+    return out
+
+
+def test_library_exports_every_declared_symbol():
+    decl = _declared()
+    assert {"macai_gdr_prep", "macai_gdr_state_fwd", "macai_gdr_state_bwd", "macai_gdr_chunk_bwd", "macai_gdr_decode",
+            "macai_gdr_last_error", "macai_gdr_abi_version"} <= set(decl)
+    lib = N.lib()
+    for name in decl:
+        assert hasattr(lib, name), name
+    for name, args in N.SIGNATURES.items():
+        assert decl[name] == len(args), (name, decl[name], len(args))
+    assert lib.macai_gdr_abi_version() == N.ABI_VERSION
+
+
+def _prep(**over):
+    a = dict(q=1 << 20, k=1 << 20, v=1 << 20, g=1 << 20, beta=1 << 20, W=1 << 20, U=1 << 20, M=None, Mt=None, A=None,
+             At=None, B=1, T=64, H=1, DK=128, DV=128, dtype=1, l2=1, scale=1.0, stream=None)
+    a.update(over)
+    return N.lib().macai_gdr_prep(*a.values())
+
+
+def test_abi_rejects_bad_arguments_before_launch():
+    L = N.lib()
+    assert _prep(DK=96) == N.EUNSUP and b"key head width" in L.macai_gdr_last_error()
+    assert _prep(DV=48) == N.EUNSUP and b"value head width" in L.macai_gdr_last_error()
+    assert _prep(dtype=7) == N.EUNSUP
+    assert _prep(T=0) == N.EINVAL
+    assert _prep(k=None) == N.EINVAL and b"null" in L.macai_gdr_last_error()
+    assert _prep(A=1 << 20) == N.EINVAL and b"A and At" in L.macai_gdr_last_error()
+    assert _prep(W=(1 << 20) + 4) == N.EINVAL and b"aligned" in L.macai_gdr_last_error()
+    assert _prep(M=1 << 20, q=None) == N.EINVAL
+    p = 1 << 20
+    # state pass: flags that ask for nothing, a split that does not divide DV / 16, a missing output
+    assert L.macai_gdr_state_fwd(p, p, p, p, p, p, None, p, None, None, None, 1, 64, 1, 128, 128, 1, 1, 1.0, 8, 0,
+                                 None) == N.EINVAL
+    assert L.macai_gdr_state_fwd(p, p, p, p, p, p, None, p, None, None, None, 1, 64, 1, 128, 128, 1, 1, 1.0, 0, 3,
+                                 None) == N.EINVAL
+    assert b"split" in L.macai_gdr_last_error()
+    assert L.macai_gdr_state_fwd(p, p, p, p, p, None, None, p, None, None, None, 1, 64, 1, 128, 128, 1, 1, 1.0, 0, 0,
+                                 None) == N.EINVAL
+    assert L.macai_gdr_state_bwd(p, p, p, p, p, None, None, p, p, p, 1, 64, 1, 128, 128, 1, 1, 1.0, 0,
+                                 None) == N.EINVAL
+    assert L.macai_gdr_chunk_bwd(*([p] * 16), None, 1, 64, 1, 128, 128, 1, 1, 1.0, None) == N.EINVAL
+    assert L.macai_gdr_decode(p, p, p, p, p, p, p, p, 1, 1, 256, 128, 1, 1, 1.0, None) == N.EUNSUP
+
+
+def test_call_maps_codes_to_exceptions():
+    with pytest.raises(NotImplementedError, match="key head width"):
+        N.call("macai_gdr_prep", *([1 << 20] * 7), None, None, None, None, 1, 64, 1, 96, 128, 1, 1, 1.0, None)
+    with pytest.raises(ValueError, match="null"):
+        N.call("macai_gdr_prep", *([None] * 11), 1, 64, 1, 128, 128, 1, 1, 1.0, None)
+
+
+def test_packed_rows_refused():
+    """cu_seqlens is refused before anything else (reference op.py:270-273; tests/test_harness.py:169-173)."""
+    x = torch.zeros(1, 4, 1, 128)
+    with pytest.raises(NotImplementedError):
+        chunk_gated_delta_rule(x, x, x, x[..., 0], x[..., 0], cu_seqlens=torch.tensor([0, 2, 4]))
+
+
+def test_cpu_tensors_refused_loudly():
+    """No CPU fallback: the product path raises on tensors that are not on a HIP device."""
+    x = torch.zeros(1, 4, 1, 128)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        chunk_gated_delta_rule(x, x, x, x[..., 0], x[..., 0])
+
+
+def test_split_rule():
+    """VALUE_SPLIT 'auto': the smallest power-of-two split giving >= 256 workgroups, capped at DV / 16 slices; an int
+    setting rounds down to a divisor (reference op.split_for semantics, test_chunking.py:176-199)."""
+    assert op.split_for(64, 1024, 128) == 4
+    assert op.split_for(16, 32768, 128) == 8
+    assert op.split_for(512, 1024, 128) == 1
+    assert op.split_for(2048, 1, 128) == 1
+    assert op.split_for(1, 64, 32) == 2
+    old = op.VALUE_SPLIT
+    try:
+        op.VALUE_SPLIT = 3
+        assert op.split_for(64, 1024, 128) == 2
+        op.VALUE_SPLIT = 16
+        assert op.split_for(64, 1024, 128) == 8
+    finally:
+        op.VALUE_SPLIT = old
+
+
+def test_patch_swaps_the_name_and_restores_it():
+    mod = pytest.importorskip("transformers.models.qwen3_5.modeling_qwen3_5")
+    import macai.patch as patch
+    from macai.gated_delta import recurrent_gated_delta_rule
+    orig, orig_dec = mod.torch_chunk_gated_delta_rule, mod.torch_recurrent_gated_delta_rule
+    with patch.installed(decode=True):
+        assert mod.torch_chunk_gated_delta_rule is chunk_gated_delta_rule
+        assert mod.torch_recurrent_gated_delta_rule is recurrent_gated_delta_rule
+    assert mod.torch_chunk_gated_delta_rule is orig and mod.torch_recurrent_gated_delta_rule is orig_dec
+    done = patch.install()
+    try:
+        assert ("transformers.models.qwen3_5.modeling_qwen3_5", patch.NAME) in done
+        assert mod.torch_recurrent_gated_delta_rule is orig_dec
+        assert patch.install() == []           # idempotent
+    finally:
+        patch.uninstall()
+    assert mod.torch_chunk_gated_delta_rule is orig
+
+
+def test_product_never_imports_the_oracle():
+    pkg = os.path.join(ROOT, "mac-ai-engineering_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".h", ".cpp")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert not re.search(r"^\s*(from|import)\s+oracle\b", text, re.M), f
