@@ -69,20 +69,21 @@ def kernel_costs(B, T, H, DK, DV, es=2):
     io_k, io_v = tok * DK * es, tok * DV * es
     gb = tok * 4 * 2                     # g and beta
     cdk, cdv, cc = C * DK, C * DV, C * C
+    sdk = DK * DV * 4                    # one fp32 state
     cost = {}
-    # the forward
-    cost["prep_fwd"] = dict(bytes=2 * io_k + io_v + gb + n * (cdk * es + cdv * 4 + cc * es),
+    # the forward: prep writes W, U, KeT, GL, Qg, M; the state pass reads them and writes o
+    cost["prep_fwd"] = dict(bytes=2 * io_k + io_v + gb + n * (3 * cdk * es + cdv * 4 + cc * es + 4),
                             flops=n * (2 * 2 * cc * DK + cc * C / 3 + 2 * cc * DK + 2 * cc * DV))
-    cost["state_fwd_out"] = dict(bytes=2 * io_k + tok * 4 + n * (cdk * es + cdv * 4 + cc * es) + io_v,
+    cost["state_fwd_out"] = dict(bytes=n * (3 * cdk * es + cdv * 4 + cc * es + 4) + io_v,
                                  flops=n * (3 * 2 * C * DK * DV + 2 * cc * DV))
-    # the backward
-    cost["prep_bwd"] = dict(bytes=io_k + io_v + gb + n * (cdk * es + cdv * 4 + cc * es + 2 * cc * 4),
-                            flops=n * (2 * cc * DK + cc * C / 3 + 2 * cc * DK + 2 * cc * DV))
-    cost["state_fwd_store"] = dict(bytes=io_k + tok * 4 + n * (cdk * es + cdv * 4 + DK * DV * 4 + cdv * 4),
+    # the backward: prep writes W, U, KeT, GL, Ke, QgT, WT, Mt, A, At
+    cost["prep_bwd"] = dict(bytes=2 * io_k + io_v + gb + n * (5 * cdk * es + cdv * 4 + cc * es + 2 * cc * 4 + 4),
+                            flops=n * (2 * 2 * cc * DK + cc * C / 3 + 2 * cc * DK + 2 * cc * DV))
+    cost["state_fwd_store"] = dict(bytes=n * (2 * cdk * es + cdv * 4 + 4 + sdk + cdv * 4),
                                    flops=n * (2 * 2 * C * DK * DV))
-    cost["state_bwd"] = dict(bytes=2 * io_k + tok * 4 + io_v + n * (cdk * es + cc * es + DK * DV * 4 + cdv * 4),
+    cost["state_bwd"] = dict(bytes=n * (3 * cdk * es + cc * es + 4 + sdk + cdv * 4) + io_v,
                              flops=n * (3 * 2 * C * DK * DV + 2 * cc * DV))
-    cost["chunk_bwd"] = dict(bytes=2 * io_k + 2 * io_v + gb + n * (2 * cc * 4 + 2 * DK * DV * 4 + 2 * cdv * 4)
+    cost["chunk_bwd"] = dict(bytes=2 * io_k + 2 * io_v + gb + n * (2 * cc * 4 + 2 * sdk + 2 * cdv * 4)
                              + 2 * io_k + io_v + gb,
                              flops=n * (3 * 2 * C * DK * DV + 2 * cc * DK + 3 * 2 * cc * DK + 2 * 2 * cc * DV
                                         + 2 * 2 * cc * C + 3 * 2 * cc * DK + 2 * cc * DV))
@@ -103,29 +104,27 @@ def time_kernels(inp, reps=20):
     code, st = N.dtype_code(dt), N.stream_of(q)
     sc = DK ** -0.5
     split = op.split_for(B * H, T, DV)
-    W = torch.empty(B, H, NT, C, DK, device=dev, dtype=dt)
-    U = torch.empty(B, H, NT, C, DV, device=dev, dtype=f32)
-    M = torch.empty(B, H, NT, C, C, device=dev, dtype=dt)
-    Mt, A, At = torch.empty_like(M), torch.empty(B, H, NT, C, C, device=dev, dtype=f32), None
-    At = torch.empty_like(A)
+    e = lambda *shape, d=dt: torch.empty(*shape, device=dev, dtype=d)
+    W, U, KeT, GL, Qg, M = e(B, H, NT, C, DK), e(B, H, NT, C, DV, d=f32), e(B, H, NT, DK, C), e(B, H, NT, d=f32), \
+        e(B, H, NT, C, DK), e(B, H, NT, C, C)
+    Ke, QgT, WT, Mt = e(B, H, NT, C, DK), e(B, H, NT, DK, C), e(B, H, NT, DK, C), e(B, H, NT, C, C)
+    A, At = e(B, H, NT, C, C, d=f32), e(B, H, NT, C, C, d=f32)
     o = torch.empty_like(v)
-    Sc = torch.empty(B, H, NT, DK, DV, device=dev, dtype=f32)
-    Vn = torch.empty(B, H, NT, C, DV, device=dev, dtype=f32)
-    dSn, dVn = torch.empty_like(Sc), torch.empty_like(Vn)
-    ds0 = torch.empty(B, H, DK, DV, device=dev, dtype=f32)
+    Sc, Vn = e(B, H, NT, DK, DV, d=f32), e(B, H, NT, C, DV, d=f32)
+    dSn, dVn, ds0 = torch.empty_like(Sc), torch.empty_like(Vn), e(B, H, DK, DV, d=f32)
     dq, dk, dv, dg, db = (torch.empty_like(x) for x in (q, k, v, g, beta))
     P = N.ptr
     calls = {
-        "prep_fwd": ("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), P(M), None, None, None,
-                     B, T, H, DK, DV, code, 1, sc, st),
-        "state_fwd_out": ("macai_gdr_state_fwd", P(q), P(k), P(g), P(W), P(U), P(M), P(s0), P(o), None, None, None,
-                          B, T, H, DK, DV, code, 1, sc, 0, split, st),
-        "prep_bwd": ("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), None, P(Mt), P(A), P(At),
-                     B, T, H, DK, DV, code, 1, sc, st),
-        "state_fwd_store": ("macai_gdr_state_fwd", P(q), P(k), P(g), P(W), P(U), None, P(s0), None, None, P(Sc), P(Vn),
-                            B, T, H, DK, DV, code, 1, sc, N.STORE_STATES | N.NO_OUTPUT, split, st),
-        "state_bwd": ("macai_gdr_state_bwd", P(q), P(k), P(g), P(W), P(Mt), P(do), None, P(dSn), P(dVn), P(ds0),
-                      B, T, H, DK, DV, code, 1, sc, split, st),
+        "prep_fwd": ("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), P(KeT), P(GL), P(Qg), P(M),
+                     None, None, None, None, None, None, B, T, H, DK, DV, code, 1, sc, st),
+        "state_fwd_out": ("macai_gdr_state_fwd", P(W), P(U), P(KeT), P(GL), P(Qg), P(M), P(s0), P(o), None, None,
+                          None, B, T, H, DK, DV, code, 0, split, st),
+        "prep_bwd": ("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), P(KeT), P(GL), None, None, P(Ke),
+                     P(QgT), P(WT), P(Mt), P(A), P(At), B, T, H, DK, DV, code, 1, sc, st),
+        "state_fwd_store": ("macai_gdr_state_fwd", P(W), P(U), P(KeT), P(GL), None, None, P(s0), None, None, P(Sc),
+                            P(Vn), B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, st),
+        "state_bwd": ("macai_gdr_state_bwd", P(Ke), P(QgT), P(WT), P(Mt), P(GL), P(do), None, P(dSn), P(dVn), P(ds0),
+                      B, T, H, DK, DV, code, split, st),
         "chunk_bwd": ("macai_gdr_chunk_bwd", P(q), P(k), P(v), P(g), P(beta), P(do), P(A), P(At), P(Sc), P(dSn),
                       P(Vn), P(dVn), P(dq), P(dk), P(dv), P(dg), P(db), B, T, H, DK, DV, code, 1, sc, st),
     }

@@ -12,13 +12,16 @@
  *   v, o, dO    [B, T, H, DV]   dtype
  *   g, beta     [B, T, H]       float32   (g = log decay <= 0)
  *   states      [B, H, DK, DV]  float32   (initial_state, final state, their gradients)
- *   per chunk   NT = ceil(T / 64) chunks of 64 tokens, padding rows zero:
- *     W   [B, H, NT, 64, DK] dtype     W = A diag(beta gamma) K^
- *     U   [B, H, NT, 64, DV] float32   U = A diag(beta) V
- *     M   [B, H, NT, 64, 64] dtype     M = (Q^ K^T) * exp(G_i - G_j), lower with the diagonal;  Mt = M^T
- *     A   [B, H, NT, 64, 64] float32   A = (I + L)^-1;  At = A^T
- *     Sc, dSn [B, H, NT, DK, DV] float32   state entering each chunk; dLoss/dS_{c+1}
- *     Vn, dVn [B, H, NT, 64, DV] float32   per-token corrections U - W S_c and their gradient
+ *   per chunk   NT = ceil(T / 64) chunks of 64 tokens, padding rows zero (written by macai_gdr_prep):
+ *     W, Qg, Ke   [B, H, NT, 64, DK] dtype   W = A diag(beta gamma) K^;  diag(gamma) Q^;  diag(e) K^
+ *     KeT, QgT, WT [B, H, NT, DK, 64] dtype  (diag(e) K^)^T, (diag(gamma) Q^)^T, W^T
+ *     U           [B, H, NT, 64, DV] float32  U = A diag(beta) V
+ *     M, Mt       [B, H, NT, 64, 64] dtype   M = (Q^ K^T) * exp(G_i - G_j) (lower with the diagonal); M^T
+ *     A, At       [B, H, NT, 64, 64] float32 A = (I + L)^-1; A^T
+ *     GL          [B, H, NT]         float32 exp(G_last) of each chunk
+ *     Sc, dSn     [B, H, NT, DK, DV] float32 state entering each chunk; dLoss/dS_{c+1}
+ *     Vn, dVn     [B, H, NT, 64, DV] float32 per-token corrections U - W S_c and their gradient
+ *   G_r = sum_{s<=r} g_s inside the chunk, gamma = exp(G), e = exp(G_last - G), q^ / k^ the prologue's outputs.
  * With use_l2norm = 1 the kernels apply the reference prologue (_norm.py:1-10) themselves: q^ = q * rsqrt(|q|^2 + 1e-6)
  * * q_scale, k^ = k * rsqrt(|k|^2 + 1e-6), and the backward returns gradients w.r.t. the raw q and k.
  * Supported widths: DK in {32, 64, 128}; DV a multiple of 32 up to 512.  Pointers must be 16-byte aligned.
@@ -35,7 +38,7 @@
 extern "C" {
 #endif
 
-#define MACAI_GDR_ABI_VERSION 1
+#define MACAI_GDR_ABI_VERSION 2
 
 /* dtype codes */
 #define MACAI_GDR_F32 0
@@ -54,31 +57,32 @@ extern "C" {
 const char* macai_gdr_last_error(void);
 int macai_gdr_abi_version(void);
 
-/* Per-chunk preparation (north star (1), the intra-chunk kernel): G, L, A = (I + L)^-1, W, U, and M and/or Mt when
- * given, A and At when given.  Replaces `lib.gdc_prep(q, k, g, beta, gc, a, m, kg, T, H, ...)` (reference
+/* Per-chunk preparation (north star (1), the intra-chunk kernel), every chunk independent: G, L, A = (I + L)^-1,
+ * W, U, KeT and GL always; each other output when its pointer is non-NULL (the forward needs Qg and M; the backward
+ * Ke, QgT, WT, Mt, A and At).  Replaces `lib.gdc_prep(q, k, g, beta, gc, a, m, kg, T, H, ...)` (reference
  * op.py:63-72; kernel _chunked.py:220-313) and the fused prologue l2n_fwd (_norm.py:97). */
 int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, const float* beta, void* W, float* U,
-                   void* M, void* Mt, float* A, float* At, int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV,
-                   int32_t dtype, int32_t use_l2norm, float q_scale, void* stream);
+                   void* KeT, float* GL, void* Qg, void* M, void* Ke, void* QgT, void* WT, void* Mt, float* A, float* At,
+                   int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm,
+                   float q_scale, void* stream);
 
 /* The sequential state pass (north star (2) + (3)): S <- exp(G_last) S + K^T diag(e) (U - W S) over the chunks from
- * s0 (NULL = zeros), with the output O = diag(gamma) Q S + M Vn written to o (dtype) unless MACAI_GDR_NO_OUTPUT, the
- * final state to sT when sT != NULL, and Sc / Vn when MACAI_GDR_STORE_STATES.  split = workgroups per head-row's
- * value columns (a divisor of DV / 16; 0 = automatic).  Replaces `lib.gdc_fwd(q, k, v, beta, s0, gc, a, m, o, sT, sc,
- * vn, xu, ckpt, T, H, DV, flags, ...)` (reference op.py:159, 217; kernel _chunked.py:315-659). */
-int macai_gdr_state_fwd(const void* q, const void* k, const float* g, const void* W, const float* U, const void* M,
+ * s0 (NULL = zeros).  flags = 0: the output O = diag(gamma) Q S + M Vn to o (dtype) and the final state to sT when
+ * sT != NULL (needs Qg, M); flags = STORE_STATES | NO_OUTPUT: Sc and Vn for the backward.  split = workgroups per
+ * head-row's value columns (DV / 16 / split must be 1, 2, 4 or 8; 0 = automatic).  Replaces `lib.gdc_fwd(q, k, v,
+ * beta, s0, gc, a, m, o, sT, sc, vn, xu, ckpt, T, H, DV, flags, ...)` (reference op.py:159, 217; kernel
+ * _chunked.py:315-659). */
+int macai_gdr_state_fwd(const void* W, const float* U, const void* KeT, const float* GL, const void* Qg, const void* M,
                         const float* s0, void* o, float* sT, float* Sc, float* Vn, int64_t B, int64_t T, int64_t H,
-                        int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, int32_t flags,
-                        int32_t split, void* stream);
+                        int64_t DK, int64_t DV, int32_t dtype, int32_t flags, int32_t split, void* stream);
 
 /* The reverse state pass (north star (4)): from dS_NT = dsT (NULL = zeros) back over the chunks, dVn = M^T dO +
  * diag(e) K dS, dS <- exp(G_last) dS + (diag(gamma) Q)^T dO - W^T dVn; stores dSn (= dS_{c+1}) and dVn per chunk and
  * writes ds0 = dLoss/d initial_state.  Replaces `lib.gdc_bwd_state(q, k, beta, do, dsT, gc, a, m, dsn, dvn, ds0, T,
  * H, DV, ...)` (reference op.py:234; kernel _chunked.py:661-903). */
-int macai_gdr_state_bwd(const void* q, const void* k, const float* g, const void* W, const void* Mt, const void* dO,
-                        const float* dsT, float* dSn, float* dVn, float* ds0, int64_t B, int64_t T, int64_t H,
-                        int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, int32_t split,
-                        void* stream);
+int macai_gdr_state_bwd(const void* Ke, const void* QgT, const void* WT, const void* Mt, const float* GL,
+                        const void* dO, const float* dsT, float* dSn, float* dVn, float* ds0, int64_t B, int64_t T,
+                        int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t split, void* stream);
 
 /* The per-chunk backward (north star (4)): dq, dk (w.r.t. the raw inputs when use_l2norm), dv in dtype; dg, dbeta in
  * float32; one writer per element (bitwise deterministic).  Replaces `lib.gdc_bwd_chunk(q, k, beta, do, gc, a, kg, m,

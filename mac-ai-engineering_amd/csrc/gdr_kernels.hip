@@ -27,6 +27,7 @@
 
 #include "gdr_common.h"
 #include "gdr_stage.h"
+#include "gdr_lds.h"
 #include "macai_gdr.h"
 
 namespace gdr {
@@ -39,45 +40,45 @@ struct PrepArgs {
   const float *g, *beta;
   void* W;       // [B,H,NT,C,DK] MT   W = A diag(beta gamma) K^
   float* U;      // [B,H,NT,C,DV] fp32 U = A diag(beta) V
-  void* M;       // [B,H,NT,C,C]  MT   M (row-major [t][s]) or null
-  void* Mt;      // [B,H,NT,C,C]  MT   M^T ([s][t]) or null
-  float* A;      // [B,H,NT,C,C]  fp32 A or null
-  float* At;     // [B,H,NT,C,C]  fp32 A^T or null
+  void* KeT;     // [B,H,NT,DK,C] MT   (diag(e) K^)^T
+  float* GL;     // [B,H,NT]      fp32 exp(G_last)
+  void* Qg;      // [B,H,NT,C,DK] MT   diag(gamma) Q^            (or null)
+  void* M;       // [B,H,NT,C,C]  MT   M, row-major [t][s]       (or null)
+  void* Ke;      // [B,H,NT,C,DK] MT   diag(e) K^                (or null)
+  void* QgT;     // [B,H,NT,DK,C] MT   (diag(gamma) Q^)^T        (or null)
+  void* WT;      // [B,H,NT,DK,C] MT   W^T                       (or null)
+  void* Mt;      // [B,H,NT,C,C]  MT   M^T                       (or null)
+  float* A;      // [B,H,NT,C,C]  fp32 A                         (or null)
+  float* At;     // [B,H,NT,C,C]  fp32 A^T                       (or null)
   int B, T, H, DV, NT;
   int l2norm;
   float q_scale;
 };
 
 struct StateFwdArgs {
-  const void *q, *k;
-  const float* g;
-  const void* W;
+  const void *W;
   const float* U;
-  const void* M;
+  const void *KeT;
+  const float* GL;
+  const void *Qg, *M;
   const float* s0;
   void* o;
   float* sT;
   float* Sc;     // [B,H,NT,DK,DV]
   float* Vn;     // [B,H,NT,C,DV]
   int B, T, H, DV, NT;
-  int l2norm;
-  float q_scale;
   int nslice;    // workgroups per head-row
 };
 
 struct StateBwdArgs {
-  const void *q, *k;
-  const float* g;
-  const void* W;
-  const void* Mt;
+  const void *Ke, *QgT, *WT, *Mt;
+  const float* GL;
   const void* dO;
   const float* dsT;
   float* dSn;    // [B,H,NT,DK,DV]  dS_{c+1}
   float* dVn;    // [B,H,NT,C,DV]
   float* ds0;    // [B,H,DK,DV]
   int B, T, H, DV, NT;
-  int l2norm;
-  float q_scale;
   int nslice;
 };
 
@@ -139,19 +140,53 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
   const IT* q = (const IT*)a.q + qk_base;
   const IT* k = (const IT*)a.k + qk_base;
   const IT* v = (const IT*)a.v + v_base;
-  const bool wantM = a.M != nullptr || a.Mt != nullptr;
+  const bool needQ = a.M || a.Mt || a.Qg || a.QgT;
 
   if (w == 0) chunk_scalars(cs, a.g, a.beta, s_base, H, t0, T);
   if (a.l2norm) {
     row_rnorms<IT, DK>(rk, (const IT*)a.k, qk_base, qk_pitch, t0, T, 4);
-    if (wantM) row_rnorms<IT, DK>(rq, (const IT*)a.q, qk_base, qk_pitch, t0, T, 4);
+    if (needQ) row_rnorms<IT, DK>(rq, (const IT*)a.q, qk_base, qk_pitch, t0, T, 4);
   } else if (threadIdx.x < C) {
     rk[threadIdx.x] = 1.f;
     rq[threadIdx.x] = 1.f;
   }
   __syncthreads();
-  stage_rows<MT, IT>(sK, KP, k, qk_pitch, t0, T, DK, [&](int r) { return rk[r]; });
-  if (wantM) stage_rows<MT, IT>(sQ, KP, q, qk_pitch, t0, T, DK, [&](int r) { return rq[r] * a.q_scale; });
+  if (threadIdx.x == 0) a.GL[bhc] = cs.gam[C - 1];
+  const float qs = a.q_scale;
+  // K^ rows into LDS; diag(e) K^ rows out (row-major).  Q^ rows into LDS; diag(gamma) Q^ rows out.
+  {
+    MT* Ke = a.Ke ? (MT*)a.Ke + bhc * C * DK : nullptr;
+    MT* Qg = a.Qg ? (MT*)a.Qg + bhc * C * DK : nullptr;
+    constexpr int PR = DK / 8;
+    for (int i = threadIdx.x; i < C * PR; i += blockDim.x) {
+      const int r = i / PR, c8 = (i - r * PR) * 8, t = t0 + r;
+      float x[8], y[8];
+      if (t < T) load8(k + (size_t)t * qk_pitch + c8, x);
+      else
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        y[e] = x[e] * rk[r];
+        x[e] = y[e] * cs.e[r];
+      }
+      store8(sK + r * KP + c8, y);
+      if (Ke) store8(Ke + r * DK + c8, x);
+      if (needQ) {
+        if (t < T) load8(q + (size_t)t * qk_pitch + c8, x);
+        else
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          y[e] = x[e] * (rq[r] * qs);
+          x[e] = y[e] * cs.gam[r];
+        }
+        store8(sQ + r * KP + c8, y);
+        if (Qg) store8(Qg + r * DK + c8, x);
+      }
+    }
+  }
   __syncthreads();
 
   // K K^T and Q K^T on the lower 16 x 16 tiles: wave w owns row block w.  L (strictly lower, fp32) into LDS; M out.
@@ -165,7 +200,7 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
           Frag<MT> bk = frag_k_raw(sK, KP, 16 * ni, 32 * p);
           Frag<MT> ak = frag_k_raw(sK, KP, 16 * mi, 32 * p);
           mma(kk, ak, bk);
-          if (wantM) {
+          if (needQ) {
             Frag<MT> aq = frag_k_raw(sQ, KP, 16 * mi, 32 * p);
             mma(qk, aq, bk);
           }
@@ -177,7 +212,7 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
         const int row = 16 * mi + 4 * j + r;
         const float gm = (row >= col) ? cs.decay(row, col) : 0.f;   // mask before the exponent
         sL[row * FP + col] = (row > col) ? cs.beta[row] * kk[r] * gm : 0.f;
-        if (wantM) {
+        if (needQ) {
           const MT mv = from_f<MT>((row >= col) ? qk[r] * gm : 0.f);
           if (a.M) ((MT*)a.M)[bhc * C * C + row * C + col] = mv;
           if (a.Mt) ((MT*)a.Mt)[bhc * C * C + col * C + row] = mv;
@@ -187,8 +222,35 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
   }
   __syncthreads();
 
-  // (beta gamma K^)^T for W, from the raw keys (one rounding)
-  stage_rows_T<MT, IT>(sQ, CP, k, qk_pitch, t0, T, DK, [&](int r) { return rk[r] * cs.beta[r] * cs.gam[r]; });
+  // transposed operands from the raw rows (one rounding each; consecutive lanes take consecutive rows, so the
+  // transposed global stores are coalesced): (diag(e) K^)^T, (diag(gamma) Q^)^T out; (beta gamma K^)^T into LDS for W
+  {
+    MT* KeT = (MT*)a.KeT + bhc * DK * C;
+    MT* QgT = a.QgT ? (MT*)a.QgT + bhc * DK * C : nullptr;
+    for (int i = threadIdx.x; i < C * (DK / 8); i += blockDim.x) {
+      const int r = i % C, c8 = (i / C) * 8, t = t0 + r;
+      float x[8];
+      if (t < T) load8(k + (size_t)t * qk_pitch + c8, x);
+      else
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = 0.f;
+      const float sk = rk[r] * cs.e[r], sb = rk[r] * cs.beta[r] * cs.gam[r];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        KeT[(c8 + e) * C + r] = from_f<MT>(x[e] * sk);
+        sQ[(c8 + e) * CP + r] = from_f<MT>(x[e] * sb);
+      }
+      if (QgT) {
+        if (t < T) load8(q + (size_t)t * qk_pitch + c8, x);
+        else
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = 0.f;
+        const float sq = rq[r] * qs * cs.gam[r];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) QgT[(c8 + e) * C + r] = from_f<MT>(x[e] * sq);
+      }
+    }
+  }
 
   // A = (I + L)^-1.  Diagonal 16 x 16 blocks by forward substitution: wave 0, lane = (block l/16, column l%16).
   if (w == 0) {
@@ -196,11 +258,11 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
     float x[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      float s = (i == cc) ? 1.f : 0.f;
+      float sacc = (i == cc) ? 1.f : 0.f;
       const float* Lr = sL + (16 * bb + i) * FP + 16 * bb;
 #pragma unroll
-      for (int m = 0; m < i; ++m) s = fmaf(-Lr[m], x[m], s);
-      x[i] = s;
+      for (int m = 0; m < i; ++m) sacc = fmaf(-Lr[m], x[m], sacc);
+      x[i] = sacc;
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) sA[(16 * bb + i) * FP + 16 * bb + cc] = x[i];
@@ -238,11 +300,15 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
     for (int p = 0; p < 2; ++p) af[p] = cvt<MT>(frag_k_f32(sA, FP, 16 * w, 32 * p));
     const int np = (16 * w + 15) / 32 + 1;
     MT* Wc = (MT*)a.W + bhc * C * DK;
+    MT* WTc = a.WT ? (MT*)a.WT + bhc * DK * C : nullptr;
     for (int ni = 0; ni < DK / 16; ++ni) {
       f4 acc = {0.f, 0.f, 0.f, 0.f};
       for (int p = 0; p < np; ++p) mma(acc, af[p], frag_k_raw(sQ, CP, 16 * ni, 32 * p));
 #pragma unroll
       for (int r = 0; r < 4; ++r) Wc[(16 * w + 4 * j + r) * DK + 16 * ni + (l & 15)] = from_f<MT>(acc[r]);
+      if (WTc)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) WTc[(16 * ni + (l & 15)) * C + 16 * w + 4 * j + r] = from_f<MT>(acc[r]);
     }
     // U = A (beta V), 64 value columns at a time staged transposed in sK
     float* Uc = a.U + bhc * C * DV;
@@ -280,59 +346,108 @@ __device__ __forceinline__ bool state_map(int nslice, int HR, int& hr, int& slic
   return hr < HR;
 }
 
+// The state's 16-column slice of a wave into accumulator tiles (rows 16 di + 4 j + r, column col); zeros for NULL.  One
+// uniform branch, so all the loads of the slice are in flight together.
+template <int ND>
+__device__ __forceinline__ void load_state(f4 (&S)[ND], const float* src, size_t base, int DV, int col) {
+  const int j = lane_id() >> 4;
+  if (src) {
+#pragma unroll
+    for (int di = 0; di < ND; ++di)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) S[di][r] = src[base + (size_t)(16 * di + 4 * j + r) * DV + col];
+  } else {
+#pragma unroll
+    for (int di = 0; di < ND; ++di) S[di] = f4{0.f, 0.f, 0.f, 0.f};
+  }
+}
+
+// double-buffer the chunk stages when two fit in LDS
+constexpr int LDS_BYTES = 160 * 1024 - 2048;
+template <int STAGE_BYTES>
+struct Buffers {
+  static constexpr int N = (2 * STAGE_BYTES <= LDS_BYTES) ? 2 : 1;
+};
+
 // ---------------------------------------------------------------------------------------------------------------------
-// the forward state pass (+ output), sequential over chunks
+// the forward state pass (+ output), sequential over chunks.  Per chunk the workgroup streams W, (diag(e) K^)^T and, for
+// the output, diag(gamma) Q^ and M into a swizzled LDS stage by asynchronous copies -- the next chunk's copies are in
+// flight while this chunk's MFMAs run -- and each wave keeps its 16 columns of S in accumulators.
 // ---------------------------------------------------------------------------------------------------------------------
-template <typename IT, typename MT, int DK, bool OUT, bool STORE>
-__global__ void __launch_bounds__(512) state_fwd_kernel(StateFwdArgs a) {
-  constexpr int KP = DK + 8, CP = C + 8, ND = DK / 16;
-  __shared__ __attribute__((aligned(16))) MT sW[C * KP];
-  __shared__ __attribute__((aligned(16))) MT sKeT[DK * CP];
-  __shared__ __attribute__((aligned(16))) MT sQg[OUT ? C * KP : 8];
-  __shared__ __attribute__((aligned(16))) MT sM[OUT ? C * CP : 8];
-  __shared__ ChunkScalars cs;
-  __shared__ float rk[C], rq[C];
+template <typename MT, int DK, int NW, bool OUT, bool STORE>
+__global__ void __launch_bounds__(64 * NW) state_fwd_kernel(StateFwdArgs a) {
+  using GW = Swz<MT, C, DK>;    // W, diag(gamma) Q^     [t][d]
+  using GKT = Swz<MT, DK, C>;   // (diag(e) K^)^T        [d][t]
+  using GM = Swz<MT, C, C>;     // M                     [t][s]
+  constexpr int ND = DK / 16;
+  constexpr int O_KT = GW::ELEMS, O_Q = O_KT + GKT::ELEMS, O_M = O_Q + (OUT ? GW::ELEMS : 0);
+  constexpr int SZ = O_M + (OUT ? GM::ELEMS : 0);
+  constexpr int NBUF = Buffers<SZ * (int)sizeof(MT)>::N;
+  __shared__ __attribute__((aligned(1024))) MT lds[NBUF * SZ];
 
   const int T = a.T, H = a.H, DV = a.DV, NT = a.NT;
   int hr, slice;
   if (!state_map(a.nslice, a.B * H, hr, slice)) return;
   const int b = hr / H, h = hr % H;
-  const int nw = blockDim.x >> 6;
   const int l = lane_id(), w = wave_id(), j = l >> 4;
-  const int v0 = (slice * nw + w) * 16;
+  const int v0 = (slice * NW + w) * 16;
   const int col = v0 + (l & 15);
-  const size_t qk_base = ((size_t)b * T * H + h) * DK, qk_pitch = (size_t)H * DK;
   const size_t o_base = ((size_t)b * T * H + h) * DV, o_pitch = (size_t)H * DV;
-  const size_t s_base = (size_t)b * T * H + h;
-  const IT* q = (const IT*)a.q + qk_base;
-  const IT* k = (const IT*)a.k + qk_base;
+
+  auto issue = [&](int c, int buf) {
+    MT* st = lds + buf * SZ;
+    const size_t bhc = (size_t)hr * NT + c;
+    GW::dma(st, (const MT*)a.W + bhc * C * DK, DK, w, NW);
+    GKT::dma(st + O_KT, (const MT*)a.KeT + bhc * DK * C, C, w, NW);
+    if (OUT) {
+      GW::dma(st + O_Q, (const MT*)a.Qg + bhc * C * DK, DK, w, NW);
+      GM::dma(st + O_M, (const MT*)a.M + bhc * C * C, C, w, NW);
+    }
+  };
+  auto loadU = [&](int c, f4* U) {
+    const float* Uc = a.U + ((size_t)hr * NT + c) * C * DV;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) U[mi][r] = Uc[(16 * mi + 4 * j + r) * DV + col];
+  };
 
   f4 S[ND];
-#pragma unroll
-  for (int di = 0; di < ND; ++di)
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      S[di][r] = a.s0 ? a.s0[(size_t)hr * DK * DV + (16 * di + 4 * j + r) * DV + col] : 0.f;
+  load_state(S, a.s0, (size_t)hr * DK * DV, DV, col);
 
+  f4 Un[4];
+  float gln = 0.f;
+  if (NBUF == 2) {
+    issue(0, 0);
+    loadU(0, Un);
+    gln = a.GL[(size_t)hr * NT];
+    wait_dma();
+    __syncthreads();
+  }
   for (int c = 0; c < NT; ++c) {
     const int t0 = c * C;
     const size_t bhc = (size_t)hr * NT + c;
-    if (w == 0) chunk_scalars(cs, a.g, nullptr, s_base, H, t0, T);
-    if (a.l2norm) {
-      row_rnorms<IT, DK>(rk, (const IT*)a.k, qk_base, qk_pitch, t0, T, nw);
-      if (OUT) row_rnorms<IT, DK>(rq, (const IT*)a.q, qk_base, qk_pitch, t0, T, nw);
-    } else if (threadIdx.x < C) {
-      rk[threadIdx.x] = 1.f;
-      rq[threadIdx.x] = 1.f;
+    int buf = 0;
+    f4 U[4];
+    float gl;
+    if (NBUF == 2) {
+      buf = c & 1;
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) U[mi] = Un[mi];
+      gl = gln;
+      if (c + 1 < NT) {
+        issue(c + 1, buf ^ 1);
+        loadU(c + 1, Un);
+        gln = a.GL[bhc + 1];
+      }
+    } else {
+      issue(c, 0);
+      loadU(c, U);
+      gl = a.GL[bhc];
+      wait_dma();
+      __syncthreads();
     }
-    __syncthreads();
-    stage_copy<MT>(sW, KP, (const MT*)a.W + bhc * C * DK, C, DK);
-    stage_rows_T<MT, IT>(sKeT, CP, k, qk_pitch, t0, T, DK, [&](int r) { return rk[r] * cs.e[r]; });
-    if (OUT) {
-      stage_rows<MT, IT>(sQg, KP, q, qk_pitch, t0, T, DK, [&](int r) { return rq[r] * a.q_scale * cs.gam[r]; });
-      stage_copy<MT>(sM, CP, (const MT*)a.M + bhc * C * C, C, C);
-    }
-    __syncthreads();
+    const MT* st = lds + buf * SZ;
 
     // S as the B operand (k = state rows)
     Frag<MT> Sf[ND / 2];
@@ -340,14 +455,24 @@ __global__ void __launch_bounds__(512) state_fwd_kernel(StateFwdArgs a) {
     for (int p = 0; p < ND / 2; ++p) Sf[p] = frag_acc<MT>(S[2 * p], S[2 * p + 1]);
     // Vn = U - W S
     f4 Vn[4];
-    const float* Uc = a.U + bhc * C * DV;
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
       f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int p = 0; p < ND / 2; ++p) mma(acc, frag_k_raw(sW, KP, 16 * mi, 32 * p), Sf[p]);
+      for (int p = 0; p < ND / 2; ++p) mma(acc, frag_swz<MT, GW>(st, 16 * mi, 32 * p), Sf[p]);
+      Vn[mi] = U[mi] - acc;
+    }
+    Frag<MT> Vf[2];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) Vn[mi][r] = Uc[(16 * mi + 4 * j + r) * DV + col] - acc[r];
+    for (int p = 0; p < 2; ++p) Vf[p] = frag_acc<MT>(Vn[2 * p], Vn[2 * p + 1]);
+    // S <- exp(G_last) S + (diag(e) K)^T Vn   (the chain to the next chunk; the rest below is off it)
+    f4 Sn[ND];
+#pragma unroll
+    for (int di = 0; di < ND; ++di) {
+      f4 acc = S[di] * gl;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) mma(acc, frag_swz<MT, GKT>(st + O_KT, 16 * di, 32 * p), Vf[p]);
+      Sn[di] = acc;
     }
     if (STORE) {
       float* Scc = a.Sc + bhc * DK * DV;
@@ -361,35 +486,26 @@ __global__ void __launch_bounds__(512) state_fwd_kernel(StateFwdArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) Vnc[(16 * mi + 4 * j + r) * DV + col] = Vn[mi][r];
     }
-    Frag<MT> Vf[2];
-#pragma unroll
-    for (int p = 0; p < 2; ++p) Vf[p] = frag_acc<MT>(Vn[2 * p], Vn[2 * p + 1]);
     if (OUT) {
       // O = diag(gamma) Q S + M Vn (M lower triangular: k-blocks past the row block are zero)
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) {
         f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int p = 0; p < ND / 2; ++p) mma(acc, frag_k_raw(sQg, KP, 16 * mi, 32 * p), Sf[p]);
+        for (int p = 0; p < ND / 2; ++p) mma(acc, frag_swz<MT, GW>(st + O_Q, 16 * mi, 32 * p), Sf[p]);
 #pragma unroll
         for (int p = 0; p < 2; ++p)
-          if (32 * p <= 16 * mi + 15) mma(acc, frag_k_raw(sM, CP, 16 * mi, 32 * p), Vf[p]);
+          if (32 * p <= 16 * mi + 15) mma(acc, frag_swz<MT, GM>(st + O_M, 16 * mi, 32 * p), Vf[p]);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int t = t0 + 16 * mi + 4 * j + r;
-          if (t < T) ((IT*)a.o)[o_base + (size_t)t * o_pitch + col] = from_f<IT>(acc[r]);
+          if (t < T) ((MT*)a.o)[o_base + (size_t)t * o_pitch + col] = from_f<MT>(acc[r]);
         }
       }
     }
-    // S <- exp(G_last) S + (diag(e) K)^T Vn
-    const float gl = cs.gam[C - 1];
 #pragma unroll
-    for (int di = 0; di < ND; ++di) {
-      f4 acc = S[di] * gl;
-#pragma unroll
-      for (int p = 0; p < 2; ++p) mma(acc, frag_k_raw(sKeT, CP, 16 * di, 32 * p), Vf[p]);
-      S[di] = acc;
-    }
+    for (int di = 0; di < ND; ++di) S[di] = Sn[di];
+    if (NBUF == 2) wait_dma();
     __syncthreads();
   }
   if (a.sT) {
@@ -401,61 +517,74 @@ __global__ void __launch_bounds__(512) state_fwd_kernel(StateFwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
-// the reverse state pass
+// the reverse state pass: streams diag(e) K^, (diag(gamma) Q^)^T, W^T, M^T and the workgroup's dO columns per chunk
 // ---------------------------------------------------------------------------------------------------------------------
-template <typename IT, typename MT, int DK>
-__global__ void __launch_bounds__(512) state_bwd_kernel(StateBwdArgs a) {
-  constexpr int KP = DK + 8, CP = C + 8, ND = DK / 16;
-  __shared__ __attribute__((aligned(16))) MT sKe[C * KP];     // diag(e) K^ rows
-  __shared__ __attribute__((aligned(16))) MT sQgT[DK * CP];   // (diag(gamma) Q^)^T
-  __shared__ __attribute__((aligned(16))) MT sWT[DK * CP];    // W^T
-  __shared__ __attribute__((aligned(16))) MT sMT[C * CP];     // M^T
-  __shared__ ChunkScalars cs;
-  __shared__ float rk[C], rq[C];
+template <typename MT, int DK, int NW>
+__global__ void __launch_bounds__(64 * NW) state_bwd_kernel(StateBwdArgs a) {
+  using GK = Swz<MT, C, DK>;        // diag(e) K^          [t][d]
+  using GT = Swz<MT, DK, C>;        // QgT, WT             [d][t]
+  using GM = Swz<MT, C, C>;         // M^T                 [s][t]
+  using GO = Swz<MT, C, 16 * NW>;   // dO columns          [t][v]
+  constexpr int ND = DK / 16;
+  constexpr int O_Q = GK::ELEMS, O_W = O_Q + GT::ELEMS, O_M = O_W + GT::ELEMS, O_O = O_M + GM::ELEMS;
+  constexpr int SZ = O_O + GO::ELEMS;
+  constexpr int NBUF = Buffers<SZ * (int)sizeof(MT)>::N;
+  __shared__ __attribute__((aligned(1024))) MT lds[NBUF * SZ];
 
   const int T = a.T, H = a.H, DV = a.DV, NT = a.NT;
   int hr, slice;
   if (!state_map(a.nslice, a.B * H, hr, slice)) return;
   const int b = hr / H, h = hr % H;
-  const int nw = blockDim.x >> 6;
   const int l = lane_id(), w = wave_id(), j = l >> 4;
-  const int v0 = (slice * nw + w) * 16;
-  const int col = v0 + (l & 15);
-  const size_t qk_base = ((size_t)b * T * H + h) * DK, qk_pitch = (size_t)H * DK;
+  const int vg = slice * NW * 16;            // the workgroup's first value column
+  const int col = vg + w * 16 + (l & 15);
   const size_t o_base = ((size_t)b * T * H + h) * DV, o_pitch = (size_t)H * DV;
-  const size_t s_base = (size_t)b * T * H + h;
-  const IT* q = (const IT*)a.q + qk_base;
-  const IT* k = (const IT*)a.k + qk_base;
-  const IT* dO = (const IT*)a.dO + o_base;
+
+  auto issue = [&](int c, int buf) {
+    MT* st = lds + buf * SZ;
+    const size_t bhc = (size_t)hr * NT + c;
+    const int t0 = c * C;
+    GK::dma(st, (const MT*)a.Ke + bhc * C * DK, DK, w, NW);
+    GT::dma(st + O_Q, (const MT*)a.QgT + bhc * DK * C, C, w, NW);
+    GT::dma(st + O_W, (const MT*)a.WT + bhc * DK * C, C, w, NW);
+    GM::dma(st + O_M, (const MT*)a.Mt + bhc * C * C, C, w, NW);
+    GO::dma(st + O_O, (const MT*)a.dO + o_base + (size_t)t0 * o_pitch + vg, o_pitch, w, NW,
+            (T - t0 < C) ? T - t0 : C);
+  };
 
   f4 dS[ND];
-#pragma unroll
-  for (int di = 0; di < ND; ++di)
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      dS[di][r] = a.dsT ? a.dsT[(size_t)hr * DK * DV + (16 * di + 4 * j + r) * DV + col] : 0.f;
+  load_state(dS, a.dsT, (size_t)hr * DK * DV, DV, col);
 
-  for (int c = NT - 1; c >= 0; --c) {
+  float gln = 0.f;
+  if (NBUF == 2) {
+    issue(NT - 1, 0);
+    gln = a.GL[(size_t)hr * NT + NT - 1];
+    wait_dma();
+    __syncthreads();
+  }
+  for (int c = NT - 1, it = 0; c >= 0; --c, ++it) {
     const int t0 = c * C;
     const size_t bhc = (size_t)hr * NT + c;
-    if (w == 0) chunk_scalars(cs, a.g, nullptr, s_base, H, t0, T);
-    if (a.l2norm) {
-      row_rnorms<IT, DK>(rk, (const IT*)a.k, qk_base, qk_pitch, t0, T, nw);
-      row_rnorms<IT, DK>(rq, (const IT*)a.q, qk_base, qk_pitch, t0, T, nw);
-    } else if (threadIdx.x < C) {
-      rk[threadIdx.x] = 1.f;
-      rq[threadIdx.x] = 1.f;
+    int buf = 0;
+    float gl;
+    if (NBUF == 2) {
+      buf = it & 1;
+      gl = gln;
+      if (c > 0) {
+        issue(c - 1, buf ^ 1);
+        gln = a.GL[bhc - 1];
+      }
+    } else {
+      issue(c, 0);
+      gl = a.GL[bhc];
+      wait_dma();
+      __syncthreads();
     }
-    __syncthreads();
-    stage_rows<MT, IT>(sKe, KP, k, qk_pitch, t0, T, DK, [&](int r) { return rk[r] * cs.e[r]; });
-    stage_rows_T<MT, IT>(sQgT, CP, q, qk_pitch, t0, T, DK, [&](int r) { return rq[r] * a.q_scale * cs.gam[r]; });
-    stage_copy_T<MT>(sWT, CP, (const MT*)a.W + bhc * C * DK, C, DK);
-    stage_copy<MT>(sMT, CP, (const MT*)a.Mt + bhc * C * C, C, C);
-    __syncthreads();
+    const MT* st = lds + buf * SZ;
 
     Frag<MT> Of[2];
 #pragma unroll
-    for (int p = 0; p < 2; ++p) Of[p] = frag_rows<MT, IT>(dO, o_pitch, t0, T, 32 * p, col, One());
+    for (int p = 0; p < 2; ++p) Of[p] = frag_swz_rows<MT, MT, GO>(st + O_O, 32 * p, w * 16 + (l & 15), t0, T);
     Frag<MT> Sf[ND / 2];
 #pragma unroll
     for (int p = 0; p < ND / 2; ++p) Sf[p] = frag_acc<MT>(dS[2 * p], dS[2 * p + 1]);
@@ -465,11 +594,26 @@ __global__ void __launch_bounds__(512) state_bwd_kernel(StateBwdArgs a) {
     for (int mi = 0; mi < 4; ++mi) {
       f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int p = 0; p < 2; ++p)
-        if (32 * p + 31 >= 16 * mi) mma(acc, frag_k_raw(sMT, CP, 16 * mi, 32 * p), Of[p]);
+      for (int p = 0; p < ND / 2; ++p) mma(acc, frag_swz<MT, GK>(st, 16 * mi, 32 * p), Sf[p]);
 #pragma unroll
-      for (int p = 0; p < ND / 2; ++p) mma(acc, frag_k_raw(sKe, KP, 16 * mi, 32 * p), Sf[p]);
+      for (int p = 0; p < 2; ++p)
+        if (32 * p + 31 >= 16 * mi) mma(acc, frag_swz<MT, GM>(st + O_M, 16 * mi, 32 * p), Of[p]);
       dV[mi] = acc;
+    }
+    Frag<MT> Vf[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) Vf[p] = frag_acc<MT>(dV[2 * p], dV[2 * p + 1], -1.f);
+    // dS <- exp(G_last) dS + (diag(gamma) Q^)^T dO - W^T dVn
+    f4 dSn[ND];
+#pragma unroll
+    for (int di = 0; di < ND; ++di) {
+      f4 acc = dS[di] * gl;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        mma(acc, frag_swz<MT, GT>(st + O_W, 16 * di, 32 * p), Vf[p]);
+        mma(acc, frag_swz<MT, GT>(st + O_Q, 16 * di, 32 * p), Of[p]);
+      }
+      dSn[di] = acc;
     }
     {
       float* dSc = a.dSn + bhc * DK * DV;
@@ -483,21 +627,9 @@ __global__ void __launch_bounds__(512) state_bwd_kernel(StateBwdArgs a) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) dVc[(16 * mi + 4 * j + r) * DV + col] = dV[mi][r];
     }
-    Frag<MT> Vf[2];
 #pragma unroll
-    for (int p = 0; p < 2; ++p) Vf[p] = frag_acc<MT>(dV[2 * p], dV[2 * p + 1], -1.f);
-    // dS <- exp(G_last) dS + (diag(gamma) Q^)^T dO - W^T dVn
-    const float gl = cs.gam[C - 1];
-#pragma unroll
-    for (int di = 0; di < ND; ++di) {
-      f4 acc = dS[di] * gl;
-#pragma unroll
-      for (int p = 0; p < 2; ++p) {
-        mma(acc, frag_k_raw(sQgT, CP, 16 * di, 32 * p), Of[p]);
-        mma(acc, frag_k_raw(sWT, CP, 16 * di, 32 * p), Vf[p]);
-      }
-      dS[di] = acc;
-    }
+    for (int di = 0; di < ND; ++di) dS[di] = dSn[di];
+    if (NBUF == 2) wait_dma();
     __syncthreads();
   }
 #pragma unroll
@@ -1009,17 +1141,17 @@ static int check_common(const char* what, int64_t B, int64_t T, int64_t H, int64
   }
 
 static int pick_waves(int64_t DV, int split, const char* what, int* nw_out, int* nslice_out) {
-  const int ncb = (int)(DV / 16);   // 16-column slices of the value width
-  int s = split;
-  if (s <= 0) s = -1;
+  // a workgroup holds NW in {1, 2, 4, 8} waves of 16 value columns; split = workgroups per head-row
+  const int ncb = (int)(DV / 16);
   int nw;
-  if (s < 0) {
-    nw = ncb >= 8 ? 8 : ncb;        // default: one workgroup of up to 8 waves per head-row
-    while (ncb % nw) --nw;
+  if (split <= 0) {
+    nw = 8;
+    while (ncb % nw) nw >>= 1;
   } else {
-    if (ncb % s) return fail(MACAI_GDR_EINVAL, "%s: split %d does not divide the %d value-column slices", what, s, ncb);
-    nw = ncb / s;
-    if (nw > 8) return fail(MACAI_GDR_EINVAL, "%s: split %d leaves %d waves per workgroup (max 8)", what, s, nw);
+    if (ncb % split) return fail(MACAI_GDR_EINVAL, "%s: split %d does not divide the %d value-column slices", what, split, ncb);
+    nw = ncb / split;
+    if (nw != 1 && nw != 2 && nw != 4 && nw != 8)
+      return fail(MACAI_GDR_EINVAL, "%s: split %d gives %d waves per workgroup (1, 2, 4 or 8 allowed)", what, split, nw);
   }
   *nw_out = nw;
   *nslice_out = ncb / nw;
@@ -1033,19 +1165,21 @@ const char* macai_gdr_last_error(void) { return g_err; }
 int macai_gdr_abi_version(void) { return MACAI_GDR_ABI_VERSION; }
 
 int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, const float* beta, void* W, float* U,
-                   void* M, void* Mt, float* A, float* At, int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV,
-                   int32_t dtype, int32_t use_l2norm, float q_scale, void* stream) {
+                   void* KeT, float* GL, void* Qg, void* M, void* Ke, void* QgT, void* WT, void* Mt, float* A, float* At,
+                   int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm,
+                   float q_scale, void* stream) {
   const char* what = "macai_gdr_prep";
   int rc = check_common(what, B, T, H, DK, DV, dtype);
   if (rc) return rc;
-  if (!k || !v || !g || !beta || !W || !U) return fail(MACAI_GDR_EINVAL, "%s: null input or output pointer", what);
-  if ((M || Mt) && !q) return fail(MACAI_GDR_EINVAL, "%s: M needs q", what);
+  if (!k || !v || !g || !beta || !W || !U || !KeT || !GL)
+    return fail(MACAI_GDR_EINVAL, "%s: null input or output pointer", what);
+  if ((Qg || M || QgT || Mt) && !q) return fail(MACAI_GDR_EINVAL, "%s: Qg, M, QgT and Mt need q", what);
   if ((A == nullptr) != (At == nullptr)) return fail(MACAI_GDR_EINVAL, "%s: A and At go together", what);
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(W) || !aligned16(U) || !aligned16(M) ||
-      !aligned16(Mt) || !aligned16(A) || !aligned16(At))
-    return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
-  PrepArgs a{q, k, v, g, beta, W, U, M, Mt, A, At, (int)B, (int)T, (int)H, (int)DV, (int)((T + C - 1) / C),
-             use_l2norm, q_scale};
+  const void* ps[] = {q, k, v, W, U, KeT, Qg, M, Ke, QgT, WT, Mt, A, At};
+  for (const void* p : ps)
+    if (!aligned16(p)) return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
+  PrepArgs a{q, k, v, g, beta, W, U, KeT, GL, Qg, M, Ke, QgT, WT, Mt, A, At, (int)B, (int)T, (int)H, (int)DV,
+             (int)((T + C - 1) / C), use_l2norm, q_scale};
   dim3 grid(a.NT, (unsigned)H, (unsigned)B);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == MACAI_GDR_F32) {
@@ -1056,66 +1190,73 @@ int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, 
   return launched(what);
 }
 
-int macai_gdr_state_fwd(const void* q, const void* k, const float* g, const void* W, const float* U, const void* M,
+#define DISPATCH_NW(NW, ...)                                  \
+  switch (NW) {                                               \
+    case 1: { constexpr int NWC = 1; __VA_ARGS__; } break;    \
+    case 2: { constexpr int NWC = 2; __VA_ARGS__; } break;    \
+    case 4: { constexpr int NWC = 4; __VA_ARGS__; } break;    \
+    default: { constexpr int NWC = 8; __VA_ARGS__; } break;   \
+  }
+
+int macai_gdr_state_fwd(const void* W, const float* U, const void* KeT, const float* GL, const void* Qg, const void* M,
                         const float* s0, void* o, float* sT, float* Sc, float* Vn, int64_t B, int64_t T, int64_t H,
-                        int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, int32_t flags,
-                        int32_t split, void* stream) {
+                        int64_t DK, int64_t DV, int32_t dtype, int32_t flags, int32_t split, void* stream) {
   const char* what = "macai_gdr_state_fwd";
   int rc = check_common(what, B, T, H, DK, DV, dtype);
   if (rc) return rc;
   const bool store = flags & MACAI_GDR_STORE_STATES, out = !(flags & MACAI_GDR_NO_OUTPUT);
-  if (!k || !g || !W || !U) return fail(MACAI_GDR_EINVAL, "%s: null input pointer", what);
-  if (out && (!q || !M || !o)) return fail(MACAI_GDR_EINVAL, "%s: the output needs q, M and o", what);
+  if (out == store)
+    return fail(MACAI_GDR_EINVAL, "%s: flags must be 0 (output) or STORE_STATES | NO_OUTPUT (recompute)", what);
+  if (!W || !U || !KeT || !GL) return fail(MACAI_GDR_EINVAL, "%s: null input pointer", what);
+  if (out && (!Qg || !M || !o)) return fail(MACAI_GDR_EINVAL, "%s: the output needs Qg, M and o", what);
   if (store && (!Sc || !Vn)) return fail(MACAI_GDR_EINVAL, "%s: storing states needs Sc and Vn", what);
-  if (!out && !store) return fail(MACAI_GDR_EINVAL, "%s: flags ask for nothing", what);
-  if (!aligned16(q) || !aligned16(k) || !aligned16(W) || !aligned16(M) || !aligned16(U))
-    return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
+  const void* ps[] = {W, U, KeT, Qg, M, s0, sT, Sc, Vn};
+  for (const void* p : ps)
+    if (!aligned16(p)) return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
   int nw, nslice;
   if ((rc = pick_waves(DV, split, what, &nw, &nslice))) return rc;
-  StateFwdArgs a{q, k, g, W, U, M, s0, o, out ? sT : nullptr, Sc, Vn, (int)B, (int)T, (int)H, (int)DV,
-                 (int)((T + C - 1) / C), use_l2norm, q_scale, nslice};
+  StateFwdArgs a{W, U, KeT, GL, Qg, M, s0, o, out ? sT : nullptr, Sc, Vn, (int)B, (int)T, (int)H, (int)DV,
+                 (int)((T + C - 1) / C), nslice};
   const int HR = (int)(B * H);
   dim3 grid((unsigned)(8 * nslice * ((HR + 7) / 8)));
   dim3 block(64 * nw);
   hipStream_t st = (hipStream_t)stream;
-#define LAUNCH_SF(IT, MT, O, S) \
-  DISPATCH_DK(DK, hipLaunchKernelGGL((state_fwd_kernel<IT, MT, DKC, O, S>), grid, block, 0, st, a))
+#define LAUNCH_SF(MT, O, S) \
+  DISPATCH_DK(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_fwd_kernel<MT, DKC, NWC, O, S>), grid, block, 0, st, a)))
   if (dtype == MACAI_GDR_F32) {
-    if (out && store) { LAUNCH_SF(float, float, true, true); }
-    else if (out) { LAUNCH_SF(float, float, true, false); }
-    else { LAUNCH_SF(float, float, false, true); }
+    if (out) { LAUNCH_SF(float, true, false); }
+    else { LAUNCH_SF(float, false, true); }
   } else {
-    if (out && store) { LAUNCH_SF(bf16, bf16, true, true); }
-    else if (out) { LAUNCH_SF(bf16, bf16, true, false); }
-    else { LAUNCH_SF(bf16, bf16, false, true); }
+    if (out) { LAUNCH_SF(bf16, true, false); }
+    else { LAUNCH_SF(bf16, false, true); }
   }
 #undef LAUNCH_SF
   return launched(what);
 }
 
-int macai_gdr_state_bwd(const void* q, const void* k, const float* g, const void* W, const void* Mt, const void* dO,
-                        const float* dsT, float* dSn, float* dVn, float* ds0, int64_t B, int64_t T, int64_t H,
-                        int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, int32_t split,
-                        void* stream) {
+int macai_gdr_state_bwd(const void* Ke, const void* QgT, const void* WT, const void* Mt, const float* GL,
+                        const void* dO, const float* dsT, float* dSn, float* dVn, float* ds0, int64_t B, int64_t T,
+                        int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t split, void* stream) {
   const char* what = "macai_gdr_state_bwd";
   int rc = check_common(what, B, T, H, DK, DV, dtype);
   if (rc) return rc;
-  if (!q || !k || !g || !W || !Mt || !dO || !dSn || !dVn || !ds0)
+  if (!Ke || !QgT || !WT || !Mt || !GL || !dO || !dSn || !dVn || !ds0)
     return fail(MACAI_GDR_EINVAL, "%s: null pointer", what);
-  if (!aligned16(q) || !aligned16(k) || !aligned16(W) || !aligned16(Mt))
-    return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
+  const void* ps[] = {Ke, QgT, WT, Mt, dO, dsT, dSn, dVn, ds0};
+  for (const void* p : ps)
+    if (!aligned16(p)) return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
   int nw, nslice;
   if ((rc = pick_waves(DV, split, what, &nw, &nslice))) return rc;
-  StateBwdArgs a{q, k, g, W, Mt, dO, dsT, dSn, dVn, ds0, (int)B, (int)T, (int)H, (int)DV, (int)((T + C - 1) / C),
-                 use_l2norm, q_scale, nslice};
+  StateBwdArgs a{Ke, QgT, WT, Mt, GL, dO, dsT, dSn, dVn, ds0, (int)B, (int)T, (int)H, (int)DV, (int)((T + C - 1) / C),
+                 nslice};
   const int HR = (int)(B * H);
   dim3 grid((unsigned)(8 * nslice * ((HR + 7) / 8)));
   dim3 block(64 * nw);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == MACAI_GDR_F32) {
-    DISPATCH_DK(DK, hipLaunchKernelGGL((state_bwd_kernel<float, float, DKC>), grid, block, 0, st, a));
+    DISPATCH_DK(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_bwd_kernel<float, DKC, NWC>), grid, block, 0, st, a)));
   } else {
-    DISPATCH_DK(DK, hipLaunchKernelGGL((state_bwd_kernel<bf16, bf16, DKC>), grid, block, 0, st, a));
+    DISPATCH_DK(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_bwd_kernel<bf16, DKC, NWC>), grid, block, 0, st, a)));
   }
   return launched(what);
 }

@@ -22,21 +22,25 @@ VALUE_SPLIT = "auto"
 CALLS = collections.Counter()
 
 
-def split_for(rows: int, T: int, dv: int) -> int:
-    """VALUE_SPLIT's choice for `rows` head-rows (B x H) of value width dv: "auto" takes the smallest split (a divisor of
-    dv / 16) that gives at least 256 workgroups, one per CU, or every 16-column slice its own workgroup; an int setting
-    is rounded down to a divisor."""
+def valid_splits(dv: int) -> list:
+    """Splits the state kernels take: s divides the dv / 16 column slices and leaves 1, 2, 4 or 8 waves per
+    workgroup."""
     slices = dv // 16
+    return [s for s in range(1, slices + 1) if slices % s == 0 and slices // s in (1, 2, 4, 8)]
+
+
+def split_for(rows: int, T: int, dv: int) -> int:
+    """VALUE_SPLIT's choice for `rows` head-rows (B x H) of value width dv: "auto" takes the smallest valid split that
+    gives at least 256 workgroups (one per CU), else the largest; an int setting is rounded down to a valid split."""
+    valid = valid_splits(dv)
     if VALUE_SPLIT == "auto":
-        s = 1
-        while s < slices and rows * s < 256:
-            s *= 2
-    else:
-        s = int(VALUE_SPLIT)
-    s = max(1, min(s, slices))
-    while slices % s:
-        s -= 1
-    return s
+        for s in valid:
+            if rows * s >= 256:
+                return s
+        return valid[-1]
+    want = int(VALUE_SPLIT)
+    below = [s for s in valid if s <= want]
+    return below[-1] if below else valid[0]
 
 
 def _check(q, k, v, g, beta, s0):
@@ -62,60 +66,65 @@ def _dims(q, v):
 
 
 def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool):
-    """prep (W, U, M) then the state pass with the output: returns (o in q's dtype, sT or None)."""
-    B, T, H, DK, DV, NT = _dims(q, v)
-    dev, dt = q.device, q.dtype
-    code, stream = N.dtype_code(dt), N.stream_of(q)
-    W = torch.empty(B, H, NT, CHUNK, DK, device=dev, dtype=dt)
-    U = torch.empty(B, H, NT, CHUNK, DV, device=dev, dtype=torch.float32)
-    M = torch.empty(B, H, NT, CHUNK, CHUNK, device=dev, dtype=dt)
-    N.call("macai_gdr_prep", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(g), N.ptr(beta), N.ptr(W), N.ptr(U), N.ptr(M), None,
-           None, None, B, T, H, DK, DV, code, int(l2norm), q_scale, stream)
-    o = torch.empty(B, T, H, DV, device=dev, dtype=dt)
-    sT = torch.empty(B, H, DK, DV, device=dev, dtype=torch.float32) if want_sT else None
-    split = split_for(B * H, T, DV)
-    N.call("macai_gdr_state_fwd", N.ptr(q), N.ptr(k), N.ptr(g), N.ptr(W), N.ptr(U), N.ptr(M), N.ptr(s0), N.ptr(o),
-           N.ptr(sT), None, None, B, T, H, DK, DV, code, int(l2norm), q_scale, 0, split, stream)
-    CALLS[f"fwd s{split}"] += 1
-    return o, sT
-
-
-def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float):
-    """Recompute (prep with M^T, A, A^T; the state pass storing S_c and Vn), the reverse state pass, the per-chunk
-    backward.  Returns (dq, dk, dv in q's dtype; dg, dbeta, ds0 float32)."""
+    """prep (W, U, (diag(e) K^)^T, exp(G_last), diag(gamma) Q^, M) then the state pass with the output: returns (o in
+    q's dtype, sT or None)."""
     B, T, H, DK, DV, NT = _dims(q, v)
     dev, dt = q.device, q.dtype
     code, stream = N.dtype_code(dt), N.stream_of(q)
     f32 = torch.float32
     W = torch.empty(B, H, NT, CHUNK, DK, device=dev, dtype=dt)
     U = torch.empty(B, H, NT, CHUNK, DV, device=dev, dtype=f32)
+    KeT = torch.empty(B, H, NT, DK, CHUNK, device=dev, dtype=dt)
+    GL = torch.empty(B, H, NT, device=dev, dtype=f32)
+    Qg = torch.empty_like(W)
+    M = torch.empty(B, H, NT, CHUNK, CHUNK, device=dev, dtype=dt)
+    P = N.ptr
+    N.call("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), P(KeT), P(GL), P(Qg), P(M), None, None, None,
+           None, None, None, B, T, H, DK, DV, code, int(l2norm), q_scale, stream)
+    o = torch.empty(B, T, H, DV, device=dev, dtype=dt)
+    sT = torch.empty(B, H, DK, DV, device=dev, dtype=f32) if want_sT else None
+    split = split_for(B * H, T, DV)
+    N.call("macai_gdr_state_fwd", P(W), P(U), P(KeT), P(GL), P(Qg), P(M), P(s0), P(o), P(sT), None, None,
+           B, T, H, DK, DV, code, 0, split, stream)
+    CALLS[f"fwd s{split}"] += 1
+    return o, sT
+
+
+def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float):
+    """Recompute (prep with the backward's operands; the state pass storing S_c and Vn), the reverse state pass, the
+    per-chunk backward.  Returns (dq, dk, dv in q's dtype; dg, dbeta, ds0 float32)."""
+    B, T, H, DK, DV, NT = _dims(q, v)
+    dev, dt = q.device, q.dtype
+    code, stream = N.dtype_code(dt), N.stream_of(q)
+    f32 = torch.float32
+    W = torch.empty(B, H, NT, CHUNK, DK, device=dev, dtype=dt)
+    U = torch.empty(B, H, NT, CHUNK, DV, device=dev, dtype=f32)
+    KeT = torch.empty(B, H, NT, DK, CHUNK, device=dev, dtype=dt)
+    GL = torch.empty(B, H, NT, device=dev, dtype=f32)
+    Ke = torch.empty_like(W)
+    QgT, WT = torch.empty_like(KeT), torch.empty_like(KeT)
     Mt = torch.empty(B, H, NT, CHUNK, CHUNK, device=dev, dtype=dt)
     A = torch.empty(B, H, NT, CHUNK, CHUNK, device=dev, dtype=f32)
     At = torch.empty_like(A)
-    N.call("macai_gdr_prep", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(g), N.ptr(beta), N.ptr(W), N.ptr(U), None, N.ptr(Mt),
-           N.ptr(A), N.ptr(At), B, T, H, DK, DV, code, int(l2norm), q_scale, stream)
+    P = N.ptr
+    N.call("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), P(KeT), P(GL), None, None, P(Ke), P(QgT),
+           P(WT), P(Mt), P(A), P(At), B, T, H, DK, DV, code, int(l2norm), q_scale, stream)
     split = split_for(B * H, T, DV)
     Sc = torch.empty(B, H, NT, DK, DV, device=dev, dtype=f32)
     Vn = torch.empty(B, H, NT, CHUNK, DV, device=dev, dtype=f32)
-    N.call("macai_gdr_state_fwd", N.ptr(q), N.ptr(k), N.ptr(g), N.ptr(W), N.ptr(U), None, N.ptr(s0), None, None,
-           N.ptr(Sc), N.ptr(Vn), B, T, H, DK, DV, code, int(l2norm), q_scale, N.STORE_STATES | N.NO_OUTPUT, split,
-           stream)
+    N.call("macai_gdr_state_fwd", P(W), P(U), P(KeT), P(GL), None, None, P(s0), None, None, P(Sc), P(Vn),
+           B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, stream)
     dSn = torch.empty_like(Sc)
     dVn = torch.empty_like(Vn)
     ds0 = torch.empty(B, H, DK, DV, device=dev, dtype=f32)
-    N.call("macai_gdr_state_bwd", N.ptr(q), N.ptr(k), N.ptr(g), N.ptr(W), N.ptr(Mt), N.ptr(do), N.ptr(dsT), N.ptr(dSn),
-           N.ptr(dVn), N.ptr(ds0), B, T, H, DK, DV, code, int(l2norm), q_scale, split, stream)
+    N.call("macai_gdr_state_bwd", P(Ke), P(QgT), P(WT), P(Mt), P(GL), P(do), P(dsT), P(dSn), P(dVn), P(ds0),
+           B, T, H, DK, DV, code, split, stream)
     CALLS[f"bwd s{split}"] += 1
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     dg, dbeta = torch.empty_like(g), torch.empty_like(beta)
-    N.call("macai_gdr_chunk_bwd", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(g), N.ptr(beta), N.ptr(do), N.ptr(A), N.ptr(At),
-           N.ptr(Sc), N.ptr(dSn), N.ptr(Vn), N.ptr(dVn), N.ptr(dq), N.ptr(dk), N.ptr(dv), N.ptr(dg), N.ptr(dbeta),
-           B, T, H, DK, DV, code, int(l2norm), q_scale, stream)
+    N.call("macai_gdr_chunk_bwd", P(q), P(k), P(v), P(g), P(beta), P(do), P(A), P(At), P(Sc), P(dSn), P(Vn), P(dVn),
+           P(dq), P(dk), P(dv), P(dg), P(dbeta), B, T, H, DK, DV, code, int(l2norm), q_scale, stream)
     return dq, dk, dv, dg, dbeta, ds0
-
-
-def _grad_in(x, like_shape, dtype, dev):
-    return None if x is None else x.to(dtype).contiguous()
 
 
 class GatedDeltaRule(torch.autograd.Function):

@@ -38,8 +38,9 @@ def test_library_exports_every_declared_symbol():
 
 
 def _prep(**over):
-    a = dict(q=1 << 20, k=1 << 20, v=1 << 20, g=1 << 20, beta=1 << 20, W=1 << 20, U=1 << 20, M=None, Mt=None, A=None,
-             At=None, B=1, T=64, H=1, DK=128, DV=128, dtype=1, l2=1, scale=1.0, stream=None)
+    p = 1 << 20
+    a = dict(q=p, k=p, v=p, g=p, beta=p, W=p, U=p, KeT=p, GL=p, Qg=None, M=None, Ke=None, QgT=None, WT=None, Mt=None,
+             A=None, At=None, B=1, T=64, H=1, DK=128, DV=128, dtype=1, l2=1, scale=1.0, stream=None)
     a.update(over)
     return N.lib().macai_gdr_prep(*a.values())
 
@@ -51,29 +52,28 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert _prep(dtype=7) == N.EUNSUP
     assert _prep(T=0) == N.EINVAL
     assert _prep(k=None) == N.EINVAL and b"null" in L.macai_gdr_last_error()
+    assert _prep(KeT=None) == N.EINVAL
     assert _prep(A=1 << 20) == N.EINVAL and b"A and At" in L.macai_gdr_last_error()
     assert _prep(W=(1 << 20) + 4) == N.EINVAL and b"aligned" in L.macai_gdr_last_error()
     assert _prep(M=1 << 20, q=None) == N.EINVAL
     p = 1 << 20
-    # state pass: flags that ask for nothing, a split that does not divide DV / 16, a missing output
-    assert L.macai_gdr_state_fwd(p, p, p, p, p, p, None, p, None, None, None, 1, 64, 1, 128, 128, 1, 1, 1.0, 8, 0,
-                                 None) == N.EINVAL
-    assert L.macai_gdr_state_fwd(p, p, p, p, p, p, None, p, None, None, None, 1, 64, 1, 128, 128, 1, 1, 1.0, 0, 3,
-                                 None) == N.EINVAL
-    assert b"split" in L.macai_gdr_last_error()
-    assert L.macai_gdr_state_fwd(p, p, p, p, p, None, None, p, None, None, None, 1, 64, 1, 128, 128, 1, 1, 1.0, 0, 0,
-                                 None) == N.EINVAL
-    assert L.macai_gdr_state_bwd(p, p, p, p, p, None, None, p, p, p, 1, 64, 1, 128, 128, 1, 1, 1.0, 0,
-                                 None) == N.EINVAL
+    sf = lambda *ptrs, flags=0, split=0, DV=128: L.macai_gdr_state_fwd(*ptrs, 1, 64, 1, 128, DV, 1, flags, split, None)
+    # flags that ask for nothing or both, a split that does not divide DV / 16, a missing output operand
+    assert sf(p, p, p, p, p, p, None, p, None, None, None, flags=8) == N.EINVAL
+    assert sf(p, p, p, p, p, p, None, p, None, p, p, flags=1) == N.EINVAL and b"flags" in L.macai_gdr_last_error()
+    assert sf(p, p, p, p, p, p, None, p, None, None, None, split=3) == N.EINVAL and b"split" in L.macai_gdr_last_error()
+    assert sf(p, p, p, p, p, p, None, p, None, None, None, split=1, DV=96) == N.EINVAL
+    assert sf(p, p, p, p, p, None, None, p, None, None, None) == N.EINVAL
+    assert L.macai_gdr_state_bwd(p, p, p, p, p, None, None, p, p, p, 1, 64, 1, 128, 128, 1, 0, None) == N.EINVAL
     assert L.macai_gdr_chunk_bwd(*([p] * 16), None, 1, 64, 1, 128, 128, 1, 1, 1.0, None) == N.EINVAL
     assert L.macai_gdr_decode(p, p, p, p, p, p, p, p, 1, 1, 256, 128, 1, 1, 1.0, None) == N.EUNSUP
 
 
 def test_call_maps_codes_to_exceptions():
     with pytest.raises(NotImplementedError, match="key head width"):
-        N.call("macai_gdr_prep", *([1 << 20] * 7), None, None, None, None, 1, 64, 1, 96, 128, 1, 1, 1.0, None)
+        N.call("macai_gdr_prep", *([1 << 20] * 9), *([None] * 8), 1, 64, 1, 96, 128, 1, 1, 1.0, None)
     with pytest.raises(ValueError, match="null"):
-        N.call("macai_gdr_prep", *([None] * 11), 1, 64, 1, 128, 128, 1, 1, 1.0, None)
+        N.call("macai_gdr_prep", *([None] * 17), 1, 64, 1, 128, 128, 1, 1, 1.0, None)
 
 
 def test_packed_rows_refused():
@@ -91,19 +91,24 @@ def test_cpu_tensors_refused_loudly():
 
 
 def test_split_rule():
-    """VALUE_SPLIT 'auto': the smallest power-of-two split giving >= 256 workgroups, capped at DV / 16 slices; an int
-    setting rounds down to a divisor (reference op.split_for semantics, test_chunking.py:176-199)."""
+    """VALUE_SPLIT 'auto': the smallest valid split (1, 2, 4 or 8 waves of 16 columns per workgroup) giving >= 256
+    workgroups, else the largest; an int setting rounds down to a valid split (reference op.split_for semantics,
+    test_chunking.py:176-199)."""
+    assert op.valid_splits(128) == [1, 2, 4, 8] and op.valid_splits(96) == [3, 6] and op.valid_splits(32) == [1, 2]
     assert op.split_for(64, 1024, 128) == 4
     assert op.split_for(16, 32768, 128) == 8
     assert op.split_for(512, 1024, 128) == 1
     assert op.split_for(2048, 1, 128) == 1
     assert op.split_for(1, 64, 32) == 2
+    assert op.split_for(2, 130, 96) == 6
     old = op.VALUE_SPLIT
     try:
         op.VALUE_SPLIT = 3
         assert op.split_for(64, 1024, 128) == 2
         op.VALUE_SPLIT = 16
         assert op.split_for(64, 1024, 128) == 8
+        op.VALUE_SPLIT = 1
+        assert op.split_for(64, 1024, 96) == 3
     finally:
         op.VALUE_SPLIT = old
 
