@@ -77,13 +77,13 @@ def kernel_costs(B, T, H, DK, DV, es=2):
     cost["state_fwd_out"] = dict(bytes=n * (3 * cdk * es + cdv * 4 + cc * es + 4) + io_v,
                                  flops=n * (3 * 2 * C * DK * DV + 2 * cc * DV))
     # the backward: prep writes W, U, KeT, GL, Ke, QgT, WT, Mt, A, At
-    cost["prep_bwd"] = dict(bytes=2 * io_k + io_v + gb + n * (5 * cdk * es + cdv * 4 + cc * es + 2 * cc * 4 + 4),
+    cost["prep_bwd"] = dict(bytes=2 * io_k + io_v + gb + n * (5 * cdk * es + cdv * 4 + 3 * cc * es + 4),
                             flops=n * (2 * 2 * cc * DK + cc * C / 3 + 2 * cc * DK + 2 * cc * DV))
-    cost["state_fwd_store"] = dict(bytes=n * (2 * cdk * es + cdv * 4 + 4 + sdk + cdv * 4),
+    cost["state_fwd_store"] = dict(bytes=n * (2 * cdk * es + cdv * 4 + 4 + sdk + cdv * es),
                                    flops=n * (2 * 2 * C * DK * DV))
-    cost["state_bwd"] = dict(bytes=n * (3 * cdk * es + cc * es + 4 + sdk + cdv * 4) + io_v,
+    cost["state_bwd"] = dict(bytes=n * (3 * cdk * es + cc * es + 4 + DK * DV * es + cdv * es) + io_v,
                              flops=n * (3 * 2 * C * DK * DV + 2 * cc * DV))
-    cost["chunk_bwd"] = dict(bytes=2 * io_k + 2 * io_v + gb + n * (2 * cc * 4 + 2 * sdk + 2 * cdv * 4)
+    cost["chunk_bwd"] = dict(bytes=2 * io_k + 2 * io_v + gb + n * (2 * cc * es + sdk + DK * DV * es + 2 * cdv * es)
                              + 2 * io_k + io_v + gb,
                              flops=n * (3 * 2 * C * DK * DV + 2 * cc * DK + 3 * 2 * cc * DK + 2 * 2 * cc * DV
                                         + 2 * 2 * cc * C + 3 * 2 * cc * DK + 2 * cc * DV))
@@ -108,10 +108,10 @@ def time_kernels(inp, reps=20):
     W, U, KeT, GL, Qg, M = e(B, H, NT, C, DK), e(B, H, NT, C, DV, d=f32), e(B, H, NT, DK, C), e(B, H, NT, d=f32), \
         e(B, H, NT, C, DK), e(B, H, NT, C, C)
     Ke, QgT, WT, Mt = e(B, H, NT, C, DK), e(B, H, NT, DK, C), e(B, H, NT, DK, C), e(B, H, NT, C, C)
-    A, At = e(B, H, NT, C, C, d=f32), e(B, H, NT, C, C, d=f32)
+    A, At = e(B, H, NT, C, C), e(B, H, NT, C, C)
     o = torch.empty_like(v)
-    Sc, Vn = e(B, H, NT, DK, DV, d=f32), e(B, H, NT, C, DV, d=f32)
-    dSn, dVn, ds0 = torch.empty_like(Sc), torch.empty_like(Vn), e(B, H, DK, DV, d=f32)
+    Sc, Vn = e(B, H, NT, DK, DV, d=f32), e(B, H, NT, C, DV)
+    dSn, dVn, ds0 = e(B, H, NT, DK, DV), torch.empty_like(Vn), e(B, H, DK, DV, d=f32)
     dq, dk, dv, dg, db = (torch.empty_like(x) for x in (q, k, v, g, beta))
     P = N.ptr
     calls = {

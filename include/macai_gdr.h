@@ -17,14 +17,16 @@
  *     KeT, QgT, WT [B, H, NT, DK, 64] dtype  (diag(e) K^)^T, (diag(gamma) Q^)^T, W^T
  *     U           [B, H, NT, 64, DV] float32  U = A diag(beta) V
  *     M, Mt       [B, H, NT, 64, 64] dtype   M = (Q^ K^T) * exp(G_i - G_j) (lower with the diagonal); M^T
- *     A, At       [B, H, NT, 64, 64] float32 A = (I + L)^-1; A^T
+ *     A, At       [B, H, NT, 64, 64] dtype   A = (I + L)^-1 (solved in fp32); A^T
  *     GL          [B, H, NT]         float32 exp(G_last) of each chunk
- *     Sc, dSn     [B, H, NT, DK, DV] float32 state entering each chunk; dLoss/dS_{c+1}
- *     Vn, dVn     [B, H, NT, 64, DV] float32 per-token corrections U - W S_c and their gradient
+ *     Sc          [B, H, NT, DK, DV] float32 state entering each chunk
+ *     dSn         [B, H, NT, DK, DV] dtype   dLoss/dS_{c+1} (carried in fp32, stored as the MFMA operand it is read as)
+ *     Vn, dVn     [B, H, NT, 64, DV] dtype   per-token corrections U - W S_c and their gradient
  *   G_r = sum_{s<=r} g_s inside the chunk, gamma = exp(G), e = exp(G_last - G), q^ / k^ the prologue's outputs.
  * With use_l2norm = 1 the kernels apply the reference prologue (_norm.py:1-10) themselves: q^ = q * rsqrt(|q|^2 + 1e-6)
  * * q_scale, k^ = k * rsqrt(|k|^2 + 1e-6), and the backward returns gradients w.r.t. the raw q and k.
- * Supported widths: DK in {32, 64, 128}; DV a multiple of 32 up to 512.  Pointers must be 16-byte aligned.
+ * Supported widths: DK in {32, 64, 128}; DV a multiple of 32 up to 512 (the backward: 32, 64, 96 or 128).
+ * Pointers must be 16-byte aligned.
  *
  * Return value: 0 on success, else an error code below; macai_gdr_last_error() describes the last failure of the
  * calling thread.  Argument checks run before any launch, so they are testable without a GPU.
@@ -62,7 +64,7 @@ int macai_gdr_abi_version(void);
  * Ke, QgT, WT, Mt, A and At).  Replaces `lib.gdc_prep(q, k, g, beta, gc, a, m, kg, T, H, ...)` (reference
  * op.py:63-72; kernel _chunked.py:220-313) and the fused prologue l2n_fwd (_norm.py:97). */
 int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, const float* beta, void* W, float* U,
-                   void* KeT, float* GL, void* Qg, void* M, void* Ke, void* QgT, void* WT, void* Mt, float* A, float* At,
+                   void* KeT, float* GL, void* Qg, void* M, void* Ke, void* QgT, void* WT, void* Mt, void* A, void* At,
                    int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm,
                    float q_scale, void* stream);
 
@@ -73,7 +75,7 @@ int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, 
  * beta, s0, gc, a, m, o, sT, sc, vn, xu, ckpt, T, H, DV, flags, ...)` (reference op.py:159, 217; kernel
  * _chunked.py:315-659). */
 int macai_gdr_state_fwd(const void* W, const float* U, const void* KeT, const float* GL, const void* Qg, const void* M,
-                        const float* s0, void* o, float* sT, float* Sc, float* Vn, int64_t B, int64_t T, int64_t H,
+                        const float* s0, void* o, float* sT, float* Sc, void* Vn, int64_t B, int64_t T, int64_t H,
                         int64_t DK, int64_t DV, int32_t dtype, int32_t flags, int32_t split, void* stream);
 
 /* The reverse state pass (north star (4)): from dS_NT = dsT (NULL = zeros) back over the chunks, dVn = M^T dO +
@@ -81,7 +83,7 @@ int macai_gdr_state_fwd(const void* W, const float* U, const void* KeT, const fl
  * writes ds0 = dLoss/d initial_state.  Replaces `lib.gdc_bwd_state(q, k, beta, do, dsT, gc, a, m, dsn, dvn, ds0, T,
  * H, DV, ...)` (reference op.py:234; kernel _chunked.py:661-903). */
 int macai_gdr_state_bwd(const void* Ke, const void* QgT, const void* WT, const void* Mt, const float* GL,
-                        const void* dO, const float* dsT, float* dSn, float* dVn, float* ds0, int64_t B, int64_t T,
+                        const void* dO, const float* dsT, void* dSn, void* dVn, float* ds0, int64_t B, int64_t T,
                         int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t split, void* stream);
 
 /* The per-chunk backward (north star (4)): dq, dk (w.r.t. the raw inputs when use_l2norm), dv in dtype; dg, dbeta in
@@ -89,8 +91,8 @@ int macai_gdr_state_bwd(const void* Ke, const void* QgT, const void* WT, const v
  * sc, dsn, vn, xu, dvn, dq, dk, dv, dg, dbeta, T, H, DV, ...)` (reference op.py:241-242; kernel
  * _chunked.py:905-1177) and the prologue's backward l2n_bwd (_norm.py:113). */
 int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float* g, const float* beta, const void* dO,
-                        const float* A, const float* At, const float* Sc, const float* dSn, const float* Vn,
-                        const float* dVn, void* dq, void* dk, void* dv, float* dg, float* dbeta, int64_t B, int64_t T,
+                        const void* A, const void* At, const float* Sc, const void* dSn, const void* Vn,
+                        const void* dVn, void* dq, void* dk, void* dv, float* dg, float* dbeta, int64_t B, int64_t T,
                         int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale,
                         void* stream);
 

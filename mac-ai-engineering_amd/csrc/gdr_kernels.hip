@@ -48,8 +48,8 @@ struct PrepArgs {
   void* QgT;     // [B,H,NT,DK,C] MT   (diag(gamma) Q^)^T        (or null)
   void* WT;      // [B,H,NT,DK,C] MT   W^T                       (or null)
   void* Mt;      // [B,H,NT,C,C]  MT   M^T                       (or null)
-  float* A;      // [B,H,NT,C,C]  fp32 A                         (or null)
-  float* At;     // [B,H,NT,C,C]  fp32 A^T                       (or null)
+  void* A;       // [B,H,NT,C,C]  MT   A                         (or null)
+  void* At;      // [B,H,NT,C,C]  MT   A^T                       (or null)
   int B, T, H, DV, NT;
   int l2norm;
   float q_scale;
@@ -64,8 +64,8 @@ struct StateFwdArgs {
   const float* s0;
   void* o;
   float* sT;
-  float* Sc;     // [B,H,NT,DK,DV]
-  float* Vn;     // [B,H,NT,C,DV]
+  float* Sc;     // [B,H,NT,DK,DV] fp32 (the backward's <S_c, dS_{c+1}> needs it unrounded)
+  void* Vn;      // [B,H,NT,C,DV]  MT
   int B, T, H, DV, NT;
   int nslice;    // workgroups per head-row
 };
@@ -75,8 +75,8 @@ struct StateBwdArgs {
   const float* GL;
   const void* dO;
   const float* dsT;
-  float* dSn;    // [B,H,NT,DK,DV]  dS_{c+1}
-  float* dVn;    // [B,H,NT,C,DV]
+  void* dSn;     // [B,H,NT,DK,DV] MT  dS_{c+1}
+  void* dVn;     // [B,H,NT,C,DV]  MT
   float* ds0;    // [B,H,DK,DV]
   int B, T, H, DV, NT;
   int nslice;
@@ -86,7 +86,9 @@ struct ChunkBwdArgs {
   const void *q, *k, *v;
   const float *g, *beta;
   const void* dO;
-  const float *A, *At, *Sc, *dSn, *Vn, *dVn;
+  const void *A, *At;                         // MT
+  const float* Sc;                            // fp32
+  const void *dSn, *Vn, *dVn;                 // MT
   void *dq, *dk, *dv;
   float *dg, *dbeta;
   int B, T, H, DV, NT;
@@ -326,11 +328,11 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
     }
   }
   if (a.A) {
-    float* Ag = a.A + bhc * C * C;
-    float* Atg = a.At + bhc * C * C;
+    MT* Ag = (MT*)a.A + bhc * C * C;
+    MT* Atg = (MT*)a.At + bhc * C * C;
     for (int i = threadIdx.x; i < C * C; i += blockDim.x) {
       const int row = i / C, col = i % C;
-      const float x = sA[row * FP + col];
+      const MT x = from_f<MT>(sA[row * FP + col]);
       Ag[row * C + col] = x;
       Atg[col * C + row] = x;
     }
@@ -376,9 +378,9 @@ struct Buffers {
 // ---------------------------------------------------------------------------------------------------------------------
 template <typename MT, int DK, int NW, bool OUT, bool STORE>
 __global__ void __launch_bounds__(64 * NW) state_fwd_kernel(StateFwdArgs a) {
-  using GW = Swz<MT, C, DK>;    // W, diag(gamma) Q^     [t][d]
-  using GKT = Swz<MT, DK, C>;   // (diag(e) K^)^T        [d][t]
-  using GM = Swz<MT, C, C>;     // M                     [t][s]
+  using GW = Tile<MT, C, DK>;    // W, diag(gamma) Q^     [t][d]
+  using GKT = Tile<MT, DK, C>;   // (diag(e) K^)^T        [d][t]
+  using GM = Tile<MT, C, C>;     // M                     [t][s]
   constexpr int ND = DK / 16;
   constexpr int O_KT = GW::ELEMS, O_Q = O_KT + GKT::ELEMS, O_M = O_Q + (OUT ? GW::ELEMS : 0);
   constexpr int SZ = O_M + (OUT ? GM::ELEMS : 0);
@@ -459,7 +461,7 @@ __global__ void __launch_bounds__(64 * NW) state_fwd_kernel(StateFwdArgs a) {
     for (int mi = 0; mi < 4; ++mi) {
       f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int p = 0; p < ND / 2; ++p) mma(acc, frag_swz<MT, GW>(st, 16 * mi, 32 * p), Sf[p]);
+      for (int p = 0; p < ND / 2; ++p) mma(acc, frag_tile<MT, GW>(st, 16 * mi, 32 * p), Sf[p]);
       Vn[mi] = U[mi] - acc;
     }
     Frag<MT> Vf[2];
@@ -471,7 +473,7 @@ __global__ void __launch_bounds__(64 * NW) state_fwd_kernel(StateFwdArgs a) {
     for (int di = 0; di < ND; ++di) {
       f4 acc = S[di] * gl;
 #pragma unroll
-      for (int p = 0; p < 2; ++p) mma(acc, frag_swz<MT, GKT>(st + O_KT, 16 * di, 32 * p), Vf[p]);
+      for (int p = 0; p < 2; ++p) mma(acc, frag_tile<MT, GKT>(st + O_KT, 16 * di, 32 * p), Vf[p]);
       Sn[di] = acc;
     }
     if (STORE) {
@@ -480,11 +482,11 @@ __global__ void __launch_bounds__(64 * NW) state_fwd_kernel(StateFwdArgs a) {
       for (int di = 0; di < ND; ++di)
 #pragma unroll
         for (int r = 0; r < 4; ++r) Scc[(16 * di + 4 * j + r) * DV + col] = S[di][r];
-      float* Vnc = a.Vn + bhc * C * DV;
+      MT* Vnc = (MT*)a.Vn + bhc * C * DV;
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) Vnc[(16 * mi + 4 * j + r) * DV + col] = Vn[mi][r];
+        for (int r = 0; r < 4; ++r) Vnc[(16 * mi + 4 * j + r) * DV + col] = from_f<MT>(Vn[mi][r]);
     }
     if (OUT) {
       // O = diag(gamma) Q S + M Vn (M lower triangular: k-blocks past the row block are zero)
@@ -492,10 +494,10 @@ __global__ void __launch_bounds__(64 * NW) state_fwd_kernel(StateFwdArgs a) {
       for (int mi = 0; mi < 4; ++mi) {
         f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int p = 0; p < ND / 2; ++p) mma(acc, frag_swz<MT, GW>(st + O_Q, 16 * mi, 32 * p), Sf[p]);
+        for (int p = 0; p < ND / 2; ++p) mma(acc, frag_tile<MT, GW>(st + O_Q, 16 * mi, 32 * p), Sf[p]);
 #pragma unroll
         for (int p = 0; p < 2; ++p)
-          if (32 * p <= 16 * mi + 15) mma(acc, frag_swz<MT, GM>(st + O_M, 16 * mi, 32 * p), Vf[p]);
+          if (32 * p <= 16 * mi + 15) mma(acc, frag_tile<MT, GM>(st + O_M, 16 * mi, 32 * p), Vf[p]);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int t = t0 + 16 * mi + 4 * j + r;
@@ -521,10 +523,10 @@ __global__ void __launch_bounds__(64 * NW) state_fwd_kernel(StateFwdArgs a) {
 // ---------------------------------------------------------------------------------------------------------------------
 template <typename MT, int DK, int NW>
 __global__ void __launch_bounds__(64 * NW) state_bwd_kernel(StateBwdArgs a) {
-  using GK = Swz<MT, C, DK>;        // diag(e) K^          [t][d]
-  using GT = Swz<MT, DK, C>;        // QgT, WT             [d][t]
-  using GM = Swz<MT, C, C>;         // M^T                 [s][t]
-  using GO = Swz<MT, C, 16 * NW>;   // dO columns          [t][v]
+  using GK = Tile<MT, C, DK>;        // diag(e) K^          [t][d]
+  using GT = Tile<MT, DK, C>;        // QgT, WT             [d][t]
+  using GM = Tile<MT, C, C>;         // M^T                 [s][t]
+  using GO = Tile<MT, C, 16 * NW>;   // dO columns          [t][v]
   constexpr int ND = DK / 16;
   constexpr int O_Q = GK::ELEMS, O_W = O_Q + GT::ELEMS, O_M = O_W + GT::ELEMS, O_O = O_M + GM::ELEMS;
   constexpr int SZ = O_O + GO::ELEMS;
@@ -584,7 +586,13 @@ __global__ void __launch_bounds__(64 * NW) state_bwd_kernel(StateBwdArgs a) {
 
     Frag<MT> Of[2];
 #pragma unroll
-    for (int p = 0; p < 2; ++p) Of[p] = frag_swz_rows<MT, MT, GO>(st + O_O, 32 * p, w * 16 + (l & 15), t0, T);
+    for (int p = 0; p < 2; ++p) {
+      Of[p] = frag_tile_rows<MT, GO>(st + O_O, 32 * p, w * 16 + (l & 15));
+      if (t0 + C > T)   // rows past the sequence end hold copies of the last row: zero them
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (t0 + 32 * p + kmap(j, e) >= T) Of[p].set(e, 0.f);
+    }
     Frag<MT> Sf[ND / 2];
 #pragma unroll
     for (int p = 0; p < ND / 2; ++p) Sf[p] = frag_acc<MT>(dS[2 * p], dS[2 * p + 1]);
@@ -594,10 +602,10 @@ __global__ void __launch_bounds__(64 * NW) state_bwd_kernel(StateBwdArgs a) {
     for (int mi = 0; mi < 4; ++mi) {
       f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int p = 0; p < ND / 2; ++p) mma(acc, frag_swz<MT, GK>(st, 16 * mi, 32 * p), Sf[p]);
+      for (int p = 0; p < ND / 2; ++p) mma(acc, frag_tile<MT, GK>(st, 16 * mi, 32 * p), Sf[p]);
 #pragma unroll
       for (int p = 0; p < 2; ++p)
-        if (32 * p + 31 >= 16 * mi) mma(acc, frag_swz<MT, GM>(st + O_M, 16 * mi, 32 * p), Of[p]);
+        if (32 * p + 31 >= 16 * mi) mma(acc, frag_tile<MT, GM>(st + O_M, 16 * mi, 32 * p), Of[p]);
       dV[mi] = acc;
     }
     Frag<MT> Vf[2];
@@ -610,22 +618,22 @@ __global__ void __launch_bounds__(64 * NW) state_bwd_kernel(StateBwdArgs a) {
       f4 acc = dS[di] * gl;
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        mma(acc, frag_swz<MT, GT>(st + O_W, 16 * di, 32 * p), Vf[p]);
-        mma(acc, frag_swz<MT, GT>(st + O_Q, 16 * di, 32 * p), Of[p]);
+        mma(acc, frag_tile<MT, GT>(st + O_W, 16 * di, 32 * p), Vf[p]);
+        mma(acc, frag_tile<MT, GT>(st + O_Q, 16 * di, 32 * p), Of[p]);
       }
       dSn[di] = acc;
     }
     {
-      float* dSc = a.dSn + bhc * DK * DV;
+      MT* dSc = (MT*)a.dSn + bhc * DK * DV;
 #pragma unroll
       for (int di = 0; di < ND; ++di)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dSc[(16 * di + 4 * j + r) * DV + col] = dS[di][r];
-      float* dVc = a.dVn + bhc * C * DV;
+        for (int r = 0; r < 4; ++r) dSc[(16 * di + 4 * j + r) * DV + col] = from_f<MT>(dS[di][r]);
+      MT* dVc = (MT*)a.dVn + bhc * C * DV;
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dVc[(16 * mi + 4 * j + r) * DV + col] = dV[mi][r];
+        for (int r = 0; r < 4; ++r) dVc[(16 * mi + 4 * j + r) * DV + col] = from_f<MT>(dV[mi][r]);
     }
 #pragma unroll
     for (int di = 0; di < ND; ++di) dS[di] = dSn[di];
@@ -643,16 +651,37 @@ __global__ void __launch_bounds__(64 * NW) state_bwd_kernel(StateBwdArgs a) {
 // ---------------------------------------------------------------------------------------------------------------------
 enum { P_QD = 0, P_E, P_KX, P_R1, P_R2, P_VY, P_DQ, P_DK, NPART };
 
-template <typename IT, typename MT, int DK>
+template <typename MT>
+__device__ __forceinline__ Frag<MT> zero_frag() {
+  Frag<MT> o;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) o.set(r, 0.f);
+  return o;
+}
+
+// One workgroup (4 waves) per (chunk, head, batch row).  bf16 operands: the chunk's raw q, k, dO and Vn, dVn, A^T are
+// copied into padded LDS tiles at the start (asynchronous, all in flight together) and every MFMA fragment is read from
+// there; fp32 operands do not fit, so the same accessors read them from global memory.  The prologue's row scales
+// (q^ = q rq DK^-1/2, k^ = k rk) are applied to the products' rows and columns, and folded into the stored dM and Z, so
+// the raw inputs are the MFMA operands.  Wave w owns key-column blocks w, w + 4, ... of the [C x DK] products, column
+// block w of the [C x C] ones and value-column blocks w, w + 4, ...
+template <typename MT, int DK, int DV>
 __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
-  constexpr int KP = DK + 8, CP = C + 8, FP = C + 4;
+  constexpr bool STAGE = sizeof(MT) == 2;
+  constexpr int KP = DK + 8, CP = C + 8;
   constexpr int NBD = DK / 16;            // 16-column blocks of the key width
   constexpr int NBW = (NBD + 3) / 4;      // most blocks a wave owns
+  using GQ = Tile<MT, C, DK>;
+  using GV = Tile<MT, C, DV>;
+  using GA = Tile<MT, C, C>;
+  constexpr int O_K = GQ::ELEMS, O_O = 2 * GQ::ELEMS, O_VN = O_O + GV::ELEMS, O_DV = O_VN + GV::ELEMS,
+                O_AT = O_DV + GV::ELEMS, TILES = STAGE ? O_AT + GA::ELEMS : 8;
+  __shared__ __attribute__((aligned(16))) MT tiles[TILES];
   __shared__ __attribute__((aligned(16))) MT sdW[C * KP];   // dW = -dVn S_c^T
-  __shared__ __attribute__((aligned(16))) MT sdM[C * CP];   // dM = Gamma * (dO Vn^T)
-  __shared__ __attribute__((aligned(16))) MT sdMT[C * CP];  // dM^T
-  __shared__ __attribute__((aligned(16))) MT sZ[C * CP];    // Z = diag(beta) P + (diag(beta) P)^T
-  __shared__ __attribute__((aligned(16))) float sdA[C * FP];
+  __shared__ __attribute__((aligned(16))) MT sdMk[C * CP];  // dM diag(rk):            [t][s] = dM[t][s] rk_s
+  __shared__ __attribute__((aligned(16))) MT sdMq[C * CP];  // dM^T diag(rq DK^-1/2):  [t][s] = dM[s][t] rq_s qs
+  __shared__ __attribute__((aligned(16))) MT sZk[C * CP];   // Z diag(rk), Z = diag(beta) P + (diag(beta) P)^T
+  __shared__ __attribute__((aligned(16))) MT sdA[C * CP];   // dA
   __shared__ ChunkScalars cs;
   __shared__ float rk[C], rq[C];
   __shared__ float part[NPART][4][C];
@@ -660,36 +689,97 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
   __shared__ float colR1[C], colR2b[C];
 
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int T = a.T, H = a.H, DV = a.DV, NT = a.NT;
-  const int t0 = c * C;
+  const int T = a.T, H = a.H, NT = a.NT;
+  const int t0 = c * C, nrows = (T - t0 < C) ? T - t0 : C;
   const int l = lane_id(), w = wave_id(), j = l >> 4;
   const size_t qk_base = ((size_t)b * T * H + h) * DK, qk_pitch = (size_t)H * DK;
   const size_t v_base = ((size_t)b * T * H + h) * DV, v_pitch = (size_t)H * DV;
   const size_t s_base = (size_t)b * T * H + h;
   const size_t bhc = ((size_t)b * H + h) * NT + c;
-  const IT* q = (const IT*)a.q + qk_base;
-  const IT* k = (const IT*)a.k + qk_base;
-  const IT* v = (const IT*)a.v + v_base;
-  const IT* dO = (const IT*)a.dO + v_base;
+  const MT* q = (const MT*)a.q + qk_base;
+  const MT* k = (const MT*)a.k + qk_base;
+  const MT* v = (const MT*)a.v + v_base;
+  const MT* dO = (const MT*)a.dO + v_base;
   const float* Scc = a.Sc + bhc * DK * DV;
-  const float* dSc = a.dSn + bhc * DK * DV;
-  const float* Vnc = a.Vn + bhc * C * DV;
-  const float* dVc = a.dVn + bhc * C * DV;
-  const float* Ac = a.A + bhc * C * C;
-  const float* Atc = a.At + bhc * C * C;
+  const MT* dSc = (const MT*)a.dSn + bhc * DK * DV;
+  const MT* Vnc = (const MT*)a.Vn + bhc * C * DV;
+  const MT* dVc = (const MT*)a.dVn + bhc * C * DV;
+  const MT* Ac = (const MT*)a.A + bhc * C * C;
+  const MT* Atc = (const MT*)a.At + bhc * C * C;
   const float qs = a.q_scale;
 
+  if constexpr (STAGE) {
+    GQ::dma(tiles, q + (size_t)t0 * qk_pitch, qk_pitch, w, 4, nrows);
+    GQ::dma(tiles + O_K, k + (size_t)t0 * qk_pitch, qk_pitch, w, 4, nrows);
+    GV::dma(tiles + O_O, dO + (size_t)t0 * v_pitch, v_pitch, w, 4, nrows);
+    GV::dma(tiles + O_VN, Vnc, DV, w, 4);
+    GV::dma(tiles + O_DV, dVc, DV, w, 4);
+    GA::dma(tiles + O_AT, Atc, C, w, 4);
+  }
   if (w == 0) chunk_scalars(cs, a.g, a.beta, s_base, H, t0, T);
   if (a.l2norm) {
-    row_rnorms<IT, DK>(rk, (const IT*)a.k, qk_base, qk_pitch, t0, T, 4);
-    row_rnorms<IT, DK>(rq, (const IT*)a.q, qk_base, qk_pitch, t0, T, 4);
+    row_rnorms<MT, DK>(rk, (const MT*)a.k, qk_base, qk_pitch, t0, T, 4);
+    row_rnorms<MT, DK>(rq, (const MT*)a.q, qk_base, qk_pitch, t0, T, 4);
   } else if (threadIdx.x < C) {
-    rk[threadIdx.x] = 1.f;
-    rq[threadIdx.x] = 1.f;
+    rk[threadIdx.x] = (int)threadIdx.x < nrows ? 1.f : 0.f;
+    rq[threadIdx.x] = (int)threadIdx.x < nrows ? 1.f : 0.f;
   }
+  if constexpr (STAGE) wait_dma();
   __syncthreads();
-  auto qrow = [&](int r) { return rq[r] * qs; };
-  auto krow = [&](int r) { return rk[r]; };
+
+  // operand accessors: raw rows (masked past the sequence end where the tile holds copies of the last row)
+  auto fq = [&](int row0, int k0) -> Frag<MT> {   // raw q rows
+    if constexpr (STAGE) return (row0 + (l & 15) < nrows) ? frag_tile<MT, GQ>(tiles, row0, k0) : zero_frag<MT>();
+    else return frag_k_seq<MT, MT>(q, qk_pitch, t0, T, row0, k0, One());
+  };
+  auto fk = [&](int row0, int k0) -> Frag<MT> {   // raw k rows
+    if constexpr (STAGE) return (row0 + (l & 15) < nrows) ? frag_tile<MT, GQ>(tiles + O_K, row0, k0) : zero_frag<MT>();
+    else return frag_k_seq<MT, MT>(k, qk_pitch, t0, T, row0, k0, One());
+  };
+  auto rows_masked = [&](Frag<MT> f, int krow0) -> Frag<MT> {
+    if (nrows < C)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (krow0 + kmap(j, e) >= nrows) f.set(e, 0.f);
+    return f;
+  };
+  auto fqrows = [&](int krow0, int col) -> Frag<MT> {   // raw q, k = rows
+    if constexpr (STAGE) return rows_masked(frag_tile_rows<MT, GQ>(tiles, krow0, col), krow0);
+    else return frag_rows<MT, MT>(q, qk_pitch, t0, T, krow0, col, One());
+  };
+  auto fkrows = [&](int krow0, int col) -> Frag<MT> {   // raw k, k = rows
+    if constexpr (STAGE) return rows_masked(frag_tile_rows<MT, GQ>(tiles + O_K, krow0, col), krow0);
+    else return frag_rows<MT, MT>(k, qk_pitch, t0, T, krow0, col, One());
+  };
+  auto fO = [&](int row0, int k0) -> Frag<MT> {
+    if constexpr (STAGE) return (row0 + (l & 15) < nrows) ? frag_tile<MT, GV>(tiles + O_O, row0, k0) : zero_frag<MT>();
+    else return frag_k_seq<MT, MT>(dO, v_pitch, t0, T, row0, k0, One());
+  };
+  auto fVn = [&](int row0, int k0) -> Frag<MT> {
+    if constexpr (STAGE) return frag_tile<MT, GV>(tiles + O_VN, row0, k0);
+    else return frag_k<MT, MT>(Vnc, DV, row0, k0);
+  };
+  auto fdVn = [&](int row0, int k0) -> Frag<MT> {
+    if constexpr (STAGE) return frag_tile<MT, GV>(tiles + O_DV, row0, k0);
+    else return frag_k<MT, MT>(dVc, DV, row0, k0);
+  };
+  auto fdVnrows = [&](int krow0, int col) -> Frag<MT> {
+    if constexpr (STAGE) return frag_tile_rows<MT, GV>(tiles + O_DV, krow0, col);
+    else return frag_rows<MT, MT>(dVc, DV, 0, C, krow0, col, One());
+  };
+  auto fAt = [&](int row0, int k0) -> Frag<MT> {
+    if constexpr (STAGE) return frag_tile<MT, GA>(tiles + O_AT, row0, k0);
+    else return frag_k<MT, MT>(Atc, C, row0, k0);
+  };
+  // raw q / k at (chunk row, key column) times the row's inverse norm: the unit-norm direction (0 past the end)
+  auto xq = [&](int row, int d) -> float {
+    if constexpr (STAGE) return to_f(tiles[GQ::offset(row, d)]) * rq[row];
+    else return (t0 + row < T) ? to_f(q[(size_t)(t0 + row) * qk_pitch + d]) * rq[row] : 0.f;
+  };
+  auto xk = [&](int row, int d) -> float {
+    if constexpr (STAGE) return to_f(tiles[O_K + GQ::offset(row, d)]) * rk[row];
+    else return (t0 + row < T) ? to_f(k[(size_t)(t0 + row) * qk_pitch + d]) * rk[row] : 0.f;
+  };
 
   // ---- B: products with the chunk states; wave w owns key-column blocks w, w + 4, ...
   f4 dQ[NBW][4], dK[NBW][4];
@@ -707,17 +797,25 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
     f4 aO[4], aV[4], aD[4];
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) aO[mi] = aV[mi] = aD[mi] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
     for (int kb = 0; kb < DV / 32; ++kb) {
       const Frag<float> s32 = frag_k_f32(Scc, DV, d0, 32 * kb);
-      const Frag<float> d32 = frag_k_f32(dSc, DV, d0, 32 * kb);
+      const Frag<MT> bS = cvt<MT>(s32);
+      const Frag<MT> bD = frag_k<MT, MT>(dSc, DV, d0, 32 * kb);
 #pragma unroll
-      for (int r = 0; r < 8; ++r) sds = fmaf(s32.v[r], d32.v[r], sds);
-      const Frag<MT> bS = cvt<MT>(s32), bD = cvt<MT>(d32);
+      for (int r = 0; r < 8; ++r) sds = fmaf(s32.v[r], bD.get(r), sds);
+      Frag<MT> fo[4], fv[4], fd[4];
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) {
-        mma(aO[mi], frag_k_seq<MT, IT>(dO, v_pitch, t0, T, 16 * mi, 32 * kb, One()), bS);
-        mma(aV[mi], frag_k<MT, float>(Vnc, DV, 16 * mi, 32 * kb), bD);
-        mma(aD[mi], frag_k<MT, float>(dVc, DV, 16 * mi, 32 * kb), bS);
+        fo[mi] = fO(16 * mi, 32 * kb);
+        fv[mi] = fVn(16 * mi, 32 * kb);
+        fd[mi] = fdVn(16 * mi, 32 * kb);
+      }
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+        mma(aO[mi], fo[mi], bS);
+        mma(aV[mi], fv[mi], bD);
+        mma(aD[mi], fd[mi], bS);
       }
     }
     float kv[4][4];
@@ -725,9 +823,9 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = 16 * mi + 4 * j + r, t = t0 + row;
-        const float qv = (t < T) ? to_f(q[(size_t)t * qk_pitch + d]) * rq[row] * qs : 0.f;
-        kv[mi][r] = (t < T) ? to_f(k[(size_t)t * qk_pitch + d]) * rk[row] : 0.f;
+        const int row = 16 * mi + 4 * j + r;
+        const float qv = xq(row, d) * qs;
+        kv[mi][r] = xk(row, d);
         const float oq = aO[mi][r] * cs.gam[row];
         dQ[ib][mi][r] = oq;
         pQD[mi][r] = fmaf(qv, oq, pQD[mi][r]);
@@ -737,13 +835,15 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
         sdW[row * KP + d] = from_f<MT>(-aD[mi][r]);
       }
     // X = A^T dW = -A^T (dVn S_c^T)   (A^T upper triangular)
+    Frag<MT> xf[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) xf[p] = frag_acc<MT>(aD[2 * p], aD[2 * p + 1], -1.f);
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
       f4 x = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int p = 0; p < 2; ++p)
-        if (32 * p + 31 >= 16 * mi)
-          mma(x, frag_k<MT, float>(Atc, C, 16 * mi, 32 * p), frag_acc<MT>(aD[2 * p], aD[2 * p + 1], -1.f));
+        if (32 * p + 31 >= 16 * mi) mma(x, fAt(16 * mi, 32 * p), xf[p]);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * mi + 4 * j + r;
@@ -775,44 +875,59 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
   for (int mi = 0; mi < 4; ++mi) QK[mi] = KK[mi] = dOV[mi] = Ta[mi] = Tb[mi] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int p = 0; p < DK / 32; ++p) {
-    const Frag<MT> bk = frag_k_seq<MT, IT>(k, qk_pitch, t0, T, 16 * cb, 32 * p, krow);
+    const Frag<MT> bk = fk(16 * cb, 32 * p);
+    Frag<MT> fa[4], fb[4], fw[4];
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
-      mma(QK[mi], frag_k_seq<MT, IT>(q, qk_pitch, t0, T, 16 * mi, 32 * p, qrow), bk);
-      mma(KK[mi], frag_k_seq<MT, IT>(k, qk_pitch, t0, T, 16 * mi, 32 * p, krow), bk);
-      mma(Ta[mi], frag_k_raw(sdW, KP, 16 * mi, 32 * p), bk);
+      fa[mi] = fq(16 * mi, 32 * p);
+      fb[mi] = fk(16 * mi, 32 * p);
+      fw[mi] = frag_k_raw(sdW, KP, 16 * mi, 32 * p);
+    }
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      mma(QK[mi], fa[mi], bk);
+      mma(KK[mi], fb[mi], bk);
+      mma(Ta[mi], fw[mi], bk);
     }
   }
+#pragma unroll
   for (int kb = 0; kb < DV / 32; ++kb) {
-    const Frag<MT> bvn = frag_k<MT, float>(Vnc, DV, 16 * cb, 32 * kb);
-    const Frag<MT> bv = frag_k_seq<MT, IT>(v, v_pitch, t0, T, 16 * cb, 32 * kb, One());
+    const Frag<MT> bvn = fVn(16 * cb, 32 * kb);
+    const Frag<MT> bv = frag_k_seq<MT, MT>(v, v_pitch, t0, T, 16 * cb, 32 * kb, One());
+    Frag<MT> fo[4], fd[4];
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
-      mma(dOV[mi], frag_k_seq<MT, IT>(dO, v_pitch, t0, T, 16 * mi, 32 * kb, One()), bvn);
-      mma(Tb[mi], frag_k<MT, float>(dVc, DV, 16 * mi, 32 * kb), bv);
+      fo[mi] = fO(16 * mi, 32 * kb);
+      fd[mi] = fdVn(16 * mi, 32 * kb);
+    }
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      mma(dOV[mi], fo[mi], bvn);
+      mma(Tb[mi], fd[mi], bv);
     }
   }
-  float KG[4][4];
+  float gm[4][4], KG[4][4];
   {
     float cR1 = 0.f;
     float pR1[4][4];
-    const float bs = cs.beta[s], bgs = cs.beta[s] * cs.gam[s];
+    const float bs = cs.beta[s], bgs = cs.beta[s] * cs.gam[s], rks = rk[s], rqs = rq[s] * qs;
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * mi + 4 * j + r;
-        const float gm = (row >= s) ? cs.decay(row, s) : 0.f;
-        const float Mv = QK[mi][r] * gm;
-        const float dMv = dOV[mi][r] * gm;
-        sdM[row * CP + s] = from_f<MT>(dMv);
-        sdMT[s * CP + row] = from_f<MT>(dMv);
+        gm[mi][r] = (row >= s) ? cs.decay(row, s) : 0.f;
+        const float Mv = QK[mi][r] * (rq[row] * qs * rks) * gm[mi][r];
+        const float dMv = dOV[mi][r] * gm[mi][r];
+        sdMk[row * CP + s] = from_f<MT>(dMv * rks);
+        sdMq[s * CP + row] = from_f<MT>(dMv * (rq[row] * qs));
         const float r1 = (row > s) ? dOV[mi][r] * Mv : 0.f;
         pR1[mi][r] = r1;
         cR1 += r1;
-        sdA[row * FP + s] = (row > s) ? fmaf(Ta[mi][r], bgs, Tb[mi][r] * bs) : 0.f;
-        KG[mi][r] = (row > s) ? KK[mi][r] * gm : 0.f;
+        sdA[row * CP + s] = from_f<MT>((row > s) ? fmaf(Ta[mi][r] * rks, bgs, Tb[mi][r] * bs) : 0.f);
+        KG[mi][r] = (row > s) ? KK[mi][r] * (rk[row] * rks) * gm[mi][r] : 0.f;
       }
+    (void)rqs;
     cR1 = across_groups_sum(cR1);
     if (j == 0) colR1[s] = cR1;
 #pragma unroll
@@ -832,7 +947,7 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
 #pragma unroll
     for (int p = 0; p < 2; ++p)
       if (32 * p <= 16 * mi + 15 && 32 * p <= 16 * cb + 15)
-        mma(T1[mi], frag_k<MT, float>(sdA, FP, 16 * mi, 32 * p), frag_k<MT, float>(Ac, C, 16 * cb, 32 * p));
+        mma(T1[mi], frag_k_raw(sdA, CP, 16 * mi, 32 * p), frag_k<MT, MT>(Ac, C, 16 * cb, 32 * p));
   }
   Frag<MT> T1f[2];
 #pragma unroll
@@ -842,29 +957,28 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
     f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int p = 0; p < 2; ++p)
-      if (32 * p + 31 >= 16 * mi) mma(acc, frag_k<MT, float>(Atc, C, 16 * mi, 32 * p), T1f[p]);
+      if (32 * p + 31 >= 16 * mi) mma(acc, fAt(16 * mi, 32 * p), T1f[p]);
     dL[mi] = acc;
   }
   {
     float cR2 = 0.f;
     float pR2[4][4];
+    const float rks = rk[s];
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * mi + 4 * j + r;
         const float dl = (row > s) ? -dL[mi][r] : 0.f;
-        const float gm = (row > s) ? cs.decay(row, s) : 0.f;
-        const float Pv = dl * gm;
         const float r2 = dl * KG[mi][r];
         pR2[mi][r] = r2;
         cR2 = fmaf(cs.beta[row], r2, cR2);
-        const float z = cs.beta[row] * Pv;
+        const float z = cs.beta[row] * dl * gm[mi][r];    // Z[row][s] = Z[s][row] = beta_row P[row][s]
         if (row > s) {
-          sZ[row * CP + s] = from_f<MT>(z);
-          sZ[s * CP + row] = from_f<MT>(z);
+          sZk[row * CP + s] = from_f<MT>(z * rks);
+          sZk[s * CP + row] = from_f<MT>(z * rk[row]);
         } else if (row == s) {
-          sZ[row * CP + s] = from_f<MT>(0.f);
+          sZk[row * CP + s] = from_f<MT>(0.f);
         }
       }
     cR2 = across_groups_sum(cR2);
@@ -879,7 +993,7 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
   }
   __syncthreads();
 
-  // ---- D: dQ^ += dM K^; dK^ += dM^T Q^ + Z K^   (own key-column blocks)
+  // ---- D: dQ^ += (dM diag(rk)) K; dK^ += (dM^T diag(rq qs)) Q + (Z diag(rk)) K   (own key-column blocks)
   float pDQ[4][4], pDK[4][4];
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi)
@@ -892,13 +1006,20 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
     const int d = 16 * nb + (l & 15);
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      const Frag<MT> bK = frag_rows<MT, IT>(k, qk_pitch, t0, T, 32 * p, d, krow);
-      const Frag<MT> bQ = frag_rows<MT, IT>(q, qk_pitch, t0, T, 32 * p, d, qrow);
+      const Frag<MT> bK = fkrows(32 * p, d);
+      const Frag<MT> bQ = fqrows(32 * p, d);
+      Frag<MT> fm[4], fmt[4], fz[4];
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) {
-        if (32 * p <= 16 * mi + 15) mma(dQ[ib][mi], frag_k_raw(sdM, CP, 16 * mi, 32 * p), bK);
-        if (32 * p + 31 >= 16 * mi) mma(dK[ib][mi], frag_k_raw(sdMT, CP, 16 * mi, 32 * p), bQ);
-        mma(dK[ib][mi], frag_k_raw(sZ, CP, 16 * mi, 32 * p), bK);
+        fm[mi] = frag_k_raw(sdMk, CP, 16 * mi, 32 * p);
+        fmt[mi] = frag_k_raw(sdMq, CP, 16 * mi, 32 * p);
+        fz[mi] = frag_k_raw(sZk, CP, 16 * mi, 32 * p);
+      }
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+        if (32 * p <= 16 * mi + 15) mma(dQ[ib][mi], fm[mi], bK);
+        if (32 * p + 31 >= 16 * mi) mma(dK[ib][mi], fmt[mi], bQ);
+        mma(dK[ib][mi], fz[mi], bK);
       }
     }
     if (a.l2norm) {
@@ -906,11 +1027,9 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
       for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int row = 16 * mi + 4 * j + r, t = t0 + row;
-          if (t < T) {
-            pDQ[mi][r] = fmaf(to_f(q[(size_t)t * qk_pitch + d]) * rq[row], dQ[ib][mi][r], pDQ[mi][r]);
-            pDK[mi][r] = fmaf(to_f(k[(size_t)t * qk_pitch + d]) * rk[row], dK[ib][mi][r], pDK[mi][r]);
-          }
+          const int row = 16 * mi + 4 * j + r;
+          pDQ[mi][r] = fmaf(xq(row, d), dQ[ib][mi][r], pDQ[mi][r]);
+          pDK[mi][r] = fmaf(xk(row, d), dK[ib][mi][r], pDK[mi][r]);
         }
     }
   }
@@ -936,18 +1055,18 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
       const int vc = 16 * vb + (l & 15);
       Frag<MT> bdv[2];
 #pragma unroll
-      for (int p = 0; p < 2; ++p) bdv[p] = frag_rows<MT, float>(dVc, DV, 0, C, 32 * p, vc, One());
+      for (int p = 0; p < 2; ++p) bdv[p] = fdVnrows(32 * p, vc);
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) {
         f4 y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int p = 0; p < 2; ++p)
-          if (32 * p + 31 >= 16 * mi) mma(y, frag_k<MT, float>(Atc, C, 16 * mi, 32 * p), bdv[p]);
+          if (32 * p + 31 >= 16 * mi) mma(y, fAt(16 * mi, 32 * p), bdv[p]);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int row = 16 * mi + 4 * j + r, t = t0 + row;
           if (t < T) {
-            ((IT*)a.dv)[v_base + (size_t)t * v_pitch + vc] = from_f<IT>(cs.beta[row] * y[r]);
+            ((MT*)a.dv)[v_base + (size_t)t * v_pitch + vc] = from_f<MT>(cs.beta[row] * y[r]);
             pVY[mi][r] = fmaf(to_f(v[(size_t)t * v_pitch + vc]), y[r], pVY[mi][r]);
           }
         }
@@ -968,15 +1087,14 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
     const int r = l, t = t0 + r;
     auto sum4 = [&](int pi) { return ((part[pi][0][r] + part[pi][1][r]) + part[pi][2][r]) + part[pi][3][r]; };
     const float kx = sum4(P_KX), qd = sum4(P_QD), E = sum4(P_E), r1 = sum4(P_R1), r2 = sum4(P_R2), vy = sum4(P_VY);
-    const float gm = cs.gam[r], bt = cs.beta[r];
-    const float db = fmaf(gm, kx, vy) + r2;
-    float dG = qd + bt * gm * kx + (r1 - colR1[r]) + (bt * r2 - colR2b[r]);
+    const float gmr = cs.gam[r], bt = cs.beta[r];
+    const float db = fmaf(gmr, kx, vy) + r2;
+    float dG = qd + bt * gmr * kx + (r1 - colR1[r]) + (bt * r2 - colR2b[r]);
     if (r == C - 1) dG += cs.gam[C - 1] * (((partS[0] + partS[1]) + partS[2]) + partS[3]);
-    // dg_t = sum_{s >= t} dG_s + sum_{r < t} E_r
+    // dg_t = sum_{s >= t} dG_s + sum_{r < t} E_r; the exclusive prefix by a shift, not incl - E: E on the last valid
+    // row is O(1) while the earlier ones carry exp(G_last - G_r) and can be ~1e-9 of it
     const float rev = __shfl(dG, C - 1 - r, 64);
     const float suf = __shfl(wave_incl_scan(rev), C - 1 - r, 64);
-    // exclusive prefix by a shift, not incl - E: E on the last valid row is O(1) while the earlier ones carry
-    // exp(G_last - G_r) and can be ~1e-9 of it; the subtraction would cancel them away
     float Esh = __shfl_up(E, 1, 64);
     if (r == 0) Esh = 0.f;
     const float pre = wave_incl_scan(Esh);
@@ -1002,15 +1120,13 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
         if (a.l2norm) {
           const float dq_dot = ((part[P_DQ][0][row] + part[P_DQ][1][row]) + part[P_DQ][2][row]) + part[P_DQ][3][row];
           const float dk_dot = ((part[P_DK][0][row] + part[P_DK][1][row]) + part[P_DK][2][row]) + part[P_DK][3][row];
-          const float xq = to_f(q[(size_t)t * qk_pitch + d]) * rq[row];
-          const float xk = to_f(k[(size_t)t * qk_pitch + d]) * rk[row];
-          gq = qs * rq[row] * fmaf(-xq, dq_dot, gq);
-          gk = rk[row] * fmaf(-xk, dk_dot, gk);
+          gq = qs * rq[row] * fmaf(-xq(row, d), dq_dot, gq);
+          gk = rk[row] * fmaf(-xk(row, d), dk_dot, gk);
         } else {
           gq = qs * gq;
         }
-        ((IT*)a.dq)[qk_base + (size_t)t * qk_pitch + d] = from_f<IT>(gq);
-        ((IT*)a.dk)[qk_base + (size_t)t * qk_pitch + d] = from_f<IT>(gk);
+        ((MT*)a.dq)[qk_base + (size_t)t * qk_pitch + d] = from_f<MT>(gq);
+        ((MT*)a.dk)[qk_base + (size_t)t * qk_pitch + d] = from_f<MT>(gk);
       }
   }
 }
@@ -1165,7 +1281,7 @@ const char* macai_gdr_last_error(void) { return g_err; }
 int macai_gdr_abi_version(void) { return MACAI_GDR_ABI_VERSION; }
 
 int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, const float* beta, void* W, float* U,
-                   void* KeT, float* GL, void* Qg, void* M, void* Ke, void* QgT, void* WT, void* Mt, float* A, float* At,
+                   void* KeT, float* GL, void* Qg, void* M, void* Ke, void* QgT, void* WT, void* Mt, void* A, void* At,
                    int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm,
                    float q_scale, void* stream) {
   const char* what = "macai_gdr_prep";
@@ -1199,7 +1315,7 @@ int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, 
   }
 
 int macai_gdr_state_fwd(const void* W, const float* U, const void* KeT, const float* GL, const void* Qg, const void* M,
-                        const float* s0, void* o, float* sT, float* Sc, float* Vn, int64_t B, int64_t T, int64_t H,
+                        const float* s0, void* o, float* sT, float* Sc, void* Vn, int64_t B, int64_t T, int64_t H,
                         int64_t DK, int64_t DV, int32_t dtype, int32_t flags, int32_t split, void* stream) {
   const char* what = "macai_gdr_state_fwd";
   int rc = check_common(what, B, T, H, DK, DV, dtype);
@@ -1235,7 +1351,7 @@ int macai_gdr_state_fwd(const void* W, const float* U, const void* KeT, const fl
 }
 
 int macai_gdr_state_bwd(const void* Ke, const void* QgT, const void* WT, const void* Mt, const float* GL,
-                        const void* dO, const float* dsT, float* dSn, float* dVn, float* ds0, int64_t B, int64_t T,
+                        const void* dO, const float* dsT, void* dSn, void* dVn, float* ds0, int64_t B, int64_t T,
                         int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t split, void* stream) {
   const char* what = "macai_gdr_state_bwd";
   int rc = check_common(what, B, T, H, DK, DV, dtype);
@@ -1262,28 +1378,39 @@ int macai_gdr_state_bwd(const void* Ke, const void* QgT, const void* WT, const v
 }
 
 int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float* g, const float* beta, const void* dO,
-                        const float* A, const float* At, const float* Sc, const float* dSn, const float* Vn,
-                        const float* dVn, void* dq, void* dk, void* dv, float* dg, float* dbeta, int64_t B, int64_t T,
+                        const void* A, const void* At, const float* Sc, const void* dSn, const void* Vn,
+                        const void* dVn, void* dq, void* dk, void* dv, float* dg, float* dbeta, int64_t B, int64_t T,
                         int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale,
                         void* stream) {
   const char* what = "macai_gdr_chunk_bwd";
   int rc = check_common(what, B, T, H, DK, DV, dtype);
   if (rc) return rc;
+  if (DV != 32 && DV != 64 && DV != 96 && DV != 128)
+    return fail(MACAI_GDR_EUNSUP, "%s: the backward takes value head widths 32, 64, 96 or 128 (got %lld)", what,
+                (long long)DV);
   if (!q || !k || !v || !g || !beta || !dO || !A || !At || !Sc || !dSn || !Vn || !dVn || !dq || !dk || !dv || !dg ||
       !dbeta)
     return fail(MACAI_GDR_EINVAL, "%s: null pointer", what);
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(dO) || !aligned16(A) || !aligned16(At) ||
-      !aligned16(Sc) || !aligned16(dSn) || !aligned16(Vn) || !aligned16(dVn))
-    return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
+  const void* ps[] = {q, k, v, dO, A, At, Sc, dSn, Vn, dVn};
+  for (const void* p : ps)
+    if (!aligned16(p)) return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
   ChunkBwdArgs a{q, k, v, g, beta, dO, A, At, Sc, dSn, Vn, dVn, dq, dk, dv, dg, dbeta, (int)B, (int)T, (int)H,
                  (int)DV, (int)((T + C - 1) / C), use_l2norm, q_scale};
   dim3 grid(a.NT, (unsigned)H, (unsigned)B);
   hipStream_t st = (hipStream_t)stream;
+#define LAUNCH_CB(MT)                                                                                               \
+  DISPATCH_DK(DK, switch (DV) {                                                                                    \
+    case 32: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 32>), grid, dim3(256), 0, st, a); break;                \
+    case 64: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 64>), grid, dim3(256), 0, st, a); break;                \
+    case 96: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 96>), grid, dim3(256), 0, st, a); break;                \
+    default: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 128>), grid, dim3(256), 0, st, a); break;               \
+  })
   if (dtype == MACAI_GDR_F32) {
-    DISPATCH_DK(DK, hipLaunchKernelGGL((chunk_bwd_kernel<float, float, DKC>), grid, dim3(256), 0, st, a));
+    LAUNCH_CB(float);
   } else {
-    DISPATCH_DK(DK, hipLaunchKernelGGL((chunk_bwd_kernel<bf16, bf16, DKC>), grid, dim3(256), 0, st, a));
+    LAUNCH_CB(bf16);
   }
+#undef LAUNCH_CB
   return launched(what);
 }
 

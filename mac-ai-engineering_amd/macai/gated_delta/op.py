@@ -104,17 +104,17 @@ def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float):
     Ke = torch.empty_like(W)
     QgT, WT = torch.empty_like(KeT), torch.empty_like(KeT)
     Mt = torch.empty(B, H, NT, CHUNK, CHUNK, device=dev, dtype=dt)
-    A = torch.empty(B, H, NT, CHUNK, CHUNK, device=dev, dtype=f32)
+    A = torch.empty(B, H, NT, CHUNK, CHUNK, device=dev, dtype=dt)
     At = torch.empty_like(A)
     P = N.ptr
     N.call("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), P(KeT), P(GL), None, None, P(Ke), P(QgT),
            P(WT), P(Mt), P(A), P(At), B, T, H, DK, DV, code, int(l2norm), q_scale, stream)
     split = split_for(B * H, T, DV)
     Sc = torch.empty(B, H, NT, DK, DV, device=dev, dtype=f32)
-    Vn = torch.empty(B, H, NT, CHUNK, DV, device=dev, dtype=f32)
+    Vn = torch.empty(B, H, NT, CHUNK, DV, device=dev, dtype=dt)
     N.call("macai_gdr_state_fwd", P(W), P(U), P(KeT), P(GL), None, None, P(s0), None, None, P(Sc), P(Vn),
            B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, stream)
-    dSn = torch.empty_like(Sc)
+    dSn = torch.empty(B, H, NT, DK, DV, device=dev, dtype=dt)
     dVn = torch.empty_like(Vn)
     ds0 = torch.empty(B, H, DK, DV, device=dev, dtype=f32)
     N.call("macai_gdr_state_bwd", P(Ke), P(QgT), P(WT), P(Mt), P(GL), P(do), P(dsT), P(dSn), P(dVn), P(ds0),

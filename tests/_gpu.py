@@ -32,13 +32,13 @@ def passes(q, k, v, g, beta, s0, do, dsT, l2norm=False, q_scale=1.0, split=0):
     # backward-mode prep, recompute, reverse pass, per-chunk backward
     W2, U2, KeT2, GL2 = e(B, H, NT, C, DK, d=dt), e(B, H, NT, C, DV), e(B, H, NT, DK, C, d=dt), e(B, H, NT)
     r["Ke"], r["QgT"], r["WT"] = e(B, H, NT, C, DK, d=dt), e(B, H, NT, DK, C, d=dt), e(B, H, NT, DK, C, d=dt)
-    r["Mt"], r["A"], r["At"] = e(B, H, NT, C, C, d=dt), e(B, H, NT, C, C), e(B, H, NT, C, C)
+    r["Mt"], r["A"], r["At"] = e(B, H, NT, C, C, d=dt), e(B, H, NT, C, C, d=dt), e(B, H, NT, C, C, d=dt)
     N.call("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W2), P(U2), P(KeT2), P(GL2), None, None, P(r["Ke"]),
            P(r["QgT"]), P(r["WT"]), P(r["Mt"]), P(r["A"]), P(r["At"]), B, T, H, DK, DV, code, int(l2norm), q_scale, st)
-    r["Sc"], r["Vn"] = e(B, H, NT, DK, DV), e(B, H, NT, C, DV)
+    r["Sc"], r["Vn"] = e(B, H, NT, DK, DV), e(B, H, NT, C, DV, d=dt)
     N.call("macai_gdr_state_fwd", P(W2), P(U2), P(KeT2), P(GL2), None, None, P(s0), None, None, P(r["Sc"]),
            P(r["Vn"]), B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, st)
-    r["dSn"], r["dVn"], r["ds0"] = e(B, H, NT, DK, DV), e(B, H, NT, C, DV), e(B, H, DK, DV)
+    r["dSn"], r["dVn"], r["ds0"] = e(B, H, NT, DK, DV, d=dt), e(B, H, NT, C, DV, d=dt), e(B, H, DK, DV)
     N.call("macai_gdr_state_bwd", P(r["Ke"]), P(r["QgT"]), P(r["WT"]), P(r["Mt"]), P(GL2), P(do), P(dsT),
            P(r["dSn"]), P(r["dVn"]), P(r["ds0"]), B, T, H, DK, DV, code, split, st)
     r["dq"], r["dk"], r["dv"] = e(B, T, H, DK, d=dt), e(B, T, H, DK, d=dt), e(B, T, H, DV, d=dt)
