@@ -396,22 +396,55 @@ __global__ void __launch_bounds__(64 * NW) state_fwd_kernel(StateFwdArgs a) {
   const int col = v0 + (l & 15);
   const size_t o_base = ((size_t)b * T * H + h) * DV, o_pitch = (size_t)H * DV;
 
+  int offW[GW::per_wave(NW)], offKT[GKT::per_wave(NW)], offM[GM::per_wave(NW)];
+  GW::template plan<NW>(offW, w, DK);
+  GKT::template plan<NW>(offKT, w, C);
+  if (OUT) GM::template plan<NW>(offM, w, C);
   auto issue = [&](int c, int buf) {
     MT* st = lds + buf * SZ;
     const size_t bhc = (size_t)hr * NT + c;
-    GW::dma(st, (const MT*)a.W + bhc * C * DK, DK, w, NW);
-    GKT::dma(st + O_KT, (const MT*)a.KeT + bhc * DK * C, C, w, NW);
+    GW::template dma_planned<NW>(st, (const MT*)a.W + bhc * C * DK, offW, w);
+    GKT::template dma_planned<NW>(st + O_KT, (const MT*)a.KeT + bhc * DK * C, offKT, w);
     if (OUT) {
-      GW::dma(st + O_Q, (const MT*)a.Qg + bhc * C * DK, DK, w, NW);
-      GM::dma(st + O_M, (const MT*)a.M + bhc * C * C, C, w, NW);
+      GW::template dma_planned<NW>(st + O_Q, (const MT*)a.Qg + bhc * C * DK, offW, w);
+      GM::template dma_planned<NW>(st + O_M, (const MT*)a.M + bhc * C * C, offM, w);
     }
   };
   auto loadU = [&](int c, f4* U) {
-    const float* Uc = a.U + ((size_t)hr * NT + c) * C * DV;
+    const float* Uc = a.U + ((size_t)hr * NT + c) * C * DV + (size_t)(4 * j) * DV + col;
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) U[mi][r] = Uc[(16 * mi + 4 * j + r) * DV + col];
+      for (int r = 0; r < 4; ++r) U[mi][r] = Uc[(16 * mi + r) * DV];
+  };
+  // the results of a chunk are written during the next one, so the wait that ends a chunk waits only on its loads
+  f4 pO[4], pS[ND], pV[4];
+  int pend = -1;
+  auto flush = [&]() {
+    if (pend < 0) return;
+    const int pt0 = pend * C;
+    const size_t pbhc = (size_t)hr * NT + pend;
+    if (OUT) {
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = pt0 + 16 * mi + 4 * j + r;
+          if (t < T) ((MT*)a.o)[o_base + (size_t)t * o_pitch + col] = from_f<MT>(pO[mi][r]);
+        }
+    }
+    if (STORE) {
+      float* Scc = a.Sc + pbhc * DK * DV + (size_t)(4 * j) * DV + col;
+#pragma unroll
+      for (int di = 0; di < ND; ++di)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) Scc[(16 * di + r) * DV] = pS[di][r];
+      MT* Vnc = (MT*)a.Vn + pbhc * C * DV + (size_t)(4 * j) * DV + col;
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) Vnc[(16 * mi + r) * DV] = from_f<MT>(pV[mi][r]);
+    }
   };
 
   f4 S[ND];
@@ -427,7 +460,6 @@ __global__ void __launch_bounds__(64 * NW) state_fwd_kernel(StateFwdArgs a) {
     __syncthreads();
   }
   for (int c = 0; c < NT; ++c) {
-    const int t0 = c * C;
     const size_t bhc = (size_t)hr * NT + c;
     int buf = 0;
     f4 U[4];
@@ -442,7 +474,9 @@ __global__ void __launch_bounds__(64 * NW) state_fwd_kernel(StateFwdArgs a) {
         loadU(c + 1, Un);
         gln = a.GL[bhc + 1];
       }
+      flush();
     } else {
+      flush();
       issue(c, 0);
       loadU(c, U);
       gl = a.GL[bhc];
@@ -459,9 +493,12 @@ __global__ void __launch_bounds__(64 * NW) state_fwd_kernel(StateFwdArgs a) {
     f4 Vn[4];
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
+      Frag<MT> fw[ND / 2];
+#pragma unroll
+      for (int p = 0; p < ND / 2; ++p) fw[p] = frag_tile<MT, GW>(st, 16 * mi, 32 * p);
       f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int p = 0; p < ND / 2; ++p) mma(acc, frag_tile<MT, GW>(st, 16 * mi, 32 * p), Sf[p]);
+      for (int p = 0; p < ND / 2; ++p) mma(acc, fw[p], Sf[p]);
       Vn[mi] = U[mi] - acc;
     }
     Frag<MT> Vf[2];
@@ -471,45 +508,43 @@ __global__ void __launch_bounds__(64 * NW) state_fwd_kernel(StateFwdArgs a) {
     f4 Sn[ND];
 #pragma unroll
     for (int di = 0; di < ND; ++di) {
+      Frag<MT> fk[2];
+#pragma unroll
+      for (int p = 0; p < 2; ++p) fk[p] = frag_tile<MT, GKT>(st + O_KT, 16 * di, 32 * p);
       f4 acc = S[di] * gl;
 #pragma unroll
-      for (int p = 0; p < 2; ++p) mma(acc, frag_tile<MT, GKT>(st + O_KT, 16 * di, 32 * p), Vf[p]);
+      for (int p = 0; p < 2; ++p) mma(acc, fk[p], Vf[p]);
       Sn[di] = acc;
-    }
-    if (STORE) {
-      float* Scc = a.Sc + bhc * DK * DV;
-#pragma unroll
-      for (int di = 0; di < ND; ++di)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) Scc[(16 * di + 4 * j + r) * DV + col] = S[di][r];
-      MT* Vnc = (MT*)a.Vn + bhc * C * DV;
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) Vnc[(16 * mi + 4 * j + r) * DV + col] = from_f<MT>(Vn[mi][r]);
     }
     if (OUT) {
       // O = diag(gamma) Q S + M Vn (M lower triangular: k-blocks past the row block are zero)
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) {
+        Frag<MT> fq[ND / 2];
+#pragma unroll
+        for (int p = 0; p < ND / 2; ++p) fq[p] = frag_tile<MT, GW>(st + O_Q, 16 * mi, 32 * p);
         f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int p = 0; p < ND / 2; ++p) mma(acc, frag_tile<MT, GW>(st + O_Q, 16 * mi, 32 * p), Sf[p]);
+        for (int p = 0; p < ND / 2; ++p) mma(acc, fq[p], Sf[p]);
 #pragma unroll
         for (int p = 0; p < 2; ++p)
           if (32 * p <= 16 * mi + 15) mma(acc, frag_tile<MT, GM>(st + O_M, 16 * mi, 32 * p), Vf[p]);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int t = t0 + 16 * mi + 4 * j + r;
-          if (t < T) ((MT*)a.o)[o_base + (size_t)t * o_pitch + col] = from_f<MT>(acc[r]);
-        }
+        pO[mi] = acc;
       }
     }
+    if (STORE) {
+#pragma unroll
+      for (int di = 0; di < ND; ++di) pS[di] = S[di];
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) pV[mi] = Vn[mi];
+    }
+    pend = c;
 #pragma unroll
     for (int di = 0; di < ND; ++di) S[di] = Sn[di];
     if (NBUF == 2) wait_dma();
     __syncthreads();
   }
+  flush();
   if (a.sT) {
 #pragma unroll
     for (int di = 0; di < ND; ++di)
@@ -542,16 +577,39 @@ __global__ void __launch_bounds__(64 * NW) state_bwd_kernel(StateBwdArgs a) {
   const int col = vg + w * 16 + (l & 15);
   const size_t o_base = ((size_t)b * T * H + h) * DV, o_pitch = (size_t)H * DV;
 
+  int offK[GK::per_wave(NW)], offT[GT::per_wave(NW)], offM[GM::per_wave(NW)], offO[GO::per_wave(NW)];
+  GK::template plan<NW>(offK, w, DK);
+  GT::template plan<NW>(offT, w, C);
+  GM::template plan<NW>(offM, w, C);
+  GO::template plan<NW>(offO, w, (int)o_pitch);
   auto issue = [&](int c, int buf) {
     MT* st = lds + buf * SZ;
     const size_t bhc = (size_t)hr * NT + c;
     const int t0 = c * C;
-    GK::dma(st, (const MT*)a.Ke + bhc * C * DK, DK, w, NW);
-    GT::dma(st + O_Q, (const MT*)a.QgT + bhc * DK * C, C, w, NW);
-    GT::dma(st + O_W, (const MT*)a.WT + bhc * DK * C, C, w, NW);
-    GM::dma(st + O_M, (const MT*)a.Mt + bhc * C * C, C, w, NW);
-    GO::dma(st + O_O, (const MT*)a.dO + o_base + (size_t)t0 * o_pitch + vg, o_pitch, w, NW,
-            (T - t0 < C) ? T - t0 : C);
+    GK::template dma_planned<NW>(st, (const MT*)a.Ke + bhc * C * DK, offK, w);
+    GT::template dma_planned<NW>(st + O_Q, (const MT*)a.QgT + bhc * DK * C, offT, w);
+    GT::template dma_planned<NW>(st + O_W, (const MT*)a.WT + bhc * DK * C, offT, w);
+    GM::template dma_planned<NW>(st + O_M, (const MT*)a.Mt + bhc * C * C, offM, w);
+    const MT* og = (const MT*)a.dO + o_base + (size_t)t0 * o_pitch + vg;
+    if (t0 + C <= T) GO::template dma_planned<NW>(st + O_O, og, offO, w);
+    else GO::dma(st + O_O, og, o_pitch, w, NW, T - t0);   // the last, partial chunk: rows clamped in range
+  };
+  // results written during the next chunk (see state_fwd_kernel)
+  f4 pS[ND], pV[4];
+  int pend = -1;
+  auto flush = [&]() {
+    if (pend < 0) return;
+    const size_t pbhc = (size_t)hr * NT + pend;
+    MT* dSc = (MT*)a.dSn + pbhc * DK * DV + (size_t)(4 * j) * DV + col;
+#pragma unroll
+    for (int di = 0; di < ND; ++di)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dSc[(16 * di + r) * DV] = from_f<MT>(pS[di][r]);
+    MT* dVc = (MT*)a.dVn + pbhc * C * DV + (size_t)(4 * j) * DV + col;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dVc[(16 * mi + r) * DV] = from_f<MT>(pV[mi][r]);
   };
 
   f4 dS[ND];
@@ -576,7 +634,9 @@ __global__ void __launch_bounds__(64 * NW) state_bwd_kernel(StateBwdArgs a) {
         issue(c - 1, buf ^ 1);
         gln = a.GL[bhc - 1];
       }
+      flush();
     } else {
+      flush();
       issue(c, 0);
       gl = a.GL[bhc];
       wait_dma();
@@ -600,9 +660,12 @@ __global__ void __launch_bounds__(64 * NW) state_bwd_kernel(StateBwdArgs a) {
     f4 dV[4];
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
+      Frag<MT> fk[ND / 2];
+#pragma unroll
+      for (int p = 0; p < ND / 2; ++p) fk[p] = frag_tile<MT, GK>(st, 16 * mi, 32 * p);
       f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int p = 0; p < ND / 2; ++p) mma(acc, frag_tile<MT, GK>(st, 16 * mi, 32 * p), Sf[p]);
+      for (int p = 0; p < ND / 2; ++p) mma(acc, fk[p], Sf[p]);
 #pragma unroll
       for (int p = 0; p < 2; ++p)
         if (32 * p + 31 >= 16 * mi) mma(acc, frag_tile<MT, GM>(st + O_M, 16 * mi, 32 * p), Of[p]);
@@ -615,31 +678,31 @@ __global__ void __launch_bounds__(64 * NW) state_bwd_kernel(StateBwdArgs a) {
     f4 dSn[ND];
 #pragma unroll
     for (int di = 0; di < ND; ++di) {
+      Frag<MT> fw[2], fq[2];
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        fw[p] = frag_tile<MT, GT>(st + O_W, 16 * di, 32 * p);
+        fq[p] = frag_tile<MT, GT>(st + O_Q, 16 * di, 32 * p);
+      }
       f4 acc = dS[di] * gl;
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        mma(acc, frag_tile<MT, GT>(st + O_W, 16 * di, 32 * p), Vf[p]);
-        mma(acc, frag_tile<MT, GT>(st + O_Q, 16 * di, 32 * p), Of[p]);
+        mma(acc, fw[p], Vf[p]);
+        mma(acc, fq[p], Of[p]);
       }
       dSn[di] = acc;
     }
-    {
-      MT* dSc = (MT*)a.dSn + bhc * DK * DV;
 #pragma unroll
-      for (int di = 0; di < ND; ++di)
+    for (int di = 0; di < ND; ++di) pS[di] = dS[di];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dSc[(16 * di + 4 * j + r) * DV + col] = from_f<MT>(dS[di][r]);
-      MT* dVc = (MT*)a.dVn + bhc * C * DV;
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dVc[(16 * mi + 4 * j + r) * DV + col] = from_f<MT>(dV[mi][r]);
-    }
+    for (int mi = 0; mi < 4; ++mi) pV[mi] = dV[mi];
+    pend = c;
 #pragma unroll
     for (int di = 0; di < ND; ++di) dS[di] = dSn[di];
     if (NBUF == 2) wait_dma();
     __syncthreads();
   }
+  flush();
 #pragma unroll
   for (int di = 0; di < ND; ++di)
 #pragma unroll

@@ -23,6 +23,29 @@ struct Tile {
   static_assert(COLS % EPU == 0, "tile rows must be whole 16-byte units");
 
   __device__ static __forceinline__ int offset(int row, int col) { return row * PITCH + col; }
+  static constexpr int per_wave(int nw) { return (NI + nw - 1) / nw; }
+
+  // The element offsets (from the tile's global base, row pitch gpitch) that this lane copies in the wave's
+  // instructions w, w + NW, ...: the same for every chunk of a dense tile, so the sequential passes compute them once.
+  template <int NW>
+  __device__ static __forceinline__ void plan(int (&off)[per_wave(NW)], int w, int gpitch) {
+    const int l = lane_id();
+#pragma unroll
+    for (int k = 0; k < per_wave(NW); ++k) {
+      const int i = w + k * NW;
+      const int u = i * 64 + l, row = u / RU, cu = u - row * RU;
+      off[k] = (i < NI && row < R && cu < PU) ? row * gpitch + cu * EPU : 0;
+    }
+  }
+  template <int NW>
+  __device__ static __forceinline__ void dma_planned(T* base, const T* g, const int (&off)[per_wave(NW)], int w) {
+#pragma unroll
+    for (int k = 0; k < per_wave(NW); ++k) {
+      const int i = w + k * NW;
+      if (i < NI)
+        __builtin_amdgcn_global_load_lds((const void*)(g + off[k]), (lds_void*)(base + i * 64 * EPU), 16, 0, 0);
+    }
+  }
   // Copy a global tile (row r at g + r * gpitch; rows >= nrows re-read row nrows - 1, to be masked by the reader) into
   // LDS `base`; waves w, w + nw, ... share the wave instructions.
   __device__ static __forceinline__ void dma(T* base, const T* g, size_t gpitch, int w, int nw, int nrows = R) {
