@@ -81,9 +81,9 @@ def kernel_costs(B, T, H, DK, DV, es=2):
                             flops=n * (2 * 2 * cc * DK + cc * C / 3 + 2 * cc * DK + 2 * cc * DV))
     cost["state_fwd_store"] = dict(bytes=n * (2 * cdk * es + cdv * 4 + 4 + sdk + cdv * es),
                                    flops=n * (2 * 2 * C * DK * DV))
-    cost["state_bwd"] = dict(bytes=n * (3 * cdk * es + cc * es + 4 + DK * DV * es + cdv * es) + io_v,
+    cost["state_bwd"] = dict(bytes=n * (3 * cdk * es + cc * es + 4 + sdk + cdv * es) + io_v,
                              flops=n * (3 * 2 * C * DK * DV + 2 * cc * DV))
-    cost["chunk_bwd"] = dict(bytes=2 * io_k + 2 * io_v + gb + n * (2 * cc * es + sdk + DK * DV * es + 2 * cdv * es)
+    cost["chunk_bwd"] = dict(bytes=2 * io_k + 2 * io_v + gb + n * (2 * cc * es + 2 * sdk + 2 * cdv * es)
                              + 2 * io_k + io_v + gb,
                              flops=n * (3 * 2 * C * DK * DV + 2 * cc * DK + 3 * 2 * cc * DK + 2 * 2 * cc * DV
                                         + 2 * 2 * cc * C + 3 * 2 * cc * DK + 2 * cc * DV))
@@ -111,7 +111,7 @@ def time_kernels(inp, reps=20):
     A, At = e(B, H, NT, C, C), e(B, H, NT, C, C)
     o = torch.empty_like(v)
     Sc, Vn = e(B, H, NT, DK, DV, d=f32), e(B, H, NT, C, DV)
-    dSn, dVn, ds0 = e(B, H, NT, DK, DV), torch.empty_like(Vn), e(B, H, DK, DV, d=f32)
+    dSn, dVn, ds0 = e(B, H, NT, DK, DV, d=f32), torch.empty_like(Vn), e(B, H, DK, DV, d=f32)
     dq, dk, dv, dg, db = (torch.empty_like(x) for x in (q, k, v, g, beta))
     P = N.ptr
     calls = {
@@ -181,6 +181,8 @@ def main():
     ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="also run one plain device copy of this many MiB (calibrates rocprof byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the gated delta rule has no cross-GPU step in this build "
@@ -220,6 +222,11 @@ def main():
     ms = elapsed / args.steps * 1e3
 
     ktime, split = time_kernels(inp)
+    if args.copy_mib:
+        src = torch.ones(args.copy_mib << 18, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
     cost = kernel_costs(B, T, H, DK, DV)
     kernels = {}
     for name, t in ktime.items():

@@ -20,7 +20,7 @@
  *     A, At       [B, H, NT, 64, 64] dtype   A = (I + L)^-1 (solved in fp32); A^T
  *     GL          [B, H, NT]         float32 exp(G_last) of each chunk
  *     Sc          [B, H, NT, DK, DV] float32 state entering each chunk
- *     dSn         [B, H, NT, DK, DV] dtype   dLoss/dS_{c+1} (carried in fp32, stored as the MFMA operand it is read as)
+ *     dSn         [B, H, NT, DK, DV] float32 dLoss/dS_{c+1}
  *     Vn, dVn     [B, H, NT, 64, DV] dtype   per-token corrections U - W S_c and their gradient
  *   G_r = sum_{s<=r} g_s inside the chunk, gamma = exp(G), e = exp(G_last - G), q^ / k^ the prologue's outputs.
  * With use_l2norm = 1 the kernels apply the reference prologue (_norm.py:1-10) themselves: q^ = q * rsqrt(|q|^2 + 1e-6)
@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define MACAI_GDR_ABI_VERSION 2
+#define MACAI_GDR_ABI_VERSION 3
 
 /* dtype codes */
 #define MACAI_GDR_F32 0
@@ -83,7 +83,7 @@ int macai_gdr_state_fwd(const void* W, const float* U, const void* KeT, const fl
  * writes ds0 = dLoss/d initial_state.  Replaces `lib.gdc_bwd_state(q, k, beta, do, dsT, gc, a, m, dsn, dvn, ds0, T,
  * H, DV, ...)` (reference op.py:234; kernel _chunked.py:661-903). */
 int macai_gdr_state_bwd(const void* Ke, const void* QgT, const void* WT, const void* Mt, const float* GL,
-                        const void* dO, const float* dsT, void* dSn, void* dVn, float* ds0, int64_t B, int64_t T,
+                        const void* dO, const float* dsT, float* dSn, void* dVn, float* ds0, int64_t B, int64_t T,
                         int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t split, void* stream);
 
 /* The per-chunk backward (north star (4)): dq, dk (w.r.t. the raw inputs when use_l2norm), dv in dtype; dg, dbeta in
@@ -91,7 +91,7 @@ int macai_gdr_state_bwd(const void* Ke, const void* QgT, const void* WT, const v
  * sc, dsn, vn, xu, dvn, dq, dk, dv, dg, dbeta, T, H, DV, ...)` (reference op.py:241-242; kernel
  * _chunked.py:905-1177) and the prologue's backward l2n_bwd (_norm.py:113). */
 int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float* g, const float* beta, const void* dO,
-                        const void* A, const void* At, const float* Sc, const void* dSn, const void* Vn,
+                        const void* A, const void* At, const float* Sc, const float* dSn, const void* Vn,
                         const void* dVn, void* dq, void* dk, void* dv, float* dg, float* dbeta, int64_t B, int64_t T,
                         int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale,
                         void* stream);

@@ -132,11 +132,42 @@ __device__ __forceinline__ float wave_incl_scan(float x) {
   }
   return x;
 }
-// sum over the 16 lanes of a lane group (lanes with equal l / 16), result in every lane of the group
+// lane permutations inside each 16-lane DPP row (no LDS round trip): quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror
+// (lane i <-> 7 - i within each 8), row_mirror (i <-> 15 - i)
+enum : int { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140 };
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+// sum over the 16 lanes of a lane group (lanes with equal l / 16), result in every lane of the group.  A pairwise tree:
+// pairs, quads, halves, the row; every lane of the group ends with the same bits.
 __device__ __forceinline__ float group16_sum(float x) {
-#pragma unroll
-  for (int off = 1; off < 16; off <<= 1) x += __shfl_xor(x, off, 64);
+  x += dpp<DPP_XOR1>(x);
+  x += dpp<DPP_XOR2>(x);
+  x += dpp<DPP_HALF_MIRROR>(x);
+  x += dpp<DPP_MIRROR>(x);
   return x;
+}
+// Eight sums over the 16 lanes of a lane group at once, by a butterfly that halves the values at every exchange
+// (partners l ^ 15, l ^ 7, l ^ 2, l ^ 1 -- they span the group): lane l returns the group's sum of v[(l % 16) / 2];
+// lanes l and l ^ 1 hold the same bits.  30 VALU operations where eight group16_sum take 64.
+__device__ __forceinline__ float group16_sum8(const float (&v)[8]) {
+  const int i = lane_id() & 15;
+  const bool b3 = i & 8, b2 = i & 4, b1 = i & 2;
+  float u[4], w[2];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float keep = b3 ? v[4 + k] : v[k], send = b3 ? v[k] : v[4 + k];
+    u[k] = keep + dpp<DPP_MIRROR>(send);
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const float keep = b2 ? u[2 + k] : u[k], send = b2 ? u[k] : u[2 + k];
+    w[k] = keep + dpp<DPP_HALF_MIRROR>(send);
+  }
+  const float keep = b1 ? w[1] : w[0], send = b1 ? w[0] : w[1];
+  const float x = keep + dpp<DPP_XOR2>(send);
+  return x + dpp<DPP_XOR1>(x);
 }
 // sum over lanes with equal l % 16 (the 4 lane groups), result in every lane
 __device__ __forceinline__ float across_groups_sum(float x) {
@@ -191,11 +222,12 @@ __device__ __forceinline__ void chunk_scalars(ChunkScalars& cs, const float* g, 
 // ---- row norms ----------------------------------------------------------------------------------------------------
 // Inverse l2 norm of chunk rows: rinv = 1 / sqrt(sum x^2 + eps).  Every kernel computes it with this one routine: a row
 // is summed by the 16 lanes of a lane group, each over D/16 consecutive elements in order, then a fixed butterfly, so
-// all kernels produce the same bits.  A wave handles rows w*4 + (l/16), stepping by 4 * nwaves.
+// all kernels produce the same bits.  Wave w (of the nwaves taking part) handles rows w*4 + (l/16), stepping by
+// 4 * nwaves.
 template <typename IT, int D>
 __device__ __forceinline__ void row_rnorms(float* out, const IT* x, size_t row_base, size_t row_stride, int t0, int T,
-                                           int nwaves) {
-  const int l = lane_id(), w = wave_id();
+                                           int nwaves, int w = wave_id()) {
+  const int l = lane_id();
   constexpr int PER = D / 16;
   for (int r0 = w * 4; r0 < C; r0 += 4 * nwaves) {
     const int r = r0 + (l >> 4);

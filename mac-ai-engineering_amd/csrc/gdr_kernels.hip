@@ -75,7 +75,7 @@ struct StateBwdArgs {
   const float* GL;
   const void* dO;
   const float* dsT;
-  void* dSn;     // [B,H,NT,DK,DV] MT  dS_{c+1}
+  float* dSn;    // [B,H,NT,DK,DV] f32 dS_{c+1}
   void* dVn;     // [B,H,NT,C,DV]  MT
   float* ds0;    // [B,H,DK,DV]
   int B, T, H, DV, NT;
@@ -88,7 +88,8 @@ struct ChunkBwdArgs {
   const void* dO;
   const void *A, *At;                         // MT
   const float* Sc;                            // fp32
-  const void *dSn, *Vn, *dVn;                 // MT
+  const float* dSn;                           // fp32
+  const void *Vn, *dVn;                       // MT
   void *dq, *dk, *dv;
   float *dg, *dbeta;
   int B, T, H, DV, NT;
@@ -600,11 +601,11 @@ __global__ void __launch_bounds__(64 * NW) state_bwd_kernel(StateBwdArgs a) {
   auto flush = [&]() {
     if (pend < 0) return;
     const size_t pbhc = (size_t)hr * NT + pend;
-    MT* dSc = (MT*)a.dSn + pbhc * DK * DV + (size_t)(4 * j) * DV + col;
+    float* dSc = a.dSn + pbhc * DK * DV + (size_t)(4 * j) * DV + col;
 #pragma unroll
     for (int di = 0; di < ND; ++di)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) dSc[(16 * di + r) * DV] = from_f<MT>(pS[di][r]);
+      for (int r = 0; r < 4; ++r) dSc[(16 * di + r) * DV] = pS[di][r];
     MT* dVc = (MT*)a.dVn + pbhc * C * DV + (size_t)(4 * j) * DV + col;
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
@@ -764,7 +765,7 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
   const MT* v = (const MT*)a.v + v_base;
   const MT* dO = (const MT*)a.dO + v_base;
   const float* Scc = a.Sc + bhc * DK * DV;
-  const MT* dSc = (const MT*)a.dSn + bhc * DK * DV;
+  const float* dSc = a.dSn + bhc * DK * DV;
   const MT* Vnc = (const MT*)a.Vn + bhc * C * DV;
   const MT* dVc = (const MT*)a.dVn + bhc * C * DV;
   const MT* Ac = (const MT*)a.A + bhc * C * C;
@@ -864,7 +865,7 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
     for (int kb = 0; kb < DV / 32; ++kb) {
       const Frag<float> s32 = frag_k_f32(Scc, DV, d0, 32 * kb);
       const Frag<MT> bS = cvt<MT>(s32);
-      const Frag<MT> bD = frag_k<MT, MT>(dSc, DV, d0, 32 * kb);
+      const Frag<MT> bD = frag_k<MT, float>(dSc, DV, d0, 32 * kb);
 #pragma unroll
       for (int r = 0; r < 8; ++r) sds = fmaf(s32.v[r], bD.get(r), sds);
       Frag<MT> fo[4], fv[4], fd[4];
@@ -1195,6 +1196,453 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
+// the per-chunk backward for bf16 operands: 8 waves, every operand in LDS
+// ---------------------------------------------------------------------------------------------------------------------
+// One workgroup of 8 waves (two per SIMD) per (chunk, head, batch row).  The chunk's raw q, k, dO and Vn, dVn, A^T
+// are copied into padded LDS tiles at the start (asynchronous; rows past the sequence end are zeroed), and v replaces
+// dO once dO is consumed.  The [C x D] products are formed transposed, as [D x C] with the chunk's tokens as the MFMA
+// columns, so that in their epilogues a lane holds one token and 4 consecutive features: per-token scalars are lane
+// values and the feature quads are 8-byte LDS accesses.  Contractions over chunk rows read their operand with LDS
+// transpose reads.  The prologue's row scales (q^ = q rq DK^-1/2, k^ = k rk) are applied to products and folded into
+// the stored dM and Z, so the raw inputs are the MFMA operands.  Wave w owns key block w and value block w (16
+// features each) of the [D x C] products, and column block w % 4, row tiles 2 (w / 4) and 2 (w / 4) + 1 of the [C x C]
+// ones.  dq, dk and dv are staged in LDS and written as whole rows.
+template <int DK, int DV>
+__global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
+  using MT = bf16;
+  constexpr int NW = 8;
+  constexpr int NBD = DK / 16, NBV = DV / 16;   // feature blocks (<= NW)
+  constexpr int KP = DK + 8, CP = C + 8;
+  using GQ = Tile<MT, C, DK>;
+  using GV = Tile<MT, C, DV>;
+  using GA = Tile<MT, C, C>;
+  static_assert(GQ::PITCH == KP && GA::PITCH == CP && NBD <= NW && NBV <= NW, "chunk_bwd8 tiling");
+  constexpr int VP = GV::PITCH;
+  constexpr int O_K = GQ::ELEMS, O_O = 2 * GQ::ELEMS, O_VN = O_O + GV::ELEMS, O_DV = O_VN + GV::ELEMS,
+                O_AT = O_DV + GV::ELEMS, TILES = O_AT + GA::ELEMS;
+  __shared__ __attribute__((aligned(16))) MT tiles[TILES];   // q, k, dO (then v), Vn (then dv), dVn, A^T
+  __shared__ __attribute__((aligned(16))) MT sdW[C * KP];    // dW = -dVn S_c^T, [t][d]
+  __shared__ __attribute__((aligned(16))) MT sMkT[C * CP];   // [s][t] = dM[t][s] rk_s
+  __shared__ __attribute__((aligned(16))) MT sMqT[C * CP];   // [s][t] = dM[t][s] rq_t qs
+  __shared__ __attribute__((aligned(16))) MT sAZ[C * CP];    // dA^T: [s][t] = dA[t][s]; then [s][t] = Z[t][s] rk_t
+  __shared__ ChunkScalars cs;
+  __shared__ __attribute__((aligned(16))) float rk[C], rq[C];
+  __shared__ float part[NPART][NW][C];
+  __shared__ float colp[2][2][C];
+  __shared__ float partS[NW];
+
+  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int T = a.T, H = a.H, NT = a.NT;
+  const int t0 = c * C, nrows = (T - t0 < C) ? T - t0 : C;
+  const int l = lane_id(), w = wave_id(), j = l >> 4, n = l & 15;
+  const size_t qk_base = ((size_t)b * T * H + h) * DK, qk_pitch = (size_t)H * DK;
+  const size_t v_base = ((size_t)b * T * H + h) * DV, v_pitch = (size_t)H * DV;
+  const size_t s_base = (size_t)b * T * H + h;
+  const size_t bhc = ((size_t)b * H + h) * NT + c;
+  const MT* q = (const MT*)a.q + qk_base;
+  const MT* k = (const MT*)a.k + qk_base;
+  const MT* v = (const MT*)a.v + v_base;
+  const MT* dO = (const MT*)a.dO + v_base;
+  const float* Scc = a.Sc + bhc * DK * DV;
+  const float* dSc = a.dSn + bhc * DK * DV;
+  const MT* Vnc = (const MT*)a.Vn + bhc * C * DV;
+  const MT* dVc = (const MT*)a.dVn + bhc * C * DV;
+  const MT* Atc = (const MT*)a.At + bhc * C * C;
+  const float qs = a.q_scale;
+  MT* const tq = tiles;
+  MT* const tk = tiles + O_K;
+  MT* const tO = tiles + O_O;
+  MT* const tVn = tiles + O_VN;
+  MT* const tdV = tiles + O_DV;
+  MT* const tAt = tiles + O_AT;
+  const int cb = w & 3, hh = w >> 2;       // [C x C] column block and row half
+
+  // ---- 0: global operands into registers first (their latency overlaps the tile copies), then the tiles
+  Frag<float> s32[DV / 32];               // S_c rows of key block w (A operand, k = value features)
+  Frag<float> sD[DV / 32];                // dS_{c+1} rows of key block w
+  if (w < NBD) {
+#pragma unroll
+    for (int kb = 0; kb < DV / 32; ++kb) {
+      s32[kb] = frag_k_f32(Scc, DV, 16 * w, 32 * kb);
+      sD[kb] = frag_k_f32(dSc, DV, 16 * w, 32 * kb);
+    }
+  }
+  Frag<MT> vf[DV / 32];                   // v rows of column block cb (B operand of dVn V^T)
+#pragma unroll
+  for (int kb = 0; kb < DV / 32; ++kb) vf[kb] = frag_k_seq<MT, MT>(v, v_pitch, t0, T, 16 * cb, 32 * kb, One());
+  GQ::dma(tq, q + (size_t)t0 * qk_pitch, qk_pitch, w, NW, nrows);
+  GQ::dma(tk, k + (size_t)t0 * qk_pitch, qk_pitch, w, NW, nrows);
+  GV::dma(tO, dO + (size_t)t0 * v_pitch, v_pitch, w, NW, nrows);
+  GV::dma(tVn, Vnc, DV, w, NW);
+  GV::dma(tdV, dVc, DV, w, NW);
+  GA::dma(tAt, Atc, C, w, NW);
+  if (w == 0) chunk_scalars(cs, a.g, a.beta, s_base, H, t0, T);
+  if (a.l2norm) {
+    if (w >= 4 && w < 6) row_rnorms<MT, DK>(rk, (const MT*)a.k, qk_base, qk_pitch, t0, T, 2, w - 4);
+    if (w >= 6) row_rnorms<MT, DK>(rq, (const MT*)a.q, qk_base, qk_pitch, t0, T, 2, w - 6);
+  } else if (threadIdx.x < C) {
+    rk[threadIdx.x] = (int)threadIdx.x < nrows ? 1.f : 0.f;
+    rq[threadIdx.x] = (int)threadIdx.x < nrows ? 1.f : 0.f;
+  }
+  wait_dma();
+  __syncthreads();
+  if (nrows < C) {                         // rows past the end: zeros in q, k and dO
+    constexpr int UQ = KP / 8, UV = VP / 8;
+    const int nz = C - nrows;
+    for (int i = threadIdx.x; i < nz * (2 * UQ + UV); i += blockDim.x) {
+      const int row = nrows + i % nz, u = i / nz;
+      MT* p = u < UQ ? tq + row * KP + 8 * u : u < 2 * UQ ? tk + row * KP + 8 * (u - UQ) : tO + row * VP + 8 * (u - 2 * UQ);
+      *reinterpret_cast<bf16x8*>(p) = bf16x8{};
+    }
+    __syncthreads();
+  }
+
+  // ---- B: products with the chunk states, transposed: [key block w] x [token tiles]
+  //   dQ^T = gamma * (S_c dO^T),  dK^T = e * (dS Vn^T),  dW^T = -(S_c dVn^T),  X^T = dW^T A,  dK^T += beta gamma X^T
+  f4 dQt[4], dKt[4];
+  float sds = 0.f;
+  if (w < NBD) {
+    const int d0 = 16 * w + 4 * j;        // this lane's 4 key features
+    f4 aO[4], aV[4], aD[4];
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) aO[ti] = aV[ti] = aD[ti] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < DV / 32; ++kb) {
+      const Frag<MT> fS = cvt<MT>(s32[kb]);
+      Frag<MT> dHi, dLo;                  // dS as hi + lo: the e k . (Vn dS^T) terms of dg sum 64 rows of it
+      frag_split<MT>(sD[kb], dHi, dLo);
+#pragma unroll
+      for (int r = 0; r < 8; ++r) sds = fmaf(s32[kb].v[r], sD[kb].v[r], sds);
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) {
+        const Frag<MT> fv = frag_tile<MT, GV>(tVn, 16 * ti, 32 * kb);
+        mma(aO[ti], fS, frag_tile<MT, GV>(tO, 16 * ti, 32 * kb));
+        mma(aV[ti], dHi, fv);
+        mma(aV[ti], dLo, fv);
+        mma(aD[ti], fS, frag_tile<MT, GV>(tdV, 16 * ti, 32 * kb));
+      }
+    }
+    float pQD[4], pE[4];
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) {
+      const int t = 16 * ti + n;
+      const f4 q4 = load4(tq + t * KP + d0), k4 = load4(tk + t * KP + d0);
+      dQt[ti] = aO[ti] * cs.gam[t];
+      dKt[ti] = aV[ti] * cs.e[t];
+      pQD[ti] = (rq[t] * qs) * (((q4[0] * dQt[ti][0] + q4[1] * dQt[ti][1]) + q4[2] * dQt[ti][2]) + q4[3] * dQt[ti][3]);
+      pE[ti] = rk[t] * (((k4[0] * dKt[ti][0] + k4[1] * dKt[ti][1]) + k4[2] * dKt[ti][2]) + k4[3] * dKt[ti][3]);
+      *reinterpret_cast<bf16x4*>(sdW + t * KP + d0) =
+          bf16x4{(bf16)(-aD[ti][0]), (bf16)(-aD[ti][1]), (bf16)(-aD[ti][2]), (bf16)(-aD[ti][3])};
+    }
+    // X^T = dW^T A (this wave's own dW^T columns, just written): A is lower triangular
+    Frag<MT> fW[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) fW[p] = frag_tr(sdW, KP, 32 * p, 16 * w);
+    float pKX[4];
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) {
+      f4 x = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+        if (32 * p + 31 >= 16 * ti) mma(x, fW[p], frag_tile<MT, GA>(tAt, 16 * ti, 32 * p));
+      const int t = 16 * ti + n;
+      const f4 k4 = load4(tk + t * KP + d0);
+      dKt[ti] += (cs.beta[t] * cs.gam[t]) * x;
+      pKX[ti] = rk[t] * (((k4[0] * x[0] + k4[1] * x[1]) + k4[2] * x[2]) + k4[3] * x[3]);
+    }
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) {
+      const float s1 = across_groups_sum(pQD[ti]), s2 = across_groups_sum(pE[ti]), s3 = across_groups_sum(pKX[ti]);
+      if (j == 0) {
+        part[P_QD][w][16 * ti + n] = s1;
+        part[P_E][w][16 * ti + n] = s2;
+        part[P_KX][w][16 * ti + n] = s3;
+      }
+    }
+    sds = across_groups_sum(group16_sum(sds));
+    if (l == 0) partS[w] = sds;
+  }
+  __syncthreads();
+
+  // ---- C: the C x C products on this wave's row tiles mi = 2 hh, 2 hh + 1 of column block cb (lower tiles only)
+  float KG[2][4], gmv[2][4];
+  {
+    f4 QK[2], KK[2], Ta[2], dOV[2], Tb[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) QK[i] = KK[i] = Ta[i] = dOV[i] = Tb[i] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < DK / 32; ++p) {
+      const Frag<MT> bk = frag_tile<MT, GQ>(tk, 16 * cb, 32 * p);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int mi = 2 * hh + i;
+        if (mi < cb) continue;
+        mma(QK[i], frag_tile<MT, GQ>(tq, 16 * mi, 32 * p), bk);
+        mma(KK[i], frag_tile<MT, GQ>(tk, 16 * mi, 32 * p), bk);
+        mma(Ta[i], frag_k_raw(sdW, KP, 16 * mi, 32 * p), bk);
+      }
+    }
+#pragma unroll
+    for (int kb = 0; kb < DV / 32; ++kb) {
+      const Frag<MT> bvn = frag_tile<MT, GV>(tVn, 16 * cb, 32 * kb);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int mi = 2 * hh + i;
+        if (mi < cb) continue;
+        mma(dOV[i], frag_tile<MT, GV>(tO, 16 * mi, 32 * kb), bvn);
+        mma(Tb[i], frag_tile<MT, GV>(tdV, 16 * mi, 32 * kb), vf[kb]);
+      }
+    }
+    const int s = 16 * cb + n;
+    const float bs = cs.beta[s], bgs = bs * cs.gam[s], rks = rk[s];
+    const double Gs = cs.G[s];
+    float pR1[8], cR1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r0 = 16 * (2 * hh + i) + 4 * j;   // this lane's 4 rows
+      const f4 rq4 = *reinterpret_cast<const f4*>(rq + r0), rk4 = *reinterpret_cast<const f4*>(rk + r0);
+      float mk[4], mq[4], da[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = r0 + r;
+        const float gm = (row >= s) ? expf((float)(cs.G[row] - Gs)) : 0.f;
+        gmv[i][r] = gm;
+        const float Mv = QK[i][r] * (rq4[r] * qs * rks) * gm;
+        const float dMv = dOV[i][r] * gm;
+        mk[r] = dMv * rks;
+        mq[r] = dMv * (rq4[r] * qs);
+        const float r1 = (row > s) ? dOV[i][r] * Mv : 0.f;
+        pR1[4 * i + r] = r1;
+        cR1 += r1;
+        da[r] = (row > s) ? fmaf(Ta[i][r] * rks, bgs, Tb[i][r] * bs) : 0.f;
+        KG[i][r] = (row > s) ? KK[i][r] * (rk4[r] * rks) * gm : 0.f;
+      }
+      *reinterpret_cast<bf16x4*>(sMkT + s * CP + r0) = bf16x4{(bf16)mk[0], (bf16)mk[1], (bf16)mk[2], (bf16)mk[3]};
+      *reinterpret_cast<bf16x4*>(sMqT + s * CP + r0) = bf16x4{(bf16)mq[0], (bf16)mq[1], (bf16)mq[2], (bf16)mq[3]};
+      *reinterpret_cast<bf16x4*>(sAZ + s * CP + r0) = bf16x4{(bf16)da[0], (bf16)da[1], (bf16)da[2], (bf16)da[3]};
+    }
+    const float rs = group16_sum8(pR1);            // row (l % 16) / 2 of the 8: tile i = idx / 4, r = idx % 4
+    if ((n & 1) == 0) {
+      const int idx = n >> 1;
+      part[P_R1][cb][16 * (2 * hh + (idx >> 2)) + 4 * j + (idx & 3)] = rs;
+    }
+    cR1 = across_groups_sum(cR1);
+    if (j == 0) colp[0][hh][s] = cR1;
+  }
+  __syncthreads();
+  // dO is consumed: v takes its tile (needed from E on)
+  GV::dma(tO, v + (size_t)t0 * v_pitch, v_pitch, w, NW, nrows);
+
+  // ---- T1 = dA A^T (column block cb, all four row tiles), then dL = strictLower(-A^T T1) on this wave's tiles
+  {
+    f4 T1[4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) T1[mi] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      if (32 * p > 16 * cb + 15) continue;
+      const Frag<MT> bA = frag_tr(tAt, CP, 32 * p, 16 * cb);        // B[s][t'] = A[t'][s]
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+        if (32 * p <= 16 * mi + 15) mma(T1[mi], frag_tr(sAZ, CP, 32 * p, 16 * mi), bA);
+    }
+    __syncthreads();                       // every wave has read dA^T: Z may overwrite it
+    Frag<MT> T1f[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) T1f[p] = frag_acc<MT>(T1[2 * p], T1[2 * p + 1]);
+    const int s = 16 * cb + n;
+    const float rks = rk[s];
+    float pR2[8], cR2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int mi = 2 * hh + i, r0 = 16 * mi + 4 * j;
+      f4 dL = {0.f, 0.f, 0.f, 0.f};
+      if (mi >= cb) {
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+          if (32 * p + 31 >= 16 * mi) mma(dL, frag_tile<MT, GA>(tAt, 16 * mi, 32 * p), T1f[p]);
+      }
+      const f4 rk4 = *reinterpret_cast<const f4*>(rk + r0), b4 = *reinterpret_cast<const f4*>(cs.beta + r0);
+      float zt[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = r0 + r;
+        const float dl = (row > s) ? -dL[r] : 0.f;
+        const float r2 = dl * KG[i][r];
+        pR2[4 * i + r] = r2;
+        cR2 = fmaf(b4[r], r2, cR2);
+        const float z = b4[r] * dl * gmv[i][r];     // Z[row][s] = Z[s][row] = beta_row P[row][s]
+        zt[r] = z * rk4[r];
+        if (mi == cb) {                              // diagonal tile: element by element
+          if (row > s) {
+            sAZ[s * CP + row] = (bf16)zt[r];
+            sAZ[row * CP + s] = (bf16)(z * rks);
+          } else if (row == s) {
+            sAZ[s * CP + row] = (bf16)0.f;
+          }
+        } else if (mi > cb) {
+          sAZ[row * CP + s] = (bf16)(z * rks);
+        }
+      }
+      if (mi > cb)
+        *reinterpret_cast<bf16x4*>(sAZ + s * CP + r0) = bf16x4{(bf16)zt[0], (bf16)zt[1], (bf16)zt[2], (bf16)zt[3]};
+    }
+    const float rs = group16_sum8(pR2);
+    if ((n & 1) == 0) {
+      const int idx = n >> 1;
+      part[P_R2][cb][16 * (2 * hh + (idx >> 2)) + 4 * j + (idx & 3)] = rs;
+    }
+    cR2 = across_groups_sum(cR2);
+    if (j == 0) colp[1][hh][s] = cR2;
+  }
+  __syncthreads();
+
+  // ---- D: dQ^T += k^T (dM diag(rk))^T;  dK^T += q^T (diag(rq qs) dM) + k^T (diag(rk) Z)   (key block w)
+  if (w < NBD) {
+    Frag<MT> kT[2], qT[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      kT[p] = frag_tr(tk, KP, 32 * p, 16 * w);
+      qT[p] = frag_tr(tq, KP, 32 * p, 16 * w);
+    }
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) {
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        if (32 * p <= 16 * ti + 15) mma(dQt[ti], kT[p], frag_tr(sMkT, CP, 32 * p, 16 * ti));
+        if (32 * p + 31 >= 16 * ti) mma(dKt[ti], qT[p], frag_k_raw(sMqT, CP, 16 * ti, 32 * p));
+        mma(dKt[ti], kT[p], frag_k_raw(sAZ, CP, 16 * ti, 32 * p));
+      }
+    }
+    if (a.l2norm) {
+      const int d0 = 16 * w + 4 * j;
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) {
+        const int t = 16 * ti + n;
+        const f4 q4 = load4(tq + t * KP + d0), k4 = load4(tk + t * KP + d0);
+        const float s1 = across_groups_sum(
+            rq[t] * (((q4[0] * dQt[ti][0] + q4[1] * dQt[ti][1]) + q4[2] * dQt[ti][2]) + q4[3] * dQt[ti][3]));
+        const float s2 = across_groups_sum(
+            rk[t] * (((k4[0] * dKt[ti][0] + k4[1] * dKt[ti][1]) + k4[2] * dKt[ti][2]) + k4[3] * dKt[ti][3]));
+        if (j == 0) {
+          part[P_DQ][w][t] = s1;
+          part[P_DK][w][t] = s2;
+        }
+      }
+    }
+  }
+  wait_dma();                              // v
+  __syncthreads();
+
+  // ---- E: Y^T = dVn^T A (value block w), dv = beta Y staged in Vn's tile, v . Y row sums
+  if (w < NBV) {
+    const int c0 = 16 * w + 4 * j;        // this lane's 4 value features
+    Frag<MT> fdv[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) fdv[p] = frag_tr(tdV, VP, 32 * p, 16 * w);
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) {
+      f4 y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+        if (32 * p + 31 >= 16 * ti) mma(y, fdv[p], frag_tile<MT, GA>(tAt, 16 * ti, 32 * p));
+      const int t = 16 * ti + n;
+      const float bt = cs.beta[t];
+      *reinterpret_cast<bf16x4*>(tVn + t * VP + c0) = bf16x4{(bf16)(bt * y[0]), (bf16)(bt * y[1]), (bf16)(bt * y[2]),
+                                                            (bf16)(bt * y[3])};
+      const f4 v4 = load4(tO + t * VP + c0);
+      const float s1 = across_groups_sum(((v4[0] * y[0] + v4[1] * y[1]) + v4[2] * y[2]) + v4[3] * y[3]);
+      if (j == 0) part[P_VY][w][t] = s1;
+    }
+  }
+  __syncthreads();
+
+  // ---- F: dbeta and dg (wave 0, lane = chunk row), fixed-order sums of the partials
+  if (w == 0) {
+    const int r = l, t = t0 + r;
+    auto sum = [&](int pi, int np) {
+      float x = part[pi][0][r];
+      for (int i = 1; i < np; ++i) x += part[pi][i][r];
+      return x;
+    };
+    const float kx = sum(P_KX, NBD), qd = sum(P_QD, NBD), E = sum(P_E, NBD), r1 = sum(P_R1, 4), r2 = sum(P_R2, 4),
+                vy = sum(P_VY, NBV);
+    const float gmr = cs.gam[r], bt = cs.beta[r];
+    const float db = fmaf(gmr, kx, vy) + r2;
+    float dG = qd + bt * gmr * kx + (r1 - (colp[0][0][r] + colp[0][1][r])) + (bt * r2 - (colp[1][0][r] + colp[1][1][r]));
+    if (r == C - 1) {
+      float ss = partS[0];
+      for (int i = 1; i < NBD; ++i) ss += partS[i];
+      dG += cs.gam[C - 1] * ss;
+    }
+    // dg_t = sum_{s >= t} dG_s + sum_{r < t} E_r; the exclusive prefix by a shift, not incl - E: E on the last valid
+    // row is O(1) while the earlier ones carry exp(G_last - G_r) and can be ~1e-9 of it
+    const float rev = __shfl(dG, C - 1 - r, 64);
+    const float suf = __shfl(wave_incl_scan(rev), C - 1 - r, 64);
+    float Esh = __shfl_up(E, 1, 64);
+    if (r == 0) Esh = 0.f;
+    const float pre = wave_incl_scan(Esh);
+    if (t < T) {
+      a.dg[s_base + (size_t)t * H] = suf + pre;
+      a.dbeta[s_base + (size_t)t * H] = db;
+    }
+  }
+
+  // ---- G: the prologue's backward; dq and dk staged over q's and k's tiles
+  f4 gq[4], gk[4];
+  if (w < NBD) {
+    const int d0 = 16 * w + 4 * j;
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) {
+      const int t = 16 * ti + n;
+      if (a.l2norm) {
+        float dq_dot = part[P_DQ][0][t], dk_dot = part[P_DK][0][t];
+        for (int i = 1; i < NBD; ++i) {
+          dq_dot += part[P_DQ][i][t];
+          dk_dot += part[P_DK][i][t];
+        }
+        const float rqt = rq[t], rkt = rk[t];
+        const f4 xq = load4(tq + t * KP + d0) * rqt, xk = load4(tk + t * KP + d0) * rkt;
+        gq[ti] = (qs * rqt) * (dQt[ti] - xq * dq_dot);
+        gk[ti] = rkt * (dKt[ti] - xk * dk_dot);
+      } else {
+        gq[ti] = qs * dQt[ti];
+        gk[ti] = dKt[ti];
+      }
+    }
+  }
+  __syncthreads();                         // q and k tiles are read: they become the dq and dk staging
+  if (w < NBD) {
+    const int d0 = 16 * w + 4 * j;
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) {
+      const int t = 16 * ti + n;
+      *reinterpret_cast<bf16x4*>(tq + t * KP + d0) =
+          bf16x4{(bf16)gq[ti][0], (bf16)gq[ti][1], (bf16)gq[ti][2], (bf16)gq[ti][3]};
+      *reinterpret_cast<bf16x4*>(tk + t * KP + d0) =
+          bf16x4{(bf16)gk[ti][0], (bf16)gk[ti][1], (bf16)gk[ti][2], (bf16)gk[ti][3]};
+    }
+  }
+  __syncthreads();
+  // whole rows out: 16 bytes per lane
+  {
+    constexpr int UK = DK / 8, UV = DV / 8;
+    MT* dq = (MT*)a.dq + qk_base + (size_t)t0 * qk_pitch;
+    MT* dk = (MT*)a.dk + qk_base + (size_t)t0 * qk_pitch;
+    MT* dv = (MT*)a.dv + v_base + (size_t)t0 * v_pitch;
+    for (int i = threadIdx.x; i < nrows * UK; i += blockDim.x) {
+      const int row = i / UK, u = i - row * UK;
+      *reinterpret_cast<bf16x8*>(dq + row * qk_pitch + 8 * u) = *reinterpret_cast<const bf16x8*>(tq + row * KP + 8 * u);
+      *reinterpret_cast<bf16x8*>(dk + row * qk_pitch + 8 * u) = *reinterpret_cast<const bf16x8*>(tk + row * KP + 8 * u);
+    }
+    for (int i = threadIdx.x; i < nrows * UV; i += blockDim.x) {
+      const int row = i / UV, u = i - row * UV;
+      *reinterpret_cast<bf16x8*>(dv + row * v_pitch + 8 * u) = *reinterpret_cast<const bf16x8*>(tVn + row * VP + 8 * u);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
 // decode: one token per head-row
 // ---------------------------------------------------------------------------------------------------------------------
 template <typename IT, int DK, int DV>
@@ -1414,7 +1862,7 @@ int macai_gdr_state_fwd(const void* W, const float* U, const void* KeT, const fl
 }
 
 int macai_gdr_state_bwd(const void* Ke, const void* QgT, const void* WT, const void* Mt, const float* GL,
-                        const void* dO, const float* dsT, void* dSn, void* dVn, float* ds0, int64_t B, int64_t T,
+                        const void* dO, const float* dsT, float* dSn, void* dVn, float* ds0, int64_t B, int64_t T,
                         int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t split, void* stream) {
   const char* what = "macai_gdr_state_bwd";
   int rc = check_common(what, B, T, H, DK, DV, dtype);
@@ -1441,7 +1889,7 @@ int macai_gdr_state_bwd(const void* Ke, const void* QgT, const void* WT, const v
 }
 
 int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float* g, const float* beta, const void* dO,
-                        const void* A, const void* At, const float* Sc, const void* dSn, const void* Vn,
+                        const void* A, const void* At, const float* Sc, const float* dSn, const void* Vn,
                         const void* dVn, void* dq, void* dk, void* dv, float* dg, float* dbeta, int64_t B, int64_t T,
                         int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale,
                         void* stream) {
@@ -1471,7 +1919,12 @@ int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float
   if (dtype == MACAI_GDR_F32) {
     LAUNCH_CB(float);
   } else {
-    LAUNCH_CB(bf16);
+    DISPATCH_DK(DK, switch (DV) {
+      case 32: hipLaunchKernelGGL((chunk_bwd8_kernel<DKC, 32>), grid, dim3(512), 0, st, a); break;
+      case 64: hipLaunchKernelGGL((chunk_bwd8_kernel<DKC, 64>), grid, dim3(512), 0, st, a); break;
+      case 96: hipLaunchKernelGGL((chunk_bwd8_kernel<DKC, 96>), grid, dim3(512), 0, st, a); break;
+      default: hipLaunchKernelGGL((chunk_bwd8_kernel<DKC, 128>), grid, dim3(512), 0, st, a); break;
+    })
   }
 #undef LAUNCH_CB
   return launched(what);

@@ -93,4 +93,31 @@ __device__ __forceinline__ Frag<MT> frag_tile_rows(const MT* base, int krow0, in
 
 __device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0); }
 
+// ---- gfx950 LDS transpose reads (ds_read_b64_tr_b16) ---------------------------------------------------------------
+// In each 16-lane group, lane s supplies the address of 4 consecutive 16-bit elements; lane i receives element i % 4 of
+// the 4 elements supplied by lanes 4e + i / 4, e = 0..3 (its result element e).  So if lane s points at
+// X[r0 + s / 4][c0 + 4 (s % 4)] of a row-major matrix, lane i receives X[r0 + e][c0 + i], e = 0..3: four consecutive
+// rows of column c0 + i.  Addresses must be 8-byte aligned.
+typedef __attribute__((address_space(3))) bf16x4* lds_bf16x4;
+__device__ __forceinline__ bf16x4 read_tr(const bf16* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4)(p));
+}
+// Fragment whose k runs over the ROWS of a row-major bf16 matrix X[k][n] (B operand with k = row, or A operand of X^T):
+// lane l (j = l / 16) takes column n0 + l % 16 and rows k0 + kmap(j, 0..7).  Two transpose reads.
+__device__ __forceinline__ Frag<bf16> frag_tr(const bf16* X, int pitch, int k0, int n0) {
+  const int l = lane_id(), j = l >> 4, s = l & 15;
+  const bf16* p = X + (k0 + 4 * j + (s >> 2)) * pitch + n0 + 4 * (s & 3);
+  const bf16x4 lo = read_tr(p), hi = read_tr(p + 16 * pitch);
+  Frag<bf16> f;
+  f.v = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return f;
+}
+// The accumulator layout of a 16 x 16 block of a row-major bf16 matrix X: lane l gets X[r0 + 4j + e][c0 + l % 16],
+// e = 0..3, as floats.  One transpose read.
+__device__ __forceinline__ f4 acc_tr(const bf16* X, int pitch, int r0, int c0) {
+  const int l = lane_id(), j = l >> 4, s = l & 15;
+  const bf16x4 x = read_tr(X + (r0 + 4 * j + (s >> 2)) * pitch + c0 + 4 * (s & 3));
+  return f4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
+}
+
 }  // namespace gdr

@@ -114,7 +114,7 @@ def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float):
     Vn = torch.empty(B, H, NT, CHUNK, DV, device=dev, dtype=dt)
     N.call("macai_gdr_state_fwd", P(W), P(U), P(KeT), P(GL), None, None, P(s0), None, None, P(Sc), P(Vn),
            B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, stream)
-    dSn = torch.empty(B, H, NT, DK, DV, device=dev, dtype=dt)
+    dSn = torch.empty(B, H, NT, DK, DV, device=dev, dtype=f32)
     dVn = torch.empty_like(Vn)
     ds0 = torch.empty(B, H, DK, DV, device=dev, dtype=f32)
     N.call("macai_gdr_state_bwd", P(Ke), P(QgT), P(WT), P(Mt), P(GL), P(do), P(dsT), P(dSn), P(dVn), P(ds0),

@@ -38,7 +38,7 @@ def passes(q, k, v, g, beta, s0, do, dsT, l2norm=False, q_scale=1.0, split=0):
     r["Sc"], r["Vn"] = e(B, H, NT, DK, DV), e(B, H, NT, C, DV, d=dt)
     N.call("macai_gdr_state_fwd", P(W2), P(U2), P(KeT2), P(GL2), None, None, P(s0), None, None, P(r["Sc"]),
            P(r["Vn"]), B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, st)
-    r["dSn"], r["dVn"], r["ds0"] = e(B, H, NT, DK, DV, d=dt), e(B, H, NT, C, DV, d=dt), e(B, H, DK, DV)
+    r["dSn"], r["dVn"], r["ds0"] = e(B, H, NT, DK, DV), e(B, H, NT, C, DV, d=dt), e(B, H, DK, DV)
     N.call("macai_gdr_state_bwd", P(r["Ke"]), P(r["QgT"]), P(r["WT"]), P(r["Mt"]), P(GL2), P(do), P(dsT),
            P(r["dSn"]), P(r["dVn"]), P(r["ds0"]), B, T, H, DK, DV, code, split, st)
     r["dq"], r["dk"], r["dv"] = e(B, T, H, DK, d=dt), e(B, T, H, DK, d=dt), e(B, T, H, DV, d=dt)
