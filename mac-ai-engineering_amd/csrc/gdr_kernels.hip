@@ -378,7 +378,7 @@ struct Buffers {
 // flight while this chunk's MFMAs run -- and each wave keeps its 16 columns of S in accumulators.
 // ---------------------------------------------------------------------------------------------------------------------
 template <typename MT, int DK, int NW, bool OUT, bool STORE>
-__global__ void __launch_bounds__(64 * NW) state_fwd_kernel(StateFwdArgs a) {
+__global__ void __launch_bounds__(64 * (NW + 1)) state_fwd_kernel(StateFwdArgs a) {
   using GW = Tile<MT, C, DK>;    // W, diag(gamma) Q^     [t][d]
   using GKT = Tile<MT, DK, C>;   // (diag(e) K^)^T        [d][t]
   using GM = Tile<MT, C, C>;     // M                     [t][s]
@@ -393,24 +393,47 @@ __global__ void __launch_bounds__(64 * NW) state_fwd_kernel(StateFwdArgs a) {
   if (!state_map(a.nslice, a.B * H, hr, slice)) return;
   const int b = hr / H, h = hr % H;
   const int l = lane_id(), w = wave_id(), j = l >> 4;
+
+  if (w == NW) {
+    // the loader wave: every asynchronous copy of the chunk tiles, one chunk ahead of the compute waves, so that their
+    // issue (a CU's load path takes ~1K cycles for a chunk's tiles) never stalls the MFMA chain
+    int offW[GW::per_wave(1)], offKT[GKT::per_wave(1)], offM[GM::per_wave(1)];
+    GW::template plan<1>(offW, 0, DK);
+    GKT::template plan<1>(offKT, 0, C);
+    if (OUT) GM::template plan<1>(offM, 0, C);
+    auto issue = [&](int c, int buf) {
+      MT* st = lds + buf * SZ;
+      const size_t bhc = (size_t)hr * NT + c;
+      GW::template dma_planned<1>(st, (const MT*)a.W + bhc * C * DK, offW, 0);
+      GKT::template dma_planned<1>(st + O_KT, (const MT*)a.KeT + bhc * DK * C, offKT, 0);
+      if (OUT) {
+        GW::template dma_planned<1>(st + O_Q, (const MT*)a.Qg + bhc * C * DK, offW, 0);
+        GM::template dma_planned<1>(st + O_M, (const MT*)a.M + bhc * C * C, offM, 0);
+      }
+    };
+    if (NBUF == 2) {
+      issue(0, 0);
+      wait_dma();
+      __syncthreads();
+      for (int c = 0; c < NT; ++c) {
+        if (c + 1 < NT) issue(c + 1, (c + 1) & 1);
+        wait_dma();
+        __syncthreads();
+      }
+    } else {
+      for (int c = 0; c < NT; ++c) {
+        issue(c, 0);
+        wait_dma();
+        __syncthreads();   // chunk c is in LDS
+        __syncthreads();   // the compute waves are done with it
+      }
+    }
+    return;                // the compute waves pass no barrier after their loop
+  }
+
   const int v0 = (slice * NW + w) * 16;
   const int col = v0 + (l & 15);
   const size_t o_base = ((size_t)b * T * H + h) * DV, o_pitch = (size_t)H * DV;
-
-  int offW[GW::per_wave(NW)], offKT[GKT::per_wave(NW)], offM[GM::per_wave(NW)];
-  GW::template plan<NW>(offW, w, DK);
-  GKT::template plan<NW>(offKT, w, C);
-  if (OUT) GM::template plan<NW>(offM, w, C);
-  auto issue = [&](int c, int buf) {
-    MT* st = lds + buf * SZ;
-    const size_t bhc = (size_t)hr * NT + c;
-    GW::template dma_planned<NW>(st, (const MT*)a.W + bhc * C * DK, offW, w);
-    GKT::template dma_planned<NW>(st + O_KT, (const MT*)a.KeT + bhc * DK * C, offKT, w);
-    if (OUT) {
-      GW::template dma_planned<NW>(st + O_Q, (const MT*)a.Qg + bhc * C * DK, offW, w);
-      GM::template dma_planned<NW>(st + O_M, (const MT*)a.M + bhc * C * C, offM, w);
-    }
-  };
   auto loadU = [&](int c, f4* U) {
     const float* Uc = a.U + ((size_t)hr * NT + c) * C * DV + (size_t)(4 * j) * DV + col;
 #pragma unroll
@@ -418,72 +441,52 @@ __global__ void __launch_bounds__(64 * NW) state_fwd_kernel(StateFwdArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) U[mi][r] = Uc[(16 * mi + r) * DV];
   };
-  // the results of a chunk are written during the next one, so the wait that ends a chunk waits only on its loads
-  f4 pO[4], pS[ND], pV[4];
-  int pend = -1;
-  auto flush = [&]() {
-    if (pend < 0) return;
-    const int pt0 = pend * C;
-    const size_t pbhc = (size_t)hr * NT + pend;
-    if (OUT) {
+  // results go out as soon as they exist, after the next chunk's U loads are issued (vmcnt is in order, so waiting on
+  // those loads never waits on the stores)
+  auto store_o = [&](int c, const f4 (&O)[4]) {
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
+    for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int t = pt0 + 16 * mi + 4 * j + r;
-          if (t < T) ((MT*)a.o)[o_base + (size_t)t * o_pitch + col] = from_f<MT>(pO[mi][r]);
-        }
-    }
-    if (STORE) {
-      float* Scc = a.Sc + pbhc * DK * DV + (size_t)(4 * j) * DV + col;
+      for (int r = 0; r < 4; ++r) {
+        const int t = c * C + 16 * mi + 4 * j + r;
+        if (t < T) ((MT*)a.o)[o_base + (size_t)t * o_pitch + col] = from_f<MT>(O[mi][r]);
+      }
+  };
+  auto store_sc = [&](int c, const f4 (&X)[ND]) {
+    float* Scc = a.Sc + ((size_t)hr * NT + c) * DK * DV + (size_t)(4 * j) * DV + col;
 #pragma unroll
-      for (int di = 0; di < ND; ++di)
+    for (int di = 0; di < ND; ++di)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) Scc[(16 * di + r) * DV] = pS[di][r];
-      MT* Vnc = (MT*)a.Vn + pbhc * C * DV + (size_t)(4 * j) * DV + col;
+      for (int r = 0; r < 4; ++r) Scc[(16 * di + r) * DV] = X[di][r];
+  };
+  auto store_vn = [&](int c, const f4 (&X)[4]) {
+    MT* Vnc = (MT*)a.Vn + ((size_t)hr * NT + c) * C * DV + (size_t)(4 * j) * DV + col;
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
+    for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) Vnc[(16 * mi + r) * DV] = from_f<MT>(pV[mi][r]);
-    }
+      for (int r = 0; r < 4; ++r) Vnc[(16 * mi + r) * DV] = from_f<MT>(X[mi][r]);
   };
 
   f4 S[ND];
   load_state(S, a.s0, (size_t)hr * DK * DV, DV, col);
 
   f4 Un[4];
-  float gln = 0.f;
-  if (NBUF == 2) {
-    issue(0, 0);
-    loadU(0, Un);
-    gln = a.GL[(size_t)hr * NT];
-    wait_dma();
-    __syncthreads();
-  }
+  loadU(0, Un);
+  float gln = a.GL[(size_t)hr * NT];
+  if (NBUF == 2) __syncthreads();          // chunk 0 is in LDS
   for (int c = 0; c < NT; ++c) {
     const size_t bhc = (size_t)hr * NT + c;
-    int buf = 0;
+    const int buf = (NBUF == 2) ? (c & 1) : 0;
     f4 U[4];
-    float gl;
-    if (NBUF == 2) {
-      buf = c & 1;
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi) U[mi] = Un[mi];
-      gl = gln;
-      if (c + 1 < NT) {
-        issue(c + 1, buf ^ 1);
-        loadU(c + 1, Un);
-        gln = a.GL[bhc + 1];
-      }
-      flush();
-    } else {
-      flush();
-      issue(c, 0);
-      loadU(c, U);
-      gl = a.GL[bhc];
-      wait_dma();
-      __syncthreads();
+    for (int mi = 0; mi < 4; ++mi) U[mi] = Un[mi];
+    const float gl = gln;
+    if (c + 1 < NT) {
+      loadU(c + 1, Un);
+      gln = a.GL[bhc + 1];
     }
+    if (STORE) store_sc(c, S);
+    if (NBUF == 1) __syncthreads();        // chunk c is in LDS
     const MT* st = lds + buf * SZ;
 
     // S as the B operand (k = state rows)
@@ -505,6 +508,7 @@ __global__ void __launch_bounds__(64 * NW) state_fwd_kernel(StateFwdArgs a) {
     Frag<MT> Vf[2];
 #pragma unroll
     for (int p = 0; p < 2; ++p) Vf[p] = frag_acc<MT>(Vn[2 * p], Vn[2 * p + 1]);
+    if (STORE) store_vn(c, Vn);
     // S <- exp(G_last) S + (diag(e) K)^T Vn   (the chain to the next chunk; the rest below is off it)
     f4 Sn[ND];
 #pragma unroll
@@ -519,6 +523,7 @@ __global__ void __launch_bounds__(64 * NW) state_fwd_kernel(StateFwdArgs a) {
     }
     if (OUT) {
       // O = diag(gamma) Q S + M Vn (M lower triangular: k-blocks past the row block are zero)
+      f4 pO[4];
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) {
         Frag<MT> fq[ND / 2];
@@ -532,20 +537,12 @@ __global__ void __launch_bounds__(64 * NW) state_fwd_kernel(StateFwdArgs a) {
           if (32 * p <= 16 * mi + 15) mma(acc, frag_tile<MT, GM>(st + O_M, 16 * mi, 32 * p), Vf[p]);
         pO[mi] = acc;
       }
+      store_o(c, pO);
     }
-    if (STORE) {
-#pragma unroll
-      for (int di = 0; di < ND; ++di) pS[di] = S[di];
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi) pV[mi] = Vn[mi];
-    }
-    pend = c;
 #pragma unroll
     for (int di = 0; di < ND; ++di) S[di] = Sn[di];
-    if (NBUF == 2) wait_dma();
-    __syncthreads();
+    __syncthreads();                       // end of chunk c: the next chunk is in, this buffer may be refilled
   }
-  flush();
   if (a.sT) {
 #pragma unroll
     for (int di = 0; di < ND; ++di)
@@ -558,7 +555,7 @@ __global__ void __launch_bounds__(64 * NW) state_fwd_kernel(StateFwdArgs a) {
 // the reverse state pass: streams diag(e) K^, (diag(gamma) Q^)^T, W^T, M^T and the workgroup's dO columns per chunk
 // ---------------------------------------------------------------------------------------------------------------------
 template <typename MT, int DK, int NW>
-__global__ void __launch_bounds__(64 * NW) state_bwd_kernel(StateBwdArgs a) {
+__global__ void __launch_bounds__(64 * (NW + 1)) state_bwd_kernel(StateBwdArgs a) {
   using GK = Tile<MT, C, DK>;        // diag(e) K^          [t][d]
   using GT = Tile<MT, DK, C>;        // QgT, WT             [d][t]
   using GM = Tile<MT, C, C>;         // M^T                 [s][t]
@@ -575,80 +572,83 @@ __global__ void __launch_bounds__(64 * NW) state_bwd_kernel(StateBwdArgs a) {
   const int b = hr / H, h = hr % H;
   const int l = lane_id(), w = wave_id(), j = l >> 4;
   const int vg = slice * NW * 16;            // the workgroup's first value column
-  const int col = vg + w * 16 + (l & 15);
   const size_t o_base = ((size_t)b * T * H + h) * DV, o_pitch = (size_t)H * DV;
 
-  int offK[GK::per_wave(NW)], offT[GT::per_wave(NW)], offM[GM::per_wave(NW)], offO[GO::per_wave(NW)];
-  GK::template plan<NW>(offK, w, DK);
-  GT::template plan<NW>(offT, w, C);
-  GM::template plan<NW>(offM, w, C);
-  GO::template plan<NW>(offO, w, (int)o_pitch);
-  auto issue = [&](int c, int buf) {
-    MT* st = lds + buf * SZ;
-    const size_t bhc = (size_t)hr * NT + c;
-    const int t0 = c * C;
-    GK::template dma_planned<NW>(st, (const MT*)a.Ke + bhc * C * DK, offK, w);
-    GT::template dma_planned<NW>(st + O_Q, (const MT*)a.QgT + bhc * DK * C, offT, w);
-    GT::template dma_planned<NW>(st + O_W, (const MT*)a.WT + bhc * DK * C, offT, w);
-    GM::template dma_planned<NW>(st + O_M, (const MT*)a.Mt + bhc * C * C, offM, w);
-    const MT* og = (const MT*)a.dO + o_base + (size_t)t0 * o_pitch + vg;
-    if (t0 + C <= T) GO::template dma_planned<NW>(st + O_O, og, offO, w);
-    else GO::dma(st + O_O, og, o_pitch, w, NW, T - t0);   // the last, partial chunk: rows clamped in range
-  };
-  // results written during the next chunk (see state_fwd_kernel)
-  f4 pS[ND], pV[4];
-  int pend = -1;
-  auto flush = [&]() {
-    if (pend < 0) return;
-    const size_t pbhc = (size_t)hr * NT + pend;
-    float* dSc = a.dSn + pbhc * DK * DV + (size_t)(4 * j) * DV + col;
+  if (w == NW) {
+    // the loader wave (see state_fwd_kernel), walking the chunks backwards
+    int offK[GK::per_wave(1)], offT[GT::per_wave(1)], offM[GM::per_wave(1)], offO[GO::per_wave(1)];
+    GK::template plan<1>(offK, 0, DK);
+    GT::template plan<1>(offT, 0, C);
+    GM::template plan<1>(offM, 0, C);
+    GO::template plan<1>(offO, 0, (int)o_pitch);
+    auto issue = [&](int c, int buf) {
+      MT* st = lds + buf * SZ;
+      const size_t bhc = (size_t)hr * NT + c;
+      const int t0 = c * C;
+      GK::template dma_planned<1>(st, (const MT*)a.Ke + bhc * C * DK, offK, 0);
+      GT::template dma_planned<1>(st + O_Q, (const MT*)a.QgT + bhc * DK * C, offT, 0);
+      GT::template dma_planned<1>(st + O_W, (const MT*)a.WT + bhc * DK * C, offT, 0);
+      GM::template dma_planned<1>(st + O_M, (const MT*)a.Mt + bhc * C * C, offM, 0);
+      const MT* og = (const MT*)a.dO + o_base + (size_t)t0 * o_pitch + vg;
+      if (t0 + C <= T) GO::template dma_planned<1>(st + O_O, og, offO, 0);
+      else GO::dma(st + O_O, og, o_pitch, 0, 1, T - t0);   // the last, partial chunk: rows clamped in range
+    };
+    if (NBUF == 2) {
+      issue(NT - 1, 0);
+      wait_dma();
+      __syncthreads();
+      for (int c = NT - 1, it = 0; c >= 0; --c, ++it) {
+        if (c > 0) issue(c - 1, (it + 1) & 1);
+        wait_dma();
+        __syncthreads();
+      }
+    } else {
+      for (int c = NT - 1; c >= 0; --c) {
+        issue(c, 0);
+        wait_dma();
+        __syncthreads();
+        __syncthreads();
+      }
+    }
+    return;
+  }
+  const int col = vg + w * 16 + (l & 15);
+  // dS_{c+1} and dVn go out as soon as they exist
+  auto store_ds = [&](int c, const f4 (&X)[ND]) {
+    float* dSc = a.dSn + ((size_t)hr * NT + c) * DK * DV + (size_t)(4 * j) * DV + col;
 #pragma unroll
     for (int di = 0; di < ND; ++di)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) dSc[(16 * di + r) * DV] = pS[di][r];
-    MT* dVc = (MT*)a.dVn + pbhc * C * DV + (size_t)(4 * j) * DV + col;
+      for (int r = 0; r < 4; ++r) dSc[(16 * di + r) * DV] = X[di][r];
+  };
+  auto store_dv = [&](int c, const f4 (&X)[4]) {
+    MT* dVc = (MT*)a.dVn + ((size_t)hr * NT + c) * C * DV + (size_t)(4 * j) * DV + col;
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) dVc[(16 * mi + r) * DV] = from_f<MT>(pV[mi][r]);
+      for (int r = 0; r < 4; ++r) dVc[(16 * mi + r) * DV] = from_f<MT>(X[mi][r]);
   };
 
   f4 dS[ND];
   load_state(dS, a.dsT, (size_t)hr * DK * DV, DV, col);
 
-  float gln = 0.f;
-  if (NBUF == 2) {
-    issue(NT - 1, 0);
-    gln = a.GL[(size_t)hr * NT + NT - 1];
-    wait_dma();
-    __syncthreads();
-  }
+  float gln = a.GL[(size_t)hr * NT + NT - 1];
+  if (NBUF == 2) __syncthreads();          // the last chunk is in LDS
   for (int c = NT - 1, it = 0; c >= 0; --c, ++it) {
     const int t0 = c * C;
     const size_t bhc = (size_t)hr * NT + c;
-    int buf = 0;
-    float gl;
-    if (NBUF == 2) {
-      buf = it & 1;
-      gl = gln;
-      if (c > 0) {
-        issue(c - 1, buf ^ 1);
-        gln = a.GL[bhc - 1];
-      }
-      flush();
-    } else {
-      flush();
-      issue(c, 0);
-      gl = a.GL[bhc];
-      wait_dma();
-      __syncthreads();
-    }
+    const int buf = (NBUF == 2) ? (it & 1) : 0;
+    const float gl = gln;
+    if (c > 0) gln = a.GL[bhc - 1];
+    store_ds(c, dS);
+    if (NBUF == 1) __syncthreads();        // chunk c is in LDS
     const MT* st = lds + buf * SZ;
 
     Frag<MT> Of[2];
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      Of[p] = frag_tile_rows<MT, GO>(st + O_O, 32 * p, w * 16 + (l & 15));
+      if constexpr (sizeof(MT) == 2) Of[p] = frag_tr(st + O_O, GO::PITCH, 32 * p, w * 16);
+      else Of[p] = frag_tile_rows<MT, GO>(st + O_O, 32 * p, w * 16 + (l & 15));
       if (t0 + C > T)   // rows past the sequence end hold copies of the last row: zero them
 #pragma unroll
         for (int e = 0; e < 8; ++e)
@@ -675,6 +675,7 @@ __global__ void __launch_bounds__(64 * NW) state_bwd_kernel(StateBwdArgs a) {
     Frag<MT> Vf[2];
 #pragma unroll
     for (int p = 0; p < 2; ++p) Vf[p] = frag_acc<MT>(dV[2 * p], dV[2 * p + 1], -1.f);
+    store_dv(c, dV);
     // dS <- exp(G_last) dS + (diag(gamma) Q^)^T dO - W^T dVn
     f4 dSn[ND];
 #pragma unroll
@@ -694,16 +695,9 @@ __global__ void __launch_bounds__(64 * NW) state_bwd_kernel(StateBwdArgs a) {
       dSn[di] = acc;
     }
 #pragma unroll
-    for (int di = 0; di < ND; ++di) pS[di] = dS[di];
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi) pV[mi] = dV[mi];
-    pend = c;
-#pragma unroll
     for (int di = 0; di < ND; ++di) dS[di] = dSn[di];
-    if (NBUF == 2) wait_dma();
-    __syncthreads();
+    __syncthreads();                       // end of chunk c
   }
-  flush();
 #pragma unroll
   for (int di = 0; di < ND; ++di)
 #pragma unroll
@@ -1846,7 +1840,7 @@ int macai_gdr_state_fwd(const void* W, const float* U, const void* KeT, const fl
                  (int)((T + C - 1) / C), nslice};
   const int HR = (int)(B * H);
   dim3 grid((unsigned)(8 * nslice * ((HR + 7) / 8)));
-  dim3 block(64 * nw);
+  dim3 block(64 * (nw + 1));   // nw compute waves and the loader wave
   hipStream_t st = (hipStream_t)stream;
 #define LAUNCH_SF(MT, O, S) \
   DISPATCH_DK(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_fwd_kernel<MT, DKC, NWC, O, S>), grid, block, 0, st, a)))
@@ -1878,7 +1872,7 @@ int macai_gdr_state_bwd(const void* Ke, const void* QgT, const void* WT, const v
                  nslice};
   const int HR = (int)(B * H);
   dim3 grid((unsigned)(8 * nslice * ((HR + 7) / 8)));
-  dim3 block(64 * nw);
+  dim3 block(64 * (nw + 1));   // nw compute waves and the loader wave
   hipStream_t st = (hipStream_t)stream;
   if (dtype == MACAI_GDR_F32) {
     DISPATCH_DK(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_bwd_kernel<float, DKC, NWC>), grid, block, 0, st, a)));
