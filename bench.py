@@ -71,20 +71,22 @@ def kernel_costs(B, T, H, DK, DV, es=2):
     cdk, cdv, cc = C * DK, C * DV, C * C
     sdk = DK * DV * 4                    # one fp32 state
     cost = {}
-    # the forward: prep writes W, U, KeT, GL, Qg, M; the state pass reads them and writes o
-    cost["prep_fwd"] = dict(bytes=2 * io_k + io_v + gb + n * (3 * cdk * es + cdv * 4 + cc * es + 4),
+    pre = 3 * cdk * es + cdv * 4 + cc * es + 4      # prep's row-major outputs W, Ke, Qg, U, M, GL
+    inp = 2 * io_k + io_v + gb                        # q, k, v, g, beta
+    # the forward: prep, then the state pass reads W, U, Ke, GL, Qg, M and writes o
+    cost["prep_fwd"] = dict(bytes=inp + n * pre,
                             flops=n * (2 * 2 * cc * DK + cc * C / 3 + 2 * cc * DK + 2 * cc * DV))
-    cost["state_fwd_out"] = dict(bytes=n * (3 * cdk * es + cdv * 4 + cc * es + 4) + io_v,
-                                 flops=n * (3 * 2 * C * DK * DV + 2 * cc * DV))
-    # the backward: prep writes W, U, KeT, GL, Ke, QgT, WT, Mt, A, At
-    cost["prep_bwd"] = dict(bytes=2 * io_k + io_v + gb + n * (5 * cdk * es + cdv * 4 + 3 * cc * es + 4),
+    cost["state_fwd_out"] = dict(bytes=n * pre + io_v, flops=n * (3 * 2 * C * DK * DV + 2 * cc * DV))
+    # the backward: prep also writes A; the recompute pass reads W, U, Ke, GL and writes S_c (fp32) and Vn; the reverse
+    # pass reads Ke, Qg, W, M, GL, dO and writes dS_{c+1} (fp32) and dVn
+    cost["prep_bwd"] = dict(bytes=inp + n * (pre + cc * es),
                             flops=n * (2 * 2 * cc * DK + cc * C / 3 + 2 * cc * DK + 2 * cc * DV))
     cost["state_fwd_store"] = dict(bytes=n * (2 * cdk * es + cdv * 4 + 4 + sdk + cdv * es),
                                    flops=n * (2 * 2 * C * DK * DV))
     cost["state_bwd"] = dict(bytes=n * (3 * cdk * es + cc * es + 4 + sdk + cdv * es) + io_v,
                              flops=n * (3 * 2 * C * DK * DV + 2 * cc * DV))
-    cost["chunk_bwd"] = dict(bytes=2 * io_k + 2 * io_v + gb + n * (2 * cc * es + 2 * sdk + 2 * cdv * es)
-                             + 2 * io_k + io_v + gb,
+    # the per-chunk backward reads q, k, v, g, beta, dO, A, S_c, dS_{c+1}, Vn, dVn; writes dq, dk, dv, dg, dbeta
+    cost["chunk_bwd"] = dict(bytes=inp + io_v + n * (cc * es + 2 * sdk + 2 * cdv * es) + 2 * io_k + io_v + gb,
                              flops=n * (3 * 2 * C * DK * DV + 2 * cc * DK + 3 * 2 * cc * DK + 2 * 2 * cc * DV
                                         + 2 * 2 * cc * C + 3 * 2 * cc * DK + 2 * cc * DV))
     return cost
@@ -105,27 +107,26 @@ def time_kernels(inp, reps=20):
     sc = DK ** -0.5
     split = op.split_for(B * H, T, DV)
     e = lambda *shape, d=dt: torch.empty(*shape, device=dev, dtype=d)
-    W, U, KeT, GL, Qg, M = e(B, H, NT, C, DK), e(B, H, NT, C, DV, d=f32), e(B, H, NT, DK, C), e(B, H, NT, d=f32), \
+    W, U, Ke, GL, Qg, M = e(B, H, NT, C, DK), e(B, H, NT, C, DV, d=f32), e(B, H, NT, C, DK), e(B, H, NT, d=f32), \
         e(B, H, NT, C, DK), e(B, H, NT, C, C)
-    Ke, QgT, WT, Mt = e(B, H, NT, C, DK), e(B, H, NT, DK, C), e(B, H, NT, DK, C), e(B, H, NT, C, C)
-    A, At = e(B, H, NT, C, C), e(B, H, NT, C, C)
+    A = e(B, H, NT, C, C)
     o = torch.empty_like(v)
     Sc, Vn = e(B, H, NT, DK, DV, d=f32), e(B, H, NT, C, DV)
     dSn, dVn, ds0 = e(B, H, NT, DK, DV, d=f32), torch.empty_like(Vn), e(B, H, DK, DV, d=f32)
     dq, dk, dv, dg, db = (torch.empty_like(x) for x in (q, k, v, g, beta))
     P = N.ptr
     calls = {
-        "prep_fwd": ("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), P(KeT), P(GL), P(Qg), P(M),
-                     None, None, None, None, None, None, B, T, H, DK, DV, code, 1, sc, st),
-        "state_fwd_out": ("macai_gdr_state_fwd", P(W), P(U), P(KeT), P(GL), P(Qg), P(M), P(s0), P(o), None, None,
+        "prep_fwd": ("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), P(Ke), P(GL), P(Qg), P(M), None,
+                     B, T, H, DK, DV, code, 1, sc, st),
+        "state_fwd_out": ("macai_gdr_state_fwd", P(W), P(U), P(Ke), P(GL), P(Qg), P(M), P(s0), P(o), None, None,
                           None, B, T, H, DK, DV, code, 0, split, st),
-        "prep_bwd": ("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), P(KeT), P(GL), None, None, P(Ke),
-                     P(QgT), P(WT), P(Mt), P(A), P(At), B, T, H, DK, DV, code, 1, sc, st),
-        "state_fwd_store": ("macai_gdr_state_fwd", P(W), P(U), P(KeT), P(GL), None, None, P(s0), None, None, P(Sc),
+        "prep_bwd": ("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), P(Ke), P(GL), P(Qg), P(M), P(A),
+                     B, T, H, DK, DV, code, 1, sc, st),
+        "state_fwd_store": ("macai_gdr_state_fwd", P(W), P(U), P(Ke), P(GL), None, None, P(s0), None, None, P(Sc),
                             P(Vn), B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, st),
-        "state_bwd": ("macai_gdr_state_bwd", P(Ke), P(QgT), P(WT), P(Mt), P(GL), P(do), None, P(dSn), P(dVn), P(ds0),
+        "state_bwd": ("macai_gdr_state_bwd", P(Ke), P(Qg), P(W), P(M), P(GL), P(do), None, P(dSn), P(dVn), P(ds0),
                       B, T, H, DK, DV, code, split, st),
-        "chunk_bwd": ("macai_gdr_chunk_bwd", P(q), P(k), P(v), P(g), P(beta), P(do), P(A), P(At), P(Sc), P(dSn),
+        "chunk_bwd": ("macai_gdr_chunk_bwd", P(q), P(k), P(v), P(g), P(beta), P(do), P(A), P(Sc), P(dSn),
                       P(Vn), P(dVn), P(dq), P(dk), P(dv), P(dg), P(db), B, T, H, DK, DV, code, 1, sc, st),
     }
     order = ["prep_fwd", "state_fwd_out", "prep_bwd", "state_fwd_store", "state_bwd", "chunk_bwd"]

@@ -12,12 +12,12 @@
  *   v, o, dO    [B, T, H, DV]   dtype
  *   g, beta     [B, T, H]       float32   (g = log decay <= 0)
  *   states      [B, H, DK, DV]  float32   (initial_state, final state, their gradients)
- *   per chunk   NT = ceil(T / 64) chunks of 64 tokens, padding rows zero (written by macai_gdr_prep):
+ *   per chunk   NT = ceil(T / 64) chunks of 64 tokens, padding rows zero (written by macai_gdr_prep), all row-major
+ *               with the chunk's tokens as rows (the kernels read the transposes they need from LDS):
  *     W, Qg, Ke   [B, H, NT, 64, DK] dtype   W = A diag(beta gamma) K^;  diag(gamma) Q^;  diag(e) K^
- *     KeT, QgT, WT [B, H, NT, DK, 64] dtype  (diag(e) K^)^T, (diag(gamma) Q^)^T, W^T
  *     U           [B, H, NT, 64, DV] float32  U = A diag(beta) V
- *     M, Mt       [B, H, NT, 64, 64] dtype   M = (Q^ K^T) * exp(G_i - G_j) (lower with the diagonal); M^T
- *     A, At       [B, H, NT, 64, 64] dtype   A = (I + L)^-1 (solved in fp32); A^T
+ *     M           [B, H, NT, 64, 64] dtype   M = (Q^ K^T) * exp(G_i - G_j) (lower with the diagonal)
+ *     A           [B, H, NT, 64, 64] dtype   A = (I + L)^-1 (solved in fp32)
  *     GL          [B, H, NT]         float32 exp(G_last) of each chunk
  *     Sc          [B, H, NT, DK, DV] float32 state entering each chunk
  *     dSn         [B, H, NT, DK, DV] float32 dLoss/dS_{c+1}
@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define MACAI_GDR_ABI_VERSION 3
+#define MACAI_GDR_ABI_VERSION 4
 
 /* dtype codes */
 #define MACAI_GDR_F32 0
@@ -59,14 +59,13 @@ extern "C" {
 const char* macai_gdr_last_error(void);
 int macai_gdr_abi_version(void);
 
-/* Per-chunk preparation (north star (1), the intra-chunk kernel), every chunk independent: G, L, A = (I + L)^-1,
- * W, U, KeT and GL always; each other output when its pointer is non-NULL (the forward needs Qg and M; the backward
- * Ke, QgT, WT, Mt, A and At).  Replaces `lib.gdc_prep(q, k, g, beta, gc, a, m, kg, T, H, ...)` (reference
- * op.py:63-72; kernel _chunked.py:220-313) and the fused prologue l2n_fwd (_norm.py:97). */
+/* Per-chunk preparation (north star (1), the intra-chunk kernel), every chunk independent: G, L, A = (I + L)^-1 and
+ * W, U, Ke, GL, Qg, M; A itself when A is non-NULL (the backward's per-chunk pass needs it).  Replaces
+ * `lib.gdc_prep(q, k, g, beta, gc, a, m, kg, T, H, ...)` (reference op.py:63-72; kernel _chunked.py:220-313) and the
+ * fused prologue l2n_fwd (_norm.py:97). */
 int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, const float* beta, void* W, float* U,
-                   void* KeT, float* GL, void* Qg, void* M, void* Ke, void* QgT, void* WT, void* Mt, void* A, void* At,
-                   int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm,
-                   float q_scale, void* stream);
+                   void* Ke, float* GL, void* Qg, void* M, void* A, int64_t B, int64_t T, int64_t H, int64_t DK,
+                   int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, void* stream);
 
 /* The sequential state pass (north star (2) + (3)): S <- exp(G_last) S + K^T diag(e) (U - W S) over the chunks from
  * s0 (NULL = zeros).  flags = 0: the output O = diag(gamma) Q S + M Vn to o (dtype) and the final state to sT when
@@ -74,7 +73,7 @@ int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, 
  * head-row's value columns (DV / 16 / split must be 1, 2, 4 or 8; 0 = automatic).  Replaces `lib.gdc_fwd(q, k, v,
  * beta, s0, gc, a, m, o, sT, sc, vn, xu, ckpt, T, H, DV, flags, ...)` (reference op.py:159, 217; kernel
  * _chunked.py:315-659). */
-int macai_gdr_state_fwd(const void* W, const float* U, const void* KeT, const float* GL, const void* Qg, const void* M,
+int macai_gdr_state_fwd(const void* W, const float* U, const void* Ke, const float* GL, const void* Qg, const void* M,
                         const float* s0, void* o, float* sT, float* Sc, void* Vn, int64_t B, int64_t T, int64_t H,
                         int64_t DK, int64_t DV, int32_t dtype, int32_t flags, int32_t split, void* stream);
 
@@ -82,7 +81,7 @@ int macai_gdr_state_fwd(const void* W, const float* U, const void* KeT, const fl
  * diag(e) K dS, dS <- exp(G_last) dS + (diag(gamma) Q)^T dO - W^T dVn; stores dSn (= dS_{c+1}) and dVn per chunk and
  * writes ds0 = dLoss/d initial_state.  Replaces `lib.gdc_bwd_state(q, k, beta, do, dsT, gc, a, m, dsn, dvn, ds0, T,
  * H, DV, ...)` (reference op.py:234; kernel _chunked.py:661-903). */
-int macai_gdr_state_bwd(const void* Ke, const void* QgT, const void* WT, const void* Mt, const float* GL,
+int macai_gdr_state_bwd(const void* Ke, const void* Qg, const void* W, const void* M, const float* GL,
                         const void* dO, const float* dsT, float* dSn, void* dVn, float* ds0, int64_t B, int64_t T,
                         int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t split, void* stream);
 
@@ -91,7 +90,7 @@ int macai_gdr_state_bwd(const void* Ke, const void* QgT, const void* WT, const v
  * sc, dsn, vn, xu, dvn, dq, dk, dv, dg, dbeta, T, H, DV, ...)` (reference op.py:241-242; kernel
  * _chunked.py:905-1177) and the prologue's backward l2n_bwd (_norm.py:113). */
 int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float* g, const float* beta, const void* dO,
-                        const void* A, const void* At, const float* Sc, const float* dSn, const void* Vn,
+                        const void* A, const float* Sc, const float* dSn, const void* Vn,
                         const void* dVn, void* dq, void* dk, void* dv, float* dg, float* dbeta, int64_t B, int64_t T,
                         int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale,
                         void* stream);

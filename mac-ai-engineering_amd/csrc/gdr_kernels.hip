@@ -40,16 +40,11 @@ struct PrepArgs {
   const float *g, *beta;
   void* W;       // [B,H,NT,C,DK] MT   W = A diag(beta gamma) K^
   float* U;      // [B,H,NT,C,DV] fp32 U = A diag(beta) V
-  void* KeT;     // [B,H,NT,DK,C] MT   (diag(e) K^)^T
+  void* Ke;      // [B,H,NT,C,DK] MT   diag(e) K^
   float* GL;     // [B,H,NT]      fp32 exp(G_last)
-  void* Qg;      // [B,H,NT,C,DK] MT   diag(gamma) Q^            (or null)
-  void* M;       // [B,H,NT,C,C]  MT   M, row-major [t][s]       (or null)
-  void* Ke;      // [B,H,NT,C,DK] MT   diag(e) K^                (or null)
-  void* QgT;     // [B,H,NT,DK,C] MT   (diag(gamma) Q^)^T        (or null)
-  void* WT;      // [B,H,NT,DK,C] MT   W^T                       (or null)
-  void* Mt;      // [B,H,NT,C,C]  MT   M^T                       (or null)
+  void* Qg;      // [B,H,NT,C,DK] MT   diag(gamma) Q^
+  void* M;       // [B,H,NT,C,C]  MT   M, row-major [t][s]
   void* A;       // [B,H,NT,C,C]  MT   A                         (or null)
-  void* At;      // [B,H,NT,C,C]  MT   A^T                       (or null)
   int B, T, H, DV, NT;
   int l2norm;
   float q_scale;
@@ -58,7 +53,7 @@ struct PrepArgs {
 struct StateFwdArgs {
   const void *W;
   const float* U;
-  const void *KeT;
+  const void *Ke;
   const float* GL;
   const void *Qg, *M;
   const float* s0;
@@ -71,7 +66,7 @@ struct StateFwdArgs {
 };
 
 struct StateBwdArgs {
-  const void *Ke, *QgT, *WT, *Mt;
+  const void *Ke, *Qg, *W, *M;
   const float* GL;
   const void* dO;
   const float* dsT;
@@ -86,7 +81,7 @@ struct ChunkBwdArgs {
   const void *q, *k, *v;
   const float *g, *beta;
   const void* dO;
-  const void *A, *At;                         // MT
+  const void* A;                              // MT
   const float* Sc;                            // fp32
   const float* dSn;                           // fp32
   const void *Vn, *dVn;                       // MT
@@ -143,12 +138,11 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
   const IT* q = (const IT*)a.q + qk_base;
   const IT* k = (const IT*)a.k + qk_base;
   const IT* v = (const IT*)a.v + v_base;
-  const bool needQ = a.M || a.Mt || a.Qg || a.QgT;
 
   if (w == 0) chunk_scalars(cs, a.g, a.beta, s_base, H, t0, T);
   if (a.l2norm) {
     row_rnorms<IT, DK>(rk, (const IT*)a.k, qk_base, qk_pitch, t0, T, 4);
-    if (needQ) row_rnorms<IT, DK>(rq, (const IT*)a.q, qk_base, qk_pitch, t0, T, 4);
+    row_rnorms<IT, DK>(rq, (const IT*)a.q, qk_base, qk_pitch, t0, T, 4);
   } else if (threadIdx.x < C) {
     rk[threadIdx.x] = 1.f;
     rq[threadIdx.x] = 1.f;
@@ -158,8 +152,8 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
   const float qs = a.q_scale;
   // K^ rows into LDS; diag(e) K^ rows out (row-major).  Q^ rows into LDS; diag(gamma) Q^ rows out.
   {
-    MT* Ke = a.Ke ? (MT*)a.Ke + bhc * C * DK : nullptr;
-    MT* Qg = a.Qg ? (MT*)a.Qg + bhc * C * DK : nullptr;
+    MT* Ke = (MT*)a.Ke + bhc * C * DK;
+    MT* Qg = (MT*)a.Qg + bhc * C * DK;
     constexpr int PR = DK / 8;
     for (int i = threadIdx.x; i < C * PR; i += blockDim.x) {
       const int r = i / PR, c8 = (i - r * PR) * 8, t = t0 + r;
@@ -174,20 +168,18 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
         x[e] = y[e] * cs.e[r];
       }
       store8(sK + r * KP + c8, y);
-      if (Ke) store8(Ke + r * DK + c8, x);
-      if (needQ) {
-        if (t < T) load8(q + (size_t)t * qk_pitch + c8, x);
-        else
+      store8(Ke + r * DK + c8, x);
+      if (t < T) load8(q + (size_t)t * qk_pitch + c8, x);
+      else
 #pragma unroll
-          for (int e = 0; e < 8; ++e) x[e] = 0.f;
+        for (int e = 0; e < 8; ++e) x[e] = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          y[e] = x[e] * (rq[r] * qs);
-          x[e] = y[e] * cs.gam[r];
-        }
-        store8(sQ + r * KP + c8, y);
-        if (Qg) store8(Qg + r * DK + c8, x);
+      for (int e = 0; e < 8; ++e) {
+        y[e] = x[e] * (rq[r] * qs);
+        x[e] = y[e] * cs.gam[r];
       }
+      store8(sQ + r * KP + c8, y);
+      store8(Qg + r * DK + c8, x);
     }
   }
   __syncthreads();
@@ -203,10 +195,7 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
           Frag<MT> bk = frag_k_raw(sK, KP, 16 * ni, 32 * p);
           Frag<MT> ak = frag_k_raw(sK, KP, 16 * mi, 32 * p);
           mma(kk, ak, bk);
-          if (needQ) {
-            Frag<MT> aq = frag_k_raw(sQ, KP, 16 * mi, 32 * p);
-            mma(qk, aq, bk);
-          }
+          mma(qk, frag_k_raw(sQ, KP, 16 * mi, 32 * p), bk);
         }
       }
       const int col = 16 * ni + (l & 15);
@@ -215,44 +204,23 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
         const int row = 16 * mi + 4 * j + r;
         const float gm = (row >= col) ? cs.decay(row, col) : 0.f;   // mask before the exponent
         sL[row * FP + col] = (row > col) ? cs.beta[row] * kk[r] * gm : 0.f;
-        if (needQ) {
-          const MT mv = from_f<MT>((row >= col) ? qk[r] * gm : 0.f);
-          if (a.M) ((MT*)a.M)[bhc * C * C + row * C + col] = mv;
-          if (a.Mt) ((MT*)a.Mt)[bhc * C * C + col * C + row] = mv;
-        }
+        ((MT*)a.M)[bhc * C * C + row * C + col] = from_f<MT>((row >= col) ? qk[r] * gm : 0.f);
       }
     }
   }
   __syncthreads();
 
-  // transposed operands from the raw rows (one rounding each; consecutive lanes take consecutive rows, so the
-  // transposed global stores are coalesced): (diag(e) K^)^T, (diag(gamma) Q^)^T out; (beta gamma K^)^T into LDS for W
-  {
-    MT* KeT = (MT*)a.KeT + bhc * DK * C;
-    MT* QgT = a.QgT ? (MT*)a.QgT + bhc * DK * C : nullptr;
-    for (int i = threadIdx.x; i < C * (DK / 8); i += blockDim.x) {
-      const int r = i % C, c8 = (i / C) * 8, t = t0 + r;
-      float x[8];
-      if (t < T) load8(k + (size_t)t * qk_pitch + c8, x);
-      else
+  // (beta gamma K^)^T into LDS for W, from the raw rows (one rounding)
+  for (int i = threadIdx.x; i < C * (DK / 8); i += blockDim.x) {
+    const int r = i % C, c8 = (i / C) * 8, t = t0 + r;
+    float x[8];
+    if (t < T) load8(k + (size_t)t * qk_pitch + c8, x);
+    else
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = 0.f;
-      const float sk = rk[r] * cs.e[r], sb = rk[r] * cs.beta[r] * cs.gam[r];
+      for (int e = 0; e < 8; ++e) x[e] = 0.f;
+    const float sb = rk[r] * cs.beta[r] * cs.gam[r];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        KeT[(c8 + e) * C + r] = from_f<MT>(x[e] * sk);
-        sQ[(c8 + e) * CP + r] = from_f<MT>(x[e] * sb);
-      }
-      if (QgT) {
-        if (t < T) load8(q + (size_t)t * qk_pitch + c8, x);
-        else
-#pragma unroll
-          for (int e = 0; e < 8; ++e) x[e] = 0.f;
-        const float sq = rq[r] * qs * cs.gam[r];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) QgT[(c8 + e) * C + r] = from_f<MT>(x[e] * sq);
-      }
-    }
+    for (int e = 0; e < 8; ++e) sQ[(c8 + e) * CP + r] = from_f<MT>(x[e] * sb);
   }
 
   // A = (I + L)^-1.  Diagonal 16 x 16 blocks by forward substitution: wave 0, lane = (block l/16, column l%16).
@@ -303,15 +271,11 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
     for (int p = 0; p < 2; ++p) af[p] = cvt<MT>(frag_k_f32(sA, FP, 16 * w, 32 * p));
     const int np = (16 * w + 15) / 32 + 1;
     MT* Wc = (MT*)a.W + bhc * C * DK;
-    MT* WTc = a.WT ? (MT*)a.WT + bhc * DK * C : nullptr;
     for (int ni = 0; ni < DK / 16; ++ni) {
       f4 acc = {0.f, 0.f, 0.f, 0.f};
       for (int p = 0; p < np; ++p) mma(acc, af[p], frag_k_raw(sQ, CP, 16 * ni, 32 * p));
 #pragma unroll
       for (int r = 0; r < 4; ++r) Wc[(16 * w + 4 * j + r) * DK + 16 * ni + (l & 15)] = from_f<MT>(acc[r]);
-      if (WTc)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) WTc[(16 * ni + (l & 15)) * C + 16 * w + 4 * j + r] = from_f<MT>(acc[r]);
     }
     // U = A (beta V), 64 value columns at a time staged transposed in sK
     float* Uc = a.U + bhc * C * DV;
@@ -330,12 +294,9 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
   }
   if (a.A) {
     MT* Ag = (MT*)a.A + bhc * C * C;
-    MT* Atg = (MT*)a.At + bhc * C * C;
     for (int i = threadIdx.x; i < C * C; i += blockDim.x) {
       const int row = i / C, col = i % C;
-      const MT x = from_f<MT>(sA[row * FP + col]);
-      Ag[row * C + col] = x;
-      Atg[col * C + row] = x;
+      Ag[row * C + col] = from_f<MT>(sA[row * FP + col]);
     }
   }
 }
@@ -373,17 +334,16 @@ struct Buffers {
 };
 
 // ---------------------------------------------------------------------------------------------------------------------
-// the forward state pass (+ output), sequential over chunks.  Per chunk the workgroup streams W, (diag(e) K^)^T and, for
+// the forward state pass (+ output), sequential over chunks.  Per chunk the workgroup streams W, diag(e) K^ and, for
 // the output, diag(gamma) Q^ and M into a swizzled LDS stage by asynchronous copies -- the next chunk's copies are in
 // flight while this chunk's MFMAs run -- and each wave keeps its 16 columns of S in accumulators.
 // ---------------------------------------------------------------------------------------------------------------------
 template <typename MT, int DK, int NW, bool OUT, bool STORE>
 __global__ void __launch_bounds__(64 * (NW + 1)) state_fwd_kernel(StateFwdArgs a) {
-  using GW = Tile<MT, C, DK>;    // W, diag(gamma) Q^     [t][d]
-  using GKT = Tile<MT, DK, C>;   // (diag(e) K^)^T        [d][t]
-  using GM = Tile<MT, C, C>;     // M                     [t][s]
+  using GW = Tile<MT, C, DK>;    // W, diag(e) K^, diag(gamma) Q^     [t][d]
+  using GM = Tile<MT, C, C>;     // M                                  [t][s]
   constexpr int ND = DK / 16;
-  constexpr int O_KT = GW::ELEMS, O_Q = O_KT + GKT::ELEMS, O_M = O_Q + (OUT ? GW::ELEMS : 0);
+  constexpr int O_KE = GW::ELEMS, O_Q = O_KE + GW::ELEMS, O_M = O_Q + (OUT ? GW::ELEMS : 0);
   constexpr int SZ = O_M + (OUT ? GM::ELEMS : 0);
   constexpr int NBUF = Buffers<SZ * (int)sizeof(MT)>::N;
   __shared__ __attribute__((aligned(1024))) MT lds[NBUF * SZ];
@@ -397,15 +357,14 @@ __global__ void __launch_bounds__(64 * (NW + 1)) state_fwd_kernel(StateFwdArgs a
   if (w == NW) {
     // the loader wave: every asynchronous copy of the chunk tiles, one chunk ahead of the compute waves, so that their
     // issue (a CU's load path takes ~1K cycles for a chunk's tiles) never stalls the MFMA chain
-    int offW[GW::per_wave(1)], offKT[GKT::per_wave(1)], offM[GM::per_wave(1)];
+    int offW[GW::per_wave(1)], offM[GM::per_wave(1)];
     GW::template plan<1>(offW, 0, DK);
-    GKT::template plan<1>(offKT, 0, C);
     if (OUT) GM::template plan<1>(offM, 0, C);
     auto issue = [&](int c, int buf) {
       MT* st = lds + buf * SZ;
       const size_t bhc = (size_t)hr * NT + c;
       GW::template dma_planned<1>(st, (const MT*)a.W + bhc * C * DK, offW, 0);
-      GKT::template dma_planned<1>(st + O_KT, (const MT*)a.KeT + bhc * DK * C, offKT, 0);
+      GW::template dma_planned<1>(st + O_KE, (const MT*)a.Ke + bhc * C * DK, offW, 0);
       if (OUT) {
         GW::template dma_planned<1>(st + O_Q, (const MT*)a.Qg + bhc * C * DK, offW, 0);
         GM::template dma_planned<1>(st + O_M, (const MT*)a.M + bhc * C * C, offM, 0);
@@ -515,7 +474,7 @@ __global__ void __launch_bounds__(64 * (NW + 1)) state_fwd_kernel(StateFwdArgs a
     for (int di = 0; di < ND; ++di) {
       Frag<MT> fk[2];
 #pragma unroll
-      for (int p = 0; p < 2; ++p) fk[p] = frag_tile<MT, GKT>(st + O_KT, 16 * di, 32 * p);
+      for (int p = 0; p < 2; ++p) fk[p] = frag_tile_tr<MT, GW>(st + O_KE, 32 * p, 16 * di);
       f4 acc = S[di] * gl;
 #pragma unroll
       for (int p = 0; p < 2; ++p) mma(acc, fk[p], Vf[p]);
@@ -552,16 +511,15 @@ __global__ void __launch_bounds__(64 * (NW + 1)) state_fwd_kernel(StateFwdArgs a
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
-// the reverse state pass: streams diag(e) K^, (diag(gamma) Q^)^T, W^T, M^T and the workgroup's dO columns per chunk
+// the reverse state pass: streams diag(e) K^, diag(gamma) Q^, W, M and the workgroup's dO columns per chunk
 // ---------------------------------------------------------------------------------------------------------------------
 template <typename MT, int DK, int NW>
 __global__ void __launch_bounds__(64 * (NW + 1)) state_bwd_kernel(StateBwdArgs a) {
-  using GK = Tile<MT, C, DK>;        // diag(e) K^          [t][d]
-  using GT = Tile<MT, DK, C>;        // QgT, WT             [d][t]
-  using GM = Tile<MT, C, C>;         // M^T                 [s][t]
-  using GO = Tile<MT, C, 16 * NW>;   // dO columns          [t][v]
+  using GK = Tile<MT, C, DK>;        // diag(e) K^, diag(gamma) Q^, W    [t][d]
+  using GM = Tile<MT, C, C>;         // M                                [t][s]
+  using GO = Tile<MT, C, 16 * NW>;   // dO columns                       [t][v]
   constexpr int ND = DK / 16;
-  constexpr int O_Q = GK::ELEMS, O_W = O_Q + GT::ELEMS, O_M = O_W + GT::ELEMS, O_O = O_M + GM::ELEMS;
+  constexpr int O_Q = GK::ELEMS, O_W = O_Q + GK::ELEMS, O_M = O_W + GK::ELEMS, O_O = O_M + GM::ELEMS;
   constexpr int SZ = O_O + GO::ELEMS;
   constexpr int NBUF = Buffers<SZ * (int)sizeof(MT)>::N;
   __shared__ __attribute__((aligned(1024))) MT lds[NBUF * SZ];
@@ -576,9 +534,8 @@ __global__ void __launch_bounds__(64 * (NW + 1)) state_bwd_kernel(StateBwdArgs a
 
   if (w == NW) {
     // the loader wave (see state_fwd_kernel), walking the chunks backwards
-    int offK[GK::per_wave(1)], offT[GT::per_wave(1)], offM[GM::per_wave(1)], offO[GO::per_wave(1)];
+    int offK[GK::per_wave(1)], offM[GM::per_wave(1)], offO[GO::per_wave(1)];
     GK::template plan<1>(offK, 0, DK);
-    GT::template plan<1>(offT, 0, C);
     GM::template plan<1>(offM, 0, C);
     GO::template plan<1>(offO, 0, (int)o_pitch);
     auto issue = [&](int c, int buf) {
@@ -586,9 +543,9 @@ __global__ void __launch_bounds__(64 * (NW + 1)) state_bwd_kernel(StateBwdArgs a
       const size_t bhc = (size_t)hr * NT + c;
       const int t0 = c * C;
       GK::template dma_planned<1>(st, (const MT*)a.Ke + bhc * C * DK, offK, 0);
-      GT::template dma_planned<1>(st + O_Q, (const MT*)a.QgT + bhc * DK * C, offT, 0);
-      GT::template dma_planned<1>(st + O_W, (const MT*)a.WT + bhc * DK * C, offT, 0);
-      GM::template dma_planned<1>(st + O_M, (const MT*)a.Mt + bhc * C * C, offM, 0);
+      GK::template dma_planned<1>(st + O_Q, (const MT*)a.Qg + bhc * C * DK, offK, 0);
+      GK::template dma_planned<1>(st + O_W, (const MT*)a.W + bhc * C * DK, offK, 0);
+      GM::template dma_planned<1>(st + O_M, (const MT*)a.M + bhc * C * C, offM, 0);
       const MT* og = (const MT*)a.dO + o_base + (size_t)t0 * o_pitch + vg;
       if (t0 + C <= T) GO::template dma_planned<1>(st + O_O, og, offO, 0);
       else GO::dma(st + O_O, og, o_pitch, 0, 1, T - t0);   // the last, partial chunk: rows clamped in range
@@ -669,7 +626,7 @@ __global__ void __launch_bounds__(64 * (NW + 1)) state_bwd_kernel(StateBwdArgs a
       for (int p = 0; p < ND / 2; ++p) mma(acc, fk[p], Sf[p]);
 #pragma unroll
       for (int p = 0; p < 2; ++p)
-        if (32 * p + 31 >= 16 * mi) mma(acc, frag_tile<MT, GM>(st + O_M, 16 * mi, 32 * p), Of[p]);
+        if (32 * p + 31 >= 16 * mi) mma(acc, frag_tile_tr<MT, GM>(st + O_M, 32 * p, 16 * mi), Of[p]);
       dV[mi] = acc;
     }
     Frag<MT> Vf[2];
@@ -683,8 +640,8 @@ __global__ void __launch_bounds__(64 * (NW + 1)) state_bwd_kernel(StateBwdArgs a
       Frag<MT> fw[2], fq[2];
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        fw[p] = frag_tile<MT, GT>(st + O_W, 16 * di, 32 * p);
-        fq[p] = frag_tile<MT, GT>(st + O_Q, 16 * di, 32 * p);
+        fw[p] = frag_tile_tr<MT, GK>(st + O_W, 32 * p, 16 * di);
+        fq[p] = frag_tile_tr<MT, GK>(st + O_Q, 32 * p, 16 * di);
       }
       f4 acc = dS[di] * gl;
 #pragma unroll
@@ -717,24 +674,17 @@ __device__ __forceinline__ Frag<MT> zero_frag() {
   return o;
 }
 
-// One workgroup (4 waves) per (chunk, head, batch row).  bf16 operands: the chunk's raw q, k, dO and Vn, dVn, A^T are
-// copied into padded LDS tiles at the start (asynchronous, all in flight together) and every MFMA fragment is read from
-// there; fp32 operands do not fit, so the same accessors read them from global memory.  The prologue's row scales
+// The fp32 per-chunk backward (bf16 operands take chunk_bwd8_kernel): one workgroup (4 waves) per (chunk, head, batch
+// row), fragments read straight from global memory (fp32 tiles do not fit LDS).  The prologue's row scales
 // (q^ = q rq DK^-1/2, k^ = k rk) are applied to the products' rows and columns, and folded into the stored dM and Z, so
 // the raw inputs are the MFMA operands.  Wave w owns key-column blocks w, w + 4, ... of the [C x DK] products, column
 // block w of the [C x C] ones and value-column blocks w, w + 4, ...
 template <typename MT, int DK, int DV>
 __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
-  constexpr bool STAGE = sizeof(MT) == 2;
+  static_assert(sizeof(MT) == 4, "bf16 operands take chunk_bwd8_kernel");
   constexpr int KP = DK + 8, CP = C + 8;
   constexpr int NBD = DK / 16;            // 16-column blocks of the key width
   constexpr int NBW = (NBD + 3) / 4;      // most blocks a wave owns
-  using GQ = Tile<MT, C, DK>;
-  using GV = Tile<MT, C, DV>;
-  using GA = Tile<MT, C, C>;
-  constexpr int O_K = GQ::ELEMS, O_O = 2 * GQ::ELEMS, O_VN = O_O + GV::ELEMS, O_DV = O_VN + GV::ELEMS,
-                O_AT = O_DV + GV::ELEMS, TILES = STAGE ? O_AT + GA::ELEMS : 8;
-  __shared__ __attribute__((aligned(16))) MT tiles[TILES];
   __shared__ __attribute__((aligned(16))) MT sdW[C * KP];   // dW = -dVn S_c^T
   __shared__ __attribute__((aligned(16))) MT sdMk[C * CP];  // dM diag(rk):            [t][s] = dM[t][s] rk_s
   __shared__ __attribute__((aligned(16))) MT sdMq[C * CP];  // dM^T diag(rq DK^-1/2):  [t][s] = dM[s][t] rq_s qs
@@ -763,17 +713,8 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
   const MT* Vnc = (const MT*)a.Vn + bhc * C * DV;
   const MT* dVc = (const MT*)a.dVn + bhc * C * DV;
   const MT* Ac = (const MT*)a.A + bhc * C * C;
-  const MT* Atc = (const MT*)a.At + bhc * C * C;
   const float qs = a.q_scale;
 
-  if constexpr (STAGE) {
-    GQ::dma(tiles, q + (size_t)t0 * qk_pitch, qk_pitch, w, 4, nrows);
-    GQ::dma(tiles + O_K, k + (size_t)t0 * qk_pitch, qk_pitch, w, 4, nrows);
-    GV::dma(tiles + O_O, dO + (size_t)t0 * v_pitch, v_pitch, w, 4, nrows);
-    GV::dma(tiles + O_VN, Vnc, DV, w, 4);
-    GV::dma(tiles + O_DV, dVc, DV, w, 4);
-    GA::dma(tiles + O_AT, Atc, C, w, 4);
-  }
   if (w == 0) chunk_scalars(cs, a.g, a.beta, s_base, H, t0, T);
   if (a.l2norm) {
     row_rnorms<MT, DK>(rk, (const MT*)a.k, qk_base, qk_pitch, t0, T, 4);
@@ -782,61 +723,25 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
     rk[threadIdx.x] = (int)threadIdx.x < nrows ? 1.f : 0.f;
     rq[threadIdx.x] = (int)threadIdx.x < nrows ? 1.f : 0.f;
   }
-  if constexpr (STAGE) wait_dma();
   __syncthreads();
 
-  // operand accessors: raw rows (masked past the sequence end where the tile holds copies of the last row)
-  auto fq = [&](int row0, int k0) -> Frag<MT> {   // raw q rows
-    if constexpr (STAGE) return (row0 + (l & 15) < nrows) ? frag_tile<MT, GQ>(tiles, row0, k0) : zero_frag<MT>();
-    else return frag_k_seq<MT, MT>(q, qk_pitch, t0, T, row0, k0, One());
-  };
-  auto fk = [&](int row0, int k0) -> Frag<MT> {   // raw k rows
-    if constexpr (STAGE) return (row0 + (l & 15) < nrows) ? frag_tile<MT, GQ>(tiles + O_K, row0, k0) : zero_frag<MT>();
-    else return frag_k_seq<MT, MT>(k, qk_pitch, t0, T, row0, k0, One());
-  };
-  auto rows_masked = [&](Frag<MT> f, int krow0) -> Frag<MT> {
-    if (nrows < C)
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (krow0 + kmap(j, e) >= nrows) f.set(e, 0.f);
-    return f;
-  };
-  auto fqrows = [&](int krow0, int col) -> Frag<MT> {   // raw q, k = rows
-    if constexpr (STAGE) return rows_masked(frag_tile_rows<MT, GQ>(tiles, krow0, col), krow0);
-    else return frag_rows<MT, MT>(q, qk_pitch, t0, T, krow0, col, One());
-  };
-  auto fkrows = [&](int krow0, int col) -> Frag<MT> {   // raw k, k = rows
-    if constexpr (STAGE) return rows_masked(frag_tile_rows<MT, GQ>(tiles + O_K, krow0, col), krow0);
-    else return frag_rows<MT, MT>(k, qk_pitch, t0, T, krow0, col, One());
-  };
-  auto fO = [&](int row0, int k0) -> Frag<MT> {
-    if constexpr (STAGE) return (row0 + (l & 15) < nrows) ? frag_tile<MT, GV>(tiles + O_O, row0, k0) : zero_frag<MT>();
-    else return frag_k_seq<MT, MT>(dO, v_pitch, t0, T, row0, k0, One());
-  };
-  auto fVn = [&](int row0, int k0) -> Frag<MT> {
-    if constexpr (STAGE) return frag_tile<MT, GV>(tiles + O_VN, row0, k0);
-    else return frag_k<MT, MT>(Vnc, DV, row0, k0);
-  };
-  auto fdVn = [&](int row0, int k0) -> Frag<MT> {
-    if constexpr (STAGE) return frag_tile<MT, GV>(tiles + O_DV, row0, k0);
-    else return frag_k<MT, MT>(dVc, DV, row0, k0);
-  };
-  auto fdVnrows = [&](int krow0, int col) -> Frag<MT> {
-    if constexpr (STAGE) return frag_tile_rows<MT, GV>(tiles + O_DV, krow0, col);
-    else return frag_rows<MT, MT>(dVc, DV, 0, C, krow0, col, One());
-  };
-  auto fAt = [&](int row0, int k0) -> Frag<MT> {
-    if constexpr (STAGE) return frag_tile<MT, GA>(tiles + O_AT, row0, k0);
-    else return frag_k<MT, MT>(Atc, C, row0, k0);
-  };
+  // operand accessors: raw rows (zero past the sequence end)
+  auto fq = [&](int row0, int k0) { return frag_k_seq<MT, MT>(q, qk_pitch, t0, T, row0, k0, One()); };
+  auto fk = [&](int row0, int k0) { return frag_k_seq<MT, MT>(k, qk_pitch, t0, T, row0, k0, One()); };
+  auto fqrows = [&](int krow0, int col) { return frag_rows<MT, MT>(q, qk_pitch, t0, T, krow0, col, One()); };
+  auto fkrows = [&](int krow0, int col) { return frag_rows<MT, MT>(k, qk_pitch, t0, T, krow0, col, One()); };
+  auto fO = [&](int row0, int k0) { return frag_k_seq<MT, MT>(dO, v_pitch, t0, T, row0, k0, One()); };
+  auto fVn = [&](int row0, int k0) { return frag_k<MT, MT>(Vnc, DV, row0, k0); };
+  auto fdVn = [&](int row0, int k0) { return frag_k<MT, MT>(dVc, DV, row0, k0); };
+  auto fdVnrows = [&](int krow0, int col) { return frag_rows<MT, MT>(dVc, DV, 0, C, krow0, col, One()); };
+  // A^T rows row0.. (A operand): column row0 + l % 16 of A, k over A's rows
+  auto fAt = [&](int row0, int k0) { return frag_rows<MT, MT>(Ac, C, 0, C, k0, row0 + (l & 15), One()); };
   // raw q / k at (chunk row, key column) times the row's inverse norm: the unit-norm direction (0 past the end)
   auto xq = [&](int row, int d) -> float {
-    if constexpr (STAGE) return to_f(tiles[GQ::offset(row, d)]) * rq[row];
-    else return (t0 + row < T) ? to_f(q[(size_t)(t0 + row) * qk_pitch + d]) * rq[row] : 0.f;
+    return (t0 + row < T) ? to_f(q[(size_t)(t0 + row) * qk_pitch + d]) * rq[row] : 0.f;
   };
   auto xk = [&](int row, int d) -> float {
-    if constexpr (STAGE) return to_f(tiles[O_K + GQ::offset(row, d)]) * rk[row];
-    else return (t0 + row < T) ? to_f(k[(size_t)(t0 + row) * qk_pitch + d]) * rk[row] : 0.f;
+    return (t0 + row < T) ? to_f(k[(size_t)(t0 + row) * qk_pitch + d]) * rk[row] : 0.f;
   };
 
   // ---- B: products with the chunk states; wave w owns key-column blocks w, w + 4, ...
@@ -1192,7 +1097,7 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
 // ---------------------------------------------------------------------------------------------------------------------
 // the per-chunk backward for bf16 operands: 8 waves, every operand in LDS
 // ---------------------------------------------------------------------------------------------------------------------
-// One workgroup of 8 waves (two per SIMD) per (chunk, head, batch row).  The chunk's raw q, k, dO and Vn, dVn, A^T
+// One workgroup of 8 waves (two per SIMD) per (chunk, head, batch row).  The chunk's raw q, k, dO and Vn, dVn, A
 // are copied into padded LDS tiles at the start (asynchronous; rows past the sequence end are zeroed), and v replaces
 // dO once dO is consumed.  The [C x D] products are formed transposed, as [D x C] with the chunk's tokens as the MFMA
 // columns, so that in their epilogues a lane holds one token and 4 consecutive features: per-token scalars are lane
@@ -1214,7 +1119,7 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   constexpr int VP = GV::PITCH;
   constexpr int O_K = GQ::ELEMS, O_O = 2 * GQ::ELEMS, O_VN = O_O + GV::ELEMS, O_DV = O_VN + GV::ELEMS,
                 O_AT = O_DV + GV::ELEMS, TILES = O_AT + GA::ELEMS;
-  __shared__ __attribute__((aligned(16))) MT tiles[TILES];   // q, k, dO (then v), Vn (then dv), dVn, A^T
+  __shared__ __attribute__((aligned(16))) MT tiles[TILES];   // q, k, dO (then v), Vn (then dv), dVn, A
   __shared__ __attribute__((aligned(16))) MT sdW[C * KP];    // dW = -dVn S_c^T, [t][d]
   __shared__ __attribute__((aligned(16))) MT sMkT[C * CP];   // [s][t] = dM[t][s] rk_s
   __shared__ __attribute__((aligned(16))) MT sMqT[C * CP];   // [s][t] = dM[t][s] rq_t qs
@@ -1241,14 +1146,14 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   const float* dSc = a.dSn + bhc * DK * DV;
   const MT* Vnc = (const MT*)a.Vn + bhc * C * DV;
   const MT* dVc = (const MT*)a.dVn + bhc * C * DV;
-  const MT* Atc = (const MT*)a.At + bhc * C * C;
+  const MT* Ac = (const MT*)a.A + bhc * C * C;
   const float qs = a.q_scale;
   MT* const tq = tiles;
   MT* const tk = tiles + O_K;
   MT* const tO = tiles + O_O;
   MT* const tVn = tiles + O_VN;
   MT* const tdV = tiles + O_DV;
-  MT* const tAt = tiles + O_AT;
+  MT* const tA = tiles + O_AT;
   const int cb = w & 3, hh = w >> 2;       // [C x C] column block and row half
 
   // ---- 0: global operands into registers first (their latency overlaps the tile copies), then the tiles
@@ -1269,7 +1174,7 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   GV::dma(tO, dO + (size_t)t0 * v_pitch, v_pitch, w, NW, nrows);
   GV::dma(tVn, Vnc, DV, w, NW);
   GV::dma(tdV, dVc, DV, w, NW);
-  GA::dma(tAt, Atc, C, w, NW);
+  GA::dma(tA, Ac, C, w, NW);
   if (w == 0) chunk_scalars(cs, a.g, a.beta, s_base, H, t0, T);
   if (a.l2norm) {
     if (w >= 4 && w < 6) row_rnorms<MT, DK>(rk, (const MT*)a.k, qk_base, qk_pitch, t0, T, 2, w - 4);
@@ -1338,7 +1243,7 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
       f4 x = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int p = 0; p < 2; ++p)
-        if (32 * p + 31 >= 16 * ti) mma(x, fW[p], frag_tile<MT, GA>(tAt, 16 * ti, 32 * p));
+        if (32 * p + 31 >= 16 * ti) mma(x, fW[p], frag_tr(tA, CP, 32 * p, 16 * ti));
       const int t = 16 * ti + n;
       const f4 k4 = load4(tk + t * KP + d0);
       dKt[ti] += (cs.beta[t] * cs.gam[t]) * x;
@@ -1435,7 +1340,7 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
       if (32 * p > 16 * cb + 15) continue;
-      const Frag<MT> bA = frag_tr(tAt, CP, 32 * p, 16 * cb);        // B[s][t'] = A[t'][s]
+      const Frag<MT> bA = frag_tile<MT, GA>(tA, 16 * cb, 32 * p);   // B[s][t'] = A[t'][s]
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi)
         if (32 * p <= 16 * mi + 15) mma(T1[mi], frag_tr(sAZ, CP, 32 * p, 16 * mi), bA);
@@ -1454,7 +1359,7 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
       if (mi >= cb) {
 #pragma unroll
         for (int p = 0; p < 2; ++p)
-          if (32 * p + 31 >= 16 * mi) mma(dL, frag_tile<MT, GA>(tAt, 16 * mi, 32 * p), T1f[p]);
+          if (32 * p + 31 >= 16 * mi) mma(dL, frag_tr(tA, CP, 32 * p, 16 * mi), T1f[p]);
       }
       const f4 rk4 = *reinterpret_cast<const f4*>(rk + r0), b4 = *reinterpret_cast<const f4*>(cs.beta + r0);
       float zt[4];
@@ -1539,7 +1444,7 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
       f4 y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int p = 0; p < 2; ++p)
-        if (32 * p + 31 >= 16 * ti) mma(y, fdv[p], frag_tile<MT, GA>(tAt, 16 * ti, 32 * p));
+        if (32 * p + 31 >= 16 * ti) mma(y, fdv[p], frag_tr(tA, CP, 32 * p, 16 * ti));
       const int t = 16 * ti + n;
       const float bt = cs.beta[t];
       *reinterpret_cast<bf16x4*>(tVn + t * VP + c0) = bf16x4{(bf16)(bt * y[0]), (bf16)(bt * y[1]), (bf16)(bt * y[2]),
@@ -1786,21 +1691,18 @@ const char* macai_gdr_last_error(void) { return g_err; }
 int macai_gdr_abi_version(void) { return MACAI_GDR_ABI_VERSION; }
 
 int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, const float* beta, void* W, float* U,
-                   void* KeT, float* GL, void* Qg, void* M, void* Ke, void* QgT, void* WT, void* Mt, void* A, void* At,
-                   int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm,
-                   float q_scale, void* stream) {
+                   void* Ke, float* GL, void* Qg, void* M, void* A, int64_t B, int64_t T, int64_t H, int64_t DK,
+                   int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, void* stream) {
   const char* what = "macai_gdr_prep";
   int rc = check_common(what, B, T, H, DK, DV, dtype);
   if (rc) return rc;
-  if (!k || !v || !g || !beta || !W || !U || !KeT || !GL)
+  if (!q || !k || !v || !g || !beta || !W || !U || !Ke || !GL || !Qg || !M)
     return fail(MACAI_GDR_EINVAL, "%s: null input or output pointer", what);
-  if ((Qg || M || QgT || Mt) && !q) return fail(MACAI_GDR_EINVAL, "%s: Qg, M, QgT and Mt need q", what);
-  if ((A == nullptr) != (At == nullptr)) return fail(MACAI_GDR_EINVAL, "%s: A and At go together", what);
-  const void* ps[] = {q, k, v, W, U, KeT, Qg, M, Ke, QgT, WT, Mt, A, At};
+  const void* ps[] = {q, k, v, W, U, Ke, Qg, M, A};
   for (const void* p : ps)
     if (!aligned16(p)) return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
-  PrepArgs a{q, k, v, g, beta, W, U, KeT, GL, Qg, M, Ke, QgT, WT, Mt, A, At, (int)B, (int)T, (int)H, (int)DV,
-             (int)((T + C - 1) / C), use_l2norm, q_scale};
+  PrepArgs a{q, k, v, g, beta, W, U, Ke, GL, Qg, M, A, (int)B, (int)T, (int)H, (int)DV, (int)((T + C - 1) / C),
+             use_l2norm, q_scale};
   dim3 grid(a.NT, (unsigned)H, (unsigned)B);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == MACAI_GDR_F32) {
@@ -1819,7 +1721,7 @@ int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, 
     default: { constexpr int NWC = 8; __VA_ARGS__; } break;   \
   }
 
-int macai_gdr_state_fwd(const void* W, const float* U, const void* KeT, const float* GL, const void* Qg, const void* M,
+int macai_gdr_state_fwd(const void* W, const float* U, const void* Ke, const float* GL, const void* Qg, const void* M,
                         const float* s0, void* o, float* sT, float* Sc, void* Vn, int64_t B, int64_t T, int64_t H,
                         int64_t DK, int64_t DV, int32_t dtype, int32_t flags, int32_t split, void* stream) {
   const char* what = "macai_gdr_state_fwd";
@@ -1828,15 +1730,15 @@ int macai_gdr_state_fwd(const void* W, const float* U, const void* KeT, const fl
   const bool store = flags & MACAI_GDR_STORE_STATES, out = !(flags & MACAI_GDR_NO_OUTPUT);
   if (out == store)
     return fail(MACAI_GDR_EINVAL, "%s: flags must be 0 (output) or STORE_STATES | NO_OUTPUT (recompute)", what);
-  if (!W || !U || !KeT || !GL) return fail(MACAI_GDR_EINVAL, "%s: null input pointer", what);
+  if (!W || !U || !Ke || !GL) return fail(MACAI_GDR_EINVAL, "%s: null input pointer", what);
   if (out && (!Qg || !M || !o)) return fail(MACAI_GDR_EINVAL, "%s: the output needs Qg, M and o", what);
   if (store && (!Sc || !Vn)) return fail(MACAI_GDR_EINVAL, "%s: storing states needs Sc and Vn", what);
-  const void* ps[] = {W, U, KeT, Qg, M, s0, sT, Sc, Vn};
+  const void* ps[] = {W, U, Ke, Qg, M, s0, sT, Sc, Vn};
   for (const void* p : ps)
     if (!aligned16(p)) return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
   int nw, nslice;
   if ((rc = pick_waves(DV, split, what, &nw, &nslice))) return rc;
-  StateFwdArgs a{W, U, KeT, GL, Qg, M, s0, o, out ? sT : nullptr, Sc, Vn, (int)B, (int)T, (int)H, (int)DV,
+  StateFwdArgs a{W, U, Ke, GL, Qg, M, s0, o, out ? sT : nullptr, Sc, Vn, (int)B, (int)T, (int)H, (int)DV,
                  (int)((T + C - 1) / C), nslice};
   const int HR = (int)(B * H);
   dim3 grid((unsigned)(8 * nslice * ((HR + 7) / 8)));
@@ -1855,20 +1757,20 @@ int macai_gdr_state_fwd(const void* W, const float* U, const void* KeT, const fl
   return launched(what);
 }
 
-int macai_gdr_state_bwd(const void* Ke, const void* QgT, const void* WT, const void* Mt, const float* GL,
+int macai_gdr_state_bwd(const void* Ke, const void* Qg, const void* W, const void* M, const float* GL,
                         const void* dO, const float* dsT, float* dSn, void* dVn, float* ds0, int64_t B, int64_t T,
                         int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t split, void* stream) {
   const char* what = "macai_gdr_state_bwd";
   int rc = check_common(what, B, T, H, DK, DV, dtype);
   if (rc) return rc;
-  if (!Ke || !QgT || !WT || !Mt || !GL || !dO || !dSn || !dVn || !ds0)
+  if (!Ke || !Qg || !W || !M || !GL || !dO || !dSn || !dVn || !ds0)
     return fail(MACAI_GDR_EINVAL, "%s: null pointer", what);
-  const void* ps[] = {Ke, QgT, WT, Mt, dO, dsT, dSn, dVn, ds0};
+  const void* ps[] = {Ke, Qg, W, M, dO, dsT, dSn, dVn, ds0};
   for (const void* p : ps)
     if (!aligned16(p)) return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
   int nw, nslice;
   if ((rc = pick_waves(DV, split, what, &nw, &nslice))) return rc;
-  StateBwdArgs a{Ke, QgT, WT, Mt, GL, dO, dsT, dSn, dVn, ds0, (int)B, (int)T, (int)H, (int)DV, (int)((T + C - 1) / C),
+  StateBwdArgs a{Ke, Qg, W, M, GL, dO, dsT, dSn, dVn, ds0, (int)B, (int)T, (int)H, (int)DV, (int)((T + C - 1) / C),
                  nslice};
   const int HR = (int)(B * H);
   dim3 grid((unsigned)(8 * nslice * ((HR + 7) / 8)));
@@ -1883,7 +1785,7 @@ int macai_gdr_state_bwd(const void* Ke, const void* QgT, const void* WT, const v
 }
 
 int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float* g, const float* beta, const void* dO,
-                        const void* A, const void* At, const float* Sc, const float* dSn, const void* Vn,
+                        const void* A, const float* Sc, const float* dSn, const void* Vn,
                         const void* dVn, void* dq, void* dk, void* dv, float* dg, float* dbeta, int64_t B, int64_t T,
                         int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale,
                         void* stream) {
@@ -1893,13 +1795,13 @@ int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float
   if (DV != 32 && DV != 64 && DV != 96 && DV != 128)
     return fail(MACAI_GDR_EUNSUP, "%s: the backward takes value head widths 32, 64, 96 or 128 (got %lld)", what,
                 (long long)DV);
-  if (!q || !k || !v || !g || !beta || !dO || !A || !At || !Sc || !dSn || !Vn || !dVn || !dq || !dk || !dv || !dg ||
+  if (!q || !k || !v || !g || !beta || !dO || !A || !Sc || !dSn || !Vn || !dVn || !dq || !dk || !dv || !dg ||
       !dbeta)
     return fail(MACAI_GDR_EINVAL, "%s: null pointer", what);
-  const void* ps[] = {q, k, v, dO, A, At, Sc, dSn, Vn, dVn};
+  const void* ps[] = {q, k, v, dO, A, Sc, dSn, Vn, dVn};
   for (const void* p : ps)
     if (!aligned16(p)) return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
-  ChunkBwdArgs a{q, k, v, g, beta, dO, A, At, Sc, dSn, Vn, dVn, dq, dk, dv, dg, dbeta, (int)B, (int)T, (int)H,
+  ChunkBwdArgs a{q, k, v, g, beta, dO, A, Sc, dSn, Vn, dVn, dq, dk, dv, dg, dbeta, (int)B, (int)T, (int)H,
                  (int)DV, (int)((T + C - 1) / C), use_l2norm, q_scale};
   dim3 grid(a.NT, (unsigned)H, (unsigned)B);
   hipStream_t st = (hipStream_t)stream;

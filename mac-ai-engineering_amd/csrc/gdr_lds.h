@@ -112,6 +112,13 @@ __device__ __forceinline__ Frag<bf16> frag_tr(const bf16* X, int pitch, int k0, 
   f.v = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   return f;
 }
+// The fragment of X^T for a row-major tile X of layout G: k over X's rows k0.., the lane's column n0 + l % 16.  LDS
+// transpose reads for bf16; element gathers for fp32 (no transpose read exists for 32-bit data).
+template <typename MT, typename G>
+__device__ __forceinline__ Frag<MT> frag_tile_tr(const MT* base, int k0, int n0) {
+  if constexpr (sizeof(MT) == 2) return frag_tr(base, G::PITCH, k0, n0);
+  else return frag_tile_rows<MT, G>(base, k0, n0 + (lane_id() & 15));
+}
 // The accumulator layout of a 16 x 16 block of a row-major bf16 matrix X: lane l gets X[r0 + 4j + e][c0 + l % 16],
 // e = 0..3, as floats.  One transpose read.
 __device__ __forceinline__ f4 acc_tr(const bf16* X, int pitch, int r0, int c0) {

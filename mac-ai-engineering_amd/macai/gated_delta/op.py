@@ -65,64 +65,62 @@ def _dims(q, v):
     return B, T, H, DK, v.shape[-1], math.ceil(T / CHUNK)
 
 
+def _prep(q, k, v, g, beta, l2norm: bool, q_scale: float, with_A: bool):
+    """The per-chunk operands (row-major, tokens as rows): W, U, diag(e) K^, exp(G_last), diag(gamma) Q^, M, and A when
+    asked (the backward's per-chunk pass)."""
+    B, T, H, DK, DV, NT = _dims(q, v)
+    dev, dt = q.device, q.dtype
+    f32 = torch.float32
+    W = torch.empty(B, H, NT, CHUNK, DK, device=dev, dtype=dt)
+    r = dict(W=W, U=torch.empty(B, H, NT, CHUNK, DV, device=dev, dtype=f32), Ke=torch.empty_like(W),
+             GL=torch.empty(B, H, NT, device=dev, dtype=f32), Qg=torch.empty_like(W),
+             M=torch.empty(B, H, NT, CHUNK, CHUNK, device=dev, dtype=dt),
+             A=torch.empty(B, H, NT, CHUNK, CHUNK, device=dev, dtype=dt) if with_A else None)
+    P = N.ptr
+    N.call("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(r["W"]), P(r["U"]), P(r["Ke"]), P(r["GL"]), P(r["Qg"]),
+           P(r["M"]), P(r["A"]), B, T, H, DK, DV, N.dtype_code(dt), int(l2norm), q_scale, N.stream_of(q))
+    return r
+
+
 def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool):
-    """prep (W, U, (diag(e) K^)^T, exp(G_last), diag(gamma) Q^, M) then the state pass with the output: returns (o in
-    q's dtype, sT or None)."""
+    """prep, then the state pass with the output: returns (o in q's dtype, sT or None)."""
     B, T, H, DK, DV, NT = _dims(q, v)
     dev, dt = q.device, q.dtype
     code, stream = N.dtype_code(dt), N.stream_of(q)
-    f32 = torch.float32
-    W = torch.empty(B, H, NT, CHUNK, DK, device=dev, dtype=dt)
-    U = torch.empty(B, H, NT, CHUNK, DV, device=dev, dtype=f32)
-    KeT = torch.empty(B, H, NT, DK, CHUNK, device=dev, dtype=dt)
-    GL = torch.empty(B, H, NT, device=dev, dtype=f32)
-    Qg = torch.empty_like(W)
-    M = torch.empty(B, H, NT, CHUNK, CHUNK, device=dev, dtype=dt)
-    P = N.ptr
-    N.call("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), P(KeT), P(GL), P(Qg), P(M), None, None, None,
-           None, None, None, B, T, H, DK, DV, code, int(l2norm), q_scale, stream)
+    r = _prep(q, k, v, g, beta, l2norm, q_scale, False)
     o = torch.empty(B, T, H, DV, device=dev, dtype=dt)
-    sT = torch.empty(B, H, DK, DV, device=dev, dtype=f32) if want_sT else None
+    sT = torch.empty(B, H, DK, DV, device=dev, dtype=torch.float32) if want_sT else None
     split = split_for(B * H, T, DV)
-    N.call("macai_gdr_state_fwd", P(W), P(U), P(KeT), P(GL), P(Qg), P(M), P(s0), P(o), P(sT), None, None,
-           B, T, H, DK, DV, code, 0, split, stream)
+    P = N.ptr
+    N.call("macai_gdr_state_fwd", P(r["W"]), P(r["U"]), P(r["Ke"]), P(r["GL"]), P(r["Qg"]), P(r["M"]), P(s0), P(o),
+           P(sT), None, None, B, T, H, DK, DV, code, 0, split, stream)
     CALLS[f"fwd s{split}"] += 1
     return o, sT
 
 
 def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float):
-    """Recompute (prep with the backward's operands; the state pass storing S_c and Vn), the reverse state pass, the
-    per-chunk backward.  Returns (dq, dk, dv in q's dtype; dg, dbeta, ds0 float32)."""
+    """Recompute (prep; the state pass storing S_c and Vn), the reverse state pass, the per-chunk backward.  Returns
+    (dq, dk, dv in q's dtype; dg, dbeta, ds0 float32)."""
     B, T, H, DK, DV, NT = _dims(q, v)
     dev, dt = q.device, q.dtype
     code, stream = N.dtype_code(dt), N.stream_of(q)
     f32 = torch.float32
-    W = torch.empty(B, H, NT, CHUNK, DK, device=dev, dtype=dt)
-    U = torch.empty(B, H, NT, CHUNK, DV, device=dev, dtype=f32)
-    KeT = torch.empty(B, H, NT, DK, CHUNK, device=dev, dtype=dt)
-    GL = torch.empty(B, H, NT, device=dev, dtype=f32)
-    Ke = torch.empty_like(W)
-    QgT, WT = torch.empty_like(KeT), torch.empty_like(KeT)
-    Mt = torch.empty(B, H, NT, CHUNK, CHUNK, device=dev, dtype=dt)
-    A = torch.empty(B, H, NT, CHUNK, CHUNK, device=dev, dtype=dt)
-    At = torch.empty_like(A)
-    P = N.ptr
-    N.call("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), P(KeT), P(GL), None, None, P(Ke), P(QgT),
-           P(WT), P(Mt), P(A), P(At), B, T, H, DK, DV, code, int(l2norm), q_scale, stream)
+    r = _prep(q, k, v, g, beta, l2norm, q_scale, True)
     split = split_for(B * H, T, DV)
+    P = N.ptr
     Sc = torch.empty(B, H, NT, DK, DV, device=dev, dtype=f32)
     Vn = torch.empty(B, H, NT, CHUNK, DV, device=dev, dtype=dt)
-    N.call("macai_gdr_state_fwd", P(W), P(U), P(KeT), P(GL), None, None, P(s0), None, None, P(Sc), P(Vn),
-           B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, stream)
+    N.call("macai_gdr_state_fwd", P(r["W"]), P(r["U"]), P(r["Ke"]), P(r["GL"]), None, None, P(s0), None, None, P(Sc),
+           P(Vn), B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, stream)
     dSn = torch.empty(B, H, NT, DK, DV, device=dev, dtype=f32)
     dVn = torch.empty_like(Vn)
     ds0 = torch.empty(B, H, DK, DV, device=dev, dtype=f32)
-    N.call("macai_gdr_state_bwd", P(Ke), P(QgT), P(WT), P(Mt), P(GL), P(do), P(dsT), P(dSn), P(dVn), P(ds0),
-           B, T, H, DK, DV, code, split, stream)
+    N.call("macai_gdr_state_bwd", P(r["Ke"]), P(r["Qg"]), P(r["W"]), P(r["M"]), P(r["GL"]), P(do), P(dsT), P(dSn),
+           P(dVn), P(ds0), B, T, H, DK, DV, code, split, stream)
     CALLS[f"bwd s{split}"] += 1
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     dg, dbeta = torch.empty_like(g), torch.empty_like(beta)
-    N.call("macai_gdr_chunk_bwd", P(q), P(k), P(v), P(g), P(beta), P(do), P(A), P(At), P(Sc), P(dSn), P(Vn), P(dVn),
+    N.call("macai_gdr_chunk_bwd", P(q), P(k), P(v), P(g), P(beta), P(do), P(r["A"]), P(Sc), P(dSn), P(Vn), P(dVn),
            P(dq), P(dk), P(dv), P(dg), P(dbeta), B, T, H, DK, DV, code, int(l2norm), q_scale, stream)
     return dq, dk, dv, dg, dbeta, ds0
 

@@ -22,31 +22,31 @@ def passes(q, k, v, g, beta, s0, do, dsT, l2norm=False, q_scale=1.0, split=0):
     r = {}
     e = lambda *s, d=f32: torch.full(s, float("nan"), device=dev, dtype=d)
     # forward-mode prep, then the output pass
-    r["W"], r["U"], r["KeT"], r["GL"] = e(B, H, NT, C, DK, d=dt), e(B, H, NT, C, DV), e(B, H, NT, DK, C, d=dt), e(B, H, NT)
-    r["Qg"], r["M"] = e(B, H, NT, C, DK, d=dt), e(B, H, NT, C, C, d=dt)
-    N.call("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(r["W"]), P(r["U"]), P(r["KeT"]), P(r["GL"]),
-           P(r["Qg"]), P(r["M"]), None, None, None, None, None, None, B, T, H, DK, DV, code, int(l2norm), q_scale, st)
+    for n_, shape, d in (("W", (B, H, NT, C, DK), dt), ("U", (B, H, NT, C, DV), f32), ("Ke", (B, H, NT, C, DK), dt),
+                         ("GL", (B, H, NT), f32), ("Qg", (B, H, NT, C, DK), dt), ("M", (B, H, NT, C, C), dt)):
+        r[n_] = e(*shape, d=d)
+    N.call("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(r["W"]), P(r["U"]), P(r["Ke"]), P(r["GL"]),
+           P(r["Qg"]), P(r["M"]), None, B, T, H, DK, DV, code, int(l2norm), q_scale, st)
     r["o"], r["sT"] = e(B, T, H, DV, d=dt), e(B, H, DK, DV)
-    N.call("macai_gdr_state_fwd", P(r["W"]), P(r["U"]), P(r["KeT"]), P(r["GL"]), P(r["Qg"]), P(r["M"]), P(s0),
+    N.call("macai_gdr_state_fwd", P(r["W"]), P(r["U"]), P(r["Ke"]), P(r["GL"]), P(r["Qg"]), P(r["M"]), P(s0),
            P(r["o"]), P(r["sT"]), None, None, B, T, H, DK, DV, code, 0, split, st)
-    # backward-mode prep, recompute, reverse pass, per-chunk backward
-    W2, U2, KeT2, GL2 = e(B, H, NT, C, DK, d=dt), e(B, H, NT, C, DV), e(B, H, NT, DK, C, d=dt), e(B, H, NT)
-    r["Ke"], r["QgT"], r["WT"] = e(B, H, NT, C, DK, d=dt), e(B, H, NT, DK, C, d=dt), e(B, H, NT, DK, C, d=dt)
-    r["Mt"], r["A"], r["At"] = e(B, H, NT, C, C, d=dt), e(B, H, NT, C, C, d=dt), e(B, H, NT, C, C, d=dt)
-    N.call("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W2), P(U2), P(KeT2), P(GL2), None, None, P(r["Ke"]),
-           P(r["QgT"]), P(r["WT"]), P(r["Mt"]), P(r["A"]), P(r["At"]), B, T, H, DK, DV, code, int(l2norm), q_scale, st)
+    # backward-mode prep (adds A), recompute, reverse pass, per-chunk backward
+    b2 = {n_: e(*x.shape, d=x.dtype) for n_, x in r.items() if n_ in ("W", "U", "Ke", "GL", "Qg", "M")}
+    r["A"] = e(B, H, NT, C, C, d=dt)
+    N.call("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(b2["W"]), P(b2["U"]), P(b2["Ke"]), P(b2["GL"]),
+           P(b2["Qg"]), P(b2["M"]), P(r["A"]), B, T, H, DK, DV, code, int(l2norm), q_scale, st)
     r["Sc"], r["Vn"] = e(B, H, NT, DK, DV), e(B, H, NT, C, DV, d=dt)
-    N.call("macai_gdr_state_fwd", P(W2), P(U2), P(KeT2), P(GL2), None, None, P(s0), None, None, P(r["Sc"]),
-           P(r["Vn"]), B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, st)
+    N.call("macai_gdr_state_fwd", P(b2["W"]), P(b2["U"]), P(b2["Ke"]), P(b2["GL"]), None, None, P(s0), None, None,
+           P(r["Sc"]), P(r["Vn"]), B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, st)
     r["dSn"], r["dVn"], r["ds0"] = e(B, H, NT, DK, DV), e(B, H, NT, C, DV, d=dt), e(B, H, DK, DV)
-    N.call("macai_gdr_state_bwd", P(r["Ke"]), P(r["QgT"]), P(r["WT"]), P(r["Mt"]), P(GL2), P(do), P(dsT),
+    N.call("macai_gdr_state_bwd", P(b2["Ke"]), P(b2["Qg"]), P(b2["W"]), P(b2["M"]), P(b2["GL"]), P(do), P(dsT),
            P(r["dSn"]), P(r["dVn"]), P(r["ds0"]), B, T, H, DK, DV, code, split, st)
     r["dq"], r["dk"], r["dv"] = e(B, T, H, DK, d=dt), e(B, T, H, DK, d=dt), e(B, T, H, DV, d=dt)
     r["dg"], r["dbeta"] = e(B, T, H), e(B, T, H)
-    N.call("macai_gdr_chunk_bwd", P(q), P(k), P(v), P(g), P(beta), P(do), P(r["A"]), P(r["At"]), P(r["Sc"]),
-           P(r["dSn"]), P(r["Vn"]), P(r["dVn"]), P(r["dq"]), P(r["dk"]), P(r["dv"]), P(r["dg"]), P(r["dbeta"]),
+    N.call("macai_gdr_chunk_bwd", P(q), P(k), P(v), P(g), P(beta), P(do), P(r["A"]), P(r["Sc"]), P(r["dSn"]),
+           P(r["Vn"]), P(r["dVn"]), P(r["dq"]), P(r["dk"]), P(r["dv"]), P(r["dg"]), P(r["dbeta"]),
            B, T, H, DK, DV, code, int(l2norm), q_scale, st)
     torch.cuda.synchronize()
     out = {k_: x.cpu() for k_, x in r.items()}
-    out["W2_equal"] = torch.equal(W2.cpu(), out["W"]) and torch.equal(KeT2.cpu(), out["KeT"])
+    out["W2_equal"] = all(torch.equal(b2[n_].cpu(), out[n_]) for n_ in b2)
     return out

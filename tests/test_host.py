@@ -39,8 +39,8 @@ def test_library_exports_every_declared_symbol():
 
 def _prep(**over):
     p = 1 << 20
-    a = dict(q=p, k=p, v=p, g=p, beta=p, W=p, U=p, KeT=p, GL=p, Qg=None, M=None, Ke=None, QgT=None, WT=None, Mt=None,
-             A=None, At=None, B=1, T=64, H=1, DK=128, DV=128, dtype=1, l2=1, scale=1.0, stream=None)
+    a = dict(q=p, k=p, v=p, g=p, beta=p, W=p, U=p, Ke=p, GL=p, Qg=p, M=p, A=None, B=1, T=64, H=1, DK=128, DV=128,
+             dtype=1, l2=1, scale=1.0, stream=None)
     a.update(over)
     return N.lib().macai_gdr_prep(*a.values())
 
@@ -52,10 +52,11 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert _prep(dtype=7) == N.EUNSUP
     assert _prep(T=0) == N.EINVAL
     assert _prep(k=None) == N.EINVAL and b"null" in L.macai_gdr_last_error()
-    assert _prep(KeT=None) == N.EINVAL
-    assert _prep(A=1 << 20) == N.EINVAL and b"A and At" in L.macai_gdr_last_error()
+    assert _prep(Ke=None) == N.EINVAL
+    assert _prep(M=None) == N.EINVAL
     assert _prep(W=(1 << 20) + 4) == N.EINVAL and b"aligned" in L.macai_gdr_last_error()
-    assert _prep(M=1 << 20, q=None) == N.EINVAL
+    assert _prep(A=(1 << 20) + 8) == N.EINVAL and b"aligned" in L.macai_gdr_last_error()
+    assert _prep(q=None) == N.EINVAL
     p = 1 << 20
     sf = lambda *ptrs, flags=0, split=0, DV=128: L.macai_gdr_state_fwd(*ptrs, 1, 64, 1, 128, DV, 1, flags, split, None)
     # flags that ask for nothing or both, a split that does not divide DV / 16, a missing output operand
@@ -65,15 +66,15 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert sf(p, p, p, p, p, p, None, p, None, None, None, split=1, DV=96) == N.EINVAL
     assert sf(p, p, p, p, p, None, None, p, None, None, None) == N.EINVAL
     assert L.macai_gdr_state_bwd(p, p, p, p, p, None, None, p, p, p, 1, 64, 1, 128, 128, 1, 0, None) == N.EINVAL
-    assert L.macai_gdr_chunk_bwd(*([p] * 16), None, 1, 64, 1, 128, 128, 1, 1, 1.0, None) == N.EINVAL
+    assert L.macai_gdr_chunk_bwd(*([p] * 15), None, 1, 64, 1, 128, 128, 1, 1, 1.0, None) == N.EINVAL
     assert L.macai_gdr_decode(p, p, p, p, p, p, p, p, 1, 1, 256, 128, 1, 1, 1.0, None) == N.EUNSUP
 
 
 def test_call_maps_codes_to_exceptions():
     with pytest.raises(NotImplementedError, match="key head width"):
-        N.call("macai_gdr_prep", *([1 << 20] * 9), *([None] * 8), 1, 64, 1, 96, 128, 1, 1, 1.0, None)
+        N.call("macai_gdr_prep", *([1 << 20] * 11), None, 1, 64, 1, 96, 128, 1, 1, 1.0, None)
     with pytest.raises(ValueError, match="null"):
-        N.call("macai_gdr_prep", *([None] * 17), 1, 64, 1, 128, 128, 1, 1, 1.0, None)
+        N.call("macai_gdr_prep", *([None] * 12), 1, 64, 1, 128, 128, 1, 1, 1.0, None)
 
 
 def test_packed_rows_refused():
