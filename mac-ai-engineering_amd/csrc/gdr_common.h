@@ -181,7 +181,7 @@ __device__ __forceinline__ float across_groups_sum(float x) {
 // scanned in double: under strong decay |G| reaches ~1e3 within a chunk, where one fp32 ulp (6e-5) would become a
 // relative error of exp(G_i - G_j) -- the decays are formed from the double differences.  G_last is G of the last
 // valid row exactly (padding rows copy it), so e = exp(G_last - G) is exactly 1 on that row.
-struct ChunkScalars {
+struct __attribute__((aligned(16))) ChunkScalars {   // 16-byte aligned: rows are read 4 at a time
   double G[C];
   float gam[C];    // exp(G_r)
   float e[C];      // exp(G_last - G_r)

@@ -301,6 +301,264 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------------------------------
+// prep for bf16 operands: 8 waves, the chunk's raw q, k, v in LDS
+// ---------------------------------------------------------------------------------------------------------------------
+// One workgroup of 8 waves per (chunk, head, batch row).  The raw q, k and v rows are copied into padded LDS tiles
+// (asynchronous; the row norms and chunk scalars are computed meanwhile), so every product reads raw bf16 operands and
+// the prologue's scales are applied in fp32 to the products: L and M from q k^T and k k^T, W = (A diag(beta gamma rk)) k
+// and U = (A diag(beta)) v, formed transposed (tokens as the MFMA columns) with k and v read by LDS transpose reads.
+// The inverse is the same substitution + block products as prep_kernel.  Every output is staged in LDS and written as
+// whole rows.  VB = value columns per pass (DV is a multiple of it).
+template <int DK, int VB>
+__global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
+  using MT = bf16;
+  constexpr int NW = 8, KP = DK + 8, CP = C + 8, FP = C + 4, UP = VB + 4;
+  constexpr int NBD = DK / 16, NBV = VB / 16;
+  using GQ = Tile<MT, C, DK>;
+  using GV = Tile<MT, C, VB>;
+  static_assert(GQ::PITCH == KP && NBD <= NW && NBV <= NW, "prep8 tiling");
+  constexpr int VP = GV::PITCH;
+  __shared__ __attribute__((aligned(16))) MT tq[GQ::ELEMS];
+  __shared__ __attribute__((aligned(16))) MT tk[GQ::ELEMS];
+  __shared__ __attribute__((aligned(16))) MT tv[GV::ELEMS];
+  __shared__ __attribute__((aligned(16))) float sL[C * FP];
+  __shared__ __attribute__((aligned(16))) float sA[C * FP];
+  constexpr int STAGE = (C * UP > C * KP / 2) ? C * UP : C * KP / 2;   // floats: U (fp32), W or M (bf16)
+  __shared__ __attribute__((aligned(16))) float stage[STAGE];
+  __shared__ ChunkScalars cs;
+  __shared__ __attribute__((aligned(16))) float rk[C], rq[C], fW[C], fU[C];
+
+  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int T = a.T, H = a.H, DV = a.DV, NT = a.NT;
+  const int t0 = c * C, nrows = (T - t0 < C) ? T - t0 : C;
+  const int l = lane_id(), w = wave_id(), j = l >> 4, n = l & 15;
+  const size_t qk_base = ((size_t)b * T * H + h) * DK, qk_pitch = (size_t)H * DK;
+  const size_t v_base = ((size_t)b * T * H + h) * DV, v_pitch = (size_t)H * DV;
+  const size_t s_base = (size_t)b * T * H + h;
+  const size_t bhc = ((size_t)b * H + h) * NT + c;
+  const MT* q = (const MT*)a.q + qk_base;
+  const MT* k = (const MT*)a.k + qk_base;
+  const MT* v = (const MT*)a.v + v_base;
+  const float qs = a.q_scale;
+  MT* const stb = reinterpret_cast<MT*>(stage);
+
+  // ---- 0: tiles in flight; scalars and norms meanwhile
+  GQ::dma(tq, q + (size_t)t0 * qk_pitch, qk_pitch, w, NW, nrows);
+  GQ::dma(tk, k + (size_t)t0 * qk_pitch, qk_pitch, w, NW, nrows);
+  GV::dma(tv, v + (size_t)t0 * v_pitch, v_pitch, w, NW, nrows);
+  if (w == 0) chunk_scalars(cs, a.g, a.beta, s_base, H, t0, T);
+  if (a.l2norm) {
+    if (w >= 4 && w < 6) row_rnorms<MT, DK>(rk, k - qk_base, qk_base, qk_pitch, t0, T, 2, w - 4);
+    if (w >= 6) row_rnorms<MT, DK>(rq, q - qk_base, qk_base, qk_pitch, t0, T, 2, w - 6);
+  } else if (threadIdx.x < C) {
+    rk[threadIdx.x] = 1.f;
+    rq[threadIdx.x] = 1.f;
+  }
+  wait_dma();
+  __syncthreads();
+  if (nrows < C) {                         // rows past the end: zeros in q, k and v
+    constexpr int UQ = KP / 8, UV = VP / 8;
+    const int nz = C - nrows;
+    for (int i = threadIdx.x; i < nz * (2 * UQ + UV); i += blockDim.x) {
+      const int row = nrows + i % nz, u = i / nz;
+      MT* p = u < UQ ? tq + row * KP + 8 * u : u < 2 * UQ ? tk + row * KP + 8 * (u - UQ) : tv + row * VP + 8 * (u - 2 * UQ);
+      *reinterpret_cast<bf16x8*>(p) = bf16x8{};
+    }
+  }
+  if (threadIdx.x < C) {
+    const int s = threadIdx.x;
+    fW[s] = cs.beta[s] * cs.gam[s] * rk[s];
+    fU[s] = cs.beta[s];
+  }
+  if (threadIdx.x == 0) a.GL[bhc] = cs.gam[C - 1];
+  __syncthreads();
+
+  // ---- 1a: diag(e) K^ and diag(gamma) Q^ rows out (16 bytes a lane)
+  {
+    constexpr int UQ = DK / 8;
+    MT* Ke = (MT*)a.Ke + bhc * C * DK;
+    MT* Qg = (MT*)a.Qg + bhc * C * DK;
+    for (int i = threadIdx.x; i < C * UQ; i += blockDim.x) {
+      const int t = i / UQ, u = i - t * UQ;
+      const float fk = rk[t] * cs.e[t], fq = rq[t] * qs * cs.gam[t];
+      const bf16x8 xk = *reinterpret_cast<const bf16x8*>(tk + t * KP + 8 * u);
+      const bf16x8 xq = *reinterpret_cast<const bf16x8*>(tq + t * KP + 8 * u);
+      bf16x8 ok, oq;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        ok[e] = (bf16)((float)xk[e] * fk);
+        oq[e] = (bf16)((float)xq[e] * fq);
+      }
+      *reinterpret_cast<bf16x8*>(Ke + t * DK + 8 * u) = ok;
+      *reinterpret_cast<bf16x8*>(Qg + t * DK + 8 * u) = oq;
+    }
+  }
+  // ---- 1b: k k^T and q k^T on this wave's tiles (column block cb, row tiles 2 hh, 2 hh + 1): L into LDS, M staged
+  {
+    const int cb = w & 3, hh = w >> 2;
+    f4 KK[2], QK[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) KK[i] = QK[i] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < DK / 32; ++p) {
+      const Frag<MT> bk = frag_tile<MT, GQ>(tk, 16 * cb, 32 * p);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int mi = 2 * hh + i;
+        if (mi < cb) continue;
+        mma(KK[i], frag_tile<MT, GQ>(tk, 16 * mi, 32 * p), bk);
+        mma(QK[i], frag_tile<MT, GQ>(tq, 16 * mi, 32 * p), bk);
+      }
+    }
+    const int s = 16 * cb + n;
+    const float rks = rk[s];
+    const double Gs = cs.G[s];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r0 = 16 * (2 * hh + i) + 4 * j;
+      const f4 rq4 = *reinterpret_cast<const f4*>(rq + r0), rk4 = *reinterpret_cast<const f4*>(rk + r0);
+      const f4 b4 = *reinterpret_cast<const f4*>(cs.beta + r0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = r0 + r;
+        const float gm = (row >= s) ? expf((float)(cs.G[row] - Gs)) : 0.f;   // mask before the exponent
+        sL[row * FP + s] = (row > s) ? b4[r] * (KK[i][r] * (rk4[r] * rks)) * gm : 0.f;
+        stb[row * CP + s] = (bf16)((row >= s) ? QK[i][r] * (rq4[r] * qs * rks) * gm : 0.f);
+      }
+    }
+  }
+  __syncthreads();
+  // ---- 1c: M out; the diagonal 16 x 16 blocks of A = (I + L)^-1 by forward substitution (wave 0, lane = (block l / 16,
+  // column l % 16), column form: the same fmaf sequence per element as the row form), zeros above the diagonal blocks
+  {
+    MT* Mg = (MT*)a.M + bhc * C * C;
+    for (int i = threadIdx.x; i < C * (C / 8); i += blockDim.x) {
+      const int t = i >> 3, u = i & 7;
+      *reinterpret_cast<bf16x8*>(Mg + t * C + 8 * u) = *reinterpret_cast<const bf16x8*>(stb + t * CP + 8 * u);
+    }
+  }
+  if (w == 0) {
+    const int bb = l >> 4, cc = l & 15;
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = (i == cc) ? 1.f : 0.f;
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const float* Lc = sL + (16 * bb) * FP + 16 * bb + m;
+#pragma unroll
+      for (int i = m + 1; i < 16; ++i) x[i] = fmaf(-Lc[i * FP], x[m], x[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sA[(16 * bb + i) * FP + 16 * bb + cc] = x[i];
+  } else {
+    for (int i = threadIdx.x - 64; i < C * C; i += blockDim.x - 64) {
+      const int row = i / C, col = i % C;
+      if ((col >> 4) > (row >> 4)) sA[row * FP + col] = 0.f;
+    }
+  }
+  __syncthreads();
+  // ---- 2: blocks below the diagonal, one block-distance at a time: A_ij = -A_ii sum_{m=j}^{i-1} L_im A_mj (fp32 MFMA)
+  for (int dist = 1; dist < 4; ++dist) {
+    if (w < 4 - dist) {
+      const int bi = w + dist, bj = w;
+      f4 t = {0.f, 0.f, 0.f, 0.f};
+      for (int m = bj; m < bi; ++m) {
+#pragma unroll
+        for (int kk = 0; kk < 16; kk += 4)
+          t = __builtin_amdgcn_mfma_f32_16x16x4f32(sL[(16 * bi + (l & 15)) * FP + 16 * m + kk + j],
+                                                   sA[(16 * m + kk + j) * FP + 16 * bj + (l & 15)], t, 0, 0, 0);
+      }
+      f4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        o = __builtin_amdgcn_mfma_f32_16x16x4f32(sA[(16 * bi + (l & 15)) * FP + 16 * bi + 4 * j + r], t[r], o, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sA[(16 * bi + 4 * j + r) * FP + 16 * bj + (l & 15)] = -o[r];
+    }
+    __syncthreads();
+  }
+
+  // ---- 3: A out; W^T = k^T (A diag(beta gamma rk))^T staged and written
+  if (a.A) {
+    MT* Ag = (MT*)a.A + bhc * C * C;
+    const int t = threadIdx.x >> 3, u = threadIdx.x & 7;     // 512 threads = 64 rows x 8 units
+    const f4 lo = *reinterpret_cast<const f4*>(sA + t * FP + 8 * u), hi = *reinterpret_cast<const f4*>(sA + t * FP + 8 * u + 4);
+    *reinterpret_cast<bf16x8*>(Ag + t * C + 8 * u) =
+        bf16x8{(bf16)lo[0], (bf16)lo[1], (bf16)lo[2], (bf16)lo[3], (bf16)hi[0], (bf16)hi[1], (bf16)hi[2], (bf16)hi[3]};
+  }
+  // B operand (A diag(f))^T, k = s: lane's token t = 16 ti + l % 16, slots s = 32 p + kmap(j, .)
+  auto fragAf = [&](int ti, int p, const float* f) -> Frag<MT> {
+    const int t = 16 * ti + n, s0 = 32 * p + 4 * j;
+    const f4 a0 = *reinterpret_cast<const f4*>(sA + t * FP + s0), a1 = *reinterpret_cast<const f4*>(sA + t * FP + s0 + 16);
+    const f4 f0 = *reinterpret_cast<const f4*>(f + s0), f1 = *reinterpret_cast<const f4*>(f + s0 + 16);
+    Frag<MT> fr;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      fr.set(e, a0[e] * f0[e]);
+      fr.set(e + 4, a1[e] * f1[e]);
+    }
+    return fr;
+  };
+  if (w < NBD) {
+    Frag<MT> kT[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) kT[p] = frag_tr(tk, KP, 32 * p, 16 * w);
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) {
+      f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+        if (32 * p <= 16 * ti + 15) mma(acc, kT[p], fragAf(ti, p, fW));
+      const int t = 16 * ti + n;
+      *reinterpret_cast<bf16x4*>(stb + t * KP + 16 * w + 4 * j) = bf16x4{(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
+    }
+  }
+  __syncthreads();
+  {
+    constexpr int UQ = DK / 8;
+    MT* Wg = (MT*)a.W + bhc * C * DK;
+    for (int i = threadIdx.x; i < C * UQ; i += blockDim.x) {
+      const int t = i / UQ, u = i - t * UQ;
+      *reinterpret_cast<bf16x8*>(Wg + t * DK + 8 * u) = *reinterpret_cast<const bf16x8*>(stb + t * KP + 8 * u);
+    }
+  }
+  // ---- 4: U^T = v^T (A diag(beta))^T, VB value columns per pass, staged (fp32) and written
+  float* Ug = a.U + bhc * C * DV;
+  for (int vb = 0; vb < DV; vb += VB) {
+    if (vb > 0) {                          // the next block of v (the previous one is consumed)
+      GV::dma(tv, v + (size_t)t0 * v_pitch + vb, v_pitch, w, NW, nrows);
+      wait_dma();
+      __syncthreads();
+      if (nrows < C) {
+        constexpr int UV = VP / 8;
+        for (int i = threadIdx.x; i < (C - nrows) * UV; i += blockDim.x)
+          *reinterpret_cast<bf16x8*>(tv + (nrows + i / UV) * VP + 8 * (i % UV)) = bf16x8{};
+      }
+    }
+    __syncthreads();                       // W's (or the previous block's) copy-out has read the stage
+    if (w < NBV) {
+      Frag<MT> vT[2];
+#pragma unroll
+      for (int p = 0; p < 2; ++p) vT[p] = frag_tr(tv, VP, 32 * p, 16 * w);
+#pragma unroll
+      for (int ti = 0; ti < 4; ++ti) {
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+          if (32 * p <= 16 * ti + 15) mma(acc, vT[p], fragAf(ti, p, fU));
+        *reinterpret_cast<f4*>(stage + (16 * ti + n) * UP + 16 * w + 4 * j) = acc;
+      }
+    }
+    __syncthreads();
+    constexpr int UU = VB / 4;
+    for (int i = threadIdx.x; i < C * UU; i += blockDim.x) {
+      const int t = i / UU, u = i - t * UU;
+      *reinterpret_cast<f4*>(Ug + (size_t)t * DV + vb + 4 * u) = *reinterpret_cast<const f4*>(stage + t * UP + 4 * u);
+    }
+  }
+}
+
 // XCD-aware map of a flat workgroup id to (head-row, column slice): the slices of one head-row share an XCD (and its
 // L2), since consecutive workgroup ids go to consecutive XCDs.  Returns false for the padding workgroups.
 __device__ __forceinline__ bool state_map(int nslice, int HR, int& hr, int& slice) {
@@ -1707,6 +1965,13 @@ int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, 
   hipStream_t st = (hipStream_t)stream;
   if (dtype == MACAI_GDR_F32) {
     DISPATCH_DK(DK, hipLaunchKernelGGL((prep_kernel<float, float, DKC>), grid, dim3(256), 0, st, a));
+  } else if (DV <= 128 || DV % 128 == 0) {
+    DISPATCH_DK(DK, switch (DV) {
+      case 32: hipLaunchKernelGGL((prep8_kernel<DKC, 32>), grid, dim3(512), 0, st, a); break;
+      case 64: hipLaunchKernelGGL((prep8_kernel<DKC, 64>), grid, dim3(512), 0, st, a); break;
+      case 96: hipLaunchKernelGGL((prep8_kernel<DKC, 96>), grid, dim3(512), 0, st, a); break;
+      default: hipLaunchKernelGGL((prep8_kernel<DKC, 128>), grid, dim3(512), 0, st, a); break;
+    })
   } else {
     DISPATCH_DK(DK, hipLaunchKernelGGL((prep_kernel<bf16, bf16, DKC>), grid, dim3(256), 0, st, a));
   }
