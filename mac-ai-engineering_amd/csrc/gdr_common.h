@@ -246,6 +246,28 @@ __device__ __forceinline__ void row_rnorms(float* out, const IT* x, size_t row_b
   }
 }
 
+// row_rnorms over a bf16 tile already in LDS (rows < nrows; 0 past them), with row_rnorms' arithmetic -- the same
+// per-lane element order and butterfly -- so both give the same bits.
+template <int D>
+__device__ __forceinline__ void row_rnorms_lds(float* out, const bf16* tile, int pitch, int nrows, int nwaves, int w) {
+  const int l = lane_id();
+  constexpr int PER = D / 16;
+  for (int r0 = w * 4; r0 < C; r0 += 4 * nwaves) {
+    const int r = r0 + (l >> 4);
+    float ss = 0.f;
+    if (r < nrows) {
+      const bf16* p = tile + r * pitch + (l & 15) * PER;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const float v = (float)p[i];
+        ss = fmaf(v, v, ss);
+      }
+    }
+    ss = group16_sum(ss);
+    if ((l & 15) == 0) out[r] = (r < nrows) ? 1.0f / sqrtf(ss + L2_EPS) : 0.f;
+  }
+}
+
 // ---- global I/O helpers -------------------------------------------------------------------------------------------
 template <typename T> __device__ __forceinline__ void store(T* p, float x) { *p = from_f<T>(x); }
 

@@ -304,28 +304,29 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
 // ---------------------------------------------------------------------------------------------------------------------
 // prep for bf16 operands: 8 waves, the chunk's raw q, k, v in LDS
 // ---------------------------------------------------------------------------------------------------------------------
-// One workgroup of 8 waves per (chunk, head, batch row).  The raw q, k and v rows are copied into padded LDS tiles
-// (asynchronous; the row norms and chunk scalars are computed meanwhile), so every product reads raw bf16 operands and
-// the prologue's scales are applied in fp32 to the products: L and M from q k^T and k k^T, W = (A diag(beta gamma rk)) k
-// and U = (A diag(beta)) v, formed transposed (tokens as the MFMA columns) with k and v read by LDS transpose reads.
-// The inverse is the same substitution + block products as prep_kernel.  Every output is staged in LDS and written as
-// whole rows.  VB = value columns per pass (DV is a multiple of it).
+// One workgroup of 8 waves per (chunk, head, batch row), two workgroups per CU (under 80 KB of LDS: A reuses q's tile,
+// W is staged in L's), so one's copies and latencies overlap the other's work.  The raw q, k and v rows are copied into
+// padded LDS tiles (asynchronous; the chunk scalars are computed meanwhile), so every product reads raw bf16 operands
+// and the prologue's scales are applied in fp32 to the products: L and M from q k^T and k k^T, W = (A diag(beta gamma
+// rk)) k and U = (A diag(beta)) v, formed transposed (tokens as the MFMA columns) with k and v read by LDS transpose
+// reads.  The inverse is the same substitution + block products as prep_kernel.  Ke, Qg, M, A and W leave as whole
+// rows; U (fp32) as the accumulators' 4-column quads.  VB = value columns per pass (DV is a multiple of it).
 template <int DK, int VB>
 __global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
   using MT = bf16;
-  constexpr int NW = 8, KP = DK + 8, CP = C + 8, FP = C + 4, UP = VB + 4;
+  constexpr int NW = 8, KP = DK + 8, CP = C + 8, FP = C + 4;
   constexpr int NBD = DK / 16, NBV = VB / 16;
   using GQ = Tile<MT, C, DK>;
   using GV = Tile<MT, C, VB>;
   static_assert(GQ::PITCH == KP && NBD <= NW && NBV <= NW, "prep8 tiling");
   constexpr int VP = GV::PITCH;
-  __shared__ __attribute__((aligned(16))) MT tq[GQ::ELEMS];
+  constexpr int QA = (GQ::ELEMS * 2 > C * FP * 4) ? GQ::ELEMS * 2 : C * FP * 4;   // bytes: q's tile, then A (fp32)
+  constexpr int LW = (C * FP * 4 > C * KP * 2) ? C * FP * 4 : C * KP * 2;          // bytes: L (fp32), then W staged
+  __shared__ __attribute__((aligned(16))) unsigned char qa[QA];
   __shared__ __attribute__((aligned(16))) MT tk[GQ::ELEMS];
   __shared__ __attribute__((aligned(16))) MT tv[GV::ELEMS];
-  __shared__ __attribute__((aligned(16))) float sL[C * FP];
-  __shared__ __attribute__((aligned(16))) float sA[C * FP];
-  constexpr int STAGE = (C * UP > C * KP / 2) ? C * UP : C * KP / 2;   // floats: U (fp32), W or M (bf16)
-  __shared__ __attribute__((aligned(16))) float stage[STAGE];
+  __shared__ __attribute__((aligned(16))) unsigned char lw[LW];
+  __shared__ __attribute__((aligned(16))) MT sM[C * CP];                            // M staged
   __shared__ ChunkScalars cs;
   __shared__ __attribute__((aligned(16))) float rk[C], rq[C], fW[C], fU[C];
 
@@ -341,22 +342,25 @@ __global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
   const MT* k = (const MT*)a.k + qk_base;
   const MT* v = (const MT*)a.v + v_base;
   const float qs = a.q_scale;
-  MT* const stb = reinterpret_cast<MT*>(stage);
+  MT* const tq = reinterpret_cast<MT*>(qa);
+  float* const sA = reinterpret_cast<float*>(qa);   // q's tile is consumed by then
+  float* const sL = reinterpret_cast<float*>(lw);
+  MT* const stW = reinterpret_cast<MT*>(lw);        // L is consumed by then
 
-  // ---- 0: tiles in flight; scalars and norms meanwhile
+  // ---- 0: tiles in flight, the chunk scalars meanwhile; then the row norms from the tiles
   GQ::dma(tq, q + (size_t)t0 * qk_pitch, qk_pitch, w, NW, nrows);
   GQ::dma(tk, k + (size_t)t0 * qk_pitch, qk_pitch, w, NW, nrows);
   GV::dma(tv, v + (size_t)t0 * v_pitch, v_pitch, w, NW, nrows);
   if (w == 0) chunk_scalars(cs, a.g, a.beta, s_base, H, t0, T);
+  wait_dma();
+  __syncthreads();
   if (a.l2norm) {
-    if (w >= 4 && w < 6) row_rnorms<MT, DK>(rk, k - qk_base, qk_base, qk_pitch, t0, T, 2, w - 4);
-    if (w >= 6) row_rnorms<MT, DK>(rq, q - qk_base, qk_base, qk_pitch, t0, T, 2, w - 6);
+    if (w < 4) row_rnorms_lds<DK>(rq, tq, KP, nrows, 4, w);
+    else row_rnorms_lds<DK>(rk, tk, KP, nrows, 4, w - 4);
   } else if (threadIdx.x < C) {
     rk[threadIdx.x] = 1.f;
     rq[threadIdx.x] = 1.f;
   }
-  wait_dma();
-  __syncthreads();
   if (nrows < C) {                         // rows past the end: zeros in q, k and v
     constexpr int UQ = KP / 8, UV = VP / 8;
     const int nz = C - nrows;
@@ -366,13 +370,13 @@ __global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
       *reinterpret_cast<bf16x8*>(p) = bf16x8{};
     }
   }
-  if (threadIdx.x < C) {
+  __syncthreads();
+  if (threadIdx.x < C) {                   // read from phase 3 on, after several barriers
     const int s = threadIdx.x;
     fW[s] = cs.beta[s] * cs.gam[s] * rk[s];
     fU[s] = cs.beta[s];
   }
   if (threadIdx.x == 0) a.GL[bhc] = cs.gam[C - 1];
-  __syncthreads();
 
   // ---- 1a: diag(e) K^ and diag(gamma) Q^ rows out (16 bytes a lane)
   {
@@ -424,7 +428,7 @@ __global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
         const int row = r0 + r;
         const float gm = (row >= s) ? expf((float)(cs.G[row] - Gs)) : 0.f;   // mask before the exponent
         sL[row * FP + s] = (row > s) ? b4[r] * (KK[i][r] * (rk4[r] * rks)) * gm : 0.f;
-        stb[row * CP + s] = (bf16)((row >= s) ? QK[i][r] * (rq4[r] * qs * rks) * gm : 0.f);
+        sM[row * CP + s] = (bf16)((row >= s) ? QK[i][r] * (rq4[r] * qs * rks) * gm : 0.f);
       }
     }
   }
@@ -435,7 +439,7 @@ __global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
     MT* Mg = (MT*)a.M + bhc * C * C;
     for (int i = threadIdx.x; i < C * (C / 8); i += blockDim.x) {
       const int t = i >> 3, u = i & 7;
-      *reinterpret_cast<bf16x8*>(Mg + t * C + 8 * u) = *reinterpret_cast<const bf16x8*>(stb + t * CP + 8 * u);
+      *reinterpret_cast<bf16x8*>(Mg + t * C + 8 * u) = *reinterpret_cast<const bf16x8*>(sM + t * CP + 8 * u);
     }
   }
   if (w == 0) {
@@ -511,7 +515,7 @@ __global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
       for (int p = 0; p < 2; ++p)
         if (32 * p <= 16 * ti + 15) mma(acc, kT[p], fragAf(ti, p, fW));
       const int t = 16 * ti + n;
-      *reinterpret_cast<bf16x4*>(stb + t * KP + 16 * w + 4 * j) = bf16x4{(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
+      *reinterpret_cast<bf16x4*>(stW + t * KP + 16 * w + 4 * j) = bf16x4{(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
     }
   }
   __syncthreads();
@@ -520,13 +524,14 @@ __global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
     MT* Wg = (MT*)a.W + bhc * C * DK;
     for (int i = threadIdx.x; i < C * UQ; i += blockDim.x) {
       const int t = i / UQ, u = i - t * UQ;
-      *reinterpret_cast<bf16x8*>(Wg + t * DK + 8 * u) = *reinterpret_cast<const bf16x8*>(stb + t * KP + 8 * u);
+      *reinterpret_cast<bf16x8*>(Wg + t * DK + 8 * u) = *reinterpret_cast<const bf16x8*>(stW + t * KP + 8 * u);
     }
   }
-  // ---- 4: U^T = v^T (A diag(beta))^T, VB value columns per pass, staged (fp32) and written
+  // ---- 4: U^T = v^T (A diag(beta))^T, VB value columns per pass, written from the accumulators (4 fp32 columns a lane)
   float* Ug = a.U + bhc * C * DV;
   for (int vb = 0; vb < DV; vb += VB) {
-    if (vb > 0) {                          // the next block of v (the previous one is consumed)
+    if (vb > 0) {                          // the next block of v, once every wave is done with this one
+      __syncthreads();
       GV::dma(tv, v + (size_t)t0 * v_pitch + vb, v_pitch, w, NW, nrows);
       wait_dma();
       __syncthreads();
@@ -534,9 +539,9 @@ __global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
         constexpr int UV = VP / 8;
         for (int i = threadIdx.x; i < (C - nrows) * UV; i += blockDim.x)
           *reinterpret_cast<bf16x8*>(tv + (nrows + i / UV) * VP + 8 * (i % UV)) = bf16x8{};
+        __syncthreads();
       }
     }
-    __syncthreads();                       // W's (or the previous block's) copy-out has read the stage
     if (w < NBV) {
       Frag<MT> vT[2];
 #pragma unroll
@@ -547,14 +552,8 @@ __global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
 #pragma unroll
         for (int p = 0; p < 2; ++p)
           if (32 * p <= 16 * ti + 15) mma(acc, vT[p], fragAf(ti, p, fU));
-        *reinterpret_cast<f4*>(stage + (16 * ti + n) * UP + 16 * w + 4 * j) = acc;
+        *reinterpret_cast<f4*>(Ug + (size_t)(16 * ti + n) * DV + vb + 16 * w + 4 * j) = acc;
       }
-    }
-    __syncthreads();
-    constexpr int UU = VB / 4;
-    for (int i = threadIdx.x; i < C * UU; i += blockDim.x) {
-      const int t = i / UU, u = i - t * UU;
-      *reinterpret_cast<f4*>(Ug + (size_t)t * DV + vb + 4 * u) = *reinterpret_cast<const f4*>(stage + t * UP + 4 * u);
     }
   }
 }
@@ -1434,15 +1433,15 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   GV::dma(tdV, dVc, DV, w, NW);
   GA::dma(tA, Ac, C, w, NW);
   if (w == 0) chunk_scalars(cs, a.g, a.beta, s_base, H, t0, T);
-  if (a.l2norm) {
-    if (w >= 4 && w < 6) row_rnorms<MT, DK>(rk, (const MT*)a.k, qk_base, qk_pitch, t0, T, 2, w - 4);
-    if (w >= 6) row_rnorms<MT, DK>(rq, (const MT*)a.q, qk_base, qk_pitch, t0, T, 2, w - 6);
+  wait_dma();
+  __syncthreads();
+  if (a.l2norm) {                          // the row norms from the tiles (rows past the end: 0)
+    if (w < 4) row_rnorms_lds<DK>(rq, tq, KP, nrows, 4, w);
+    else row_rnorms_lds<DK>(rk, tk, KP, nrows, 4, w - 4);
   } else if (threadIdx.x < C) {
     rk[threadIdx.x] = (int)threadIdx.x < nrows ? 1.f : 0.f;
     rq[threadIdx.x] = (int)threadIdx.x < nrows ? 1.f : 0.f;
   }
-  wait_dma();
-  __syncthreads();
   if (nrows < C) {                         // rows past the end: zeros in q, k and dO
     constexpr int UQ = KP / 8, UV = VP / 8;
     const int nz = C - nrows;
@@ -1451,8 +1450,8 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
       MT* p = u < UQ ? tq + row * KP + 8 * u : u < 2 * UQ ? tk + row * KP + 8 * (u - UQ) : tO + row * VP + 8 * (u - 2 * UQ);
       *reinterpret_cast<bf16x8*>(p) = bf16x8{};
     }
-    __syncthreads();
   }
+  __syncthreads();                         // norms and zeroed rows visible
 
   // ---- B: products with the chunk states, transposed: [key block w] x [token tiles]
   //   dQ^T = gamma * (S_c dO^T),  dK^T = e * (dS Vn^T),  dW^T = -(S_c dVn^T),  X^T = dW^T A,  dK^T += beta gamma X^T
