@@ -26,9 +26,11 @@ HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
 MFMA_PEAK = {"bf16": 2.5e15, "f32": 157.3e12}
 PUBLISHED = 401.1e3        # reference's own fwd+bwd tokens/s at this config (M3 Max)
 C = 64
-# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (profiles/), scaled by the copy-kernel factor;
-# None until measured for a kernel at this workload
-TRAFFIC = {}
+# HBM bytes per launch at config 1 from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (profiles/gated_delta_config1.md),
+# FETCH_SIZE scaled by 2.000 and WRITE_SIZE by 1.000 (the factors a plain 256 MiB device copy gives); the two prep
+# launches are profiled together (their average)
+TRAFFIC = {1: {"chunk_bwd": 304.8e6, "state_bwd": 163.8e6, "state_fwd_store": 151.3e6, "state_fwd_out": 109.3e6,
+               "prep_fwd": 147.6e6, "prep_bwd": 147.6e6}}
 
 CONFIGS = {
     1: dict(B=4, T=1024, Hk=16, Hv=16, DK=128, DV=128, s0=False),
@@ -234,11 +236,12 @@ def main():
         bw = cost[name]["bytes"] / t
         fl = cost[name]["flops"] / t
         kernels[name] = {"us": round(t * 1e6, 2), "GB/s": round(bw / 1e9, 1), "hbm_frac": round(bw / HBM_PEAK, 4),
-                         "TFLOP/s": round(fl / 1e12, 2), "mfma_frac": round(fl / MFMA_PEAK["bf16"], 4)}
+                         "TFLOP/s": round(fl / 1e12, 2), "mfma_frac": round(fl / MFMA_PEAK["bf16"], 4),
+                         "traffic": TRAFFIC.get(args.config, {}).get(name)}
     dom = max(ktime, key=ktime.get)
     bw = cost[dom]["bytes"] / ktime[dom]
     roof = {"kernel": dom, "bound": "hbm", "achieved": round(bw / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-            "frac": round(bw / HBM_PEAK, 4), "traffic": TRAFFIC.get(dom)}
+            "frac": round(bw / HBM_PEAK, 4), "traffic": TRAFFIC.get(args.config, {}).get(dom)}
     line = {"metric": METRIC, "value": round(tokens / (elapsed / args.steps), 1), "unit": "tokens/s", "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
             "scaling": "weak", "vs_baseline": round(tokens / (elapsed / args.steps) / PUBLISHED, 2)
