@@ -5,7 +5,9 @@
 A step = one call of macai.gated_delta.chunk_gated_delta_rule (use_qk_l2norm_in_kernel=True, bf16 q/k/v, fp32 g and
 beta) followed by its backward for a seeded upstream gradient dO (torch.autograd.grad, so no gradient accumulation),
 on synthetic inputs already resident in HBM.  Prints ONE JSON line (rank 0).  Beside the step time it times every
-kernel of the step alone with HIP events on the launch stream (the roofline of the dominant kernel), and the
+pass inside steps identical to the timed ones with HIP events on the launch stream (macai.gated_delta.op.EVENTS; the
+roofline of the dominant kernel) and, for comparison, each pass alone (back-to-back repeats, whose inputs stay in the
+Infinity Cache), and the
 reference's torch path on the host CPU (the oracle's restatement of transformers' torch_chunk_gated_delta_rule,
 float32, autograd backward) on a bounded sample, as a reported baseline.
 """
@@ -87,6 +89,9 @@ def kernel_costs(B, T, H, DK, DV, es=2):
                                    flops=n * (2 * 2 * C * DK * DV))
     cost["state_bwd"] = dict(bytes=n * (3 * cdk * es + cc * es + 4 + sdk + cdv * es) + io_v,
                              flops=n * (3 * 2 * C * DK * DV + 2 * cc * DV))
+    # the two in one launch (macai_gdr_state_pair)
+    cost["state_pair"] = dict(bytes=cost["state_fwd_store"]["bytes"] + cost["state_bwd"]["bytes"],
+                              flops=cost["state_fwd_store"]["flops"] + cost["state_bwd"]["flops"])
     # the per-chunk backward reads q, k, v, g, beta, dO, A, S_c, dS_{c+1}, Vn, dVn; writes dq, dk, dv, dg, dbeta
     cost["chunk_bwd"] = dict(bytes=inp + io_v + n * (cc * es + 2 * sdk + 2 * cdv * es) + 2 * io_k + io_v + gb,
                              flops=n * (3 * 2 * C * DK * DV + 2 * cc * DK + 3 * 2 * cc * DK + 2 * 2 * cc * DV
@@ -108,6 +113,7 @@ def time_kernels(inp, reps=20):
     code, st = N.dtype_code(dt), N.stream_of(q)
     sc = DK ** -0.5
     split = op.split_for(B * H, T, DV)
+    split2 = op.split_for(B * H, T, DV, 2)
     e = lambda *shape, d=dt: torch.empty(*shape, device=dev, dtype=d)
     W, U, Ke, GL, Qg, M = e(B, H, NT, C, DK), e(B, H, NT, C, DV, d=f32), e(B, H, NT, C, DK), e(B, H, NT, d=f32), \
         e(B, H, NT, C, DK), e(B, H, NT, C, C)
@@ -128,10 +134,12 @@ def time_kernels(inp, reps=20):
                             P(Vn), B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, st),
         "state_bwd": ("macai_gdr_state_bwd", P(Ke), P(Qg), P(W), P(M), P(GL), P(do), None, P(dSn), P(dVn), P(ds0),
                       B, T, H, DK, DV, code, split, st),
+        "state_pair": ("macai_gdr_state_pair", P(W), P(U), P(Ke), P(Qg), P(M), P(GL), P(s0), P(do), None, P(Sc), P(Vn),
+                       P(dSn), P(dVn), P(ds0), B, T, H, DK, DV, code, split2, st),
         "chunk_bwd": ("macai_gdr_chunk_bwd", P(q), P(k), P(v), P(g), P(beta), P(do), P(A), P(Sc), P(dSn),
                       P(Vn), P(dVn), P(dq), P(dk), P(dv), P(dg), P(db), B, T, H, DK, DV, code, 1, sc, st),
     }
-    order = ["prep_fwd", "state_fwd_out", "prep_bwd", "state_fwd_store", "state_bwd", "chunk_bwd"]
+    order = ["prep_fwd", "state_fwd_out", "prep_bwd", "state_fwd_store", "state_bwd", "state_pair", "chunk_bwd"]
     for name in order:                   # warm, and produce every input of the later passes
         N.call(*calls[name])
     torch.cuda.synchronize()
@@ -207,6 +215,7 @@ def main():
                                       use_qk_l2norm_in_kernel=True)
         return torch.autograd.grad(o, leaves, do)
 
+    from macai.gated_delta import op
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -219,12 +228,24 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     gpu = e0.elapsed_time(e1) * 1e-3
+    # every pass timed in the step: HIP events on the launch stream around each launch, over further steps identical
+    # to the timed ones (an event record costs the stream ~4 us, so the timed steps above carry none)
+    op.EVENTS = []
+    for _ in range(min(args.steps, 20)):
+        step()
+    torch.cuda.synchronize()
+    in_step = {}
+    for name, a, b in op.EVENTS:
+        in_step.setdefault(name, []).append(a.elapsed_time(b) * 1e-3)
+    op.EVENTS = None
+    in_step = {name: sum(ts) / len(ts) for name, ts in in_step.items()}
     elapsed = max(wall, gpu)
     B, T, H, DK, DV = c["B"], c["T"], c["Hv"], c["DK"], c["DV"]
     tokens = B * T
     ms = elapsed / args.steps * 1e3
 
-    ktime, split = time_kernels(inp)
+    alone, split = time_kernels(inp)
+    ktime = dict(in_step)                # the passes as the step runs them
     if args.copy_mib:
         src = torch.ones(args.copy_mib << 18, device=dev)
         dst = torch.empty_like(src)
@@ -235,12 +256,14 @@ def main():
     for name, t in ktime.items():
         bw = cost[name]["bytes"] / t
         fl = cost[name]["flops"] / t
-        kernels[name] = {"us": round(t * 1e6, 2), "GB/s": round(bw / 1e9, 1), "hbm_frac": round(bw / HBM_PEAK, 4),
+        kernels[name] = {"us": round(t * 1e6, 2), "us_alone": round(alone[name] * 1e6, 2),
+                         "GB/s": round(bw / 1e9, 1), "hbm_frac": round(bw / HBM_PEAK, 4),
                          "TFLOP/s": round(fl / 1e12, 2), "mfma_frac": round(fl / MFMA_PEAK["bf16"], 4),
                          "traffic": TRAFFIC.get(args.config, {}).get(name)}
     dom = max(ktime, key=ktime.get)
     bw = cost[dom]["bytes"] / ktime[dom]
-    roof = {"kernel": dom, "bound": "hbm", "achieved": round(bw / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+    roof = {"kernel": dom, "timing": "in-step HIP events", "bound": "hbm", "achieved": round(bw / 1e9, 1),
+            "peak": HBM_PEAK / 1e9, "unit": "GB/s",
             "frac": round(bw / HBM_PEAK, 4), "traffic": TRAFFIC.get(args.config, {}).get(dom)}
     line = {"metric": METRIC, "value": round(tokens / (elapsed / args.steps), 1), "unit": "tokens/s", "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
@@ -249,7 +272,8 @@ def main():
             "dtype": "bf16", "data": "synthetic",
             "config": {"workload": f"gated-delta drop-in fwd+bwd, BASELINE config {args.config}", "B": B, "T": T,
                        "Hk": c["Hk"], "Hv": H, "DK": DK, "DV": DV, "chunk": C, "l2norm_in_kernel": True,
-                       "initial_state": c["s0"], "value_split": split},
+                       "initial_state": c["s0"], "value_split": split, "overlap_split": op.split_for(B * H, T, DV, 2),
+                       "overlapped_state_passes": op.OVERLAP},
             "roofline": roof, "kernels": kernels}
     if not args.no_cpu:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)

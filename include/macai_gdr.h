@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define MACAI_GDR_ABI_VERSION 4
+#define MACAI_GDR_ABI_VERSION 5
 
 /* dtype codes */
 #define MACAI_GDR_F32 0
@@ -84,6 +84,16 @@ int macai_gdr_state_fwd(const void* W, const float* U, const void* Ke, const flo
 int macai_gdr_state_bwd(const void* Ke, const void* Qg, const void* W, const void* M, const float* GL,
                         const void* dO, const float* dsT, float* dSn, void* dVn, float* ds0, int64_t B, int64_t T,
                         int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t split, void* stream);
+
+/* The backward's recompute pass (macai_gdr_state_fwd with STORE_STATES | NO_OUTPUT: Sc, Vn) and its reverse pass
+ * (macai_gdr_state_bwd: dSn, dVn, ds0) in one launch, side by side on the CUs: they read prep's outputs, not each
+ * other's.  Each is a sequential chain of chunks whose speed hardly depends on its share of the CUs, so running them
+ * at once (with `split` chosen for half the chip) nearly hides one.  Replaces the reference's two launches
+ * `lib.gdc_fwd(..., flags 1 | 8)` and `lib.gdc_bwd_state(...)` (op.py:217, 234). */
+int macai_gdr_state_pair(const void* W, const float* U, const void* Ke, const void* Qg, const void* M, const float* GL,
+                         const float* s0, const void* dO, const float* dsT, float* Sc, void* Vn, float* dSn, void* dVn,
+                         float* ds0, int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV, int32_t dtype,
+                         int32_t split, void* stream);
 
 /* The per-chunk backward (north star (4)): dq, dk (w.r.t. the raw inputs when use_l2norm), dv in dtype; dg, dbeta in
  * float32; one writer per element (bitwise deterministic).  Replaces `lib.gdc_bwd_chunk(q, k, beta, do, gc, a, kg, m,

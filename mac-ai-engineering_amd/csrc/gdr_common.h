@@ -200,16 +200,10 @@ __device__ __forceinline__ double wave_incl_scan_d(double x) {
   return x;
 }
 
-__device__ __forceinline__ void chunk_scalars(ChunkScalars& cs, const float* g, const float* beta, size_t row_base,
-                                              size_t row_stride, int t0, int T) {
+// from this lane's g and beta (0 past the sequence end)
+__device__ __forceinline__ void chunk_scalars_from(ChunkScalars& cs, float gv, float bv, int t0, int T) {
   const int l = lane_id();
-  const int t = t0 + l;
   const int last = (T - t0 < C ? T - t0 : C) - 1;
-  float gv = 0.f, bv = 0.f;
-  if (t < T) {
-    gv = g[row_base + (size_t)t * row_stride];
-    if (beta) bv = beta[row_base + (size_t)t * row_stride];
-  }
   double G = wave_incl_scan_d((double)gv);
   const double Gl = __shfl(G, last, 64);
   if (l > last) G = Gl;
@@ -217,6 +211,16 @@ __device__ __forceinline__ void chunk_scalars(ChunkScalars& cs, const float* g, 
   cs.gam[l] = (float)exp(G);
   cs.e[l] = (float)exp(Gl - G);
   cs.beta[l] = bv;
+}
+__device__ __forceinline__ void chunk_scalars(ChunkScalars& cs, const float* g, const float* beta, size_t row_base,
+                                              size_t row_stride, int t0, int T) {
+  const int t = t0 + lane_id();
+  float gv = 0.f, bv = 0.f;
+  if (t < T) {
+    gv = g[row_base + (size_t)t * row_stride];
+    if (beta) bv = beta[row_base + (size_t)t * row_stride];
+  }
+  chunk_scalars_from(cs, gv, bv, t0, T);
 }
 
 // ---- row norms ----------------------------------------------------------------------------------------------------

@@ -560,8 +560,8 @@ __global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
 
 // XCD-aware map of a flat workgroup id to (head-row, column slice): the slices of one head-row share an XCD (and its
 // L2), since consecutive workgroup ids go to consecutive XCDs.  Returns false for the padding workgroups.
-__device__ __forceinline__ bool state_map(int nslice, int HR, int& hr, int& slice) {
-  const int f = blockIdx.x, xcd = f & 7, kx = f >> 3;
+__device__ __forceinline__ bool state_map(int nslice, int HR, int& hr, int& slice, int f) {
+  const int xcd = f & 7, kx = f >> 3;
   hr = (kx / nslice) * 8 + xcd;
   slice = kx % nslice;
   return hr < HR;
@@ -595,19 +595,28 @@ struct Buffers {
 // the output, diag(gamma) Q^ and M into a swizzled LDS stage by asynchronous copies -- the next chunk's copies are in
 // flight while this chunk's MFMAs run -- and each wave keeps its 16 columns of S in accumulators.
 // ---------------------------------------------------------------------------------------------------------------------
-template <typename MT, int DK, int NW, bool OUT, bool STORE>
-__global__ void __launch_bounds__(64 * (NW + 1)) state_fwd_kernel(StateFwdArgs a) {
+template <typename MT, int DK, bool OUT>
+struct StateFwdLds {
   using GW = Tile<MT, C, DK>;    // W, diag(e) K^, diag(gamma) Q^     [t][d]
   using GM = Tile<MT, C, C>;     // M                                  [t][s]
+  static constexpr int O_KE = GW::ELEMS, O_Q = O_KE + GW::ELEMS, O_M = O_Q + (OUT ? GW::ELEMS : 0);
+  static constexpr int SZ = O_M + (OUT ? GM::ELEMS : 0);
+  static constexpr int NBUF = Buffers<SZ * (int)sizeof(MT)>::N;
+  static constexpr int ELEMS = NBUF * SZ;
+};
+
+// The pass of workgroup f of the launch (see state_map), with `lds` the workgroup's LDS (StateFwdLds::ELEMS elements).
+template <typename MT, int DK, int NW, bool OUT, bool STORE>
+__device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, int f) {
+  using L = StateFwdLds<MT, DK, OUT>;
+  using GW = typename L::GW;
+  using GM = typename L::GM;
   constexpr int ND = DK / 16;
-  constexpr int O_KE = GW::ELEMS, O_Q = O_KE + GW::ELEMS, O_M = O_Q + (OUT ? GW::ELEMS : 0);
-  constexpr int SZ = O_M + (OUT ? GM::ELEMS : 0);
-  constexpr int NBUF = Buffers<SZ * (int)sizeof(MT)>::N;
-  __shared__ __attribute__((aligned(1024))) MT lds[NBUF * SZ];
+  constexpr int O_KE = L::O_KE, O_Q = L::O_Q, O_M = L::O_M, SZ = L::SZ, NBUF = L::NBUF;
 
   const int T = a.T, H = a.H, DV = a.DV, NT = a.NT;
   int hr, slice;
-  if (!state_map(a.nslice, a.B * H, hr, slice)) return;
+  if (!state_map(a.nslice, a.B * H, hr, slice, f)) return;
   const int b = hr / H, h = hr % H;
   const int l = lane_id(), w = wave_id(), j = l >> 4;
 
@@ -767,23 +776,38 @@ __global__ void __launch_bounds__(64 * (NW + 1)) state_fwd_kernel(StateFwdArgs a
   }
 }
 
+template <typename MT, int DK, int NW, bool OUT, bool STORE>
+__global__ void __launch_bounds__(64 * (NW + 1)) state_fwd_kernel(StateFwdArgs a) {
+  __shared__ __attribute__((aligned(1024))) MT lds[StateFwdLds<MT, DK, OUT>::ELEMS];
+  state_fwd_body<MT, DK, NW, OUT, STORE>(a, lds, blockIdx.x);
+}
+
 // ---------------------------------------------------------------------------------------------------------------------
 // the reverse state pass: streams diag(e) K^, diag(gamma) Q^, W, M and the workgroup's dO columns per chunk
 // ---------------------------------------------------------------------------------------------------------------------
 template <typename MT, int DK, int NW>
-__global__ void __launch_bounds__(64 * (NW + 1)) state_bwd_kernel(StateBwdArgs a) {
+struct StateBwdLds {
   using GK = Tile<MT, C, DK>;        // diag(e) K^, diag(gamma) Q^, W    [t][d]
   using GM = Tile<MT, C, C>;         // M                                [t][s]
   using GO = Tile<MT, C, 16 * NW>;   // dO columns                       [t][v]
+  static constexpr int O_Q = GK::ELEMS, O_W = O_Q + GK::ELEMS, O_M = O_W + GK::ELEMS, O_O = O_M + GM::ELEMS;
+  static constexpr int SZ = O_O + GO::ELEMS;
+  static constexpr int NBUF = Buffers<SZ * (int)sizeof(MT)>::N;
+  static constexpr int ELEMS = NBUF * SZ;
+};
+
+template <typename MT, int DK, int NW>
+__device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, int f) {
+  using L = StateBwdLds<MT, DK, NW>;
+  using GK = typename L::GK;
+  using GM = typename L::GM;
+  using GO = typename L::GO;
   constexpr int ND = DK / 16;
-  constexpr int O_Q = GK::ELEMS, O_W = O_Q + GK::ELEMS, O_M = O_W + GK::ELEMS, O_O = O_M + GM::ELEMS;
-  constexpr int SZ = O_O + GO::ELEMS;
-  constexpr int NBUF = Buffers<SZ * (int)sizeof(MT)>::N;
-  __shared__ __attribute__((aligned(1024))) MT lds[NBUF * SZ];
+  constexpr int O_Q = L::O_Q, O_W = L::O_W, O_M = L::O_M, O_O = L::O_O, SZ = L::SZ, NBUF = L::NBUF;
 
   const int T = a.T, H = a.H, DV = a.DV, NT = a.NT;
   int hr, slice;
-  if (!state_map(a.nslice, a.B * H, hr, slice)) return;
+  if (!state_map(a.nslice, a.B * H, hr, slice, f)) return;
   const int b = hr / H, h = hr % H;
   const int l = lane_id(), w = wave_id(), j = l >> 4;
   const int vg = slice * NW * 16;            // the workgroup's first value column
@@ -916,6 +940,23 @@ __global__ void __launch_bounds__(64 * (NW + 1)) state_bwd_kernel(StateBwdArgs a
   for (int di = 0; di < ND; ++di)
 #pragma unroll
     for (int r = 0; r < 4; ++r) a.ds0[(size_t)hr * DK * DV + (16 * di + 4 * j + r) * DV + col] = dS[di][r];
+}
+
+template <typename MT, int DK, int NW>
+__global__ void __launch_bounds__(64 * (NW + 1)) state_bwd_kernel(StateBwdArgs a) {
+  __shared__ __attribute__((aligned(1024))) MT lds[StateBwdLds<MT, DK, NW>::ELEMS];
+  state_bwd_body<MT, DK, NW>(a, lds, blockIdx.x);
+}
+
+// The backward's recompute pass (storing S_c, Vn) and its reverse pass in one launch: they read prep's outputs and
+// not each other's, so workgroups [0, nfwd) run the first and the rest the second, side by side on the CUs, with no
+// stream synchronisation between them.
+template <typename MT, int DK, int NW>
+__global__ void __launch_bounds__(64 * (NW + 1)) state_pair_kernel(StateFwdArgs af, StateBwdArgs ab, int nfwd) {
+  constexpr int EF = StateFwdLds<MT, DK, false>::ELEMS, EB = StateBwdLds<MT, DK, NW>::ELEMS;
+  __shared__ __attribute__((aligned(1024))) MT lds[EF > EB ? EF : EB];
+  if ((int)blockIdx.x < nfwd) state_fwd_body<MT, DK, NW, false, true>(af, lds, blockIdx.x);
+  else state_bwd_body<MT, DK, NW>(ab, lds, blockIdx.x - nfwd);
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
@@ -2044,6 +2085,39 @@ int macai_gdr_state_bwd(const void* Ke, const void* Qg, const void* W, const voi
     DISPATCH_DK(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_bwd_kernel<float, DKC, NWC>), grid, block, 0, st, a)));
   } else {
     DISPATCH_DK(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_bwd_kernel<bf16, DKC, NWC>), grid, block, 0, st, a)));
+  }
+  return launched(what);
+}
+
+int macai_gdr_state_pair(const void* W, const float* U, const void* Ke, const void* Qg, const void* M, const float* GL,
+                         const float* s0, const void* dO, const float* dsT, float* Sc, void* Vn, float* dSn, void* dVn,
+                         float* ds0, int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV, int32_t dtype,
+                         int32_t split, void* stream) {
+  const char* what = "macai_gdr_state_pair";
+  int rc = check_common(what, B, T, H, DK, DV, dtype);
+  if (rc) return rc;
+  if (!W || !U || !Ke || !Qg || !M || !GL || !dO || !Sc || !Vn || !dSn || !dVn || !ds0)
+    return fail(MACAI_GDR_EINVAL, "%s: null pointer", what);
+  const void* ps[] = {W, U, Ke, Qg, M, s0, dO, dsT, Sc, Vn, dSn, dVn, ds0};
+  for (const void* p : ps)
+    if (!aligned16(p)) return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
+  int nw, nslice;
+  if ((rc = pick_waves(DV, split, what, &nw, &nslice))) return rc;
+  const int NTi = (int)((T + C - 1) / C);
+  StateFwdArgs af{W, U, Ke, GL, nullptr, nullptr, s0, nullptr, nullptr, Sc, Vn, (int)B, (int)T, (int)H, (int)DV, NTi,
+                  nslice};
+  StateBwdArgs ab{Ke, Qg, W, M, GL, dO, dsT, dSn, dVn, ds0, (int)B, (int)T, (int)H, (int)DV, NTi, nslice};
+  const int HR = (int)(B * H);
+  const int nfwd = 8 * nslice * ((HR + 7) / 8);   // a multiple of 8: the second pass keeps state_map's XCD layout
+  dim3 grid((unsigned)(2 * nfwd));
+  dim3 block(64 * (nw + 1));
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == MACAI_GDR_F32) {
+    DISPATCH_DK(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_pair_kernel<float, DKC, NWC>), grid, block, 0, st, af, ab,
+                                                       nfwd)));
+  } else {
+    DISPATCH_DK(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_pair_kernel<bf16, DKC, NWC>), grid, block, 0, st, af, ab,
+                                                       nfwd)));
   }
   return launched(what);
 }

@@ -20,6 +20,25 @@ CHUNK = 64   # chunk length of the kernels; the drop-in's chunk_size is accepted
 VALUE_SPLIT = "auto"
 # the passes' calls by what they ran, "fwd s<split>" / "bwd s<split>" (counted at every call; no GPU work)
 CALLS = collections.Counter()
+# Measurement hook: set to a list to record (pass, start event, end event) around every launch, on the launch stream;
+# None (the default) records nothing.
+EVENTS = None
+# The backward's recompute pass (storing S_c, Vn) and its reverse pass need only prep's outputs, not each other: with
+# OVERLAP they run in one launch (macai_gdr_state_pair), each on about half the CUs.  Both are sequential chunk chains
+# whose speed hardly depends on how many CUs they get, so this nearly hides one of them.
+OVERLAP = True
+
+
+def _launch(name: str, entry: str, *args):
+    """One C-ABI launch; timed on the launch stream when EVENTS is a list."""
+    if EVENTS is None:
+        N.call(entry, *args)
+        return
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    N.call(entry, *args)
+    e1.record()
+    EVENTS.append((name, e0, e1))
 
 
 def valid_splits(dv: int) -> list:
@@ -29,13 +48,14 @@ def valid_splits(dv: int) -> list:
     return [s for s in range(1, slices + 1) if slices % s == 0 and slices // s in (1, 2, 4, 8)]
 
 
-def split_for(rows: int, T: int, dv: int) -> int:
-    """VALUE_SPLIT's choice for `rows` head-rows (B x H) of value width dv: "auto" takes the smallest valid split that
-    gives at least 256 workgroups (one per CU), else the largest; an int setting is rounded down to a valid split."""
+def split_for(rows: int, T: int, dv: int, share: int = 1) -> int:
+    """VALUE_SPLIT's choice for `rows` head-rows (B x H) of value width dv, for a pass that gets 1 / share of the
+    chip: "auto" takes the smallest valid split that gives at least 256 / share workgroups (one per CU), else the
+    largest; an int setting is rounded down to a valid split."""
     valid = valid_splits(dv)
     if VALUE_SPLIT == "auto":
         for s in valid:
-            if rows * s >= 256:
+            if rows * s * share >= 256:
                 return s
         return valid[-1]
     want = int(VALUE_SPLIT)
@@ -77,8 +97,9 @@ def _prep(q, k, v, g, beta, l2norm: bool, q_scale: float, with_A: bool):
              M=torch.empty(B, H, NT, CHUNK, CHUNK, device=dev, dtype=dt),
              A=torch.empty(B, H, NT, CHUNK, CHUNK, device=dev, dtype=dt) if with_A else None)
     P = N.ptr
-    N.call("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(r["W"]), P(r["U"]), P(r["Ke"]), P(r["GL"]), P(r["Qg"]),
-           P(r["M"]), P(r["A"]), B, T, H, DK, DV, N.dtype_code(dt), int(l2norm), q_scale, N.stream_of(q))
+    _launch("prep_bwd" if with_A else "prep_fwd", "macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(r["W"]),
+            P(r["U"]), P(r["Ke"]), P(r["GL"]), P(r["Qg"]), P(r["M"]), P(r["A"]), B, T, H, DK, DV, N.dtype_code(dt),
+            int(l2norm), q_scale, N.stream_of(q))
     return r
 
 
@@ -92,8 +113,8 @@ def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool):
     sT = torch.empty(B, H, DK, DV, device=dev, dtype=torch.float32) if want_sT else None
     split = split_for(B * H, T, DV)
     P = N.ptr
-    N.call("macai_gdr_state_fwd", P(r["W"]), P(r["U"]), P(r["Ke"]), P(r["GL"]), P(r["Qg"]), P(r["M"]), P(s0), P(o),
-           P(sT), None, None, B, T, H, DK, DV, code, 0, split, stream)
+    _launch("state_fwd_out", "macai_gdr_state_fwd", P(r["W"]), P(r["U"]), P(r["Ke"]), P(r["GL"]), P(r["Qg"]), P(r["M"]),
+            P(s0), P(o), P(sT), None, None, B, T, H, DK, DV, code, 0, split, stream)
     CALLS[f"fwd s{split}"] += 1
     return o, sT
 
@@ -106,22 +127,27 @@ def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float):
     code, stream = N.dtype_code(dt), N.stream_of(q)
     f32 = torch.float32
     r = _prep(q, k, v, g, beta, l2norm, q_scale, True)
-    split = split_for(B * H, T, DV)
     P = N.ptr
+    split = split_for(B * H, T, DV, 2 if OVERLAP else 1)
     Sc = torch.empty(B, H, NT, DK, DV, device=dev, dtype=f32)
     Vn = torch.empty(B, H, NT, CHUNK, DV, device=dev, dtype=dt)
-    N.call("macai_gdr_state_fwd", P(r["W"]), P(r["U"]), P(r["Ke"]), P(r["GL"]), None, None, P(s0), None, None, P(Sc),
-           P(Vn), B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, stream)
     dSn = torch.empty(B, H, NT, DK, DV, device=dev, dtype=f32)
     dVn = torch.empty_like(Vn)
     ds0 = torch.empty(B, H, DK, DV, device=dev, dtype=f32)
-    N.call("macai_gdr_state_bwd", P(r["Ke"]), P(r["Qg"]), P(r["W"]), P(r["M"]), P(r["GL"]), P(do), P(dsT), P(dSn),
-           P(dVn), P(ds0), B, T, H, DK, DV, code, split, stream)
+    if OVERLAP:
+        _launch("state_pair", "macai_gdr_state_pair", P(r["W"]), P(r["U"]), P(r["Ke"]), P(r["Qg"]), P(r["M"]),
+                P(r["GL"]), P(s0), P(do), P(dsT), P(Sc), P(Vn), P(dSn), P(dVn), P(ds0), B, T, H, DK, DV, code, split,
+                stream)
+    else:
+        _launch("state_fwd_store", "macai_gdr_state_fwd", P(r["W"]), P(r["U"]), P(r["Ke"]), P(r["GL"]), None, None,
+                P(s0), None, None, P(Sc), P(Vn), B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, stream)
+        _launch("state_bwd", "macai_gdr_state_bwd", P(r["Ke"]), P(r["Qg"]), P(r["W"]), P(r["M"]), P(r["GL"]), P(do),
+                P(dsT), P(dSn), P(dVn), P(ds0), B, T, H, DK, DV, code, split, stream)
     CALLS[f"bwd s{split}"] += 1
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     dg, dbeta = torch.empty_like(g), torch.empty_like(beta)
-    N.call("macai_gdr_chunk_bwd", P(q), P(k), P(v), P(g), P(beta), P(do), P(r["A"]), P(Sc), P(dSn), P(Vn), P(dVn),
-           P(dq), P(dk), P(dv), P(dg), P(dbeta), B, T, H, DK, DV, code, int(l2norm), q_scale, stream)
+    _launch("chunk_bwd", "macai_gdr_chunk_bwd", P(q), P(k), P(v), P(g), P(beta), P(do), P(r["A"]), P(Sc), P(dSn), P(Vn),
+            P(dVn), P(dq), P(dk), P(dv), P(dg), P(dbeta), B, T, H, DK, DV, code, int(l2norm), q_scale, stream)
     return dq, dk, dv, dg, dbeta, ds0
 
 

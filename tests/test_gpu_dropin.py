@@ -269,3 +269,19 @@ def test_value_split_changes_no_bits():
     inp = gdr.make_inputs(1, 150, 3, 3, 128, 128, torch.bfloat16, s0=True, seed=6)
     runs = [_grads_once(inp, s) for s in (1, 2, 4, 8)]
     assert all(torch.equal(a, b) for r in runs[1:] for a, b in zip(runs[0], r))
+
+
+def test_overlapped_passes_change_no_bits():
+    """The backward's recompute and reverse passes run at once on two streams (op.OVERLAP) or one after the other:
+    identical bits, several times in a row with host synchronisations between (the streams' ordering holds)."""
+    _say("case overlap bits")
+    inp = gdr.make_inputs(2, 200, 4, 4, 128, 128, torch.bfloat16, s0=True, seed=8)
+    old = op.OVERLAP
+    try:
+        op.OVERLAP = False
+        ref = _grads_once(inp)
+        op.OVERLAP = True
+        runs = [_grads_once(inp) for _ in range(3)]
+    finally:
+        op.OVERLAP = old
+    assert all(torch.equal(a, b) for r in runs for a, b in zip(ref, r))

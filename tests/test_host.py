@@ -67,6 +67,9 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert sf(p, p, p, p, p, None, None, p, None, None, None) == N.EINVAL
     assert L.macai_gdr_state_bwd(p, p, p, p, p, None, None, p, p, p, 1, 64, 1, 128, 128, 1, 0, None) == N.EINVAL
     assert L.macai_gdr_chunk_bwd(*([p] * 15), None, 1, 64, 1, 128, 128, 1, 1, 1.0, None) == N.EINVAL
+    pair = lambda *ptrs, split=0: L.macai_gdr_state_pair(*ptrs, 1, 64, 1, 128, 128, 1, split, None)
+    assert pair(*([p] * 6), None, p, None, p, p, p, p, None) == N.EINVAL and b"null" in L.macai_gdr_last_error()
+    assert pair(*([p] * 6), None, p, None, *([p] * 5), split=3) == N.EINVAL
     assert L.macai_gdr_decode(p, p, p, p, p, p, p, p, 1, 1, 256, 128, 1, 1, 1.0, None) == N.EUNSUP
 
 
@@ -102,6 +105,8 @@ def test_split_rule():
     assert op.split_for(2048, 1, 128) == 1
     assert op.split_for(1, 64, 32) == 2
     assert op.split_for(2, 130, 96) == 6
+    assert op.split_for(64, 1024, 128, 2) == 2      # a pass on half the chip (the backward's overlapped passes)
+    assert op.split_for(16, 32768, 128, 2) == 8
     old = op.VALUE_SPLIT
     try:
         op.VALUE_SPLIT = 3
