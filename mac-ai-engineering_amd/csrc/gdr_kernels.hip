@@ -714,6 +714,22 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
     if (NBUF == 1) __syncthreads();        // chunk c is in LDS
     const MT* st = lds + buf * SZ;
 
+    // The output pass (one wave per SIMD, registers to spare) reads every fragment that does not depend on S first, so
+    // the LDS latency overlaps the conversions and the MFMAs, and runs the products k-block by k-block across their
+    // tiles (independent accumulators between dependent ones).  The store pass, which shares a launch with the reverse
+    // pass at two waves per SIMD, keeps the register-lean order (fragments next to their MFMAs).
+    constexpr bool EARLY = OUT && NW <= 4;   // 9 waves (NW = 8) leave 168 registers a wave: lean order there
+    Frag<MT> fw[4][ND / 2], fk[ND][2];
+    if constexpr (EARLY) {
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int p = 0; p < ND / 2; ++p) fw[mi][p] = frag_tile<MT, GW>(st, 16 * mi, 32 * p);
+#pragma unroll
+      for (int di = 0; di < ND; ++di)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) fk[di][p] = frag_tile_tr<MT, GW>(st + O_KE, 32 * p, 16 * di);
+    }
     // S as the B operand (k = state rows)
     Frag<MT> Sf[ND / 2];
 #pragma unroll
@@ -721,15 +737,20 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
     // Vn = U - W S
     f4 Vn[4];
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-      Frag<MT> fw[ND / 2];
+    for (int mi = 0; mi < 4; ++mi) Vn[mi] = f4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (EARLY) {
 #pragma unroll
-      for (int p = 0; p < ND / 2; ++p) fw[p] = frag_tile<MT, GW>(st, 16 * mi, 32 * p);
-      f4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int p = 0; p < ND / 2; ++p)
 #pragma unroll
-      for (int p = 0; p < ND / 2; ++p) mma(acc, fw[p], Sf[p]);
-      Vn[mi] = U[mi] - acc;
+        for (int mi = 0; mi < 4; ++mi) mma(Vn[mi], fw[mi][p], Sf[p]);
+    } else {
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int p = 0; p < ND / 2; ++p) mma(Vn[mi], frag_tile<MT, GW>(st, 16 * mi, 32 * p), Sf[p]);
     }
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) Vn[mi] = U[mi] - Vn[mi];
     Frag<MT> Vf[2];
 #pragma unroll
     for (int p = 0; p < 2; ++p) Vf[p] = frag_acc<MT>(Vn[2 * p], Vn[2 * p + 1]);
@@ -737,31 +758,41 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
     // S <- exp(G_last) S + (diag(e) K)^T Vn   (the chain to the next chunk; the rest below is off it)
     f4 Sn[ND];
 #pragma unroll
-    for (int di = 0; di < ND; ++di) {
-      Frag<MT> fk[2];
+    for (int di = 0; di < ND; ++di) Sn[di] = S[di] * gl;
+    if constexpr (EARLY) {
 #pragma unroll
-      for (int p = 0; p < 2; ++p) fk[p] = frag_tile_tr<MT, GW>(st + O_KE, 32 * p, 16 * di);
-      f4 acc = S[di] * gl;
+      for (int p = 0; p < 2; ++p)
 #pragma unroll
-      for (int p = 0; p < 2; ++p) mma(acc, fk[p], Vf[p]);
-      Sn[di] = acc;
+        for (int di = 0; di < ND; ++di) mma(Sn[di], fk[di][p], Vf[p]);
+    } else {
+#pragma unroll
+      for (int di = 0; di < ND; ++di)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) mma(Sn[di], frag_tile_tr<MT, GW>(st + O_KE, 32 * p, 16 * di), Vf[p]);
     }
     if (OUT) {
       // O = diag(gamma) Q S + M Vn (M lower triangular: k-blocks past the row block are zero)
-      f4 pO[4];
+      Frag<MT> fq[4][ND / 2], fm[4][2];
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) {
-        Frag<MT> fq[ND / 2];
 #pragma unroll
-        for (int p = 0; p < ND / 2; ++p) fq[p] = frag_tile<MT, GW>(st + O_Q, 16 * mi, 32 * p);
-        f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int p = 0; p < ND / 2; ++p) mma(acc, fq[p], Sf[p]);
+        for (int p = 0; p < ND / 2; ++p) fq[mi][p] = frag_tile<MT, GW>(st + O_Q, 16 * mi, 32 * p);
 #pragma unroll
         for (int p = 0; p < 2; ++p)
-          if (32 * p <= 16 * mi + 15) mma(acc, frag_tile<MT, GM>(st + O_M, 16 * mi, 32 * p), Vf[p]);
-        pO[mi] = acc;
+          if (32 * p <= 16 * mi + 15) fm[mi][p] = frag_tile<MT, GM>(st + O_M, 16 * mi, 32 * p);
       }
+      f4 pO[4];
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) pO[mi] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p = 0; p < ND / 2; ++p)
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) mma(pO[mi], fq[mi][p], Sf[p]);
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi)
+          if (32 * p <= 16 * mi + 15) mma(pO[mi], fm[mi][p], Vf[p]);
       store_o(c, pO);
     }
 #pragma unroll
