@@ -27,6 +27,17 @@ constexpr float L2_EPS = 1e-6f; // l2norm epsilon of the reference prologue (_no
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
+// Workgroup barrier for LDS data: each wave's LDS accesses complete (lgkmcnt(0)) before s_barrier, and the compiler
+// moves no memory access across it.  Unlike __syncthreads() it does not wait for outstanding global loads and stores,
+// nor for asynchronous global->LDS copies (vmcnt): the waves that issued a copy wait for it (wait_vmcnt / wait_dma)
+// before the barrier that publishes its tile.  (A workgroup release fence on LDS would wait for every copy in flight.)
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);      // lgkmcnt(0); vmcnt and expcnt at their maxima
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // ---- scalar conversions -------------------------------------------------------------------------------------------
 __device__ __forceinline__ float to_f(float x) { return x; }
 __device__ __forceinline__ float to_f(bf16 x) { return (float)x; }

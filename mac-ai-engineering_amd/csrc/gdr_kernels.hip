@@ -1446,9 +1446,9 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   using GA = Tile<MT, C, C>;
   static_assert(GQ::PITCH == KP && GA::PITCH == CP && NBD <= NW && NBV <= NW, "chunk_bwd8 tiling");
   constexpr int VP = GV::PITCH;
-  constexpr int O_K = GQ::ELEMS, O_O = 2 * GQ::ELEMS, O_VN = O_O + GV::ELEMS, O_DV = O_VN + GV::ELEMS,
-                O_AT = O_DV + GV::ELEMS, TILES = O_AT + GA::ELEMS;
-  __shared__ __attribute__((aligned(16))) MT tiles[TILES];   // q, k, dO (then v), Vn (then dv), dVn, A
+  // two arrays: the compiler then knows that reads of the first do not depend on copies still in flight into the second
+  __shared__ __attribute__((aligned(16))) MT tiles1[3 * GV::ELEMS];                 // dO (then v), Vn (then dv), dVn
+  __shared__ __attribute__((aligned(16))) MT tiles2[2 * GQ::ELEMS + GA::ELEMS];     // q, k, A
   __shared__ __attribute__((aligned(16))) MT sdW[C * KP];    // dW = -dVn S_c^T, [t][d]
   __shared__ __attribute__((aligned(16))) MT sMkT[C * CP];   // [s][t] = dM[t][s] rk_s
   __shared__ __attribute__((aligned(16))) MT sMqT[C * CP];   // [s][t] = dM[t][s] rq_t qs
@@ -1477,36 +1477,126 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   const MT* dVc = (const MT*)a.dVn + bhc * C * DV;
   const MT* Ac = (const MT*)a.A + bhc * C * C;
   const float qs = a.q_scale;
-  MT* const tq = tiles;
-  MT* const tk = tiles + O_K;
-  MT* const tO = tiles + O_O;
-  MT* const tVn = tiles + O_VN;
-  MT* const tdV = tiles + O_DV;
-  MT* const tA = tiles + O_AT;
+  MT* const tq = tiles2;
+  MT* const tk = tiles2 + GQ::ELEMS;
+  MT* const tA = tiles2 + 2 * GQ::ELEMS;
+  MT* const tO = tiles1;
+  MT* const tVn = tiles1 + GV::ELEMS;
+  MT* const tdV = tiles1 + 2 * GV::ELEMS;
   const int cb = w & 3, hh = w >> 2;       // [C x C] column block and row half
 
-  // ---- 0: global operands into registers first (their latency overlaps the tile copies), then the tiles
+  // ---- 0: global reads in two groups.  Group 1 is what the state products of B consume: the chunk states (into
+  // registers) and the dO, Vn, dVn tiles.  Group 2 -- the v fragments and the q, k, A tiles -- lands while those
+  // products run.  Every read below is unconditional (rows past the end re-read the last row and are masked later) and
+  // the tile copies are branch-free with a fixed count per wave, so after group 1 each wave has exactly N2 loads
+  // outstanding once group 1 has retired (loads retire in issue order).  Ragged chunks wait for everything.
+  float gv, bv;                            // this lane's g and beta (used by wave 0)
+  {
+    const size_t o = s_base + (size_t)(t0 + l < T ? t0 + l : T - 1) * H;
+    gv = a.g[o];
+    bv = a.beta[o];
+  }
   Frag<float> s32[DV / 32];               // S_c rows of key block w (A operand, k = value features)
   Frag<float> sD[DV / 32];                // dS_{c+1} rows of key block w
-  if (w < NBD) {
+  if (NBD == NW || w < NBD) {
 #pragma unroll
     for (int kb = 0; kb < DV / 32; ++kb) {
       s32[kb] = frag_k_f32(Scc, DV, 16 * w, 32 * kb);
       sD[kb] = frag_k_f32(dSc, DV, 16 * w, 32 * kb);
     }
   }
+  GV::template dma_exact<NW>(tO, dO + (size_t)t0 * v_pitch, v_pitch, w, nrows);
+  GV::template dma_exact<NW>(tVn, Vnc, DV, w);
+  GV::template dma_exact<NW>(tdV, dVc, DV, w);
+  __builtin_amdgcn_sched_barrier(0);       // group 2 is issued after all of group 1
   Frag<MT> vf[DV / 32];                   // v rows of column block cb (B operand of dVn V^T)
+  const int tv = t0 + 16 * cb + n;        // this lane's v row
+  {
+    const MT* pv = v + (size_t)(tv < T ? tv : T - 1) * v_pitch + 4 * j;
 #pragma unroll
-  for (int kb = 0; kb < DV / 32; ++kb) vf[kb] = frag_k_seq<MT, MT>(v, v_pitch, t0, T, 16 * cb, 32 * kb, One());
-  GQ::dma(tq, q + (size_t)t0 * qk_pitch, qk_pitch, w, NW, nrows);
-  GQ::dma(tk, k + (size_t)t0 * qk_pitch, qk_pitch, w, NW, nrows);
-  GV::dma(tO, dO + (size_t)t0 * v_pitch, v_pitch, w, NW, nrows);
-  GV::dma(tVn, Vnc, DV, w, NW);
-  GV::dma(tdV, dVc, DV, w, NW);
-  GA::dma(tA, Ac, C, w, NW);
-  if (w == 0) chunk_scalars(cs, a.g, a.beta, s_base, H, t0, T);
+    for (int kb = 0; kb < DV / 32; ++kb) {
+      const bf16x4 lo = *reinterpret_cast<const bf16x4*>(pv + 32 * kb), hi = *reinterpret_cast<const bf16x4*>(pv + 32 * kb + 16);
+      vf[kb].v = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+  }
+  GQ::template dma_exact<NW>(tq, q + (size_t)t0 * qk_pitch, qk_pitch, w, nrows);
+  GQ::template dma_exact<NW>(tk, k + (size_t)t0 * qk_pitch, qk_pitch, w, nrows);
+  GA::template dma_exact<NW>(tA, Ac, C, w);
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vmcnt<2 * GQ::per_wave(NW) + GA::per_wave(NW)>();   // group 1 (the q, k, A copies were issued last)
+  if (tv >= T) {
+#pragma unroll
+    for (int kb = 0; kb < DV / 32; ++kb) vf[kb].v = bf16x8{};
+  }
+  if (w == 0) chunk_scalars_from(cs, t0 + l < T ? gv : 0.f, t0 + l < T ? bv : 0.f, t0, T);
+  // the chunk states in their MFMA forms at once (S_c in bf16; dS_{c+1} as hi + lo bf16: the e k . (Vn dS^T) terms of
+  // dg sum 64 rows of it), and the last-row dg term <S_c, dS_{c+1}> from the fp32 values
+  Frag<MT> fS[DV / 32], dHi[DV / 32], dLo[DV / 32];
+  float sds = 0.f;
+  if (NBD == NW || w < NBD) {
+#pragma unroll
+    for (int kb = 0; kb < DV / 32; ++kb) {
+      fS[kb] = cvt<MT>(s32[kb]);
+      frag_split<MT>(sD[kb], dHi[kb], dLo[kb]);
+#pragma unroll
+      for (int r = 0; r < 8; ++r) sds = fmaf(s32[kb].v[r], sD[kb].v[r], sds);
+    }
+  }
+  lds_barrier();                         // group 1 and the chunk scalars visible
+  if (nrows < C) {                         // rows past the end: zeros in dO
+    constexpr int UV = VP / 8;
+    const int nz = C - nrows;
+    for (int i = threadIdx.x; i < nz * UV; i += blockDim.x)
+      *reinterpret_cast<bf16x8*>(tO + (nrows + i % nz) * VP + 8 * (i / nz)) = bf16x8{};
+    lds_barrier();
+  }
+
+  // ---- B: products with the chunk states, transposed: [key block w] x [token tiles]
+  //   dQ^T = gamma * (S_c dO^T),  dK^T = e * (dS Vn^T),  dW^T = -(S_c dVn^T),  X^T = dW^T A,  dK^T += beta gamma X^T
+  f4 dQt[4], dKt[4];
+  f4 aO[4], aV[4], aD[4];
+  if (w < NBD) {
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) aO[ti] = aV[ti] = aD[ti] = f4{0.f, 0.f, 0.f, 0.f};
+    // stage sg = (value block kb = sg / 2, token tiles 2 (sg % 2) and 2 (sg % 2) + 1): its dO, Vn, dVn fragments are
+    // read one stage ahead of its products
+    constexpr int NS = 2 * (DV / 32);
+    Frag<MT> st[2][6];
+    auto load = [&](int sg, Frag<MT>(&f)[6]) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int ti = 2 * (sg & 1) + u;
+        f[3 * u] = frag_tile<MT, GV>(tO, 16 * ti, 32 * (sg >> 1));
+        f[3 * u + 1] = frag_tile<MT, GV>(tVn, 16 * ti, 32 * (sg >> 1));
+        f[3 * u + 2] = frag_tile<MT, GV>(tdV, 16 * ti, 32 * (sg >> 1));
+      }
+    };
+    load(0, st[0]);
+#pragma unroll
+    for (int sg = 0; sg < NS; ++sg) {
+      if (sg + 1 < NS) load(sg + 1, st[(sg + 1) & 1]);
+      const int kb = sg >> 1;
+      const Frag<MT>(&f)[6] = st[sg & 1];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int ti = 2 * (sg & 1) + u;
+        mma(aO[ti], fS[kb], f[3 * u]);
+        mma(aV[ti], dHi[kb], f[3 * u + 1]);
+        mma(aV[ti], dLo[kb], f[3 * u + 1]);
+        mma(aD[ti], fS[kb], f[3 * u + 2]);
+      }
+    }
+  }
   wait_dma();
-  __syncthreads();
+  lds_barrier();                         // group 2 visible
+  if (nrows < C) {                         // rows past the end: zeros in q and k (the norms read rows < nrows only)
+    constexpr int UQ = KP / 8;
+    const int nz = C - nrows;
+    for (int i = threadIdx.x; i < nz * 2 * UQ; i += blockDim.x) {
+      const int row = nrows + i % nz, u = i / nz;
+      *reinterpret_cast<bf16x8*>(u < UQ ? tq + row * KP + 8 * u : tk + row * KP + 8 * (u - UQ)) = bf16x8{};
+    }
+  }
   if (a.l2norm) {                          // the row norms from the tiles (rows past the end: 0)
     if (w < 4) row_rnorms_lds<DK>(rq, tq, KP, nrows, 4, w);
     else row_rnorms_lds<DK>(rk, tk, KP, nrows, 4, w - 4);
@@ -1514,42 +1604,9 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
     rk[threadIdx.x] = (int)threadIdx.x < nrows ? 1.f : 0.f;
     rq[threadIdx.x] = (int)threadIdx.x < nrows ? 1.f : 0.f;
   }
-  if (nrows < C) {                         // rows past the end: zeros in q, k and dO
-    constexpr int UQ = KP / 8, UV = VP / 8;
-    const int nz = C - nrows;
-    for (int i = threadIdx.x; i < nz * (2 * UQ + UV); i += blockDim.x) {
-      const int row = nrows + i % nz, u = i / nz;
-      MT* p = u < UQ ? tq + row * KP + 8 * u : u < 2 * UQ ? tk + row * KP + 8 * (u - UQ) : tO + row * VP + 8 * (u - 2 * UQ);
-      *reinterpret_cast<bf16x8*>(p) = bf16x8{};
-    }
-  }
-  __syncthreads();                         // norms and zeroed rows visible
-
-  // ---- B: products with the chunk states, transposed: [key block w] x [token tiles]
-  //   dQ^T = gamma * (S_c dO^T),  dK^T = e * (dS Vn^T),  dW^T = -(S_c dVn^T),  X^T = dW^T A,  dK^T += beta gamma X^T
-  f4 dQt[4], dKt[4];
-  float sds = 0.f;
+  lds_barrier();                         // norms visible
   if (w < NBD) {
     const int d0 = 16 * w + 4 * j;        // this lane's 4 key features
-    f4 aO[4], aV[4], aD[4];
-#pragma unroll
-    for (int ti = 0; ti < 4; ++ti) aO[ti] = aV[ti] = aD[ti] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kb = 0; kb < DV / 32; ++kb) {
-      const Frag<MT> fS = cvt<MT>(s32[kb]);
-      Frag<MT> dHi, dLo;                  // dS as hi + lo: the e k . (Vn dS^T) terms of dg sum 64 rows of it
-      frag_split<MT>(sD[kb], dHi, dLo);
-#pragma unroll
-      for (int r = 0; r < 8; ++r) sds = fmaf(s32[kb].v[r], sD[kb].v[r], sds);
-#pragma unroll
-      for (int ti = 0; ti < 4; ++ti) {
-        const Frag<MT> fv = frag_tile<MT, GV>(tVn, 16 * ti, 32 * kb);
-        mma(aO[ti], fS, frag_tile<MT, GV>(tO, 16 * ti, 32 * kb));
-        mma(aV[ti], dHi, fv);
-        mma(aV[ti], dLo, fv);
-        mma(aD[ti], fS, frag_tile<MT, GV>(tdV, 16 * ti, 32 * kb));
-      }
-    }
     float pQD[4], pE[4];
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
@@ -1564,15 +1621,21 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
     }
     // X^T = dW^T A (this wave's own dW^T columns, just written): A is lower triangular
     Frag<MT> fW[2];
+    Frag<MT> fx[4][2];                     // A's nonzero blocks, all read before the products
 #pragma unroll
     for (int p = 0; p < 2; ++p) fW[p] = frag_tr(sdW, KP, 32 * p, 16 * w);
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+        if (32 * p + 31 >= 16 * ti) fx[ti][p] = frag_tr(tA, CP, 32 * p, 16 * ti);
     float pKX[4];
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
       f4 x = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int p = 0; p < 2; ++p)
-        if (32 * p + 31 >= 16 * ti) mma(x, fW[p], frag_tr(tA, CP, 32 * p, 16 * ti));
+        if (32 * p + 31 >= 16 * ti) mma(x, fW[p], fx[ti][p]);
       const int t = 16 * ti + n;
       const f4 k4 = load4(tk + t * KP + d0);
       dKt[ti] += (cs.beta[t] * cs.gam[t]) * x;
@@ -1590,35 +1653,59 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
     sds = across_groups_sum(group16_sum(sds));
     if (l == 0) partS[w] = sds;
   }
-  __syncthreads();
+  lds_barrier();
 
-  // ---- C: the C x C products on this wave's row tiles mi = 2 hh, 2 hh + 1 of column block cb (lower tiles only)
+  // ---- C: the C x C products on this wave's row tiles mi = 2 hh, 2 hh + 1 of column block cb.  Tiles above the
+  // diagonal are computed too (their results are masked to zero below): no wave-dependent branch splits the loop, so the
+  // fragment reads of stage s + 1 are issued before the products of stage s.
   float KG[2][4], gmv[2][4];
   {
     f4 QK[2], KK[2], Ta[2], dOV[2], Tb[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) QK[i] = KK[i] = Ta[i] = dOV[i] = Tb[i] = f4{0.f, 0.f, 0.f, 0.f};
+    // stage s < NP: key features 32 s (B = k rows of block cb; A = q, k, dW rows of the two tiles);
+    // stage NP + kb: value features 32 kb (B = Vn rows of block cb; A = dO rows; A = dVn rows against v)
+    constexpr int NP = DK / 32, NS = NP + DV / 32;
+    Frag<MT> st[2][7];
+    auto load = [&](int sg, Frag<MT>(&f)[7]) {
+      if (sg < NP) {
+        f[0] = frag_tile<MT, GQ>(tk, 16 * cb, 32 * sg);
 #pragma unroll
-    for (int p = 0; p < DK / 32; ++p) {
-      const Frag<MT> bk = frag_tile<MT, GQ>(tk, 16 * cb, 32 * p);
+        for (int i = 0; i < 2; ++i) {
+          const int mi = 2 * hh + i;
+          f[1 + 3 * i] = frag_tile<MT, GQ>(tq, 16 * mi, 32 * sg);
+          f[2 + 3 * i] = frag_tile<MT, GQ>(tk, 16 * mi, 32 * sg);
+          f[3 + 3 * i] = frag_k_raw(sdW, KP, 16 * mi, 32 * sg);
+        }
+      } else {
+        const int kb = sg - NP;
+        f[0] = frag_tile<MT, GV>(tVn, 16 * cb, 32 * kb);
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int mi = 2 * hh + i;
-        if (mi < cb) continue;
-        mma(QK[i], frag_tile<MT, GQ>(tq, 16 * mi, 32 * p), bk);
-        mma(KK[i], frag_tile<MT, GQ>(tk, 16 * mi, 32 * p), bk);
-        mma(Ta[i], frag_k_raw(sdW, KP, 16 * mi, 32 * p), bk);
+        for (int i = 0; i < 2; ++i) {
+          const int mi = 2 * hh + i;
+          f[1 + 2 * i] = frag_tile<MT, GV>(tO, 16 * mi, 32 * kb);
+          f[2 + 2 * i] = frag_tile<MT, GV>(tdV, 16 * mi, 32 * kb);
+        }
       }
-    }
+    };
+    load(0, st[0]);
 #pragma unroll
-    for (int kb = 0; kb < DV / 32; ++kb) {
-      const Frag<MT> bvn = frag_tile<MT, GV>(tVn, 16 * cb, 32 * kb);
+    for (int sg = 0; sg < NS; ++sg) {
+      if (sg + 1 < NS) load(sg + 1, st[(sg + 1) & 1]);
+      const Frag<MT>(&f)[7] = st[sg & 1];
+      if (sg < NP) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int mi = 2 * hh + i;
-        if (mi < cb) continue;
-        mma(dOV[i], frag_tile<MT, GV>(tO, 16 * mi, 32 * kb), bvn);
-        mma(Tb[i], frag_tile<MT, GV>(tdV, 16 * mi, 32 * kb), vf[kb]);
+        for (int i = 0; i < 2; ++i) {
+          mma(QK[i], f[1 + 3 * i], f[0]);
+          mma(KK[i], f[2 + 3 * i], f[0]);
+          mma(Ta[i], f[3 + 3 * i], f[0]);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          mma(dOV[i], f[1 + 2 * i], f[0]);
+          mma(Tb[i], f[2 + 2 * i], vf[sg - NP]);
+        }
       }
     }
     const int s = 16 * cb + n;
@@ -1657,39 +1744,45 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
     cR1 = across_groups_sum(cR1);
     if (j == 0) colp[0][hh][s] = cR1;
   }
-  __syncthreads();
+  lds_barrier();
   // dO is consumed: v takes its tile (needed from E on)
-  GV::dma(tO, v + (size_t)t0 * v_pitch, v_pitch, w, NW, nrows);
+  GV::template dma_exact<NW>(tO, v + (size_t)t0 * v_pitch, v_pitch, w, nrows);
 
   // ---- T1 = dA A^T (column block cb, all four row tiles), then dL = strictLower(-A^T T1) on this wave's tiles
   {
     f4 T1[4];
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) T1[mi] = f4{0.f, 0.f, 0.f, 0.f};
+    // every operand read first; blocks of A above the diagonal are zero, so no wave-dependent skip is needed
+    Frag<MT> bA[2], fz[6];
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      if (32 * p > 16 * cb + 15) continue;
-      const Frag<MT> bA = frag_tile<MT, GA>(tA, 16 * cb, 32 * p);   // B[s][t'] = A[t'][s]
+    for (int p = 0; p < 2; ++p) bA[p] = frag_tile<MT, GA>(tA, 16 * cb, 32 * p);   // B[s][t'] = A[t'][s]
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
-        if (32 * p <= 16 * mi + 15) mma(T1[mi], frag_tr(sAZ, CP, 32 * p, 16 * mi), bA);
-    }
-    __syncthreads();                       // every wave has read dA^T: Z may overwrite it
+    for (int mi = 0; mi < 4; ++mi) fz[mi] = frag_tr(sAZ, CP, 0, 16 * mi);
+    fz[4] = frag_tr(sAZ, CP, 32, 32);
+    fz[5] = frag_tr(sAZ, CP, 32, 48);
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) mma(T1[mi], fz[mi], bA[0]);
+    mma(T1[2], fz[4], bA[1]);              // dA is strictly lower: rows 0-31 have no terms at t' >= 32
+    mma(T1[3], fz[5], bA[1]);
+    lds_barrier();                       // every wave has read dA^T: Z may overwrite it
     Frag<MT> T1f[2];
 #pragma unroll
     for (int p = 0; p < 2; ++p) T1f[p] = frag_acc<MT>(T1[2 * p], T1[2 * p + 1]);
     const int s = 16 * cb + n;
     const float rks = rk[s];
     float pR2[8], cR2 = 0.f;
+    Frag<MT> fa[2][2];                     // A^T rows of the two tiles (A's zero upper blocks included)
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int p = 0; p < 2; ++p) fa[i][p] = frag_tr(tA, CP, 32 * p, 16 * (2 * hh + i));
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int mi = 2 * hh + i, r0 = 16 * mi + 4 * j;
-      f4 dL = {0.f, 0.f, 0.f, 0.f};
-      if (mi >= cb) {
+      f4 dL = {0.f, 0.f, 0.f, 0.f};       // tiles above the diagonal (mi < cb) are masked by row > s below
 #pragma unroll
-        for (int p = 0; p < 2; ++p)
-          if (32 * p + 31 >= 16 * mi) mma(dL, frag_tr(tA, CP, 32 * p, 16 * mi), T1f[p]);
-      }
+      for (int p = 0; p < 2; ++p) mma(dL, fa[i][p], T1f[p]);
       const f4 rk4 = *reinterpret_cast<const f4*>(rk + r0), b4 = *reinterpret_cast<const f4*>(cs.beta + r0);
       float zt[4];
 #pragma unroll
@@ -1723,7 +1816,7 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
     cR2 = across_groups_sum(cR2);
     if (j == 0) colp[1][hh][s] = cR2;
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- D: dQ^T += k^T (dM diag(rk))^T;  dK^T += q^T (diag(rq qs) dM) + k^T (diag(rk) Z)   (key block w)
   if (w < NBD) {
@@ -1733,13 +1826,26 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
       kT[p] = frag_tr(tk, KP, 32 * p, 16 * w);
       qT[p] = frag_tr(tq, KP, 32 * p, 16 * w);
     }
-#pragma unroll
-    for (int ti = 0; ti < 4; ++ti) {
+    // token tile ti is one stage: its dM and Z fragments are read one stage ahead of its products
+    Frag<MT> st[2][6];
+    auto load = [&](int ti, Frag<MT>(&f)[6]) {
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        if (32 * p <= 16 * ti + 15) mma(dQt[ti], kT[p], frag_tr(sMkT, CP, 32 * p, 16 * ti));
-        if (32 * p + 31 >= 16 * ti) mma(dKt[ti], qT[p], frag_k_raw(sMqT, CP, 16 * ti, 32 * p));
-        mma(dKt[ti], kT[p], frag_k_raw(sAZ, CP, 16 * ti, 32 * p));
+        if (32 * p <= 16 * ti + 15) f[3 * p] = frag_tr(sMkT, CP, 32 * p, 16 * ti);
+        if (32 * p + 31 >= 16 * ti) f[3 * p + 1] = frag_k_raw(sMqT, CP, 16 * ti, 32 * p);
+        f[3 * p + 2] = frag_k_raw(sAZ, CP, 16 * ti, 32 * p);
+      }
+    };
+    load(0, st[0]);
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti) {
+      if (ti + 1 < 4) load(ti + 1, st[(ti + 1) & 1]);
+      const Frag<MT>(&f)[6] = st[ti & 1];
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        if (32 * p <= 16 * ti + 15) mma(dQt[ti], kT[p], f[3 * p]);
+        if (32 * p + 31 >= 16 * ti) mma(dKt[ti], qT[p], f[3 * p + 1]);
+        mma(dKt[ti], kT[p], f[3 * p + 2]);
       }
     }
     if (a.l2norm) {
@@ -1760,20 +1866,26 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
     }
   }
   wait_dma();                              // v
-  __syncthreads();
+  lds_barrier();
 
   // ---- E: Y^T = dVn^T A (value block w), dv = beta Y staged in Vn's tile, v . Y row sums
   if (w < NBV) {
     const int c0 = 16 * w + 4 * j;        // this lane's 4 value features
     Frag<MT> fdv[2];
+    Frag<MT> fy[4][2];
 #pragma unroll
     for (int p = 0; p < 2; ++p) fdv[p] = frag_tr(tdV, VP, 32 * p, 16 * w);
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+        if (32 * p + 31 >= 16 * ti) fy[ti][p] = frag_tr(tA, CP, 32 * p, 16 * ti);
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
       f4 y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int p = 0; p < 2; ++p)
-        if (32 * p + 31 >= 16 * ti) mma(y, fdv[p], frag_tr(tA, CP, 32 * p, 16 * ti));
+        if (32 * p + 31 >= 16 * ti) mma(y, fdv[p], fy[ti][p]);
       const int t = 16 * ti + n;
       const float bt = cs.beta[t];
       *reinterpret_cast<bf16x4*>(tVn + t * VP + c0) = bf16x4{(bf16)(bt * y[0]), (bf16)(bt * y[1]), (bf16)(bt * y[2]),
@@ -1783,7 +1895,7 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
       if (j == 0) part[P_VY][w][t] = s1;
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- F: dbeta and dg (wave 0, lane = chunk row), fixed-order sums of the partials
   if (w == 0) {
@@ -1839,7 +1951,7 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
       }
     }
   }
-  __syncthreads();                         // q and k tiles are read: they become the dq and dk staging
+  lds_barrier();                         // q and k tiles are read: they become the dq and dk staging
   if (w < NBD) {
     const int d0 = 16 * w + 4 * j;
 #pragma unroll
@@ -1851,7 +1963,7 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
           bf16x4{(bf16)gk[ti][0], (bf16)gk[ti][1], (bf16)gk[ti][2], (bf16)gk[ti][3]};
     }
   }
-  __syncthreads();
+  lds_barrier();
   // whole rows out: 16 bytes per lane
   {
     constexpr int UK = DK / 8, UV = DV / 8;

@@ -46,6 +46,26 @@ struct Tile {
         __builtin_amdgcn_global_load_lds((const void*)(g + off[k]), (lds_void*)(base + i * 64 * EPU), 16, 0, 0);
     }
   }
+  // dma() with every wave issuing exactly per_wave(NW) copy instructions, unrolled and branch-free (a wave past the
+  // tile's last instruction repeats it, writing the same bytes again), so that the number of loads a wave has issued
+  // after the copy is a compile-time constant and a partial vmcnt wait can follow it.  The copies are buffer loads
+  // (buffer_load_dwordx4 ... lds, LDS base in M0) rather than global_load_lds: with a FLAT-encoded copy in flight the
+  // compiler can no longer order the vector-memory counter and waits for zero before every use of a loaded register.
+  // Byte offsets within the tile must fit 31 bits.
+  template <int NW>
+  __device__ static __forceinline__ void dma_exact(T* base, const T* g, size_t gpitch, int w, int nrows = R) {
+    const int l = lane_id();
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)g, 0, 0x7fffffff, 0x00020000);
+#pragma unroll
+    for (int k = 0; k < per_wave(NW); ++k) {
+      const int i = w + k * NW < NI ? w + k * NW : NI - 1;
+      const int u = i * 64 + l;
+      const int row = u / RU, cu = u - row * RU;
+      int off = 0;
+      if (row < R && cu < PU) off = (int)(((size_t)(row < nrows ? row : nrows - 1) * gpitch + cu * EPU) * sizeof(T));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(base + i * 64 * EPU), 16, off, 0, 0, 0);
+    }
+  }
   // Copy a global tile (row r at g + r * gpitch; rows >= nrows re-read row nrows - 1, to be masked by the reader) into
   // LDS `base`; waves w, w + nw, ... share the wave instructions.
   __device__ static __forceinline__ void dma(T* base, const T* g, size_t gpitch, int w, int nw, int nrows = R) {
@@ -92,6 +112,15 @@ __device__ __forceinline__ Frag<MT> frag_tile_rows(const MT* base, int krow0, in
 }
 
 __device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0); }
+
+// Wait until at most N vector-memory operations of this wave are outstanding (gfx9 s_waitcnt: vmcnt in bits 3:0 and
+// 15:14, expcnt and lgkmcnt left at their maxima).  Loads retire in issue order, so this waits for everything issued
+// before the last N.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 
 // ---- gfx950 LDS transpose reads (ds_read_b64_tr_b16) ---------------------------------------------------------------
 // In each 16-lane group, lane s supplies the address of 4 consecutive 16-bit elements; lane i receives element i % 4 of
