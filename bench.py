@@ -31,8 +31,8 @@ C = 64
 # HBM bytes per launch at config 1 from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (profiles/gated_delta_config1.md),
 # FETCH_SIZE scaled by 2.000 and WRITE_SIZE by 1.000 (the factors a plain 256 MiB device copy gives); the two prep
 # launches are profiled together (their average)
-TRAFFIC = {1: {"chunk_bwd": 304.8e6, "state_bwd": 163.8e6, "state_fwd_store": 151.3e6, "state_fwd_out": 109.3e6,
-               "prep_fwd": 147.6e6, "prep_bwd": 147.6e6}}
+TRAFFIC = {1: {"chunk_bwd": 304.8e6, "state_pair": 311.6e6, "state_bwd": 163.8e6, "state_fwd_store": 151.2e6,
+               "state_fwd_out": 109.3e6, "prep_fwd": 147.6e6, "prep_bwd": 147.6e6}}
 
 CONFIGS = {
     1: dict(B=4, T=1024, Hk=16, Hv=16, DK=128, DV=128, s0=False),
