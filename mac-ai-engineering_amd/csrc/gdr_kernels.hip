@@ -1508,7 +1508,8 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   GV::template dma_exact<NW>(tO, dO + (size_t)t0 * v_pitch, v_pitch, w, nrows);
   GV::template dma_exact<NW>(tVn, Vnc, DV, w);
   GV::template dma_exact<NW>(tdV, dVc, DV, w);
-  __builtin_amdgcn_sched_barrier(0);       // group 2 is issued after all of group 1
+  wait_dma();                              // group 1 (and g, beta) has landed
+  __builtin_amdgcn_sched_barrier(0);       // group 2 is issued only now: it lands while the state products run
   Frag<MT> vf[DV / 32];                   // v rows of column block cb (B operand of dVn V^T)
   const int tv = t0 + 16 * cb + n;        // this lane's v row
   {
@@ -1523,11 +1524,6 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   GQ::template dma_exact<NW>(tk, k + (size_t)t0 * qk_pitch, qk_pitch, w, nrows);
   GA::template dma_exact<NW>(tA, Ac, C, w);
   __builtin_amdgcn_sched_barrier(0);
-  wait_vmcnt<2 * GQ::per_wave(NW) + GA::per_wave(NW)>();   // group 1 (the q, k, A copies were issued last)
-  if (tv >= T) {
-#pragma unroll
-    for (int kb = 0; kb < DV / 32; ++kb) vf[kb].v = bf16x8{};
-  }
   if (w == 0) chunk_scalars_from(cs, t0 + l < T ? gv : 0.f, t0 + l < T ? bv : 0.f, t0, T);
   // the chunk states in their MFMA forms at once (S_c in bf16; dS_{c+1} as hi + lo bf16: the e k . (Vn dS^T) terms of
   // dg sum 64 rows of it), and the last-row dg term <S_c, dS_{c+1}> from the fp32 values
@@ -1589,6 +1585,10 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   }
   wait_dma();
   lds_barrier();                         // group 2 visible
+  if (tv >= T) {                           // v rows past the end
+#pragma unroll
+    for (int kb = 0; kb < DV / 32; ++kb) vf[kb].v = bf16x8{};
+  }
   if (nrows < C) {                         // rows past the end: zeros in q and k (the norms read rows < nrows only)
     constexpr int UQ = KP / 8;
     const int nz = C - nrows;
