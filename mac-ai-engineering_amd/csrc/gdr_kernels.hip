@@ -1509,21 +1509,27 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   GV::template dma_exact<NW>(tVn, Vnc, DV, w);
   GV::template dma_exact<NW>(tdV, dVc, DV, w);
   wait_dma();                              // group 1 (and g, beta) has landed
-  __builtin_amdgcn_sched_barrier(0);       // group 2 is issued only now: it lands while the state products run
+  // Group 2 -- the v fragments and the q, k, A tile units -- goes through registers. Its loads are spread over the
+  // state products' stages below: an issue stalls while the memory system is saturated, so issuing them all here
+  // would hold the products back. The tile units are written to LDS after the products.
+  constexpr int NQ = GQ::per_wave(NW), NA = GA::per_wave(NW);
+  constexpr int NG2 = DV / 32 + 2 * NQ + NA;                   // load slots: v fragments, q units, k units, A units
   Frag<MT> vf[DV / 32];                   // v rows of column block cb (B operand of dVn V^T)
+  u32x4 uq[NQ], uk[NQ], ua[NA];
   const int tv = t0 + 16 * cb + n;        // this lane's v row
-  {
-    const MT* pv = v + (size_t)(tv < T ? tv : T - 1) * v_pitch + 4 * j;
-#pragma unroll
-    for (int kb = 0; kb < DV / 32; ++kb) {
-      const bf16x4 lo = *reinterpret_cast<const bf16x4*>(pv + 32 * kb), hi = *reinterpret_cast<const bf16x4*>(pv + 32 * kb + 16);
-      vf[kb].v = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  const MT* const pv = v + (size_t)(tv < T ? tv : T - 1) * v_pitch + 4 * j;
+  auto issue_g2 = [&](int sl) {
+    if (sl < DV / 32) {
+      const bf16x4 lo = *reinterpret_cast<const bf16x4*>(pv + 32 * sl), hi = *reinterpret_cast<const bf16x4*>(pv + 32 * sl + 16);
+      vf[sl].v = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    } else if (sl < DV / 32 + NQ) {
+      uq[sl - DV / 32] = GQ::template load_unit<NW>(q + (size_t)t0 * qk_pitch, qk_pitch, w, sl - DV / 32, nrows);
+    } else if (sl < DV / 32 + 2 * NQ) {
+      uk[sl - DV / 32 - NQ] = GQ::template load_unit<NW>(k + (size_t)t0 * qk_pitch, qk_pitch, w, sl - DV / 32 - NQ, nrows);
+    } else if (sl < NG2) {
+      ua[sl - DV / 32 - 2 * NQ] = GA::template load_unit<NW>(Ac, C, w, sl - DV / 32 - 2 * NQ);
     }
-  }
-  GQ::template dma_exact<NW>(tq, q + (size_t)t0 * qk_pitch, qk_pitch, w, nrows);
-  GQ::template dma_exact<NW>(tk, k + (size_t)t0 * qk_pitch, qk_pitch, w, nrows);
-  GA::template dma_exact<NW>(tA, Ac, C, w);
-  __builtin_amdgcn_sched_barrier(0);
+  };
   if (w == 0) chunk_scalars_from(cs, t0 + l < T ? gv : 0.f, t0 + l < T ? bv : 0.f, t0, T);
   // the chunk states in their MFMA forms at once (S_c in bf16; dS_{c+1} as hi + lo bf16: the e k . (Vn dS^T) terms of
   // dg sum 64 rows of it), and the last-row dg term <S_c, dS_{c+1}> from the fp32 values
@@ -1551,12 +1557,12 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   //   dQ^T = gamma * (S_c dO^T),  dK^T = e * (dS Vn^T),  dW^T = -(S_c dVn^T),  X^T = dW^T A,  dK^T += beta gamma X^T
   f4 dQt[4], dKt[4];
   f4 aO[4], aV[4], aD[4];
-  if (w < NBD) {
+  constexpr int NS = 2 * (DV / 32), PER = (NG2 + NS - 1) / NS;   // stages; group-2 loads issued per stage
+  if (NBD == NW || w < NBD) {
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) aO[ti] = aV[ti] = aD[ti] = f4{0.f, 0.f, 0.f, 0.f};
     // stage sg = (value block kb = sg / 2, token tiles 2 (sg % 2) and 2 (sg % 2) + 1): its dO, Vn, dVn fragments are
     // read one stage ahead of its products
-    constexpr int NS = 2 * (DV / 32);
     Frag<MT> st[2][6];
     auto load = [&](int sg, Frag<MT>(&f)[6]) {
 #pragma unroll
@@ -1570,6 +1576,8 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
     load(0, st[0]);
 #pragma unroll
     for (int sg = 0; sg < NS; ++sg) {
+#pragma unroll
+      for (int p = 0; p < PER; ++p) issue_g2(PER * sg + p);
       if (sg + 1 < NS) load(sg + 1, st[(sg + 1) & 1]);
       const int kb = sg >> 1;
       const Frag<MT>(&f)[6] = st[sg & 1];
@@ -1582,8 +1590,18 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
         mma(aD[ti], fS[kb], f[3 * u + 2]);
       }
     }
+  } else {
+#pragma unroll
+    for (int sl = 0; sl < NG2; ++sl) issue_g2(sl);
   }
-  wait_dma();
+  wait_dma();                              // group 2 is in registers
+#pragma unroll
+  for (int u = 0; u < NQ; ++u) {
+    GQ::template store_unit<NW>(tq, w, u, uq[u]);
+    GQ::template store_unit<NW>(tk, w, u, uk[u]);
+  }
+#pragma unroll
+  for (int u = 0; u < NA; ++u) GA::template store_unit<NW>(tA, w, u, ua[u]);
   lds_barrier();                         // group 2 visible
   if (tv >= T) {                           // v rows past the end
 #pragma unroll

@@ -11,6 +11,7 @@
 namespace gdr {
 
 typedef __attribute__((address_space(3))) void lds_void;
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 template <typename T, int R, int COLS>
 struct Tile {
@@ -65,6 +66,24 @@ struct Tile {
       if (row < R && cu < PU) off = (int)(((size_t)(row < nrows ? row : nrows - 1) * gpitch + cu * EPU) * sizeof(T));
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(base + i * 64 * EPU), 16, off, 0, 0, 0);
     }
+  }
+  // The same copy through registers, one instruction's unit at a time: load_unit(k) reads the 16 bytes that
+  // dma_exact's k-th instruction of wave w would move for this lane, store_unit(k) writes them to the same LDS place.
+  // Loads issued this way are ordinary register loads, so they can be spread between other work without the compiler
+  // treating every LDS read as dependent on them (which it does for copies into LDS in flight).
+  template <int NW>
+  __device__ static __forceinline__ u32x4 load_unit(const T* g, size_t gpitch, int w, int k, int nrows = R) {
+    const int i = w + k * NW < NI ? w + k * NW : NI - 1;
+    const int u = i * 64 + lane_id();
+    const int row = u / RU, cu = u - row * RU;
+    const T* src = g;
+    if (row < R && cu < PU) src = g + (size_t)(row < nrows ? row : nrows - 1) * gpitch + cu * EPU;
+    return *reinterpret_cast<const u32x4*>(src);
+  }
+  template <int NW>
+  __device__ static __forceinline__ void store_unit(T* base, int w, int k, u32x4 x) {
+    const int i = w + k * NW < NI ? w + k * NW : NI - 1;
+    *reinterpret_cast<u32x4*>(base + i * 64 * EPU + lane_id() * EPU) = x;
   }
   // Copy a global tile (row r at g + r * gpitch; rows >= nrows re-read row nrows - 1, to be masked by the reader) into
   // LDS `base`; waves w, w + nw, ... share the wave instructions.
