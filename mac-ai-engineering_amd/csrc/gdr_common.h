@@ -74,6 +74,12 @@ __device__ __forceinline__ f4 load4(const bf16* p) {
   bf16x4 x = *reinterpret_cast<const bf16x4*>(p);
   return f4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
 }
+// 4 contiguous values to memory (one 16-byte store for fp32, one 8-byte store for bf16)
+template <typename T> __device__ __forceinline__ void store4(T* p, const f4& x);
+template <> __device__ __forceinline__ void store4<float>(float* p, const f4& x) { *reinterpret_cast<f4*>(p) = x; }
+template <> __device__ __forceinline__ void store4<bf16>(bf16* p, const f4& x) {
+  *reinterpret_cast<bf16x4*>(p) = bf16x4{(bf16)x[0], (bf16)x[1], (bf16)x[2], (bf16)x[3]};
+}
 
 // Fragment of a k-contiguous ("row-major along k") matrix X: lane takes row `row0 + l % 16`, k-block at k0.  For an A
 // operand X = A ([m][k]); for a B operand X = B^T ([n][k]).  `scale` multiplies the values before rounding to MT.

@@ -668,14 +668,14 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
   };
   // results go out as soon as they exist, after the next chunk's U loads are issued (vmcnt is in order, so waiting on
   // those loads never waits on the stores)
-  auto store_o = [&](int c, const f4 (&O)[4]) {
+  // O^T tiles: lane l holds O[16 mi + l % 16][v0 + 4 j + 0..3], four adjacent outputs of one token (one 8- or
+  // 16-byte store each)
+  auto store_o = [&](int c, const f4 (&Ot)[4]) {
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = c * C + 16 * mi + 4 * j + r;
-        if (t < T) ((MT*)a.o)[o_base + (size_t)t * o_pitch + col] = from_f<MT>(O[mi][r]);
-      }
+    for (int mi = 0; mi < 4; ++mi) {
+      const int t = c * C + 16 * mi + (l & 15);
+      if (t < T) store4<MT>((MT*)a.o + o_base + (size_t)t * o_pitch + v0 + 4 * j, Ot[mi]);
+    }
   };
   auto store_sc = [&](int c, const f4 (&X)[ND]) {
     float* Scc = a.Sc + ((size_t)hr * NT + c) * DK * DV + (size_t)(4 * j) * DV + col;
@@ -781,18 +781,19 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
         for (int p = 0; p < 2; ++p)
           if (32 * p <= 16 * mi + 15) fm[mi][p] = frag_tile<MT, GM>(st + O_M, 16 * mi, 32 * p);
       }
+      // O^T = S^T (diag(gamma) Q)^T + Vn^T M^T: the same fragments with A and B swapped
       f4 pO[4];
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) pO[mi] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int p = 0; p < ND / 2; ++p)
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi) mma(pO[mi], fq[mi][p], Sf[p]);
+        for (int mi = 0; mi < 4; ++mi) mma(pO[mi], Sf[p], fq[mi][p]);
 #pragma unroll
       for (int p = 0; p < 2; ++p)
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi)
-          if (32 * p <= 16 * mi + 15) mma(pO[mi], fm[mi][p], Vf[p]);
+          if (32 * p <= 16 * mi + 15) mma(pO[mi], Vf[p], fm[mi][p]);
       store_o(c, pO);
     }
 #pragma unroll
