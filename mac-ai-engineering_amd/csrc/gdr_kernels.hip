@@ -585,9 +585,9 @@ __device__ __forceinline__ void load_state(f4 (&S)[ND], const float* src, size_t
 
 // double-buffer the chunk stages when two fit in LDS
 constexpr int LDS_BYTES = 160 * 1024 - 2048;
-template <int STAGE_BYTES>
+template <int STAGE_BYTES, int EXTRA_BYTES = 0>
 struct Buffers {
-  static constexpr int N = (2 * STAGE_BYTES <= LDS_BYTES) ? 2 : 1;
+  static constexpr int N = (2 * STAGE_BYTES + EXTRA_BYTES <= LDS_BYTES) ? 2 : 1;
 };
 
 // ---------------------------------------------------------------------------------------------------------------------
@@ -595,20 +595,23 @@ struct Buffers {
 // the output, diag(gamma) Q^ and M into a swizzled LDS stage by asynchronous copies -- the next chunk's copies are in
 // flight while this chunk's MFMAs run -- and each wave keeps its 16 columns of S in accumulators.
 // ---------------------------------------------------------------------------------------------------------------------
-template <typename MT, int DK, bool OUT>
+template <typename MT, int DK, bool OUT, int NW>
 struct StateFwdLds {
   using GW = Tile<MT, C, DK>;    // W, diag(e) K^, diag(gamma) Q^     [t][d]
   using GM = Tile<MT, C, C>;     // M                                  [t][s]
   static constexpr int O_KE = GW::ELEMS, O_Q = O_KE + GW::ELEMS, O_M = O_Q + (OUT ? GW::ELEMS : 0);
   static constexpr int SZ = O_M + (OUT ? GM::ELEMS : 0);
-  static constexpr int NBUF = Buffers<SZ * (int)sizeof(MT)>::N;
-  static constexpr int ELEMS = NBUF * SZ;
+  // bf16 Vn leaves through per-wave row staging (store mode)
+  static constexpr int STG = (!OUT && sizeof(MT) == 2) ? NW * ColStage::ELEMS : 0;
+  static constexpr int NBUF = Buffers<SZ * (int)sizeof(MT), STG * (int)sizeof(MT)>::N;
+  static constexpr int O_STG = NBUF * SZ;
+  static constexpr int ELEMS = O_STG + STG;
 };
 
 // The pass of workgroup f of the launch (see state_map), with `lds` the workgroup's LDS (StateFwdLds::ELEMS elements).
 template <typename MT, int DK, int NW, bool OUT, bool STORE>
 __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, int f) {
-  using L = StateFwdLds<MT, DK, OUT>;
+  using L = StateFwdLds<MT, DK, OUT, NW>;
   using GW = typename L::GW;
   using GM = typename L::GM;
   constexpr int ND = DK / 16;
@@ -685,11 +688,15 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
       for (int r = 0; r < 4; ++r) Scc[(16 * di + r) * DV] = X[di][r];
   };
   auto store_vn = [&](int c, const f4 (&X)[4]) {
-    MT* Vnc = (MT*)a.Vn + ((size_t)hr * NT + c) * C * DV + (size_t)(4 * j) * DV + col;
+    if constexpr (sizeof(MT) == 2) {
+      store_cols(lds + L::O_STG + w * ColStage::ELEMS, (MT*)a.Vn + ((size_t)hr * NT + c) * C * DV + v0, DV, X);
+    } else {
+      MT* Vnc = (MT*)a.Vn + ((size_t)hr * NT + c) * C * DV + (size_t)(4 * j) * DV + col;
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+      for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) Vnc[(16 * mi + r) * DV] = from_f<MT>(X[mi][r]);
+        for (int r = 0; r < 4; ++r) Vnc[(16 * mi + r) * DV] = from_f<MT>(X[mi][r]);
+    }
   };
 
   f4 S[ND];
@@ -810,7 +817,7 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
 
 template <typename MT, int DK, int NW, bool OUT, bool STORE>
 __global__ void __launch_bounds__(64 * (NW + 1)) state_fwd_kernel(StateFwdArgs a) {
-  __shared__ __attribute__((aligned(1024))) MT lds[StateFwdLds<MT, DK, OUT>::ELEMS];
+  __shared__ __attribute__((aligned(1024))) MT lds[StateFwdLds<MT, DK, OUT, NW>::ELEMS];
   state_fwd_body<MT, DK, NW, OUT, STORE>(a, lds, blockIdx.x);
 }
 
@@ -824,8 +831,10 @@ struct StateBwdLds {
   using GO = Tile<MT, C, 16 * NW>;   // dO columns                       [t][v]
   static constexpr int O_Q = GK::ELEMS, O_W = O_Q + GK::ELEMS, O_M = O_W + GK::ELEMS, O_O = O_M + GM::ELEMS;
   static constexpr int SZ = O_O + GO::ELEMS;
-  static constexpr int NBUF = Buffers<SZ * (int)sizeof(MT)>::N;
-  static constexpr int ELEMS = NBUF * SZ;
+  static constexpr int STG = sizeof(MT) == 2 ? NW * ColStage::ELEMS : 0;   // bf16 dVn leaves through row staging
+  static constexpr int NBUF = Buffers<SZ * (int)sizeof(MT), STG * (int)sizeof(MT)>::N;
+  static constexpr int O_STG = NBUF * SZ;
+  static constexpr int ELEMS = O_STG + STG;
 };
 
 template <typename MT, int DK, int NW>
@@ -892,11 +901,15 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
       for (int r = 0; r < 4; ++r) dSc[(16 * di + r) * DV] = X[di][r];
   };
   auto store_dv = [&](int c, const f4 (&X)[4]) {
-    MT* dVc = (MT*)a.dVn + ((size_t)hr * NT + c) * C * DV + (size_t)(4 * j) * DV + col;
+    if constexpr (sizeof(MT) == 2) {
+      store_cols(lds + L::O_STG + w * ColStage::ELEMS, (MT*)a.dVn + ((size_t)hr * NT + c) * C * DV + vg + 16 * w, DV, X);
+    } else {
+      MT* dVc = (MT*)a.dVn + ((size_t)hr * NT + c) * C * DV + (size_t)(4 * j) * DV + col;
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+      for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) dVc[(16 * mi + r) * DV] = from_f<MT>(X[mi][r]);
+        for (int r = 0; r < 4; ++r) dVc[(16 * mi + r) * DV] = from_f<MT>(X[mi][r]);
+    }
   };
 
   f4 dS[ND];
@@ -985,7 +998,7 @@ __global__ void __launch_bounds__(64 * (NW + 1)) state_bwd_kernel(StateBwdArgs a
 // stream synchronisation between them.
 template <typename MT, int DK, int NW>
 __global__ void __launch_bounds__(64 * (NW + 1)) state_pair_kernel(StateFwdArgs af, StateBwdArgs ab, int nfwd) {
-  constexpr int EF = StateFwdLds<MT, DK, false>::ELEMS, EB = StateBwdLds<MT, DK, NW>::ELEMS;
+  constexpr int EF = StateFwdLds<MT, DK, false, NW>::ELEMS, EB = StateBwdLds<MT, DK, NW>::ELEMS;
   __shared__ __attribute__((aligned(1024))) MT lds[EF > EB ? EF : EB];
   if ((int)blockIdx.x < nfwd) state_fwd_body<MT, DK, NW, false, true>(af, lds, blockIdx.x);
   else state_bwd_body<MT, DK, NW>(ab, lds, blockIdx.x - nfwd);

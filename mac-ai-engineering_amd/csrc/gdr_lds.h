@@ -175,4 +175,24 @@ __device__ __forceinline__ f4 acc_tr(const bf16* X, int pitch, int r0, int c0) {
   return f4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
 }
 
+// Storing a wave's 64 x 16 block of bf16 results held in accumulator layout (lane l: rows 16 mi + 4 j + r, column
+// l % 16) as whole 16-byte row pieces instead of 16 two-byte stores per lane: the lane's values go to a per-wave LDS
+// staging area and come back by rows.  A wave's LDS accesses execute in order, so no barrier is involved.
+struct ColStage {
+  static constexpr int P = 24;                   // row pitch (elements): 48 bytes, 16-byte aligned rows
+  static constexpr int ELEMS = 64 * P;
+};
+__device__ __forceinline__ void store_cols(bf16* stg, bf16* g, size_t gpitch, const f4 (&X)[4]) {
+  const int l = lane_id(), j = l >> 4, n = l & 15;
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) stg[(16 * mi + 4 * j + r) * ColStage::P + n] = (bf16)X[mi][r];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {                  // 128 units: row u / 2, columns 8 (u % 2) .. + 7
+    const int u = 64 * k + l, row = u >> 1, cu = u & 1;
+    *reinterpret_cast<u32x4*>(g + row * gpitch + 8 * cu) = *reinterpret_cast<const u32x4*>(stg + row * ColStage::P + 8 * cu);
+  }
+}
+
 }  // namespace gdr
