@@ -241,51 +241,52 @@ __device__ __forceinline__ void chunk_scalars(ChunkScalars& cs, const float* g, 
 }
 
 // ---- row norms ----------------------------------------------------------------------------------------------------
-// Inverse l2 norm of chunk rows: rinv = 1 / sqrt(sum x^2 + eps).  Every kernel computes it with this one routine: a row
-// is summed by the 16 lanes of a lane group, each over D/16 consecutive elements in order, then a fixed butterfly, so
-// all kernels produce the same bits.  Wave w (of the nwaves taking part) handles rows w*4 + (l/16), stepping by
-// 4 * nwaves.
+// 1 / sqrt(|x_r|^2 + eps) of chunk rows r (the prologue's l2norm, eps 1e-6), 0 past the sequence end.  One pass covers
+// 16 rows per wave: lane l takes row l / 4 and sums the squares of x[r][32 s + 8 (l % 4) + i] in (s, i) order; the
+// four partial sums of a row combine as (a + b) + (c + d) in every lane.  The global and the LDS versions follow the
+// same order, so every kernel computes the same bits.
+__device__ __forceinline__ float row4_sum(float x) {
+  const float y = x + dpp<DPP_XOR1>(x);
+  return y + dpp<DPP_XOR2>(y);
+}
 template <typename IT, int D>
 __device__ __forceinline__ void row_rnorms(float* out, const IT* x, size_t row_base, size_t row_stride, int t0, int T,
                                            int nwaves, int w = wave_id()) {
-  const int l = lane_id();
-  constexpr int PER = D / 16;
-  for (int r0 = w * 4; r0 < C; r0 += 4 * nwaves) {
-    const int r = r0 + (l >> 4);
-    const int t = t0 + r;
+  const int l = lane_id(), part = l & 3;
+  for (int r0 = 16 * w; r0 < C; r0 += 16 * nwaves) {
+    const int r = r0 + (l >> 2), t = t0 + r;
+    const IT* p = x + row_base + (size_t)(t < T ? t : T - 1) * row_stride + 8 * part;   // rows past T: masked below
     float ss = 0.f;
-    if (t < T) {
-      const IT* p = x + row_base + (size_t)t * row_stride + (l & 15) * PER;
 #pragma unroll
-      for (int i = 0; i < PER; ++i) {
-        float v = to_f(p[i]);
+    for (int st = 0; st < D / 32; ++st)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float v = to_f(p[32 * st + i]);
         ss = fmaf(v, v, ss);
       }
-    }
-    ss = group16_sum(ss);
-    if ((l & 15) == 0) out[r] = (t < T) ? 1.0f / sqrtf(ss + L2_EPS) : 0.f;
+    ss = row4_sum(ss);
+    if (part == 0) out[r] = (t < T) ? 1.0f / sqrtf(ss + L2_EPS) : 0.f;
   }
 }
-
-// row_rnorms over a bf16 tile already in LDS (rows < nrows; 0 past them), with row_rnorms' arithmetic -- the same
-// per-lane element order and butterfly -- so both give the same bits.
+// The same over a bf16 tile already in LDS (row pitch `pitch` elements; rows < nrows, 0 past them).
 template <int D>
 __device__ __forceinline__ void row_rnorms_lds(float* out, const bf16* tile, int pitch, int nrows, int nwaves, int w) {
-  const int l = lane_id();
-  constexpr int PER = D / 16;
-  for (int r0 = w * 4; r0 < C; r0 += 4 * nwaves) {
-    const int r = r0 + (l >> 4);
+  const int l = lane_id(), part = l & 3;
+  for (int r0 = 16 * w; r0 < C; r0 += 16 * nwaves) {
+    const int r = r0 + (l >> 2);
+    const bf16* p = tile + r * pitch + 8 * part;   // rows past nrows hold copies of a valid row: masked below
     float ss = 0.f;
-    if (r < nrows) {
-      const bf16* p = tile + r * pitch + (l & 15) * PER;
 #pragma unroll
-      for (int i = 0; i < PER; ++i) {
-        const float v = (float)p[i];
+    for (int st = 0; st < D / 32; ++st) {
+      const bf16x8 x8 = *reinterpret_cast<const bf16x8*>(p + 32 * st);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float v = (float)x8[i];
         ss = fmaf(v, v, ss);
       }
     }
-    ss = group16_sum(ss);
-    if ((l & 15) == 0) out[r] = (r < nrows) ? 1.0f / sqrtf(ss + L2_EPS) : 0.f;
+    ss = row4_sum(ss);
+    if (part == 0) out[r] = (r < nrows) ? 1.0f / sqrtf(ss + L2_EPS) : 0.f;
   }
 }
 

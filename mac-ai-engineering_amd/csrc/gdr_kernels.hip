@@ -404,15 +404,26 @@ __global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
     f4 KK[2], QK[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) KK[i] = QK[i] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int p = 0; p < DK / 32; ++p) {
-      const Frag<MT> bk = frag_tile<MT, GQ>(tk, 16 * cb, 32 * p);
+    // tiles above the diagonal (mi < cb) are computed too and masked below: no wave-dependent branch, so each
+    // k-block's fragments are read one stage ahead of its products
+    Frag<MT> st[2][5];
+    auto load = [&](int p, Frag<MT>(&f)[5]) {
+      f[0] = frag_tile<MT, GQ>(tk, 16 * cb, 32 * p);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const int mi = 2 * hh + i;
-        if (mi < cb) continue;
-        mma(KK[i], frag_tile<MT, GQ>(tk, 16 * mi, 32 * p), bk);
-        mma(QK[i], frag_tile<MT, GQ>(tq, 16 * mi, 32 * p), bk);
+        f[1 + 2 * i] = frag_tile<MT, GQ>(tk, 16 * (2 * hh + i), 32 * p);
+        f[2 + 2 * i] = frag_tile<MT, GQ>(tq, 16 * (2 * hh + i), 32 * p);
+      }
+    };
+    load(0, st[0]);
+#pragma unroll
+    for (int p = 0; p < DK / 32; ++p) {
+      if (p + 1 < DK / 32) load(p + 1, st[(p + 1) & 1]);
+      const Frag<MT>(&f)[5] = st[p & 1];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        mma(KK[i], f[1 + 2 * i], f[0]);
+        mma(QK[i], f[2 + 2 * i], f[0]);
       }
     }
     const int s = 16 * cb + n;
