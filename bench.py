@@ -125,11 +125,11 @@ def time_kernels(inp, reps=20):
     P = N.ptr
     calls = {
         "prep_fwd": ("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), P(Ke), P(GL), P(Qg), P(M), None,
-                     B, T, H, DK, DV, code, 1, sc, st),
+                     B, T, H, H, DK, DV, code, 1, sc, st),
         "state_fwd_out": ("macai_gdr_state_fwd", P(W), P(U), P(Ke), P(GL), P(Qg), P(M), P(s0), P(o), None, None,
                           None, B, T, H, DK, DV, code, 0, split, st),
         "prep_bwd": ("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), P(Ke), P(GL), P(Qg), P(M), P(A),
-                     B, T, H, DK, DV, code, 1, sc, st),
+                     B, T, H, H, DK, DV, code, 1, sc, st),
         "state_fwd_store": ("macai_gdr_state_fwd", P(W), P(U), P(Ke), P(GL), None, None, P(s0), None, None, P(Sc),
                             P(Vn), B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, st),
         "state_bwd": ("macai_gdr_state_bwd", P(Ke), P(Qg), P(W), P(M), P(GL), P(do), None, P(dSn), P(dVn), P(ds0),
@@ -137,7 +137,7 @@ def time_kernels(inp, reps=20):
         "state_pair": ("macai_gdr_state_pair", P(W), P(U), P(Ke), P(Qg), P(M), P(GL), P(s0), P(do), None, P(Sc), P(Vn),
                        P(dSn), P(dVn), P(ds0), B, T, H, DK, DV, code, split2, st),
         "chunk_bwd": ("macai_gdr_chunk_bwd", P(q), P(k), P(v), P(g), P(beta), P(do), P(A), P(Sc), P(dSn),
-                      P(Vn), P(dVn), P(dq), P(dk), P(dv), P(dg), P(db), B, T, H, DK, DV, code, 1, sc, st),
+                      P(Vn), P(dVn), P(dq), P(dk), P(dv), P(dg), P(db), B, T, H, H, DK, DV, code, 1, sc, st),
     }
     order = ["prep_fwd", "state_fwd_out", "prep_bwd", "state_fwd_store", "state_bwd", "state_pair", "chunk_bwd"]
     for name in order:                   # warm, and produce every input of the later passes

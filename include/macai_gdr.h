@@ -7,8 +7,10 @@
  * including the per-chunk scratch, and passes raw device pointers, sizes and the HIP stream (hipStream_t as void*).
  * The library allocates nothing and keeps no state between calls; every call only enqueues work on `stream`.
  *
- * Layouts (all contiguous, row-major):
- *   q, k        [B, T, H, DK]   dtype (float32 or bfloat16; raw, or already normalised when use_l2norm = 0)
+ * Layouts (all contiguous, row-major); H counts value heads, Hk key heads (H a multiple of Hk; value head h uses key
+ * head h / (H / Hk), the grouped-value layout of Qwen3.5 / Qwen3-Next without repeating q and k first):
+ *   q, k        [B, T, Hk, DK]  dtype (float32 or bfloat16; raw, or already normalised when use_l2norm = 0)
+ *   dq, dk      [B, T, H, DK]   dtype, per value head (macai_gdr_group_sum folds a group into [B, T, Hk, DK])
  *   v, o, dO    [B, T, H, DV]   dtype
  *   g, beta     [B, T, H]       float32   (g = log decay <= 0)
  *   states      [B, H, DK, DV]  float32   (initial_state, final state, their gradients)
@@ -40,7 +42,7 @@
 extern "C" {
 #endif
 
-#define MACAI_GDR_ABI_VERSION 5
+#define MACAI_GDR_ABI_VERSION 6
 
 /* dtype codes */
 #define MACAI_GDR_F32 0
@@ -64,8 +66,8 @@ int macai_gdr_abi_version(void);
  * `lib.gdc_prep(q, k, g, beta, gc, a, m, kg, T, H, ...)` (reference op.py:63-72; kernel _chunked.py:220-313) and the
  * fused prologue l2n_fwd (_norm.py:97). */
 int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, const float* beta, void* W, float* U,
-                   void* Ke, float* GL, void* Qg, void* M, void* A, int64_t B, int64_t T, int64_t H, int64_t DK,
-                   int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, void* stream);
+                   void* Ke, float* GL, void* Qg, void* M, void* A, int64_t B, int64_t T, int64_t H, int64_t Hk,
+                   int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, void* stream);
 
 /* The sequential state pass (north star (2) + (3)): S <- exp(G_last) S + K^T diag(e) (U - W S) over the chunks from
  * s0 (NULL = zeros).  flags = 0: the output O = diag(gamma) Q S + M Vn to o (dtype) and the final state to sT when
@@ -95,23 +97,30 @@ int macai_gdr_state_pair(const void* W, const float* U, const void* Ke, const vo
                          float* ds0, int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV, int32_t dtype,
                          int32_t split, void* stream);
 
-/* The per-chunk backward (north star (4)): dq, dk (w.r.t. the raw inputs when use_l2norm), dv in dtype; dg, dbeta in
- * float32; one writer per element (bitwise deterministic).  Replaces `lib.gdc_bwd_chunk(q, k, beta, do, gc, a, kg, m,
- * sc, dsn, vn, xu, dvn, dq, dk, dv, dg, dbeta, T, H, DV, ...)` (reference op.py:241-242; kernel
- * _chunked.py:905-1177) and the prologue's backward l2n_bwd (_norm.py:113). */
+/* The per-chunk backward (north star (4)): dq, dk (w.r.t. the raw inputs when use_l2norm; per value head, [B, T, H,
+ * DK]), dv in dtype; dg, dbeta in float32; one writer per element (bitwise deterministic).  Replaces
+ * `lib.gdc_bwd_chunk(q, k, beta, do, gc, a, kg, m, sc, dsn, vn, xu, dvn, dq, dk, dv, dg, dbeta, T, H, DV, ...)`
+ * (reference op.py:241-242; kernel _chunked.py:905-1177) and the prologue's backward l2n_bwd (_norm.py:113). */
 int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float* g, const float* beta, const void* dO,
                         const void* A, const float* Sc, const float* dSn, const void* Vn,
                         const void* dVn, void* dq, void* dk, void* dv, float* dg, float* dbeta, int64_t B, int64_t T,
-                        int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale,
-                        void* stream);
+                        int64_t H, int64_t Hk, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm,
+                        float q_scale, void* stream);
 
-/* One recurrent step per sequence (T = 1): q, k [B, 1, H, DK], v [B, 1, H, DV] dtype; g, beta [B, 1, H] float32;
+/* One recurrent step per sequence (T = 1): q, k [B, 1, Hk, DK], v [B, 1, H, DV] dtype; g, beta [B, 1, H] float32;
  * s_in, s_out [B, H, DK, DV] float32 (s_out may equal s_in).  S' = e^g S + k beta (v - e^g S^T k)^T, o = S'^T q.  The
  * math of the reference's recurrence (op.py:308-313) and of transformers' torch_recurrent_gated_delta_rule
  * (modeling_qwen3_5.py:330-380), which the reference leaves unpatched (patch.py:27-29).  (DK, DV) in {64, 128}^2. */
 int macai_gdr_decode(const void* q, const void* k, const void* v, const float* g, const float* beta,
-                     const float* s_in, void* o, float* s_out, int64_t B, int64_t H, int64_t DK, int64_t DV,
-                     int32_t dtype, int32_t use_l2norm, float q_scale, void* stream);
+                     const float* s_in, void* o, float* s_out, int64_t B, int64_t H, int64_t Hk, int64_t DK,
+                     int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, void* stream);
+
+/* Key-head gradients of grouped heads: y [B, T, Hk, D] = the sum over each group's H / Hk value heads of x [B, T, H,
+ * D] (fp32 accumulation in head order, dtype in and out; D a multiple of 8).  Replaces the backward of the
+ * q.repeat_interleave(H / Hk, dim=2) / k.repeat_interleave(...) that precede the rule in the model
+ * (transformers modeling_qwen3_5.py:500-502; reference layer/_qwen3_5.py:155-157), which the grouped layout removes. */
+int macai_gdr_group_sum(const void* x, void* y, int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D, int32_t dtype,
+                        void* stream);
 
 #ifdef __cplusplus
 }

@@ -48,6 +48,7 @@ struct PrepArgs {
   int B, T, H, DV, NT;
   int l2norm;
   float q_scale;
+  int Hk;        // key heads of q, k ([B,T,Hk,DK]); value head h reads key head h / (H / Hk)
 };
 
 struct StateFwdArgs {
@@ -85,11 +86,12 @@ struct ChunkBwdArgs {
   const float* Sc;                            // fp32
   const float* dSn;                           // fp32
   const void *Vn, *dVn;                       // MT
-  void *dq, *dk, *dv;
+  void *dq, *dk, *dv;                         // dq, dk per VALUE head [B,T,H,DK] (the caller sums a group)
   float *dg, *dbeta;
   int B, T, H, DV, NT;
   int l2norm;
   float q_scale;
+  int Hk;                                     // key heads of q, k; value head h reads key head h / (H / Hk)
 };
 
 struct DecodeArgs {
@@ -100,6 +102,7 @@ struct DecodeArgs {
   int B, H;
   int l2norm;
   float q_scale;
+  int Hk;        // key heads of q, k; value head h reads key head h / (H / Hk)
 };
 
 template <typename MT>
@@ -131,7 +134,7 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
   const int T = a.T, H = a.H, DV = a.DV, NT = a.NT;
   const int t0 = c * C;
   const int l = lane_id(), w = wave_id(), j = l >> 4;
-  const size_t qk_base = ((size_t)b * T * H + h) * DK, qk_pitch = (size_t)H * DK;
+  const size_t qk_base = ((size_t)b * T * a.Hk + h / (H / a.Hk)) * DK, qk_pitch = (size_t)a.Hk * DK;
   const size_t v_base = ((size_t)b * T * H + h) * DV, v_pitch = (size_t)H * DV;
   const size_t s_base = (size_t)b * T * H + h;
   const size_t bhc = ((size_t)b * H + h) * NT + c;
@@ -334,7 +337,7 @@ __global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
   const int T = a.T, H = a.H, DV = a.DV, NT = a.NT;
   const int t0 = c * C, nrows = (T - t0 < C) ? T - t0 : C;
   const int l = lane_id(), w = wave_id(), j = l >> 4, n = l & 15;
-  const size_t qk_base = ((size_t)b * T * H + h) * DK, qk_pitch = (size_t)H * DK;
+  const size_t qk_base = ((size_t)b * T * a.Hk + h / (H / a.Hk)) * DK, qk_pitch = (size_t)a.Hk * DK;
   const size_t v_base = ((size_t)b * T * H + h) * DV, v_pitch = (size_t)H * DV;
   const size_t s_base = (size_t)b * T * H + h;
   const size_t bhc = ((size_t)b * H + h) * NT + c;
@@ -1054,7 +1057,8 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
   const int T = a.T, H = a.H, NT = a.NT;
   const int t0 = c * C, nrows = (T - t0 < C) ? T - t0 : C;
   const int l = lane_id(), w = wave_id(), j = l >> 4;
-  const size_t qk_base = ((size_t)b * T * H + h) * DK, qk_pitch = (size_t)H * DK;
+  const size_t qk_base = ((size_t)b * T * a.Hk + h / (H / a.Hk)) * DK, qk_pitch = (size_t)a.Hk * DK;
+  const size_t dqk_base = ((size_t)b * T * H + h) * DK, dqk_pitch = (size_t)H * DK;   // dq, dk: value heads
   const size_t v_base = ((size_t)b * T * H + h) * DV, v_pitch = (size_t)H * DV;
   const size_t s_base = (size_t)b * T * H + h;
   const size_t bhc = ((size_t)b * H + h) * NT + c;
@@ -1442,8 +1446,8 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
         } else {
           gq = qs * gq;
         }
-        ((MT*)a.dq)[qk_base + (size_t)t * qk_pitch + d] = from_f<MT>(gq);
-        ((MT*)a.dk)[qk_base + (size_t)t * qk_pitch + d] = from_f<MT>(gk);
+        ((MT*)a.dq)[dqk_base + (size_t)t * dqk_pitch + d] = from_f<MT>(gq);
+        ((MT*)a.dk)[dqk_base + (size_t)t * dqk_pitch + d] = from_f<MT>(gk);
       }
   }
 }
@@ -1488,7 +1492,8 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   const int T = a.T, H = a.H, NT = a.NT;
   const int t0 = c * C, nrows = (T - t0 < C) ? T - t0 : C;
   const int l = lane_id(), w = wave_id(), j = l >> 4, n = l & 15;
-  const size_t qk_base = ((size_t)b * T * H + h) * DK, qk_pitch = (size_t)H * DK;
+  const size_t qk_base = ((size_t)b * T * a.Hk + h / (H / a.Hk)) * DK, qk_pitch = (size_t)a.Hk * DK;
+  const size_t dqk_base = ((size_t)b * T * H + h) * DK, dqk_pitch = (size_t)H * DK;   // dq, dk: value heads
   const size_t v_base = ((size_t)b * T * H + h) * DV, v_pitch = (size_t)H * DV;
   const size_t s_base = (size_t)b * T * H + h;
   const size_t bhc = ((size_t)b * H + h) * NT + c;
@@ -2010,13 +2015,13 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   // whole rows out: 16 bytes per lane
   {
     constexpr int UK = DK / 8, UV = DV / 8;
-    MT* dq = (MT*)a.dq + qk_base + (size_t)t0 * qk_pitch;
-    MT* dk = (MT*)a.dk + qk_base + (size_t)t0 * qk_pitch;
+    MT* dq = (MT*)a.dq + dqk_base + (size_t)t0 * dqk_pitch;
+    MT* dk = (MT*)a.dk + dqk_base + (size_t)t0 * dqk_pitch;
     MT* dv = (MT*)a.dv + v_base + (size_t)t0 * v_pitch;
     for (int i = threadIdx.x; i < nrows * UK; i += blockDim.x) {
       const int row = i / UK, u = i - row * UK;
-      *reinterpret_cast<bf16x8*>(dq + row * qk_pitch + 8 * u) = *reinterpret_cast<const bf16x8*>(tq + row * KP + 8 * u);
-      *reinterpret_cast<bf16x8*>(dk + row * qk_pitch + 8 * u) = *reinterpret_cast<const bf16x8*>(tk + row * KP + 8 * u);
+      *reinterpret_cast<bf16x8*>(dq + row * dqk_pitch + 8 * u) = *reinterpret_cast<const bf16x8*>(tq + row * KP + 8 * u);
+      *reinterpret_cast<bf16x8*>(dk + row * dqk_pitch + 8 * u) = *reinterpret_cast<const bf16x8*>(tk + row * KP + 8 * u);
     }
     for (int i = threadIdx.x; i < nrows * UV; i += blockDim.x) {
       const int row = i / UV, u = i - row * UV;
@@ -2039,8 +2044,9 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
   __shared__ float sc[2];
   const int bh = blockIdx.x;
   const int l = lane_id(), w = wave_id();
-  const IT* q = (const IT*)a.q + (size_t)bh * DK;
-  const IT* k = (const IT*)a.k + (size_t)bh * DK;
+  const size_t bhk = (size_t)(bh / a.H) * a.Hk + (bh % a.H) / (a.H / a.Hk);   // the key head of value head bh
+  const IT* q = (const IT*)a.q + bhk * DK;
+  const IT* k = (const IT*)a.k + bhk * DK;
   if (w == 0) {
     float qq = 0.f, kk = 0.f;
     for (int i = l; i < DK; i += 64) {
@@ -2109,6 +2115,30 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
 // =====================================================================================================================
 using namespace gdr;
 
+// y[b, t, hk, :] = sum of x[b, t, hk G + g, :] over the G = H / Hk value heads of a group, in head order with fp32
+// accumulation: the key-head gradients of grouped heads.  One thread per 8 elements; rows_k = B T Hk.
+template <typename T>
+__global__ void __launch_bounds__(256) group_sum_kernel(const T* x, T* y, int64_t rows_k, int G, int D) {
+  const int U = D / 8;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= rows_k * U) return;
+  const int64_t rk = i / U;
+  const int u = (int)(i - rk * U);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int g = 0; g < G; ++g) {
+    const T* src = x + (rk * G + g) * D + 8 * u;
+    const f4 lo = load4(src), hi = load4(src + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc[e] += lo[e];
+      acc[e + 4] += hi[e];
+    }
+  }
+  T* dst = y + rk * D + 8 * u;
+  store4<T>(dst, f4{acc[0], acc[1], acc[2], acc[3]});
+  store4<T>(dst + 4, f4{acc[4], acc[5], acc[6], acc[7]});
+}
+
 static thread_local char g_err[512] = "";
 
 static int fail(int code, const char* fmt, ...) {
@@ -2140,6 +2170,13 @@ static int check_common(const char* what, int64_t B, int64_t T, int64_t H, int64
     return fail(MACAI_GDR_EUNSUP, "%s: dtype code must be 0 (float32) or 1 (bfloat16), got %d", what, dtype);
   if (B * T * H * (DK > DV ? DK : DV) >= ((int64_t)1 << 31) * 4)
     return fail(MACAI_GDR_EINVAL, "%s: tensor too large", what);
+  return MACAI_GDR_OK;
+}
+
+static int check_heads(const char* what, int64_t H, int64_t Hk) {
+  if (Hk < 1 || H % Hk != 0)
+    return fail(MACAI_GDR_EINVAL, "%s: key heads must divide value heads (got Hk = %lld, H = %lld)", what,
+                (long long)Hk, (long long)H);
   return MACAI_GDR_OK;
 }
 
@@ -2175,10 +2212,11 @@ const char* macai_gdr_last_error(void) { return g_err; }
 int macai_gdr_abi_version(void) { return MACAI_GDR_ABI_VERSION; }
 
 int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, const float* beta, void* W, float* U,
-                   void* Ke, float* GL, void* Qg, void* M, void* A, int64_t B, int64_t T, int64_t H, int64_t DK,
-                   int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, void* stream) {
+                   void* Ke, float* GL, void* Qg, void* M, void* A, int64_t B, int64_t T, int64_t H, int64_t Hk,
+                   int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, void* stream) {
   const char* what = "macai_gdr_prep";
   int rc = check_common(what, B, T, H, DK, DV, dtype);
+  if (!rc) rc = check_heads(what, H, Hk);
   if (rc) return rc;
   if (!q || !k || !v || !g || !beta || !W || !U || !Ke || !GL || !Qg || !M)
     return fail(MACAI_GDR_EINVAL, "%s: null input or output pointer", what);
@@ -2186,7 +2224,7 @@ int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, 
   for (const void* p : ps)
     if (!aligned16(p)) return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
   PrepArgs a{q, k, v, g, beta, W, U, Ke, GL, Qg, M, A, (int)B, (int)T, (int)H, (int)DV, (int)((T + C - 1) / C),
-             use_l2norm, q_scale};
+             use_l2norm, q_scale, (int)Hk};
   dim3 grid(a.NT, (unsigned)H, (unsigned)B);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == MACAI_GDR_F32) {
@@ -2311,10 +2349,11 @@ int macai_gdr_state_pair(const void* W, const float* U, const void* Ke, const vo
 int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float* g, const float* beta, const void* dO,
                         const void* A, const float* Sc, const float* dSn, const void* Vn,
                         const void* dVn, void* dq, void* dk, void* dv, float* dg, float* dbeta, int64_t B, int64_t T,
-                        int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale,
+                        int64_t H, int64_t Hk, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale,
                         void* stream) {
   const char* what = "macai_gdr_chunk_bwd";
   int rc = check_common(what, B, T, H, DK, DV, dtype);
+  if (!rc) rc = check_heads(what, H, Hk);
   if (rc) return rc;
   if (DV != 32 && DV != 64 && DV != 96 && DV != 128)
     return fail(MACAI_GDR_EUNSUP, "%s: the backward takes value head widths 32, 64, 96 or 128 (got %lld)", what,
@@ -2326,7 +2365,7 @@ int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float
   for (const void* p : ps)
     if (!aligned16(p)) return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
   ChunkBwdArgs a{q, k, v, g, beta, dO, A, Sc, dSn, Vn, dVn, dq, dk, dv, dg, dbeta, (int)B, (int)T, (int)H,
-                 (int)DV, (int)((T + C - 1) / C), use_l2norm, q_scale};
+                 (int)DV, (int)((T + C - 1) / C), use_l2norm, q_scale, (int)Hk};
   dim3 grid(a.NT, (unsigned)H, (unsigned)B);
   hipStream_t st = (hipStream_t)stream;
 #define LAUNCH_CB(MT)                                                                                               \
@@ -2351,10 +2390,11 @@ int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float
 }
 
 int macai_gdr_decode(const void* q, const void* k, const void* v, const float* g, const float* beta,
-                     const float* s_in, void* o, float* s_out, int64_t B, int64_t H, int64_t DK, int64_t DV,
-                     int32_t dtype, int32_t use_l2norm, float q_scale, void* stream) {
+                     const float* s_in, void* o, float* s_out, int64_t B, int64_t H, int64_t Hk, int64_t DK,
+                     int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, void* stream) {
   const char* what = "macai_gdr_decode";
   if (B < 1 || H < 1) return fail(MACAI_GDR_EINVAL, "%s: B and H must be >= 1", what);
+  if (int rc = check_heads(what, H, Hk)) return rc;
   if (!((DK == 128 && DV == 128) || (DK == 64 && DV == 64) || (DK == 128 && DV == 64) || (DK == 64 && DV == 128)))
     return fail(MACAI_GDR_EUNSUP, "%s: head widths (DK, DV) must be 64 or 128 each (got %lld, %lld)", what,
                 (long long)DK, (long long)DV);
@@ -2362,7 +2402,7 @@ int macai_gdr_decode(const void* q, const void* k, const void* v, const float* g
     return fail(MACAI_GDR_EUNSUP, "%s: dtype code must be 0 or 1, got %d", what, dtype);
   if (!q || !k || !v || !g || !beta || !s_in || !o || !s_out) return fail(MACAI_GDR_EINVAL, "%s: null pointer", what);
   if (!aligned16(s_in) || !aligned16(s_out)) return fail(MACAI_GDR_EINVAL, "%s: states must be 16-byte aligned", what);
-  DecodeArgs a{q, k, v, g, beta, s_in, o, s_out, (int)B, (int)H, use_l2norm, q_scale};
+  DecodeArgs a{q, k, v, g, beta, s_in, o, s_out, (int)B, (int)H, use_l2norm, q_scale, (int)Hk};
   dim3 grid((unsigned)(B * H));
   hipStream_t st = (hipStream_t)stream;
 #define LAUNCH_DEC(IT)                                                                                           \
@@ -2376,6 +2416,30 @@ int macai_gdr_decode(const void* q, const void* k, const void* v, const float* g
     LAUNCH_DEC(bf16)
   }
 #undef LAUNCH_DEC
+  return launched(what);
+}
+
+int macai_gdr_group_sum(const void* x, void* y, int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D, int32_t dtype,
+                        void* stream) {
+  const char* what = "macai_gdr_group_sum";
+  if (B < 1 || T < 1 || H < 1) return fail(MACAI_GDR_EINVAL, "%s: B, T, H must be >= 1", what);
+  if (int rc = check_heads(what, H, Hk)) return rc;
+  if (D < 8 || D % 8 != 0) return fail(MACAI_GDR_EUNSUP, "%s: row width must be a multiple of 8 (got %lld)", what,
+                                       (long long)D);
+  if (dtype != MACAI_GDR_F32 && dtype != MACAI_GDR_BF16)
+    return fail(MACAI_GDR_EUNSUP, "%s: dtype code must be 0 or 1, got %d", what, dtype);
+  if (!x || !y) return fail(MACAI_GDR_EINVAL, "%s: null pointer", what);
+  if (!aligned16(x) || !aligned16(y)) return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
+  if (B * T * H * D >= ((int64_t)1 << 31) * 4) return fail(MACAI_GDR_EINVAL, "%s: tensor too large", what);
+  const int64_t rows_k = B * T * Hk, units = rows_k * (D / 8);
+  const dim3 grid((unsigned)((units + 255) / 256));
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == MACAI_GDR_F32)
+    hipLaunchKernelGGL((group_sum_kernel<float>), grid, dim3(256), 0, st, (const float*)x, (float*)y, rows_k,
+                       (int)(H / Hk), (int)D);
+  else
+    hipLaunchKernelGGL((group_sum_kernel<bf16>), grid, dim3(256), 0, st, (const bf16*)x, (bf16*)y, rows_k,
+                       (int)(H / Hk), (int)D);
   return launched(what);
 }
 

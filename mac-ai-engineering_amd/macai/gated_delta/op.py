@@ -64,12 +64,17 @@ def split_for(rows: int, T: int, dv: int, share: int = 1) -> int:
 
 
 def _check(q, k, v, g, beta, s0):
+    """q, k [B, T, Hk, DK], v [B, T, H, DV] with H a multiple of Hk (grouped value heads: value head h reads key head
+    h // (H // Hk), the layout of q.repeat_interleave(H // Hk, dim=2)); g, beta [B, T, H]; s0 [B, H, DK, DV]."""
     if not q.is_cuda:
         raise RuntimeError("macai's gated delta rule runs on a HIP device (MI355X); got tensors on " + str(q.device))
-    if q.dim() != 4 or k.shape != q.shape or v.dim() != 4 or v.shape[:3] != q.shape[:3]:
-        raise ValueError(f"q, k [B, T, H, DK] and v [B, T, H, DV] expected, got {tuple(q.shape)}, {tuple(k.shape)}, "
+    if q.dim() != 4 or k.shape != q.shape or v.dim() != 4 or v.shape[:2] != q.shape[:2]:
+        raise ValueError(f"q, k [B, T, Hk, DK] and v [B, T, H, DV] expected, got {tuple(q.shape)}, {tuple(k.shape)}, "
                          f"{tuple(v.shape)}")
-    B, T, H, DK = q.shape
+    B, T, Hk, DK = q.shape
+    H = v.shape[2]
+    if H % Hk != 0:
+        raise ValueError(f"the key heads of q and k ({Hk}) must divide the value heads of v ({H})")
     if g.shape != (B, T, H) or beta.shape != (B, T, H):
         raise ValueError(f"g and beta must be [B, T, H] = {(B, T, H)}, got {tuple(g.shape)}, {tuple(beta.shape)}")
     if s0 is not None and s0.shape != (B, H, DK, v.shape[-1]):
@@ -81,14 +86,15 @@ def _check(q, k, v, g, beta, s0):
 
 
 def _dims(q, v):
-    B, T, H, DK = q.shape
-    return B, T, H, DK, v.shape[-1], math.ceil(T / CHUNK)
+    """(B, T, H value heads, Hk key heads, DK, DV, NT)."""
+    B, T, Hk, DK = q.shape
+    return B, T, v.shape[2], Hk, DK, v.shape[-1], math.ceil(T / CHUNK)
 
 
 def _prep(q, k, v, g, beta, l2norm: bool, q_scale: float, with_A: bool):
     """The per-chunk operands (row-major, tokens as rows): W, U, diag(e) K^, exp(G_last), diag(gamma) Q^, M, and A when
     asked (the backward's per-chunk pass)."""
-    B, T, H, DK, DV, NT = _dims(q, v)
+    B, T, H, Hk, DK, DV, NT = _dims(q, v)
     dev, dt = q.device, q.dtype
     f32 = torch.float32
     W = torch.empty(B, H, NT, CHUNK, DK, device=dev, dtype=dt)
@@ -98,14 +104,14 @@ def _prep(q, k, v, g, beta, l2norm: bool, q_scale: float, with_A: bool):
              A=torch.empty(B, H, NT, CHUNK, CHUNK, device=dev, dtype=dt) if with_A else None)
     P = N.ptr
     _launch("prep_bwd" if with_A else "prep_fwd", "macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(r["W"]),
-            P(r["U"]), P(r["Ke"]), P(r["GL"]), P(r["Qg"]), P(r["M"]), P(r["A"]), B, T, H, DK, DV, N.dtype_code(dt),
-            int(l2norm), q_scale, N.stream_of(q))
+            P(r["U"]), P(r["Ke"]), P(r["GL"]), P(r["Qg"]), P(r["M"]), P(r["A"]), B, T, H, Hk, DK, DV,
+            N.dtype_code(dt), int(l2norm), q_scale, N.stream_of(q))
     return r
 
 
 def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool):
     """prep, then the state pass with the output: returns (o in q's dtype, sT or None)."""
-    B, T, H, DK, DV, NT = _dims(q, v)
+    B, T, H, Hk, DK, DV, NT = _dims(q, v)
     dev, dt = q.device, q.dtype
     code, stream = N.dtype_code(dt), N.stream_of(q)
     r = _prep(q, k, v, g, beta, l2norm, q_scale, False)
@@ -121,8 +127,10 @@ def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool):
 
 def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float):
     """Recompute (prep; the state pass storing S_c and Vn), the reverse state pass, the per-chunk backward.  Returns
-    (dq, dk, dv in q's dtype; dg, dbeta, ds0 float32)."""
-    B, T, H, DK, DV, NT = _dims(q, v)
+    (dq, dk, dv in q's dtype; dg, dbeta, ds0 float32).  With grouped heads (Hk < H) the per-chunk backward writes dq,
+    dk per value head and macai_gdr_group_sum folds each group (the backward of the repeat the grouped layout
+    replaces)."""
+    B, T, H, Hk, DK, DV, NT = _dims(q, v)
     dev, dt = q.device, q.dtype
     code, stream = N.dtype_code(dt), N.stream_of(q)
     f32 = torch.float32
@@ -144,16 +152,27 @@ def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float):
         _launch("state_bwd", "macai_gdr_state_bwd", P(r["Ke"]), P(r["Qg"]), P(r["W"]), P(r["M"]), P(r["GL"]), P(do),
                 P(dsT), P(dSn), P(dVn), P(ds0), B, T, H, DK, DV, code, split, stream)
     CALLS[f"bwd s{split}"] += 1
-    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    if Hk == H:
+        dqh, dkh = torch.empty_like(q), torch.empty_like(k)
+    else:
+        dqh = torch.empty(B, T, H, DK, device=dev, dtype=dt)
+        dkh = torch.empty_like(dqh)
+    dv = torch.empty_like(v)
     dg, dbeta = torch.empty_like(g), torch.empty_like(beta)
     _launch("chunk_bwd", "macai_gdr_chunk_bwd", P(q), P(k), P(v), P(g), P(beta), P(do), P(r["A"]), P(Sc), P(dSn), P(Vn),
-            P(dVn), P(dq), P(dk), P(dv), P(dg), P(dbeta), B, T, H, DK, DV, code, int(l2norm), q_scale, stream)
+            P(dVn), P(dqh), P(dkh), P(dv), P(dg), P(dbeta), B, T, H, Hk, DK, DV, code, int(l2norm), q_scale, stream)
+    if Hk == H:
+        return dqh, dkh, dv, dg, dbeta, ds0
+    dq, dk = torch.empty_like(q), torch.empty_like(k)
+    _launch("group_sum", "macai_gdr_group_sum", P(dqh), P(dq), B, T, H, Hk, DK, code, stream)
+    _launch("group_sum", "macai_gdr_group_sum", P(dkh), P(dk), B, T, H, Hk, DK, code, stream)
     return dq, dk, dv, dg, dbeta, ds0
 
 
 class GatedDeltaRule(torch.autograd.Function):
     """o, S_T = recurrence(q, k, v, g, beta, S_0) on [B, T, H, D] tensors (q already normalised and scaled): the
-    reference's contract (op.py:116-257).  q, k, v float32 or bfloat16 (o in that dtype), g, beta, s0 float32.
+    reference's contract (op.py:116-257).  q and k may also have fewer heads Hk dividing H (grouped value heads, value
+    head h using key head h // (H // Hk)); their gradients then come back in that shape.  q, k, v float32 or bfloat16 (o in that dtype), g, beta, s0 float32.
     backward -> (dq, dk, dv, dg, dbeta, ds0, None); None upstream gradients count as zeros (op.py:194-200)."""
 
     @staticmethod
@@ -210,7 +229,8 @@ def l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
 def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size: int = 64, initial_state=None,
                            output_final_state: bool = False, use_qk_l2norm_in_kernel: bool = False, **kwargs):
     """Drop-in for transformers' torch_chunk_gated_delta_rule: query, key [B, T, H, DK]; value [B, T, H, DV]; g (log
-    decay, <= 0) and beta [B, T, H]; initial_state [B, H, DK, DV] or None.  Returns the output [B, T, H, DV] in the
+    decay, <= 0) and beta [B, T, H]; initial_state [B, H, DK, DV] or None.  query and key may also come with fewer
+    heads Hk dividing H, unrepeated (value head h reads key head h // (H // Hk), as after repeat_interleave).  Returns the output [B, T, H, DV] in the
     query's dtype and the final state (float32) when output_final_state, else None.  chunk_size is accepted and unused
     (the kernels use 64-token chunks).  bfloat16 inputs run on bf16 MFMA with fp32 accumulation and an fp32 state;
     float32 inputs on fp32 MFMA; float16 inputs are computed as float32."""
@@ -249,8 +269,8 @@ def recurrent_gated_delta_rule(query, key, value, g, beta, initial_state=None, o
     cdt = torch.bfloat16 if dtype == torch.bfloat16 else torch.float32
     q, k, v = (x.to(cdt).contiguous() for x in (query, key, value))
     gf, bf = g.to(torch.float32).contiguous(), beta.to(torch.float32).contiguous()
-    B, _, H, DK = q.shape
-    DV = v.shape[-1]
+    B, _, Hk, DK = q.shape
+    H, DV = v.shape[2], v.shape[-1]
     s_in = (torch.zeros(B, H, DK, DV, device=q.device, dtype=torch.float32) if initial_state is None
             else initial_state.to(torch.float32).contiguous())
     _check(q, k, v, gf, bf, s_in)
@@ -258,7 +278,7 @@ def recurrent_gated_delta_rule(query, key, value, g, beta, initial_state=None, o
     s_out = torch.empty_like(s_in)
     with torch.cuda.device(q.device):
         N.call("macai_gdr_decode", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gf), N.ptr(bf), N.ptr(s_in), N.ptr(o),
-               N.ptr(s_out), B, H, DK, DV, N.dtype_code(cdt), int(bool(use_qk_l2norm_in_kernel)), DK ** -0.5,
+               N.ptr(s_out), B, H, Hk, DK, DV, N.dtype_code(cdt), int(bool(use_qk_l2norm_in_kernel)), DK ** -0.5,
                N.stream_of(q))
     return o.to(dtype), (s_out if output_final_state else None)
 

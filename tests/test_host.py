@@ -27,8 +27,9 @@ def _declared():
 
 def test_library_exports_every_declared_symbol():
     decl = _declared()
-    assert {"macai_gdr_prep", "macai_gdr_state_fwd", "macai_gdr_state_bwd", "macai_gdr_chunk_bwd", "macai_gdr_decode",
-            "macai_gdr_last_error", "macai_gdr_abi_version"} <= set(decl)
+    assert {"macai_gdr_prep", "macai_gdr_state_fwd", "macai_gdr_state_bwd", "macai_gdr_state_pair",
+            "macai_gdr_chunk_bwd", "macai_gdr_decode", "macai_gdr_group_sum", "macai_gdr_last_error",
+            "macai_gdr_abi_version"} <= set(decl)
     lib = N.lib()
     for name in decl:
         assert hasattr(lib, name), name
@@ -39,8 +40,8 @@ def test_library_exports_every_declared_symbol():
 
 def _prep(**over):
     p = 1 << 20
-    a = dict(q=p, k=p, v=p, g=p, beta=p, W=p, U=p, Ke=p, GL=p, Qg=p, M=p, A=None, B=1, T=64, H=1, DK=128, DV=128,
-             dtype=1, l2=1, scale=1.0, stream=None)
+    a = dict(q=p, k=p, v=p, g=p, beta=p, W=p, U=p, Ke=p, GL=p, Qg=p, M=p, A=None, B=1, T=64, H=1, Hk=1, DK=128,
+             DV=128, dtype=1, l2=1, scale=1.0, stream=None)
     a.update(over)
     return N.lib().macai_gdr_prep(*a.values())
 
@@ -57,6 +58,9 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert _prep(W=(1 << 20) + 4) == N.EINVAL and b"aligned" in L.macai_gdr_last_error()
     assert _prep(A=(1 << 20) + 8) == N.EINVAL and b"aligned" in L.macai_gdr_last_error()
     assert _prep(q=None) == N.EINVAL
+    # key heads must divide value heads
+    assert _prep(H=4, Hk=3) == N.EINVAL and b"key heads must divide" in L.macai_gdr_last_error()
+    assert _prep(H=4, Hk=0) == N.EINVAL
     p = 1 << 20
     sf = lambda *ptrs, flags=0, split=0, DV=128: L.macai_gdr_state_fwd(*ptrs, 1, 64, 1, 128, DV, 1, flags, split, None)
     # flags that ask for nothing or both, a split that does not divide DV / 16, a missing output operand
@@ -66,18 +70,25 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert sf(p, p, p, p, p, p, None, p, None, None, None, split=1, DV=96) == N.EINVAL
     assert sf(p, p, p, p, p, None, None, p, None, None, None) == N.EINVAL
     assert L.macai_gdr_state_bwd(p, p, p, p, p, None, None, p, p, p, 1, 64, 1, 128, 128, 1, 0, None) == N.EINVAL
-    assert L.macai_gdr_chunk_bwd(*([p] * 15), None, 1, 64, 1, 128, 128, 1, 1, 1.0, None) == N.EINVAL
+    assert L.macai_gdr_chunk_bwd(*([p] * 15), None, 1, 64, 1, 1, 128, 128, 1, 1, 1.0, None) == N.EINVAL
+    assert L.macai_gdr_chunk_bwd(*([p] * 16), 1, 64, 6, 4, 128, 128, 1, 1, 1.0, None) == N.EINVAL
     pair = lambda *ptrs, split=0: L.macai_gdr_state_pair(*ptrs, 1, 64, 1, 128, 128, 1, split, None)
     assert pair(*([p] * 6), None, p, None, p, p, p, p, None) == N.EINVAL and b"null" in L.macai_gdr_last_error()
     assert pair(*([p] * 6), None, p, None, *([p] * 5), split=3) == N.EINVAL
-    assert L.macai_gdr_decode(p, p, p, p, p, p, p, p, 1, 1, 256, 128, 1, 1, 1.0, None) == N.EUNSUP
+    assert L.macai_gdr_decode(p, p, p, p, p, p, p, p, 1, 1, 1, 256, 128, 1, 1, 1.0, None) == N.EUNSUP
+    assert L.macai_gdr_decode(p, p, p, p, p, p, p, p, 1, 4, 3, 128, 128, 1, 1, 1.0, None) == N.EINVAL
+    gs = lambda x, y, H=4, Hk=2, D=128, dtype=1: L.macai_gdr_group_sum(x, y, 1, 64, H, Hk, D, dtype, None)
+    assert gs(p, None) == N.EINVAL and b"null" in L.macai_gdr_last_error()
+    assert gs(p, p, Hk=3) == N.EINVAL
+    assert gs(p, p, D=12) == N.EUNSUP
+    assert gs(p + 4, p) == N.EINVAL and b"aligned" in L.macai_gdr_last_error()
 
 
 def test_call_maps_codes_to_exceptions():
     with pytest.raises(NotImplementedError, match="key head width"):
-        N.call("macai_gdr_prep", *([1 << 20] * 11), None, 1, 64, 1, 96, 128, 1, 1, 1.0, None)
+        N.call("macai_gdr_prep", *([1 << 20] * 11), None, 1, 64, 1, 1, 96, 128, 1, 1, 1.0, None)
     with pytest.raises(ValueError, match="null"):
-        N.call("macai_gdr_prep", *([None] * 12), 1, 64, 1, 128, 128, 1, 1, 1.0, None)
+        N.call("macai_gdr_prep", *([None] * 12), 1, 64, 1, 1, 128, 128, 1, 1, 1.0, None)
 
 
 def test_packed_rows_refused():
