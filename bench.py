@@ -64,19 +64,22 @@ def make_inputs(cfg, seed, dev):
     return out, c
 
 
-def kernel_costs(B, T, H, DK, DV, es=2):
+def kernel_costs(B, T, H, DK, DV, es=2, Hk=None):
     """Algorithmic bytes (each declared input read once, each output written once, from argument sizes) and dense
-    FLOPs (2 per multiply-add, triangular products counted dense) per launch of each kernel of the training step."""
+    FLOPs (2 per multiply-add, triangular products counted dense) per launch of each kernel of the training step.
+    Hk: key heads of q and k when they come unrepeated (grouped value heads); H by default."""
+    Hk = Hk or H
     NT = math.ceil(T / C)
     n = B * H * NT                       # chunk-heads
     tok = B * T * H
     io_k, io_v = tok * DK * es, tok * DV * es
+    io_kk = B * T * Hk * DK * es         # one of q, k as the kernels read them
     gb = tok * 4 * 2                     # g and beta
     cdk, cdv, cc = C * DK, C * DV, C * C
     sdk = DK * DV * 4                    # one fp32 state
     cost = {}
     pre = 3 * cdk * es + cdv * 4 + cc * es + 4      # prep's row-major outputs W, Ke, Qg, U, M, GL
-    inp = 2 * io_k + io_v + gb                        # q, k, v, g, beta
+    inp = 2 * io_kk + io_v + gb                       # q, k, v, g, beta
     # the forward: prep, then the state pass reads W, U, Ke, GL, Qg, M and writes o
     cost["prep_fwd"] = dict(bytes=inp + n * pre,
                             flops=n * (2 * 2 * cc * DK + cc * C / 3 + 2 * cc * DK + 2 * cc * DV))
@@ -96,6 +99,8 @@ def kernel_costs(B, T, H, DK, DV, es=2):
     cost["chunk_bwd"] = dict(bytes=inp + io_v + n * (cc * es + 2 * sdk + 2 * cdv * es) + 2 * io_k + io_v + gb,
                              flops=n * (3 * 2 * C * DK * DV + 2 * cc * DK + 3 * 2 * cc * DK + 2 * 2 * cc * DV
                                         + 2 * 2 * cc * C + 3 * 2 * cc * DK + 2 * cc * DV))
+    # grouped heads: each of dq, dk folded from per-value-head rows (read H heads, write Hk)
+    cost["group_sum"] = dict(bytes=io_k + io_kk, flops=tok * DK)
     return cost
 
 
@@ -192,6 +197,9 @@ def main():
     ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--grouped", action="store_true",
+                    help="configs with Hk < Hv: q and k go to the rule unrepeated (grouped value heads); without it the "
+                         "step repeats them first, as the model does (repeat_interleave inside the timed step)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run one plain device copy of this many MiB (calibrates rocprof byte counters)")
     args = ap.parse_args()
@@ -203,7 +211,11 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     inp, c = make_inputs(args.config, 1000 + args.config, dev)
-    leaves = [inp[n].requires_grad_(True) for n in ("query", "key", "value", "g", "beta")]
+    rep = c["Hv"] // c["Hk"]
+    # q, k leaves at the model's key heads (make_inputs draws them per key head and repeats)
+    kq = {n: inp[n][:, :, ::rep].contiguous() for n in ("query", "key")}
+    leaves = [kq["query"], kq["key"]] + [inp[n] for n in ("value", "g", "beta")]
+    leaves = [x.requires_grad_(True) for x in leaves]
     s0 = inp["initial_state"]
     if s0 is not None:
         s0.requires_grad_(True)
@@ -211,7 +223,10 @@ def main():
     do = inp["do"]
 
     def step():
-        o, _ = chunk_gated_delta_rule(*leaves[:5], initial_state=s0, output_final_state=False,
+        q, k = leaves[0], leaves[1]
+        if rep > 1 and not args.grouped:          # the model's layout: repeat over each group first
+            q, k = q.repeat_interleave(rep, 2), k.repeat_interleave(rep, 2)
+        o, _ = chunk_gated_delta_rule(q, k, *leaves[2:5], initial_state=s0, output_final_state=False,
                                       use_qk_l2norm_in_kernel=True)
         return torch.autograd.grad(o, leaves, do)
 
@@ -251,12 +266,12 @@ def main():
         dst = torch.empty_like(src)
         dst.copy_(src)
         torch.cuda.synchronize()
-    cost = kernel_costs(B, T, H, DK, DV)
+    cost = kernel_costs(B, T, H, DK, DV, Hk=c["Hk"] if args.grouped else None)
     kernels = {}
     for name, t in ktime.items():
         bw = cost[name]["bytes"] / t
         fl = cost[name]["flops"] / t
-        kernels[name] = {"us": round(t * 1e6, 2), "us_alone": round(alone[name] * 1e6, 2),
+        kernels[name] = {"us": round(t * 1e6, 2), "us_alone": round(alone[name] * 1e6, 2) if name in alone else None,
                          "GB/s": round(bw / 1e9, 1), "hbm_frac": round(bw / HBM_PEAK, 4),
                          "TFLOP/s": round(fl / 1e12, 2), "mfma_frac": round(fl / MFMA_PEAK["bf16"], 4),
                          "traffic": TRAFFIC.get(args.config, {}).get(name)}
@@ -272,6 +287,7 @@ def main():
             "dtype": "bf16", "data": "synthetic",
             "config": {"workload": f"gated-delta drop-in fwd+bwd, BASELINE config {args.config}", "B": B, "T": T,
                        "Hk": c["Hk"], "Hv": H, "DK": DK, "DV": DV, "chunk": C, "l2norm_in_kernel": True,
+                       "qk_heads_to_the_rule": c["Hk"] if args.grouped else H,
                        "initial_state": c["s0"], "value_split": split, "overlap_split": op.split_for(B * H, T, DV, 2),
                        "overlapped_state_passes": op.OVERLAP},
             "roofline": roof, "kernels": kernels}
