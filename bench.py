@@ -130,19 +130,19 @@ def time_kernels(inp, reps=20):
     P = N.ptr
     calls = {
         "prep_fwd": ("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), P(Ke), P(GL), P(Qg), P(M), None,
-                     B, T, H, H, DK, DV, code, 1, sc, st),
+                     B, T, H, H, DK, DV, code, 1, sc, None, 0, st),
         "state_fwd_out": ("macai_gdr_state_fwd", P(W), P(U), P(Ke), P(GL), P(Qg), P(M), P(s0), P(o), None, None,
-                          None, B, T, H, DK, DV, code, 0, split, st),
+                          None, B, T, H, DK, DV, code, 0, split, None, 0, st),
         "prep_bwd": ("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), P(Ke), P(GL), P(Qg), P(M), P(A),
-                     B, T, H, H, DK, DV, code, 1, sc, st),
+                     B, T, H, H, DK, DV, code, 1, sc, None, 0, st),
         "state_fwd_store": ("macai_gdr_state_fwd", P(W), P(U), P(Ke), P(GL), None, None, P(s0), None, None, P(Sc),
-                            P(Vn), B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, st),
+                            P(Vn), B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, None, 0, st),
         "state_bwd": ("macai_gdr_state_bwd", P(Ke), P(Qg), P(W), P(M), P(GL), P(do), None, P(dSn), P(dVn), P(ds0),
-                      B, T, H, DK, DV, code, split, st),
+                      B, T, H, DK, DV, code, split, None, 0, st),
         "state_pair": ("macai_gdr_state_pair", P(W), P(U), P(Ke), P(Qg), P(M), P(GL), P(s0), P(do), None, P(Sc), P(Vn),
-                       P(dSn), P(dVn), P(ds0), B, T, H, DK, DV, code, split2, st),
+                       P(dSn), P(dVn), P(ds0), B, T, H, DK, DV, code, split2, None, 0, st),
         "chunk_bwd": ("macai_gdr_chunk_bwd", P(q), P(k), P(v), P(g), P(beta), P(do), P(A), P(Sc), P(dSn),
-                      P(Vn), P(dVn), P(dq), P(dk), P(dv), P(dg), P(db), B, T, H, H, DK, DV, code, 1, sc, st),
+                      P(Vn), P(dVn), P(dq), P(dk), P(dv), P(dg), P(db), B, T, H, H, DK, DV, code, 1, sc, None, 0, st),
     }
     order = ["prep_fwd", "state_fwd_out", "prep_bwd", "state_fwd_store", "state_bwd", "state_pair", "chunk_bwd"]
     for name in order:                   # warm, and produce every input of the later passes
@@ -198,7 +198,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--grouped", action="store_true",
-                    help="configs with Hk < Hv: q and k go to the rule unrepeated (grouped value heads); without it the "
+                    help="configs with Hk < Hv: q and k go to the rule unrepeated (grouped value heads); without "
+                         "it the "
                          "step repeats them first, as the model does (repeat_interleave inside the timed step)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run one plain device copy of this many MiB (calibrates rocprof byte counters)")

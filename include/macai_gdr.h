@@ -30,6 +30,14 @@
  * Supported widths: DK in {32, 64, 128}; DV a multiple of 32 up to 512 (the backward: 32, 64, 96 or 128).
  * Pointers must be 16-byte aligned.
  *
+ * Packed rows (several sequences in one row, transformers' cu_seqlens): pass `pack`, a device int32 table, and its
+ * chunk count NT (`pack` = NULL: every batch row is one sequence and NT = ceil(T / 64)).  Sequence n spans tokens
+ * cu[n] .. cu[n+1] of a single row and is chunked on its own (ceil(len / 64) chunks, the last one partial); the
+ * state restarts at each sequence.  Then B counts sequences: token tensors are [1, T, H, D], per-chunk tensors
+ * [1, H, NT, ...], states [B, H, DK, DV].  Table layout ([2 NT + B + 1] int32): each chunk's first token, then the
+ * end of each chunk's sequence, then each sequence's first chunk (B + 1 entries, the last = NT).  The library does
+ * not read the table on the host; a wrong table is undefined behaviour.
+ *
  * Return value: 0 on success, else an error code below; macai_gdr_last_error() describes the last failure of the
  * calling thread.  Argument checks run before any launch, so they are testable without a GPU.
  */
@@ -42,7 +50,7 @@
 extern "C" {
 #endif
 
-#define MACAI_GDR_ABI_VERSION 6
+#define MACAI_GDR_ABI_VERSION 7
 
 /* dtype codes */
 #define MACAI_GDR_F32 0
@@ -67,7 +75,8 @@ int macai_gdr_abi_version(void);
  * fused prologue l2n_fwd (_norm.py:97). */
 int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, const float* beta, void* W, float* U,
                    void* Ke, float* GL, void* Qg, void* M, void* A, int64_t B, int64_t T, int64_t H, int64_t Hk,
-                   int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, void* stream);
+                   int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, const int32_t* pack,
+                   int64_t NT, void* stream);
 
 /* The sequential state pass (north star (2) + (3)): S <- exp(G_last) S + K^T diag(e) (U - W S) over the chunks from
  * s0 (NULL = zeros).  flags = 0: the output O = diag(gamma) Q S + M Vn to o (dtype) and the final state to sT when
@@ -77,7 +86,8 @@ int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, 
  * _chunked.py:315-659). */
 int macai_gdr_state_fwd(const void* W, const float* U, const void* Ke, const float* GL, const void* Qg, const void* M,
                         const float* s0, void* o, float* sT, float* Sc, void* Vn, int64_t B, int64_t T, int64_t H,
-                        int64_t DK, int64_t DV, int32_t dtype, int32_t flags, int32_t split, void* stream);
+                        int64_t DK, int64_t DV, int32_t dtype, int32_t flags, int32_t split, const int32_t* pack,
+                        int64_t NT, void* stream);
 
 /* The reverse state pass (north star (4)): from dS_NT = dsT (NULL = zeros) back over the chunks, dVn = M^T dO +
  * diag(e) K dS, dS <- exp(G_last) dS + (diag(gamma) Q)^T dO - W^T dVn; stores dSn (= dS_{c+1}) and dVn per chunk and
@@ -85,7 +95,8 @@ int macai_gdr_state_fwd(const void* W, const float* U, const void* Ke, const flo
  * H, DV, ...)` (reference op.py:234; kernel _chunked.py:661-903). */
 int macai_gdr_state_bwd(const void* Ke, const void* Qg, const void* W, const void* M, const float* GL,
                         const void* dO, const float* dsT, float* dSn, void* dVn, float* ds0, int64_t B, int64_t T,
-                        int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t split, void* stream);
+                        int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t split, const int32_t* pack,
+                        int64_t NT, void* stream);
 
 /* The backward's recompute pass (macai_gdr_state_fwd with STORE_STATES | NO_OUTPUT: Sc, Vn) and its reverse pass
  * (macai_gdr_state_bwd: dSn, dVn, ds0) in one launch, side by side on the CUs: they read prep's outputs, not each
@@ -95,7 +106,7 @@ int macai_gdr_state_bwd(const void* Ke, const void* Qg, const void* W, const voi
 int macai_gdr_state_pair(const void* W, const float* U, const void* Ke, const void* Qg, const void* M, const float* GL,
                          const float* s0, const void* dO, const float* dsT, float* Sc, void* Vn, float* dSn, void* dVn,
                          float* ds0, int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV, int32_t dtype,
-                         int32_t split, void* stream);
+                         int32_t split, const int32_t* pack, int64_t NT, void* stream);
 
 /* The per-chunk backward (north star (4)): dq, dk (w.r.t. the raw inputs when use_l2norm; per value head, [B, T, H,
  * DK]), dv in dtype; dg, dbeta in float32; one writer per element (bitwise deterministic).  Replaces
@@ -105,7 +116,7 @@ int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float
                         const void* A, const float* Sc, const float* dSn, const void* Vn,
                         const void* dVn, void* dq, void* dk, void* dv, float* dg, float* dbeta, int64_t B, int64_t T,
                         int64_t H, int64_t Hk, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm,
-                        float q_scale, void* stream);
+                        float q_scale, const int32_t* pack, int64_t NT, void* stream);
 
 /* One recurrent step per sequence (T = 1): q, k [B, 1, Hk, DK], v [B, 1, H, DV] dtype; g, beta [B, 1, H] float32;
  * s_in, s_out [B, H, DK, DV] float32 (s_out may equal s_in).  S' = e^g S + k beta (v - e^g S^T k)^T, o = S'^T q.  The

@@ -49,6 +49,7 @@ struct PrepArgs {
   int l2norm;
   float q_scale;
   int Hk;        // key heads of q, k ([B,T,Hk,DK]); value head h reads key head h / (H / Hk)
+  const int* pack;  // packed rows (see chunk_span) or null
 };
 
 struct StateFwdArgs {
@@ -64,6 +65,7 @@ struct StateFwdArgs {
   void* Vn;      // [B,H,NT,C,DV]  MT
   int B, T, H, DV, NT;
   int nslice;    // workgroups per head-row
+  const int* pack;  // packed rows (see chunk_span) or null
 };
 
 struct StateBwdArgs {
@@ -76,6 +78,7 @@ struct StateBwdArgs {
   float* ds0;    // [B,H,DK,DV]
   int B, T, H, DV, NT;
   int nslice;
+  const int* pack;  // packed rows (see chunk_span) or null
 };
 
 struct ChunkBwdArgs {
@@ -92,7 +95,32 @@ struct ChunkBwdArgs {
   int l2norm;
   float q_scale;
   int Hk;                                     // key heads of q, k; value head h reads key head h / (H / Hk)
+  const int* pack;                            // packed rows (see chunk_span) or null
 };
+
+// Packed rows (several sequences in one row, cu_seqlens): `pack` holds, for the NT chunks of all sequences, each
+// chunk's first token and its sequence's end, then each sequence's first chunk ([t0 x NT | end x NT | c0 x (B + 1)]).
+// Token tensors are then [1, T, ...] and per-chunk tensors [1, H, NT, ...]; B counts sequences (the state passes run
+// B x H head-rows, each over its sequence's chunks; states are [B, H, DK, DV]).  Without it, chunk c of batch row b
+// spans tokens 64 c .. min(64 c + 64, T) of that row.
+__device__ __forceinline__ void chunk_span(const int* pack, int NT, int c, int T, int& t0, int& tend) {
+  if (pack) {
+    t0 = pack[c];
+    tend = pack[NT + c];
+  } else {
+    t0 = c * C;
+    tend = T;
+  }
+}
+__device__ __forceinline__ void seq_chunks(const int* pack, int NT, int seq, int& cb, int& ce) {
+  if (pack) {
+    cb = pack[2 * NT + seq];
+    ce = pack[2 * NT + seq + 1];
+  } else {
+    cb = 0;
+    ce = NT;
+  }
+}
 
 struct DecodeArgs {
   const void *q, *k, *v;
@@ -131,12 +159,13 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
   __shared__ float rk[C], rq[C];
 
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int T = a.T, H = a.H, DV = a.DV, NT = a.NT;
-  const int t0 = c * C;
+  const int H = a.H, DV = a.DV, NT = a.NT;
+  int t0, T;                               // the chunk's first token; T: its sequence's end (the bound for its rows)
+  chunk_span(a.pack, NT, c, a.T, t0, T);
   const int l = lane_id(), w = wave_id(), j = l >> 4;
-  const size_t qk_base = ((size_t)b * T * a.Hk + h / (H / a.Hk)) * DK, qk_pitch = (size_t)a.Hk * DK;
-  const size_t v_base = ((size_t)b * T * H + h) * DV, v_pitch = (size_t)H * DV;
-  const size_t s_base = (size_t)b * T * H + h;
+  const size_t qk_base = ((size_t)b * a.T * a.Hk + h / (H / a.Hk)) * DK, qk_pitch = (size_t)a.Hk * DK;
+  const size_t v_base = ((size_t)b * a.T * H + h) * DV, v_pitch = (size_t)H * DV;
+  const size_t s_base = (size_t)b * a.T * H + h;
   const size_t bhc = ((size_t)b * H + h) * NT + c;
   const IT* q = (const IT*)a.q + qk_base;
   const IT* k = (const IT*)a.k + qk_base;
@@ -334,12 +363,14 @@ __global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
   __shared__ __attribute__((aligned(16))) float rk[C], rq[C], fW[C], fU[C];
 
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int T = a.T, H = a.H, DV = a.DV, NT = a.NT;
-  const int t0 = c * C, nrows = (T - t0 < C) ? T - t0 : C;
+  const int H = a.H, DV = a.DV, NT = a.NT;
+  int t0, T;                               // the chunk's first token; T: its sequence's end (the bound for its rows)
+  chunk_span(a.pack, NT, c, a.T, t0, T);
+  const int nrows = (T - t0 < C) ? T - t0 : C;
   const int l = lane_id(), w = wave_id(), j = l >> 4, n = l & 15;
-  const size_t qk_base = ((size_t)b * T * a.Hk + h / (H / a.Hk)) * DK, qk_pitch = (size_t)a.Hk * DK;
-  const size_t v_base = ((size_t)b * T * H + h) * DV, v_pitch = (size_t)H * DV;
-  const size_t s_base = (size_t)b * T * H + h;
+  const size_t qk_base = ((size_t)b * a.T * a.Hk + h / (H / a.Hk)) * DK, qk_pitch = (size_t)a.Hk * DK;
+  const size_t v_base = ((size_t)b * a.T * H + h) * DV, v_pitch = (size_t)H * DV;
+  const size_t s_base = (size_t)b * a.T * H + h;
   const size_t bhc = ((size_t)b * H + h) * NT + c;
   const MT* q = (const MT*)a.q + qk_base;
   const MT* k = (const MT*)a.k + qk_base;
@@ -636,6 +667,10 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
   if (!state_map(a.nslice, a.B * H, hr, slice, f)) return;
   const int b = hr / H, h = hr % H;
   const int l = lane_id(), w = wave_id(), j = l >> 4;
+  int cb, ce;                              // this head-row's chunks (its sequence's, for packed rows)
+  seq_chunks(a.pack, NT, b, cb, ce);
+  const size_t crow = a.pack ? (size_t)h : (size_t)hr;   // row of the per-chunk tensors [*, H, NT, ...]
+  const int tb = a.pack ? 0 : b;           // batch row of the token tensors
 
   if (w == NW) {
     // the loader wave: every asynchronous copy of the chunk tiles, one chunk ahead of the compute waves, so that their
@@ -645,7 +680,7 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
     if (OUT) GM::template plan<1>(offM, 0, C);
     auto issue = [&](int c, int buf) {
       MT* st = lds + buf * SZ;
-      const size_t bhc = (size_t)hr * NT + c;
+      const size_t bhc = crow * NT + c;
       GW::template dma_planned<1>(st, (const MT*)a.W + bhc * C * DK, offW, 0);
       GW::template dma_planned<1>(st + O_KE, (const MT*)a.Ke + bhc * C * DK, offW, 0);
       if (OUT) {
@@ -654,16 +689,18 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
       }
     };
     if (NBUF == 2) {
-      issue(0, 0);
-      wait_dma();
-      __syncthreads();
-      for (int c = 0; c < NT; ++c) {
-        if (c + 1 < NT) issue(c + 1, (c + 1) & 1);
+      if (cb < ce) {
+        issue(cb, 0);
+        wait_dma();
+        __syncthreads();
+      }
+      for (int c = cb; c < ce; ++c) {
+        if (c + 1 < ce) issue(c + 1, (c + 1 - cb) & 1);
         wait_dma();
         __syncthreads();
       }
     } else {
-      for (int c = 0; c < NT; ++c) {
+      for (int c = cb; c < ce; ++c) {
         issue(c, 0);
         wait_dma();
         __syncthreads();   // chunk c is in LDS
@@ -675,9 +712,9 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
 
   const int v0 = (slice * NW + w) * 16;
   const int col = v0 + (l & 15);
-  const size_t o_base = ((size_t)b * T * H + h) * DV, o_pitch = (size_t)H * DV;
+  const size_t o_base = ((size_t)tb * T * H + h) * DV, o_pitch = (size_t)H * DV;
   auto loadU = [&](int c, f4* U) {
-    const float* Uc = a.U + ((size_t)hr * NT + c) * C * DV + (size_t)(4 * j) * DV + col;
+    const float* Uc = a.U + (crow * NT + c) * C * DV + (size_t)(4 * j) * DV + col;
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
@@ -688,14 +725,16 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
   // O^T tiles: lane l holds O[16 mi + l % 16][v0 + 4 j + 0..3], four adjacent outputs of one token (one 8- or
   // 16-byte store each)
   auto store_o = [&](int c, const f4 (&Ot)[4]) {
+    int t0, tend;
+    chunk_span(a.pack, NT, c, T, t0, tend);
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
-      const int t = c * C + 16 * mi + (l & 15);
-      if (t < T) store4<MT>((MT*)a.o + o_base + (size_t)t * o_pitch + v0 + 4 * j, Ot[mi]);
+      const int t = t0 + 16 * mi + (l & 15);
+      if (t < tend) store4<MT>((MT*)a.o + o_base + (size_t)t * o_pitch + v0 + 4 * j, Ot[mi]);
     }
   };
   auto store_sc = [&](int c, const f4 (&X)[ND]) {
-    float* Scc = a.Sc + ((size_t)hr * NT + c) * DK * DV + (size_t)(4 * j) * DV + col;
+    float* Scc = a.Sc + (crow * NT + c) * DK * DV + (size_t)(4 * j) * DV + col;
 #pragma unroll
     for (int di = 0; di < ND; ++di)
 #pragma unroll
@@ -703,9 +742,9 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
   };
   auto store_vn = [&](int c, const f4 (&X)[4]) {
     if constexpr (sizeof(MT) == 2) {
-      store_cols(lds + L::O_STG + w * ColStage::ELEMS, (MT*)a.Vn + ((size_t)hr * NT + c) * C * DV + v0, DV, X);
+      store_cols(lds + L::O_STG + w * ColStage::ELEMS, (MT*)a.Vn + (crow * NT + c) * C * DV + v0, DV, X);
     } else {
-      MT* Vnc = (MT*)a.Vn + ((size_t)hr * NT + c) * C * DV + (size_t)(4 * j) * DV + col;
+      MT* Vnc = (MT*)a.Vn + (crow * NT + c) * C * DV + (size_t)(4 * j) * DV + col;
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
@@ -717,17 +756,20 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
   load_state(S, a.s0, (size_t)hr * DK * DV, DV, col);
 
   f4 Un[4];
-  loadU(0, Un);
-  float gln = a.GL[(size_t)hr * NT];
-  if (NBUF == 2) __syncthreads();          // chunk 0 is in LDS
-  for (int c = 0; c < NT; ++c) {
-    const size_t bhc = (size_t)hr * NT + c;
-    const int buf = (NBUF == 2) ? (c & 1) : 0;
+  float gln = 0.f;
+  if (cb < ce) {
+    loadU(cb, Un);
+    gln = a.GL[crow * NT + cb];
+    if (NBUF == 2) __syncthreads();        // the first chunk is in LDS
+  }
+  for (int c = cb; c < ce; ++c) {
+    const size_t bhc = crow * NT + c;
+    const int buf = (NBUF == 2) ? ((c - cb) & 1) : 0;
     f4 U[4];
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) U[mi] = Un[mi];
     const float gl = gln;
-    if (c + 1 < NT) {
+    if (c + 1 < ce) {
       loadU(c + 1, Un);
       gln = a.GL[bhc + 1];
     }
@@ -866,7 +908,11 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
   const int b = hr / H, h = hr % H;
   const int l = lane_id(), w = wave_id(), j = l >> 4;
   const int vg = slice * NW * 16;            // the workgroup's first value column
-  const size_t o_base = ((size_t)b * T * H + h) * DV, o_pitch = (size_t)H * DV;
+  int cb, ce;                                // this head-row's chunks (its sequence's, for packed rows)
+  seq_chunks(a.pack, NT, b, cb, ce);
+  const size_t crow = a.pack ? (size_t)h : (size_t)hr;   // row of the per-chunk tensors [*, H, NT, ...]
+  const int tb = a.pack ? 0 : b;             // batch row of the token tensors
+  const size_t o_base = ((size_t)tb * T * H + h) * DV, o_pitch = (size_t)H * DV;
 
   if (w == NW) {
     // the loader wave (see state_fwd_kernel), walking the chunks backwards
@@ -876,27 +922,30 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
     GO::template plan<1>(offO, 0, (int)o_pitch);
     auto issue = [&](int c, int buf) {
       MT* st = lds + buf * SZ;
-      const size_t bhc = (size_t)hr * NT + c;
-      const int t0 = c * C;
+      const size_t bhc = crow * NT + c;
+      int t0, tend;
+      chunk_span(a.pack, NT, c, T, t0, tend);
       GK::template dma_planned<1>(st, (const MT*)a.Ke + bhc * C * DK, offK, 0);
       GK::template dma_planned<1>(st + O_Q, (const MT*)a.Qg + bhc * C * DK, offK, 0);
       GK::template dma_planned<1>(st + O_W, (const MT*)a.W + bhc * C * DK, offK, 0);
       GM::template dma_planned<1>(st + O_M, (const MT*)a.M + bhc * C * C, offM, 0);
       const MT* og = (const MT*)a.dO + o_base + (size_t)t0 * o_pitch + vg;
-      if (t0 + C <= T) GO::template dma_planned<1>(st + O_O, og, offO, 0);
-      else GO::dma(st + O_O, og, o_pitch, 0, 1, T - t0);   // the last, partial chunk: rows clamped in range
+      if (t0 + C <= tend) GO::template dma_planned<1>(st + O_O, og, offO, 0);
+      else GO::dma(st + O_O, og, o_pitch, 0, 1, tend - t0);   // a partial chunk: rows clamped to the sequence
     };
     if (NBUF == 2) {
-      issue(NT - 1, 0);
-      wait_dma();
-      __syncthreads();
-      for (int c = NT - 1, it = 0; c >= 0; --c, ++it) {
-        if (c > 0) issue(c - 1, (it + 1) & 1);
+      if (cb < ce) {
+        issue(ce - 1, 0);
+        wait_dma();
+        __syncthreads();
+      }
+      for (int c = ce - 1, it = 0; c >= cb; --c, ++it) {
+        if (c > cb) issue(c - 1, (it + 1) & 1);
         wait_dma();
         __syncthreads();
       }
     } else {
-      for (int c = NT - 1; c >= 0; --c) {
+      for (int c = ce - 1; c >= cb; --c) {
         issue(c, 0);
         wait_dma();
         __syncthreads();
@@ -908,7 +957,7 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
   const int col = vg + w * 16 + (l & 15);
   // dS_{c+1} and dVn go out as soon as they exist
   auto store_ds = [&](int c, const f4 (&X)[ND]) {
-    float* dSc = a.dSn + ((size_t)hr * NT + c) * DK * DV + (size_t)(4 * j) * DV + col;
+    float* dSc = a.dSn + (crow * NT + c) * DK * DV + (size_t)(4 * j) * DV + col;
 #pragma unroll
     for (int di = 0; di < ND; ++di)
 #pragma unroll
@@ -916,9 +965,9 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
   };
   auto store_dv = [&](int c, const f4 (&X)[4]) {
     if constexpr (sizeof(MT) == 2) {
-      store_cols(lds + L::O_STG + w * ColStage::ELEMS, (MT*)a.dVn + ((size_t)hr * NT + c) * C * DV + vg + 16 * w, DV, X);
+      store_cols(lds + L::O_STG + w * ColStage::ELEMS, (MT*)a.dVn + (crow * NT + c) * C * DV + vg + 16 * w, DV, X);
     } else {
-      MT* dVc = (MT*)a.dVn + ((size_t)hr * NT + c) * C * DV + (size_t)(4 * j) * DV + col;
+      MT* dVc = (MT*)a.dVn + (crow * NT + c) * C * DV + (size_t)(4 * j) * DV + col;
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
@@ -929,14 +978,18 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
   f4 dS[ND];
   load_state(dS, a.dsT, (size_t)hr * DK * DV, DV, col);
 
-  float gln = a.GL[(size_t)hr * NT + NT - 1];
-  if (NBUF == 2) __syncthreads();          // the last chunk is in LDS
-  for (int c = NT - 1, it = 0; c >= 0; --c, ++it) {
-    const int t0 = c * C;
-    const size_t bhc = (size_t)hr * NT + c;
+  float gln = 0.f;
+  if (cb < ce) {
+    gln = a.GL[crow * NT + ce - 1];
+    if (NBUF == 2) __syncthreads();        // the last chunk is in LDS
+  }
+  for (int c = ce - 1, it = 0; c >= cb; --c, ++it) {
+    int t0, tend;
+    chunk_span(a.pack, NT, c, T, t0, tend);
+    const size_t bhc = crow * NT + c;
     const int buf = (NBUF == 2) ? (it & 1) : 0;
     const float gl = gln;
-    if (c > 0) gln = a.GL[bhc - 1];
+    if (c > cb) gln = a.GL[bhc - 1];
     store_ds(c, dS);
     if (NBUF == 1) __syncthreads();        // chunk c is in LDS
     const MT* st = lds + buf * SZ;
@@ -946,10 +999,10 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
     for (int p = 0; p < 2; ++p) {
       if constexpr (sizeof(MT) == 2) Of[p] = frag_tr(st + O_O, GO::PITCH, 32 * p, w * 16);
       else Of[p] = frag_tile_rows<MT, GO>(st + O_O, 32 * p, w * 16 + (l & 15));
-      if (t0 + C > T)   // rows past the sequence end hold copies of the last row: zero them
+      if (t0 + C > tend)   // rows past the sequence end hold copies of its last row: zero them
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          if (t0 + 32 * p + kmap(j, e) >= T) Of[p].set(e, 0.f);
+          if (t0 + 32 * p + kmap(j, e) >= tend) Of[p].set(e, 0.f);
     }
     Frag<MT> Sf[ND / 2];
 #pragma unroll
@@ -1054,13 +1107,15 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
   __shared__ float colR1[C], colR2b[C];
 
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int T = a.T, H = a.H, NT = a.NT;
-  const int t0 = c * C, nrows = (T - t0 < C) ? T - t0 : C;
+  const int H = a.H, NT = a.NT;
+  int t0, T;                               // the chunk's first token; T: its sequence's end (the bound for its rows)
+  chunk_span(a.pack, NT, c, a.T, t0, T);
+  const int nrows = (T - t0 < C) ? T - t0 : C;
   const int l = lane_id(), w = wave_id(), j = l >> 4;
-  const size_t qk_base = ((size_t)b * T * a.Hk + h / (H / a.Hk)) * DK, qk_pitch = (size_t)a.Hk * DK;
-  const size_t dqk_base = ((size_t)b * T * H + h) * DK, dqk_pitch = (size_t)H * DK;   // dq, dk: value heads
-  const size_t v_base = ((size_t)b * T * H + h) * DV, v_pitch = (size_t)H * DV;
-  const size_t s_base = (size_t)b * T * H + h;
+  const size_t qk_base = ((size_t)b * a.T * a.Hk + h / (H / a.Hk)) * DK, qk_pitch = (size_t)a.Hk * DK;
+  const size_t dqk_base = ((size_t)b * a.T * H + h) * DK, dqk_pitch = (size_t)H * DK;   // dq, dk: value heads
+  const size_t v_base = ((size_t)b * a.T * H + h) * DV, v_pitch = (size_t)H * DV;
+  const size_t s_base = (size_t)b * a.T * H + h;
   const size_t bhc = ((size_t)b * H + h) * NT + c;
   const MT* q = (const MT*)a.q + qk_base;
   const MT* k = (const MT*)a.k + qk_base;
@@ -1489,13 +1544,15 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   __shared__ float partS[NW];
 
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int T = a.T, H = a.H, NT = a.NT;
-  const int t0 = c * C, nrows = (T - t0 < C) ? T - t0 : C;
+  const int H = a.H, NT = a.NT;
+  int t0, T;                               // the chunk's first token; T: its sequence's end (the bound for its rows)
+  chunk_span(a.pack, NT, c, a.T, t0, T);
+  const int nrows = (T - t0 < C) ? T - t0 : C;
   const int l = lane_id(), w = wave_id(), j = l >> 4, n = l & 15;
-  const size_t qk_base = ((size_t)b * T * a.Hk + h / (H / a.Hk)) * DK, qk_pitch = (size_t)a.Hk * DK;
-  const size_t dqk_base = ((size_t)b * T * H + h) * DK, dqk_pitch = (size_t)H * DK;   // dq, dk: value heads
-  const size_t v_base = ((size_t)b * T * H + h) * DV, v_pitch = (size_t)H * DV;
-  const size_t s_base = (size_t)b * T * H + h;
+  const size_t qk_base = ((size_t)b * a.T * a.Hk + h / (H / a.Hk)) * DK, qk_pitch = (size_t)a.Hk * DK;
+  const size_t dqk_base = ((size_t)b * a.T * H + h) * DK, dqk_pitch = (size_t)H * DK;   // dq, dk: value heads
+  const size_t v_base = ((size_t)b * a.T * H + h) * DV, v_pitch = (size_t)H * DV;
+  const size_t s_base = (size_t)b * a.T * H + h;
   const size_t bhc = ((size_t)b * H + h) * NT + c;
   const MT* q = (const MT*)a.q + qk_base;
   const MT* k = (const MT*)a.k + qk_base;
@@ -2173,6 +2230,21 @@ static int check_common(const char* what, int64_t B, int64_t T, int64_t H, int64
   return MACAI_GDR_OK;
 }
 
+// Packed rows: `pack` (NULL = each batch row is one sequence) with its chunk count; sets NT.  The table's contents
+// (built by the caller from cu_seqlens) are on the device and are not checked here.
+static int pack_chunks(const char* what, const int32_t* pack, int64_t NT_packed, int64_t B, int64_t T, int64_t* NT) {
+  if (!pack) {
+    *NT = (T + C - 1) / C;
+    return MACAI_GDR_OK;
+  }
+  if (NT_packed < 1 || NT_packed > T || NT_packed + B + 1 > ((int64_t)1 << 28))
+    return fail(MACAI_GDR_EINVAL, "%s: packed rows need 1 <= chunks <= T (got %lld chunks, T = %lld)", what,
+                (long long)NT_packed, (long long)T);
+  if (((uintptr_t)pack & 3u) != 0) return fail(MACAI_GDR_EINVAL, "%s: the packed-row table must be 4-byte aligned", what);
+  *NT = NT_packed;
+  return MACAI_GDR_OK;
+}
+
 static int check_heads(const char* what, int64_t H, int64_t Hk) {
   if (Hk < 1 || H % Hk != 0)
     return fail(MACAI_GDR_EINVAL, "%s: key heads must divide value heads (got Hk = %lld, H = %lld)", what,
@@ -2213,19 +2285,22 @@ int macai_gdr_abi_version(void) { return MACAI_GDR_ABI_VERSION; }
 
 int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, const float* beta, void* W, float* U,
                    void* Ke, float* GL, void* Qg, void* M, void* A, int64_t B, int64_t T, int64_t H, int64_t Hk,
-                   int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, void* stream) {
+                   int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, const int32_t* pack,
+                   int64_t NT_packed, void* stream) {
   const char* what = "macai_gdr_prep";
-  int rc = check_common(what, B, T, H, DK, DV, dtype);
+  int64_t NT = 0;
+  int rc = check_common(what, pack ? 1 : B, T, H, DK, DV, dtype);
   if (!rc) rc = check_heads(what, H, Hk);
+  if (!rc) rc = pack_chunks(what, pack, NT_packed, B, T, &NT);
   if (rc) return rc;
   if (!q || !k || !v || !g || !beta || !W || !U || !Ke || !GL || !Qg || !M)
     return fail(MACAI_GDR_EINVAL, "%s: null input or output pointer", what);
   const void* ps[] = {q, k, v, W, U, Ke, Qg, M, A};
   for (const void* p : ps)
     if (!aligned16(p)) return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
-  PrepArgs a{q, k, v, g, beta, W, U, Ke, GL, Qg, M, A, (int)B, (int)T, (int)H, (int)DV, (int)((T + C - 1) / C),
-             use_l2norm, q_scale, (int)Hk};
-  dim3 grid(a.NT, (unsigned)H, (unsigned)B);
+  PrepArgs a{q, k, v, g, beta, W, U, Ke, GL, Qg, M, A, (int)B, (int)T, (int)H, (int)DV, (int)NT,
+             use_l2norm, q_scale, (int)Hk, pack};
+  dim3 grid(a.NT, (unsigned)H, pack ? 1u : (unsigned)B);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == MACAI_GDR_F32) {
     DISPATCH_DK(DK, hipLaunchKernelGGL((prep_kernel<float, float, DKC>), grid, dim3(256), 0, st, a));
@@ -2252,9 +2327,12 @@ int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, 
 
 int macai_gdr_state_fwd(const void* W, const float* U, const void* Ke, const float* GL, const void* Qg, const void* M,
                         const float* s0, void* o, float* sT, float* Sc, void* Vn, int64_t B, int64_t T, int64_t H,
-                        int64_t DK, int64_t DV, int32_t dtype, int32_t flags, int32_t split, void* stream) {
+                        int64_t DK, int64_t DV, int32_t dtype, int32_t flags, int32_t split, const int32_t* pack,
+                        int64_t NT_packed, void* stream) {
   const char* what = "macai_gdr_state_fwd";
-  int rc = check_common(what, B, T, H, DK, DV, dtype);
+  int64_t NT = 0;
+  int rc = check_common(what, pack ? 1 : B, T, H, DK, DV, dtype);
+  if (!rc) rc = pack_chunks(what, pack, NT_packed, B, T, &NT);
   if (rc) return rc;
   const bool store = flags & MACAI_GDR_STORE_STATES, out = !(flags & MACAI_GDR_NO_OUTPUT);
   if (out == store)
@@ -2268,7 +2346,7 @@ int macai_gdr_state_fwd(const void* W, const float* U, const void* Ke, const flo
   int nw, nslice;
   if ((rc = pick_waves(DV, split, what, &nw, &nslice))) return rc;
   StateFwdArgs a{W, U, Ke, GL, Qg, M, s0, o, out ? sT : nullptr, Sc, Vn, (int)B, (int)T, (int)H, (int)DV,
-                 (int)((T + C - 1) / C), nslice};
+                 (int)NT, nslice, pack};
   const int HR = (int)(B * H);
   dim3 grid((unsigned)(8 * nslice * ((HR + 7) / 8)));
   dim3 block(64 * (nw + 1));   // nw compute waves and the loader wave
@@ -2288,9 +2366,12 @@ int macai_gdr_state_fwd(const void* W, const float* U, const void* Ke, const flo
 
 int macai_gdr_state_bwd(const void* Ke, const void* Qg, const void* W, const void* M, const float* GL,
                         const void* dO, const float* dsT, float* dSn, void* dVn, float* ds0, int64_t B, int64_t T,
-                        int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t split, void* stream) {
+                        int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t split, const int32_t* pack,
+                        int64_t NT_packed, void* stream) {
   const char* what = "macai_gdr_state_bwd";
-  int rc = check_common(what, B, T, H, DK, DV, dtype);
+  int64_t NT = 0;
+  int rc = check_common(what, pack ? 1 : B, T, H, DK, DV, dtype);
+  if (!rc) rc = pack_chunks(what, pack, NT_packed, B, T, &NT);
   if (rc) return rc;
   if (!Ke || !Qg || !W || !M || !GL || !dO || !dSn || !dVn || !ds0)
     return fail(MACAI_GDR_EINVAL, "%s: null pointer", what);
@@ -2299,8 +2380,7 @@ int macai_gdr_state_bwd(const void* Ke, const void* Qg, const void* W, const voi
     if (!aligned16(p)) return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
   int nw, nslice;
   if ((rc = pick_waves(DV, split, what, &nw, &nslice))) return rc;
-  StateBwdArgs a{Ke, Qg, W, M, GL, dO, dsT, dSn, dVn, ds0, (int)B, (int)T, (int)H, (int)DV, (int)((T + C - 1) / C),
-                 nslice};
+  StateBwdArgs a{Ke, Qg, W, M, GL, dO, dsT, dSn, dVn, ds0, (int)B, (int)T, (int)H, (int)DV, (int)NT, nslice, pack};
   const int HR = (int)(B * H);
   dim3 grid((unsigned)(8 * nslice * ((HR + 7) / 8)));
   dim3 block(64 * (nw + 1));   // nw compute waves and the loader wave
@@ -2316,9 +2396,11 @@ int macai_gdr_state_bwd(const void* Ke, const void* Qg, const void* W, const voi
 int macai_gdr_state_pair(const void* W, const float* U, const void* Ke, const void* Qg, const void* M, const float* GL,
                          const float* s0, const void* dO, const float* dsT, float* Sc, void* Vn, float* dSn, void* dVn,
                          float* ds0, int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV, int32_t dtype,
-                         int32_t split, void* stream) {
+                         int32_t split, const int32_t* pack, int64_t NT_packed, void* stream) {
   const char* what = "macai_gdr_state_pair";
-  int rc = check_common(what, B, T, H, DK, DV, dtype);
+  int64_t NT = 0;
+  int rc = check_common(what, pack ? 1 : B, T, H, DK, DV, dtype);
+  if (!rc) rc = pack_chunks(what, pack, NT_packed, B, T, &NT);
   if (rc) return rc;
   if (!W || !U || !Ke || !Qg || !M || !GL || !dO || !Sc || !Vn || !dSn || !dVn || !ds0)
     return fail(MACAI_GDR_EINVAL, "%s: null pointer", what);
@@ -2327,10 +2409,10 @@ int macai_gdr_state_pair(const void* W, const float* U, const void* Ke, const vo
     if (!aligned16(p)) return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
   int nw, nslice;
   if ((rc = pick_waves(DV, split, what, &nw, &nslice))) return rc;
-  const int NTi = (int)((T + C - 1) / C);
+  const int NTi = (int)NT;
   StateFwdArgs af{W, U, Ke, GL, nullptr, nullptr, s0, nullptr, nullptr, Sc, Vn, (int)B, (int)T, (int)H, (int)DV, NTi,
-                  nslice};
-  StateBwdArgs ab{Ke, Qg, W, M, GL, dO, dsT, dSn, dVn, ds0, (int)B, (int)T, (int)H, (int)DV, NTi, nslice};
+                  nslice, pack};
+  StateBwdArgs ab{Ke, Qg, W, M, GL, dO, dsT, dSn, dVn, ds0, (int)B, (int)T, (int)H, (int)DV, NTi, nslice, pack};
   const int HR = (int)(B * H);
   const int nfwd = 8 * nslice * ((HR + 7) / 8);   // a multiple of 8: the second pass keeps state_map's XCD layout
   dim3 grid((unsigned)(2 * nfwd));
@@ -2350,10 +2432,12 @@ int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float
                         const void* A, const float* Sc, const float* dSn, const void* Vn,
                         const void* dVn, void* dq, void* dk, void* dv, float* dg, float* dbeta, int64_t B, int64_t T,
                         int64_t H, int64_t Hk, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale,
-                        void* stream) {
+                        const int32_t* pack, int64_t NT_packed, void* stream) {
   const char* what = "macai_gdr_chunk_bwd";
-  int rc = check_common(what, B, T, H, DK, DV, dtype);
+  int64_t NT = 0;
+  int rc = check_common(what, pack ? 1 : B, T, H, DK, DV, dtype);
   if (!rc) rc = check_heads(what, H, Hk);
+  if (!rc) rc = pack_chunks(what, pack, NT_packed, B, T, &NT);
   if (rc) return rc;
   if (DV != 32 && DV != 64 && DV != 96 && DV != 128)
     return fail(MACAI_GDR_EUNSUP, "%s: the backward takes value head widths 32, 64, 96 or 128 (got %lld)", what,
@@ -2365,8 +2449,8 @@ int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float
   for (const void* p : ps)
     if (!aligned16(p)) return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
   ChunkBwdArgs a{q, k, v, g, beta, dO, A, Sc, dSn, Vn, dVn, dq, dk, dv, dg, dbeta, (int)B, (int)T, (int)H,
-                 (int)DV, (int)((T + C - 1) / C), use_l2norm, q_scale, (int)Hk};
-  dim3 grid(a.NT, (unsigned)H, (unsigned)B);
+                 (int)DV, (int)NT, use_l2norm, q_scale, (int)Hk, pack};
+  dim3 grid(a.NT, (unsigned)H, pack ? 1u : (unsigned)B);
   hipStream_t st = (hipStream_t)stream;
 #define LAUNCH_CB(MT)                                                                                               \
   DISPATCH_DK(DK, switch (DV) {                                                                                    \

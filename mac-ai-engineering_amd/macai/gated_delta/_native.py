@@ -14,16 +14,16 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 F32, BF16 = 0, 1
 OK, EINVAL, EUNSUP, ELAUNCH = 0, 1, 2, 3
 STORE_STATES, NO_OUTPUT = 1, 8
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _p, _i64, _i32, _f = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 # name -> argument types (the order of include/macai_gdr.h)
 SIGNATURES = {
-    "macai_gdr_prep": [_p] * 12 + [_i64] * 6 + [_i32, _i32, _f, _p],
-    "macai_gdr_state_fwd": [_p] * 11 + [_i64] * 5 + [_i32, _i32, _i32, _p],
-    "macai_gdr_state_bwd": [_p] * 10 + [_i64] * 5 + [_i32, _i32, _p],
-    "macai_gdr_state_pair": [_p] * 14 + [_i64] * 5 + [_i32, _i32, _p],
-    "macai_gdr_chunk_bwd": [_p] * 16 + [_i64] * 6 + [_i32, _i32, _f, _p],
+    "macai_gdr_prep": [_p] * 12 + [_i64] * 6 + [_i32, _i32, _f, _p, _i64, _p],
+    "macai_gdr_state_fwd": [_p] * 11 + [_i64] * 5 + [_i32, _i32, _i32, _p, _i64, _p],
+    "macai_gdr_state_bwd": [_p] * 10 + [_i64] * 5 + [_i32, _i32, _p, _i64, _p],
+    "macai_gdr_state_pair": [_p] * 14 + [_i64] * 5 + [_i32, _i32, _p, _i64, _p],
+    "macai_gdr_chunk_bwd": [_p] * 16 + [_i64] * 6 + [_i32, _i32, _f, _p, _i64, _p],
     "macai_gdr_decode": [_p] * 8 + [_i64] * 5 + [_i32, _i32, _f, _p],
     "macai_gdr_group_sum": [_p] * 2 + [_i64] * 5 + [_i32, _p],
 }

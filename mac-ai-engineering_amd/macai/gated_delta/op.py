@@ -63,9 +63,10 @@ def split_for(rows: int, T: int, dv: int, share: int = 1) -> int:
     return below[-1] if below else valid[0]
 
 
-def _check(q, k, v, g, beta, s0):
+def _check(q, k, v, g, beta, s0, nseq=None):
     """q, k [B, T, Hk, DK], v [B, T, H, DV] with H a multiple of Hk (grouped value heads: value head h reads key head
-    h // (H // Hk), the layout of q.repeat_interleave(H // Hk, dim=2)); g, beta [B, T, H]; s0 [B, H, DK, DV]."""
+    h // (H // Hk), the layout of q.repeat_interleave(H // Hk, dim=2)); g, beta [B, T, H]; s0 [B, H, DK, DV] -- or,
+    for packed rows (nseq sequences in one row), B = 1 and s0 [nseq, H, DK, DV]."""
     if not q.is_cuda:
         raise RuntimeError("macai's gated delta rule runs on a HIP device (MI355X); got tensors on " + str(q.device))
     if q.dim() != 4 or k.shape != q.shape or v.dim() != 4 or v.shape[:2] != q.shape[:2]:
@@ -77,103 +78,136 @@ def _check(q, k, v, g, beta, s0):
         raise ValueError(f"the key heads of q and k ({Hk}) must divide the value heads of v ({H})")
     if g.shape != (B, T, H) or beta.shape != (B, T, H):
         raise ValueError(f"g and beta must be [B, T, H] = {(B, T, H)}, got {tuple(g.shape)}, {tuple(beta.shape)}")
-    if s0 is not None and s0.shape != (B, H, DK, v.shape[-1]):
-        raise ValueError(f"initial_state must be [B, H, DK, DV] = {(B, H, DK, v.shape[-1])}, got {tuple(s0.shape)}")
+    if nseq is not None and B != 1:
+        raise ValueError(f"packed rows (cu_seqlens) take a batch of one row, got B = {B}")
+    S = B if nseq is None else nseq
+    if s0 is not None and s0.shape != (S, H, DK, v.shape[-1]):
+        raise ValueError(f"initial_state must be [{'B' if nseq is None else 'sequences'}, H, DK, DV] = "
+                         f"{(S, H, DK, v.shape[-1])}, got {tuple(s0.shape)}")
     if not (q.dtype == k.dtype == v.dtype):
         raise ValueError(f"q, k, v must share a dtype, got {q.dtype}, {k.dtype}, {v.dtype}")
     if g.dtype != torch.float32 or beta.dtype != torch.float32 or (s0 is not None and s0.dtype != torch.float32):
         raise ValueError("g, beta and the state must be float32")
 
 
-def _dims(q, v):
-    """(B, T, H value heads, Hk key heads, DK, DV, NT)."""
+def _dims(q, v, pack=None):
+    """(B, T, H value heads, Hk key heads, DK, DV, NT); with packed rows B is the number of sequences and NT the
+    chunks of all of them."""
     B, T, Hk, DK = q.shape
+    if pack is not None:
+        return pack[2], T, v.shape[2], Hk, DK, v.shape[-1], pack[1]
     return B, T, v.shape[2], Hk, DK, v.shape[-1], math.ceil(T / CHUNK)
 
 
-def _prep(q, k, v, g, beta, l2norm: bool, q_scale: float, with_A: bool):
+def _pack(cu_seqlens, T: int, device):
+    """The packed-row table of include/macai_gdr.h for sequences cu[n] .. cu[n+1] of one row of T tokens: each
+    sequence chunked on its own.  Returns (table [2 NT + N + 1] int32 on `device`, NT, N)."""
+    cu = torch.as_tensor(cu_seqlens).reshape(-1).to("cpu", torch.int64).tolist()
+    if len(cu) < 2 or cu[0] != 0 or cu[-1] != T or any(b < a for a, b in zip(cu, cu[1:])):
+        raise ValueError(f"cu_seqlens must rise from 0 to T = {T} (got {cu[:8]}{'...' if len(cu) > 8 else ''})")
+    t0s, ends, c0 = [], [], [0]
+    for a, b in zip(cu, cu[1:]):
+        for t in range(a, b, CHUNK):
+            t0s.append(t)
+            ends.append(b)
+        c0.append(len(t0s))
+    table = torch.tensor(t0s + ends + c0, dtype=torch.int32, device=device)
+    return table, len(t0s), len(cu) - 1
+
+
+def _pack_args(pack):
+    return (None, 0) if pack is None else (N.ptr(pack[0]), pack[1])
+
+
+def _prep(q, k, v, g, beta, l2norm: bool, q_scale: float, with_A: bool, pack=None):
     """The per-chunk operands (row-major, tokens as rows): W, U, diag(e) K^, exp(G_last), diag(gamma) Q^, M, and A when
-    asked (the backward's per-chunk pass)."""
-    B, T, H, Hk, DK, DV, NT = _dims(q, v)
+    asked (the backward's per-chunk pass).  Per-chunk tensors are [B, H, NT, ...] ([1, H, NT, ...] for packed rows)."""
+    B, T, H, Hk, DK, DV, NT = _dims(q, v, pack)
+    Bc = q.shape[0]
     dev, dt = q.device, q.dtype
     f32 = torch.float32
-    W = torch.empty(B, H, NT, CHUNK, DK, device=dev, dtype=dt)
-    r = dict(W=W, U=torch.empty(B, H, NT, CHUNK, DV, device=dev, dtype=f32), Ke=torch.empty_like(W),
-             GL=torch.empty(B, H, NT, device=dev, dtype=f32), Qg=torch.empty_like(W),
-             M=torch.empty(B, H, NT, CHUNK, CHUNK, device=dev, dtype=dt),
-             A=torch.empty(B, H, NT, CHUNK, CHUNK, device=dev, dtype=dt) if with_A else None)
+    W = torch.empty(Bc, H, NT, CHUNK, DK, device=dev, dtype=dt)
+    r = dict(W=W, U=torch.empty(Bc, H, NT, CHUNK, DV, device=dev, dtype=f32), Ke=torch.empty_like(W),
+             GL=torch.empty(Bc, H, NT, device=dev, dtype=f32), Qg=torch.empty_like(W),
+             M=torch.empty(Bc, H, NT, CHUNK, CHUNK, device=dev, dtype=dt),
+             A=torch.empty(Bc, H, NT, CHUNK, CHUNK, device=dev, dtype=dt) if with_A else None)
     P = N.ptr
     _launch("prep_bwd" if with_A else "prep_fwd", "macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(r["W"]),
             P(r["U"]), P(r["Ke"]), P(r["GL"]), P(r["Qg"]), P(r["M"]), P(r["A"]), B, T, H, Hk, DK, DV,
-            N.dtype_code(dt), int(l2norm), q_scale, N.stream_of(q))
+            N.dtype_code(dt), int(l2norm), q_scale, *_pack_args(pack), N.stream_of(q))
     return r
 
 
-def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool):
+def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, pack=None):
     """prep, then the state pass with the output: returns (o in q's dtype, sT or None)."""
-    B, T, H, Hk, DK, DV, NT = _dims(q, v)
+    B, T, H, Hk, DK, DV, NT = _dims(q, v, pack)
     dev, dt = q.device, q.dtype
     code, stream = N.dtype_code(dt), N.stream_of(q)
-    r = _prep(q, k, v, g, beta, l2norm, q_scale, False)
-    o = torch.empty(B, T, H, DV, device=dev, dtype=dt)
+    r = _prep(q, k, v, g, beta, l2norm, q_scale, False, pack)
+    o = torch.empty(q.shape[0], T, H, DV, device=dev, dtype=dt)
     sT = torch.empty(B, H, DK, DV, device=dev, dtype=torch.float32) if want_sT else None
     split = split_for(B * H, T, DV)
     P = N.ptr
     _launch("state_fwd_out", "macai_gdr_state_fwd", P(r["W"]), P(r["U"]), P(r["Ke"]), P(r["GL"]), P(r["Qg"]), P(r["M"]),
-            P(s0), P(o), P(sT), None, None, B, T, H, DK, DV, code, 0, split, stream)
+            P(s0), P(o), P(sT), None, None, B, T, H, DK, DV, code, 0, split, *_pack_args(pack), stream)
     CALLS[f"fwd s{split}"] += 1
     return o, sT
 
 
-def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float):
+def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=None):
     """Recompute (prep; the state pass storing S_c and Vn), the reverse state pass, the per-chunk backward.  Returns
     (dq, dk, dv in q's dtype; dg, dbeta, ds0 float32).  With grouped heads (Hk < H) the per-chunk backward writes dq,
     dk per value head and macai_gdr_group_sum folds each group (the backward of the repeat the grouped layout
     replaces)."""
-    B, T, H, Hk, DK, DV, NT = _dims(q, v)
+    B, T, H, Hk, DK, DV, NT = _dims(q, v, pack)
+    Bc = q.shape[0]
     dev, dt = q.device, q.dtype
     code, stream = N.dtype_code(dt), N.stream_of(q)
     f32 = torch.float32
-    r = _prep(q, k, v, g, beta, l2norm, q_scale, True)
+    r = _prep(q, k, v, g, beta, l2norm, q_scale, True, pack)
     P = N.ptr
+    pk = _pack_args(pack)
     split = split_for(B * H, T, DV, 2 if OVERLAP else 1)
-    Sc = torch.empty(B, H, NT, DK, DV, device=dev, dtype=f32)
-    Vn = torch.empty(B, H, NT, CHUNK, DV, device=dev, dtype=dt)
-    dSn = torch.empty(B, H, NT, DK, DV, device=dev, dtype=f32)
+    Sc = torch.empty(Bc, H, NT, DK, DV, device=dev, dtype=f32)
+    Vn = torch.empty(Bc, H, NT, CHUNK, DV, device=dev, dtype=dt)
+    dSn = torch.empty(Bc, H, NT, DK, DV, device=dev, dtype=f32)
     dVn = torch.empty_like(Vn)
     ds0 = torch.empty(B, H, DK, DV, device=dev, dtype=f32)
     if OVERLAP:
         _launch("state_pair", "macai_gdr_state_pair", P(r["W"]), P(r["U"]), P(r["Ke"]), P(r["Qg"]), P(r["M"]),
                 P(r["GL"]), P(s0), P(do), P(dsT), P(Sc), P(Vn), P(dSn), P(dVn), P(ds0), B, T, H, DK, DV, code, split,
-                stream)
+                *pk, stream)
     else:
         _launch("state_fwd_store", "macai_gdr_state_fwd", P(r["W"]), P(r["U"]), P(r["Ke"]), P(r["GL"]), None, None,
-                P(s0), None, None, P(Sc), P(Vn), B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, stream)
+                P(s0), None, None, P(Sc), P(Vn), B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, *pk,
+                stream)
         _launch("state_bwd", "macai_gdr_state_bwd", P(r["Ke"]), P(r["Qg"]), P(r["W"]), P(r["M"]), P(r["GL"]), P(do),
-                P(dsT), P(dSn), P(dVn), P(ds0), B, T, H, DK, DV, code, split, stream)
+                P(dsT), P(dSn), P(dVn), P(ds0), B, T, H, DK, DV, code, split, *pk, stream)
     CALLS[f"bwd s{split}"] += 1
     if Hk == H:
         dqh, dkh = torch.empty_like(q), torch.empty_like(k)
     else:
-        dqh = torch.empty(B, T, H, DK, device=dev, dtype=dt)
+        dqh = torch.empty(Bc, T, H, DK, device=dev, dtype=dt)
         dkh = torch.empty_like(dqh)
     dv = torch.empty_like(v)
     dg, dbeta = torch.empty_like(g), torch.empty_like(beta)
     _launch("chunk_bwd", "macai_gdr_chunk_bwd", P(q), P(k), P(v), P(g), P(beta), P(do), P(r["A"]), P(Sc), P(dSn), P(Vn),
-            P(dVn), P(dqh), P(dkh), P(dv), P(dg), P(dbeta), B, T, H, Hk, DK, DV, code, int(l2norm), q_scale, stream)
+            P(dVn), P(dqh), P(dkh), P(dv), P(dg), P(dbeta), B, T, H, Hk, DK, DV, code, int(l2norm), q_scale, *pk,
+            stream)
     if Hk == H:
         return dqh, dkh, dv, dg, dbeta, ds0
     dq, dk = torch.empty_like(q), torch.empty_like(k)
-    _launch("group_sum", "macai_gdr_group_sum", P(dqh), P(dq), B, T, H, Hk, DK, code, stream)
-    _launch("group_sum", "macai_gdr_group_sum", P(dkh), P(dk), B, T, H, Hk, DK, code, stream)
+    _launch("group_sum", "macai_gdr_group_sum", P(dqh), P(dq), Bc, T, H, Hk, DK, code, stream)
+    _launch("group_sum", "macai_gdr_group_sum", P(dkh), P(dk), Bc, T, H, Hk, DK, code, stream)
     return dq, dk, dv, dg, dbeta, ds0
 
 
 class GatedDeltaRule(torch.autograd.Function):
     """o, S_T = recurrence(q, k, v, g, beta, S_0) on [B, T, H, D] tensors (q already normalised and scaled): the
-    reference's contract (op.py:116-257).  q and k may also have fewer heads Hk dividing H (grouped value heads, value
-    head h using key head h // (H // Hk)); their gradients then come back in that shape.  q, k, v float32 or bfloat16 (o in that dtype), g, beta, s0 float32.
-    backward -> (dq, dk, dv, dg, dbeta, ds0, None); None upstream gradients count as zeros (op.py:194-200)."""
+    reference's contract (op.py:116-257).  q and k may also have fewer heads Hk dividing H (grouped value heads,
+    value head h using key head h // (H // Hk)); their gradients then come back in that shape.  q, k, v float32 or
+    bfloat16 (o in that dtype), g, beta, s0 float32. backward -> (dq, dk, dv, dg, dbeta, ds0, None); None upstream
+    gradients count as zeros (op.py:194-200)."""
 
     @staticmethod
     def forward(ctx, q, k, v, g, beta, s0, save: bool):
@@ -198,15 +232,18 @@ class GatedDeltaRule(torch.autograd.Function):
 class _DropIn(torch.autograd.Function):
     """The drop-in's rule on the raw query / key: the l2norm prologue (and q's DK^-1/2 scale) is applied inside the
     kernels and its backward fused into the per-chunk backward (the reference runs it as separate L2NormScale passes,
-    _norm.py:81-114).  s0 may be None (zeros); sT is returned only when want_sT."""
+    _norm.py:81-114).  s0 may be None (zeros); sT is returned only when want_sT.  pack: the packed-row table of
+    _pack (cu_seqlens) or None."""
 
     @staticmethod
-    def forward(ctx, query, key, value, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, save: bool):
+    def forward(ctx, query, key, value, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, save: bool,
+                pack=None):
         with torch.cuda.device(query.device):
-            o, sT = _forward(query, key, value, g, beta, s0, l2norm, q_scale, want_sT)
+            o, sT = _forward(query, key, value, g, beta, s0, l2norm, q_scale, want_sT, pack)
         if save:
             ctx.save_for_backward(query, key, value, g, beta, s0)
             ctx.cfg = (l2norm, q_scale, s0 is not None)
+            ctx.pack = pack
         if sT is None:
             return o
         return o, sT
@@ -218,8 +255,8 @@ class _DropIn(torch.autograd.Function):
         do = torch.zeros_like(value) if do is None else do.to(value.dtype).contiguous()
         dsT = None if dsT is None else dsT.to(torch.float32).contiguous()
         with torch.cuda.device(query.device):
-            dq, dk, dv, dg, dbeta, ds0 = _backward(query, key, value, g, beta, s0, do, dsT, l2norm, q_scale)
-        return dq, dk, dv, dg, dbeta, (ds0 if has_s0 else None), None, None, None, None
+            dq, dk, dv, dg, dbeta, ds0 = _backward(query, key, value, g, beta, s0, do, dsT, l2norm, q_scale, ctx.pack)
+        return dq, dk, dv, dg, dbeta, (ds0 if has_s0 else None), None, None, None, None, None
 
 
 def l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
@@ -230,24 +267,26 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size: int = 64, ini
                            output_final_state: bool = False, use_qk_l2norm_in_kernel: bool = False, **kwargs):
     """Drop-in for transformers' torch_chunk_gated_delta_rule: query, key [B, T, H, DK]; value [B, T, H, DV]; g (log
     decay, <= 0) and beta [B, T, H]; initial_state [B, H, DK, DV] or None.  query and key may also come with fewer
-    heads Hk dividing H, unrepeated (value head h reads key head h // (H // Hk), as after repeat_interleave).  Returns the output [B, T, H, DV] in the
-    query's dtype and the final state (float32) when output_final_state, else None.  chunk_size is accepted and unused
-    (the kernels use 64-token chunks).  bfloat16 inputs run on bf16 MFMA with fp32 accumulation and an fp32 state;
-    float32 inputs on fp32 MFMA; float16 inputs are computed as float32."""
-    if kwargs.get("cu_seqlens") is not None:
-        # packed rows (several sequences in one row): the state must restart at each boundary; not implemented, and
-        # running without it would silently carry state across sequences (op.py:270-273)
-        raise NotImplementedError("macai's gated delta rule does not take packed rows (cu_seqlens) yet")
+    heads Hk dividing H, unrepeated (value head h reads key head h // (H // Hk), as after repeat_interleave).
+    cu_seqlens (packed rows, transformers' varlen form): B = 1 and the row holds the sequences cu[n] .. cu[n+1],
+    each run on its own from initial_state[n] (initial_state [N, H, DK, DV] or None); the final state is [N, H, DK,
+    DV]. The reference refuses cu_seqlens (op.py:270-273); here each sequence is chunked separately inside the
+    kernels. Returns the output [B, T, H, DV] in the query's dtype and the final state (float32) when
+    output_final_state, else None.  chunk_size is accepted and unused (the kernels use 64-token chunks).  bfloat16
+    inputs run on bf16 MFMA with fp32 accumulation and an fp32 state; float32 inputs on fp32 MFMA; float16 inputs
+    are computed as float32."""
+    cu = kwargs.get("cu_seqlens")
+    pack = None if cu is None else _pack(cu, query.shape[1], query.device)
     dtype = query.dtype
     cdt = torch.bfloat16 if dtype == torch.bfloat16 else torch.float32
     q, k, v = (x.to(cdt).contiguous() for x in (query, key, value))
     gf, bf = g.to(torch.float32).contiguous(), beta.to(torch.float32).contiguous()
     s0 = None if initial_state is None else initial_state.to(torch.float32).contiguous()
-    _check(q, k, v, gf, bf, s0)
+    _check(q, k, v, gf, bf, s0, None if pack is None else pack[2])
     tensors = (q, k, v, gf, bf) + (() if s0 is None else (s0,))
     save = torch.is_grad_enabled() and any(t.requires_grad for t in tensors)
     res = _DropIn.apply(q, k, v, gf, bf, s0, bool(use_qk_l2norm_in_kernel), q.shape[-1] ** -0.5,
-                        bool(output_final_state), save)
+                        bool(output_final_state), save, pack)
     out, sT = (res, None) if not output_final_state else res
     return out.to(dtype), sT
 
@@ -261,10 +300,11 @@ def recurrent_gated_delta_rule(query, key, value, g, beta, initial_state=None, o
     T = query.shape[1]
     needs_grad = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (query, key, value, g, beta, initial_state))
-    if T != 1 or needs_grad:
+    if T != 1 or needs_grad or kwargs.get("cu_seqlens") is not None:
         return chunk_gated_delta_rule(query, key, value, g, beta, initial_state=initial_state,
                                       output_final_state=output_final_state,
-                                      use_qk_l2norm_in_kernel=use_qk_l2norm_in_kernel)
+                                      use_qk_l2norm_in_kernel=use_qk_l2norm_in_kernel,
+                                      cu_seqlens=kwargs.get("cu_seqlens"))
     dtype = query.dtype
     cdt = torch.bfloat16 if dtype == torch.bfloat16 else torch.float32
     q, k, v = (x.to(cdt).contiguous() for x in (query, key, value))

@@ -41,7 +41,7 @@ def test_library_exports_every_declared_symbol():
 def _prep(**over):
     p = 1 << 20
     a = dict(q=p, k=p, v=p, g=p, beta=p, W=p, U=p, Ke=p, GL=p, Qg=p, M=p, A=None, B=1, T=64, H=1, Hk=1, DK=128,
-             DV=128, dtype=1, l2=1, scale=1.0, stream=None)
+             DV=128, dtype=1, l2=1, scale=1.0, pack=None, NT=0, stream=None)
     a.update(over)
     return N.lib().macai_gdr_prep(*a.values())
 
@@ -62,17 +62,19 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert _prep(H=4, Hk=3) == N.EINVAL and b"key heads must divide" in L.macai_gdr_last_error()
     assert _prep(H=4, Hk=0) == N.EINVAL
     p = 1 << 20
-    sf = lambda *ptrs, flags=0, split=0, DV=128: L.macai_gdr_state_fwd(*ptrs, 1, 64, 1, 128, DV, 1, flags, split, None)
+    sf = lambda *ptrs, flags=0, split=0, DV=128: L.macai_gdr_state_fwd(*ptrs, 1, 64, 1, 128, DV, 1, flags, split,
+                                                                       None, 0, None)
     # flags that ask for nothing or both, a split that does not divide DV / 16, a missing output operand
     assert sf(p, p, p, p, p, p, None, p, None, None, None, flags=8) == N.EINVAL
     assert sf(p, p, p, p, p, p, None, p, None, p, p, flags=1) == N.EINVAL and b"flags" in L.macai_gdr_last_error()
     assert sf(p, p, p, p, p, p, None, p, None, None, None, split=3) == N.EINVAL and b"split" in L.macai_gdr_last_error()
     assert sf(p, p, p, p, p, p, None, p, None, None, None, split=1, DV=96) == N.EINVAL
     assert sf(p, p, p, p, p, None, None, p, None, None, None) == N.EINVAL
-    assert L.macai_gdr_state_bwd(p, p, p, p, p, None, None, p, p, p, 1, 64, 1, 128, 128, 1, 0, None) == N.EINVAL
-    assert L.macai_gdr_chunk_bwd(*([p] * 15), None, 1, 64, 1, 1, 128, 128, 1, 1, 1.0, None) == N.EINVAL
-    assert L.macai_gdr_chunk_bwd(*([p] * 16), 1, 64, 6, 4, 128, 128, 1, 1, 1.0, None) == N.EINVAL
-    pair = lambda *ptrs, split=0: L.macai_gdr_state_pair(*ptrs, 1, 64, 1, 128, 128, 1, split, None)
+    assert L.macai_gdr_state_bwd(p, p, p, p, p, None, None, p, p, p, 1, 64, 1, 128, 128, 1, 0, None, 0,
+                                 None) == N.EINVAL
+    assert L.macai_gdr_chunk_bwd(*([p] * 15), None, 1, 64, 1, 1, 128, 128, 1, 1, 1.0, None, 0, None) == N.EINVAL
+    assert L.macai_gdr_chunk_bwd(*([p] * 16), 1, 64, 6, 4, 128, 128, 1, 1, 1.0, None, 0, None) == N.EINVAL
+    pair = lambda *ptrs, split=0: L.macai_gdr_state_pair(*ptrs, 1, 64, 1, 128, 128, 1, split, None, 0, None)
     assert pair(*([p] * 6), None, p, None, p, p, p, p, None) == N.EINVAL and b"null" in L.macai_gdr_last_error()
     assert pair(*([p] * 6), None, p, None, *([p] * 5), split=3) == N.EINVAL
     assert L.macai_gdr_decode(p, p, p, p, p, p, p, p, 1, 1, 1, 256, 128, 1, 1, 1.0, None) == N.EUNSUP
@@ -86,16 +88,37 @@ def test_abi_rejects_bad_arguments_before_launch():
 
 def test_call_maps_codes_to_exceptions():
     with pytest.raises(NotImplementedError, match="key head width"):
-        N.call("macai_gdr_prep", *([1 << 20] * 11), None, 1, 64, 1, 1, 96, 128, 1, 1, 1.0, None)
+        N.call("macai_gdr_prep", *([1 << 20] * 11), None, 1, 64, 1, 1, 96, 128, 1, 1, 1.0, None, 0, None)
     with pytest.raises(ValueError, match="null"):
-        N.call("macai_gdr_prep", *([None] * 12), 1, 64, 1, 1, 128, 128, 1, 1, 1.0, None)
+        N.call("macai_gdr_prep", *([None] * 12), 1, 64, 1, 1, 128, 128, 1, 1, 1.0, None, 0, None)
 
 
-def test_packed_rows_refused():
-    """cu_seqlens is refused before anything else (reference op.py:270-273; tests/test_harness.py:169-173)."""
+def test_packed_row_table():
+    """cu_seqlens -> the packed-row table of include/macai_gdr.h: each sequence chunked on its own (a 64-token chunk
+    never crosses a boundary), empty sequences own no chunk, the last entry is the chunk count."""
+    table, NT, N_ = op._pack(torch.tensor([0, 130, 130, 194, 200]), 200, "cpu")
+    assert (NT, N_) == (5, 4)
+    t0, end, c0 = table[:NT].tolist(), table[NT:2 * NT].tolist(), table[2 * NT:].tolist()
+    assert t0 == [0, 64, 128, 130, 194] and end == [130, 130, 130, 194, 200] and c0 == [0, 3, 3, 4, 5]
+    assert table.dtype == torch.int32
+
+
+def test_packed_rows_validated():
+    """cu_seqlens must rise from 0 to T; checked before any device work (the reference refused it altogether,
+    op.py:270-273)."""
     x = torch.zeros(1, 4, 1, 128)
-    with pytest.raises(NotImplementedError):
-        chunk_gated_delta_rule(x, x, x, x[..., 0], x[..., 0], cu_seqlens=torch.tensor([0, 2, 4]))
+    for bad in ([0, 2, 3], [1, 4], [0, 3, 2, 4], [0]):
+        with pytest.raises(ValueError, match="cu_seqlens"):
+            chunk_gated_delta_rule(x, x, x, x[..., 0], x[..., 0], cu_seqlens=torch.tensor(bad))
+
+
+def test_packed_row_arguments_checked_by_the_abi():
+    L = N.lib()
+    p = 1 << 20
+    # the chunk count must lie in [1, T]; the table must be 4-byte aligned
+    assert _prep(pack=p, NT=0) == N.EINVAL and b"packed rows" in L.macai_gdr_last_error()
+    assert _prep(pack=p, NT=65) == N.EINVAL
+    assert _prep(pack=p + 2, NT=1) == N.EINVAL and b"aligned" in L.macai_gdr_last_error()
 
 
 def test_cpu_tensors_refused_loudly():
