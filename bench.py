@@ -64,13 +64,14 @@ def make_inputs(cfg, seed, dev):
     return out, c
 
 
-def kernel_costs(B, T, H, DK, DV, es=2, Hk=None):
+def kernel_costs(B, T, H, DK, DV, es=2, Hk=None, chunks=None):
     """Algorithmic bytes (each declared input read once, each output written once, from argument sizes) and dense
     FLOPs (2 per multiply-add, triangular products counted dense) per launch of each kernel of the training step.
-    Hk: key heads of q and k when they come unrepeated (grouped value heads); H by default."""
+    Hk: key heads of q and k when they come unrepeated (grouped value heads); H by default.  chunks: chunks per head
+    over the batch (B ceil(T / 64) by default; packed rows chunk each sequence on its own)."""
     Hk = Hk or H
-    NT = math.ceil(T / C)
-    n = B * H * NT                       # chunk-heads
+    chunks = chunks or B * math.ceil(T / C)
+    n = H * chunks                       # chunk-heads
     tok = B * T * H
     io_k, io_v = tok * DK * es, tok * DV * es
     io_kk = B * T * Hk * DK * es         # one of q, k as the kernels read them
@@ -201,6 +202,9 @@ def main():
                     help="configs with Hk < Hv: q and k go to the rule unrepeated (grouped value heads); without "
                          "it the "
                          "step repeats them first, as the model does (repeat_interleave inside the timed step)")
+    ap.add_argument("--packed", choices=["uniform", "ragged"],
+                    help="run the batch as one packed row (cu_seqlens): B sequences of T tokens, or seeded ragged "
+                         "lengths with the same total")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run one plain device copy of this many MiB (calibrates rocprof byte counters)")
     args = ap.parse_args()
@@ -216,6 +220,21 @@ def main():
     # q, k leaves at the model's key heads (make_inputs draws them per key head and repeats)
     kq = {n: inp[n][:, :, ::rep].contiguous() for n in ("query", "key")}
     leaves = [kq["query"], kq["key"]] + [inp[n] for n in ("value", "g", "beta")]
+    kw = {}
+    if args.packed:                           # the B rows as one row of B * T tokens
+        Bp, Tp = c["B"], c["T"]
+        leaves = [x.reshape(1, Bp * Tp, *x.shape[2:]) for x in leaves]
+        inp["do"] = inp["do"].reshape(1, Bp * Tp, *inp["do"].shape[2:])
+        if args.packed == "uniform":
+            lens = [Tp] * Bp
+        else:                                 # 4 B seeded lengths summing to B * T
+            gen = torch.Generator().manual_seed(7)
+            w = torch.rand(4 * Bp, generator=gen) + 0.01
+            lens = (w / w.sum() * Bp * Tp).long().clamp_min(1).tolist()
+            lens[-1] += Bp * Tp - sum(lens)
+        kw["cu_seqlens"] = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32, device=dev)
+        if inp["initial_state"] is not None:
+            inp["initial_state"] = None       # one state per sequence would be needed; the packed runs start at zero
     leaves = [x.requires_grad_(True) for x in leaves]
     s0 = inp["initial_state"]
     if s0 is not None:
@@ -228,7 +247,7 @@ def main():
         if rep > 1 and not args.grouped:          # the model's layout: repeat over each group first
             q, k = q.repeat_interleave(rep, 2), k.repeat_interleave(rep, 2)
         o, _ = chunk_gated_delta_rule(q, k, *leaves[2:5], initial_state=s0, output_final_state=False,
-                                      use_qk_l2norm_in_kernel=True)
+                                      use_qk_l2norm_in_kernel=True, **kw)
         return torch.autograd.grad(o, leaves, do)
 
     from macai.gated_delta import op
@@ -260,14 +279,23 @@ def main():
     tokens = B * T
     ms = elapsed / args.steps * 1e3
 
-    alone, split = time_kernels(inp)
+    # each pass alone at the batched layout; packed rows (whose per-sequence chunking those launches do not follow)
+    # report the in-step times only
+    rows = B * H if not args.packed else (len(kw["cu_seqlens"]) - 1) * H
+    alone, split = time_kernels(inp) if not args.packed else ({}, op.split_for(rows, T, DV))
     ktime = dict(in_step)                # the passes as the step runs them
     if args.copy_mib:
         src = torch.ones(args.copy_mib << 18, device=dev)
         dst = torch.empty_like(src)
         dst.copy_(src)
         torch.cuda.synchronize()
-    cost = kernel_costs(B, T, H, DK, DV, Hk=c["Hk"] if args.grouped else None)
+    chunks = None
+    if args.packed:
+        cu = kw["cu_seqlens"].tolist()
+        chunks = sum(math.ceil((b - a) / C) for a, b in zip(cu, cu[1:]))
+    cost = kernel_costs(B, T, H, DK, DV, Hk=c["Hk"] if args.grouped else None, chunks=chunks)
+    # rocprof traffic was measured on the batched layout
+    traffic = {} if args.packed else TRAFFIC.get(args.config, {})
     kernels = {}
     for name, t in ktime.items():
         bw = cost[name]["bytes"] / t
@@ -275,12 +303,12 @@ def main():
         kernels[name] = {"us": round(t * 1e6, 2), "us_alone": round(alone[name] * 1e6, 2) if name in alone else None,
                          "GB/s": round(bw / 1e9, 1), "hbm_frac": round(bw / HBM_PEAK, 4),
                          "TFLOP/s": round(fl / 1e12, 2), "mfma_frac": round(fl / MFMA_PEAK["bf16"], 4),
-                         "traffic": TRAFFIC.get(args.config, {}).get(name)}
+                         "traffic": traffic.get(name)}
     dom = max(ktime, key=ktime.get)
     bw = cost[dom]["bytes"] / ktime[dom]
     roof = {"kernel": dom, "timing": "in-step HIP events", "bound": "hbm", "achieved": round(bw / 1e9, 1),
             "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-            "frac": round(bw / HBM_PEAK, 4), "traffic": TRAFFIC.get(args.config, {}).get(dom)}
+            "frac": round(bw / HBM_PEAK, 4), "traffic": traffic.get(dom)}
     line = {"metric": METRIC, "value": round(tokens / (elapsed / args.steps), 1), "unit": "tokens/s", "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
             "scaling": "weak", "vs_baseline": round(tokens / (elapsed / args.steps) / PUBLISHED, 2)
@@ -289,7 +317,10 @@ def main():
             "config": {"workload": f"gated-delta drop-in fwd+bwd, BASELINE config {args.config}", "B": B, "T": T,
                        "Hk": c["Hk"], "Hv": H, "DK": DK, "DV": DV, "chunk": C, "l2norm_in_kernel": True,
                        "qk_heads_to_the_rule": c["Hk"] if args.grouped else H,
-                       "initial_state": c["s0"], "value_split": split, "overlap_split": op.split_for(B * H, T, DV, 2),
+                       "packed_rows": None if not args.packed else {"mode": args.packed,
+                                                                     "sequences": len(kw["cu_seqlens"]) - 1,
+                                                                     "chunks_per_head": chunks},
+                       "initial_state": c["s0"], "value_split": split, "overlap_split": op.split_for(rows, T, DV, 2),
                        "overlapped_state_passes": op.OVERLAP},
             "roofline": roof, "kernels": kernels}
     if not args.no_cpu:

@@ -9,6 +9,7 @@ the per-chunk matrices and chunk states (the reference's RECOMPUTE_STATES defaul
 """
 import collections
 import math
+import weakref
 
 import torch
 
@@ -51,9 +52,12 @@ def valid_splits(dv: int) -> list:
 def split_for(rows: int, T: int, dv: int, share: int = 1) -> int:
     """VALUE_SPLIT's choice for `rows` head-rows (B x H) of value width dv, for a pass that gets 1 / share of the
     chip: "auto" takes the smallest valid split that gives at least 256 / share workgroups (one per CU), else the
-    largest; an int setting is rounded down to a valid split."""
+    largest; an int setting is rounded down to a valid split.  "auto" leaves out the splits with 8 waves of columns
+    per workgroup where another exists: with the loader wave that is 9 waves, 3 on one SIMD, which caps a wave at 168
+    VGPRs: the 128-wide state kernels spill there (the backward's pair pass ran 2.1-2.8x slower than at 4 waves)."""
     valid = valid_splits(dv)
     if VALUE_SPLIT == "auto":
+        valid = [s for s in valid if (dv // 16) // s <= 4] or valid
         for s in valid:
             if rows * s * share >= 256:
                 return s
@@ -99,9 +103,19 @@ def _dims(q, v, pack=None):
     return B, T, v.shape[2], Hk, DK, v.shape[-1], math.ceil(T / CHUNK)
 
 
+# packed-row tables by cu_seqlens tensor: a model passes the same one to every layer, and building the table reads it
+# back to the host (a synchronisation), so it is built once per tensor (and per in-place change of it)
+_PACKS = {}   # id(tensor) -> (weak reference, (version, T, device), table); an entry goes when its tensor does
+
+
 def _pack(cu_seqlens, T: int, device):
     """The packed-row table of include/macai_gdr.h for sequences cu[n] .. cu[n+1] of one row of T tokens: each
     sequence chunked on its own.  Returns (table [2 NT + N + 1] int32 on `device`, NT, N)."""
+    key = cu_seqlens if isinstance(cu_seqlens, torch.Tensor) else None
+    if key is not None:
+        hit = _PACKS.get(id(key))
+        if hit is not None and hit[0]() is key and hit[1] == (key._version, T, str(device)):
+            return hit[2]
     cu = torch.as_tensor(cu_seqlens).reshape(-1).to("cpu", torch.int64).tolist()
     if len(cu) < 2 or cu[0] != 0 or cu[-1] != T or any(b < a for a, b in zip(cu, cu[1:])):
         raise ValueError(f"cu_seqlens must rise from 0 to T = {T} (got {cu[:8]}{'...' if len(cu) > 8 else ''})")
@@ -112,7 +126,12 @@ def _pack(cu_seqlens, T: int, device):
             ends.append(b)
         c0.append(len(t0s))
     table = torch.tensor(t0s + ends + c0, dtype=torch.int32, device=device)
-    return table, len(t0s), len(cu) - 1
+    out = (table, len(t0s), len(cu) - 1)
+    if key is not None:
+        if id(key) not in _PACKS:
+            weakref.finalize(key, _PACKS.pop, id(key), None)
+        _PACKS[id(key)] = (weakref.ref(key), (key._version, T, str(device)), out)
+    return out
 
 
 def _pack_args(pack):

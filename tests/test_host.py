@@ -129,14 +129,16 @@ def test_cpu_tensors_refused_loudly():
 
 
 def test_split_rule():
-    """VALUE_SPLIT 'auto': the smallest valid split (1, 2, 4 or 8 waves of 16 columns per workgroup) giving >= 256
-    workgroups, else the largest; an int setting rounds down to a valid split (reference op.split_for semantics,
-    test_chunking.py:176-199)."""
+    """VALUE_SPLIT 'auto': the smallest valid split (1, 2, 4 or 8 waves of 16 columns per workgroup; 8 only when
+    nothing else is valid) giving >= 256 workgroups, else the largest; an int setting rounds down to a valid split
+    (reference op.split_for semantics, test_chunking.py:176-199)."""
     assert op.valid_splits(128) == [1, 2, 4, 8] and op.valid_splits(96) == [3, 6] and op.valid_splits(32) == [1, 2]
     assert op.split_for(64, 1024, 128) == 4
     assert op.split_for(16, 32768, 128) == 8
-    assert op.split_for(512, 1024, 128) == 1
-    assert op.split_for(2048, 1, 128) == 1
+    assert op.split_for(512, 1024, 128) == 2        # never 8 waves of columns when "auto" has another choice
+    assert op.split_for(2048, 1, 128) == 2
+    assert op.split_for(256, 1024, 128, 2) == 2
+    assert op.split_for(4096, 1, 64) == 1           # 4 waves
     assert op.split_for(1, 64, 32) == 2
     assert op.split_for(2, 130, 96) == 6
     assert op.split_for(64, 1024, 128, 2) == 2      # a pass on half the chip (the backward's overlapped passes)
