@@ -1,10 +1,13 @@
 """Benchmark of the MI355X gated delta rule: the drop-in's forward + backward at BASELINE config 1.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--config 1|2]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--config 1|2] [--grouped]
+                    [--packed uniform|ragged] [--recompute]
 
 A step = one call of macai.gated_delta.chunk_gated_delta_rule (use_qk_l2norm_in_kernel=True, bf16 q/k/v, fp32 g and
 beta) followed by its backward for a seeded upstream gradient dO (torch.autograd.grad, so no gradient accumulation),
-on synthetic inputs already resident in HBM.  Prints ONE JSON line (rank 0).  Beside the step time it times every
+on synthetic inputs already resident in HBM.  The forward keeps prep's per-chunk operands for the backward
+(op.RECOMPUTE_STATES = False, the library's default); --recompute measures the reference's default instead, where the
+backward reruns prep.  Prints ONE JSON line (rank 0).  Beside the step time it times every
 pass inside steps identical to the timed ones with HIP events on the launch stream (macai.gated_delta.op.EVENTS; the
 roofline of the dominant kernel) and, for comparison, each pass alone (back-to-back repeats, whose inputs stay in the
 Infinity Cache), and the
@@ -64,11 +67,12 @@ def make_inputs(cfg, seed, dev):
     return out, c
 
 
-def kernel_costs(B, T, H, DK, DV, es=2, Hk=None, chunks=None):
+def kernel_costs(B, T, H, DK, DV, es=2, Hk=None, chunks=None, keep=False):
     """Algorithmic bytes (each declared input read once, each output written once, from argument sizes) and dense
     FLOPs (2 per multiply-add, triangular products counted dense) per launch of each kernel of the training step.
     Hk: key heads of q and k when they come unrepeated (grouped value heads); H by default.  chunks: chunks per head
-    over the batch (B ceil(T / 64) by default; packed rows chunk each sequence on its own)."""
+    over the batch (B ceil(T / 64) by default; packed rows chunk each sequence on its own).  keep: the forward's prep
+    also writes A (the training forward keeps prep's operands; there is no prep_bwd launch)."""
     Hk = Hk or H
     chunks = chunks or B * math.ceil(T / C)
     n = H * chunks                       # chunk-heads
@@ -82,7 +86,7 @@ def kernel_costs(B, T, H, DK, DV, es=2, Hk=None, chunks=None):
     pre = 3 * cdk * es + cdv * 4 + cc * es + 4      # prep's row-major outputs W, Ke, Qg, U, M, GL
     inp = 2 * io_kk + io_v + gb                       # q, k, v, g, beta
     # the forward: prep, then the state pass reads W, U, Ke, GL, Qg, M and writes o
-    cost["prep_fwd"] = dict(bytes=inp + n * pre,
+    cost["prep_fwd"] = dict(bytes=inp + n * (pre + (cc * es if keep else 0)),
                             flops=n * (2 * 2 * cc * DK + cc * C / 3 + 2 * cc * DK + 2 * cc * DV))
     cost["state_fwd_out"] = dict(bytes=n * pre + io_v, flops=n * (3 * 2 * C * DK * DV + 2 * cc * DV))
     # the backward: prep also writes A; the recompute pass reads W, U, Ke, GL and writes S_c (fp32) and Vn; the reverse
@@ -105,8 +109,9 @@ def kernel_costs(B, T, H, DK, DV, es=2, Hk=None, chunks=None):
     return cost
 
 
-def time_kernels(inp, reps=20):
-    """Each pass of the step alone: HIP events on the current (launch) stream around `reps` back-to-back launches."""
+def time_kernels(inp, reps=20, keep=False):
+    """Each pass of the step alone: HIP events on the current (launch) stream around `reps` back-to-back launches.
+    keep: the forward's prep writes A too (the training forward keeps prep's operands for the backward)."""
     from macai.gated_delta import _native as N
     from macai.gated_delta import op
     q, k, v, g, beta, do = (inp[n] for n in ("query", "key", "value", "g", "beta", "do"))
@@ -130,8 +135,8 @@ def time_kernels(inp, reps=20):
     dq, dk, dv, dg, db = (torch.empty_like(x) for x in (q, k, v, g, beta))
     P = N.ptr
     calls = {
-        "prep_fwd": ("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), P(Ke), P(GL), P(Qg), P(M), None,
-                     B, T, H, H, DK, DV, code, 1, sc, None, 0, st),
+        "prep_fwd": ("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), P(Ke), P(GL), P(Qg), P(M),
+                     P(A) if keep else None, B, T, H, H, DK, DV, code, 1, sc, None, 0, st),
         "state_fwd_out": ("macai_gdr_state_fwd", P(W), P(U), P(Ke), P(GL), P(Qg), P(M), P(s0), P(o), None, None,
                           None, B, T, H, DK, DV, code, 0, split, None, 0, st),
         "prep_bwd": ("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), P(Ke), P(GL), P(Qg), P(M), P(A),
@@ -198,6 +203,9 @@ def main():
     ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--recompute", action="store_true",
+                    help="the training forward keeps only its inputs and the backward reruns prep (op.RECOMPUTE_STATES "
+                         "= True, the reference's default); without it the forward keeps prep's operands")
     ap.add_argument("--grouped", action="store_true",
                     help="configs with Hk < Hv: q and k go to the rule unrepeated (grouped value heads); without "
                          "it the "
@@ -251,6 +259,9 @@ def main():
         return torch.autograd.grad(o, leaves, do)
 
     from macai.gated_delta import op
+    if args.recompute:
+        op.RECOMPUTE_STATES = True
+    keep = not op.RECOMPUTE_STATES
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -282,7 +293,7 @@ def main():
     # each pass alone at the batched layout; packed rows (whose per-sequence chunking those launches do not follow)
     # report the in-step times only
     rows = B * H if not args.packed else (len(kw["cu_seqlens"]) - 1) * H
-    alone, split = time_kernels(inp) if not args.packed else ({}, op.split_for(rows, T, DV))
+    alone, split = time_kernels(inp, keep=keep) if not args.packed else ({}, op.split_for(rows, T, DV))
     ktime = dict(in_step)                # the passes as the step runs them
     if args.copy_mib:
         src = torch.ones(args.copy_mib << 18, device=dev)
@@ -293,7 +304,7 @@ def main():
     if args.packed:
         cu = kw["cu_seqlens"].tolist()
         chunks = sum(math.ceil((b - a) / C) for a, b in zip(cu, cu[1:]))
-    cost = kernel_costs(B, T, H, DK, DV, Hk=c["Hk"] if args.grouped else None, chunks=chunks)
+    cost = kernel_costs(B, T, H, DK, DV, Hk=c["Hk"] if args.grouped else None, chunks=chunks, keep=keep)
     # rocprof traffic was measured on the batched layout
     traffic = {} if args.packed else TRAFFIC.get(args.config, {})
     kernels = {}
@@ -321,7 +332,7 @@ def main():
                                                                      "sequences": len(kw["cu_seqlens"]) - 1,
                                                                      "chunks_per_head": chunks},
                        "initial_state": c["s0"], "value_split": split, "overlap_split": op.split_for(rows, T, DV, 2),
-                       "overlapped_state_passes": op.OVERLAP},
+                       "overlapped_state_passes": op.OVERLAP, "recompute_prep_in_backward": not keep},
             "roofline": roof, "kernels": kernels}
     if not args.no_cpu:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)

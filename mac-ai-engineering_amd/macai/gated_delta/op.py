@@ -4,8 +4,8 @@ torch_chunk_gated_delta_rule (same arguments, same returns).
 Mirrors the reference's src/macai/gated_delta/op.py: `GatedDeltaRule` keeps its autograd contract (op.py:116-257),
 `chunk_gated_delta_rule` its drop-in signature and behaviour (op.py:264-298), `l2norm` and `recurrent_reference` its
 helpers (op.py:260-261, 301-314).  The per-call passes (op.py:63-113, 159, 217, 234, 241-242) become the C-ABI calls of
-include/macai_gdr.h on the current HIP stream.  The training forward keeps only its inputs and the backward recomputes
-the per-chunk matrices and chunk states (the reference's RECOMPUTE_STATES default, op.py:27-33).
+include/macai_gdr.h on the current HIP stream.  What the training forward keeps for the backward follows
+RECOMPUTE_STATES (the reference's switch, op.py:27-33).
 """
 import collections
 import math
@@ -28,6 +28,14 @@ EVENTS = None
 # OVERLAP they run in one launch (macai_gdr_state_pair), each on about half the CUs.  Both are sequential chunk chains
 # whose speed hardly depends on how many CUs they get, so this nearly hides one of them.
 OVERLAP = True
+# RECOMPUTE_STATES (the reference's switch, op.py:27-33; outputs and gradients have the same bits either way):
+# False (the default here) -- the training forward runs prep in its backward mode (A as well) and keeps its per-chunk
+# operands W, U, Ke, Qg, M, GL, A for the backward, which then skips its prep launch.  At D = 128 in bf16 they hold
+# about 10x the bytes of q (96 MiB a layer at B = 4, T = 1024, H = 16): room a 288 GB part has.  True -- the forward
+# keeps only its inputs and the backward recomputes prep (the reference's default, chosen there for the Metal
+# allocator's footprint).  The chunk states are recomputed either way: that pass runs in the same launch as the
+# reverse pass (OVERLAP), where it costs little.
+RECOMPUTE_STATES = False
 
 
 def _launch(name: str, entry: str, *args):
@@ -138,9 +146,10 @@ def _pack_args(pack):
     return (None, 0) if pack is None else (N.ptr(pack[0]), pack[1])
 
 
-def _prep(q, k, v, g, beta, l2norm: bool, q_scale: float, with_A: bool, pack=None):
+def _prep(q, k, v, g, beta, l2norm: bool, q_scale: float, with_A: bool, pack=None, name=None):
     """The per-chunk operands (row-major, tokens as rows): W, U, diag(e) K^, exp(G_last), diag(gamma) Q^, M, and A when
-    asked (the backward's per-chunk pass).  Per-chunk tensors are [B, H, NT, ...] ([1, H, NT, ...] for packed rows)."""
+    asked (the backward's per-chunk pass).  Per-chunk tensors are [B, H, NT, ...] ([1, H, NT, ...] for packed rows).
+    name: the launch's name for EVENTS (by default prep_bwd with A, else prep_fwd)."""
     B, T, H, Hk, DK, DV, NT = _dims(q, v, pack)
     Bc = q.shape[0]
     dev, dt = q.device, q.dtype
@@ -151,18 +160,19 @@ def _prep(q, k, v, g, beta, l2norm: bool, q_scale: float, with_A: bool, pack=Non
              M=torch.empty(Bc, H, NT, CHUNK, CHUNK, device=dev, dtype=dt),
              A=torch.empty(Bc, H, NT, CHUNK, CHUNK, device=dev, dtype=dt) if with_A else None)
     P = N.ptr
-    _launch("prep_bwd" if with_A else "prep_fwd", "macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(r["W"]),
+    _launch(name or ("prep_bwd" if with_A else "prep_fwd"), "macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(r["W"]),
             P(r["U"]), P(r["Ke"]), P(r["GL"]), P(r["Qg"]), P(r["M"]), P(r["A"]), B, T, H, Hk, DK, DV,
             N.dtype_code(dt), int(l2norm), q_scale, *_pack_args(pack), N.stream_of(q))
     return r
 
 
-def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, pack=None):
-    """prep, then the state pass with the output: returns (o in q's dtype, sT or None)."""
+def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, pack=None, keep=False):
+    """prep, then the state pass with the output: returns (o in q's dtype, sT or None, prep's operands with A when
+    keep -- for the backward -- else None)."""
     B, T, H, Hk, DK, DV, NT = _dims(q, v, pack)
     dev, dt = q.device, q.dtype
     code, stream = N.dtype_code(dt), N.stream_of(q)
-    r = _prep(q, k, v, g, beta, l2norm, q_scale, False, pack)
+    r = _prep(q, k, v, g, beta, l2norm, q_scale, keep, pack, "prep_fwd")
     o = torch.empty(q.shape[0], T, H, DV, device=dev, dtype=dt)
     sT = torch.empty(B, H, DK, DV, device=dev, dtype=torch.float32) if want_sT else None
     split = split_for(B * H, T, DV)
@@ -170,12 +180,12 @@ def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, 
     _launch("state_fwd_out", "macai_gdr_state_fwd", P(r["W"]), P(r["U"]), P(r["Ke"]), P(r["GL"]), P(r["Qg"]), P(r["M"]),
             P(s0), P(o), P(sT), None, None, B, T, H, DK, DV, code, 0, split, *_pack_args(pack), stream)
     CALLS[f"fwd s{split}"] += 1
-    return o, sT
+    return o, sT, (r if keep else None)
 
 
-def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=None):
-    """Recompute (prep; the state pass storing S_c and Vn), the reverse state pass, the per-chunk backward.  Returns
-    (dq, dk, dv in q's dtype; dg, dbeta, ds0 float32).  With grouped heads (Hk < H) the per-chunk backward writes dq,
+def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=None, r=None):
+    """Recompute (prep unless the forward kept its operands `r`; the state pass storing S_c and Vn), the reverse state
+    pass, the per-chunk backward.  Returns (dq, dk, dv in q's dtype; dg, dbeta, ds0 float32).  With grouped heads (Hk < H) the per-chunk backward writes dq,
     dk per value head and macai_gdr_group_sum folds each group (the backward of the repeat the grouped layout
     replaces)."""
     B, T, H, Hk, DK, DV, NT = _dims(q, v, pack)
@@ -183,7 +193,8 @@ def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=
     dev, dt = q.device, q.dtype
     code, stream = N.dtype_code(dt), N.stream_of(q)
     f32 = torch.float32
-    r = _prep(q, k, v, g, beta, l2norm, q_scale, True, pack)
+    if r is None:
+        r = _prep(q, k, v, g, beta, l2norm, q_scale, True, pack)
     P = N.ptr
     pk = _pack_args(pack)
     split = split_for(B * H, T, DV, 2 if OVERLAP else 1)
@@ -232,8 +243,9 @@ class GatedDeltaRule(torch.autograd.Function):
     def forward(ctx, q, k, v, g, beta, s0, save: bool):
         _check(q, k, v, g, beta, s0)
         q, k, v, g, beta, s0 = (t.contiguous() for t in (q, k, v, g, beta, s0))
+        keep = save and not RECOMPUTE_STATES
         with torch.cuda.device(q.device):
-            o, sT = _forward(q, k, v, g, beta, s0, False, 1.0, True)
+            o, sT, ctx.prep = _forward(q, k, v, g, beta, s0, False, 1.0, True, keep=keep)
         if save:
             ctx.save_for_backward(q, k, v, g, beta, s0)
         return o, sT
@@ -244,7 +256,7 @@ class GatedDeltaRule(torch.autograd.Function):
         do = torch.zeros_like(v) if do is None else do.to(v.dtype).contiguous()
         dsT = None if dsT is None else dsT.to(torch.float32).contiguous()
         with torch.cuda.device(q.device):
-            dq, dk, dv, dg, dbeta, ds0 = _backward(q, k, v, g, beta, s0, do, dsT, False, 1.0)
+            dq, dk, dv, dg, dbeta, ds0 = _backward(q, k, v, g, beta, s0, do, dsT, False, 1.0, r=ctx.prep)
         return dq, dk, dv, dg, dbeta, ds0, None
 
 
@@ -257,8 +269,9 @@ class _DropIn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, query, key, value, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, save: bool,
                 pack=None):
+        keep = save and not RECOMPUTE_STATES
         with torch.cuda.device(query.device):
-            o, sT = _forward(query, key, value, g, beta, s0, l2norm, q_scale, want_sT, pack)
+            o, sT, ctx.prep = _forward(query, key, value, g, beta, s0, l2norm, q_scale, want_sT, pack, keep)
         if save:
             ctx.save_for_backward(query, key, value, g, beta, s0)
             ctx.cfg = (l2norm, q_scale, s0 is not None)
@@ -274,7 +287,8 @@ class _DropIn(torch.autograd.Function):
         do = torch.zeros_like(value) if do is None else do.to(value.dtype).contiguous()
         dsT = None if dsT is None else dsT.to(torch.float32).contiguous()
         with torch.cuda.device(query.device):
-            dq, dk, dv, dg, dbeta, ds0 = _backward(query, key, value, g, beta, s0, do, dsT, l2norm, q_scale, ctx.pack)
+            dq, dk, dv, dg, dbeta, ds0 = _backward(query, key, value, g, beta, s0, do, dsT, l2norm, q_scale, ctx.pack,
+                                                   ctx.prep)
         return dq, dk, dv, dg, dbeta, (ds0 if has_s0 else None), None, None, None, None, None
 
 

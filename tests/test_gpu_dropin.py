@@ -285,3 +285,22 @@ def test_overlapped_passes_change_no_bits():
     finally:
         op.OVERLAP = old
     assert all(torch.equal(a, b) for r in runs for a, b in zip(ref, r))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_kept_prep_operands_change_no_bits(dtype):
+    """The training forward keeping prep's operands (with A) for the backward (op.RECOMPUTE_STATES = False) or the
+    backward recomputing them (True, the reference's default, op.py:27-33): the same output and gradient bits
+    (the reference's claim for its switch, tests/test_memory.py)."""
+    _say("case recompute bits", dtype)
+    inp = gdr.make_inputs(2, 150, 2, 4, 128, 128, dtype, s0=True, seed=9)
+    old = op.RECOMPUTE_STATES
+    try:
+        outs = []
+        for mode in (True, False):
+            op.RECOMPUTE_STATES = mode
+            o, sT, grads = run_dropin(inp, dsT=torch.ones(2, 4, 128, 128))
+            outs.append([o, sT] + [grads[n] for n in sorted(grads)])
+    finally:
+        op.RECOMPUTE_STATES = old
+    assert all(torch.equal(a, b) for a, b in zip(*outs))
