@@ -31,11 +31,10 @@ HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
 MFMA_PEAK = {"bf16": 2.5e15, "f32": 157.3e12}
 PUBLISHED = 401.1e3        # reference's own fwd+bwd tokens/s at this config (M3 Max)
 C = 64
-# HBM bytes per launch at config 1 from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (profiles/gated_delta_config1.md),
-# FETCH_SIZE scaled by 2.000 and WRITE_SIZE by 1.000 (the factors a plain 256 MiB device copy gives); the two prep
-# launches are profiled together (their average)
-TRAFFIC = {1: {"chunk_bwd": 304.8e6, "state_pair": 311.6e6, "state_bwd": 163.8e6, "state_fwd_store": 151.2e6,
-               "state_fwd_out": 109.3e6, "prep_fwd": 147.6e6, "prep_bwd": 147.6e6}}
+# HBM bytes per launch of the training step at config 1 from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+# (profiles/gated_delta_config1.md), FETCH_SIZE scaled by 2.000 and WRITE_SIZE by 1.000 (the factors a plain 256 MiB
+# device copy gives); prep with A, as the training forward runs it
+TRAFFIC = {1: {"chunk_bwd": 297.1e6, "state_pair": 312.2e6, "state_fwd_out": 109.3e6, "prep_fwd": 151.8e6}}
 
 CONFIGS = {
     1: dict(B=4, T=1024, Hk=16, Hv=16, DK=128, DV=128, s0=False),
@@ -213,6 +212,8 @@ def main():
     ap.add_argument("--packed", choices=["uniform", "ragged"],
                     help="run the batch as one packed row (cu_seqlens): B sequences of T tokens, or seeded ragged "
                          "lengths with the same total")
+    ap.add_argument("--no-alone", action="store_true",
+                    help="skip timing each pass alone, so a kernel trace of the run holds the step's launches only")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run one plain device copy of this many MiB (calibrates rocprof byte counters)")
     args = ap.parse_args()
@@ -293,7 +294,10 @@ def main():
     # each pass alone at the batched layout; packed rows (whose per-sequence chunking those launches do not follow)
     # report the in-step times only
     rows = B * H if not args.packed else (len(kw["cu_seqlens"]) - 1) * H
-    alone, split = time_kernels(inp, keep=keep) if not args.packed else ({}, op.split_for(rows, T, DV))
+    if args.packed or args.no_alone:
+        alone, split = {}, op.split_for(rows, T, DV)
+    else:
+        alone, split = time_kernels(inp, keep=keep)
     ktime = dict(in_step)                # the passes as the step runs them
     if args.copy_mib:
         src = torch.ones(args.copy_mib << 18, device=dev)
@@ -305,8 +309,8 @@ def main():
         cu = kw["cu_seqlens"].tolist()
         chunks = sum(math.ceil((b - a) / C) for a, b in zip(cu, cu[1:]))
     cost = kernel_costs(B, T, H, DK, DV, Hk=c["Hk"] if args.grouped else None, chunks=chunks, keep=keep)
-    # rocprof traffic was measured on the batched layout
-    traffic = {} if args.packed else TRAFFIC.get(args.config, {})
+    # rocprof traffic was measured on the batched layout with the forward keeping prep's operands
+    traffic = {} if args.packed or not keep else TRAFFIC.get(args.config, {})
     kernels = {}
     for name, t in ktime.items():
         bw = cost[name]["bytes"] / t

@@ -31,7 +31,7 @@ OVERLAP = True
 # RECOMPUTE_STATES (the reference's switch, op.py:27-33; outputs and gradients have the same bits either way):
 # False (the default here) -- the training forward runs prep in its backward mode (A as well) and keeps its per-chunk
 # operands W, U, Ke, Qg, M, GL, A for the backward, which then skips its prep launch.  At D = 128 in bf16 they hold
-# about 10x the bytes of q (96 MiB a layer at B = 4, T = 1024, H = 16): room a 288 GB part has.  True -- the forward
+# 6x the bytes of q (96 MiB a layer at B = 4, T = 1024, H = 16): room a 288 GB part has.  True -- the forward
 # keeps only its inputs and the backward recomputes prep (the reference's default, chosen there for the Metal
 # allocator's footprint).  The chunk states are recomputed either way: that pass runs in the same launch as the
 # reverse pass (OVERLAP), where it costs little.
