@@ -878,6 +878,209 @@ __global__ void __launch_bounds__(64 * (NW + 1)) state_fwd_kernel(StateFwdArgs a
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
+// The forward state pass with the output, the chain and the output on separate waves (bf16, NW <= 2 column slices per
+// workgroup).  A chain wave runs only what the next chunk's state depends on -- Vn = U - W S and
+// S <- exp(G_last) S + (diag(e) K)^T Vn -- and hands S and Vn, as the bf16 MFMA fragments it formed, to its output
+// wave through LDS.  The output wave forms O = diag(gamma) Q S + M Vn for that chunk one chunk later, from the same
+// fragments with the same products in the same order as state_fwd_body (so the same bits).  The loader wave copies W
+// and diag(e) K^ one chunk ahead of the chain and diag(gamma) Q^ and M in the chunk the chain computes, for the output
+// wave's use one chunk later: each of the three LDS rings (W, Ke | Qg, M | hand-off) is two stages deep, and one
+// barrier a chunk orders them.
+// ---------------------------------------------------------------------------------------------------------------------
+template <int DK, int NW>
+struct StateOutLds {
+  using GW = Tile<bf16, C, DK>;   // W, diag(e) K^, diag(gamma) Q^     [t][d]
+  using GM = Tile<bf16, C, C>;    // M                                  [t][s]
+  static constexpr int ND = DK / 16;
+  static constexpr int O_KE = GW::ELEMS, WK = 2 * GW::ELEMS;          // a [W | Ke] stage
+  static constexpr int O_M = GW::ELEMS, QM = GW::ELEMS + GM::ELEMS;   // a [Qg | M] stage
+  static constexpr int HO = (ND / 2 + 2) * 64 * 8;                    // one chain wave's S and Vn fragments
+  static constexpr int O_QM = 2 * WK, O_HO = O_QM + 2 * QM;
+  static constexpr int ELEMS = O_HO + 2 * NW * HO;
+  static_assert(ELEMS * 2 <= LDS_BYTES, "state_out LDS");
+};
+
+template <int DK, int NW>
+__global__ void __launch_bounds__(64 * (2 * NW + 1)) state_out_kernel(StateFwdArgs a) {
+  using MT = bf16;
+  using L = StateOutLds<DK, NW>;
+  using GW = typename L::GW;
+  using GM = typename L::GM;
+  constexpr int ND = DK / 16;
+  __shared__ __attribute__((aligned(1024))) MT lds[L::ELEMS];
+
+  const int T = a.T, H = a.H, DV = a.DV, NT = a.NT;
+  int hr, slice;
+  if (!state_map(a.nslice, a.B * H, hr, slice, blockIdx.x)) return;
+  const int b = hr / H, h = hr % H;
+  const int l = lane_id(), w = wave_id(), j = l >> 4;
+  int cb, ce;                              // this head-row's chunks (its sequence's, for packed rows)
+  seq_chunks(a.pack, NT, b, cb, ce);
+  const int nc = ce - cb;
+  const size_t crow = a.pack ? (size_t)h : (size_t)hr;   // row of the per-chunk tensors [*, H, NT, ...]
+  const int tb = a.pack ? 0 : b;           // batch row of the token tensors
+  // barriers: B_0 before the first chunk, B_{i+1} at the end of the chain's chunk cb + i; every wave passes all nc + 1
+
+  if (w == 2 * NW) {                       // the loader wave
+    int offW[GW::per_wave(1)], offM[GM::per_wave(1)];
+    GW::template plan<1>(offW, 0, DK);
+    GM::template plan<1>(offM, 0, C);
+    auto wk = [&](int c, int s) {
+      MT* st = lds + s * L::WK;
+      const size_t bhc = crow * NT + c;
+      GW::template dma_planned<1>(st, (const MT*)a.W + bhc * C * DK, offW, 0);
+      GW::template dma_planned<1>(st + L::O_KE, (const MT*)a.Ke + bhc * C * DK, offW, 0);
+    };
+    auto qm = [&](int c, int s) {
+      MT* st = lds + L::O_QM + s * L::QM;
+      const size_t bhc = crow * NT + c;
+      GW::template dma_planned<1>(st, (const MT*)a.Qg + bhc * C * DK, offW, 0);
+      GM::template dma_planned<1>(st + L::O_M, (const MT*)a.M + bhc * C * C, offM, 0);
+    };
+    if (nc > 0) wk(cb, 0);
+    wait_dma();
+    lds_barrier();                         // B_0: the first [W | Ke] stage is in
+    for (int i = 0; i < nc; ++i) {
+      if (i + 1 < nc) wk(cb + i + 1, (i + 1) & 1);
+      qm(cb + i, i & 1);
+      wait_dma();
+      lds_barrier();                       // B_{i+1}
+    }
+    return;
+  }
+
+  const bool chain = w < NW;
+  const int cw = chain ? w : w - NW;       // the column slice's chain wave
+  const int v0 = (slice * NW + cw) * 16;
+  const int col = v0 + (l & 15);
+  MT* const ho = lds + L::O_HO + cw * 2 * L::HO;   // the slice's two hand-off stages
+  auto ho_frag = [&](int s, int u) { return ho + s * L::HO + (u * 64 + l) * 8; };
+
+  if (chain) {
+    auto loadU = [&](int c, f4* U) {
+      const float* Uc = a.U + (crow * NT + c) * C * DV + (size_t)(4 * j) * DV + col;
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) U[mi][r] = Uc[(16 * mi + r) * DV];
+    };
+    f4 S[ND];
+    load_state(S, a.s0, (size_t)hr * DK * DV, DV, col);
+    f4 Un[4];
+    float gln = 0.f;
+    if (nc > 0) {
+      loadU(cb, Un);
+      gln = a.GL[crow * NT + cb];
+    }
+    lds_barrier();                         // B_0
+    for (int i = 0; i < nc; ++i) {
+      const int c = cb + i, s = i & 1;
+      f4 U[4];
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) U[mi] = Un[mi];
+      const float gl = gln;
+      if (i + 1 < nc) {
+        loadU(c + 1, Un);
+        gln = a.GL[crow * NT + c + 1];
+      }
+      const MT* st = lds + s * L::WK;
+      // every fragment that does not depend on S first, then the products k-block by k-block across their tiles
+      Frag<MT> fw[4][ND / 2], fk[ND][2];
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int p = 0; p < ND / 2; ++p) fw[mi][p] = frag_tile<MT, GW>(st, 16 * mi, 32 * p);
+#pragma unroll
+      for (int di = 0; di < ND; ++di)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) fk[di][p] = frag_tile_tr<MT, GW>(st + L::O_KE, 32 * p, 16 * di);
+      // S as the B operand (k = state rows), handed off
+      Frag<MT> Sf[ND / 2];
+#pragma unroll
+      for (int p = 0; p < ND / 2; ++p) {
+        Sf[p] = frag_acc<MT>(S[2 * p], S[2 * p + 1]);
+        *reinterpret_cast<bf16x8*>(ho_frag(s, p)) = Sf[p].v;
+      }
+      // Vn = U - W S
+      f4 Vn[4];
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) Vn[mi] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p = 0; p < ND / 2; ++p)
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi) mma(Vn[mi], fw[mi][p], Sf[p]);
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) Vn[mi] = U[mi] - Vn[mi];
+      Frag<MT> Vf[2];
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        Vf[p] = frag_acc<MT>(Vn[2 * p], Vn[2 * p + 1]);
+        *reinterpret_cast<bf16x8*>(ho_frag(s, ND / 2 + p)) = Vf[p].v;
+      }
+      // S <- exp(G_last) S + (diag(e) K)^T Vn
+#pragma unroll
+      for (int di = 0; di < ND; ++di) S[di] = S[di] * gl;
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int di = 0; di < ND; ++di) mma(S[di], fk[di][p], Vf[p]);
+      lds_barrier();                       // B_{i+1}: this chunk's hand-off is visible, its [W | Ke] stage free
+    }
+    if (a.sT) {
+#pragma unroll
+      for (int di = 0; di < ND; ++di)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) a.sT[(size_t)hr * DK * DV + (16 * di + 4 * j + r) * DV + col] = S[di][r];
+    }
+    return;
+  }
+
+  // the output wave: chunk cb + i after B_{i+1}
+  const size_t o_base = ((size_t)tb * T * H + h) * DV, o_pitch = (size_t)H * DV;
+  lds_barrier();                           // B_0
+  for (int i = 0; i < nc; ++i) {
+    lds_barrier();                         // B_{i+1}
+    const int c = cb + i, s = i & 1;
+    const MT* st = lds + L::O_QM + s * L::QM;
+    Frag<MT> Sf[ND / 2], Vf[2];
+#pragma unroll
+    for (int p = 0; p < ND / 2; ++p) Sf[p].v = *reinterpret_cast<const bf16x8*>(ho_frag(s, p));
+#pragma unroll
+    for (int p = 0; p < 2; ++p) Vf[p].v = *reinterpret_cast<const bf16x8*>(ho_frag(s, ND / 2 + p));
+    // O = diag(gamma) Q S + M Vn (M lower triangular: k-blocks past the row block are zero), formed as
+    // O^T = S^T (diag(gamma) Q)^T + Vn^T M^T: lane l holds O[16 mi + l % 16][v0 + 4 j + 0..3]
+    Frag<MT> fq[4][ND / 2], fm[4][2];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+      for (int p = 0; p < ND / 2; ++p) fq[mi][p] = frag_tile<MT, GW>(st, 16 * mi, 32 * p);
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+        if (32 * p <= 16 * mi + 15) fm[mi][p] = frag_tile<MT, GM>(st + L::O_M, 16 * mi, 32 * p);
+    }
+    f4 pO[4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) pO[mi] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < ND / 2; ++p)
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) mma(pO[mi], Sf[p], fq[mi][p]);
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+        if (32 * p <= 16 * mi + 15) mma(pO[mi], Vf[p], fm[mi][p]);
+    int t0, tend;
+    chunk_span(a.pack, NT, c, T, t0, tend);
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      const int t = t0 + 16 * mi + (l & 15);
+      if (t < tend) store4<MT>((MT*)a.o + o_base + (size_t)t * o_pitch + v0 + 4 * j, pO[mi]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------------
 // the reverse state pass: streams diag(e) K^, diag(gamma) Q^, W, M and the workgroup's dO columns per chunk
 // ---------------------------------------------------------------------------------------------------------------------
 template <typename MT, int DK, int NW>
@@ -2356,6 +2559,10 @@ int macai_gdr_state_fwd(const void* W, const float* U, const void* Ke, const flo
   if (dtype == MACAI_GDR_F32) {
     if (out) { LAUNCH_SF(float, true, false); }
     else { LAUNCH_SF(float, false, true); }
+  } else if (out && nw <= 2) {             // chain and output on separate waves
+    const dim3 block2(64 * (2 * nw + 1));
+    if (nw == 1) { DISPATCH_DK(DK, hipLaunchKernelGGL((state_out_kernel<DKC, 1>), grid, block2, 0, st, a)); }
+    else { DISPATCH_DK(DK, hipLaunchKernelGGL((state_out_kernel<DKC, 2>), grid, block2, 0, st, a)); }
   } else {
     if (out) { LAUNCH_SF(bf16, true, false); }
     else { LAUNCH_SF(bf16, false, true); }
