@@ -71,7 +71,8 @@ def kernel_costs(B, T, H, DK, DV, es=2, Hk=None, chunks=None, keep=False):
     FLOPs (2 per multiply-add, triangular products counted dense) per launch of each kernel of the training step.
     Hk: key heads of q and k when they come unrepeated (grouped value heads); H by default.  chunks: chunks per head
     over the batch (B ceil(T / 64) by default; packed rows chunk each sequence on its own).  keep: the forward's prep
-    also writes A (the training forward keeps prep's operands; there is no prep_bwd launch)."""
+    also writes A and its state pass S_c and Vn (the training forward keeps them; the backward runs neither prep nor
+    the recompute pass)."""
     Hk = Hk or H
     chunks = chunks or B * math.ceil(T / C)
     n = H * chunks                       # chunk-heads
@@ -87,7 +88,8 @@ def kernel_costs(B, T, H, DK, DV, es=2, Hk=None, chunks=None, keep=False):
     # the forward: prep, then the state pass reads W, U, Ke, GL, Qg, M and writes o
     cost["prep_fwd"] = dict(bytes=inp + n * (pre + (cc * es if keep else 0)),
                             flops=n * (2 * 2 * cc * DK + cc * C / 3 + 2 * cc * DK + 2 * cc * DV))
-    cost["state_fwd_out"] = dict(bytes=n * pre + io_v, flops=n * (3 * 2 * C * DK * DV + 2 * cc * DV))
+    cost["state_fwd_out"] = dict(bytes=n * (pre + ((sdk + cdv * es) if keep else 0)) + io_v,
+                                 flops=n * (3 * 2 * C * DK * DV + 2 * cc * DV))
     # the backward: prep also writes A; the recompute pass reads W, U, Ke, GL and writes S_c (fp32) and Vn; the reverse
     # pass reads Ke, Qg, W, M, GL, dO and writes dS_{c+1} (fp32) and dVn
     cost["prep_bwd"] = dict(bytes=inp + n * (pre + cc * es),
@@ -110,7 +112,8 @@ def kernel_costs(B, T, H, DK, DV, es=2, Hk=None, chunks=None, keep=False):
 
 def time_kernels(inp, reps=20, keep=False):
     """Each pass of the step alone: HIP events on the current (launch) stream around `reps` back-to-back launches.
-    keep: the forward's prep writes A too (the training forward keeps prep's operands for the backward)."""
+    keep: the forward's prep writes A too and its state pass stores S_c, Vn (the training forward keeps them for the
+    backward)."""
     from macai.gated_delta import _native as N
     from macai.gated_delta import op
     q, k, v, g, beta, do = (inp[n] for n in ("query", "key", "value", "g", "beta", "do"))
@@ -136,8 +139,9 @@ def time_kernels(inp, reps=20, keep=False):
     calls = {
         "prep_fwd": ("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), P(Ke), P(GL), P(Qg), P(M),
                      P(A) if keep else None, B, T, H, H, DK, DV, code, 1, sc, None, 0, st),
-        "state_fwd_out": ("macai_gdr_state_fwd", P(W), P(U), P(Ke), P(GL), P(Qg), P(M), P(s0), P(o), None, None,
-                          None, B, T, H, DK, DV, code, 0, split, None, 0, st),
+        "state_fwd_out": ("macai_gdr_state_fwd", P(W), P(U), P(Ke), P(GL), P(Qg), P(M), P(s0), P(o), None,
+                          P(Sc) if keep else None, P(Vn) if keep else None, B, T, H, DK, DV, code,
+                          N.STORE_STATES if keep else 0, split, None, 0, st),
         "prep_bwd": ("macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(W), P(U), P(Ke), P(GL), P(Qg), P(M), P(A),
                      B, T, H, H, DK, DV, code, 1, sc, None, 0, st),
         "state_fwd_store": ("macai_gdr_state_fwd", P(W), P(U), P(Ke), P(GL), None, None, P(s0), None, None, P(Sc),

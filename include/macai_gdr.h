@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define MACAI_GDR_ABI_VERSION 7
+#define MACAI_GDR_ABI_VERSION 8
 
 /* dtype codes */
 #define MACAI_GDR_F32 0
@@ -63,7 +63,7 @@ extern "C" {
 #define MACAI_GDR_ELAUNCH 3 /* HIP launch error (hipGetLastError) */
 
 /* state-pass flags (the reference's gdc_fwd flags, _chunked.py:335-338) */
-#define MACAI_GDR_STORE_STATES 1 /* store Sc and Vn for the backward */
+#define MACAI_GDR_STORE_STATES 1 /* store Sc and Vn for the backward (with or without the output) */
 #define MACAI_GDR_NO_OUTPUT 8    /* write neither o nor the final state */
 
 const char* macai_gdr_last_error(void);
@@ -80,7 +80,8 @@ int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, 
 
 /* The sequential state pass (north star (2) + (3)): S <- exp(G_last) S + K^T diag(e) (U - W S) over the chunks from
  * s0 (NULL = zeros).  flags = 0: the output O = diag(gamma) Q S + M Vn to o (dtype) and the final state to sT when
- * sT != NULL (needs Qg, M); flags = STORE_STATES | NO_OUTPUT: Sc and Vn for the backward.  split = workgroups per
+ * sT != NULL (needs Qg, M); flags = STORE_STATES | NO_OUTPUT: Sc and Vn for the backward (the backward's recompute);
+ * flags = STORE_STATES: both (a training forward that keeps the states for its backward).  split = workgroups per
  * head-row's value columns (DV / 16 / split must be 1, 2, 4 or 8; 0 = automatic).  Replaces `lib.gdc_fwd(q, k, v,
  * beta, s0, gc, a, m, o, sT, sc, vn, xu, ckpt, T, H, DV, flags, ...)` (reference op.py:159, 217; kernel
  * _chunked.py:315-659). */

@@ -640,14 +640,14 @@ struct Buffers {
 // the output, diag(gamma) Q^ and M into a swizzled LDS stage by asynchronous copies -- the next chunk's copies are in
 // flight while this chunk's MFMAs run -- and each wave keeps its 16 columns of S in accumulators.
 // ---------------------------------------------------------------------------------------------------------------------
-template <typename MT, int DK, bool OUT, int NW>
+template <typename MT, int DK, bool OUT, bool STORE, int NW>
 struct StateFwdLds {
   using GW = Tile<MT, C, DK>;    // W, diag(e) K^, diag(gamma) Q^     [t][d]
   using GM = Tile<MT, C, C>;     // M                                  [t][s]
   static constexpr int O_KE = GW::ELEMS, O_Q = O_KE + GW::ELEMS, O_M = O_Q + (OUT ? GW::ELEMS : 0);
   static constexpr int SZ = O_M + (OUT ? GM::ELEMS : 0);
   // bf16 Vn leaves through per-wave row staging (store mode)
-  static constexpr int STG = (!OUT && sizeof(MT) == 2) ? NW * ColStage::ELEMS : 0;
+  static constexpr int STG = (STORE && sizeof(MT) == 2) ? NW * ColStage::ELEMS : 0;
   static constexpr int NBUF = Buffers<SZ * (int)sizeof(MT), STG * (int)sizeof(MT)>::N;
   static constexpr int O_STG = NBUF * SZ;
   static constexpr int ELEMS = O_STG + STG;
@@ -656,7 +656,7 @@ struct StateFwdLds {
 // The pass of workgroup f of the launch (see state_map), with `lds` the workgroup's LDS (StateFwdLds::ELEMS elements).
 template <typename MT, int DK, int NW, bool OUT, bool STORE>
 __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, int f) {
-  using L = StateFwdLds<MT, DK, OUT, NW>;
+  using L = StateFwdLds<MT, DK, OUT, STORE, NW>;
   using GW = typename L::GW;
   using GM = typename L::GM;
   constexpr int ND = DK / 16;
@@ -873,7 +873,7 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
 
 template <typename MT, int DK, int NW, bool OUT, bool STORE>
 __global__ void __launch_bounds__(64 * (NW + 1)) state_fwd_kernel(StateFwdArgs a) {
-  __shared__ __attribute__((aligned(1024))) MT lds[StateFwdLds<MT, DK, OUT, NW>::ELEMS];
+  __shared__ __attribute__((aligned(1024))) MT lds[StateFwdLds<MT, DK, OUT, STORE, NW>::ELEMS];
   state_fwd_body<MT, DK, NW, OUT, STORE>(a, lds, blockIdx.x);
 }
 
@@ -882,12 +882,14 @@ __global__ void __launch_bounds__(64 * (NW + 1)) state_fwd_kernel(StateFwdArgs a
 // workgroup).  A chain wave runs only what the next chunk's state depends on -- Vn = U - W S and
 // S <- exp(G_last) S + (diag(e) K)^T Vn -- and hands S and Vn, as the bf16 MFMA fragments it formed, to its output
 // wave through LDS.  The output wave forms O = diag(gamma) Q S + M Vn for that chunk one chunk later, from the same
-// fragments with the same products in the same order as state_fwd_body (so the same bits).  The loader wave copies W
-// and diag(e) K^ one chunk ahead of the chain and diag(gamma) Q^ and M in the chunk the chain computes, for the output
-// wave's use one chunk later: each of the three LDS rings (W, Ke | Qg, M | hand-off) is two stages deep, and one
-// barrier a chunk orders them.
+// fragments with the same products in the same order as state_fwd_body (so the same bits).  With STORE the pass also
+// writes the backward's S_c (fp32, by the chain wave, whose stores drain under its products) and Vn (bf16, by the
+// output wave from the hand-off: the rounding the store pass writes).  The loader wave copies W and diag(e) K^ one
+// chunk ahead of the chain and diag(gamma) Q^ and M in the chunk the chain computes, for the output wave's use one
+// chunk later: each of the three LDS rings (W, Ke | Qg, M | hand-off) is two stages deep, and one barrier a chunk
+// orders them.
 // ---------------------------------------------------------------------------------------------------------------------
-template <int DK, int NW>
+template <int DK, int NW, bool STORE>
 struct StateOutLds {
   using GW = Tile<bf16, C, DK>;   // W, diag(e) K^, diag(gamma) Q^     [t][d]
   using GM = Tile<bf16, C, C>;    // M                                  [t][s]
@@ -895,15 +897,15 @@ struct StateOutLds {
   static constexpr int O_KE = GW::ELEMS, WK = 2 * GW::ELEMS;          // a [W | Ke] stage
   static constexpr int O_M = GW::ELEMS, QM = GW::ELEMS + GM::ELEMS;   // a [Qg | M] stage
   static constexpr int HO = (ND / 2 + 2) * 64 * 8;                    // one chain wave's S and Vn fragments
-  static constexpr int O_QM = 2 * WK, O_HO = O_QM + 2 * QM;
-  static constexpr int ELEMS = O_HO + 2 * NW * HO;
+  static constexpr int O_QM = 2 * WK, O_HO = O_QM + 2 * QM, O_STG = O_HO + 2 * NW * HO;
+  static constexpr int ELEMS = O_STG + (STORE ? NW * ColStage::ELEMS : 0);   // the output waves' Vn staging
   static_assert(ELEMS * 2 <= LDS_BYTES, "state_out LDS");
 };
 
-template <int DK, int NW>
+template <int DK, int NW, bool STORE>
 __global__ void __launch_bounds__(64 * (2 * NW + 1)) state_out_kernel(StateFwdArgs a) {
   using MT = bf16;
-  using L = StateOutLds<DK, NW>;
+  using L = StateOutLds<DK, NW, STORE>;
   using GW = typename L::GW;
   using GM = typename L::GM;
   constexpr int ND = DK / 16;
@@ -1001,6 +1003,13 @@ __global__ void __launch_bounds__(64 * (2 * NW + 1)) state_out_kernel(StateFwdAr
         Sf[p] = frag_acc<MT>(S[2 * p], S[2 * p + 1]);
         *reinterpret_cast<bf16x8*>(ho_frag(s, p)) = Sf[p].v;
       }
+      if constexpr (STORE) {               // S_c in fp32
+        float* Scc = a.Sc + (crow * NT + c) * DK * DV + (size_t)(4 * j) * DV + col;
+#pragma unroll
+        for (int di = 0; di < ND; ++di)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) Scc[(16 * di + r) * DV] = S[di][r];
+      }
       // Vn = U - W S
       f4 Vn[4];
 #pragma unroll
@@ -1076,6 +1085,17 @@ __global__ void __launch_bounds__(64 * (2 * NW + 1)) state_out_kernel(StateFwdAr
     for (int mi = 0; mi < 4; ++mi) {
       const int t = t0 + 16 * mi + (l & 15);
       if (t < tend) store4<MT>((MT*)a.o + o_base + (size_t)t * o_pitch + v0 + 4 * j, pO[mi]);
+    }
+    if constexpr (STORE) {                 // Vn in accumulator layout (exact: they are bf16 values)
+      f4 Y[4];
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          Y[2 * p][r] = (float)Vf[p].v[r];
+          Y[2 * p + 1][r] = (float)Vf[p].v[r + 4];
+        }
+      store_cols(lds + L::O_STG + cw * ColStage::ELEMS, (MT*)a.Vn + (crow * NT + c) * C * DV + v0, DV, Y);
     }
   }
 }
@@ -1268,7 +1288,7 @@ __global__ void __launch_bounds__(64 * (NW + 1)) state_bwd_kernel(StateBwdArgs a
 // stream synchronisation between them.
 template <typename MT, int DK, int NW>
 __global__ void __launch_bounds__(64 * (NW + 1)) state_pair_kernel(StateFwdArgs af, StateBwdArgs ab, int nfwd) {
-  constexpr int EF = StateFwdLds<MT, DK, false, NW>::ELEMS, EB = StateBwdLds<MT, DK, NW>::ELEMS;
+  constexpr int EF = StateFwdLds<MT, DK, false, true, NW>::ELEMS, EB = StateBwdLds<MT, DK, NW>::ELEMS;
   __shared__ __attribute__((aligned(1024))) MT lds[EF > EB ? EF : EB];
   if ((int)blockIdx.x < nfwd) state_fwd_body<MT, DK, NW, false, true>(af, lds, blockIdx.x);
   else state_bwd_body<MT, DK, NW>(ab, lds, blockIdx.x - nfwd);
@@ -2538,8 +2558,10 @@ int macai_gdr_state_fwd(const void* W, const float* U, const void* Ke, const flo
   if (!rc) rc = pack_chunks(what, pack, NT_packed, B, T, &NT);
   if (rc) return rc;
   const bool store = flags & MACAI_GDR_STORE_STATES, out = !(flags & MACAI_GDR_NO_OUTPUT);
-  if (out == store)
-    return fail(MACAI_GDR_EINVAL, "%s: flags must be 0 (output) or STORE_STATES | NO_OUTPUT (recompute)", what);
+  if ((flags & ~(MACAI_GDR_STORE_STATES | MACAI_GDR_NO_OUTPUT)) || (!out && !store))
+    return fail(MACAI_GDR_EINVAL,
+                "%s: flags must be 0 (output), STORE_STATES (output and states) or STORE_STATES | NO_OUTPUT (states)",
+                what);
   if (!W || !U || !Ke || !GL) return fail(MACAI_GDR_EINVAL, "%s: null input pointer", what);
   if (out && (!Qg || !M || !o)) return fail(MACAI_GDR_EINVAL, "%s: the output needs Qg, M and o", what);
   if (store && (!Sc || !Vn)) return fail(MACAI_GDR_EINVAL, "%s: storing states needs Sc and Vn", what);
@@ -2556,17 +2578,25 @@ int macai_gdr_state_fwd(const void* W, const float* U, const void* Ke, const flo
   hipStream_t st = (hipStream_t)stream;
 #define LAUNCH_SF(MT, O, S) \
   DISPATCH_DK(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_fwd_kernel<MT, DKC, NWC, O, S>), grid, block, 0, st, a)))
+#define LAUNCH_SO(S)                                                                                                  \
+  {                                                                                                                   \
+    const dim3 block2(64 * (2 * nw + 1));                                                                             \
+    if (nw == 1) { DISPATCH_DK(DK, hipLaunchKernelGGL((state_out_kernel<DKC, 1, S>), grid, block2, 0, st, a)); }       \
+    else { DISPATCH_DK(DK, hipLaunchKernelGGL((state_out_kernel<DKC, 2, S>), grid, block2, 0, st, a)); }              \
+  }
   if (dtype == MACAI_GDR_F32) {
-    if (out) { LAUNCH_SF(float, true, false); }
+    if (out && store) { LAUNCH_SF(float, true, true); }
+    else if (out) { LAUNCH_SF(float, true, false); }
     else { LAUNCH_SF(float, false, true); }
   } else if (out && nw <= 2) {             // chain and output on separate waves
-    const dim3 block2(64 * (2 * nw + 1));
-    if (nw == 1) { DISPATCH_DK(DK, hipLaunchKernelGGL((state_out_kernel<DKC, 1>), grid, block2, 0, st, a)); }
-    else { DISPATCH_DK(DK, hipLaunchKernelGGL((state_out_kernel<DKC, 2>), grid, block2, 0, st, a)); }
+    if (store) { LAUNCH_SO(true); }
+    else { LAUNCH_SO(false); }
   } else {
-    if (out) { LAUNCH_SF(bf16, true, false); }
+    if (out && store) { LAUNCH_SF(bf16, true, true); }
+    else if (out) { LAUNCH_SF(bf16, true, false); }
     else { LAUNCH_SF(bf16, false, true); }
   }
+#undef LAUNCH_SO
 #undef LAUNCH_SF
   return launched(what);
 }

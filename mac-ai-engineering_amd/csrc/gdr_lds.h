@@ -182,17 +182,23 @@ struct ColStage {
   static constexpr int P = 24;                   // row pitch (elements): 48 bytes, 16-byte aligned rows
   static constexpr int ELEMS = 64 * P;
 };
-__device__ __forceinline__ void store_cols(bf16* stg, bf16* g, size_t gpitch, const f4 (&X)[4]) {
+// NTL = 2 or 4 accumulator tiles (32 or 64 rows) X[0 .. NTL).
+template <int NTL>
+__device__ __forceinline__ void store_rows(bf16* stg, bf16* g, size_t gpitch, const f4* X) {
+  static_assert(NTL == 2 || NTL == 4, "store_rows: 32 or 64 rows");
   const int l = lane_id(), j = l >> 4, n = l & 15;
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+  for (int mi = 0; mi < NTL; ++mi)
 #pragma unroll
     for (int r = 0; r < 4; ++r) stg[(16 * mi + 4 * j + r) * ColStage::P + n] = (bf16)X[mi][r];
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {                  // 128 units: row u / 2, columns 8 (u % 2) .. + 7
+  for (int k = 0; k < NTL / 2; ++k) {            // 32 NTL units: row u / 2, columns 8 (u % 2) .. + 7
     const int u = 64 * k + l, row = u >> 1, cu = u & 1;
     *reinterpret_cast<u32x4*>(g + row * gpitch + 8 * cu) = *reinterpret_cast<const u32x4*>(stg + row * ColStage::P + 8 * cu);
   }
+}
+__device__ __forceinline__ void store_cols(bf16* stg, bf16* g, size_t gpitch, const f4 (&X)[4]) {
+  store_rows<4>(stg, g, gpitch, X);
 }
 
 }  // namespace gdr

@@ -29,12 +29,12 @@ EVENTS = None
 # whose speed hardly depends on how many CUs they get, so this nearly hides one of them.
 OVERLAP = True
 # RECOMPUTE_STATES (the reference's switch, op.py:27-33; outputs and gradients have the same bits either way):
-# False (the default here) -- the training forward runs prep in its backward mode (A as well) and keeps its per-chunk
-# operands W, U, Ke, Qg, M, GL, A for the backward, which then skips its prep launch.  At D = 128 in bf16 they hold
-# 6x the bytes of q (96 MiB a layer at B = 4, T = 1024, H = 16): room a 288 GB part has.  True -- the forward
-# keeps only its inputs and the backward recomputes prep (the reference's default, chosen there for the Metal
-# allocator's footprint).  The chunk states are recomputed either way: that pass runs in the same launch as the
-# reverse pass (OVERLAP), where it costs little.
+# False (the default here) -- the training forward runs prep in its backward mode (A as well) and its state pass
+# stores the chunk states S_c and Vn beside the output; it keeps those and prep's per-chunk operands W, U, Ke, Qg, M,
+# GL, A for the backward, which then runs only the reverse state pass and the per-chunk backward.  At D = 128 in bf16
+# that is 2,816 bytes per token-head, 11x q's (176 MiB a layer at B = 4, T = 1024, H = 16): room a 288 GB part has.
+# True -- the forward keeps only its inputs and the backward recomputes prep and the chunk states (the reference's
+# default, chosen there for the Metal allocator's footprint).
 RECOMPUTE_STATES = False
 
 
@@ -167,24 +167,29 @@ def _prep(q, k, v, g, beta, l2norm: bool, q_scale: float, with_A: bool, pack=Non
 
 
 def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, pack=None, keep=False):
-    """prep, then the state pass with the output: returns (o in q's dtype, sT or None, prep's operands with A when
-    keep -- for the backward -- else None)."""
+    """prep, then the state pass with the output: returns (o in q's dtype, sT or None, and when keep -- for the
+    backward -- prep's operands with A and the chunk states Sc, Vn, else None)."""
     B, T, H, Hk, DK, DV, NT = _dims(q, v, pack)
+    Bc = q.shape[0]
     dev, dt = q.device, q.dtype
     code, stream = N.dtype_code(dt), N.stream_of(q)
     r = _prep(q, k, v, g, beta, l2norm, q_scale, keep, pack, "prep_fwd")
-    o = torch.empty(q.shape[0], T, H, DV, device=dev, dtype=dt)
+    o = torch.empty(Bc, T, H, DV, device=dev, dtype=dt)
     sT = torch.empty(B, H, DK, DV, device=dev, dtype=torch.float32) if want_sT else None
+    if keep:
+        r["Sc"] = torch.empty(Bc, H, NT, DK, DV, device=dev, dtype=torch.float32)
+        r["Vn"] = torch.empty(Bc, H, NT, CHUNK, DV, device=dev, dtype=dt)
     split = split_for(B * H, T, DV)
     P = N.ptr
     _launch("state_fwd_out", "macai_gdr_state_fwd", P(r["W"]), P(r["U"]), P(r["Ke"]), P(r["GL"]), P(r["Qg"]), P(r["M"]),
-            P(s0), P(o), P(sT), None, None, B, T, H, DK, DV, code, 0, split, *_pack_args(pack), stream)
+            P(s0), P(o), P(sT), P(r.get("Sc")), P(r.get("Vn")), B, T, H, DK, DV, code, N.STORE_STATES if keep else 0,
+            split, *_pack_args(pack), stream)
     CALLS[f"fwd s{split}"] += 1
     return o, sT, (r if keep else None)
 
 
 def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=None, r=None):
-    """Recompute (prep unless the forward kept its operands `r`; the state pass storing S_c and Vn), the reverse state
+    """Recompute (prep and the state pass storing S_c and Vn, unless the forward kept them in `r`), the reverse state
     pass, the per-chunk backward.  Returns (dq, dk, dv in q's dtype; dg, dbeta, ds0 float32).  With grouped heads (Hk < H) the per-chunk backward writes dq,
     dk per value head and macai_gdr_group_sum folds each group (the backward of the repeat the grouped layout
     replaces)."""
@@ -197,13 +202,17 @@ def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=
         r = _prep(q, k, v, g, beta, l2norm, q_scale, True, pack)
     P = N.ptr
     pk = _pack_args(pack)
-    split = split_for(B * H, T, DV, 2 if OVERLAP else 1)
-    Sc = torch.empty(Bc, H, NT, DK, DV, device=dev, dtype=f32)
-    Vn = torch.empty(Bc, H, NT, CHUNK, DV, device=dev, dtype=dt)
+    kept = "Sc" in r                     # the forward stored the chunk states: only the reverse pass is left
+    split = split_for(B * H, T, DV, 2 if OVERLAP and not kept else 1)
+    Sc = r["Sc"] if kept else torch.empty(Bc, H, NT, DK, DV, device=dev, dtype=f32)
+    Vn = r["Vn"] if kept else torch.empty(Bc, H, NT, CHUNK, DV, device=dev, dtype=dt)
     dSn = torch.empty(Bc, H, NT, DK, DV, device=dev, dtype=f32)
     dVn = torch.empty_like(Vn)
     ds0 = torch.empty(B, H, DK, DV, device=dev, dtype=f32)
-    if OVERLAP:
+    if kept:
+        _launch("state_bwd", "macai_gdr_state_bwd", P(r["Ke"]), P(r["Qg"]), P(r["W"]), P(r["M"]), P(r["GL"]), P(do),
+                P(dsT), P(dSn), P(dVn), P(ds0), B, T, H, DK, DV, code, split, *pk, stream)
+    elif OVERLAP:
         _launch("state_pair", "macai_gdr_state_pair", P(r["W"]), P(r["U"]), P(r["Ke"]), P(r["Qg"]), P(r["M"]),
                 P(r["GL"]), P(s0), P(do), P(dsT), P(Sc), P(Vn), P(dSn), P(dVn), P(ds0), B, T, H, DK, DV, code, split,
                 *pk, stream)

@@ -38,6 +38,12 @@ def passes(q, k, v, g, beta, s0, do, dsT, l2norm=False, q_scale=1.0, split=0):
     r["Sc"], r["Vn"] = e(B, H, NT, DK, DV), e(B, H, NT, C, DV, d=dt)
     N.call("macai_gdr_state_fwd", P(b2["W"]), P(b2["U"]), P(b2["Ke"]), P(b2["GL"]), None, None, P(s0), None, None,
            P(r["Sc"]), P(r["Vn"]), B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, None, 0, st)
+    # the training forward's form: output and states in one pass (flags STORE_STATES)
+    k2 = {"o": e(B, T, H, DV, d=dt), "sT": e(B, H, DK, DV), "Sc": e(B, H, NT, DK, DV),
+          "Vn": e(B, H, NT, C, DV, d=dt)}
+    N.call("macai_gdr_state_fwd", P(b2["W"]), P(b2["U"]), P(b2["Ke"]), P(b2["GL"]), P(b2["Qg"]), P(b2["M"]), P(s0),
+           P(k2["o"]), P(k2["sT"]), P(k2["Sc"]), P(k2["Vn"]), B, T, H, DK, DV, code, N.STORE_STATES, split, None, 0,
+           st)
     r["dSn"], r["dVn"], r["ds0"] = e(B, H, NT, DK, DV), e(B, H, NT, C, DV, d=dt), e(B, H, DK, DV)
     N.call("macai_gdr_state_bwd", P(b2["Ke"]), P(b2["Qg"]), P(b2["W"]), P(b2["M"]), P(b2["GL"]), P(do), P(dsT),
            P(r["dSn"]), P(r["dVn"]), P(r["ds0"]), B, T, H, DK, DV, code, split, None, 0, st)
@@ -49,4 +55,6 @@ def passes(q, k, v, g, beta, s0, do, dsT, l2norm=False, q_scale=1.0, split=0):
     torch.cuda.synchronize()
     out = {k_: x.cpu() for k_, x in r.items()}
     out["W2_equal"] = all(torch.equal(b2[n_].cpu(), out[n_]) for n_ in b2)
+    # the one-pass output + states must equal the output pass and the recompute pass bit for bit
+    out["store_equal"] = all(torch.equal(k2[n_].cpu(), out[n_]) for n_ in k2)
     return out

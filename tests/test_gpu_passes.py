@@ -29,6 +29,7 @@ def test_passes_fp32(shape):
                Ke=P["e"][..., None] * P["K"], Qg=P["gam"][..., None] * P["Q"], GL=P["gam"][..., -1])
     ref.update(dict(zip(NAMES, grads)))
     assert r["W2_equal"], "the forward- and backward-mode preps must give the same bits"
+    assert r["store_equal"], "the output pass storing the states must give the output and recompute passes' bits"
     errs = {n: gdr.rel(r[n], ref[n]) for n in ref}
     print(errs)
     bad = {n: e for n, e in errs.items() if not e < 2e-4}
@@ -57,6 +58,7 @@ def test_passes_bf16(shape):
     bf = lambda x: x.to(dev, torch.bfloat16).contiguous()
     f32 = lambda x: x.to(dev, torch.float32).contiguous()
     r = passes(bf(q), bf(k), bf(v), f32(g), f32(b), f32(s0), bf(do), f32(dsT))
+    assert r["W2_equal"] and r["store_equal"]
     ref = dict(o=o, sT=sT, **dict(zip(NAMES, grads)))
     errs = {n: gdr.rel(r[n].double(), ref[n]) for n in ref}
     print(errs)

@@ -64,9 +64,11 @@ def test_abi_rejects_bad_arguments_before_launch():
     p = 1 << 20
     sf = lambda *ptrs, flags=0, split=0, DV=128: L.macai_gdr_state_fwd(*ptrs, 1, 64, 1, 128, DV, 1, flags, split,
                                                                        None, 0, None)
-    # flags that ask for nothing or both, a split that does not divide DV / 16, a missing output operand
+    # flags that ask for nothing or carry unknown bits, output + states without the state buffers, a split that does
+    # not divide DV / 16, a missing output operand
     assert sf(p, p, p, p, p, p, None, p, None, None, None, flags=8) == N.EINVAL
-    assert sf(p, p, p, p, p, p, None, p, None, p, p, flags=1) == N.EINVAL and b"flags" in L.macai_gdr_last_error()
+    assert sf(p, p, p, p, p, p, None, p, None, p, p, flags=2) == N.EINVAL and b"flags" in L.macai_gdr_last_error()
+    assert sf(p, p, p, p, p, p, None, p, None, None, p, flags=1) == N.EINVAL and b"Sc" in L.macai_gdr_last_error()
     assert sf(p, p, p, p, p, p, None, p, None, None, None, split=3) == N.EINVAL and b"split" in L.macai_gdr_last_error()
     assert sf(p, p, p, p, p, p, None, p, None, None, None, split=1, DV=96) == N.EINVAL
     assert sf(p, p, p, p, p, None, None, p, None, None, None) == N.EINVAL
