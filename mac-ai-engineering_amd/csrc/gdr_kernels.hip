@@ -638,7 +638,8 @@ struct Buffers {
 // ---------------------------------------------------------------------------------------------------------------------
 // the forward state pass (+ output), sequential over chunks.  Per chunk the workgroup streams W, diag(e) K^ and, for
 // the output, diag(gamma) Q^ and M into a swizzled LDS stage by asynchronous copies -- the next chunk's copies are in
-// flight while this chunk's MFMAs run -- and each wave keeps its 16 columns of S in accumulators.
+// flight while this chunk's MFMAs run -- and each wave keeps its 16 columns of S in accumulators.  The barriers order
+// LDS only (lds_barrier): the loader waits for its copies itself, and no wave waits for its global stores.
 // ---------------------------------------------------------------------------------------------------------------------
 template <typename MT, int DK, bool OUT, bool STORE, int NW>
 struct StateFwdLds {
@@ -692,19 +693,19 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
       if (cb < ce) {
         issue(cb, 0);
         wait_dma();
-        __syncthreads();
+        lds_barrier();
       }
       for (int c = cb; c < ce; ++c) {
         if (c + 1 < ce) issue(c + 1, (c + 1 - cb) & 1);
         wait_dma();
-        __syncthreads();
+        lds_barrier();
       }
     } else {
       for (int c = cb; c < ce; ++c) {
         issue(c, 0);
         wait_dma();
-        __syncthreads();   // chunk c is in LDS
-        __syncthreads();   // the compute waves are done with it
+        lds_barrier();   // chunk c is in LDS
+        lds_barrier();   // the compute waves are done with it
       }
     }
     return;                // the compute waves pass no barrier after their loop
@@ -760,7 +761,7 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
   if (cb < ce) {
     loadU(cb, Un);
     gln = a.GL[crow * NT + cb];
-    if (NBUF == 2) __syncthreads();        // the first chunk is in LDS
+    if (NBUF == 2) lds_barrier();        // the first chunk is in LDS
   }
   for (int c = cb; c < ce; ++c) {
     const size_t bhc = crow * NT + c;
@@ -774,7 +775,7 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
       gln = a.GL[bhc + 1];
     }
     if (STORE) store_sc(c, S);
-    if (NBUF == 1) __syncthreads();        // chunk c is in LDS
+    if (NBUF == 1) lds_barrier();        // chunk c is in LDS
     const MT* st = lds + buf * SZ;
 
     // The output pass (one wave per SIMD, registers to spare) reads every fragment that does not depend on S first, so
@@ -861,7 +862,7 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
     }
 #pragma unroll
     for (int di = 0; di < ND; ++di) S[di] = Sn[di];
-    __syncthreads();                       // end of chunk c: the next chunk is in, this buffer may be refilled
+    lds_barrier();                       // end of chunk c: the next chunk is in, this buffer may be refilled
   }
   if (a.sT) {
 #pragma unroll
@@ -1160,19 +1161,19 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
       if (cb < ce) {
         issue(ce - 1, 0);
         wait_dma();
-        __syncthreads();
+        lds_barrier();
       }
       for (int c = ce - 1, it = 0; c >= cb; --c, ++it) {
         if (c > cb) issue(c - 1, (it + 1) & 1);
         wait_dma();
-        __syncthreads();
+        lds_barrier();
       }
     } else {
       for (int c = ce - 1; c >= cb; --c) {
         issue(c, 0);
         wait_dma();
-        __syncthreads();
-        __syncthreads();
+        lds_barrier();
+        lds_barrier();
       }
     }
     return;
@@ -1204,7 +1205,7 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
   float gln = 0.f;
   if (cb < ce) {
     gln = a.GL[crow * NT + ce - 1];
-    if (NBUF == 2) __syncthreads();        // the last chunk is in LDS
+    if (NBUF == 2) lds_barrier();        // the last chunk is in LDS
   }
   for (int c = ce - 1, it = 0; c >= cb; --c, ++it) {
     int t0, tend;
@@ -1214,7 +1215,7 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
     const float gl = gln;
     if (c > cb) gln = a.GL[bhc - 1];
     store_ds(c, dS);
-    if (NBUF == 1) __syncthreads();        // chunk c is in LDS
+    if (NBUF == 1) lds_barrier();        // chunk c is in LDS
     const MT* st = lds + buf * SZ;
 
     Frag<MT> Of[2];
@@ -1269,7 +1270,7 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
     }
 #pragma unroll
     for (int di = 0; di < ND; ++di) dS[di] = dSn[di];
-    __syncthreads();                       // end of chunk c
+    lds_barrier();                       // end of chunk c
   }
 #pragma unroll
   for (int di = 0; di < ND; ++di)
