@@ -29,6 +29,7 @@ SIGNATURES = {
 }
 
 _lib = None
+_fns = {}        # name -> the library's function object (a lookup per call costs host time on every launch)
 
 
 class NativeError(RuntimeError):
@@ -70,13 +71,17 @@ def dtype_code(dt):
 
 
 def stream_of(t):
-    return torch.cuda.current_stream(t.device).cuda_stream
+    """hipStream_t of torch's current stream on t's device (the raw handle, without building a Stream object)."""
+    return torch._C._cuda_getCurrentRawStream(t.get_device())
 
 
 def call(name, *args):
     """Call entry point `name`; raise on a non-zero return (ValueError for bad arguments, NotImplementedError for an
     unsupported shape or dtype, NativeError for a launch failure)."""
-    rc = getattr(lib(), name)(*args)
+    fn = _fns.get(name)
+    if fn is None:
+        fn = _fns[name] = getattr(lib(), name)
+    rc = fn(*args)
     if rc != OK:
         msg = lib().macai_gdr_last_error().decode()
         if rc == EINVAL:

@@ -8,6 +8,7 @@ include/macai_gdr.h on the current HIP stream.  What the training forward keeps 
 RECOMPUTE_STATES (the reference's switch, op.py:27-33).
 """
 import collections
+import contextlib
 import math
 import weakref
 
@@ -57,7 +58,19 @@ def valid_splits(dv: int) -> list:
     return [s for s in range(1, slices + 1) if slices % s == 0 and slices // s in (1, 2, 4, 8)]
 
 
+_SPLITS = {}     # (rows, T, dv, share, VALUE_SPLIT) -> split: the launch path asks on every call
+
+
 def split_for(rows: int, T: int, dv: int, share: int = 1) -> int:
+    """The value split for a pass (_split_for's rule), remembered per shape and VALUE_SPLIT setting."""
+    key = (rows, T, dv, share, VALUE_SPLIT)
+    s = _SPLITS.get(key)
+    if s is None:
+        s = _SPLITS[key] = _split_for(rows, T, dv, share)
+    return s
+
+
+def _split_for(rows: int, T: int, dv: int, share: int = 1) -> int:
     """VALUE_SPLIT's choice for `rows` head-rows (B x H) of value width dv, for a pass that gets 1 / share of the
     chip: "auto" takes the smallest valid split that gives at least 256 / share workgroups (one per CU), else the
     largest; an int setting is rounded down to a valid split.  "auto" leaves out the splits with 8 waves of columns
@@ -146,24 +159,58 @@ def _pack_args(pack):
     return (None, 0) if pack is None else (N.ptr(pack[0]), pack[1])
 
 
-def _prep(q, k, v, g, beta, l2norm: bool, q_scale: float, with_A: bool, pack=None, name=None):
-    """The per-chunk operands (row-major, tokens as rows): W, U, diag(e) K^, exp(G_last), diag(gamma) Q^, M, and A when
-    asked (the backward's per-chunk pass).  Per-chunk tensors are [B, H, NT, ...] ([1, H, NT, ...] for packed rows).
-    name: the launch's name for EVENTS (by default prep_bwd with A, else prep_fwd)."""
+def _on(dev):
+    """The device guard a launch needs: none when dev is already the current device (the common case, and the guard
+    costs host time on every call)."""
+    return contextlib.nullcontext() if dev.index == torch.cuda.current_device() else torch.cuda.device(dev)
+
+
+_LAYOUTS = {}    # scratch layouts by shape: (part offsets, total bytes)
+
+
+def _carve(dev, shape):
+    """One allocation for the per-chunk scratch of a call, `shape` = (Bc, H, NT, DK, DV, element size, prep, with_A,
+    states, grads) as _scratch_sizes takes it.  Returns {name: device address or None, "buf": the allocation}; every
+    part starts on a 256-byte boundary.  The kernels take raw addresses, so the parts need no tensor views."""
+    lay = _LAYOUTS.get(shape)
+    if lay is None:
+        offs, total = {}, 0
+        for name, n in _scratch_sizes(*shape).items():
+            offs[name] = total if n else None
+            total += (n + 255) & ~255
+        lay = _LAYOUTS[shape] = (offs, max(total, 1))
+    offs, total = lay
+    buf = torch.empty(total, device=dev, dtype=torch.uint8)
+    base = buf.data_ptr()
+    out = {name: (None if o is None else base + o) for name, o in offs.items()}
+    out["buf"] = buf
+    return out
+
+
+def _scratch_sizes(Bc, H, NT, DK, DV, es, prep: bool, with_A: bool, states: bool, grads: bool):
+    """Byte counts of the per-chunk tensors, all [Bc, H, NT, ...] row-major: prep's W, U, Ke, GL, Qg, M (and A); the
+    chunk states Sc (fp32) and Vn; the reverse pass's dSn (fp32) and dVn."""
+    n = Bc * H * NT
+    z = lambda on, b: b if on else 0
+    return dict(W=z(prep, n * CHUNK * DK * es), U=z(prep, n * CHUNK * DV * 4), Ke=z(prep, n * CHUNK * DK * es),
+                GL=z(prep, n * 4), Qg=z(prep, n * CHUNK * DK * es), M=z(prep, n * CHUNK * CHUNK * es),
+                A=z(prep and with_A, n * CHUNK * CHUNK * es), Sc=z(states, n * DK * DV * 4),
+                Vn=z(states, n * CHUNK * DV * es), dSn=z(grads, n * DK * DV * 4), dVn=z(grads, n * CHUNK * DV * es))
+
+
+def _as(x, dt):
+    """x in dtype dt, contiguous: x itself when it already is (skips two calls on the launch path)."""
+    return x if x.dtype == dt and x.is_contiguous() else x.to(dt).contiguous()
+
+
+def _prep(q, k, v, g, beta, l2norm: bool, q_scale: float, r, stream, pack=None, name="prep_fwd"):
+    """The per-chunk operands (row-major, tokens as rows) into the scratch r (addresses from _carve): W, U, diag(e) K^,
+    exp(G_last), diag(gamma) Q^, M, and A when r has it (the backward's per-chunk pass needs it).  Per-chunk tensors
+    are [B, H, NT, ...] ([1, H, NT, ...] for packed rows)."""
     B, T, H, Hk, DK, DV, NT = _dims(q, v, pack)
-    Bc = q.shape[0]
-    dev, dt = q.device, q.dtype
-    f32 = torch.float32
-    W = torch.empty(Bc, H, NT, CHUNK, DK, device=dev, dtype=dt)
-    r = dict(W=W, U=torch.empty(Bc, H, NT, CHUNK, DV, device=dev, dtype=f32), Ke=torch.empty_like(W),
-             GL=torch.empty(Bc, H, NT, device=dev, dtype=f32), Qg=torch.empty_like(W),
-             M=torch.empty(Bc, H, NT, CHUNK, CHUNK, device=dev, dtype=dt),
-             A=torch.empty(Bc, H, NT, CHUNK, CHUNK, device=dev, dtype=dt) if with_A else None)
     P = N.ptr
-    _launch(name or ("prep_bwd" if with_A else "prep_fwd"), "macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), P(r["W"]),
-            P(r["U"]), P(r["Ke"]), P(r["GL"]), P(r["Qg"]), P(r["M"]), P(r["A"]), B, T, H, Hk, DK, DV,
-            N.dtype_code(dt), int(l2norm), q_scale, *_pack_args(pack), N.stream_of(q))
-    return r
+    _launch(name, "macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), r["W"], r["U"], r["Ke"], r["GL"], r["Qg"], r["M"],
+            r["A"], B, T, H, Hk, DK, DV, N.dtype_code(q.dtype), int(l2norm), q_scale, *_pack_args(pack), stream)
 
 
 def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, pack=None, keep=False):
@@ -173,17 +220,14 @@ def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, 
     Bc = q.shape[0]
     dev, dt = q.device, q.dtype
     code, stream = N.dtype_code(dt), N.stream_of(q)
-    r = _prep(q, k, v, g, beta, l2norm, q_scale, keep, pack, "prep_fwd")
+    r = _carve(dev, (Bc, H, NT, DK, DV, q.element_size(), True, keep, keep, False))
+    _prep(q, k, v, g, beta, l2norm, q_scale, r, stream, pack, "prep_fwd")
     o = torch.empty(Bc, T, H, DV, device=dev, dtype=dt)
     sT = torch.empty(B, H, DK, DV, device=dev, dtype=torch.float32) if want_sT else None
-    if keep:
-        r["Sc"] = torch.empty(Bc, H, NT, DK, DV, device=dev, dtype=torch.float32)
-        r["Vn"] = torch.empty(Bc, H, NT, CHUNK, DV, device=dev, dtype=dt)
     split = split_for(B * H, T, DV)
     P = N.ptr
-    _launch("state_fwd_out", "macai_gdr_state_fwd", P(r["W"]), P(r["U"]), P(r["Ke"]), P(r["GL"]), P(r["Qg"]), P(r["M"]),
-            P(s0), P(o), P(sT), P(r.get("Sc")), P(r.get("Vn")), B, T, H, DK, DV, code, N.STORE_STATES if keep else 0,
-            split, *_pack_args(pack), stream)
+    _launch("state_fwd_out", "macai_gdr_state_fwd", r["W"], r["U"], r["Ke"], r["GL"], r["Qg"], r["M"], P(s0), P(o), P(sT),
+            r["Sc"], r["Vn"], B, T, H, DK, DV, code, N.STORE_STATES if keep else 0, split, *_pack_args(pack), stream)
     CALLS[f"fwd s{split}"] += 1
     return o, sT, (r if keep else None)
 
@@ -198,30 +242,29 @@ def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=
     dev, dt = q.device, q.dtype
     code, stream = N.dtype_code(dt), N.stream_of(q)
     f32 = torch.float32
-    if r is None:
-        r = _prep(q, k, v, g, beta, l2norm, q_scale, True, pack)
+    es = q.element_size()
+    kept = r is not None                 # the forward kept prep's operands and the chunk states: only the reverse
+    if kept:                             # pass is left
+        g2 = _carve(dev, (Bc, H, NT, DK, DV, es, False, False, False, True))
+    else:
+        r = g2 = _carve(dev, (Bc, H, NT, DK, DV, es, True, True, True, True))
+        _prep(q, k, v, g, beta, l2norm, q_scale, r, stream, pack, "prep_bwd")
     P = N.ptr
     pk = _pack_args(pack)
-    kept = "Sc" in r                     # the forward stored the chunk states: only the reverse pass is left
     split = split_for(B * H, T, DV, 2 if OVERLAP and not kept else 1)
-    Sc = r["Sc"] if kept else torch.empty(Bc, H, NT, DK, DV, device=dev, dtype=f32)
-    Vn = r["Vn"] if kept else torch.empty(Bc, H, NT, CHUNK, DV, device=dev, dtype=dt)
-    dSn = torch.empty(Bc, H, NT, DK, DV, device=dev, dtype=f32)
-    dVn = torch.empty_like(Vn)
+    Sc, Vn, dSn, dVn = r["Sc"], r["Vn"], g2["dSn"], g2["dVn"]
     ds0 = torch.empty(B, H, DK, DV, device=dev, dtype=f32)
     if kept:
-        _launch("state_bwd", "macai_gdr_state_bwd", P(r["Ke"]), P(r["Qg"]), P(r["W"]), P(r["M"]), P(r["GL"]), P(do),
-                P(dsT), P(dSn), P(dVn), P(ds0), B, T, H, DK, DV, code, split, *pk, stream)
+        _launch("state_bwd", "macai_gdr_state_bwd", r["Ke"], r["Qg"], r["W"], r["M"], r["GL"], P(do), P(dsT), dSn, dVn,
+                P(ds0), B, T, H, DK, DV, code, split, *pk, stream)
     elif OVERLAP:
-        _launch("state_pair", "macai_gdr_state_pair", P(r["W"]), P(r["U"]), P(r["Ke"]), P(r["Qg"]), P(r["M"]),
-                P(r["GL"]), P(s0), P(do), P(dsT), P(Sc), P(Vn), P(dSn), P(dVn), P(ds0), B, T, H, DK, DV, code, split,
-                *pk, stream)
+        _launch("state_pair", "macai_gdr_state_pair", r["W"], r["U"], r["Ke"], r["Qg"], r["M"], r["GL"], P(s0), P(do),
+                P(dsT), Sc, Vn, dSn, dVn, P(ds0), B, T, H, DK, DV, code, split, *pk, stream)
     else:
-        _launch("state_fwd_store", "macai_gdr_state_fwd", P(r["W"]), P(r["U"]), P(r["Ke"]), P(r["GL"]), None, None,
-                P(s0), None, None, P(Sc), P(Vn), B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, *pk,
-                stream)
-        _launch("state_bwd", "macai_gdr_state_bwd", P(r["Ke"]), P(r["Qg"]), P(r["W"]), P(r["M"]), P(r["GL"]), P(do),
-                P(dsT), P(dSn), P(dVn), P(ds0), B, T, H, DK, DV, code, split, *pk, stream)
+        _launch("state_fwd_store", "macai_gdr_state_fwd", r["W"], r["U"], r["Ke"], r["GL"], None, None, P(s0), None,
+                None, Sc, Vn, B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, *pk, stream)
+        _launch("state_bwd", "macai_gdr_state_bwd", r["Ke"], r["Qg"], r["W"], r["M"], r["GL"], P(do), P(dsT), dSn, dVn,
+                P(ds0), B, T, H, DK, DV, code, split, *pk, stream)
     CALLS[f"bwd s{split}"] += 1
     if Hk == H:
         dqh, dkh = torch.empty_like(q), torch.empty_like(k)
@@ -230,9 +273,8 @@ def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=
         dkh = torch.empty_like(dqh)
     dv = torch.empty_like(v)
     dg, dbeta = torch.empty_like(g), torch.empty_like(beta)
-    _launch("chunk_bwd", "macai_gdr_chunk_bwd", P(q), P(k), P(v), P(g), P(beta), P(do), P(r["A"]), P(Sc), P(dSn), P(Vn),
-            P(dVn), P(dqh), P(dkh), P(dv), P(dg), P(dbeta), B, T, H, Hk, DK, DV, code, int(l2norm), q_scale, *pk,
-            stream)
+    _launch("chunk_bwd", "macai_gdr_chunk_bwd", P(q), P(k), P(v), P(g), P(beta), P(do), r["A"], Sc, dSn, Vn, dVn,
+            P(dqh), P(dkh), P(dv), P(dg), P(dbeta), B, T, H, Hk, DK, DV, code, int(l2norm), q_scale, *pk, stream)
     if Hk == H:
         return dqh, dkh, dv, dg, dbeta, ds0
     dq, dk = torch.empty_like(q), torch.empty_like(k)
@@ -253,7 +295,7 @@ class GatedDeltaRule(torch.autograd.Function):
         _check(q, k, v, g, beta, s0)
         q, k, v, g, beta, s0 = (t.contiguous() for t in (q, k, v, g, beta, s0))
         keep = save and not RECOMPUTE_STATES
-        with torch.cuda.device(q.device):
+        with _on(q.device):
             o, sT, ctx.prep = _forward(q, k, v, g, beta, s0, False, 1.0, True, keep=keep)
         if save:
             ctx.save_for_backward(q, k, v, g, beta, s0)
@@ -262,9 +304,9 @@ class GatedDeltaRule(torch.autograd.Function):
     @staticmethod
     def backward(ctx, do, dsT):
         q, k, v, g, beta, s0 = ctx.saved_tensors
-        do = torch.zeros_like(v) if do is None else do.to(v.dtype).contiguous()
-        dsT = None if dsT is None else dsT.to(torch.float32).contiguous()
-        with torch.cuda.device(q.device):
+        do = torch.zeros_like(v) if do is None else _as(do, v.dtype)
+        dsT = None if dsT is None else _as(dsT, torch.float32)
+        with _on(q.device):
             dq, dk, dv, dg, dbeta, ds0 = _backward(q, k, v, g, beta, s0, do, dsT, False, 1.0, r=ctx.prep)
         return dq, dk, dv, dg, dbeta, ds0, None
 
@@ -279,7 +321,7 @@ class _DropIn(torch.autograd.Function):
     def forward(ctx, query, key, value, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, save: bool,
                 pack=None):
         keep = save and not RECOMPUTE_STATES
-        with torch.cuda.device(query.device):
+        with _on(query.device):
             o, sT, ctx.prep = _forward(query, key, value, g, beta, s0, l2norm, q_scale, want_sT, pack, keep)
         if save:
             ctx.save_for_backward(query, key, value, g, beta, s0)
@@ -293,9 +335,9 @@ class _DropIn(torch.autograd.Function):
     def backward(ctx, do, dsT=None):
         query, key, value, g, beta, s0 = ctx.saved_tensors
         l2norm, q_scale, has_s0 = ctx.cfg
-        do = torch.zeros_like(value) if do is None else do.to(value.dtype).contiguous()
-        dsT = None if dsT is None else dsT.to(torch.float32).contiguous()
-        with torch.cuda.device(query.device):
+        do = torch.zeros_like(value) if do is None else _as(do, value.dtype)
+        dsT = None if dsT is None else _as(dsT, torch.float32)
+        with _on(query.device):
             dq, dk, dv, dg, dbeta, ds0 = _backward(query, key, value, g, beta, s0, do, dsT, l2norm, q_scale, ctx.pack,
                                                    ctx.prep)
         return dq, dk, dv, dg, dbeta, (ds0 if has_s0 else None), None, None, None, None, None
@@ -321,16 +363,16 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size: int = 64, ini
     pack = None if cu is None else _pack(cu, query.shape[1], query.device)
     dtype = query.dtype
     cdt = torch.bfloat16 if dtype == torch.bfloat16 else torch.float32
-    q, k, v = (x.to(cdt).contiguous() for x in (query, key, value))
-    gf, bf = g.to(torch.float32).contiguous(), beta.to(torch.float32).contiguous()
-    s0 = None if initial_state is None else initial_state.to(torch.float32).contiguous()
+    q, k, v = _as(query, cdt), _as(key, cdt), _as(value, cdt)
+    gf, bf = _as(g, torch.float32), _as(beta, torch.float32)
+    s0 = None if initial_state is None else _as(initial_state, torch.float32)
     _check(q, k, v, gf, bf, s0, None if pack is None else pack[2])
     tensors = (q, k, v, gf, bf) + (() if s0 is None else (s0,))
     save = torch.is_grad_enabled() and any(t.requires_grad for t in tensors)
     res = _DropIn.apply(q, k, v, gf, bf, s0, bool(use_qk_l2norm_in_kernel), q.shape[-1] ** -0.5,
                         bool(output_final_state), save, pack)
     out, sT = (res, None) if not output_final_state else res
-    return out.to(dtype), sT
+    return (out if out.dtype == dtype else out.to(dtype)), sT
 
 
 def recurrent_gated_delta_rule(query, key, value, g, beta, initial_state=None, output_final_state: bool = False,
@@ -358,7 +400,7 @@ def recurrent_gated_delta_rule(query, key, value, g, beta, initial_state=None, o
     _check(q, k, v, gf, bf, s_in)
     o = torch.empty(B, 1, H, DV, device=q.device, dtype=cdt)
     s_out = torch.empty_like(s_in)
-    with torch.cuda.device(q.device):
+    with _on(q.device):
         N.call("macai_gdr_decode", N.ptr(q), N.ptr(k), N.ptr(v), N.ptr(gf), N.ptr(bf), N.ptr(s_in), N.ptr(o),
                N.ptr(s_out), B, H, Hk, DK, DV, N.dtype_code(cdt), int(bool(use_qk_l2norm_in_kernel)), DK ** -0.5,
                N.stream_of(q))
