@@ -50,11 +50,12 @@
 extern "C" {
 #endif
 
-#define MACAI_GDR_ABI_VERSION 8
+#define MACAI_GDR_ABI_VERSION 9
 
-/* dtype codes */
+/* dtype codes (the rule takes F32 and BF16; the producers also F16) */
 #define MACAI_GDR_F32 0
 #define MACAI_GDR_BF16 1
+#define MACAI_GDR_F16 2
 
 /* error codes */
 #define MACAI_GDR_OK 0
@@ -133,6 +134,42 @@ int macai_gdr_decode(const void* q, const void* k, const void* v, const float* g
  * (transformers modeling_qwen3_5.py:500-502; reference layer/_qwen3_5.py:155-157), which the grouped layout removes. */
 int macai_gdr_group_sum(const void* x, void* y, int64_t B, int64_t T, int64_t H, int64_t Hk, int64_t D, int32_t dtype,
                         void* stream);
+
+/* ---- the producers of the rule's inputs (the linear-attention layer's convolution path and gates) ----
+ *
+ * The convolution path: x [B, T, C] (the input projection's output, C = 2 KD + VD), w [C, 4] float32 taps;
+ * u[t, c] = sum_j w[c, j] x[t - 3 + j, c] (zero before the start, float32), y = u sigmoid(u) rounded once; q, k =
+ * the first two KD-channel blocks as [B, T, KD / DK * REP, DK] in x's dtype, each key head written REP times
+ * (REP = 1: key heads only, the layout the rule reads natively; REP = value heads / key heads: transformers' repeat),
+ * v = the last VD channels as [B, T, VD / DV, DV] in vdtype.  dtype, vdtype: F32, BF16 or F16.  Replaces the
+ * reference's conv_fwd kernel launch (layer/_conv.py:191-193; kernel 1-24, 47-82). */
+int macai_gdr_conv_fwd(const void* x, const float* w, void* q, void* k, void* v, int64_t B, int64_t T, int64_t C,
+                       int64_t KD, int64_t DK, int64_t REP, int64_t DV, int32_t dtype, int32_t vdtype, void* stream);
+
+/* Its backward: dx [B, T, C] in x's dtype from dq, dk (summed over the REP copies) and dv, u recomputed from x; with
+ * dwp (float32 [macai_gdr_conv_partials(B, T, C)] scratch) and dw (float32 [C, 4]) non-NULL, also the taps'
+ * gradient (partials a tile of time steps, then a fixed-order sum: deterministic).  Replaces conv_bwd and dw_sum
+ * (layer/_conv.py:221-231; kernel 84-130, 150-159). */
+int macai_gdr_conv_bwd(const void* x, const float* w, const void* dq, const void* dk, const void* dv, void* dx,
+                       float* dwp, float* dw, int64_t B, int64_t T, int64_t C, int64_t KD, int64_t DK, int64_t REP,
+                       int64_t DV, int32_t dtype, int32_t vdtype, void* stream);
+
+/* float32 elements of the conv backward's dw partials for a shape. */
+int64_t macai_gdr_conv_partials(int64_t B, int64_t T, int64_t C);
+
+/* The gates: beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias) (PyTorch's softplus threshold 20), both
+ * float32 [n] from b, a [n] in dtype (n = rows x H, head h = i % H) and A_log, dt_bias [H] float32.  Replaces the
+ * reference's gates_fwd (layer/_gates.py:91-93; kernel 22-39). */
+int macai_gdr_gates_fwd(const void* b, const void* a, const float* A_log, const float* dt_bias, float* beta, float* g,
+                        int64_t n, int64_t H, int32_t dtype, void* stream);
+
+/* Their backward: db = dbeta beta (1 - beta), da = dg (-exp(A_log)) sigmoid(a + dt_bias) (1 above the threshold), in
+ * dtype; with dA_log and ddt_bias (float32 [H]) non-NULL also the sums over the rows of dg g and dg (-exp(A_log))
+ * sigmoid(a + dt_bias) (one workgroup a head, fixed order).  Replaces gates_bwd and the reference's PyTorch
+ * reductions for trained gates (layer/_gates.py:100-118; kernel 41-55). */
+int macai_gdr_gates_bwd(const void* b, const void* a, const float* A_log, const float* dt_bias, const float* dbeta,
+                        const float* dg, void* db, void* da, float* dA_log, float* ddt_bias, int64_t n, int64_t H,
+                        int32_t dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -5,7 +5,7 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-SRC = os.path.join(HERE, "csrc", "gdr_kernels.hip")
+SRCS = [os.path.join(HERE, "csrc", f) for f in ("gdr_kernels.hip", "gdr_producers.hip")]
 OUT = os.path.join(HERE, "macai", "gated_delta", "libmacai_gdr.so")
 ARCH = os.environ.get("MACAI_GPU_ARCH", "gfx950")
 
@@ -15,7 +15,7 @@ def command(out=OUT):
             "-I", os.path.join(ROOT, "include"), "-I", os.path.join(HERE, "csrc"),
             # no packed fp32 VALU instructions: some of their forms have given wrong results on this hardware pool
             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-            SRC, "-o", out]
+            *SRCS, "-o", out]
 
 
 def build(verbose=True):

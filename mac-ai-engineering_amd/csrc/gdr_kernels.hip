@@ -25,6 +25,7 @@
 #include <string.h>
 #include <stdarg.h>
 
+#include "gdr_abi.h"
 #include "gdr_common.h"
 #include "gdr_stage.h"
 #include "gdr_lds.h"
@@ -2420,24 +2421,6 @@ __global__ void __launch_bounds__(256) group_sum_kernel(const T* x, T* y, int64_
   store4<T>(dst + 4, f4{acc[4], acc[5], acc[6], acc[7]});
 }
 
-static thread_local char g_err[512] = "";
-
-static int fail(int code, const char* fmt, ...) {
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(g_err, sizeof g_err, fmt, ap);
-  va_end(ap);
-  return code;
-}
-
-static int launched(const char* what) {
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(MACAI_GDR_ELAUNCH, "%s: HIP launch failed: %s", what, hipGetErrorString(e));
-  g_err[0] = 0;
-  return MACAI_GDR_OK;
-}
-
-static bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
 
 static int check_common(const char* what, int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV, int dtype) {
   if (B < 1 || T < 1 || H < 1) return fail(MACAI_GDR_EINVAL, "%s: B, T, H must be >= 1 (got %lld, %lld, %lld)", what,

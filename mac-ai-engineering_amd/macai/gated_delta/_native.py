@@ -11,10 +11,10 @@ import torch
 LIB_NAME = "libmacai_gdr.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
-F32, BF16 = 0, 1
+F32, BF16, F16 = 0, 1, 2
 OK, EINVAL, EUNSUP, ELAUNCH = 0, 1, 2, 3
 STORE_STATES, NO_OUTPUT = 1, 8
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _p, _i64, _i32, _f = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 # name -> argument types (the order of include/macai_gdr.h)
@@ -26,7 +26,13 @@ SIGNATURES = {
     "macai_gdr_chunk_bwd": [_p] * 16 + [_i64] * 6 + [_i32, _i32, _f, _p, _i64, _p],
     "macai_gdr_decode": [_p] * 8 + [_i64] * 5 + [_i32, _i32, _f, _p],
     "macai_gdr_group_sum": [_p] * 2 + [_i64] * 5 + [_i32, _p],
+    "macai_gdr_conv_fwd": [_p] * 5 + [_i64] * 7 + [_i32, _i32, _p],
+    "macai_gdr_conv_bwd": [_p] * 8 + [_i64] * 7 + [_i32, _i32, _p],
+    "macai_gdr_conv_partials": [_i64] * 3,
+    "macai_gdr_gates_fwd": [_p] * 6 + [_i64] * 2 + [_i32, _p],
+    "macai_gdr_gates_bwd": [_p] * 10 + [_i64] * 2 + [_i32, _p],
 }
+RESTYPES = {"macai_gdr_conv_partials": _i64}     # the rest return an int status
 
 _lib = None
 _fns = {}        # name -> the library's function object (a lookup per call costs host time on every launch)
@@ -50,7 +56,7 @@ def lib():
         L.macai_gdr_abi_version.argtypes = []
         for name, args in SIGNATURES.items():
             fn = getattr(L, name)
-            fn.restype = ctypes.c_int
+            fn.restype = RESTYPES.get(name, ctypes.c_int)
             fn.argtypes = args
         if L.macai_gdr_abi_version() != ABI_VERSION:
             raise RuntimeError(f"{LIB_PATH}: ABI version {L.macai_gdr_abi_version()}, expected {ABI_VERSION}")
@@ -62,12 +68,15 @@ def ptr(t):
     return None if t is None else t.data_ptr()
 
 
-def dtype_code(dt):
+def dtype_code(dt, f16=False):
+    """The dtype code of a torch dtype: float32 or bfloat16 (and float16 where the entry point takes it)."""
     if dt == torch.float32:
         return F32
     if dt == torch.bfloat16:
         return BF16
-    raise NotImplementedError(f"the HIP kernels take float32 or bfloat16, got {dt}")
+    if f16 and dt == torch.float16:
+        return F16
+    raise NotImplementedError(f"the HIP kernels take float32 or bfloat16{' or float16' if f16 else ''}, got {dt}")
 
 
 def stream_of(t):

@@ -16,4 +16,8 @@ Pinning (each function's checks live in tests/test_oracle.py):
   torch_chunk_gated_delta_rule -- restatement of transformers' reference (the error anchor of the parity bar);
                            pinned against the installed transformers function and against `recurrence`.
   decode_step           -- one token of the recurrence; pinned against `recurrence` with T = 1 and by hand.
+  producers.conv_qkv / producers.gates -- the layer's convolution path and gates that produce the rule's inputs
+                           (reference layer/_conv.py, layer/_gates.py); pinned in tests/test_oracle_producers.py
+                           against torch's conv1d (groups = channels) + silu, sigmoid and softplus (threshold 20), and
+                           the reference's softplus-threshold values.
 """

@@ -19,7 +19,7 @@ def _declared():
     """(name, number of parameters) of every function the header declares."""
     text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
     out = {}
-    for m in re.finditer(r"\b(?:int|const char\s*\*)\s+(macai_gdr_\w+)\s*\(([^)]*)\)\s*;", text):
+    for m in re.finditer(r"\b(?:int64_t|int|const char\s*\*)\s+(macai_gdr_\w+)\s*\(([^)]*)\)\s*;", text):
         params = [p for p in m.group(2).split(",") if p.strip() and p.strip() != "void"]
         out[m.group(1)] = len(params)
     return out
@@ -29,7 +29,8 @@ def test_library_exports_every_declared_symbol():
     decl = _declared()
     assert {"macai_gdr_prep", "macai_gdr_state_fwd", "macai_gdr_state_bwd", "macai_gdr_state_pair",
             "macai_gdr_chunk_bwd", "macai_gdr_decode", "macai_gdr_group_sum", "macai_gdr_last_error",
-            "macai_gdr_abi_version"} <= set(decl)
+            "macai_gdr_abi_version", "macai_gdr_conv_fwd", "macai_gdr_conv_bwd", "macai_gdr_conv_partials",
+            "macai_gdr_gates_fwd", "macai_gdr_gates_bwd"} <= set(decl)
     lib = N.lib()
     for name in decl:
         assert hasattr(lib, name), name
@@ -86,6 +87,26 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert gs(p, p, Hk=3) == N.EINVAL
     assert gs(p, p, D=12) == N.EUNSUP
     assert gs(p + 4, p) == N.EINVAL and b"aligned" in L.macai_gdr_last_error()
+
+
+def test_producer_abi_rejects_bad_arguments():
+    """The convolution path's and the gates' entry points check shapes, dtype codes and pointers before any launch."""
+    L = N.lib()
+    p = 1 << 20
+    conv = lambda *ptrs, C=6144, KD=2048, DK=128, REP=1, DV=128, dt=1, vdt=0, B=1, T=8: L.macai_gdr_conv_fwd(
+        *ptrs, B, T, C, KD, DK, REP, DV, dt, vdt, None)
+    assert conv(p, p, p, p, p, dt=5) == N.EUNSUP
+    assert conv(p, p, p, p, None) == N.EINVAL and b"null" in L.macai_gdr_last_error()
+    assert conv(p, p, p, p, p, C=6140) == N.EINVAL                 # not a multiple of 8
+    assert conv(p, p, p, p, p, DV=96) == N.EINVAL                  # value_dim not a multiple of the head width
+    assert conv(p, p, p, p, p, REP=3) == N.EINVAL and b"REP" in L.macai_gdr_last_error()
+    assert conv(p + 8, p, p, p, p) == N.EINVAL and b"aligned" in L.macai_gdr_last_error()
+    assert conv(p, p, p, p, p, T=0) == N.EINVAL
+    assert L.macai_gdr_conv_bwd(p, p, p, p, p, p, p, None, 1, 8, 6144, 2048, 128, 1, 128, 1, 0, None) == N.EINVAL
+    assert L.macai_gdr_conv_partials(2, 33, 6144) == 2 * 3 * 6144 * 4
+    assert L.macai_gdr_gates_fwd(p, p, p, p, p, p, 30, 16, 1, None) == N.EINVAL     # n not a multiple of H
+    assert L.macai_gdr_gates_fwd(p, p, p, p, p, p, 32, 16, 9, None) == N.EUNSUP
+    assert L.macai_gdr_gates_bwd(p, p, p, p, p, p, p, p, p, None, 32, 16, 1, None) == N.EINVAL
 
 
 def test_call_maps_codes_to_exceptions():
