@@ -198,6 +198,81 @@ def cpu_baseline(cfg, threads):
                       f"after 2 warm-ups ({dt * 1e3:.0f} ms/call)"}
 
 
+def bench_producers(cfg, reps=20):
+    """The rule's producers at the config's layer widths (key_dim = Hk DK, value_dim = Hv DV): the convolution path
+    forward (q, k at key heads, v in x's dtype: the layout the rule reads without copies), its backward (without and
+    with the taps' gradient), and the gates forward and backward.  Each entry point is launched `reps` times back to
+    back through the C ABI on preallocated buffers and timed with HIP events (the gates' kernels are shorter than a
+    launch's host cost, so their event time is a ceiling: rocprof gives their durations), beside the PyTorch path
+    (conv1d with groups = channels + silu + split) in the same dtype.  Algorithmic bytes: every input read once and
+    every output written once."""
+    from macai.gated_delta import _native as N
+    c = CONFIGS[cfg]
+    dev = torch.device("cuda", 0)
+    B, T, Hk, Hv, DK, DV = c["B"], c["T"], c["Hk"], c["Hv"], c["DK"], c["DV"]
+    kd, vd, rep = Hk * DK, Hv * DV, Hv // Hk
+    C = 2 * kd + vd
+    bf, f32 = torch.bfloat16, torch.float32
+    gen = torch.Generator(device=dev).manual_seed(5)
+    rnd = lambda *sh, dt=bf: torch.randn(*sh, device=dev, generator=gen).to(dt)
+    x, w4 = rnd(B, T, C), rnd(C, 4, dt=f32) * 0.3
+    q, k, v = rnd(B, T, Hk, DK), rnd(B, T, Hk, DK), rnd(B, T, Hv, DV)
+    dq, dk, dv, dx = rnd(B, T, Hk, DK), rnd(B, T, Hk, DK), rnd(B, T, Hv, DV), torch.empty(B, T, C, device=dev,
+                                                                                          dtype=bf)
+    dwp = torch.empty(N.lib().macai_gdr_conv_partials(B, T, C), device=dev, dtype=f32)
+    dw = torch.empty(C, 4, device=dev, dtype=f32)
+    b, a, A_log, dt = rnd(B, T, Hv), rnd(B, T, Hv), torch.zeros(Hv, device=dev), torch.zeros(Hv, device=dev)
+    beta, g, dbeta, dg = (rnd(B, T, Hv, dt=f32) for _ in range(4))
+    db, da, dA, ddt = rnd(B, T, Hv), rnd(B, T, Hv), torch.empty(Hv, device=dev), torch.empty(Hv, device=dev)
+    P, st, BF = N.ptr, N.stream_of(x), N.BF16
+    n = B * T * Hv
+    calls = {
+        "conv_fwd": (("macai_gdr_conv_fwd", P(x), P(w4), P(q), P(k), P(v), B, T, C, kd, DK, 1, DV, BF, BF, st),
+                     2 * B * T * C * 2),
+        "conv_bwd": (("macai_gdr_conv_bwd", P(x), P(w4), P(dq), P(dk), P(dv), P(dx), None, None, B, T, C, kd, DK, 1,
+                      DV, BF, BF, st), 3 * B * T * C * 2),
+        "conv_bwd_dw": (("macai_gdr_conv_bwd", P(x), P(w4), P(dq), P(dk), P(dv), P(dx), P(dwp), P(dw), B, T, C, kd,
+                         DK, 1, DV, BF, BF, st), 3 * B * T * C * 2 + 2 * dwp.numel() * 4),
+        "gates_fwd": (("macai_gdr_gates_fwd", P(b), P(a), P(A_log), P(dt), P(beta), P(g), n, Hv, BF, st),
+                      n * (2 * 2 + 2 * 4)),
+        "gates_bwd": (("macai_gdr_gates_bwd", P(b), P(a), P(A_log), P(dt), P(dbeta), P(dg), P(db), P(da), None, None,
+                       n, Hv, BF, st), n * (2 * 2 + 2 * 4 + 2 * 2)),
+    }
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e-3
+
+    wt = w4.to(bf).reshape(C, 1, 4)
+
+    def torch_conv():
+        y = torch.nn.functional.silu(torch.nn.functional.conv1d(x.transpose(1, 2), wt, padding=3, groups=C)[..., :T])
+        return torch.split(y.transpose(1, 2), [kd, kd, vd], dim=-1)
+
+    res = {}
+    for name, (args, nbytes) in calls.items():
+        t = timed(lambda: N.call(*args))
+        res[name] = {"us": round(t * 1e6, 2), "GB/s": round(nbytes / t / 1e9, 1),
+                     "hbm_frac": round(nbytes / t / HBM_PEAK, 4), "bytes": nbytes}
+    res["conv_fwd"]["torch_path_us"] = round(timed(torch_conv) * 1e6, 2)
+    line = {"metric": "gated-delta producers: conv+SiLU path and gates, GB/s of algorithmic bytes", "unit": "GB/s",
+            "value": res["conv_fwd"]["GB/s"], "n_gpus": 1, "higher_is_better": True, "dtype": "bf16",
+            "data": "synthetic", "config": {"workload": f"layer producers at BASELINE config {cfg} widths", "B": B,
+                                           "T": T, "C": C, "key_dim": kd, "value_dim": vd,
+                                           "layout": "q, k at key heads, bf16 v"},
+            "roofline": {"kernel": "conv_fwd", "bound": "hbm", "achieved": res["conv_fwd"]["GB/s"],
+                         "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": res["conv_fwd"]["hbm_frac"]},
+            "kernels": res}
+    print(json.dumps(line))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -216,6 +291,8 @@ def main():
     ap.add_argument("--packed", choices=["uniform", "ragged"],
                     help="run the batch as one packed row (cu_seqlens): B sequences of T tokens, or seeded ragged "
                          "lengths with the same total")
+    ap.add_argument("--producers", action="store_true",
+                    help="time the rule's producers (the convolution path and the gates) instead of the rule")
     ap.add_argument("--no-alone", action="store_true",
                     help="skip timing each pass alone, so a kernel trace of the run holds the step's launches only")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -225,6 +302,9 @@ def main():
         print("bench.py measures one GPU: the gated delta rule has no cross-GPU step in this build "
               "(head/batch sharding needs no collective); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.producers:
+        bench_producers(args.config)
+        return
     from macai.gated_delta import chunk_gated_delta_rule
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)

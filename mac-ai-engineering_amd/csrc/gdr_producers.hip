@@ -5,9 +5,9 @@
 //   float32), y = u sigmoid(u) rounded once, split into q, k (key_dim channels each) and v (value_dim channels);
 //   gates: beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias) (softplus's threshold 20), both float32.
 //
-// Both are streaming element-wise work bound by HBM: a thread owns 8 adjacent channels (16-byte accesses for 2-byte
-// types) and walks a tile of time steps with the convolution window in registers; no LDS, no barriers, one writer an
-// element.  The backward recomputes u from x (nothing else is kept) and gathers dx with one writer an element; the
+// Both are streaming element-wise work bound by HBM: a thread owns 4 adjacent channels and walks a tile of time steps
+// with the convolution window in registers, issuing a group of steps' loads at once; no LDS, no barriers, one writer
+// an element.  The backward recomputes u from x (nothing else is kept) and gathers dx with one writer an element; the
 // weight's gradient, when it trains, goes through float32 partial sums a tile and a fixed-order second pass.
 #include <hip/hip_runtime.h>
 
@@ -18,48 +18,49 @@ namespace gdr {
 
 typedef _Float16 f16;
 
-// 8 consecutive elements <-> float
-__device__ __forceinline__ void ld8(const float* p, float (&x)[8]) {
-  const f4 a = *reinterpret_cast<const f4*>(p), b = *reinterpret_cast<const f4*>(p + 4);
+// N = 4 or 8 consecutive elements <-> float (one 8- or 16-byte access for 2-byte types)
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+template <typename T, int N> struct VecOf;
+template <> struct VecOf<bf16, 4> { typedef bf16x4 type; };
+template <> struct VecOf<bf16, 8> { typedef bf16x8 type; };
+template <> struct VecOf<f16, 4> { typedef f16x4 type; };
+template <> struct VecOf<f16, 8> { typedef f16x8 type; };
+template <int N>
+__device__ __forceinline__ void ldn(const float* p, float (&x)[N]) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    x[i] = a[i];
-    x[i + 4] = b[i];
+  for (int h = 0; h < N / 4; ++h) {
+    const f4 a = *reinterpret_cast<const f4*>(p + 4 * h);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[4 * h + i] = a[i];
   }
 }
-__device__ __forceinline__ void ld8(const bf16* p, float (&x)[8]) {
-  const bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
+template <int N, typename T>
+__device__ __forceinline__ void ldn(const T* p, float (&x)[N]) {
+  const typename VecOf<T, N>::type v = *reinterpret_cast<const typename VecOf<T, N>::type*>(p);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) x[i] = (float)v[i];
+  for (int i = 0; i < N; ++i) x[i] = (float)v[i];
 }
-typedef f16 f16x8 __attribute__((ext_vector_type(8)));
-__device__ __forceinline__ void ld8(const f16* p, float (&x)[8]) {
-  const f16x8 v = *reinterpret_cast<const f16x8*>(p);
+template <int N>
+__device__ __forceinline__ void stn(float* p, const float (&x)[N]) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) x[i] = (float)v[i];
+  for (int h = 0; h < N / 4; ++h)
+    *reinterpret_cast<f4*>(p + 4 * h) = f4{x[4 * h], x[4 * h + 1], x[4 * h + 2], x[4 * h + 3]};
 }
-__device__ __forceinline__ void st8(float* p, const float (&x)[8]) {
-  *reinterpret_cast<f4*>(p) = f4{x[0], x[1], x[2], x[3]};
-  *reinterpret_cast<f4*>(p + 4) = f4{x[4], x[5], x[6], x[7]};
-}
-__device__ __forceinline__ void st8(bf16* p, const float (&x)[8]) {
-  bf16x8 v;
+template <int N, typename T>
+__device__ __forceinline__ void stn(T* p, const float (&x)[N]) {
+  typename VecOf<T, N>::type v;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = (bf16)x[i];
-  *reinterpret_cast<bf16x8*>(p) = v;
-}
-__device__ __forceinline__ void st8(f16* p, const float (&x)[8]) {
-  f16x8 v;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = (f16)x[i];
-  *reinterpret_cast<f16x8*>(p) = v;
+  for (int i = 0; i < N; ++i) v[i] = (T)x[i];
+  *reinterpret_cast<typename VecOf<T, N>::type*>(p) = v;
 }
 template <typename T> __device__ __forceinline__ float ld1(const T* p) { return (float)*p; }
 template <typename T> __device__ __forceinline__ void st1(T* p, float x) { *p = (T)x; }
 
 constexpr int CONV_K = 4;        // taps
-constexpr int CONV_CH = 8;       // channels a thread
+constexpr int CONV_CH = 4;       // channels a thread (8-byte accesses for 2-byte types)
 constexpr int CONV_GROUP = 256;  // threads a workgroup (along the channels)
+constexpr int CONV_U = 8;        // time steps whose loads a thread issues together (memory-level parallelism)
 
 struct ConvArgs {
   const void* x;                 // [B, T, C] T
@@ -98,14 +99,38 @@ __device__ __forceinline__ void load_taps(const float* w, int c, float (&tap)[CO
   }
 }
 
-// u = w0 x[t-3] + w1 x[t-2] + w2 x[t-1] + w3 x[t], in the reference's order (layer/_conv.py:73), summed in double
-// and rounded once: the kernel is bound by HBM, and in float32 the four roundings of the sum would set the output's
-// error (about 1 ulp of max |u| for an fp32 conv)
+// u = w0 x[t-3] + w1 x[t-2] + w2 x[t-1] + w3 x[t], in the reference's order (layer/_conv.py:73).  With float32
+// inputs (PRECISE) the sum is formed in double and rounded once, and sigmoid divides exactly: there the four roundings
+// of a float sum would set the outputs' error (about 1 ulp of max |u|).  With 2-byte inputs the outputs' own rounding
+// dominates, so the sum stays in float and exp / division take the fast forms (the work is then bound by HBM).
+template <bool PRECISE>
 __device__ __forceinline__ float conv_u(const float (&tap)[CONV_K][CONV_CH], int i, float xm3, float xm2, float xm1,
                                         float xt) {
-  return (float)fma((double)tap[3][i], (double)xt,
-                    fma((double)tap[2][i], (double)xm1, fma((double)tap[1][i], (double)xm2,
-                                                            (double)tap[0][i] * (double)xm3)));
+  if constexpr (PRECISE)
+    return (float)fma((double)tap[3][i], (double)xt,
+                      fma((double)tap[2][i], (double)xm1, fma((double)tap[1][i], (double)xm2,
+                                                              (double)tap[0][i] * (double)xm3)));
+  else
+    return fmaf(tap[3][i], xt, fmaf(tap[2][i], xm1, fmaf(tap[1][i], xm2, tap[0][i] * xm3)));
+}
+// w0 d0 + (w1 d1 + (w2 d2 + w3 d3)), with the same precision rule
+template <bool PRECISE>
+__device__ __forceinline__ float taps4(float w0, float d0, float w1, float d1, float w2, float d2, float w3, float d3) {
+  if constexpr (PRECISE)
+    return (float)fma((double)w0, (double)d0, fma((double)w1, (double)d1, fma((double)w2, (double)d2,
+                                                                            (double)w3 * (double)d3)));
+  else
+    return fmaf(w0, d0, fmaf(w1, d1, fmaf(w2, d2, w3 * d3)));
+}
+template <bool PRECISE>
+__device__ __forceinline__ float silu_of(float u) {
+  if constexpr (PRECISE) return u / (1.0f + expf(-u));
+  else return __fdividef(u, 1.0f + __expf(-u));
+}
+template <bool PRECISE>
+__device__ __forceinline__ float sigmoid_of(float u) {
+  if constexpr (PRECISE) return 1.0f / (1.0f + expf(-u));
+  else return __fdividef(1.0f, 1.0f + __expf(-u));
 }
 
 template <typename T, typename TV>
@@ -117,36 +142,45 @@ __global__ void __launch_bounds__(CONV_GROUP) conv_fwd_kernel(ConvArgs a) {
   load_taps(a.w, c, tap);
   const T* xb = (const T*)a.x + (size_t)b * a.T * a.C + c;
   float xm3[CONV_CH] = {}, xm2[CONV_CH] = {}, xm1[CONV_CH] = {};
-  if (t0 >= 3) ld8(xb + (size_t)(t0 - 3) * a.C, xm3);
-  if (t0 >= 2) ld8(xb + (size_t)(t0 - 2) * a.C, xm2);
-  if (t0 >= 1) ld8(xb + (size_t)(t0 - 1) * a.C, xm1);
+  if (t0 >= 3) ldn<CONV_CH>(xb + (size_t)(t0 - 3) * a.C, xm3);
+  if (t0 >= 2) ldn<CONV_CH>(xb + (size_t)(t0 - 2) * a.C, xm2);
+  if (t0 >= 1) ldn<CONV_CH>(xb + (size_t)(t0 - 1) * a.C, xm1);
   const ConvMap m(a, c);
   const int te = t0 + a.L < a.T ? t0 + a.L : a.T;
-  for (int t = t0; t < te; ++t) {
-    float xt[CONV_CH], y[CONV_CH];
-    ld8(xb + (size_t)t * a.C, xt);
+  for (int tb = t0; tb < te; tb += CONV_U) {
+    float xs[CONV_U][CONV_CH];            // the group's inputs, all loads in flight before the first is used
 #pragma unroll
-    for (int i = 0; i < CONV_CH; ++i) {
-      const float u = conv_u(tap, i, xm3[i], xm2[i], xm1[i], xt[i]);
-      y[i] = u / (1.0f + expf(-u));
-      xm3[i] = xm2[i];
-      xm2[i] = xm1[i];
-      xm1[i] = xt[i];
-    }
-    const size_t bt = (size_t)b * a.T + t;
-    if (m.isv) {
-      st8((TV*)a.v + bt * m.row + m.col, y);
-    } else {
-      T* dst = (T*)(c >= a.KD ? a.k : a.q) + bt * m.row + m.col;
-      for (int r = 0; r < a.REP; ++r) st8(dst + (size_t)r * a.DK, y);
+    for (int s = 0; s < CONV_U; ++s)
+      if (tb + s < te) ldn<CONV_CH>(xb + (size_t)(tb + s) * a.C, xs[s]);
+#pragma unroll
+    for (int s = 0; s < CONV_U; ++s) {
+      if (tb + s >= te) break;
+      const int t = tb + s;
+      float y[CONV_CH];
+#pragma unroll
+      for (int i = 0; i < CONV_CH; ++i) {
+        const float u = conv_u<sizeof(T) == 4>(tap, i, xm3[i], xm2[i], xm1[i], xs[s][i]);
+        y[i] = silu_of<sizeof(T) == 4>(u);
+        xm3[i] = xm2[i];
+        xm2[i] = xm1[i];
+        xm1[i] = xs[s][i];
+      }
+      const size_t bt = (size_t)b * a.T + t;
+      if (m.isv) {
+        stn<CONV_CH>((TV*)a.v + bt * m.row + m.col, y);
+      } else {
+        T* dst = (T*)(c >= a.KD ? a.k : a.q) + bt * m.row + m.col;
+        for (int r = 0; r < a.REP; ++r) stn<CONV_CH>(dst + (size_t)r * a.DK, y);
+      }
     }
   }
 }
 
 // dx[t] = sum_j w_j du[t + 3 - j] with du = dy sigmoid(u) (1 + u (1 - sigmoid(u))) (0 past the end; dy of q and k
 // summed over the REP copies in copy order); dw partials a tile: sum over its t of du[t] x[t - 3 + j].
-template <typename T, typename TV>
+template <typename T, typename TV, bool DW>
 __global__ void __launch_bounds__(CONV_GROUP) conv_bwd_kernel(ConvArgs a) {
+  constexpr int U = 4;                    // time steps whose loads are issued together
   const int c = (blockIdx.x * CONV_GROUP + threadIdx.x) * CONV_CH;
   if (c >= a.C) return;
   const int t0 = blockIdx.y * a.L, b = blockIdx.z;
@@ -155,55 +189,72 @@ __global__ void __launch_bounds__(CONV_GROUP) conv_bwd_kernel(ConvArgs a) {
   const T* xb = (const T*)a.x + (size_t)b * a.T * a.C + c;
   T* dxb = (T*)a.dx + (size_t)b * a.T * a.C + c;
   float xm3[CONV_CH] = {}, xm2[CONV_CH] = {}, xm1[CONV_CH] = {};
-  if (t0 >= 3) ld8(xb + (size_t)(t0 - 3) * a.C, xm3);
-  if (t0 >= 2) ld8(xb + (size_t)(t0 - 2) * a.C, xm2);
-  if (t0 >= 1) ld8(xb + (size_t)(t0 - 1) * a.C, xm1);
+  if (t0 >= 3) ldn<CONV_CH>(xb + (size_t)(t0 - 3) * a.C, xm3);
+  if (t0 >= 2) ldn<CONV_CH>(xb + (size_t)(t0 - 2) * a.C, xm2);
+  if (t0 >= 1) ldn<CONV_CH>(xb + (size_t)(t0 - 1) * a.C, xm1);
   float dm1[CONV_CH] = {}, dm2[CONV_CH] = {}, dm3[CONV_CH] = {};   // du[t - 1], du[t - 2], du[t - 3]
-  double acc[CONV_K][CONV_CH] = {};                                 // dw partials, in double (rounded once)
+  double acc[DW ? CONV_K : 1][CONV_CH] = {};                       // dw partials, in double (rounded once)
   const ConvMap m(a, c);
   const int tl = t0 + a.L < a.T ? t0 + a.L : a.T;                 // this tile's outputs: [t0, tl)
-  for (int t = t0; t < tl + 3; ++t) {
+  const int tw = tl + 3 < a.T ? tl + 3 : a.T;                     // the inputs the walk reads: [t0, tw)
+  for (int tb = t0; tb < tl + 3; tb += U) {
+    // the group's inputs and upstream gradients, all loads in flight before the first is used
+    float xs[U][CONV_CH], gs[U][CONV_CH];
+#pragma unroll
+    for (int s = 0; s < U; ++s) {
+      if (tb + s < tw) {
+        const size_t bt = (size_t)b * a.T + tb + s;
+        ldn<CONV_CH>(xb + (size_t)(tb + s) * a.C, xs[s]);
+        if (m.isv) ldn<CONV_CH>((const TV*)a.dv + bt * m.row + m.col, gs[s]);
+        else ldn<CONV_CH>((const T*)(c >= a.KD ? a.dk : a.dq) + bt * m.row + m.col, gs[s]);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < U; ++s) {
+    const int t = tb + s;
+    if (t >= tl + 3) break;
     float du[CONV_CH] = {}, xt[CONV_CH] = {};
     if (t < a.T) {
-      ld8(xb + (size_t)t * a.C, xt);
       const size_t bt = (size_t)b * a.T + t;
       float gy[CONV_CH];
-      if (m.isv) {
-        ld8((const TV*)a.dv + bt * m.row + m.col, gy);
-      } else {
+#pragma unroll
+      for (int i = 0; i < CONV_CH; ++i) {
+        xt[i] = xs[s][i];
+        gy[i] = gs[s][i];
+      }
+      if (!m.isv) {                        // the other copies of a repeated key head, summed in copy order
         const T* src = (const T*)(c >= a.KD ? a.dk : a.dq) + bt * m.row + m.col;
-        ld8(src, gy);
         for (int r = 1; r < a.REP; ++r) {
           float g2[CONV_CH];
-          ld8(src + (size_t)r * a.DK, g2);
+          ldn<CONV_CH>(src + (size_t)r * a.DK, g2);
 #pragma unroll
           for (int i = 0; i < CONV_CH; ++i) gy[i] += g2[i];
         }
       }
 #pragma unroll
       for (int i = 0; i < CONV_CH; ++i) {
-        const float u = conv_u(tap, i, xm3[i], xm2[i], xm1[i], xt[i]);
-        const float s = 1.0f / (1.0f + expf(-u));
+        const float u = conv_u<sizeof(T) == 4>(tap, i, xm3[i], xm2[i], xm1[i], xt[i]);
+        const float s = sigmoid_of<sizeof(T) == 4>(u);
         du[i] = gy[i] * s * (1.0f + u * (1.0f - s));
       }
-      if (a.dwp && t < tl) {
+      if constexpr (DW) {
+        if (t < tl) {
 #pragma unroll
-        for (int i = 0; i < CONV_CH; ++i) {
-          acc[0][i] = fma((double)du[i], (double)xm3[i], acc[0][i]);
-          acc[1][i] = fma((double)du[i], (double)xm2[i], acc[1][i]);
-          acc[2][i] = fma((double)du[i], (double)xm1[i], acc[2][i]);
-          acc[3][i] = fma((double)du[i], (double)xt[i], acc[3][i]);
+          for (int i = 0; i < CONV_CH; ++i) {
+            acc[0][i] = fma((double)du[i], (double)xm3[i], acc[0][i]);
+            acc[1][i] = fma((double)du[i], (double)xm2[i], acc[1][i]);
+            acc[2][i] = fma((double)du[i], (double)xm1[i], acc[2][i]);
+            acc[3][i] = fma((double)du[i], (double)xt[i], acc[3][i]);
+          }
         }
       }
     }
     if (t >= t0 + 3) {
       float dx[CONV_CH];
 #pragma unroll
-      for (int i = 0; i < CONV_CH; ++i)        // in double, rounded once (as u)
-        dx[i] = (float)fma((double)tap[0][i], (double)du[i],
-                           fma((double)tap[1][i], (double)dm1[i],
-                               fma((double)tap[2][i], (double)dm2[i], (double)tap[3][i] * (double)dm3[i])));
-      st8(dxb + (size_t)(t - 3) * a.C, dx);
+      for (int i = 0; i < CONV_CH; ++i)        // rounded once for float32 inputs (as u)
+        dx[i] = taps4<sizeof(T) == 4>(tap[0][i], du[i], tap[1][i], dm1[i], tap[2][i], dm2[i], tap[3][i], dm3[i]);
+      stn<CONV_CH>(dxb + (size_t)(t - 3) * a.C, dx);
     }
 #pragma unroll
     for (int i = 0; i < CONV_CH; ++i) {
@@ -214,8 +265,9 @@ __global__ void __launch_bounds__(CONV_GROUP) conv_bwd_kernel(ConvArgs a) {
       dm2[i] = dm1[i];
       dm1[i] = du[i];
     }
+    }
   }
-  if (a.dwp) {
+  if constexpr (DW) {
     float* p = a.dwp + ((size_t)(b * a.ntiles + blockIdx.y) * a.C + c) * CONV_K;
 #pragma unroll
     for (int i = 0; i < CONV_CH; ++i)
@@ -374,8 +426,13 @@ int macai_gdr_conv_bwd(const void* x, const float* w, const void* dq, const void
              (int)REP, CONV_TILE, ntiles};
   const dim3 grid((unsigned)((C / CONV_CH + CONV_GROUP - 1) / CONV_GROUP), (unsigned)ntiles, (unsigned)B);
   hipStream_t st = (hipStream_t)stream;
-  DISPATCH_PT(dtype, DISPATCH_PV(vdtype, hipLaunchKernelGGL((conv_bwd_kernel<PT, PV>), grid, dim3(CONV_GROUP), 0,
-                                                            st, a)))
+  if (dwp) {
+    DISPATCH_PT(dtype, DISPATCH_PV(vdtype, hipLaunchKernelGGL((conv_bwd_kernel<PT, PV, true>), grid, dim3(CONV_GROUP),
+                                                              0, st, a)))
+  } else {
+    DISPATCH_PT(dtype, DISPATCH_PV(vdtype, hipLaunchKernelGGL((conv_bwd_kernel<PT, PV, false>), grid,
+                                                              dim3(CONV_GROUP), 0, st, a)))
+  }
   if (int rc = launched(what)) return rc;
   if (dw) {
     const int n = (int)(C * CONV_K);
