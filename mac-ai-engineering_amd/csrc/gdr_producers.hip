@@ -281,7 +281,15 @@ __global__ void __launch_bounds__(256) sum_rows_kernel(const float* p, float* ou
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
   double s = 0.0;
-  for (int r = 0; r < P; ++r) s += (double)p[(size_t)r * n + i];
+  int r = 0;
+  for (; r + 8 <= P; r += 8) {           // eight rows' loads in flight, added in row order
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = p[(size_t)(r + k) * n + i];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s += (double)v[k];
+  }
+  for (; r < P; ++r) s += (double)p[(size_t)r * n + i];
   out[i] = (float)s;
 }
 
