@@ -33,8 +33,9 @@ PUBLISHED = 401.1e3        # reference's own fwd+bwd tokens/s at this config (M3
 C = 64
 # HBM bytes per launch of the training step at config 1 from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
 # (profiles/gated_delta_config1.md), FETCH_SIZE scaled by 2.000 and WRITE_SIZE by 1.000 (the factors a plain 256 MiB
-# device copy gives); prep with A, as the training forward runs it
-TRAFFIC = {1: {"chunk_bwd": 297.1e6, "state_pair": 312.2e6, "state_fwd_out": 109.3e6, "prep_fwd": 151.8e6}}
+# device copy gives); the training step as it runs by default: prep with A, the forward state pass storing S_c and Vn,
+# the reverse pass alone
+TRAFFIC = {1: {"chunk_bwd": 296.0e6, "state_bwd": 163.8e6, "state_fwd_out": 193.1e6, "prep_fwd": 151.8e6}}
 
 CONFIGS = {
     1: dict(B=4, T=1024, Hk=16, Hv=16, DK=128, DV=128, s0=False),
