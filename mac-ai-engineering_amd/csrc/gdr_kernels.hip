@@ -1797,30 +1797,36 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   MT* const tdV = tiles1 + 2 * GV::ELEMS;
   const int cb = w & 3, hh = w >> 2;       // [C x C] column block and row half
 
-  // ---- 0: global reads in two groups.  Group 1 is what the state products of B consume: the chunk states (into
-  // registers) and the dO, Vn, dVn tiles.  Group 2 -- the v fragments and the q, k, A tiles -- lands while those
-  // products run.  Every read below is unconditional (rows past the end re-read the last row and are masked later) and
-  // the tile copies are branch-free with a fixed count per wave, so after group 1 each wave has exactly N2 loads
-  // outstanding once group 1 has retired (loads retire in issue order).  Ragged chunks wait for everything.
+  // ---- 0: global reads in two groups.  Group 1 is what the state products of B consume: the dO, Vn, dVn tiles and
+  // the chunk states (into registers), issued in that order.  Loads retire in issue order, so once at most the state
+  // loads are outstanding the tiles have landed: B starts then, and each value block's states are waited for at their
+  // first use, so the tail of group 1 (the states are 128 of its 176 KiB) overlaps the first stages.  Group 2 -- the v
+  // fragments and the q, k, A tiles -- lands while B runs.  Every read is unconditional (rows past the end re-read the
+  // last row and are masked later).
   float gv, bv;                            // this lane's g and beta (used by wave 0)
   {
     const size_t o = s_base + (size_t)(t0 + l < T ? t0 + l : T - 1) * H;
     gv = a.g[o];
     bv = a.beta[o];
   }
+  GV::template dma_exact<NW>(tO, dO + (size_t)t0 * v_pitch, v_pitch, w, nrows);
+  GV::template dma_exact<NW>(tVn, Vnc, DV, w);
+  GV::template dma_exact<NW>(tdV, dVc, DV, w);
+  __builtin_amdgcn_sched_barrier(0);      // the state loads stay behind the copies (the partial wait below counts on it)
   Frag<float> s32[DV / 32];               // S_c rows of key block w (A operand, k = value features)
   Frag<float> sD[DV / 32];                // dS_{c+1} rows of key block w
+  constexpr int NSTATE = 4 * (DV / 32);   // state loads a wave issues: two 16-byte loads a fragment
   if (NBD == NW || w < NBD) {
 #pragma unroll
     for (int kb = 0; kb < DV / 32; ++kb) {
       s32[kb] = frag_k_f32(Scc, DV, 16 * w, 32 * kb);
       sD[kb] = frag_k_f32(dSc, DV, 16 * w, 32 * kb);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<NSTATE>();                  // g, beta and the tiles have landed; the states may still be in flight
+  } else {
+    wait_dma();
   }
-  GV::template dma_exact<NW>(tO, dO + (size_t)t0 * v_pitch, v_pitch, w, nrows);
-  GV::template dma_exact<NW>(tVn, Vnc, DV, w);
-  GV::template dma_exact<NW>(tdV, dVc, DV, w);
-  wait_dma();                              // group 1 (and g, beta) has landed
   // Group 2 -- the v fragments and the q, k, A tile units -- goes through registers. Its loads are spread over the
   // state products' stages below: an issue stalls while the memory system is saturated, so issuing them all here
   // would hold the products back. The tile units are written to LDS after the products.
@@ -1843,20 +1849,18 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
     }
   };
   if (w == 0) chunk_scalars_from(cs, t0 + l < T ? gv : 0.f, t0 + l < T ? bv : 0.f, t0, T);
-  // the chunk states in their MFMA forms at once (S_c in bf16; dS_{c+1} as hi + lo bf16: the e k . (Vn dS^T) terms of
-  // dg sum 64 rows of it), and the last-row dg term <S_c, dS_{c+1}> from the fp32 values
+  // the chunk states in their MFMA forms, value block by value block at its first stage (S_c in bf16; dS_{c+1} as
+  // hi + lo bf16: the e k . (Vn dS^T) terms of dg sum 64 rows of it), and the last-row dg term <S_c, dS_{c+1}> from
+  // the fp32 values, in value-block order
   Frag<MT> fS[DV / 32], dHi[DV / 32], dLo[DV / 32];
   float sds = 0.f;
-  if (NBD == NW || w < NBD) {
+  auto states = [&](int kb) {
+    fS[kb] = cvt<MT>(s32[kb]);
+    frag_split<MT>(sD[kb], dHi[kb], dLo[kb]);
 #pragma unroll
-    for (int kb = 0; kb < DV / 32; ++kb) {
-      fS[kb] = cvt<MT>(s32[kb]);
-      frag_split<MT>(sD[kb], dHi[kb], dLo[kb]);
-#pragma unroll
-      for (int r = 0; r < 8; ++r) sds = fmaf(s32[kb].v[r], sD[kb].v[r], sds);
-    }
-  }
-  lds_barrier();                         // group 1 and the chunk scalars visible
+    for (int r = 0; r < 8; ++r) sds = fmaf(s32[kb].v[r], sD[kb].v[r], sds);
+  };
+  lds_barrier();                         // the group-1 tiles and the chunk scalars visible
   if (nrows < C) {                         // rows past the end: zeros in dO
     constexpr int UV = VP / 8;
     const int nz = C - nrows;
@@ -1888,6 +1892,7 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
     load(0, st[0]);
 #pragma unroll
     for (int sg = 0; sg < NS; ++sg) {
+      if ((sg & 1) == 0) states(sg >> 1);
 #pragma unroll
       for (int p = 0; p < PER; ++p) issue_g2(PER * sg + p);
       if (sg + 1 < NS) load(sg + 1, st[(sg + 1) & 1]);
