@@ -104,10 +104,18 @@ struct ChunkBwdArgs {
 // Token tensors are then [1, T, ...] and per-chunk tensors [1, H, NT, ...]; B counts sequences (the state passes run
 // B x H head-rows, each over its sequence's chunks; states are [B, H, DK, DV]).  Without it, chunk c of batch row b
 // spans tokens 64 c .. min(64 c + 64, T) of that row.
+// A read, through the scalar cache, of memory that no kernel here writes, at a workgroup-uniform address.  Its wait is
+// on the LDS / scalar counter, so it never waits for the workgroup's outstanding global stores or copies.
+template <typename T>
+__device__ __forceinline__ T ld_const(const T* p, size_t i) {
+  return ((const __attribute__((address_space(4))) T*)p)[i];
+}
+// (SCALAR: the table through the scalar cache, for a wave whose waits must not cover its copies in flight.)
+template <bool SCALAR = false>
 __device__ __forceinline__ void chunk_span(const int* pack, int NT, int c, int T, int& t0, int& tend) {
   if (pack) {
-    t0 = pack[c];
-    tend = pack[NT + c];
+    t0 = SCALAR ? ld_const(pack, c) : pack[c];
+    tend = SCALAR ? ld_const(pack, NT + c) : pack[NT + c];
   } else {
     t0 = c * C;
     tend = T;
@@ -636,6 +644,42 @@ struct Buffers {
   static constexpr int N = (2 * STAGE_BYTES + EXTRA_BYTES <= LDS_BYTES) ? 2 : 1;
 };
 
+// The L2 prefetch of a sequential pass's loader wave.  The loader copies chunk c + 1 into LDS while chunk c computes;
+// under a training step's traffic that copy's HBM latency exceeds a chunk's compute, so the loader also touches the
+// chunk after it a period ahead: one dword a 128-byte line, copied into an LDS sink of its own (TOUCH_SINK bytes)
+// that nothing reads, so that the copy a period later finds its lines in L2.  The lines are those of the chunk's per-chunk tiles
+// (tiles[k] its tile of tensor k, `ends` the cumulative line counts, `NK` tiles) -- a head-row's value-column slices
+// read the same tiles, so the workgroup touches lines [lo, hi] only, its share -- and the first line of each of 64
+// rows of its own columns of a token-major tensor (row r at rows + min(r, nrows - 1) * pitch bytes).  It issues
+// exactly TOUCH_LOADS loads, after every copy already issued: loads retire in issue order, so
+// wait_vmcnt<TOUCH_LOADS>() after it leaves those copies landed.
+constexpr int TOUCH_SINK = 256, TOUCH_NTL = 2, TOUCH_LOADS = TOUCH_NTL + 1;
+template <int NK>
+__device__ __forceinline__ void touch_chunk(const char* const (&tiles)[NK], const int (&ends)[NK], int lo, int hi,
+                                            const char* rows, size_t pitch, int nrows) {
+  __shared__ unsigned sink[TOUCH_SINK / 4];
+  const int l = lane_id();
+  lds_void* const s = (lds_void*)sink;
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < TOUCH_NTL; ++i) {
+    const int li = min(lo + 64 * i + l, hi);
+    const char* p = tiles[0] + (size_t)li * 128;
+#pragma unroll
+    for (int k = 1; k < NK; ++k)
+      if (li >= ends[k - 1]) p = tiles[k] + (size_t)(li - ends[k - 1]) * 128;
+    __builtin_amdgcn_global_load_lds((const void*)p, s, 4, 0, 0);
+  }
+  __builtin_amdgcn_global_load_lds((const void*)(rows + (size_t)min(l, nrows - 1) * pitch), s, 4, 0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+}
+// This workgroup's share [lo, hi] of `lines` lines split over `parts` workgroups.
+__device__ __forceinline__ void touch_share(int lines, int parts, int part, int& lo, int& hi) {
+  const int per = (lines + parts - 1) / parts;
+  lo = part * per;
+  hi = min(lo + per, lines) - 1;
+}
+
 // ---------------------------------------------------------------------------------------------------------------------
 // the forward state pass (+ output), sequential over chunks.  Per chunk the workgroup streams W, diag(e) K^ and, for
 // the output, diag(gamma) Q^ and M into a swizzled LDS stage by asynchronous copies -- the next chunk's copies are in
@@ -1113,9 +1157,10 @@ struct StateBwdLds {
   static constexpr int O_Q = GK::ELEMS, O_W = O_Q + GK::ELEMS, O_M = O_W + GK::ELEMS, O_O = O_M + GM::ELEMS;
   static constexpr int SZ = O_O + GO::ELEMS;
   static constexpr int STG = sizeof(MT) == 2 ? NW * ColStage::ELEMS : 0;   // bf16 dVn leaves through row staging
-  static constexpr int NBUF = Buffers<SZ * (int)sizeof(MT), STG * (int)sizeof(MT)>::N;
-  static constexpr int O_STG = NBUF * SZ;
-  static constexpr int ELEMS = O_STG + STG;
+  static constexpr int SCAL = 32 / (int)sizeof(MT);   // per stage: the chunk's G_last (bits), t0, tend, as 4 ints
+  static constexpr int NBUF = Buffers<SZ * (int)sizeof(MT), (STG + SCAL) * (int)sizeof(MT) + TOUCH_SINK>::N;
+  static constexpr int O_STG = NBUF * SZ, O_SCAL = O_STG + STG;
+  static constexpr int ELEMS = O_SCAL + SCAL;
 };
 
 template <typename MT, int DK, int NW>
@@ -1149,7 +1194,7 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
       MT* st = lds + buf * SZ;
       const size_t bhc = crow * NT + c;
       int t0, tend;
-      chunk_span(a.pack, NT, c, T, t0, tend);
+      chunk_span<true>(a.pack, NT, c, T, t0, tend);
       GK::template dma_planned<1>(st, (const MT*)a.Ke + bhc * C * DK, offK, 0);
       GK::template dma_planned<1>(st + O_Q, (const MT*)a.Qg + bhc * C * DK, offK, 0);
       GK::template dma_planned<1>(st + O_W, (const MT*)a.W + bhc * C * DK, offK, 0);
@@ -1157,16 +1202,39 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
       const MT* og = (const MT*)a.dO + o_base + (size_t)t0 * o_pitch + vg;
       if (t0 + C <= tend) GO::template dma_planned<1>(st + O_O, og, offO, 0);
       else GO::dma(st + O_O, og, o_pitch, 0, 1, tend - t0);   // a partial chunk: rows clamped to the sequence
+      if (l == 0) {                        // the chunk's scalars beside its stage (the compute waves load nothing)
+        int* sc = (int*)(lds + L::O_SCAL) + 4 * buf;
+        sc[0] = __float_as_int(ld_const(a.GL, bhc));
+        sc[1] = t0;
+        sc[2] = tend;
+      }
+    };
+    // the L2 prefetch of chunk c - 2 (touch_chunk) while chunk c - 1 is copied
+    constexpr int LK = C * DK * (int)sizeof(MT) / 128;
+    constexpr int ENDS[4] = {LK, 2 * LK, 3 * LK, 3 * LK + C * C * (int)sizeof(MT) / 128};
+    int lo, hi;
+    touch_share(ENDS[3], a.nslice, slice, lo, hi);
+    auto touch = [&](int c) {
+      const size_t bhc = crow * NT + c, tk = bhc * C * DK * sizeof(MT);
+      int t0, tend;
+      chunk_span<true>(a.pack, NT, c, T, t0, tend);
+      const char* const tiles[4] = {(const char*)a.Ke + tk, (const char*)a.Qg + tk, (const char*)a.W + tk,
+                                    (const char*)a.M + bhc * C * C * sizeof(MT)};
+      touch_chunk<4>(tiles, ENDS, lo, hi, (const char*)((const MT*)a.dO + o_base + (size_t)t0 * o_pitch + vg),
+                     o_pitch * sizeof(MT), tend - t0);
+      wait_vmcnt<TOUCH_LOADS>();
     };
     if (NBUF == 2) {
       if (cb < ce) {
         issue(ce - 1, 0);
-        wait_dma();
+        if (ce - 2 >= cb) touch(ce - 2);
+        else wait_dma();
         lds_barrier();
       }
       for (int c = ce - 1, it = 0; c >= cb; --c, ++it) {
         if (c > cb) issue(c - 1, (it + 1) & 1);
-        wait_dma();
+        if (c - 2 >= cb) touch(c - 2);
+        else wait_dma();
         lds_barrier();
       }
     } else {
@@ -1203,20 +1271,15 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
   f4 dS[ND];
   load_state(dS, a.dsT, (size_t)hr * DK * DV, DV, col);
 
-  float gln = 0.f;
-  if (cb < ce) {
-    gln = a.GL[crow * NT + ce - 1];
-    if (NBUF == 2) lds_barrier();        // the last chunk is in LDS
-  }
+  if (cb < ce && NBUF == 2) lds_barrier();   // the last chunk is in LDS
+  // The loop issues no global loads: a wait for one would also wait for the chunk's stores issued before it.
   for (int c = ce - 1, it = 0; c >= cb; --c, ++it) {
-    int t0, tend;
-    chunk_span(a.pack, NT, c, T, t0, tend);
-    const size_t bhc = crow * NT + c;
     const int buf = (NBUF == 2) ? (it & 1) : 0;
-    const float gl = gln;
-    if (c > cb) gln = a.GL[bhc - 1];
     store_ds(c, dS);
     if (NBUF == 1) lds_barrier();        // chunk c is in LDS
+    const int* sc = (const int*)(lds + L::O_SCAL) + 4 * buf;
+    const float gl = __int_as_float(sc[0]);
+    const int t0 = sc[1], tend = sc[2];
     const MT* st = lds + buf * SZ;
 
     Frag<MT> Of[2];
