@@ -1,7 +1,7 @@
 """Benchmark of the MI355X gated delta rule: the drop-in's forward + backward at BASELINE config 1.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--config 1|2] [--grouped]
-                    [--packed uniform|ragged] [--recompute]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--config 1|2|3|4] [--hv 16|32] [--grouped]
+                    [--packed uniform|ragged] [--recompute] [--producers]
 
 A step = one call of macai.gated_delta.chunk_gated_delta_rule (use_qk_l2norm_in_kernel=True, bf16 q/k/v, fp32 g and
 beta) followed by its backward for a seeded upstream gradient dO (torch.autograd.grad, so no gradient accumulation),
@@ -40,12 +40,15 @@ TRAFFIC = {1: {"chunk_bwd": 296.0e6, "state_bwd": 163.8e6, "state_fwd_out": 193.
 CONFIGS = {
     1: dict(B=4, T=1024, Hk=16, Hv=16, DK=128, DV=128, s0=False),
     2: dict(B=2, T=1024, Hk=16, Hv=32, DK=128, DV=128, s0=True),
+    3: dict(B=1, T=32768, Hk=16, Hv=16, DK=128, DV=128, s0=False),     # Hv 16 or 32 (--hv)
+    4: dict(B=64, T=1, Hk=16, Hv=32, DK=128, DV=128, s0=True),
 }
 
 
-def make_inputs(cfg, seed, dev):
-    """The measurement plan's synthetic inputs (q, k, v, u_g, x_g, x_beta, s0, dO drawn in that order in float64)."""
-    c = CONFIGS[cfg]
+def make_inputs(cfg, seed, dev, **over):
+    """The measurement plan's synthetic inputs (q, k, v, u_g, x_g, x_beta, s0, dO drawn in that order in float64);
+    keyword overrides replace config fields."""
+    c = dict(CONFIGS[cfg], **over)
     gen = torch.Generator().manual_seed(seed)
     B, T, Hk, Hv, DK, DV = c["B"], c["T"], c["Hk"], c["Hv"], c["DK"], c["DV"]
     rep = Hv // Hk
@@ -199,6 +202,112 @@ def cpu_baseline(cfg, threads):
                       f"after 2 warm-ups ({dt * 1e3:.0f} ms/call)"}
 
 
+def _events_time(fn, reps):
+    """Seconds per call of fn: HIP events on the current stream around reps back-to-back calls (after one warm call)."""
+    fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / reps
+
+
+def bench_prefill(args):
+    """one row of 32,768 tokens, forward only (no_grad: no per-chunk states kept), the final state
+    returned; Hv value heads over 16 key heads (q and k unrepeated).  The bound is the 512-chunk chain of the state
+    pass; the line reports the value split it ran with and each pass's in-step time."""
+    from macai.gated_delta import chunk_gated_delta_rule, op
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    inp, c = make_inputs(3, 1003, dev, Hv=args.hv)
+    rep = c["Hv"] // c["Hk"]
+    q, k = (inp[n][:, :, ::rep].contiguous() for n in ("query", "key"))
+    v, g, beta = inp["value"], inp["g"], inp["beta"]
+
+    def fwd():
+        with torch.no_grad():
+            return chunk_gated_delta_rule(q, k, v, g, beta, output_final_state=True, use_qk_l2norm_in_kernel=True)
+    for _ in range(args.warmup):
+        fwd()
+    sec = _events_time(fwd, args.steps)
+    op.EVENTS = []
+    for _ in range(min(args.steps, 10)):
+        fwd()
+    torch.cuda.synchronize()
+    t = {}
+    for name, a, b in op.EVENTS:
+        t.setdefault(name, []).append(a.elapsed_time(b) * 1e-3)
+    op.EVENTS = None
+    t = {name: sum(v) / len(v) for name, v in t.items()}
+    B, T, H, DK, DV = c["B"], c["T"], c["Hv"], c["DK"], c["DV"]
+    cost = kernel_costs(B, T, H, DK, DV, Hk=c["Hk"])
+    kernels = {n: {"us": round(x * 1e6, 2), "GB/s": round(cost[n]["bytes"] / x / 1e9, 1),
+                   "hbm_frac": round(cost[n]["bytes"] / x / HBM_PEAK, 4)} for n, x in t.items()}
+    st = t["state_fwd_out"]
+    line = {"metric": f"gated-delta forward tokens/s (B1xT32768, Hv{H}, Hk16, d128 bf16, forward only)",
+            "value": round(B * T / sec, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": "BASELINE config 3: long single-row prefill, forward only", "B": B, "T": T,
+                       "Hk": c["Hk"], "Hv": H, "DK": DK, "DV": DV, "chunk": C,
+                       "value_split": op.split_for(B * H, T, DV)},
+            "roofline": {"kernel": "state_fwd_out", "timing": "in-step HIP events", "bound": "hbm",
+                         "achieved": round(cost["state_fwd_out"]["bytes"] / st / 1e9, 1), "peak": HBM_PEAK / 1e9,
+                         "unit": "GB/s", "frac": round(cost["state_fwd_out"]["bytes"] / st / HBM_PEAK, 4),
+                         "traffic": None},
+            "chain_us_per_chunk": round(st * 1e6 / math.ceil(T / C), 3),
+            "kernels": kernels}
+    print(json.dumps(line), flush=True)
+
+
+def bench_decode(args):
+    """one decode step per sequence (B = 64, Hv = 32 over Hk = 16, fp32 state [64, 32, 128, 128]),
+    through the drop-in (transformers' torch_recurrent_gated_delta_rule signature) and as the bare C-ABI launch on
+    preallocated buffers.  The step reads and writes the whole fp32 state once: HBM-bound, reported against peak."""
+    from macai.gated_delta import _native as N
+    from macai.gated_delta import recurrent_gated_delta_rule
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    inp, c = make_inputs(4, 1004, dev)
+    rep = c["Hv"] // c["Hk"]
+    q, k = (inp[n][:, :, ::rep].contiguous() for n in ("query", "key"))
+    v, g, beta, s0 = inp["value"], inp["g"], inp["beta"], inp["initial_state"]
+    B, H, Hk, DK, DV = c["B"], c["Hv"], c["Hk"], c["DK"], c["DV"]
+
+    def dropin():
+        with torch.no_grad():
+            return recurrent_gated_delta_rule(q, k, v, g, beta, initial_state=s0, output_final_state=True,
+                                              use_qk_l2norm_in_kernel=True)
+    o = torch.empty(B, 1, H, DV, device=dev, dtype=v.dtype)
+    s1 = torch.empty_like(s0)
+    P = N.ptr
+    st = N.stream_of(q)
+    args_k = ("macai_gdr_decode", P(q), P(k), P(v), P(g), P(beta), P(s0), P(o), P(s1), B, H, Hk, DK, DV,
+              N.dtype_code(v.dtype), 1, DK ** -0.5, st)
+    for _ in range(args.warmup):
+        dropin()
+    sec_dropin = _events_time(dropin, args.steps)
+    sec = _events_time(lambda: N.call(*args_k), args.steps)
+    state = B * H * DK * DV * 4
+    io = B * (2 * Hk * DK + 2 * H * DV) * 2 + B * H * 4 * 2
+    nbytes = 2 * state + io
+    line = {"metric": "gated-delta decode step GB/s (B64, Hv32, Hk16, d128; fp32 state read + write)",
+            "value": round(nbytes / sec / 1e9, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "BASELINE config 4: one recurrent decode step per sequence", "B": B, "T": 1,
+                       "Hk": Hk, "Hv": H, "DK": DK, "DV": DV},
+            "roofline": {"kernel": "decode", "timing": "HIP events, C-ABI launches on preallocated buffers",
+                         "bound": "hbm", "achieved": round(nbytes / sec / 1e9, 1), "peak": HBM_PEAK / 1e9,
+                         "unit": "GB/s", "frac": round(nbytes / sec / HBM_PEAK, 4), "traffic": None},
+            "bytes_per_step": nbytes, "tokens_per_s": round(B / sec, 1),
+            "dropin_ms_per_step": round(sec_dropin * 1e3, 4), "dropin_tokens_per_s": round(B / sec_dropin, 1)}
+    print(json.dumps(line), flush=True)
+
+
 def bench_producers(cfg, reps=20):
     """The rule's producers at the config's layer widths (key_dim = Hk DK, value_dim = Hv DV): the convolution path
     forward (q, k at key heads, v in x's dtype: the layout the rule reads without copies), its backward (without and
@@ -279,7 +388,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS))
+    ap.add_argument("--config", type=int, default=1, choices=sorted(CONFIGS),
+                    help="1 (the headline), 2: fwd+bwd steps; 3: the long prefill, forward only; 4: one decode step")
+    ap.add_argument("--hv", type=int, default=16, choices=[16, 32], help="config 3's value heads")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--recompute", action="store_true",
@@ -305,6 +416,12 @@ def main():
         sys.exit(2)
     if args.producers:
         bench_producers(args.config)
+        return
+    if args.config == 3:
+        bench_prefill(args)
+        return
+    if args.config == 4:
+        bench_decode(args)
         return
     from macai.gated_delta import chunk_gated_delta_rule
     dev = torch.device("cuda", 0)

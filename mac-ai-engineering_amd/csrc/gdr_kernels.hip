@@ -945,7 +945,7 @@ struct StateOutLds {
   static constexpr int HO = (ND / 2 + 2) * 64 * 8;                    // one chain wave's S and Vn fragments
   static constexpr int O_QM = 2 * WK, O_HO = O_QM + 2 * QM, O_STG = O_HO + 2 * NW * HO;
   static constexpr int ELEMS = O_STG + (STORE ? NW * ColStage::ELEMS : 0);   // the output waves' Vn staging
-  static_assert(ELEMS * 2 <= LDS_BYTES, "state_out LDS");
+  static_assert(ELEMS * 2 + (STORE ? 0 : TOUCH_SINK) <= LDS_BYTES, "state_out LDS");
 };
 
 template <int DK, int NW, bool STORE>
@@ -985,13 +985,31 @@ __global__ void __launch_bounds__(64 * (2 * NW + 1)) state_out_kernel(StateFwdAr
       GW::template dma_planned<1>(st, (const MT*)a.Qg + bhc * C * DK, offW, 0);
       GM::template dma_planned<1>(st + L::O_M, (const MT*)a.M + bhc * C * C, offM, 0);
     };
+    // Without the state stores the pass moves little per chunk and the chain waits on each copy's HBM latency (the
+    // long single-row prefill: 1.7 us a chunk), so the loader also touches chunk c + 2's tiles and the workgroup's U
+    // columns into L2 while chunk c + 1 is copied (touch_chunk).  With them the pass is bound by its bytes, and the
+    // touch only slowed the kernels after it.
+    constexpr bool TOUCH = !STORE;
+    constexpr int LK = C * DK * 2 / 128;
+    constexpr int ENDS[4] = {LK, 2 * LK, 3 * LK, 3 * LK + C * C * 2 / 128};
+    int lo, hi;
+    touch_share(ENDS[3], a.nslice, slice, lo, hi);
+    auto touch = [&](int c) {
+      const size_t bhc = crow * NT + c, tk = bhc * C * DK * 2;
+      const char* const tiles[4] = {(const char*)a.W + tk, (const char*)a.Ke + tk, (const char*)a.Qg + tk,
+                                    (const char*)a.M + bhc * C * C * 2};
+      touch_chunk<4>(tiles, ENDS, lo, hi, (const char*)(a.U + bhc * C * DV + slice * NW * 16), DV * sizeof(float), C);
+      wait_vmcnt<TOUCH_LOADS>();
+    };
     if (nc > 0) wk(cb, 0);
-    wait_dma();
+    if (TOUCH && nc > 1) touch(cb + 1);
+    else wait_dma();
     lds_barrier();                         // B_0: the first [W | Ke] stage is in
     for (int i = 0; i < nc; ++i) {
       if (i + 1 < nc) wk(cb + i + 1, (i + 1) & 1);
       qm(cb + i, i & 1);
-      wait_dma();
+      if (TOUCH && i + 2 < nc) touch(cb + i + 2);
+      else wait_dma();
       lds_barrier();                       // B_{i+1}
     }
     return;
