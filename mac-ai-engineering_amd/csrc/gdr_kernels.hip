@@ -644,15 +644,15 @@ struct Buffers {
   static constexpr int N = (2 * STAGE_BYTES + EXTRA_BYTES <= LDS_BYTES) ? 2 : 1;
 };
 
-// The L2 prefetch of a sequential pass's loader wave.  The loader copies chunk c + 1 into LDS while chunk c computes;
-// under a training step's traffic that copy's HBM latency exceeds a chunk's compute, so the loader also touches the
-// chunk after it a period ahead: one dword a 128-byte line, copied into an LDS sink of its own (TOUCH_SINK bytes)
-// that nothing reads, so that the copy a period later finds its lines in L2.  The lines are those of the chunk's per-chunk tiles
-// (tiles[k] its tile of tensor k, `ends` the cumulative line counts, `NK` tiles) -- a head-row's value-column slices
-// read the same tiles, so the workgroup touches lines [lo, hi] only, its share -- and the first line of each of 64
-// rows of its own columns of a token-major tensor (row r at rows + min(r, nrows - 1) * pitch bytes).  It issues
-// exactly TOUCH_LOADS loads, after every copy already issued: loads retire in issue order, so
-// wait_vmcnt<TOUCH_LOADS>() after it leaves those copies landed.
+// The L2 prefetch of a sequential pass's loader wave.  The loader copies the next chunk into LDS while this one
+// computes, and the chain waits whenever that copy's HBM latency exceeds a chunk's compute; so the loader also touches
+// the chunk after the next one, a period ahead: one dword a 128-byte line, copied into an LDS sink of its own
+// (TOUCH_SINK bytes) that nothing reads, so that its copy a period later finds the lines in L2.  The lines are those
+// of the chunk's per-chunk tiles (tiles[k] its tile of tensor k, `ends` the cumulative line counts, NK tiles) -- a
+// head-row's value-column slices read the same tiles, so the workgroup touches lines [lo, hi] only, its share -- and
+// the first line of each of 64 rows of its own columns of a token-major tensor (row r at rows + min(r, nrows - 1) *
+// pitch bytes).  It issues exactly TOUCH_LOADS loads, after every copy already issued: loads retire in issue order,
+// so wait_vmcnt<TOUCH_LOADS>() after it leaves those copies landed.
 constexpr int TOUCH_SINK = 256, TOUCH_NTL = 2, TOUCH_LOADS = TOUCH_NTL + 1;
 template <int NK>
 __device__ __forceinline__ void touch_chunk(const char* const (&tiles)[NK], const int (&ends)[NK], int lo, int hi,
