@@ -263,6 +263,12 @@ def bench_prefill(args):
     print(json.dumps(line), flush=True)
 
 
+def decode_bytes(B, H, Hk, DK, DV, es=2):
+    """Algorithmic bytes of one decode step: the fp32 state read and written once, q and k at their Hk key heads, v
+    and o at the H value heads (es bytes an element), g and beta in fp32."""
+    return 2 * B * H * DK * DV * 4 + B * (2 * Hk * DK + 2 * H * DV) * es + B * H * 4 * 2
+
+
 def bench_decode(args):
     """one decode step per sequence (B = 64, Hv = 32 over Hk = 16, fp32 state [64, 32, 128, 128]),
     through the drop-in (transformers' torch_recurrent_gated_delta_rule signature) and as the bare C-ABI launch on
@@ -291,9 +297,7 @@ def bench_decode(args):
         dropin()
     sec_dropin = _events_time(dropin, args.steps)
     sec = _events_time(lambda: N.call(*args_k), args.steps)
-    state = B * H * DK * DV * 4
-    io = B * (2 * Hk * DK + 2 * H * DV) * 2 + B * H * 4 * 2
-    nbytes = 2 * state + io
+    nbytes = decode_bytes(B, H, Hk, DK, DV)
     line = {"metric": "gated-delta decode step GB/s (B64, Hv32, Hk16, d128; fp32 state read + write)",
             "value": round(nbytes / sec / 1e9, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 4), "higher_is_better": True, "scaling": "weak",

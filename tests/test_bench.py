@@ -1,0 +1,52 @@
+"""The benchmark's contract and accounting, on the CPU: one GPU only, the configurations it measures, and the
+algorithmic bytes its roofline divides by (each declared input read once, each output written once)."""
+import os
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+import bench  # noqa: E402
+
+
+def test_more_than_one_gpu_is_refused():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+@pytest.mark.parametrize("cfg,shape", [
+    (1, dict(B=4, T=1024, Hk=16, Hv=16, DK=128, DV=128, s0=False)),
+    (2, dict(B=2, T=1024, Hk=16, Hv=32, DK=128, DV=128, s0=True)),
+    (3, dict(B=1, T=32768, Hk=16, Hv=16, DK=128, DV=128, s0=False)),
+    (4, dict(B=64, T=1, Hk=16, Hv=32, DK=128, DV=128, s0=True))])
+def test_configs_are_the_baseline_shapes(cfg, shape):
+    """BASELINE.json configs 1-4 (config 3 also runs at Hv = 32 through --hv)."""
+    assert bench.CONFIGS[cfg] == shape
+
+
+def test_training_step_bytes_per_chunk_head():
+    """Config 1's training step as the library runs it (the forward keeping prep's operands and the chunk states):
+    per chunk-head, prep with A 144.5 KiB, the state pass with the output and S_c, Vn 184.0 KiB, the reverse pass
+    152.0 KiB, the chunk backward 281.0 KiB, from the tensors' sizes: q, k, v, dO 16 KiB a chunk-head each in bf16,
+    g and beta 0.5 KiB, W, Ke, Qg 16 KiB, U 32 KiB (fp32), M and A 8 KiB, S_c and dS 64 KiB (fp32), Vn and dVn
+    16 KiB, GL 4 bytes."""
+    c = bench.CONFIGS[1]
+    cost = bench.kernel_costs(c["B"], c["T"], c["Hv"], c["DK"], c["DV"], keep=True)
+    n = c["B"] * c["Hv"] * (c["T"] // 64)
+    kib = {k: cost[k]["bytes"] / n / 1024 for k in ("prep_fwd", "state_fwd_out", "state_bwd", "chunk_bwd")}
+    assert kib["prep_fwd"] == pytest.approx(3 * 16 + 0.5 + 3 * 16 + 32 + 8 + 8 + 4 / 1024)
+    assert kib["state_fwd_out"] == pytest.approx(3 * 16 + 32 + 8 + 4 / 1024 + 64 + 16 + 16)
+    assert kib["state_bwd"] == pytest.approx(3 * 16 + 8 + 4 / 1024 + 64 + 16 + 16)
+    assert kib["chunk_bwd"] == pytest.approx(3 * 16 + 0.5 + 16 + 8 + 2 * 64 + 2 * 16 + 3 * 16 + 0.5)
+    assert [round(kib[k], 1) for k in kib] == [144.5, 184.0, 152.0, 281.0]
+
+
+def test_decode_bytes():
+    """Config 4: the fp32 state [64, 32, 128, 128] read and written (268.4 MB) plus the token tensors."""
+    b = bench.decode_bytes(64, 32, 16, 128, 128)
+    state = 64 * 32 * 128 * 128 * 4
+    assert b == 2 * state + 64 * (2 * 16 * 128 + 2 * 32 * 128) * 2 + 64 * 32 * 8
+    assert round(2 * state / 1e6, 1) == 268.4
