@@ -87,3 +87,34 @@ def test_packed_rows_against_the_oracle():
         t += L
     _say("max error", max(errs))
     assert max(errs) <= 2e-4
+
+
+@pytest.mark.parametrize("lens,Hk,Hv,dtype", [([130, 0, 64, 6, 200], 2, 2, torch.bfloat16),
+                                              ([300, 1, 700], 1, 2, torch.bfloat16),
+                                              ([40, 0, 90], 2, 2, torch.float32)])
+def test_packed_rows_forward_only(lens, Hk, Hv, dtype):
+    """Inference (no_grad: the state pass with the output only, which prefetches its next tiles into L2) on packed
+    rows: the same bits as each sequence run alone and as the training forward's output (the state pass that also
+    stores the chunk states forms the same products in the same order)."""
+    _say("case forward only", lens, Hk, Hv, dtype)
+    row, s0, dsT, cu = _inputs(lens, Hk, Hv, 128, 128, dtype, seed=60)
+    names = ("query", "key", "value", "g", "beta")
+
+    def fwd(r, s, c=None):
+        kw = {} if c is None else {"cu_seqlens": c.to(DEV)}
+        with torch.no_grad():
+            o, sT = chunk_gated_delta_rule(*(r[n].to(DEV) for n in names), initial_state=s.to(DEV),
+                                           output_final_state=True, use_qk_l2norm_in_kernel=True, **kw)
+        torch.cuda.synchronize()
+        return o.cpu(), sT.cpu()
+    o, sT = fwd(row, s0, cu)
+    to, tsT, _ = _run(row, s0, dsT, cu)
+    assert torch.equal(o, to) and torch.equal(sT, tsT), "no_grad and training forwards differ"
+    t = 0
+    for n, L in enumerate(lens):
+        if L == 0:
+            assert torch.equal(sT[n], s0[n])
+            continue
+        o1, sT1 = fwd({k: v[:, t:t + L].contiguous() for k, v in row.items()}, s0[n:n + 1])
+        assert torch.equal(o[:, t:t + L], o1) and torch.equal(sT[n:n + 1], sT1), f"sequence {n}"
+        t += L
