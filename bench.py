@@ -1,18 +1,19 @@
 """Benchmark of the MI355X gated delta rule: the drop-in's forward + backward at BASELINE config 1.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--config 1|2|3|4] [--hv 16|32] [--grouped]
-                    [--packed uniform|ragged] [--recompute] [--producers]
+                    [--packed uniform|ragged] [--stored] [--producers] [--ceilings]
 
 A step = one call of macai.gated_delta.chunk_gated_delta_rule (use_qk_l2norm_in_kernel=True, bf16 q/k/v, fp32 g and
 beta) followed by its backward for a seeded upstream gradient dO (torch.autograd.grad, so no gradient accumulation),
-on synthetic inputs already resident in HBM.  The forward keeps prep's per-chunk operands for the backward
-(op.RECOMPUTE_STATES = False, the library's default); --recompute measures the reference's default instead, where the
-backward reruns prep.  Prints ONE JSON line (rank 0).  Beside the step time it times every
-pass inside steps identical to the timed ones with HIP events on the launch stream (macai.gated_delta.op.EVENTS; the
-roofline of the dominant kernel) and, for comparison, each pass alone (back-to-back repeats, whose inputs stay in the
-Infinity Cache), and the
-reference's torch path on the host CPU (the oracle's restatement of transformers' torch_chunk_gated_delta_rule,
-float32, autograd backward) on a bounded sample, as a reported baseline.
+on synthetic inputs already resident in HBM.  The headline runs the library's default, the reference's: the forward
+keeps only its inputs and the backward reruns prep and recomputes the chunk states (op.RECOMPUTE_STATES = True,
+BASELINE config 1 as specified).  The stored-states mode (the forward keeps prep's operands and the chunk states) is
+timed the same way and reported beside it (--stored swaps the two).  Prints ONE JSON line (rank 0).  Beside the step
+time it times every pass inside steps identical to the timed ones with HIP events on the launch stream
+(macai.gated_delta.op.EVENTS; the roofline of the dominant kernel) and, for comparison, each pass alone (back-to-back
+repeats, whose inputs stay in the Infinity Cache), and the reference's torch path on the host CPU (the oracle's
+restatement of transformers' torch_chunk_gated_delta_rule, float32, autograd backward) over the whole config, as a
+reported baseline.
 """
 import argparse
 import json
@@ -31,11 +32,34 @@ HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
 MFMA_PEAK = {"bf16": 2.5e15, "f32": 157.3e12}
 PUBLISHED = 401.1e3        # reference's own fwd+bwd tokens/s at this config (M3 Max)
 C = 64
-# HBM bytes per launch of the training step at config 1 from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
-# (profiles/gated_delta_config1.md), FETCH_SIZE scaled by 2.000 and WRITE_SIZE by 1.000 (the factors a plain 256 MiB
-# device copy gives); the training step as it runs by default: prep with A, the forward state pass storing S_c and Vn,
-# the reverse pass alone
-TRAFFIC = {1: {"chunk_bwd": 296.0e6, "state_bwd": 163.8e6, "state_fwd_out": 193.1e6, "prep_fwd": 151.8e6}}
+# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --no-alone --no-cpu`, each
+# counter scaled by what it reads for a plain device copy of known size (bench.py --copy-mib 256): FETCH_SIZE x 2.000,
+# WRITE_SIZE x 1.000.  Keyed by the config and the mode the profile ran, and stamped with the fingerprint of the
+# kernel sources it was taken on: measured_traffic() reports the figures only while the sources still match.
+TRAFFIC = {}
+KERNEL_SOURCES = ("gdr_kernels.hip", "gdr_common.h", "gdr_lds.h", "gdr_stage.h")
+
+
+def kernel_fingerprint():
+    """sha256 (first 16 hex digits) of the rule's kernel sources, in KERNEL_SOURCES order."""
+    import hashlib
+    h = hashlib.sha256()
+    for f in KERNEL_SOURCES:
+        with open(os.path.join(ROOT, "mac-ai-engineering_amd", "csrc", f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+def measured_traffic(cfg, mode):
+    """{kernel: HBM bytes per launch} from TRAFFIC for (cfg, mode) while the kernel sources match the profile's,
+    with "_source" saying which (or why none)."""
+    rec = TRAFFIC.get((cfg, mode))
+    if rec is None:
+        return {"_source": "no profile of this config and mode"}
+    if rec["sources"] != kernel_fingerprint():
+        return {"_source": f"stale: the kernels changed since the profile (sources {rec['sources']})"}
+    return dict(rec["bytes"], _source=f"rocprofv3 --pmc, kernel sources {rec['sources']}")
+
 
 CONFIGS = {
     1: dict(B=4, T=1024, Hk=16, Hv=16, DK=128, DV=128, s0=False),
@@ -71,12 +95,12 @@ def make_inputs(cfg, seed, dev, **over):
 
 
 def kernel_costs(B, T, H, DK, DV, es=2, Hk=None, chunks=None, keep=False):
-    """Algorithmic bytes (each declared input read once, each output written once, from argument sizes) and dense
-    FLOPs (2 per multiply-add, triangular products counted dense) per launch of each kernel of the training step.
-    Hk: key heads of q and k when they come unrepeated (grouped value heads); H by default.  chunks: chunks per head
-    over the batch (B ceil(T / 64) by default; packed rows chunk each sequence on its own).  keep: the forward's prep
-    also writes A and its state pass S_c and Vn (the training forward keeps them; the backward runs neither prep nor
-    the recompute pass)."""
+    """Algorithmic bytes (each declared input read once, each output written once, from argument sizes), split into
+    reads and writes, and dense FLOPs (2 per multiply-add, triangular products counted dense) per launch of each
+    kernel of the training step.  Hk: key heads of q and k when they come unrepeated (grouped value heads); H by
+    default.  chunks: chunks per head over the batch (B ceil(T / 64) by default; packed rows chunk each sequence on
+    its own).  keep: the forward's prep also writes A and its state pass S_c and Vn (the stored-states mode: the
+    backward then runs neither prep nor the recompute pass)."""
     Hk = Hk or H
     chunks = chunks or B * math.ceil(T / C)
     n = H * chunks                       # chunk-heads
@@ -86,32 +110,39 @@ def kernel_costs(B, T, H, DK, DV, es=2, Hk=None, chunks=None, keep=False):
     gb = tok * 4 * 2                     # g and beta
     cdk, cdv, cc = C * DK, C * DV, C * C
     sdk = DK * DV * 4                    # one fp32 state
-    cost = {}
     pre = 3 * cdk * es + cdv * 4 + cc * es + 4      # prep's row-major outputs W, Ke, Qg, U, M, GL
     inp = 2 * io_kk + io_v + gb                       # q, k, v, g, beta
-    # the forward: prep, then the state pass reads W, U, Ke, GL, Qg, M and writes o
-    cost["prep_fwd"] = dict(bytes=inp + n * (pre + (cc * es if keep else 0)),
-                            flops=n * (2 * 2 * cc * DK + cc * C / 3 + 2 * cc * DK + 2 * cc * DV))
-    cost["state_fwd_out"] = dict(bytes=n * (pre + ((sdk + cdv * es) if keep else 0)) + io_v,
-                                 flops=n * (3 * 2 * C * DK * DV + 2 * cc * DV))
-    # the backward: prep also writes A; the recompute pass reads W, U, Ke, GL and writes S_c (fp32) and Vn; the reverse
-    # pass reads Ke, Qg, W, M, GL, dO and writes dS_{c+1} (fp32) and dVn
-    cost["prep_bwd"] = dict(bytes=inp + n * (pre + cc * es),
-                            flops=n * (2 * 2 * cc * DK + cc * C / 3 + 2 * cc * DK + 2 * cc * DV))
-    cost["state_fwd_store"] = dict(bytes=n * (2 * cdk * es + cdv * 4 + 4 + sdk + cdv * es),
-                                   flops=n * (2 * 2 * C * DK * DV))
-    cost["state_bwd"] = dict(bytes=n * (3 * cdk * es + cc * es + 4 + sdk + cdv * es) + io_v,
-                             flops=n * (3 * 2 * C * DK * DV + 2 * cc * DV))
-    # the two in one launch (macai_gdr_state_pair)
-    cost["state_pair"] = dict(bytes=cost["state_fwd_store"]["bytes"] + cost["state_bwd"]["bytes"],
-                              flops=cost["state_fwd_store"]["flops"] + cost["state_bwd"]["flops"])
-    # the per-chunk backward reads q, k, v, g, beta, dO, A, S_c, dS_{c+1}, Vn, dVn; writes dq, dk, dv, dg, dbeta
-    cost["chunk_bwd"] = dict(bytes=inp + io_v + n * (cc * es + 2 * sdk + 2 * cdv * es) + 2 * io_k + io_v + gb,
-                             flops=n * (3 * 2 * C * DK * DV + 2 * cc * DK + 3 * 2 * cc * DK + 2 * 2 * cc * DV
-                                        + 2 * 2 * cc * C + 3 * 2 * cc * DK + 2 * cc * DV))
-    # grouped heads: each of dq, dk folded from per-value-head rows (read H heads, write Hk)
-    cost["group_sum"] = dict(bytes=io_k + io_kk, flops=tok * DK)
-    return cost
+    prep_flops = n * (2 * 2 * cc * DK + cc * C / 3 + 2 * cc * DK + 2 * cc * DV)
+    state_flops = n * (3 * 2 * C * DK * DV + 2 * cc * DV)
+    rw = {
+        # the forward: prep (A too when keep), then the state pass reads W, U, Ke, GL, Qg, M and writes o (and S_c,
+        # Vn when keep)
+        "prep_fwd": (inp, n * (pre + (cc * es if keep else 0)), prep_flops),
+        "state_fwd_out": (n * pre, io_v + (n * (sdk + cdv * es) if keep else 0), state_flops),
+        # the backward: prep with A; the recompute pass reads W, U, Ke, GL and writes S_c (fp32) and Vn; the reverse
+        # pass reads Ke, Qg, W, M, GL, dO and writes dS_{c+1} (fp32) and dVn
+        "prep_bwd": (inp, n * (pre + cc * es), prep_flops),
+        "state_fwd_store": (n * (2 * cdk * es + cdv * 4 + 4), n * (sdk + cdv * es), n * (2 * 2 * C * DK * DV)),
+        "state_bwd": (n * (3 * cdk * es + cc * es + 4) + io_v, n * (sdk + cdv * es), state_flops),
+        # the per-chunk backward reads q, k, v, g, beta, dO, A, S_c, dS_{c+1}, Vn, dVn; writes dq, dk, dv, dg, dbeta
+        "chunk_bwd": (inp + io_v + n * (cc * es + 2 * sdk + 2 * cdv * es), 2 * io_k + io_v + gb,
+                      n * (3 * 2 * C * DK * DV + 2 * cc * DK + 3 * 2 * cc * DK + 2 * 2 * cc * DV + 2 * 2 * cc * C
+                           + 3 * 2 * cc * DK + 2 * cc * DV)),
+        # grouped heads: each of dq, dk folded from per-value-head rows (read H heads, write Hk)
+        "group_sum": (io_k, io_kk, tok * DK),
+    }
+    # the recompute and reverse passes in one launch (macai_gdr_state_pair)
+    rw["state_pair"] = tuple(a + b for a, b in zip(rw["state_fwd_store"], rw["state_bwd"]))
+    return {k: dict(bytes=r + w, reads=r, writes=w, flops=f) for k, (r, w, f) in rw.items()}
+
+
+def step_kernels(keep, grouped=False):
+    """The launches of one training step in order: the stored-states mode (keep) runs prep with A and the state
+    pass storing S_c, Vn, then the reverse pass and the chunk backward; the recompute mode runs prep and the output
+    pass, then prep with A, the pair pass and the chunk backward."""
+    ks = (["prep_fwd", "state_fwd_out", "state_bwd", "chunk_bwd"] if keep
+          else ["prep_fwd", "state_fwd_out", "prep_bwd", "state_pair", "chunk_bwd"])
+    return ks + (["group_sum", "group_sum"] if grouped else [])
 
 
 def time_kernels(inp, reps=20, keep=False):
@@ -173,33 +204,81 @@ def time_kernels(inp, reps=20, keep=False):
     return out, split
 
 
-def cpu_baseline(cfg, threads):
-    """The reference's torch path (transformers' algorithm, float32, autograd backward) on the host CPU: B = 1 of the
-    config's rows (a bounded sample), 2 warm-up calls, then the median of 3."""
+def cpu_info():
+    """(CPU model, physical cores, CPUs this process may run on, the thread share the environment grants):
+    /proc/cpuinfo's model name and distinct (physical id, core id) pairs, the affinity mask, OMP_NUM_THREADS."""
+    model, cores, phys = "unknown", set(), None
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                key, _, val = line.partition(":")
+                key, val = key.strip(), val.strip()
+                if key == "model name" and model == "unknown":
+                    model = val
+                elif key == "physical id":
+                    phys = val
+                elif key == "core id":
+                    cores.add((phys, val))
+    except OSError:
+        pass
+    allowed = len(os.sched_getaffinity(0))
+    physical = len(cores) or allowed
+    share = int(os.environ.get("OMP_NUM_THREADS") or allowed)
+    return model, physical, allowed, share
+
+
+def cpu_baseline(cfg, threads=0):
+    """The reference's torch path (the oracle's restatement of transformers' algorithm at C = 64, float32, the
+    solve_triangular inverse, autograd backward) on the host CPU over the whole config, the measurement plan's way
+    (bench/bench_gated_delta.py:28, 43-83): 2 warm-up calls, then the median of 5, forward alone and forward +
+    backward, with every core the process is granted (physical cores, capped by the CPUs it may run on and by the
+    OMP_NUM_THREADS share a GPU box gives one GPU) and with one thread."""
     sys.path.insert(0, ROOT)
     from oracle import gdr
-    torch.set_num_threads(threads)
+    model, physical, allowed, share = cpu_info()
+    n = threads or max(1, min(physical, allowed, share))
     c = dict(CONFIGS[cfg])
-    inp = gdr.make_inputs(1, c["T"], c["Hk"], c["Hv"], c["DK"], c["DV"], torch.float32, c["s0"], seed=1000 + cfg)
-    leaves = [inp[n].clone().requires_grad_(True) for n in ("query", "key", "value", "g", "beta")]
+    inp = gdr.make_inputs(c["B"], c["T"], c["Hk"], c["Hv"], c["DK"], c["DV"], torch.float32, c["s0"],
+                          seed=1000 + cfg)
+    leaves = [inp[x].clone().requires_grad_(True) for x in ("query", "key", "value", "g", "beta")]
 
-    def step():
+    def fwd():
+        with torch.no_grad():
+            gdr.torch_chunk_gated_delta_rule(*leaves, initial_state=inp["initial_state"], output_final_state=True,
+                                             use_qk_l2norm_in_kernel=True, inverse="solve")
+
+    def fwd_bwd():
         o, _ = gdr.torch_chunk_gated_delta_rule(*leaves, initial_state=inp["initial_state"], output_final_state=True,
                                                 use_qk_l2norm_in_kernel=True, inverse="solve")
         torch.autograd.grad(o, leaves, inp["do"].float())
 
-    for _ in range(2):
-        step()
-    ts = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        step()
-        ts.append(time.perf_counter() - t0)
-    ts.sort()
-    dt = ts[1]
-    return {"value": c["T"] / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"B=1 of config {cfg} (T={c['T']}, H={c['Hv']}, D={c['DK']}), fp32 fwd+bwd, median of 3 "
-                      f"after 2 warm-ups ({dt * 1e3:.0f} ms/call)"}
+    def median(fn):
+        for _ in range(2):
+            fn()
+        ts = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return sorted(ts)[2]
+
+    old = torch.get_num_threads()
+    try:
+        torch.set_num_threads(n)
+        t_fb, t_f = median(fwd_bwd), median(fwd)
+        torch.set_num_threads(1)
+        t1_fb, t1_f = median(fwd_bwd), median(fwd)
+    finally:
+        torch.set_num_threads(old)
+    tok = c["B"] * c["T"]
+    return {"value": round(tok / t_fb, 1), "unit": "tokens/s", "cores": n, "kind": "port",
+            "sample": f"the whole of config {cfg} (B={c['B']}, T={c['T']}, H={c['Hv']}, D={c['DK']}), fp32 fwd+bwd, "
+                      f"median of 5 after 2 warm-ups, {n} threads",
+            "ms_fwd_bwd": round(t_fb * 1e3, 2), "ms_fwd": round(t_f * 1e3, 2),
+            "fwd_tokens_per_s": round(tok / t_f, 1),
+            "one_thread": {"ms_fwd_bwd": round(t1_fb * 1e3, 2), "ms_fwd": round(t1_f * 1e3, 2),
+                           "tokens_per_s": round(tok / t1_fb, 1), "fwd_tokens_per_s": round(tok / t1_f, 1)},
+            "cpu_model": model, "physical_cores": physical, "cpus_allowed": allowed, "omp_share": share}
 
 
 def _events_time(fn, reps):
@@ -387,6 +466,46 @@ def bench_producers(cfg, reps=20):
     print(json.dumps(line))
 
 
+def bench_ceilings(args, mib=1024, reps=10):
+    """The device's own streaming rates (macai_gdr_probe_stream: read-only, write-only and copy over `mib` MiB in
+    16-byte units, grid-stride; the best of a few workgroup counts, each timed with HIP events over `reps` launches)
+    and the floor they put under the config's training step: every kernel's algorithmic reads at the read rate plus
+    its writes at the write rate, summed over the step's launches (the recompute mode and the stored-states mode)."""
+    from macai.gated_delta import _native as N
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    nbytes = mib << 20
+    src = torch.ones(nbytes // 4, device=dev)
+    dst = torch.empty_like(src)
+    st = N.stream_of(src)
+    rates = {}
+    for mode, name, moved in ((0, "read", nbytes), (1, "write", nbytes), (2, "copy", 2 * nbytes)):
+        best = None
+        for blocks in (1024, 2048, 4096, 8192, 16384):
+            sec = _events_time(lambda: N.call("macai_gdr_probe_stream", mode, N.ptr(src), N.ptr(dst), nbytes, blocks,
+                                              st), reps)
+            if best is None or sec < best[0]:
+                best = (sec, blocks)
+        rates[name] = {"GB/s": round(moved / best[0] / 1e9, 1), "blocks": best[1], "us": round(best[0] * 1e6, 2)}
+    c = CONFIGS[args.config]
+    floors = {}
+    for mode, keep in (("recompute", False), ("stored", True)):
+        cost = kernel_costs(c["B"], c["T"], c["Hv"], c["DK"], c["DV"], keep=keep)
+        ks = step_kernels(keep)
+        reads = sum(cost[k]["reads"] for k in ks)
+        writes = sum(cost[k]["writes"] for k in ks)
+        floors[mode] = {"reads_MB": round(reads / 1e6, 1), "writes_MB": round(writes / 1e6, 1),
+                        "floor_us": round((reads / (rates["read"]["GB/s"] * 1e9)
+                                           + writes / (rates["write"]["GB/s"] * 1e9)) * 1e6, 1),
+                        "floor_us_at_peak": round((reads + writes) / HBM_PEAK * 1e6, 1)}
+    line = {"metric": "device streaming ceilings (GB/s) and the training step's algorithmic-byte floor",
+            "value": rates["copy"]["GB/s"], "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
+            "data": "synthetic", "config": {"workload": f"{mib} MiB streams; step floor of BASELINE config "
+                                                        f"{args.config}"},
+            "peak": HBM_PEAK / 1e9, "rates": rates, "step_floor": floors}
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -397,9 +516,14 @@ def main():
     ap.add_argument("--hv", type=int, default=16, choices=[16, 32], help="config 3's value heads")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
-    ap.add_argument("--recompute", action="store_true",
-                    help="the training forward keeps only its inputs and the backward reruns prep (op.RECOMPUTE_STATES "
-                         "= True, the reference's default); without it the forward keeps prep's operands")
+    ap.add_argument("--stored", action="store_true",
+                    help="headline the stored-states mode (the forward keeps prep's operands and the chunk states, "
+                         "op.RECOMPUTE_STATES = False) instead of the reference's default, where the backward reruns "
+                         "prep and recomputes the chunk states; the other mode is always reported beside it")
+    ap.add_argument("--recompute", action="store_true", help="the default (kept for old command lines)")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="measure the device's streaming read / write / copy rates and the config's step floor at "
+                         "those rates instead of the rule")
     ap.add_argument("--grouped", action="store_true",
                     help="configs with Hk < Hv: q and k go to the rule unrepeated (grouped value heads); without "
                          "it the "
@@ -418,6 +542,9 @@ def main():
         print("bench.py measures one GPU: the gated delta rule has no cross-GPU step in this build "
               "(head/batch sharding needs no collective); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.ceilings:
+        bench_ceilings(args)
+        return
     if args.producers:
         bench_producers(args.config)
         return
@@ -466,9 +593,84 @@ def main():
         return torch.autograd.grad(o, leaves, do)
 
     from macai.gated_delta import op
-    if args.recompute:
-        op.RECOMPUTE_STATES = True
-    keep = not op.RECOMPUTE_STATES
+    default_mode = op.RECOMPUTE_STATES
+    modes = [not args.stored, args.stored]           # headline first, then the other mode as a second field
+    runs = []
+    try:
+        for recompute in modes:
+            op.RECOMPUTE_STATES = recompute
+            runs.append(_time_step(step, args))
+    finally:
+        op.RECOMPUTE_STATES = default_mode
+    (sec, in_step), (sec_other, in_step_other) = runs
+    keep = args.stored
+    B, T, H, DK, DV = c["B"], c["T"], c["Hv"], c["DK"], c["DV"]
+    tokens = B * T
+
+    # each pass alone at the batched layout; packed rows (whose per-sequence chunking those launches do not follow)
+    # report the in-step times only
+    rows = B * H if not args.packed else (len(kw["cu_seqlens"]) - 1) * H
+    if args.packed or args.no_alone:
+        alone, split = {}, op.split_for(rows, T, DV)
+    else:
+        alone, split = time_kernels(inp, keep=keep)
+    if args.copy_mib:
+        src = torch.ones(args.copy_mib << 18, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+    chunks = None
+    if args.packed:
+        cu = kw["cu_seqlens"].tolist()
+        chunks = sum(math.ceil((b - a) / C) for a, b in zip(cu, cu[1:]))
+    cost = kernel_costs(B, T, H, DK, DV, Hk=c["Hk"] if args.grouped else None, chunks=chunks, keep=keep)
+    traffic = measured_traffic(args.config, "stored" if keep else "recompute") if not args.packed else {}
+    kernels = {}
+    for name, t in in_step.items():
+        bw = cost[name]["bytes"] / t
+        fl = cost[name]["flops"] / t
+        kernels[name] = {"us": round(t * 1e6, 2), "us_alone": round(alone[name] * 1e6, 2) if name in alone else None,
+                         "GB/s": round(bw / 1e9, 1), "hbm_frac": round(bw / HBM_PEAK, 4),
+                         "TFLOP/s": round(fl / 1e12, 2), "mfma_frac": round(fl / MFMA_PEAK["bf16"], 4),
+                         "traffic": traffic.get(name)}
+    dom = max(in_step, key=in_step.get)
+    bw = cost[dom]["bytes"] / in_step[dom]
+    roof = {"kernel": dom, "timing": "in-step HIP events", "bound": "hbm", "achieved": round(bw / 1e9, 1),
+            "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": round(bw / HBM_PEAK, 4), "traffic": traffic.get(dom),
+            "algorithmic_bytes": cost[dom]["bytes"], "traffic_source": traffic.get("_source")}
+    value = tokens / sec
+    other_cost = kernel_costs(B, T, H, DK, DV, Hk=c["Hk"] if args.grouped else None, chunks=chunks, keep=not keep)
+    other = {"recompute_prep_in_backward": keep, "ms_per_step": round(sec_other * 1e3, 4),
+             "tokens_per_s": round(tokens / sec_other, 1),
+             "kernels": {n: {"us": round(t * 1e6, 2), "hbm_frac": round(other_cost[n]["bytes"] / t / HBM_PEAK, 4)}
+                         for n, t in in_step_other.items()}}
+    line = {"metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 4), "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": round(value / PUBLISHED, 2) if args.config == 1 and not keep and not args.packed else None,
+            "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": f"gated-delta drop-in fwd+bwd, BASELINE config {args.config}", "B": B, "T": T,
+                       "Hk": c["Hk"], "Hv": H, "DK": DK, "DV": DV, "chunk": C, "l2norm_in_kernel": True,
+                       "qk_heads_to_the_rule": c["Hk"] if args.grouped else H,
+                       "packed_rows": None if not args.packed else {"mode": args.packed,
+                                                                     "sequences": len(kw["cu_seqlens"]) - 1,
+                                                                     "chunks_per_head": chunks},
+                       "initial_state": c["s0"], "value_split": split,
+                       "pair_split": None if keep else op.split_for(rows, T, DV, 2),
+                       "overlapped_state_passes": (not keep) and op.OVERLAP, "recompute_prep_in_backward": not keep},
+            "roofline": roof, "kernels": kernels,
+            "stored_states" if not keep else "recompute_states": other}
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(args.config, args.cpu_threads)
+    print(json.dumps(line), flush=True)
+
+
+def _time_step(step, args):
+    """(seconds per step, {pass: seconds in the step}) for the current op settings: W warm-up steps, K steps timed
+    with HIP events and the wall clock (the larger counts), then up to 20 further identical steps with HIP events on
+    the launch stream around every launch (op.EVENTS; an event record costs the stream ~4 us, so the timed steps
+    carry none)."""
+    from macai.gated_delta import op
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -481,73 +683,17 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     gpu = e0.elapsed_time(e1) * 1e-3
-    # every pass timed in the step: HIP events on the launch stream around each launch, over further steps identical
-    # to the timed ones (an event record costs the stream ~4 us, so the timed steps above carry none)
     op.EVENTS = []
-    for _ in range(min(args.steps, 20)):
-        step()
-    torch.cuda.synchronize()
-    in_step = {}
-    for name, a, b in op.EVENTS:
-        in_step.setdefault(name, []).append(a.elapsed_time(b) * 1e-3)
-    op.EVENTS = None
-    in_step = {name: sum(ts) / len(ts) for name, ts in in_step.items()}
-    elapsed = max(wall, gpu)
-    B, T, H, DK, DV = c["B"], c["T"], c["Hv"], c["DK"], c["DV"]
-    tokens = B * T
-    ms = elapsed / args.steps * 1e3
-
-    # each pass alone at the batched layout; packed rows (whose per-sequence chunking those launches do not follow)
-    # report the in-step times only
-    rows = B * H if not args.packed else (len(kw["cu_seqlens"]) - 1) * H
-    if args.packed or args.no_alone:
-        alone, split = {}, op.split_for(rows, T, DV)
-    else:
-        alone, split = time_kernels(inp, keep=keep)
-    ktime = dict(in_step)                # the passes as the step runs them
-    if args.copy_mib:
-        src = torch.ones(args.copy_mib << 18, device=dev)
-        dst = torch.empty_like(src)
-        dst.copy_(src)
+    try:
+        for _ in range(min(args.steps, 20)):
+            step()
         torch.cuda.synchronize()
-    chunks = None
-    if args.packed:
-        cu = kw["cu_seqlens"].tolist()
-        chunks = sum(math.ceil((b - a) / C) for a, b in zip(cu, cu[1:]))
-    cost = kernel_costs(B, T, H, DK, DV, Hk=c["Hk"] if args.grouped else None, chunks=chunks, keep=keep)
-    # rocprof traffic was measured on the batched layout with the forward keeping prep's operands
-    traffic = {} if args.packed or not keep else TRAFFIC.get(args.config, {})
-    kernels = {}
-    for name, t in ktime.items():
-        bw = cost[name]["bytes"] / t
-        fl = cost[name]["flops"] / t
-        kernels[name] = {"us": round(t * 1e6, 2), "us_alone": round(alone[name] * 1e6, 2) if name in alone else None,
-                         "GB/s": round(bw / 1e9, 1), "hbm_frac": round(bw / HBM_PEAK, 4),
-                         "TFLOP/s": round(fl / 1e12, 2), "mfma_frac": round(fl / MFMA_PEAK["bf16"], 4),
-                         "traffic": traffic.get(name)}
-    dom = max(ktime, key=ktime.get)
-    bw = cost[dom]["bytes"] / ktime[dom]
-    roof = {"kernel": dom, "timing": "in-step HIP events", "bound": "hbm", "achieved": round(bw / 1e9, 1),
-            "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-            "frac": round(bw / HBM_PEAK, 4), "traffic": traffic.get(dom)}
-    line = {"metric": METRIC, "value": round(tokens / (elapsed / args.steps), 1), "unit": "tokens/s", "n_gpus": 1,
-            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
-            "scaling": "weak", "vs_baseline": round(tokens / (elapsed / args.steps) / PUBLISHED, 2)
-            if args.config == 1 else None,
-            "dtype": "bf16", "data": "synthetic",
-            "config": {"workload": f"gated-delta drop-in fwd+bwd, BASELINE config {args.config}", "B": B, "T": T,
-                       "Hk": c["Hk"], "Hv": H, "DK": DK, "DV": DV, "chunk": C, "l2norm_in_kernel": True,
-                       "qk_heads_to_the_rule": c["Hk"] if args.grouped else H,
-                       "packed_rows": None if not args.packed else {"mode": args.packed,
-                                                                     "sequences": len(kw["cu_seqlens"]) - 1,
-                                                                     "chunks_per_head": chunks},
-                       "initial_state": c["s0"], "value_split": split, "overlap_split": op.split_for(rows, T, DV, 2),
-                       "overlapped_state_passes": op.OVERLAP, "recompute_prep_in_backward": not keep},
-            "roofline": roof, "kernels": kernels}
-    if not args.no_cpu:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        line["cpu_baseline"] = cpu_baseline(args.config, threads)
-    print(json.dumps(line), flush=True)
+        in_step = {}
+        for name, a, b in op.EVENTS:
+            in_step.setdefault(name, []).append(a.elapsed_time(b) * 1e-3)
+    finally:
+        op.EVENTS = None
+    return max(wall, gpu) / args.steps, {name: sum(ts) / len(ts) for name, ts in in_step.items()}
 
 
 if __name__ == "__main__":

@@ -50,7 +50,7 @@
 extern "C" {
 #endif
 
-#define MACAI_GDR_ABI_VERSION 9
+#define MACAI_GDR_ABI_VERSION 10
 
 /* dtype codes (the rule takes F32 and BF16; the producers also F16) */
 #define MACAI_GDR_F32 0
@@ -120,6 +120,21 @@ int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float
                         int64_t H, int64_t Hk, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm,
                         float q_scale, const int32_t* pack, int64_t NT, void* stream);
 
+/* The inference forward in one call: macai_gdr_prep (without A) then macai_gdr_state_fwd with the output (flags 0),
+ * the per-chunk operands W, U, Ke, GL, Qg, M carved from `workspace` (256-byte aligned, at least
+ * macai_gdr_forward_workspace(...) bytes; its contents on entry do not matter).  o [B, T, H, DV] in dtype and sT (or
+ * NULL) as macai_gdr_state_fwd writes them; split 0 = automatic (the smallest split giving every CU a workgroup with
+ * at most four column waves a workgroup).  The same kernels and bits as the two calls.  Replaces the drop-in's
+ * no-grad forward, the reference's `_prep` + `lib.gdc_fwd(..., flags 0)` (op.py:63-72, 159). */
+int macai_gdr_forward(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                      const float* s0, void* o, float* sT, void* workspace, int64_t workspace_bytes, int64_t B,
+                      int64_t T, int64_t H, int64_t Hk, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm,
+                      float q_scale, int32_t split, const int32_t* pack, int64_t NT, void* stream);
+
+/* Bytes of macai_gdr_forward's workspace for a shape (NT = the packed-row chunk count, or 0 for B rows of T). */
+int64_t macai_gdr_forward_workspace(int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV, int32_t dtype,
+                                    int64_t NT);
+
 /* One recurrent step per sequence (T = 1): q, k [B, 1, Hk, DK], v [B, 1, H, DV] dtype; g, beta [B, 1, H] float32;
  * s_in, s_out [B, H, DK, DV] float32 (s_out may equal s_in).  S' = e^g S + k beta (v - e^g S^T k)^T, o = S'^T q.  The
  * math of the reference's recurrence (op.py:308-313) and of transformers' torch_recurrent_gated_delta_rule
@@ -170,6 +185,13 @@ int macai_gdr_gates_fwd(const void* b, const void* a, const float* A_log, const 
 int macai_gdr_gates_bwd(const void* b, const void* a, const float* A_log, const float* dt_bias, const float* dbeta,
                         const float* dg, void* db, void* da, float* dA_log, float* ddt_bias, int64_t n, int64_t H,
                         int32_t dtype, void* stream);
+
+/* ---- measurement ---- */
+
+/* A streaming probe of the device's memory ceilings (no counterpart in the reference; bench.py --ceilings): mode 0
+ * reads `bytes` from src (dst: a 16-byte sink, written by practically no lane), 1 writes them to dst, 2 copies src to
+ * dst; 16-byte units, grid-stride over `blocks` workgroups of 256 lanes. */
+int macai_gdr_probe_stream(int32_t mode, const void* src, void* dst, int64_t bytes, int32_t blocks, void* stream);
 
 #ifdef __cplusplus
 }

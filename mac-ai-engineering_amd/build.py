@@ -5,7 +5,7 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-SRCS = [os.path.join(HERE, "csrc", f) for f in ("gdr_kernels.hip", "gdr_producers.hip")]
+SRCS = [os.path.join(HERE, "csrc", f) for f in ("gdr_kernels.hip", "gdr_forward.hip", "gdr_producers.hip", "gdr_probe.hip")]
 OUT = os.path.join(HERE, "macai", "gated_delta", "libmacai_gdr.so")
 ARCH = os.environ.get("MACAI_GPU_ARCH", "gfx950")
 

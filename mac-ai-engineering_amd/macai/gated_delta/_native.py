@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 F32, BF16, F16 = 0, 1, 2
 OK, EINVAL, EUNSUP, ELAUNCH = 0, 1, 2, 3
 STORE_STATES, NO_OUTPUT = 1, 8
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _p, _i64, _i32, _f = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 # name -> argument types (the order of include/macai_gdr.h)
@@ -31,8 +31,12 @@ SIGNATURES = {
     "macai_gdr_conv_partials": [_i64] * 3,
     "macai_gdr_gates_fwd": [_p] * 6 + [_i64] * 2 + [_i32, _p],
     "macai_gdr_gates_bwd": [_p] * 10 + [_i64] * 2 + [_i32, _p],
+    "macai_gdr_forward": [_p] * 9 + [_i64] * 7 + [_i32, _i32, _f, _i32, _p, _i64, _p],
+    "macai_gdr_forward_workspace": [_i64] * 5 + [_i32, _i64],
+    "macai_gdr_probe_stream": [_i32, _p, _p, _i64, _i32, _p],
 }
-RESTYPES = {"macai_gdr_conv_partials": _i64}     # the rest return an int status
+# the rest return an int status
+RESTYPES = {"macai_gdr_conv_partials": _i64, "macai_gdr_forward_workspace": _i64}
 
 _lib = None
 _fns = {}        # name -> the library's function object (a lookup per call costs host time on every launch)

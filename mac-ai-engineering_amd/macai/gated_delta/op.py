@@ -20,7 +20,9 @@ CHUNK = 64   # chunk length of the kernels; the drop-in's chunk_size is accepted
 # VALUE_SPLIT: workgroups a head-row's value columns are split over in the state passes (each owns DV / VALUE_SPLIT
 # columns as DV / 16 / VALUE_SPLIT waves of 16 columns): "auto" (split_for) or 1, 2, 4, 8, ...
 VALUE_SPLIT = "auto"
-# the passes' calls by what they ran, "fwd s<split>" / "bwd s<split>" (counted at every call; no GPU work)
+# the passes' calls by what they ran, "fwd s<split>" / "bwd <state passes> s<split>" with <state passes> "pair"
+# (recompute and reverse pass in one launch), "recompute+reverse" (two launches) or "reverse" (the forward kept the
+# states); counted at every call, no GPU work
 CALLS = collections.Counter()
 # Measurement hook: set to a list to record (pass, start event, end event) around every launch, on the launch stream;
 # None (the default) records nothing.
@@ -29,14 +31,16 @@ EVENTS = None
 # OVERLAP they run in one launch (macai_gdr_state_pair), each on about half the CUs.  Both are sequential chunk chains
 # whose speed hardly depends on how many CUs they get, so this nearly hides one of them.
 OVERLAP = True
-# RECOMPUTE_STATES (the reference's switch, op.py:27-33; outputs and gradients have the same bits either way):
-# False (the default here) -- the training forward runs prep in its backward mode (A as well) and its state pass
-# stores the chunk states S_c and Vn beside the output; it keeps those and prep's per-chunk operands W, U, Ke, Qg, M,
-# GL, A for the backward, which then runs only the reverse state pass and the per-chunk backward.  At D = 128 in bf16
-# that is 2,816 bytes per token-head, 11x q's (176 MiB a layer at B = 4, T = 1024, H = 16): room a 288 GB part has.
-# True -- the forward keeps only its inputs and the backward recomputes prep and the chunk states (the reference's
-# default, chosen there for the Metal allocator's footprint).
-RECOMPUTE_STATES = False
+# RECOMPUTE_STATES (the reference's switch and default, op.py:27-33; outputs and gradients have the same bits either
+# way):
+# True (the default) -- the training forward keeps only its inputs; the backward reruns prep (with A) and recomputes
+# the chunk states S_c and Vn beside its reverse pass (macai_gdr_state_pair).
+# False -- the training forward runs prep in its backward mode (A as well) and its state pass stores S_c and Vn beside
+# the output; it keeps those and prep's per-chunk operands W, U, Ke, Qg, M, GL, A for the backward, which then runs
+# only the reverse state pass and the per-chunk backward.  At D = 128 in bf16 that is 2,816 bytes per token-head, 11x
+# q's (176 MiB a layer at B = 4, T = 1024, H = 16), in one allocation saved with save_for_backward (so saved-tensor
+# hooks, activation checkpointing and offload see it and it goes with the graph).
+RECOMPUTE_STATES = True
 
 
 def _launch(name: str, entry: str, *args):
@@ -168,10 +172,8 @@ def _on(dev):
 _LAYOUTS = {}    # scratch layouts by shape: (part offsets, total bytes)
 
 
-def _carve(dev, shape):
-    """One allocation for the per-chunk scratch of a call, `shape` = (Bc, H, NT, DK, DV, element size, prep, with_A,
-    states, grads) as _scratch_sizes takes it.  Returns {name: device address or None, "buf": the allocation}; every
-    part starts on a 256-byte boundary.  The kernels take raw addresses, so the parts need no tensor views."""
+def _layout(shape):
+    """(part offsets, total bytes) of the scratch for `shape`; every part starts on a 256-byte boundary."""
     lay = _LAYOUTS.get(shape)
     if lay is None:
         offs, total = {}, 0
@@ -179,12 +181,24 @@ def _carve(dev, shape):
             offs[name] = total if n else None
             total += (n + 255) & ~255
         lay = _LAYOUTS[shape] = (offs, max(total, 1))
-    offs, total = lay
-    buf = torch.empty(total, device=dev, dtype=torch.uint8)
+    return lay
+
+
+def _parts(buf, shape):
+    """{name: device address or None, "buf": buf, "shape": shape} for a scratch allocation of `shape`.  Addresses are
+    taken from buf each time, so a buffer that a saved-tensor hook moved and brought back is addressed where it is
+    now."""
     base = buf.data_ptr()
-    out = {name: (None if o is None else base + o) for name, o in offs.items()}
-    out["buf"] = buf
+    out = {name: (None if o is None else base + o) for name, o in _layout(shape)[0].items()}
+    out["buf"], out["shape"] = buf, shape
     return out
+
+
+def _carve(dev, shape):
+    """One allocation for the per-chunk scratch of a call, `shape` = (Bc, H, NT, DK, DV, element size, prep, with_A,
+    states, grads) as _scratch_sizes takes it.  Returns _parts of it.  The kernels take raw addresses, so the parts
+    need no tensor views."""
+    return _parts(torch.empty(_layout(shape)[1], device=dev, dtype=torch.uint8), shape)
 
 
 def _scratch_sizes(Bc, H, NT, DK, DV, es, prep: bool, with_A: bool, states: bool, grads: bool):
@@ -265,7 +279,7 @@ def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=
                 None, Sc, Vn, B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, *pk, stream)
         _launch("state_bwd", "macai_gdr_state_bwd", r["Ke"], r["Qg"], r["W"], r["M"], r["GL"], P(do), P(dsT), dSn, dVn,
                 P(ds0), B, T, H, DK, DV, code, split, *pk, stream)
-    CALLS[f"bwd s{split}"] += 1
+    CALLS[f"bwd {'reverse' if kept else 'pair' if OVERLAP else 'recompute+reverse'} s{split}"] += 1
     if Hk == H:
         dqh, dkh = torch.empty_like(q), torch.empty_like(k)
     else:
@@ -283,6 +297,19 @@ def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=
     return dq, dk, dv, dg, dbeta, ds0
 
 
+def _save(ctx, inputs, r):
+    """Save the inputs and, when the forward kept its per-chunk scratch (RECOMPUTE_STATES False), that allocation
+    with them: save_for_backward hands both to saved-tensor hooks and frees them with the graph."""
+    ctx.save_for_backward(*inputs, None if r is None else r["buf"])
+    ctx.kept_shape = None if r is None else r["shape"]
+
+
+def _saved(ctx):
+    """(inputs, the kept scratch's parts or None) from _save."""
+    *inputs, buf = ctx.saved_tensors
+    return inputs, (None if buf is None else _parts(buf, ctx.kept_shape))
+
+
 class GatedDeltaRule(torch.autograd.Function):
     """o, S_T = recurrence(q, k, v, g, beta, S_0) on [B, T, H, D] tensors (q already normalised and scaled): the
     reference's contract (op.py:116-257).  q and k may also have fewer heads Hk dividing H (grouped value heads,
@@ -296,18 +323,18 @@ class GatedDeltaRule(torch.autograd.Function):
         q, k, v, g, beta, s0 = (t.contiguous() for t in (q, k, v, g, beta, s0))
         keep = save and not RECOMPUTE_STATES
         with _on(q.device):
-            o, sT, ctx.prep = _forward(q, k, v, g, beta, s0, False, 1.0, True, keep=keep)
+            o, sT, r = _forward(q, k, v, g, beta, s0, False, 1.0, True, keep=keep)
         if save:
-            ctx.save_for_backward(q, k, v, g, beta, s0)
+            _save(ctx, (q, k, v, g, beta, s0), r)
         return o, sT
 
     @staticmethod
     def backward(ctx, do, dsT):
-        q, k, v, g, beta, s0 = ctx.saved_tensors
+        (q, k, v, g, beta, s0), r = _saved(ctx)
         do = torch.zeros_like(v) if do is None else _as(do, v.dtype)
         dsT = None if dsT is None else _as(dsT, torch.float32)
         with _on(q.device):
-            dq, dk, dv, dg, dbeta, ds0 = _backward(q, k, v, g, beta, s0, do, dsT, False, 1.0, r=ctx.prep)
+            dq, dk, dv, dg, dbeta, ds0 = _backward(q, k, v, g, beta, s0, do, dsT, False, 1.0, r=r)
         return dq, dk, dv, dg, dbeta, ds0, None
 
 
@@ -322,9 +349,9 @@ class _DropIn(torch.autograd.Function):
                 pack=None):
         keep = save and not RECOMPUTE_STATES
         with _on(query.device):
-            o, sT, ctx.prep = _forward(query, key, value, g, beta, s0, l2norm, q_scale, want_sT, pack, keep)
+            o, sT, r = _forward(query, key, value, g, beta, s0, l2norm, q_scale, want_sT, pack, keep)
         if save:
-            ctx.save_for_backward(query, key, value, g, beta, s0)
+            _save(ctx, (query, key, value, g, beta, s0), r)
             ctx.cfg = (l2norm, q_scale, s0 is not None)
             ctx.pack = pack
         if sT is None:
@@ -333,13 +360,12 @@ class _DropIn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, do, dsT=None):
-        query, key, value, g, beta, s0 = ctx.saved_tensors
+        (query, key, value, g, beta, s0), r = _saved(ctx)
         l2norm, q_scale, has_s0 = ctx.cfg
         do = torch.zeros_like(value) if do is None else _as(do, value.dtype)
         dsT = None if dsT is None else _as(dsT, torch.float32)
         with _on(query.device):
-            dq, dk, dv, dg, dbeta, ds0 = _backward(query, key, value, g, beta, s0, do, dsT, l2norm, q_scale, ctx.pack,
-                                                   ctx.prep)
+            dq, dk, dv, dg, dbeta, ds0 = _backward(query, key, value, g, beta, s0, do, dsT, l2norm, q_scale, ctx.pack, r)
         return dq, dk, dv, dg, dbeta, (ds0 if has_s0 else None), None, None, None, None, None
 
 
@@ -358,7 +384,9 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size: int = 64, ini
     kernels. Returns the output [B, T, H, DV] in the query's dtype and the final state (float32) when
     output_final_state, else None.  chunk_size is accepted and unused (the kernels use 64-token chunks).  bfloat16
     inputs run on bf16 MFMA with fp32 accumulation and an fp32 state; float32 inputs on fp32 MFMA; float16 inputs
-    are computed as float32."""
+    are upcast exactly and computed as float32, the output cast back to float16 (the reference does the same: its
+    prologue and `value.float()` run the rule in float32, op.py:276-285, 297).  With use_qk_l2norm_in_kernel=False
+    the query is only scaled by DK^-1/2 (op.py:279-283), inside the kernels."""
     cu = kwargs.get("cu_seqlens")
     pack = None if cu is None else _pack(cu, query.shape[1], query.device)
     dtype = query.dtype
@@ -408,16 +436,15 @@ def recurrent_gated_delta_rule(query, key, value, g, beta, initial_state=None, o
 
 
 def recurrent_reference(q, k, v, g, beta, s0):
-    """The recurrence step by step in plain PyTorch ([B, T, H, D] inputs, q already normalised and scaled): the
-    reference's parity helper (op.py:301-314), kept for API compatibility.  No kernel path calls it."""
-    B, T, H, DK = q.shape
-    s = s0.clone()
-    outs = []
-    for t in range(T):
-        a = g[:, t].exp()[..., None, None]
-        st = s * a
-        u = (st * k[:, t, :, :, None]).sum(-2)
-        d = beta[:, t, :, None] * (v[:, t] - u)
-        s = st + k[:, t, :, :, None] * d[:, :, None, :]
-        outs.append((s * q[:, t, :, :, None]).sum(-2))
-    return torch.stack(outs, 1), s
+    """The rule one token at a time in plain PyTorch, for [B, T, H, D] inputs with q already normalised and scaled:
+    per token the state decays by e^g, the prediction k^T S is corrected towards v by beta, and the output reads the
+    updated state with q.  Kept for callers of the reference's helper of this name (op.py:301-314); no kernel path
+    calls it.  Returns (o [B, T, H, DV], S_T)."""
+    state = s0.clone()
+    steps = []
+    for qt, kt, vt, gt, bt in zip(q.unbind(1), k.unbind(1), v.unbind(1), g.unbind(1), beta.unbind(1)):
+        state = state * torch.exp(gt)[:, :, None, None]
+        miss = (vt - torch.matmul(kt.unsqueeze(-2), state).squeeze(-2)) * bt.unsqueeze(-1)
+        state = state + kt.unsqueeze(-1) * miss.unsqueeze(-2)
+        steps.append(torch.matmul(qt.unsqueeze(-2), state).squeeze(-2))
+    return torch.stack(steps, 1), state

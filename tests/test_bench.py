@@ -50,3 +50,35 @@ def test_decode_bytes():
     state = 64 * 32 * 128 * 128 * 4
     assert b == 2 * state + 64 * (2 * 16 * 128 + 2 * 32 * 128) * 2 + 64 * 32 * 8
     assert round(2 * state / 1e6, 1) == 268.4
+
+
+def test_recompute_step_bytes_per_chunk_head():
+    """Config 1 as BASELINE specifies it (the backward recomputes): prep without A 136.5 KiB, the output-only state
+    pass 104.0 KiB, prep with A 144.5 KiB, the pair pass 296.0 KiB (recompute: W, Ke 16 KiB each, U 32 KiB, GL in;
+    S_c 64 KiB and Vn 16 KiB out; and the reverse pass's 152.0 KiB), the chunk backward 281.0 KiB; reads and writes
+    add up to the total."""
+    c = bench.CONFIGS[1]
+    cost = bench.kernel_costs(c["B"], c["T"], c["Hv"], c["DK"], c["DV"], keep=False)
+    n = c["B"] * c["Hv"] * (c["T"] // 64)
+    kib = {k: round(cost[k]["bytes"] / n / 1024, 1) for k in bench.step_kernels(False)}
+    assert kib == {"prep_fwd": 136.5, "state_fwd_out": 104.0, "prep_bwd": 144.5, "state_pair": 296.0,
+                   "chunk_bwd": 281.0}
+    for keep in (False, True):
+        for name, x in bench.kernel_costs(2, 100, 3, 128, 64, keep=keep, Hk=1).items():
+            assert x["reads"] + x["writes"] == x["bytes"], name
+
+
+def test_traffic_only_while_the_kernels_match(monkeypatch):
+    """Counter traffic is reported only for the kernel sources it was profiled on."""
+    fp = bench.kernel_fingerprint()
+    monkeypatch.setattr(bench, "TRAFFIC", {(1, "recompute"): {"sources": fp, "bytes": {"chunk_bwd": 1.0}}})
+    assert bench.measured_traffic(1, "recompute")["chunk_bwd"] == 1.0
+    assert "chunk_bwd" not in bench.measured_traffic(1, "stored")
+    monkeypatch.setattr(bench, "TRAFFIC", {(1, "recompute"): {"sources": "0" * 16, "bytes": {"chunk_bwd": 1.0}}})
+    t = bench.measured_traffic(1, "recompute")
+    assert "chunk_bwd" not in t and t["_source"].startswith("stale")
+
+
+def test_cpu_info():
+    model, physical, allowed, share = bench.cpu_info()
+    assert physical >= 1 and allowed >= 1 and share >= 1 and isinstance(model, str)

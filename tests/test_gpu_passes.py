@@ -64,3 +64,37 @@ def test_passes_bf16(shape):
     print(errs)
     bad = {n: e for n, e in errs.items() if not e < 1e-2}
     assert not bad, bad
+
+
+@pytest.mark.parametrize("shape,dtype,split", [((2, 150, 3, 3, 128, 128), torch.bfloat16, 0),
+                                               ((1, 100, 4, 2, 64, 64), torch.float32, 0),
+                                               ((4, 1024, 16, 16, 128, 128), torch.bfloat16, 0),
+                                               ((2, 77, 2, 2, 128, 96), torch.bfloat16, 3)])
+def test_one_call_forward_equals_the_two_passes(shape, dtype, split):
+    """macai_gdr_forward (prep and the output pass in one call, operands in a caller's workspace) gives the bits of
+    macai_gdr_prep + macai_gdr_state_fwd with the drop-in's own split, and of the drop-in's no-grad forward."""
+    from macai.gated_delta import _native as N
+    from macai.gated_delta import chunk_gated_delta_rule, op
+    B, T, H, Hk, DK, DV = shape
+    print("case one-call forward", shape, dtype, split, flush=True)
+    inp = gdr.make_inputs(B, T, Hk, H, DK, DV, dtype, s0=True, seed=31)
+    q, k = (inp[n][:, :, ::H // Hk].contiguous().cuda() for n in ("query", "key"))
+    v, g, beta, s0 = (inp[n].cuda() for n in ("value", "g", "beta", "initial_state"))
+    code, st, P = N.dtype_code(dtype), N.stream_of(q), N.ptr
+    nbytes = N.lib().macai_gdr_forward_workspace(B, T, H, DK, DV, code, 0)
+    ws = torch.full((nbytes,), 255, dtype=torch.uint8, device="cuda")
+    o = torch.full((B, T, H, DV), float("nan"), dtype=dtype, device="cuda")
+    sT = torch.full((B, H, DK, DV), float("nan"), device="cuda")
+    use = split or op.split_for(B * H, T, DV)
+    N.call("macai_gdr_forward", P(q), P(k), P(v), P(g), P(beta), P(s0), P(o), P(sT), P(ws), nbytes, B, T, H, Hk, DK,
+           DV, code, 1, DK ** -0.5, split, None, 0, st)
+    old = op.VALUE_SPLIT
+    try:
+        op.VALUE_SPLIT = use
+        with torch.no_grad():
+            ro, rsT = chunk_gated_delta_rule(q, k, v, g, beta, initial_state=s0, output_final_state=True,
+                                             use_qk_l2norm_in_kernel=True)
+    finally:
+        op.VALUE_SPLIT = old
+    torch.cuda.synchronize()
+    assert torch.equal(o, ro) and torch.equal(sT, rsT)

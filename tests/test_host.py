@@ -89,6 +89,27 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert gs(p + 4, p) == N.EINVAL and b"aligned" in L.macai_gdr_last_error()
 
 
+def test_forward_workspace_and_checks():
+    """macai_gdr_forward's workspace is the layout the Python host carves for the forward (prep's W, U, Ke, GL, Qg, M,
+    each on a 256-byte boundary); a short, misaligned or missing workspace is refused before any launch, and so are
+    the shapes macai_gdr_prep refuses."""
+    from macai.gated_delta import op
+    L = N.lib()
+    for (B, T, H, DK, DV, dt, nt) in [(4, 1024, 16, 128, 128, 1, 0), (2, 100, 3, 64, 32, 0, 0), (1, 300, 2, 128, 96, 1, 7)]:
+        es = 4 if dt == 0 else 2
+        Bc, NT = (1, nt) if nt else (B, -(-T // 64))
+        want = op._layout((Bc, H, NT, DK, DV, es, True, False, False, False))[1]
+        assert L.macai_gdr_forward_workspace(B, T, H, DK, DV, dt, nt) == want
+    p = 1 << 20
+    need = L.macai_gdr_forward_workspace(1, 64, 1, 128, 128, 1, 0)
+    fw = lambda ws, nbytes, DK=128: L.macai_gdr_forward(p, p, p, p, p, None, p, None, ws, nbytes, 1, 64, 1, 1, DK,
+                                                        128, 1, 1, 1.0, 0, None, 0, None)
+    assert fw(p, need - 1) == N.EINVAL and b"needs" in L.macai_gdr_last_error()
+    assert fw(p + 16, need) == N.EINVAL and b"256-byte" in L.macai_gdr_last_error()
+    assert fw(None, need) == N.EINVAL and b"workspace" in L.macai_gdr_last_error()
+    assert fw(p, 1 << 30, DK=96) == N.EUNSUP and b"key head width" in L.macai_gdr_last_error()
+
+
 def test_producer_abi_rejects_bad_arguments():
     """The convolution path's and the gates' entry points check shapes, dtype codes and pointers before any launch."""
     L = N.lib()
@@ -183,16 +204,37 @@ def test_patch_swaps_the_name_and_restores_it():
     import macai.patch as patch
     from macai.gated_delta import recurrent_gated_delta_rule
     orig, orig_dec = mod.torch_chunk_gated_delta_rule, mod.torch_recurrent_gated_delta_rule
-    with patch.installed(decode=True):
+    with patch.installed(layer=False, training=False, lora=False, decode=True):
         assert mod.torch_chunk_gated_delta_rule is chunk_gated_delta_rule
         assert mod.torch_recurrent_gated_delta_rule is recurrent_gated_delta_rule
     assert mod.torch_chunk_gated_delta_rule is orig and mod.torch_recurrent_gated_delta_rule is orig_dec
-    done = patch.install()
+    done = patch.install(layer=False, training=False, lora=False)
     try:
         assert ("transformers.models.qwen3_5.modeling_qwen3_5", patch.NAME) in done
         assert mod.torch_recurrent_gated_delta_rule is orig_dec
-        assert patch.install() == []           # idempotent
+        assert patch.install(layer=False, training=False, lora=False) == []           # idempotent
     finally:
+        patch.uninstall()
+    assert mod.torch_chunk_gated_delta_rule is orig
+
+
+def test_patch_takes_the_reference_keywords():
+    """The reference's call forms (patch.py:33, 92) work: the rule is installed, the layer / training / LoRA parts
+    (absent here) are reported absent by a RuntimeWarning once each and by the *_patches() helpers."""
+    mod = pytest.importorskip("transformers.models.qwen3_5.modeling_qwen3_5")
+    import warnings
+
+    import macai.patch as patch
+    orig = mod.torch_chunk_gated_delta_rule
+    patch._warned.clear()
+    with pytest.warns(RuntimeWarning, match="layer, training, lora"):
+        with patch.installed():
+            assert mod.torch_chunk_gated_delta_rule is chunk_gated_delta_rule
+            assert patch.layer_patches() == patch.training_patches() == patch.lora_patches() == []
+    assert mod.torch_chunk_gated_delta_rule is orig
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")          # warned once per part: a second install is silent
+        patch.install(layer=True, training=True, lora=True)
         patch.uninstall()
     assert mod.torch_chunk_gated_delta_rule is orig
 
