@@ -135,6 +135,18 @@ int macai_gdr_forward(const void* q, const void* k, const void* v, const float* 
 int64_t macai_gdr_forward_workspace(int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV, int32_t dtype,
                                     int64_t NT);
 
+/* macai_gdr_forward without a workspace argument and without allocating: no counterpart in the reference; for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The per-chunk operands live in a fixed device array of MACAI_GDR_NOALLOC_SCRATCH_BYTES, one per device,
+ * held for the process's lifetime; a shape whose operands (macai_gdr_forward_workspace) exceed it is refused with
+ * EINVAL before any launch.  Calls on one device share that array: calls that overlap on one device (different
+ * streams, or threads) race and must be serialised by the caller.  Same arguments and bits as macai_gdr_forward. */
+#define MACAI_GDR_NOALLOC_SCRATCH_BYTES ((int64_t)128 << 20)
+int macai_gdr_forward_noalloc(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                              const float* s0, void* o, float* sT, int64_t B, int64_t T, int64_t H, int64_t Hk,
+                              int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, int32_t split,
+                              const int32_t* pack, int64_t NT, void* stream);
+
 /* One recurrent step per sequence (T = 1): q, k [B, 1, Hk, DK], v [B, 1, H, DV] dtype; g, beta [B, 1, H] float32;
  * s_in, s_out [B, H, DK, DV] float32 (s_out may equal s_in).  S' = e^g S + k beta (v - e^g S^T k)^T, o = S'^T q.  The
  * math of the reference's recurrence (op.py:308-313) and of transformers' torch_recurrent_gated_delta_rule

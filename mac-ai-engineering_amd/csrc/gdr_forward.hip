@@ -1,8 +1,11 @@
 // The rule's inference forward in one call: prep, then the state pass with the output (and the final state), the two
-// launches the drop-in's forward makes without gradients, with the per-chunk operands in a workspace the caller
-// passes.  It goes through macai_gdr_prep and macai_gdr_state_fwd, so it runs the same kernels with the same arguments
-// as the separate calls: the same bits.
+// launches the drop-in's forward makes without gradients.  macai_gdr_forward takes the per-chunk operands' workspace
+// from the caller; macai_gdr_forward_noalloc takes it from a fixed device array of this file instead, for callers that
+// cannot allocate (HIP graph capture, serving loops).  Both go through macai_gdr_prep and macai_gdr_state_fwd, so they
+// run the same kernels with the same arguments as the separate calls: the same bits.
 #include <hip/hip_runtime.h>
+
+#include <mutex>
 
 #include "gdr_abi.h"
 
@@ -72,6 +75,36 @@ int forward_in(const char* what, const void* q, const void* k, const void* v, co
                              NT_packed, stream);
 }
 
+// The workspace of macai_gdr_forward_noalloc: one copy per device, held for the process's lifetime.  Host code reaches
+// it only through the address hipGetSymbolAddress returns on the current device (device_scratch), never by its name:
+// in host code the name stands for a host-side shadow, not device memory.  Every call on a device shares its copy,
+// and prep rewrites every byte the state pass then reads, so nothing in it needs clearing between calls.
+constexpr int64_t SCRATCH_BYTES = MACAI_GDR_NOALLOC_SCRATCH_BYTES;
+constexpr int MAX_DEVICES = 64;
+__device__ __align__(256) char scratch[SCRATCH_BYTES];
+
+std::mutex g_scratch_mu;
+void* g_scratch[MAX_DEVICES] = {};
+
+// The scratch array's address on the current device, looked up on the first call there.
+int device_scratch(const char* what, char** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MACAI_GDR_ELAUNCH, "%s: hipGetDevice failed: %s", what, hipGetErrorString(e));
+  if (dev < 0 || dev >= MAX_DEVICES) return fail(MACAI_GDR_EUNSUP, "%s: device %d out of range", what, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(MACAI_GDR_ELAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", what, dev,
+                  hipGetErrorString(e));
+    g_scratch[dev] = p;
+  }
+  *out = (char*)g_scratch[dev];
+  return MACAI_GDR_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -88,6 +121,26 @@ int macai_gdr_forward(const void* q, const void* k, const void* v, const float* 
                       float q_scale, int32_t split, const int32_t* pack, int64_t NT_packed, void* stream) {
   return forward_in("macai_gdr_forward", q, k, v, g, beta, s0, o, sT, (char*)workspace, workspace_bytes, B, T, H, Hk,
                     DK, DV, dtype, use_l2norm, q_scale, split, pack, NT_packed, stream);
+}
+
+int macai_gdr_forward_noalloc(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                              const float* s0, void* o, float* sT, int64_t B, int64_t T, int64_t H, int64_t Hk,
+                              int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, int32_t split,
+                              const int32_t* pack, int64_t NT_packed, void* stream) {
+  const char* what = "macai_gdr_forward_noalloc";
+  if (B >= 1 && T >= 1 && H >= 1 && DK >= 1 && DV >= 1 && (!pack || NT_packed >= 1)) {
+    int64_t off[6];
+    const int64_t need = layout(B, T, H, DK, DV, dtype, pack ? NT_packed : 0, off);
+    if (need > SCRATCH_BYTES)
+      return fail(MACAI_GDR_EINVAL,
+                  "%s: this shape needs %lld bytes of per-chunk operands, over the fixed %lld-byte scratch; use "
+                  "macai_gdr_forward with a workspace",
+                  what, (long long)need, (long long)SCRATCH_BYTES);
+  }
+  char* ws = nullptr;
+  if (int rc = device_scratch(what, &ws)) return rc;
+  return forward_in(what, q, k, v, g, beta, s0, o, sT, ws, SCRATCH_BYTES, B, T, H, Hk, DK, DV, dtype, use_l2norm,
+                    q_scale, split, pack, NT_packed, stream);
 }
 
 }  // extern "C"

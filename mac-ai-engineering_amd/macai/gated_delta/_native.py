@@ -14,6 +14,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 F32, BF16, F16 = 0, 1, 2
 OK, EINVAL, EUNSUP, ELAUNCH = 0, 1, 2, 3
 STORE_STATES, NO_OUTPUT = 1, 8
+NOALLOC_SCRATCH_BYTES = 128 << 20     # MACAI_GDR_NOALLOC_SCRATCH_BYTES
 ABI_VERSION = 10
 
 _p, _i64, _i32, _f = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
@@ -33,6 +34,7 @@ SIGNATURES = {
     "macai_gdr_gates_bwd": [_p] * 10 + [_i64] * 2 + [_i32, _p],
     "macai_gdr_forward": [_p] * 9 + [_i64] * 7 + [_i32, _i32, _f, _i32, _p, _i64, _p],
     "macai_gdr_forward_workspace": [_i64] * 5 + [_i32, _i64],
+    "macai_gdr_forward_noalloc": [_p] * 8 + [_i64] * 6 + [_i32, _i32, _f, _i32, _p, _i64, _p],
     "macai_gdr_probe_stream": [_i32, _p, _p, _i64, _i32, _p],
 }
 # the rest return an int status

@@ -246,3 +246,13 @@ def test_product_never_imports_the_oracle():
             if f.endswith((".py", ".hip", ".h", ".cpp")):
                 text = open(os.path.join(dirpath, f)).read()
                 assert not re.search(r"^\s*(from|import)\s+oracle\b", text, re.M), f
+
+
+def test_noalloc_forward_refuses_oversized_shapes_before_any_launch():
+    """The fixed scratch's limit is checked on the host, before the device is touched."""
+    L = N.lib()
+    p = 1 << 20
+    assert L.macai_gdr_forward_workspace(8, 4096, 32, 128, 128, 1, 0) > N.NOALLOC_SCRATCH_BYTES
+    rc = L.macai_gdr_forward_noalloc(*([p] * 8), 8, 4096, 32, 32, 128, 128, 1, 1, 1.0, 0, None, 0, None)
+    assert rc == N.EINVAL and b"fixed" in L.macai_gdr_last_error()
+    assert L.macai_gdr_forward_workspace(4, 1024, 16, 128, 128, 1, 0) <= N.NOALLOC_SCRATCH_BYTES
