@@ -25,6 +25,8 @@
 #include <string.h>
 #include <stdarg.h>
 
+#include <type_traits>
+
 #include "gdr_abi.h"
 #include "gdr_common.h"
 #include "gdr_stage.h"
@@ -155,13 +157,17 @@ __device__ __forceinline__ Frag<MT> cvt(const Frag<float>& x, float s = 1.0f) {
 // ---------------------------------------------------------------------------------------------------------------------
 template <typename IT, typename MT, int DK>
 __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
-  constexpr int KP = DK + 8;   // pitch of [C][DK] tiles (elements)
+  // Key features are staged DKS at a time (DK = 256 in two passes), so the tiles fit LDS at every key width: the
+  // products over the key features accumulate across the passes, and W is formed a pass of columns at a time.
+  constexpr int DKS = DK > 128 ? 128 : DK;
+  constexpr int NPASS = DK / DKS;
+  constexpr int KP = DKS + 8;  // pitch of [C][DKS] tiles (elements)
   constexpr int CP = C + 8;    // pitch of [*][C] MT tiles
   constexpr int FP = C + 4;    // pitch of fp32 [C][C] tiles
-  constexpr int QSZ = (C * KP > DK * CP) ? C * KP : DK * CP;
+  constexpr int QSZ = (C * KP > DKS * CP) ? C * KP : DKS * CP;
   constexpr int KSZ = (C * KP > C * CP) ? C * KP : C * CP;
-  __shared__ __attribute__((aligned(16))) MT sK[KSZ];    // K^ rows; then (beta V)^T column blocks
-  __shared__ __attribute__((aligned(16))) MT sQ[QSZ];    // Q^ rows; then (beta gamma K^)^T
+  __shared__ __attribute__((aligned(16))) MT sK[KSZ];    // K^ rows (a pass of columns); then (beta V)^T blocks
+  __shared__ __attribute__((aligned(16))) MT sQ[QSZ];    // Q^ rows (a pass); then (beta gamma K^)^T (a pass)
   __shared__ __attribute__((aligned(16))) float sL[C * FP];
   __shared__ __attribute__((aligned(16))) float sA[C * FP];
   __shared__ ChunkScalars cs;
@@ -191,15 +197,22 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
   __syncthreads();
   if (threadIdx.x == 0) a.GL[bhc] = cs.gam[C - 1];
   const float qs = a.q_scale;
-  // K^ rows into LDS; diag(e) K^ rows out (row-major).  Q^ rows into LDS; diag(gamma) Q^ rows out.
-  {
-    MT* Ke = (MT*)a.Ke + bhc * C * DK;
-    MT* Qg = (MT*)a.Qg + bhc * C * DK;
-    constexpr int PR = DK / 8;
+
+  // K K^T and Q K^T on the lower 16 x 16 tiles (wave w owns row block w), accumulated over the passes of key columns.
+  // Each pass stages K^ and Q^ rows of its columns into LDS and writes diag(e) K^ and diag(gamma) Q^ out.
+  f4 kk[4], qk[4];
+#pragma unroll
+  for (int ni = 0; ni < 4; ++ni) kk[ni] = qk[ni] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int ps = 0; ps < NPASS; ++ps) {
+    const int cb = ps * DKS;               // the pass's first key column
+    if (ps) __syncthreads();               // the previous pass's products are done with the tiles
+    MT* Ke = (MT*)a.Ke + bhc * C * DK + cb;
+    MT* Qg = (MT*)a.Qg + bhc * C * DK + cb;
+    constexpr int PR = DKS / 8;
     for (int i = threadIdx.x; i < C * PR; i += blockDim.x) {
       const int r = i / PR, c8 = (i - r * PR) * 8, t = t0 + r;
       float x[8], y[8];
-      if (t < T) load8(k + (size_t)t * qk_pitch + c8, x);
+      if (t < T) load8(k + (size_t)t * qk_pitch + cb + c8, x);
       else
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = 0.f;
@@ -210,7 +223,7 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
       }
       store8(sK + r * KP + c8, y);
       store8(Ke + r * DK + c8, x);
-      if (t < T) load8(q + (size_t)t * qk_pitch + c8, x);
+      if (t < T) load8(q + (size_t)t * qk_pitch + cb + c8, x);
       else
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = 0.f;
@@ -222,47 +235,53 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
       store8(sQ + r * KP + c8, y);
       store8(Qg + r * DK + c8, x);
     }
-  }
-  __syncthreads();
-
-  // K K^T and Q K^T on the lower 16 x 16 tiles: wave w owns row block w.  L (strictly lower, fp32) into LDS; M out.
-  {
+    __syncthreads();
     const int mi = w;
+#pragma unroll
     for (int ni = 0; ni < 4; ++ni) {
-      f4 kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
       if (ni <= mi) {
 #pragma unroll
-        for (int p = 0; p < DK / 32; ++p) {
+        for (int p = 0; p < DKS / 32; ++p) {
           Frag<MT> bk = frag_k_raw(sK, KP, 16 * ni, 32 * p);
           Frag<MT> ak = frag_k_raw(sK, KP, 16 * mi, 32 * p);
-          mma(kk, ak, bk);
-          mma(qk, frag_k_raw(sQ, KP, 16 * mi, 32 * p), bk);
+          mma(kk[ni], ak, bk);
+          mma(qk[ni], frag_k_raw(sQ, KP, 16 * mi, 32 * p), bk);
         }
       }
+    }
+  }
+  // L (strictly lower, fp32) into LDS; M out
+  {
+    const int mi = w;
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) {
       const int col = 16 * ni + (l & 15);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * mi + 4 * j + r;
         const float gm = (row >= col) ? cs.decay(row, col) : 0.f;   // mask before the exponent
-        sL[row * FP + col] = (row > col) ? cs.beta[row] * kk[r] * gm : 0.f;
-        ((MT*)a.M)[bhc * C * C + row * C + col] = from_f<MT>((row >= col) ? qk[r] * gm : 0.f);
+        sL[row * FP + col] = (row > col) ? cs.beta[row] * kk[ni][r] * gm : 0.f;
+        ((MT*)a.M)[bhc * C * C + row * C + col] = from_f<MT>((row >= col) ? qk[ni][r] * gm : 0.f);
       }
     }
   }
   __syncthreads();
 
-  // (beta gamma K^)^T into LDS for W, from the raw rows (one rounding)
-  for (int i = threadIdx.x; i < C * (DK / 8); i += blockDim.x) {
-    const int r = i % C, c8 = (i / C) * 8, t = t0 + r;
-    float x[8];
-    if (t < T) load8(k + (size_t)t * qk_pitch + c8, x);
-    else
+  // (beta gamma K^)^T of key columns [cb, cb + DKS) into LDS for W, from the raw rows (one rounding)
+  auto stage_kT = [&](int cb) {
+    for (int i = threadIdx.x; i < C * (DKS / 8); i += blockDim.x) {
+      const int r = i % C, c8 = (i / C) * 8, t = t0 + r;
+      float x[8];
+      if (t < T) load8(k + (size_t)t * qk_pitch + cb + c8, x);
+      else
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = 0.f;
-    const float sb = rk[r] * cs.beta[r] * cs.gam[r];
+        for (int e = 0; e < 8; ++e) x[e] = 0.f;
+      const float sb = rk[r] * cs.beta[r] * cs.gam[r];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) sQ[(c8 + e) * CP + r] = from_f<MT>(x[e] * sb);
-  }
+      for (int e = 0; e < 8; ++e) sQ[(c8 + e) * CP + r] = from_f<MT>(x[e] * sb);
+    }
+  };
+  stage_kT(0);
 
   // A = (I + L)^-1.  Diagonal 16 x 16 blocks by forward substitution: wave 0, lane = (block l/16, column l%16).
   if (w == 0) {
@@ -291,9 +310,9 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
       f4 t = {0.f, 0.f, 0.f, 0.f};
       for (int m = bj; m < bi; ++m) {
 #pragma unroll
-        for (int kk = 0; kk < 16; kk += 4)
-          t = __builtin_amdgcn_mfma_f32_16x16x4f32(sL[(16 * bi + (l & 15)) * FP + 16 * m + kk + j],
-                                                   sA[(16 * m + kk + j) * FP + 16 * bj + (l & 15)], t, 0, 0, 0);
+        for (int kk2 = 0; kk2 < 16; kk2 += 4)
+          t = __builtin_amdgcn_mfma_f32_16x16x4f32(sL[(16 * bi + (l & 15)) * FP + 16 * m + kk2 + j],
+                                                   sA[(16 * m + kk2 + j) * FP + 16 * bj + (l & 15)], t, 0, 0, 0);
       }
       f4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -312,11 +331,18 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
     for (int p = 0; p < 2; ++p) af[p] = cvt<MT>(frag_k_f32(sA, FP, 16 * w, 32 * p));
     const int np = (16 * w + 15) / 32 + 1;
     MT* Wc = (MT*)a.W + bhc * C * DK;
-    for (int ni = 0; ni < DK / 16; ++ni) {
-      f4 acc = {0.f, 0.f, 0.f, 0.f};
-      for (int p = 0; p < np; ++p) mma(acc, af[p], frag_k_raw(sQ, CP, 16 * ni, 32 * p));
+    for (int ps = 0; ps < NPASS; ++ps) {
+      if (ps) {                            // the next pass of columns of (beta gamma K^)^T
+        __syncthreads();
+        stage_kT(ps * DKS);
+        __syncthreads();
+      }
+      for (int ni = 0; ni < DKS / 16; ++ni) {
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int p = 0; p < np; ++p) mma(acc, af[p], frag_k_raw(sQ, CP, 16 * ni, 32 * p));
 #pragma unroll
-      for (int r = 0; r < 4; ++r) Wc[(16 * w + 4 * j + r) * DK + 16 * ni + (l & 15)] = from_f<MT>(acc[r]);
+        for (int r = 0; r < 4; ++r) Wc[(16 * w + 4 * j + r) * DK + ps * DKS + 16 * ni + (l & 15)] = from_f<MT>(acc[r]);
+      }
     }
     // U = A (beta V), 64 value columns at a time staged transposed in sK
     float* Uc = a.U + bhc * C * DV;
@@ -694,9 +720,12 @@ struct StateFwdLds {
   static constexpr int SZ = O_M + (OUT ? GM::ELEMS : 0);
   // bf16 Vn leaves through per-wave row staging (store mode)
   static constexpr int STG = (STORE && sizeof(MT) == 2) ? NW * ColStage::ELEMS : 0;
-  static constexpr int NBUF = Buffers<SZ * (int)sizeof(MT), STG * (int)sizeof(MT)>::N;
+  // DIRECT: one stage of the chunk's tiles does not fit LDS (fp32 at DK = 256); the compute waves then read their
+  // fragments from global memory (L2) and the loader wave has nothing to do
+  static constexpr bool DIRECT = (SZ + STG) * (int)sizeof(MT) > LDS_BYTES;
+  static constexpr int NBUF = DIRECT ? 0 : Buffers<SZ * (int)sizeof(MT), STG * (int)sizeof(MT)>::N;
   static constexpr int O_STG = NBUF * SZ;
-  static constexpr int ELEMS = O_STG + STG;
+  static constexpr int ELEMS = (O_STG + STG) > 16 ? O_STG + STG : 16;
 };
 
 // The pass of workgroup f of the launch (see state_map), with `lds` the workgroup's LDS (StateFwdLds::ELEMS elements).
@@ -707,6 +736,10 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
   using GM = typename L::GM;
   constexpr int ND = DK / 16;
   constexpr int O_KE = L::O_KE, O_Q = L::O_Q, O_M = L::O_M, SZ = L::SZ, NBUF = L::NBUF;
+  constexpr bool DIRECT = L::DIRECT;
+  // the layouts the fragment readers see: the padded LDS tiles, or the dense global ones
+  using FW = std::conditional_t<DIRECT, Dense<MT, C, DK>, GW>;
+  using FM = std::conditional_t<DIRECT, Dense<MT, C, C>, GM>;
 
   const int T = a.T, H = a.H, DV = a.DV, NT = a.NT;
   int hr, slice;
@@ -719,6 +752,7 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
   const int tb = a.pack ? 0 : b;           // batch row of the token tensors
 
   if (w == NW) {
+    if constexpr (DIRECT) return;          // no copies: the compute waves pass no barrier in this mode
     // the loader wave: every asynchronous copy of the chunk tiles, one chunk ahead of the compute waves, so that their
     // issue (a CU's load path takes ~1K cycles for a chunk's tiles) never stalls the MFMA chain
     int offW[GW::per_wave(1)], offM[GM::per_wave(1)];
@@ -822,6 +856,11 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
     if (STORE) store_sc(c, S);
     if (NBUF == 1) lds_barrier();        // chunk c is in LDS
     const MT* st = lds + buf * SZ;
+    // the chunk's tiles: W, diag(e) K^, diag(gamma) Q^, M
+    const MT* tW = DIRECT ? (const MT*)a.W + bhc * C * DK : st;
+    const MT* tK = DIRECT ? (const MT*)a.Ke + bhc * C * DK : st + O_KE;
+    const MT* tQ = DIRECT ? (const MT*)a.Qg + bhc * C * DK : st + O_Q;
+    const MT* tM = DIRECT ? (const MT*)a.M + bhc * C * C : st + O_M;
 
     // The output pass (one wave per SIMD, registers to spare) reads every fragment that does not depend on S first, so
     // the LDS latency overlaps the conversions and the MFMAs, and runs the products k-block by k-block across their
@@ -833,11 +872,11 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-        for (int p = 0; p < ND / 2; ++p) fw[mi][p] = frag_tile<MT, GW>(st, 16 * mi, 32 * p);
+        for (int p = 0; p < ND / 2; ++p) fw[mi][p] = frag_tile<MT, FW>(tW, 16 * mi, 32 * p);
 #pragma unroll
       for (int di = 0; di < ND; ++di)
 #pragma unroll
-        for (int p = 0; p < 2; ++p) fk[di][p] = frag_tile_tr<MT, GW>(st + O_KE, 32 * p, 16 * di);
+        for (int p = 0; p < 2; ++p) fk[di][p] = frag_tile_tr<MT, FW>(tK, 32 * p, 16 * di);
     }
     // S as the B operand (k = state rows)
     Frag<MT> Sf[ND / 2];
@@ -856,7 +895,7 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-        for (int p = 0; p < ND / 2; ++p) mma(Vn[mi], frag_tile<MT, GW>(st, 16 * mi, 32 * p), Sf[p]);
+        for (int p = 0; p < ND / 2; ++p) mma(Vn[mi], frag_tile<MT, FW>(tW, 16 * mi, 32 * p), Sf[p]);
     }
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) Vn[mi] = U[mi] - Vn[mi];
@@ -877,7 +916,7 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
 #pragma unroll
       for (int di = 0; di < ND; ++di)
 #pragma unroll
-        for (int p = 0; p < 2; ++p) mma(Sn[di], frag_tile_tr<MT, GW>(st + O_KE, 32 * p, 16 * di), Vf[p]);
+        for (int p = 0; p < 2; ++p) mma(Sn[di], frag_tile_tr<MT, FW>(tK, 32 * p, 16 * di), Vf[p]);
     }
     if (OUT) {
       // O = diag(gamma) Q S + M Vn (M lower triangular: k-blocks past the row block are zero)
@@ -885,10 +924,10 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) {
 #pragma unroll
-        for (int p = 0; p < ND / 2; ++p) fq[mi][p] = frag_tile<MT, GW>(st + O_Q, 16 * mi, 32 * p);
+        for (int p = 0; p < ND / 2; ++p) fq[mi][p] = frag_tile<MT, FW>(tQ, 16 * mi, 32 * p);
 #pragma unroll
         for (int p = 0; p < 2; ++p)
-          if (32 * p <= 16 * mi + 15) fm[mi][p] = frag_tile<MT, GM>(st + O_M, 16 * mi, 32 * p);
+          if (32 * p <= 16 * mi + 15) fm[mi][p] = frag_tile<MT, FM>(tM, 16 * mi, 32 * p);
       }
       // O^T = S^T (diag(gamma) Q)^T + Vn^T M^T: the same fragments with A and B swapped
       f4 pO[4];
@@ -907,7 +946,7 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
     }
 #pragma unroll
     for (int di = 0; di < ND; ++di) S[di] = Sn[di];
-    lds_barrier();                       // end of chunk c: the next chunk is in, this buffer may be refilled
+    if constexpr (!DIRECT) lds_barrier();   // end of chunk c: the next chunk is in, this buffer may be refilled
   }
   if (a.sT) {
 #pragma unroll
@@ -1176,7 +1215,9 @@ struct StateBwdLds {
   static constexpr int SZ = O_O + GO::ELEMS;
   static constexpr int STG = sizeof(MT) == 2 ? NW * ColStage::ELEMS : 0;   // bf16 dVn leaves through row staging
   static constexpr int SCAL = 32 / (int)sizeof(MT);   // per stage: the chunk's G_last (bits), t0, tend, as 4 ints
-  static constexpr int NBUF = Buffers<SZ * (int)sizeof(MT), (STG + SCAL) * (int)sizeof(MT) + TOUCH_SINK>::N;
+  // DIRECT: one stage does not fit LDS (fp32 at DK = 256): the compute waves read the tiles from global memory
+  static constexpr bool DIRECT = (SZ + STG + SCAL) * (int)sizeof(MT) + TOUCH_SINK > LDS_BYTES;
+  static constexpr int NBUF = DIRECT ? 0 : Buffers<SZ * (int)sizeof(MT), (STG + SCAL) * (int)sizeof(MT) + TOUCH_SINK>::N;
   static constexpr int O_STG = NBUF * SZ, O_SCAL = O_STG + STG;
   static constexpr int ELEMS = O_SCAL + SCAL;
 };
@@ -1189,6 +1230,9 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
   using GO = typename L::GO;
   constexpr int ND = DK / 16;
   constexpr int O_Q = L::O_Q, O_W = L::O_W, O_M = L::O_M, O_O = L::O_O, SZ = L::SZ, NBUF = L::NBUF;
+  constexpr bool DIRECT = L::DIRECT;
+  using FK = std::conditional_t<DIRECT, Dense<MT, C, DK>, GK>;
+  using FM = std::conditional_t<DIRECT, Dense<MT, C, C>, GM>;
 
   const int T = a.T, H = a.H, DV = a.DV, NT = a.NT;
   int hr, slice;
@@ -1203,6 +1247,7 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
   const size_t o_base = ((size_t)tb * T * H + h) * DV, o_pitch = (size_t)H * DV;
 
   if (w == NW) {
+    if constexpr (DIRECT) return;          // no copies: the compute waves pass no barrier in this mode
     // the loader wave (see state_fwd_kernel), walking the chunks backwards
     int offK[GK::per_wave(1)], offM[GM::per_wave(1)], offO[GO::per_wave(1)];
     GK::template plan<1>(offK, 0, DK);
@@ -1295,17 +1340,33 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
     const int buf = (NBUF == 2) ? (it & 1) : 0;
     store_ds(c, dS);
     if (NBUF == 1) lds_barrier();        // chunk c is in LDS
-    const int* sc = (const int*)(lds + L::O_SCAL) + 4 * buf;
-    const float gl = __int_as_float(sc[0]);
-    const int t0 = sc[1], tend = sc[2];
+    float gl;
+    int t0, tend;
+    if constexpr (DIRECT) {
+      gl = a.GL[crow * NT + c];
+      chunk_span(a.pack, NT, c, T, t0, tend);
+    } else {
+      const int* sc = (const int*)(lds + L::O_SCAL) + 4 * buf;
+      gl = __int_as_float(sc[0]);
+      t0 = sc[1];
+      tend = sc[2];
+    }
     const MT* st = lds + buf * SZ;
+    // the chunk's tiles: diag(e) K^, diag(gamma) Q^, W, M
+    const size_t bhc = crow * NT + c;
+    const MT* tK = DIRECT ? (const MT*)a.Ke + bhc * C * DK : st;
+    const MT* tQ = DIRECT ? (const MT*)a.Qg + bhc * C * DK : st + O_Q;
+    const MT* tW = DIRECT ? (const MT*)a.W + bhc * C * DK : st + O_W;
+    const MT* tM = DIRECT ? (const MT*)a.M + bhc * C * C : st + O_M;
 
     Frag<MT> Of[2];
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      if constexpr (sizeof(MT) == 2) Of[p] = frag_tr(st + O_O, GO::PITCH, 32 * p, w * 16);
+      if constexpr (DIRECT)    // dO rows of the lane's column straight from memory (zeros past the sequence end)
+        Of[p] = frag_rows<MT, MT>((const MT*)a.dO + o_base, o_pitch, t0, tend, 32 * p, col, One());
+      else if constexpr (sizeof(MT) == 2) Of[p] = frag_tr(st + O_O, GO::PITCH, 32 * p, w * 16);
       else Of[p] = frag_tile_rows<MT, GO>(st + O_O, 32 * p, w * 16 + (l & 15));
-      if (t0 + C > tend)   // rows past the sequence end hold copies of its last row: zero them
+      if (!DIRECT && t0 + C > tend)   // rows past the sequence end hold copies of its last row: zero them
 #pragma unroll
         for (int e = 0; e < 8; ++e)
           if (t0 + 32 * p + kmap(j, e) >= tend) Of[p].set(e, 0.f);
@@ -1319,13 +1380,13 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
     for (int mi = 0; mi < 4; ++mi) {
       Frag<MT> fk[ND / 2];
 #pragma unroll
-      for (int p = 0; p < ND / 2; ++p) fk[p] = frag_tile<MT, GK>(st, 16 * mi, 32 * p);
+      for (int p = 0; p < ND / 2; ++p) fk[p] = frag_tile<MT, FK>(tK, 16 * mi, 32 * p);
       f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int p = 0; p < ND / 2; ++p) mma(acc, fk[p], Sf[p]);
 #pragma unroll
       for (int p = 0; p < 2; ++p)
-        if (32 * p + 31 >= 16 * mi) mma(acc, frag_tile_tr<MT, GM>(st + O_M, 32 * p, 16 * mi), Of[p]);
+        if (32 * p + 31 >= 16 * mi) mma(acc, frag_tile_tr<MT, FM>(tM, 32 * p, 16 * mi), Of[p]);
       dV[mi] = acc;
     }
     Frag<MT> Vf[2];
@@ -1339,8 +1400,8 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
       Frag<MT> fw[2], fq[2];
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        fw[p] = frag_tile_tr<MT, GK>(st + O_W, 32 * p, 16 * di);
-        fq[p] = frag_tile_tr<MT, GK>(st + O_Q, 32 * p, 16 * di);
+        fw[p] = frag_tile_tr<MT, FK>(tW, 32 * p, 16 * di);
+        fq[p] = frag_tile_tr<MT, FK>(tQ, 32 * p, 16 * di);
       }
       f4 acc = dS[di] * gl;
 #pragma unroll
@@ -1352,7 +1413,7 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
     }
 #pragma unroll
     for (int di = 0; di < ND; ++di) dS[di] = dSn[di];
-    lds_barrier();                       // end of chunk c
+    if constexpr (!DIRECT) lds_barrier();   // end of chunk c
   }
 #pragma unroll
   for (int di = 0; di < ND; ++di)
@@ -2511,8 +2572,10 @@ __global__ void __launch_bounds__(256) group_sum_kernel(const T* x, T* y, int64_
 static int check_common(const char* what, int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV, int dtype) {
   if (B < 1 || T < 1 || H < 1) return fail(MACAI_GDR_EINVAL, "%s: B, T, H must be >= 1 (got %lld, %lld, %lld)", what,
                                            (long long)B, (long long)T, (long long)H);
-  if (DK != 32 && DK != 64 && DK != 128)
-    return fail(MACAI_GDR_EUNSUP, "%s: key head width must be 32, 64 or 128 (got %lld)", what, (long long)DK);
+  if (DK != 32 && DK != 64 && DK != 128 && DK != 256)
+    return fail(MACAI_GDR_EUNSUP, "%s: key head width must be 32, 64, 128 or 256 (got %lld)", what, (long long)DK);
+  if (DK == 256 && dtype != MACAI_GDR_F32)
+    return fail(MACAI_GDR_EUNSUP, "%s: key head width 256 takes float32 operands (got dtype code %d)", what, dtype);
   if (DV < 32 || DV % 32 != 0 || DV > 512)
     return fail(MACAI_GDR_EUNSUP, "%s: value head width must be a multiple of 32 in [32, 512] (got %lld)", what,
                 (long long)DV);
@@ -2549,6 +2612,15 @@ static int check_heads(const char* what, int64_t H, int64_t Hk) {
   switch (DK) {                                                \
     case 32: { constexpr int DKC = 32; __VA_ARGS__; } break;   \
     case 64: { constexpr int DKC = 64; __VA_ARGS__; } break;   \
+    default: { constexpr int DKC = 128; __VA_ARGS__; } break;  \
+  }
+// float32 operands also take key width 256 (the fp32 kernels stage key columns in passes or read chunk tiles from
+// global memory where LDS is too small)
+#define DISPATCH_DK_F32(DK, ...)                               \
+  switch (DK) {                                                \
+    case 32: { constexpr int DKC = 32; __VA_ARGS__; } break;   \
+    case 64: { constexpr int DKC = 64; __VA_ARGS__; } break;   \
+    case 256: { constexpr int DKC = 256; __VA_ARGS__; } break; \
     default: { constexpr int DKC = 128; __VA_ARGS__; } break;  \
   }
 
@@ -2596,7 +2668,7 @@ int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, 
   dim3 grid(a.NT, (unsigned)H, pack ? 1u : (unsigned)B);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == MACAI_GDR_F32) {
-    DISPATCH_DK(DK, hipLaunchKernelGGL((prep_kernel<float, float, DKC>), grid, dim3(256), 0, st, a));
+    DISPATCH_DK_F32(DK, hipLaunchKernelGGL((prep_kernel<float, float, DKC>), grid, dim3(256), 0, st, a));
   } else if (DV <= 128 || DV % 128 == 0) {
     DISPATCH_DK(DK, switch (DV) {
       case 32: hipLaunchKernelGGL((prep8_kernel<DKC, 32>), grid, dim3(512), 0, st, a); break;
@@ -2648,6 +2720,9 @@ int macai_gdr_state_fwd(const void* W, const float* U, const void* Ke, const flo
   hipStream_t st = (hipStream_t)stream;
 #define LAUNCH_SF(MT, O, S) \
   DISPATCH_DK(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_fwd_kernel<MT, DKC, NWC, O, S>), grid, block, 0, st, a)))
+#define LAUNCH_SF32(O, S)                                                                                      \
+  DISPATCH_DK_F32(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_fwd_kernel<float, DKC, NWC, O, S>), grid, block, 0, \
+                                                         st, a)))
 #define LAUNCH_SO(S)                                                                                                  \
   {                                                                                                                   \
     const dim3 block2(64 * (2 * nw + 1));                                                                             \
@@ -2655,9 +2730,9 @@ int macai_gdr_state_fwd(const void* W, const float* U, const void* Ke, const flo
     else { DISPATCH_DK(DK, hipLaunchKernelGGL((state_out_kernel<DKC, 2, S>), grid, block2, 0, st, a)); }              \
   }
   if (dtype == MACAI_GDR_F32) {
-    if (out && store) { LAUNCH_SF(float, true, true); }
-    else if (out) { LAUNCH_SF(float, true, false); }
-    else { LAUNCH_SF(float, false, true); }
+    if (out && store) { LAUNCH_SF32(true, true); }
+    else if (out) { LAUNCH_SF32(true, false); }
+    else { LAUNCH_SF32(false, true); }
   } else if (out && nw <= 2) {             // chain and output on separate waves
     if (store) { LAUNCH_SO(true); }
     else { LAUNCH_SO(false); }
@@ -2667,6 +2742,7 @@ int macai_gdr_state_fwd(const void* W, const float* U, const void* Ke, const flo
     else { LAUNCH_SF(bf16, false, true); }
   }
 #undef LAUNCH_SO
+#undef LAUNCH_SF32
 #undef LAUNCH_SF
   return launched(what);
 }
@@ -2693,7 +2769,8 @@ int macai_gdr_state_bwd(const void* Ke, const void* Qg, const void* W, const voi
   dim3 block(64 * (nw + 1));   // nw compute waves and the loader wave
   hipStream_t st = (hipStream_t)stream;
   if (dtype == MACAI_GDR_F32) {
-    DISPATCH_DK(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_bwd_kernel<float, DKC, NWC>), grid, block, 0, st, a)));
+    DISPATCH_DK_F32(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_bwd_kernel<float, DKC, NWC>), grid, block, 0, st,
+                                                           a)));
   } else {
     DISPATCH_DK(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_bwd_kernel<bf16, DKC, NWC>), grid, block, 0, st, a)));
   }
@@ -2726,8 +2803,8 @@ int macai_gdr_state_pair(const void* W, const float* U, const void* Ke, const vo
   dim3 block(64 * (nw + 1));
   hipStream_t st = (hipStream_t)stream;
   if (dtype == MACAI_GDR_F32) {
-    DISPATCH_DK(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_pair_kernel<float, DKC, NWC>), grid, block, 0, st, af, ab,
-                                                       nfwd)));
+    DISPATCH_DK_F32(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_pair_kernel<float, DKC, NWC>), grid, block, 0, st, af,
+                                                           ab, nfwd)));
   } else {
     DISPATCH_DK(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_pair_kernel<bf16, DKC, NWC>), grid, block, 0, st, af, ab,
                                                        nfwd)));
@@ -2760,7 +2837,7 @@ int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float
   dim3 grid(a.NT, (unsigned)H, pack ? 1u : (unsigned)B);
   hipStream_t st = (hipStream_t)stream;
 #define LAUNCH_CB(MT)                                                                                               \
-  DISPATCH_DK(DK, switch (DV) {                                                                                    \
+  DISPATCH_DK_F32(DK, switch (DV) {                                                                                    \
     case 32: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 32>), grid, dim3(256), 0, st, a); break;                \
     case 64: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 64>), grid, dim3(256), 0, st, a); break;                \
     case 96: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 96>), grid, dim3(256), 0, st, a); break;                \

@@ -99,6 +99,13 @@ struct Tile {
   }
 };
 
+// The layout of a dense row-major [R][COLS] tile in global memory (no pad unit): the fragment readers below take it
+// in place of a Tile where a chunk's tiles are read straight from memory instead of LDS.
+template <typename T, int R, int COLS>
+struct Dense {
+  static constexpr int PITCH = COLS;
+};
+
 // Fragment (A operand rows, or B operand columns = rows of B^T) of a k-contiguous tile.
 template <typename MT, typename G>
 __device__ __forceinline__ Frag<MT> frag_tile(const MT* base, int row0, int k0) {

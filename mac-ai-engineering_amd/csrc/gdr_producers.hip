@@ -1,14 +1,21 @@
-// The producers of the rule's inputs in the Qwen3.5 / Qwen3-Next linear-attention layer (the reference's
-// layer/_conv.py:1-24 and layer/_gates.py:1-13, restated for MI355X):
+// The producers of the rule's inputs in the Qwen3.5 / Qwen3-Next linear-attention layer, for MI355X (gfx950):
 //
-//   convolution path: u[t, c] = sum_j w[c, j] x[t - 3 + j, c] (depthwise, causal, kernel 4, zero before the start;
-//   float32), y = u sigmoid(u) rounded once, split into q, k (key_dim channels each) and v (value_dim channels);
-//   gates: beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias) (softplus's threshold 20), both float32.
+//   convolution path  u[t, c] = sum_j w[c, j] x[t - 3 + j, c] (depthwise, causal, 4 taps, zero before the start),
+//                     y = u sigmoid(u) rounded once, split into q, k (key_dim channels each) and v (value_dim);
+//   gates             beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias) (softplus's threshold 20).
+//   (The reference's layer/_conv.py:1-24 and layer/_gates.py:1-13 state the same functions.)
 //
-// Both are streaming element-wise work bound by HBM: a thread owns 4 adjacent channels and walks a tile of time steps
-// with the convolution window in registers, issuing a group of steps' loads at once; no LDS, no barriers, one writer
-// an element.  The backward recomputes u from x (nothing else is kept) and gathers dx with one writer an element; the
-// weight's gradient, when it trains, goes through float32 partial sums a tile and a fixed-order second pass.
+// The convolution is an HBM stream: every input and output byte crosses once (the 3-row halos come again through L2).
+// Work goes by 16-byte channel vectors (8 bf16 / f16 or 4 fp32 channels).  The forward gives a lane one vector over 8
+// consecutive time steps, all 11 input rows loaded at once, a wave 64 consecutive vectors (conv_fwd_kernel).  The
+// backward needs du = dy silu'(u) at 3 rows past each output row and shares it between neighbouring outputs, so it runs
+// on LDS tiles: a workgroup stages x (64 + 6 rows: a 3-row halo each side, by asynchronous global -> LDS copies) and the
+// upstream gradient (67 rows, a key head's copies summed) of 8 vectors, forms du for the tile in LDS (float32) and
+// gathers dx from du's windows, every lane in parallel over time: one writer an element.  The taps' gradient is a
+// per-tile correlation of du with x from the same LDS tiles, reduced over the tile's rows in a fixed order (lane pairs,
+// then the four waves through LDS); sum_columns_kernel adds the tiles' partials in tile order: deterministic.
+// The gates are one pass each way, an element a lane; A_log's and dt_bias's gradients take one
+// workgroup a head, rows split over its waves and summed in a fixed tree.
 #include <hip/hip_runtime.h>
 
 #include "gdr_abi.h"
@@ -18,340 +25,450 @@ namespace gdr {
 
 typedef _Float16 f16;
 
-// N = 4 or 8 consecutive elements <-> float (one 8- or 16-byte access for 2-byte types)
-typedef f16 f16x4 __attribute__((ext_vector_type(4)));
-typedef f16 f16x8 __attribute__((ext_vector_type(8)));
-template <typename T, int N> struct VecOf;
-template <> struct VecOf<bf16, 4> { typedef bf16x4 type; };
-template <> struct VecOf<bf16, 8> { typedef bf16x8 type; };
-template <> struct VecOf<f16, 4> { typedef f16x4 type; };
-template <> struct VecOf<f16, 8> { typedef f16x8 type; };
-template <int N>
-__device__ __forceinline__ void ldn(const float* p, float (&x)[N]) {
+// ---- 16-byte vectors of 2- or 4-byte elements, as floats -----------------------------------------------------------
+template <typename T> struct V16 {
+  static constexpr int N = 16 / (int)sizeof(T);   // elements in 16 bytes
+};
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+
+// The 32-bit words of N values of T (N * sizeof(T) a multiple of 4), and back.
+template <typename T, int N>
+__device__ __forceinline__ void to_words(const float (&x)[N], unsigned (&wd)[N * sizeof(T) / 4]) {
+  if constexpr (sizeof(T) == 4) {
 #pragma unroll
-  for (int h = 0; h < N / 4; ++h) {
-    const f4 a = *reinterpret_cast<const f4*>(p + 4 * h);
+    for (int i = 0; i < N; ++i) wd[i] = __float_as_uint(x[i]);
+  } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[4 * h + i] = a[i];
+    for (int i = 0; i < N / 2; ++i) {
+      const unsigned short lo = __builtin_bit_cast(unsigned short, (T)x[2 * i]);
+      const unsigned short hi = __builtin_bit_cast(unsigned short, (T)x[2 * i + 1]);
+      wd[i] = (unsigned)lo | ((unsigned)hi << 16);
+    }
   }
 }
-template <int N, typename T>
-__device__ __forceinline__ void ldn(const T* p, float (&x)[N]) {
-  const typename VecOf<T, N>::type v = *reinterpret_cast<const typename VecOf<T, N>::type*>(p);
+template <typename T, int N>
+__device__ __forceinline__ void from_words(const unsigned (&wd)[N * sizeof(T) / 4], float (&x)[N]) {
+  if constexpr (sizeof(T) == 4) {
 #pragma unroll
-  for (int i = 0; i < N; ++i) x[i] = (float)v[i];
-}
-template <int N>
-__device__ __forceinline__ void stn(float* p, const float (&x)[N]) {
+    for (int i = 0; i < N; ++i) x[i] = __uint_as_float(wd[i]);
+  } else {
 #pragma unroll
-  for (int h = 0; h < N / 4; ++h)
-    *reinterpret_cast<f4*>(p + 4 * h) = f4{x[4 * h], x[4 * h + 1], x[4 * h + 2], x[4 * h + 3]};
+    for (int i = 0; i < N / 2; ++i) {
+      x[2 * i] = (float)__builtin_bit_cast(T, (unsigned short)(wd[i] & 0xffffu));
+      x[2 * i + 1] = (float)__builtin_bit_cast(T, (unsigned short)(wd[i] >> 16));
+    }
+  }
 }
-template <int N, typename T>
-__device__ __forceinline__ void stn(T* p, const float (&x)[N]) {
-  typename VecOf<T, N>::type v;
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+// N floats written as T: N * sizeof(T) bytes (8, 16 or 32) in 16-byte stores and at most one 8-byte store.
+template <typename T, int N>
+__device__ __forceinline__ void store_as(T* p, const float (&x)[N]) {
+  constexpr int NW = N * (int)sizeof(T) / 4;
+  static_assert(NW % 2 == 0, "whole 8-byte pieces");
+  unsigned wd[NW];
+  to_words<T, N>(x, wd);
+  unsigned* q = reinterpret_cast<unsigned*>(p);
 #pragma unroll
-  for (int i = 0; i < N; ++i) v[i] = (T)x[i];
-  *reinterpret_cast<typename VecOf<T, N>::type*>(p) = v;
+  for (int s = 0; s + 4 <= NW; s += 4)
+    *reinterpret_cast<u32x4_t*>(q + s) = u32x4_t{wd[s], wd[s + 1], wd[s + 2], wd[s + 3]};
+  if constexpr (NW % 4 == 2) *reinterpret_cast<u32x2_t*>(q + NW - 2) = u32x2_t{wd[NW - 2], wd[NW - 1]};
 }
-template <typename T> __device__ __forceinline__ float ld1(const T* p) { return (float)*p; }
-template <typename T> __device__ __forceinline__ void st1(T* p, float x) { *p = (T)x; }
+// N values of T from memory as floats, with the same access widths.
+template <typename T, int N>
+__device__ __forceinline__ void load_as(const T* p, float (&x)[N]) {
+  constexpr int NW = N * (int)sizeof(T) / 4;
+  static_assert(NW % 2 == 0, "whole 8-byte pieces");
+  unsigned wd[NW];
+  const unsigned* q = reinterpret_cast<const unsigned*>(p);
+#pragma unroll
+  for (int s = 0; s + 4 <= NW; s += 4) {
+    const u32x4_t r = *reinterpret_cast<const u32x4_t*>(q + s);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wd[s + i] = r[i];
+  }
+  if constexpr (NW % 4 == 2) {
+    const u32x2_t r = *reinterpret_cast<const u32x2_t*>(q + NW - 2);
+    wd[NW - 2] = r[0];
+    wd[NW - 1] = r[1];
+  }
+  from_words<T, N>(wd, x);
+}
 
-constexpr int CONV_K = 4;        // taps
-constexpr int CONV_CH = 4;       // channels a thread (8-byte accesses for 2-byte types)
-constexpr int CONV_GROUP = 256;  // threads a workgroup (along the channels)
-constexpr int CONV_U = 8;        // time steps whose loads a thread issues together (memory-level parallelism)
+// The V16<T>::N values of T in the 16 bytes `raw`, as floats.
+template <typename T>
+__device__ __forceinline__ void unpack(const u32x4_t& raw, float (&x)[V16<T>::N]) {
+  const unsigned wd[4] = {raw[0], raw[1], raw[2], raw[3]};
+  from_words<T, V16<T>::N>(wd, x);
+}
+
+// ---- the convolution path ----------------------------------------------------------------------------------------
+constexpr int CV_TAPS = 4;
+constexpr int CV_ROWS = 64;       // output time steps a tile
+constexpr int CV_VECS = 8;        // 16-byte channel vectors a tile row
+constexpr int CV_THREADS = 256;   // 32 row groups x 8 vectors; a lane computes rows rg and rg + 32
+constexpr int CV_HALO = CV_TAPS - 1;
 
 struct ConvArgs {
-  const void* x;                 // [B, T, C] T
-  const float* w;                // [C, 4] float32 taps
-  void *q, *k, *v;               // q, k [B, T, KD * REP] T; v [B, T, C - 2 KD] TV
-  const void *dq, *dk, *dv;      // the backward's upstream gradients (same layouts)
-  void* dx;                      // [B, T, C] T
-  float* dwp;                    // [B * ntiles, C, 4] float32 partials, or null
-  int B, T, C, KD, DK, REP, L, ntiles;
+  const void* x;                  // [B, T, C] in T
+  const float* w;                 // [C, 4] float32 taps
+  void *q, *k, *v;                // forward outputs: q, k [B, T, KD * REP] in T, v [B, T, C - 2 KD] in TV
+  const void *dq, *dk, *dv;       // backward inputs, same layouts
+  void* dx;                       // [B, T, C] in T
+  float* part;                    // [B * ntiles, C * 4] per-tile taps' gradient, or null
+  int B, T, C, KD, DK, REP, ntiles;
 };
 
-// where a thread's 8 channels go: q or k (a key head written REP times, REP = 1: key heads only), or v
-struct ConvMap {
-  bool isv;
-  int cc;                        // channel within q, k or v
-  size_t row, col;               // row pitch and first column in the destination
-  __device__ ConvMap(const ConvArgs& a, int c) {
-    isv = c >= 2 * a.KD;
-    cc = isv ? c - 2 * a.KD : (c >= a.KD ? c - a.KD : c);
-    if (isv) {
-      row = (size_t)(a.C - 2 * a.KD);
-      col = cc;
+// Where a 16-byte channel vector lives among the outputs: q, k (key heads, each written REP times: REP = 1 keeps key
+// heads only) or v.  A vector never straddles a head (head widths are multiples of the vector).
+struct Dest {
+  int which;                      // 0 q, 1 k, 2 v
+  size_t pitch;                   // row pitch of the destination (elements)
+  size_t col;                     // the vector's first column there (copy 0)
+  __device__ Dest(int c, int KD, int DK, int REP, int C) {
+    if (c < 2 * KD) {
+      which = c < KD ? 0 : 1;
+      const int cc = c - which * KD;
+      pitch = (size_t)KD * REP;
+      col = (size_t)(cc / DK) * REP * DK + cc % DK;
     } else {
-      row = (size_t)a.KD * a.REP;
-      col = (size_t)(cc / a.DK) * a.REP * a.DK + cc % a.DK;
+      which = 2;
+      pitch = (size_t)(C - 2 * KD);
+      col = (size_t)(c - 2 * KD);
     }
   }
 };
 
-__device__ __forceinline__ void load_taps(const float* w, int c, float (&tap)[CONV_K][CONV_CH]) {
+// The tile's taps, tap-major: tw[j][i] = w[c + i, j] for the lane's N channels.
+template <int N>
+__device__ __forceinline__ void tile_taps(const float* w, int c, float (&tw)[CV_TAPS][N]) {
 #pragma unroll
-  for (int i = 0; i < CONV_CH; ++i) {
-    const f4 r = *reinterpret_cast<const f4*>(w + (size_t)(c + i) * CONV_K);
+  for (int i = 0; i < N; ++i) {
+    const f4 r = *reinterpret_cast<const f4*>(w + (size_t)(c + i) * CV_TAPS);
 #pragma unroll
-    for (int j = 0; j < CONV_K; ++j) tap[j][i] = r[j];
+    for (int j = 0; j < CV_TAPS; ++j) tw[j][i] = r[j];
   }
 }
 
-// u = w0 x[t-3] + w1 x[t-2] + w2 x[t-1] + w3 x[t], in the reference's order (layer/_conv.py:73).  With float32
-// inputs (PRECISE) the sum is formed in double and rounded once, and sigmoid divides exactly: there the four roundings
-// of a float sum would set the outputs' error (about 1 ulp of max |u|).  With 2-byte inputs the outputs' own rounding
-// dominates, so the sum stays in float and exp / division take the fast forms (the work is then bound by HBM).
-template <bool PRECISE>
-__device__ __forceinline__ float conv_u(const float (&tap)[CONV_K][CONV_CH], int i, float xm3, float xm2, float xm1,
-                                        float xt) {
-  if constexpr (PRECISE)
-    return (float)fma((double)tap[3][i], (double)xt,
-                      fma((double)tap[2][i], (double)xm1, fma((double)tap[1][i], (double)xm2,
-                                                              (double)tap[0][i] * (double)xm3)));
-  else
-    return fmaf(tap[3][i], xt, fmaf(tap[2][i], xm1, fmaf(tap[1][i], xm2, tap[0][i] * xm3)));
+// sum_j tw[j][i] win[j][i], j = 3 first.  float32 inputs (EXACT) sum in double and round once, so that the result is
+// within an ulp of the exact value (their error bar is twice PyTorch's fp32 path); 2-byte inputs sum in float, whose
+// rounding is far below the output's.
+template <bool EXACT, int N>
+__device__ __forceinline__ float tap_dot(const float (&tw)[CV_TAPS][N], int i, float w0, float w1, float w2, float w3) {
+  if constexpr (EXACT) {
+    double s = (double)tw[3][i] * (double)w3;
+    s = fma((double)tw[2][i], (double)w2, s);
+    s = fma((double)tw[1][i], (double)w1, s);
+    return (float)fma((double)tw[0][i], (double)w0, s);
+  } else {
+    return fmaf(tw[0][i], w0, fmaf(tw[1][i], w1, fmaf(tw[2][i], w2, tw[3][i] * w3)));
+  }
 }
-// w0 d0 + (w1 d1 + (w2 d2 + w3 d3)), with the same precision rule
-template <bool PRECISE>
-__device__ __forceinline__ float taps4(float w0, float d0, float w1, float d1, float w2, float d2, float w3, float d3) {
-  if constexpr (PRECISE)
-    return (float)fma((double)w0, (double)d0, fma((double)w1, (double)d1, fma((double)w2, (double)d2,
-                                                                            (double)w3 * (double)d3)));
-  else
-    return fmaf(w0, d0, fmaf(w1, d1, fmaf(w2, d2, w3 * d3)));
+template <bool EXACT>
+__device__ __forceinline__ float logistic(float u) {
+  if constexpr (EXACT) return 1.0f / (1.0f + expf(-u));
+  else return __frcp_rn(1.0f + __expf(-u));
 }
-template <bool PRECISE>
-__device__ __forceinline__ float silu_of(float u) {
-  if constexpr (PRECISE) return u / (1.0f + expf(-u));
-  else return __fdividef(u, 1.0f + __expf(-u));
-}
-template <bool PRECISE>
-__device__ __forceinline__ float sigmoid_of(float u) {
-  if constexpr (PRECISE) return 1.0f / (1.0f + expf(-u));
-  else return __fdividef(1.0f, 1.0f + __expf(-u));
+// u sigmoid(u) with one rounding after the exponential for float32 inputs (a division, not u times a rounded
+// reciprocal, whose two roundings put the float32 output past twice PyTorch's silu error)
+template <bool EXACT>
+__device__ __forceinline__ float silu(float u) {
+  if constexpr (EXACT) return u / (1.0f + expf(-u));
+  else return u * __frcp_rn(1.0f + __expf(-u));
 }
 
+// Stage rows [t_lo, t_lo + NROWS) x the tile's CV_VECS vectors of x (batch row b) into LDS by asynchronous 16-byte
+// copies (global -> LDS, no registers), all of a thread's issued back to back; units outside [0, T) or past the
+// channels are zeroed by LDS stores instead.  Unit u = row * CV_VECS + vector.  The caller waits (wait_copies) and
+// synchronises before reading.
+template <typename T, int NROWS>
+__device__ __forceinline__ void stage_x(u32x4_t* dst, const T* xb, int t_lo, int c0, int T_, int C) {
+  constexpr int VE = V16<T>::N;
+  constexpr int UNITS = NROWS * CV_VECS, PER = (UNITS + CV_THREADS - 1) / CV_THREADS;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int u = threadIdx.x + i * CV_THREADS;
+    if (u < UNITS) {
+      const int row = u / CV_VECS, c = c0 + (u % CV_VECS) * VE, t = t_lo + row;
+      if (t >= 0 && t < T_ && c < C)
+        __builtin_amdgcn_global_load_lds((const void*)(xb + (size_t)t * C + c),
+                                         (__attribute__((address_space(3))) void*)(dst + u - threadIdx.x % 64), 16,
+                                         0, 0);
+      else
+        dst[u] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+  }
+}
+__device__ __forceinline__ void wait_copies() { __builtin_amdgcn_s_waitcnt(0); }
+
+// The forward needs no staging: a lane owns one 16-byte channel vector over CV_FWD_STEPS consecutive time steps and
+// issues the loads of all its CV_FWD_STEPS + 3 input rows at once (the 3 halo rows come again through L2), then forms
+// each output from them.  A wave spans 64 consecutive vectors (1 KB of a bf16 row), a workgroup four consecutive time
+// blocks.  Measured at config 1's widths this ran at the box's mixed read/write rate, ahead of LDS-staged tiles (whose
+// staging and barrier put each tile's loads and stores in separate phases).
+constexpr int CV_FWD_STEPS = 8;
 template <typename T, typename TV>
-__global__ void __launch_bounds__(CONV_GROUP) conv_fwd_kernel(ConvArgs a) {
-  const int c = (blockIdx.x * CONV_GROUP + threadIdx.x) * CONV_CH;
-  if (c >= a.C) return;
-  const int t0 = blockIdx.y * a.L, b = blockIdx.z;
-  float tap[CONV_K][CONV_CH];
-  load_taps(a.w, c, tap);
+__global__ void __launch_bounds__(256) conv_fwd_kernel(ConvArgs a) {
+  constexpr int VE = V16<T>::N;
+  constexpr bool EXACT = sizeof(T) == 4;
+  constexpr int NR = CV_FWD_STEPS + CV_HALO;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = (blockIdx.x * 64 + lane) * VE;
+  const int t0 = (blockIdx.y * 4 + wave) * CV_FWD_STEPS, b = blockIdx.z;
+  if (c >= a.C || t0 >= a.T) return;
   const T* xb = (const T*)a.x + (size_t)b * a.T * a.C + c;
-  float xm3[CONV_CH] = {}, xm2[CONV_CH] = {}, xm1[CONV_CH] = {};
-  if (t0 >= 3) ldn<CONV_CH>(xb + (size_t)(t0 - 3) * a.C, xm3);
-  if (t0 >= 2) ldn<CONV_CH>(xb + (size_t)(t0 - 2) * a.C, xm2);
-  if (t0 >= 1) ldn<CONV_CH>(xb + (size_t)(t0 - 1) * a.C, xm1);
-  const ConvMap m(a, c);
-  const int te = t0 + a.L < a.T ? t0 + a.L : a.T;
-  for (int tb = t0; tb < te; tb += CONV_U) {
-    float xs[CONV_U][CONV_CH];            // the group's inputs, all loads in flight before the first is used
+  u32x4_t raw[NR];                                    // x[t0 - 3 + i], zero outside the sequence
 #pragma unroll
-    for (int s = 0; s < CONV_U; ++s)
-      if (tb + s < te) ldn<CONV_CH>(xb + (size_t)(tb + s) * a.C, xs[s]);
+  for (int i = 0; i < NR; ++i) {
+    const int t = t0 - CV_HALO + i;
+    raw[i] = (t >= 0 && t < a.T) ? *reinterpret_cast<const u32x4_t*>(xb + (size_t)t * a.C) : u32x4_t{0u, 0u, 0u, 0u};
+  }
+  float tw[CV_TAPS][VE];
+  tile_taps<VE>(a.w, c, tw);
+  const Dest d(c, a.KD, a.DK, a.REP, a.C);
 #pragma unroll
-    for (int s = 0; s < CONV_U; ++s) {
-      if (tb + s >= te) break;
-      const int t = tb + s;
-      float y[CONV_CH];
+  for (int s = 0; s < CV_FWD_STEPS; ++s) {
+    const int t = t0 + s;
+    if (t >= a.T) break;
+    float w0[VE], w1[VE], w2[VE], w3[VE];             // x[t - 3] .. x[t]
+    unpack<T>(raw[s], w0);
+    unpack<T>(raw[s + 1], w1);
+    unpack<T>(raw[s + 2], w2);
+    unpack<T>(raw[s + 3], w3);
+    float y[VE];
 #pragma unroll
-      for (int i = 0; i < CONV_CH; ++i) {
-        const float u = conv_u<sizeof(T) == 4>(tap, i, xm3[i], xm2[i], xm1[i], xs[s][i]);
-        y[i] = silu_of<sizeof(T) == 4>(u);
-        xm3[i] = xm2[i];
-        xm2[i] = xm1[i];
-        xm1[i] = xs[s][i];
+    for (int i = 0; i < VE; ++i) y[i] = silu<EXACT>(tap_dot<EXACT, VE>(tw, i, w0[i], w1[i], w2[i], w3[i]));
+    const size_t row = (size_t)b * a.T + t;
+    if (d.which == 2) {
+      store_as<TV, VE>((TV*)a.v + row * d.pitch + d.col, y);
+    } else {
+      T* dst = (T*)(d.which == 0 ? a.q : a.k) + row * d.pitch + d.col;
+      for (int rep = 0; rep < a.REP; ++rep) store_as<T, VE>(dst + (size_t)rep * a.DK, y);
+    }
+  }
+}
+
+// The backward of a tile of 64 output rows t0 .. t0 + 63 (dx there, and the tile's share of the taps' gradient):
+//   x staged for t0 - 3 .. t0 + 66, the upstream gradient dy (q's and k's copies summed in copy order) for
+//   t0 .. t0 + 66, then du = dy s (1 + u (1 - s)), s = sigmoid(u), in place (0 past the end), then
+//   dx[t] = w0 du[t + 3] + w1 du[t + 2] + w2 du[t + 1] + w3 du[t],
+//   part[tile][c, j] = sum over the tile's t of du[t] x[t - 3 + j].
+template <typename T, typename TV, bool TAPS>
+__global__ void __launch_bounds__(CV_THREADS) conv_bwd_tile_kernel(ConvArgs a) {
+  constexpr int VE = V16<T>::N;
+  constexpr bool EXACT = sizeof(T) == 4;
+  constexpr int XR = CV_ROWS + 2 * CV_HALO;          // x rows t0 - 3 .. t0 + 66
+  constexpr int DR = CV_ROWS + CV_HALO;              // du rows t0 .. t0 + 66
+  __shared__ u32x4_t xs[XR * CV_VECS];
+  __shared__ float du[DR * CV_VECS * VE];            // [row][vector][element]
+  __shared__ double red[4][32][TAPS ? VE : 1];       // the taps' gradient: one row of partials a wave
+  const int c0 = blockIdx.x * CV_VECS * VE, t0 = blockIdx.y * CV_ROWS, b = blockIdx.z;
+  const T* xb = (const T*)a.x + (size_t)b * a.T * a.C;
+  stage_x<T, XR>(xs, xb, t0 - CV_HALO, c0, a.T, a.C);
+  // dy for rows t0 .. t0 + 66 (zero past the end or past the channels): every unit's first-copy load is issued
+  // before any is used (a thread's units keep its vector, so they share one destination map)
+  {
+    constexpr int UNITS = DR * CV_VECS, PER = (UNITS + CV_THREADS - 1) / CV_THREADS;
+    const int vec = threadIdx.x % CV_VECS, c = c0 + vec * VE;
+    const Dest d(c < a.C ? c : 0, a.KD, a.DK, a.REP, a.C);
+    const T* qk = (const T*)(d.which == 0 ? a.dq : a.dk);
+    float g[PER][VE];
+    bool live[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int u = threadIdx.x + i * CV_THREADS, t = t0 + u / CV_VECS;
+      live[i] = u < UNITS && t < a.T && c < a.C;
+      const size_t r = (size_t)b * a.T + (live[i] ? t : 0);
+      if (d.which == 2) load_as<TV, VE>((const TV*)a.dv + r * d.pitch + d.col, g[i]);
+      else load_as<T, VE>(qk + r * d.pitch + d.col, g[i]);
+    }
+    if (d.which != 2)
+      for (int rep = 1; rep < a.REP; ++rep)   // the other copies of a repeated key head, added in copy order
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const int t = t0 + (threadIdx.x + i * CV_THREADS) / CV_VECS;
+          const size_t r = (size_t)b * a.T + (live[i] ? t : 0);
+          float h[VE];
+          load_as<T, VE>(qk + r * d.pitch + d.col + (size_t)rep * a.DK, h);
+#pragma unroll
+          for (int e = 0; e < VE; ++e) g[i][e] += h[e];
+        }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int u = threadIdx.x + i * CV_THREADS;
+      if (u < UNITS)
+#pragma unroll
+        for (int e = 0; e < VE; ++e) du[u * VE + e] = live[i] ? g[i][e] : 0.f;
+    }
+  }
+  wait_copies();
+  __syncthreads();
+  float tw[CV_TAPS][VE];
+  {
+    const int vec = threadIdx.x % CV_VECS, c = c0 + vec * VE;
+    if (c < a.C) tile_taps<VE>(a.w, c, tw);
+    else
+#pragma unroll
+      for (int j = 0; j < CV_TAPS; ++j)
+#pragma unroll
+        for (int i = 0; i < VE; ++i) tw[j][i] = 0.f;
+  }
+  // du in place: unit u's row sees x rows row .. row + 3 (t - 3 .. t); the lanes of a unit keep their vector, so tw
+  // is the lane's own taps
+  for (int u = threadIdx.x; u < DR * CV_VECS; u += CV_THREADS) {
+    const int row = u / CV_VECS, vec = u % CV_VECS;
+    float w0[VE], w1[VE], w2[VE], w3[VE];
+    unpack<T>(xs[(row + 0) * CV_VECS + vec], w0);
+    unpack<T>(xs[(row + 1) * CV_VECS + vec], w1);
+    unpack<T>(xs[(row + 2) * CV_VECS + vec], w2);
+    unpack<T>(xs[(row + 3) * CV_VECS + vec], w3);
+#pragma unroll
+    for (int i = 0; i < VE; ++i) {
+      const float uu = tap_dot<EXACT, VE>(tw, i, w0[i], w1[i], w2[i], w3[i]);
+      const float s = logistic<EXACT>(uu);
+      du[u * VE + i] *= s * (1.0f + uu * (1.0f - s));   // dy was staged there (0 past the end)
+    }
+  }
+  __syncthreads();
+
+  // dx for the lane's rows rg, rg + 32
+  {
+    const int vec = threadIdx.x % CV_VECS, rg = threadIdx.x / CV_VECS, c = c0 + vec * VE;
+    if (c < a.C) {
+      T* dxb = (T*)a.dx + (size_t)b * a.T * a.C + c;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int r = rg + 32 * h, t = t0 + r;
+        if (t >= a.T) break;
+        float o[VE];
+        const float* d0 = du + ((r + 3) * CV_VECS + vec) * VE;   // du[t + 3]
+        const float* d1 = du + ((r + 2) * CV_VECS + vec) * VE;
+        const float* d2 = du + ((r + 1) * CV_VECS + vec) * VE;
+        const float* d3 = du + ((r + 0) * CV_VECS + vec) * VE;   // du[t]
+#pragma unroll
+        for (int i = 0; i < VE; ++i) o[i] = tap_dot<EXACT, VE>(tw, i, d0[i], d1[i], d2[i], d3[i]);
+        store_as<T, VE>(dxb + (size_t)t * a.C, o);
       }
-      const size_t bt = (size_t)b * a.T + t;
-      if (m.isv) {
-        stn<CONV_CH>((TV*)a.v + bt * m.row + m.col, y);
-      } else {
-        T* dst = (T*)(c >= a.KD ? a.k : a.q) + bt * m.row + m.col;
-        for (int r = 0; r < a.REP; ++r) stn<CONV_CH>(dst + (size_t)r * a.DK, y);
+    }
+  }
+  if constexpr (TAPS) {
+    // combo = (vector, tap) = lane % 32; part = thread / 32 sums rows 8 part .. 8 part + 7 in double
+    const int combo = threadIdx.x % 32, part = threadIdx.x / 32, vec = combo % CV_VECS, j = combo / CV_VECS;
+    double acc[VE];
+#pragma unroll
+    for (int i = 0; i < VE; ++i) acc[i] = 0.0;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int r = 8 * part + s;                     // x[t - 3 + j] is staged row r + j
+      float xv[VE];
+      unpack<T>(xs[(r + j) * CV_VECS + vec], xv);
+      const float* dd = du + (r * CV_VECS + vec) * VE;
+#pragma unroll
+      for (int i = 0; i < VE; ++i) acc[i] = fma((double)dd[i], (double)xv[i], acc[i]);
+    }
+    // parts 2w and 2w + 1 are lanes l and l + 32 of wave w: add them, then the four waves in order through LDS
+#pragma unroll
+    for (int i = 0; i < VE; ++i) acc[i] += __shfl_xor(acc[i], 32, 64);
+    const int w = threadIdx.x / 64;
+    if ((threadIdx.x & 63) < 32)
+#pragma unroll
+      for (int i = 0; i < VE; ++i) red[w][combo][i] = acc[i];
+    __syncthreads();
+    if (threadIdx.x < 32) {
+      const int c = c0 + vec * VE;
+      if (c < a.C) {
+        float* out = a.part + (size_t)(b * a.ntiles + blockIdx.y) * a.C * CV_TAPS;
+#pragma unroll
+        for (int i = 0; i < VE; ++i)
+          out[(size_t)(c + i) * CV_TAPS + j] =
+              (float)(((red[0][combo][i] + red[1][combo][i]) + red[2][combo][i]) + red[3][combo][i]);
       }
     }
   }
 }
 
-// dx[t] = sum_j w_j du[t + 3 - j] with du = dy sigmoid(u) (1 + u (1 - sigmoid(u))) (0 past the end; dy of q and k
-// summed over the REP copies in copy order); dw partials a tile: sum over its t of du[t] x[t - 3 + j].
-template <typename T, typename TV, bool DW>
-__global__ void __launch_bounds__(CONV_GROUP) conv_bwd_kernel(ConvArgs a) {
-  constexpr int U = 4;                    // time steps whose loads are issued together
-  const int c = (blockIdx.x * CONV_GROUP + threadIdx.x) * CONV_CH;
-  if (c >= a.C) return;
-  const int t0 = blockIdx.y * a.L, b = blockIdx.z;
-  float tap[CONV_K][CONV_CH];
-  load_taps(a.w, c, tap);
-  const T* xb = (const T*)a.x + (size_t)b * a.T * a.C + c;
-  T* dxb = (T*)a.dx + (size_t)b * a.T * a.C + c;
-  float xm3[CONV_CH] = {}, xm2[CONV_CH] = {}, xm1[CONV_CH] = {};
-  if (t0 >= 3) ldn<CONV_CH>(xb + (size_t)(t0 - 3) * a.C, xm3);
-  if (t0 >= 2) ldn<CONV_CH>(xb + (size_t)(t0 - 2) * a.C, xm2);
-  if (t0 >= 1) ldn<CONV_CH>(xb + (size_t)(t0 - 1) * a.C, xm1);
-  float dm1[CONV_CH] = {}, dm2[CONV_CH] = {}, dm3[CONV_CH] = {};   // du[t - 1], du[t - 2], du[t - 3]
-  double acc[DW ? CONV_K : 1][CONV_CH] = {};                       // dw partials, in double (rounded once)
-  const ConvMap m(a, c);
-  const int tl = t0 + a.L < a.T ? t0 + a.L : a.T;                 // this tile's outputs: [t0, tl)
-  const int tw = tl + 3 < a.T ? tl + 3 : a.T;                     // the inputs the walk reads: [t0, tw)
-  for (int tb = t0; tb < tl + 3; tb += U) {
-    // the group's inputs and upstream gradients, all loads in flight before the first is used
-    float xs[U][CONV_CH], gs[U][CONV_CH];
-#pragma unroll
-    for (int s = 0; s < U; ++s) {
-      if (tb + s < tw) {
-        const size_t bt = (size_t)b * a.T + tb + s;
-        ldn<CONV_CH>(xb + (size_t)(tb + s) * a.C, xs[s]);
-        if (m.isv) ldn<CONV_CH>((const TV*)a.dv + bt * m.row + m.col, gs[s]);
-        else ldn<CONV_CH>((const T*)(c >= a.KD ? a.dk : a.dq) + bt * m.row + m.col, gs[s]);
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < U; ++s) {
-    const int t = tb + s;
-    if (t >= tl + 3) break;
-    float du[CONV_CH] = {}, xt[CONV_CH] = {};
-    if (t < a.T) {
-      const size_t bt = (size_t)b * a.T + t;
-      float gy[CONV_CH];
-#pragma unroll
-      for (int i = 0; i < CONV_CH; ++i) {
-        xt[i] = xs[s][i];
-        gy[i] = gs[s][i];
-      }
-      if (!m.isv) {                        // the other copies of a repeated key head, summed in copy order
-        const T* src = (const T*)(c >= a.KD ? a.dk : a.dq) + bt * m.row + m.col;
-        for (int r = 1; r < a.REP; ++r) {
-          float g2[CONV_CH];
-          ldn<CONV_CH>(src + (size_t)r * a.DK, g2);
-#pragma unroll
-          for (int i = 0; i < CONV_CH; ++i) gy[i] += g2[i];
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < CONV_CH; ++i) {
-        const float u = conv_u<sizeof(T) == 4>(tap, i, xm3[i], xm2[i], xm1[i], xt[i]);
-        const float s = sigmoid_of<sizeof(T) == 4>(u);
-        du[i] = gy[i] * s * (1.0f + u * (1.0f - s));
-      }
-      if constexpr (DW) {
-        if (t < tl) {
-#pragma unroll
-          for (int i = 0; i < CONV_CH; ++i) {
-            acc[0][i] = fma((double)du[i], (double)xm3[i], acc[0][i]);
-            acc[1][i] = fma((double)du[i], (double)xm2[i], acc[1][i]);
-            acc[2][i] = fma((double)du[i], (double)xm1[i], acc[2][i]);
-            acc[3][i] = fma((double)du[i], (double)xt[i], acc[3][i]);
-          }
-        }
-      }
-    }
-    if (t >= t0 + 3) {
-      float dx[CONV_CH];
-#pragma unroll
-      for (int i = 0; i < CONV_CH; ++i)        // rounded once for float32 inputs (as u)
-        dx[i] = taps4<sizeof(T) == 4>(tap[0][i], du[i], tap[1][i], dm1[i], tap[2][i], dm2[i], tap[3][i], dm3[i]);
-      stn<CONV_CH>(dxb + (size_t)(t - 3) * a.C, dx);
-    }
-#pragma unroll
-    for (int i = 0; i < CONV_CH; ++i) {
-      xm3[i] = xm2[i];
-      xm2[i] = xm1[i];
-      xm1[i] = xt[i];
-      dm3[i] = dm2[i];
-      dm2[i] = dm1[i];
-      dm1[i] = du[i];
-    }
-    }
-  }
-  if constexpr (DW) {
-    float* p = a.dwp + ((size_t)(b * a.ntiles + blockIdx.y) * a.C + c) * CONV_K;
-#pragma unroll
-    for (int i = 0; i < CONV_CH; ++i)
-      *reinterpret_cast<f4*>(p + i * CONV_K) = f4{(float)acc[0][i], (float)acc[1][i], (float)acc[2][i],
-                                                  (float)acc[3][i]};
-  }
-}
-
-// out[i] = sum over the P partial rows of p[., i], in row order, in double (one thread an element: deterministic)
-__global__ void __launch_bounds__(256) sum_rows_kernel(const float* p, float* out, int P, int n) {
+// out[i] = the sum over rows p = 0 .. P - 1 of in[p * n + i], in row order, in double, rounded once: the fixed-order
+// second stage of the taps' gradient.  A lane an output; each row's loads for a group of eight rows are in flight
+// together.
+__global__ void __launch_bounds__(256) sum_columns_kernel(const float* in, float* out, int P, int n) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
   double s = 0.0;
-  int r = 0;
-  for (; r + 8 <= P; r += 8) {           // eight rows' loads in flight, added in row order
+  int p = 0;
+  for (; p + 8 <= P; p += 8) {
     float v[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = p[(size_t)(r + k) * n + i];
+    for (int e = 0; e < 8; ++e) v[e] = in[(size_t)(p + e) * n + i];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) s += (double)v[k];
+    for (int e = 0; e < 8; ++e) s += (double)v[e];
   }
-  for (; r < P; ++r) s += (double)p[(size_t)r * n + i];
+  for (; p < P; ++p) s += (double)in[(size_t)p * n + i];
   out[i] = (float)s;
 }
 
-// ---- gates ------------------------------------------------------------------------------------------------------------
-// softplus with PyTorch's threshold of 20 (the input itself above it), log1p below it
-__device__ __forceinline__ float softplus20(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+// ---- the gates -----------------------------------------------------------------------------------------------------
+// PyTorch's softplus with threshold 20: x above it, log1p(exp(x)) below.
+__device__ __forceinline__ float softplus_t20(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+// its derivative with the same threshold: 1 above it, sigmoid(x) below
+__device__ __forceinline__ float softplus_t20_grad(float x) { return x > 20.0f ? 1.0f : 1.0f / (1.0f + expf(-x)); }
 
+// The gates move under a megabyte per layer, so they are bound by latency, not bandwidth: one element a lane, so
+// that a layer's elements spread over every lane of the chip and each lane runs one exponential chain.
+constexpr int GATE_THREADS = 256;
 template <typename T>
-__global__ void __launch_bounds__(256) gates_fwd_kernel(const T* b, const T* a, const float* alog, const float* dtb,
-                                                        float* beta, float* g, int64_t n, int H) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+__global__ void __launch_bounds__(GATE_THREADS) gates_fwd_kernel(const T* b, const T* a, const float* alog,
+                                                                 const float* dtb, float* beta, float* g, int64_t n,
+                                                                 int H) {
+  const int64_t i = (int64_t)blockIdx.x * GATE_THREADS + threadIdx.x;
   if (i >= n) return;
-  const int h = (int)(i % H);
-  beta[i] = 1.0f / (1.0f + expf(-ld1(b + i)));
-  g[i] = -expf(alog[h]) * softplus20(ld1(a + i) + dtb[h]);
+  const int head = (int)(i % H);             // heads run fastest: element i is head i mod H
+  const float rate = -expf(alog[head]);
+  beta[i] = 1.0f / (1.0f + expf(-(float)b[i]));
+  g[i] = rate * softplus_t20((float)a[i] + dtb[head]);
 }
 
-// db = dbeta beta (1 - beta); da = dg (-exp(A_log)) sigmoid(a + dt_bias) (1 above the threshold)
 template <typename T>
-__global__ void __launch_bounds__(256) gates_bwd_kernel(const T* b, const T* a, const float* alog, const float* dtb,
-                                                        const float* dbeta, const float* dg, T* db, T* da, int64_t n,
-                                                        int H) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+__global__ void __launch_bounds__(GATE_THREADS) gates_bwd_kernel(const T* b, const T* a, const float* alog,
+                                                                 const float* dtb, const float* dbeta,
+                                                                 const float* dg, T* db, T* da, int64_t n, int H) {
+  const int64_t i = (int64_t)blockIdx.x * GATE_THREADS + threadIdx.x;
   if (i >= n) return;
-  const int h = (int)(i % H);
-  const float sb = 1.0f / (1.0f + expf(-ld1(b + i)));
-  st1(db + i, dbeta[i] * sb * (1.0f - sb));
-  const float xa = ld1(a + i) + dtb[h];
-  const float sx = xa > 20.0f ? 1.0f : 1.0f / (1.0f + expf(-xa));
-  st1(da + i, dg[i] * (-expf(alog[h])) * sx);
+  const int head = (int)(i % H);
+  const float rate = -expf(alog[head]);
+  const float sig = 1.0f / (1.0f + expf(-(float)b[i]));
+  db[i] = (T)(dbeta[i] * (sig - sig * sig));          // d sigmoid = s (1 - s)
+  da[i] = (T)(dg[i] * rate * softplus_t20_grad((float)a[i] + dtb[head]));
 }
 
-// A_log's and dt_bias's gradients, one workgroup a head: dA[h] = sum_t dg g, ddt[h] = sum_t dg (-exp(A_log)) sx over
-// the n / H rows, each thread a strided part in order, then a fixed tree (deterministic)
+// dA_log[h] = sum over rows of dg g and ddt[h] = sum over rows of dg (-exp(A_log)) softplus'(a + dt_bias): one
+// workgroup a head; thread i takes rows i, i + 256, ... in order, then a wave sums its lanes by a fixed butterfly and
+// the four waves add in order.  Deterministic.
 template <typename T>
-__global__ void __launch_bounds__(256) gates_param_kernel(const T* a, const float* alog, const float* dtb,
-                                                          const float* dg, float* dA, float* ddt, int64_t rows,
-                                                          int H) {
+__global__ void __launch_bounds__(256) gates_params_kernel(const T* a, const float* alog, const float* dtb,
+                                                           const float* dg, float* dA, float* ddt, int64_t rows,
+                                                           int H) {
   const int h = blockIdx.x;
-  const float ea = expf(alog[h]);
-  float sa = 0.f, sd = 0.f;
+  const float rate = -expf(alog[h]), bias = dtb[h];
+  float s_a = 0.f, s_d = 0.f;
   for (int64_t r = threadIdx.x; r < rows; r += 256) {
     const int64_t i = r * H + h;
-    const float xa = ld1(a + i) + dtb[h];
-    const float sx = xa > 20.0f ? 1.0f : 1.0f / (1.0f + expf(-xa));
-    sa = fmaf(dg[i], -ea * softplus20(xa), sa);
-    sd = fmaf(dg[i], -ea * sx, sd);
+    const float x = (float)a[i] + bias, gv = dg[i];
+    s_a = fmaf(gv, rate * softplus_t20(x), s_a);
+    s_d = fmaf(gv, rate * softplus_t20_grad(x), s_d);
   }
-  __shared__ float pa[256], pd[256];
-  pa[threadIdx.x] = sa;
-  pd[threadIdx.x] = sd;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    s_a += __shfl_xor(s_a, off, 64);
+    s_d += __shfl_xor(s_d, off, 64);
+  }
+  __shared__ float wa[4], wd[4];
+  if ((threadIdx.x & 63) == 0) {
+    wa[threadIdx.x >> 6] = s_a;
+    wd[threadIdx.x >> 6] = s_d;
+  }
   __syncthreads();
-  for (int off = 128; off > 0; off >>= 1) {
-    if ((int)threadIdx.x < off) {
-      pa[threadIdx.x] += pa[threadIdx.x + off];
-      pd[threadIdx.x] += pd[threadIdx.x + off];
-    }
-    __syncthreads();
-  }
   if (threadIdx.x == 0) {
-    dA[h] = pa[0];
-    ddt[h] = pd[0];
+    dA[h] = ((wa[0] + wa[1]) + wa[2]) + wa[3];
+    ddt[h] = ((wd[0] + wd[1]) + wd[2]) + wd[3];
   }
 }
 
@@ -363,26 +480,33 @@ namespace {
 
 int check_conv(const char* what, int64_t B, int64_t T, int64_t C, int64_t KD, int64_t DK, int64_t REP, int64_t DV,
                int32_t dtype, int32_t vdtype) {
-  if (B < 1 || T < 1 || B > 65535 || T > 65535 * 16)
-    return fail(MACAI_GDR_EINVAL, "%s: B in [1, 65535] and T in [1, 65535 x 16] (got %lld, %lld)", what, (long long)B,
-                (long long)T);
+  constexpr int64_t T_MAX = (int64_t)65535 * 4 * CV_FWD_STEPS;   // the forward's grid rows of time blocks
+  if (B < 1 || T < 1 || B > 65535 || T > T_MAX)
+    return fail(MACAI_GDR_EINVAL, "%s: B in [1, 65535] and T in [1, %lld] (got %lld, %lld)", what, (long long)T_MAX,
+                (long long)B, (long long)T);
   if (dtype < MACAI_GDR_F32 || dtype > MACAI_GDR_F16 || vdtype < MACAI_GDR_F32 || vdtype > MACAI_GDR_F16)
     return fail(MACAI_GDR_EUNSUP, "%s: dtype codes must be F32, BF16 or F16", what);
   const int64_t VD = C - 2 * KD;
   if (KD < 1 || DK < 1 || DV < 1 || REP < 1 || VD < 1 || KD % DK || VD % DV || KD % 8 || DK % 8 || DV % 8 || C % 8)
     return fail(MACAI_GDR_EINVAL,
-                 "%s: need key_dim a multiple of the key head width, value_dim = C - 2 key_dim a multiple of the value "
-                 "head width, all multiples of 8 (got C %lld, key_dim %lld, DK %lld, DV %lld, REP %lld)",
-                 what, (long long)C, (long long)KD, (long long)DK, (long long)DV, (long long)REP);
+                "%s: need key_dim a multiple of the key head width, value_dim = C - 2 key_dim a multiple of the value "
+                "head width, all multiples of 8 (got C %lld, key_dim %lld, DK %lld, DV %lld, REP %lld)",
+                what, (long long)C, (long long)KD, (long long)DK, (long long)DV, (long long)REP);
   if (REP != 1 && (KD / DK) * REP != VD / DV)
     return fail(MACAI_GDR_EINVAL, "%s: REP must be 1 (key heads only) or value heads / key heads (%lld)", what,
-                 (long long)(VD / DV / (KD / DK)));
+                (long long)(VD / DV / (KD / DK)));
   if (B * T * C >= (int64_t)1 << 31 || B * T * KD * REP >= (int64_t)1 << 31)
     return fail(MACAI_GDR_EINVAL, "%s: tensors past 2^31 elements are not supported", what);
   return MACAI_GDR_OK;
 }
 
-constexpr int CONV_TILE = 16;   // time steps a thread walks
+int64_t conv_tiles(int64_t T) { return (T + CV_ROWS - 1) / CV_ROWS; }
+
+// the launch grid of the conv kernels for element size es: channel tiles, time tiles, batch rows
+dim3 conv_grid(int64_t B, int64_t T, int64_t C, int es) {
+  const int64_t per = (int64_t)CV_VECS * (16 / es);
+  return dim3((unsigned)((C + per - 1) / per), (unsigned)conv_tiles(T), (unsigned)B);
+}
 
 }  // namespace
 
@@ -409,13 +533,13 @@ int macai_gdr_conv_fwd(const void* x, const float* w, void* q, void* k, void* v,
   const void* ps[] = {x, w, q, k, v};
   for (const void* p : ps)
     if (!aligned16(p)) return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
-  const int ntiles = (int)((T + CONV_TILE - 1) / CONV_TILE);
   ConvArgs a{x, w, q, k, v, nullptr, nullptr, nullptr, nullptr, nullptr, (int)B, (int)T, (int)C, (int)KD, (int)DK,
-             (int)REP, CONV_TILE, ntiles};
-  const dim3 grid((unsigned)((C / CONV_CH + CONV_GROUP - 1) / CONV_GROUP), (unsigned)ntiles, (unsigned)B);
+             (int)REP, (int)conv_tiles(T)};
   hipStream_t st = (hipStream_t)stream;
-  DISPATCH_PT(dtype, DISPATCH_PV(vdtype, hipLaunchKernelGGL((conv_fwd_kernel<PT, PV>), grid, dim3(CONV_GROUP), 0,
-                                                            st, a)))
+  const int es = dtype == MACAI_GDR_F32 ? 4 : 2;
+  const dim3 grid((unsigned)((C / (16 / es) + 63) / 64), (unsigned)((T + 4 * CV_FWD_STEPS - 1) / (4 * CV_FWD_STEPS)),
+                  (unsigned)B);
+  DISPATCH_PT(dtype, DISPATCH_PV(vdtype, hipLaunchKernelGGL((conv_fwd_kernel<PT, PV>), grid, dim3(256), 0, st, a)))
   return launched(what);
 }
 
@@ -429,31 +553,29 @@ int macai_gdr_conv_bwd(const void* x, const float* w, const void* dq, const void
   const void* ps[] = {x, w, dq, dk, dv, dx, dwp};
   for (const void* p : ps)
     if (!aligned16(p)) return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
-  const int ntiles = (int)((T + CONV_TILE - 1) / CONV_TILE);
+  const int ntiles = (int)conv_tiles(T);
   ConvArgs a{x, w, nullptr, nullptr, nullptr, dq, dk, dv, dx, dwp, (int)B, (int)T, (int)C, (int)KD, (int)DK,
-             (int)REP, CONV_TILE, ntiles};
-  const dim3 grid((unsigned)((C / CONV_CH + CONV_GROUP - 1) / CONV_GROUP), (unsigned)ntiles, (unsigned)B);
+             (int)REP, ntiles};
   hipStream_t st = (hipStream_t)stream;
+  const dim3 grid = conv_grid(B, T, C, dtype == MACAI_GDR_F32 ? 4 : 2);
   if (dwp) {
-    DISPATCH_PT(dtype, DISPATCH_PV(vdtype, hipLaunchKernelGGL((conv_bwd_kernel<PT, PV, true>), grid, dim3(CONV_GROUP),
-                                                              0, st, a)))
+    DISPATCH_PT(dtype, DISPATCH_PV(vdtype, hipLaunchKernelGGL((conv_bwd_tile_kernel<PT, PV, true>), grid,
+                                                              dim3(CV_THREADS), 0, st, a)))
   } else {
-    DISPATCH_PT(dtype, DISPATCH_PV(vdtype, hipLaunchKernelGGL((conv_bwd_kernel<PT, PV, false>), grid,
-                                                              dim3(CONV_GROUP), 0, st, a)))
+    DISPATCH_PT(dtype, DISPATCH_PV(vdtype, hipLaunchKernelGGL((conv_bwd_tile_kernel<PT, PV, false>), grid,
+                                                              dim3(CV_THREADS), 0, st, a)))
   }
   if (int rc = launched(what)) return rc;
   if (dw) {
-    const int n = (int)(C * CONV_K);
-    hipLaunchKernelGGL(sum_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, dwp, dw,
+    const int n = (int)(C * CV_TAPS);
+    hipLaunchKernelGGL(sum_columns_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, dwp, dw,
                        (int)(B * ntiles), n);
     return launched(what);
   }
   return MACAI_GDR_OK;
 }
 
-int64_t macai_gdr_conv_partials(int64_t B, int64_t T, int64_t C) {
-  return B * ((T + CONV_TILE - 1) / CONV_TILE) * C * CONV_K;
-}
+int64_t macai_gdr_conv_partials(int64_t B, int64_t T, int64_t C) { return B * conv_tiles(T) * C * CV_TAPS; }
 
 int macai_gdr_gates_fwd(const void* b, const void* a, const float* A_log, const float* dt_bias, float* beta, float* g,
                         int64_t n, int64_t H, int32_t dtype, void* stream) {
@@ -461,10 +583,13 @@ int macai_gdr_gates_fwd(const void* b, const void* a, const float* A_log, const 
   if (n < 1 || H < 1 || n % H) return fail(MACAI_GDR_EINVAL, "%s: need n >= 1 a multiple of H >= 1", what);
   if (dtype < MACAI_GDR_F32 || dtype > MACAI_GDR_F16) return fail(MACAI_GDR_EUNSUP, "%s: dtype code", what);
   if (!b || !a || !A_log || !dt_bias || !beta || !g) return fail(MACAI_GDR_EINVAL, "%s: null pointer", what);
+  const void* ps[] = {b, a, beta, g};
+  for (const void* p : ps)
+    if (!aligned16(p)) return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
   hipStream_t st = (hipStream_t)stream;
-  const dim3 grid((unsigned)((n + 255) / 256));
-  DISPATCH_PT(dtype, hipLaunchKernelGGL((gates_fwd_kernel<PT>), grid, dim3(256), 0, st, (const PT*)b, (const PT*)a,
-                                        A_log, dt_bias, beta, g, n, (int)H))
+  const dim3 grid((unsigned)((n + GATE_THREADS - 1) / GATE_THREADS));
+  DISPATCH_PT(dtype, hipLaunchKernelGGL((gates_fwd_kernel<PT>), grid, dim3(GATE_THREADS), 0, st, (const PT*)b,
+                                        (const PT*)a, A_log, dt_bias, beta, g, n, (int)H))
   return launched(what);
 }
 
@@ -477,13 +602,16 @@ int macai_gdr_gates_bwd(const void* b, const void* a, const float* A_log, const 
   if (!b || !a || !A_log || !dt_bias || !dbeta || !dg || !db || !da)
     return fail(MACAI_GDR_EINVAL, "%s: null pointer", what);
   if (!dA_log != !ddt_bias) return fail(MACAI_GDR_EINVAL, "%s: dA_log and ddt_bias go together", what);
+  const void* ps[] = {b, a, dbeta, dg, db, da};
+  for (const void* p : ps)
+    if (!aligned16(p)) return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
   hipStream_t st = (hipStream_t)stream;
-  const dim3 grid((unsigned)((n + 255) / 256));
-  DISPATCH_PT(dtype, hipLaunchKernelGGL((gates_bwd_kernel<PT>), grid, dim3(256), 0, st, (const PT*)b, (const PT*)a,
-                                        A_log, dt_bias, dbeta, dg, (PT*)db, (PT*)da, n, (int)H))
+  const dim3 grid((unsigned)((n + GATE_THREADS - 1) / GATE_THREADS));
+  DISPATCH_PT(dtype, hipLaunchKernelGGL((gates_bwd_kernel<PT>), grid, dim3(GATE_THREADS), 0, st, (const PT*)b,
+                                        (const PT*)a, A_log, dt_bias, dbeta, dg, (PT*)db, (PT*)da, n, (int)H))
   if (int rc = launched(what)) return rc;
   if (dA_log) {
-    DISPATCH_PT(dtype, hipLaunchKernelGGL((gates_param_kernel<PT>), dim3((unsigned)H), dim3(256), 0, st,
+    DISPATCH_PT(dtype, hipLaunchKernelGGL((gates_params_kernel<PT>), dim3((unsigned)H), dim3(256), 0, st,
                                           (const PT*)a, A_log, dt_bias, dg, dA_log, ddt_bias, n / H, (int)H))
     return launched(what);
   }

@@ -17,6 +17,9 @@ import torch
 from . import _native as N
 
 CHUNK = 64   # chunk length of the kernels; the drop-in's chunk_size is accepted and not used (as op.py:266-269)
+# The widest key head the bf16 kernels take; wider ones (256, the reference's widest tested, tests/test_harness.py:214-230)
+# run the float32 kernels, with 2-byte inputs upcast exactly and the results cast back.
+BF16_MAX_DK = 128
 # VALUE_SPLIT: workgroups a head-row's value columns are split over in the state passes (each owns DV / VALUE_SPLIT
 # columns as DV / 16 / VALUE_SPLIT waves of 16 columns): "auto" (split_for) or 1, 2, 4, 8, ...
 VALUE_SPLIT = "auto"
@@ -320,13 +323,16 @@ class GatedDeltaRule(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, g, beta, s0, save: bool):
         _check(q, k, v, g, beta, s0)
+        ctx.io_dtype = q.dtype             # o and the q, k, v gradients come back in it
+        if q.shape[-1] > BF16_MAX_DK and q.dtype != torch.float32:
+            q, k, v = q.float(), k.float(), v.float()
         q, k, v, g, beta, s0 = (t.contiguous() for t in (q, k, v, g, beta, s0))
         keep = save and not RECOMPUTE_STATES
         with _on(q.device):
             o, sT, r = _forward(q, k, v, g, beta, s0, False, 1.0, True, keep=keep)
         if save:
             _save(ctx, (q, k, v, g, beta, s0), r)
-        return o, sT
+        return o.to(ctx.io_dtype), sT
 
     @staticmethod
     def backward(ctx, do, dsT):
@@ -335,7 +341,8 @@ class GatedDeltaRule(torch.autograd.Function):
         dsT = None if dsT is None else _as(dsT, torch.float32)
         with _on(q.device):
             dq, dk, dv, dg, dbeta, ds0 = _backward(q, k, v, g, beta, s0, do, dsT, False, 1.0, r=r)
-        return dq, dk, dv, dg, dbeta, ds0, None
+        dt = ctx.io_dtype
+        return dq.to(dt), dk.to(dt), dv.to(dt), dg, dbeta, ds0, None
 
 
 class _DropIn(torch.autograd.Function):
@@ -383,14 +390,16 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size: int = 64, ini
     DV]. The reference refuses cu_seqlens (op.py:270-273); here each sequence is chunked separately inside the
     kernels. Returns the output [B, T, H, DV] in the query's dtype and the final state (float32) when
     output_final_state, else None.  chunk_size is accepted and unused (the kernels use 64-token chunks).  bfloat16
-    inputs run on bf16 MFMA with fp32 accumulation and an fp32 state; float32 inputs on fp32 MFMA; float16 inputs
-    are upcast exactly and computed as float32, the output cast back to float16 (the reference does the same: its
-    prologue and `value.float()` run the rule in float32, op.py:276-285, 297).  With use_qk_l2norm_in_kernel=False
+    inputs run on bf16 MFMA with fp32 accumulation and an fp32 state; float32 inputs on fp32 MFMA; float16 inputs,
+    and bfloat16 ones with key heads wider than 128 (up to 256), are upcast exactly and computed as float32, the
+    output cast back (the reference runs every input this way: its prologue and `value.float()` run the rule in
+    float32, op.py:276-285, 297).  With use_qk_l2norm_in_kernel=False
     the query is only scaled by DK^-1/2 (op.py:279-283), inside the kernels."""
     cu = kwargs.get("cu_seqlens")
     pack = None if cu is None else _pack(cu, query.shape[1], query.device)
     dtype = query.dtype
-    cdt = torch.bfloat16 if dtype == torch.bfloat16 else torch.float32
+    # bf16 runs on bf16 MFMA up to key width 128; float16, float32 and wider keys on the float32 kernels
+    cdt = torch.bfloat16 if dtype == torch.bfloat16 and query.shape[-1] <= BF16_MAX_DK else torch.float32
     q, k, v = _as(query, cdt), _as(key, cdt), _as(value, cdt)
     gf, bf = _as(g, torch.float32), _as(beta, torch.float32)
     s0 = None if initial_state is None else _as(initial_state, torch.float32)
@@ -412,7 +421,9 @@ def recurrent_gated_delta_rule(query, key, value, g, beta, initial_state=None, o
     T = query.shape[1]
     needs_grad = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (query, key, value, g, beta, initial_state))
-    if T != 1 or needs_grad or kwargs.get("cu_seqlens") is not None:
+    widths = (query.shape[-1], value.shape[-1])
+    if (T != 1 or needs_grad or kwargs.get("cu_seqlens") is not None
+            or not all(w in (64, 128) for w in widths)):   # the decode kernel's head widths
         return chunk_gated_delta_rule(query, key, value, g, beta, initial_state=initial_state,
                                       output_final_state=output_final_state,
                                       use_qk_l2norm_in_kernel=use_qk_l2norm_in_kernel,

@@ -295,6 +295,42 @@ def test_rule_long_sequence(T):
     check_rule(gdr.harness_inputs(1, T, 1, 128, 128, seed=3), 1e-3)
 
 
+@pytest.mark.parametrize("shape", [(1, 33, 2, 256, 128), (2, 150, 3, 256, 64)])
+def test_rule_wide_keys(shape):
+    """Key heads of 256 (reference tests/test_harness.py:214-230, make(1, 33, 2, 256, 128)): forward and the chunked
+    backward, at the harness bar.  The float32 kernels stage key columns in two passes (prep) and read the chunk
+    tiles from memory where a stage does not fit LDS (the state passes)."""
+    _say(f"case rule_wide {shape}")
+    check_rule(gdr.harness_inputs(*shape, seed=2), 2e-4)
+
+
+@pytest.mark.parametrize("split", [2, 4, 8])
+def test_wide_keys_every_split(split):
+    """Key width 256 at each value split (4, 2 and 1 column waves a workgroup) and in both backward modes: the same
+    bits as the default launch."""
+    _say(f"case wide split={split}")
+    inp = gdr.make_inputs(1, 100, 2, 2, 256, 128, torch.float32, s0=True, seed=3)
+    ref = _grads_once(inp, dsT_width=256)
+    old = op.RECOMPUTE_STATES
+    try:
+        for mode in (True, False):
+            op.RECOMPUTE_STATES = mode
+            got = _grads_once(inp, split, dsT_width=256)
+            assert all(torch.equal(a, b) for a, b in zip(ref, got))
+    finally:
+        op.RECOMPUTE_STATES = old
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_dropin_wide_keys_2byte(dtype):
+    """bf16 / fp16 drop-in at key width 256: upcast exactly and computed by the float32 kernels, output and the q, k,
+    v gradients returned in the input dtype; within the 2-byte bar."""
+    _say(f"case dropin_wide {dtype}")
+    inp = gdr.make_inputs(2, 70, 2, 2, 256, 128, dtype, s0=True, seed=7)
+    dsT = torch.randn(2, 2, 256, 128, generator=torch.Generator().manual_seed(9))
+    check_dropin(inp, bar=5e-3, dsT=dsT)
+
+
 def test_rule_bf16_operands():
     """The contract with bf16 q/k/v (bf16 MFMA operands, fp32 accumulation): within 1e-2."""
     _say("case rule_bf16")
@@ -302,12 +338,13 @@ def test_rule_bf16_operands():
 
 
 # ---- determinism and launch-policy invariance ------------------------------------------------------------------------
-def _grads_once(inp, split=None):
+def _grads_once(inp, split=None, dsT_width=128):
     old = op.VALUE_SPLIT
     try:
         if split is not None:
             op.VALUE_SPLIT = split
-        o, sT, g = run_dropin(inp, dsT=torch.ones(inp["value"].shape[0], inp["value"].shape[2], 128, 128))
+        o, sT, g = run_dropin(inp, dsT=torch.ones(inp["value"].shape[0], inp["value"].shape[2], dsT_width,
+                                                  inp["value"].shape[-1]))
     finally:
         op.VALUE_SPLIT = old
     return [o, sT] + [g[n] for n in sorted(g)]

@@ -50,6 +50,7 @@ def _prep(**over):
 def test_abi_rejects_bad_arguments_before_launch():
     L = N.lib()
     assert _prep(DK=96) == N.EUNSUP and b"key head width" in L.macai_gdr_last_error()
+    assert _prep(DK=256) == N.EUNSUP and b"256 takes float32" in L.macai_gdr_last_error()   # bf16 at width 256
     assert _prep(DV=48) == N.EUNSUP and b"value head width" in L.macai_gdr_last_error()
     assert _prep(dtype=7) == N.EUNSUP
     assert _prep(T=0) == N.EINVAL
@@ -124,7 +125,8 @@ def test_producer_abi_rejects_bad_arguments():
     assert conv(p + 8, p, p, p, p) == N.EINVAL and b"aligned" in L.macai_gdr_last_error()
     assert conv(p, p, p, p, p, T=0) == N.EINVAL
     assert L.macai_gdr_conv_bwd(p, p, p, p, p, p, p, None, 1, 8, 6144, 2048, 128, 1, 128, 1, 0, None) == N.EINVAL
-    assert L.macai_gdr_conv_partials(2, 33, 6144) == 2 * 3 * 6144 * 4
+    assert L.macai_gdr_conv_partials(2, 33, 6144) == 2 * 1 * 6144 * 4      # tiles of 64 time steps
+    assert L.macai_gdr_conv_partials(2, 130, 6144) == 2 * 3 * 6144 * 4
     assert L.macai_gdr_gates_fwd(p, p, p, p, p, p, 30, 16, 1, None) == N.EINVAL     # n not a multiple of H
     assert L.macai_gdr_gates_fwd(p, p, p, p, p, p, 32, 16, 9, None) == N.EUNSUP
     assert L.macai_gdr_gates_bwd(p, p, p, p, p, p, p, p, p, None, 32, 16, 1, None) == N.EINVAL
