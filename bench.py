@@ -94,13 +94,14 @@ def make_inputs(cfg, seed, dev, **over):
     return out, c
 
 
-def kernel_costs(B, T, H, DK, DV, es=2, Hk=None, chunks=None, keep=False):
+def kernel_costs(B, T, H, DK, DV, es=2, Hk=None, chunks=None, keep=False, segs=1):
     """Algorithmic bytes (each declared input read once, each output written once, from argument sizes), split into
     reads and writes, and dense FLOPs (2 per multiply-add, triangular products counted dense) per launch of each
     kernel of the training step.  Hk: key heads of q and k when they come unrepeated (grouped value heads); H by
     default.  chunks: chunks per head over the batch (B ceil(T / 64) by default; packed rows chunk each sequence on
     its own).  keep: the forward's prep also writes A and its state pass S_c and Vn (the stored-states mode: the
-    backward then runs neither prep nor the recompute pass)."""
+    backward then runs neither prep nor the recompute pass).  segs: segments a row's forward runs side by side (the
+    map pass reads W, U, Ke, GL and writes each segment's [A | B]; the scan composes them)."""
     Hk = Hk or H
     chunks = chunks or B * math.ceil(T / C)
     n = H * chunks                       # chunk-heads
@@ -133,6 +134,11 @@ def kernel_costs(B, T, H, DK, DV, es=2, Hk=None, chunks=None, keep=False):
     }
     # the recompute and reverse passes in one launch (macai_gdr_state_pair)
     rw["state_pair"] = tuple(a + b for a, b in zip(rw["state_fwd_store"], rw["state_bwd"]))
+    if segs > 1:
+        maps = B * (segs - 1) * H * DK * (DK + DV) * 4    # the last segment's map is not needed
+        nm = n - B * H * (math.ceil(T / C) - (segs - 1) * math.ceil(math.ceil(T / C) / segs))
+        rw["state_map"] = (nm * (2 * cdk * es + cdv * 4 + 4), maps, nm * 2 * 2 * C * DK * (DK + DV))
+        rw["state_scan"] = (maps + B * H * sdk, B * segs * H * sdk, B * (segs - 1) * H * 2 * DK * DK * DV)
     return {k: dict(bytes=r + w, reads=r, writes=w, flops=f) for k, (r, w, f) in rw.items()}
 
 
@@ -322,7 +328,8 @@ def bench_prefill(args):
     op.EVENTS = None
     t = {name: sum(v) / len(v) for name, v in t.items()}
     B, T, H, DK, DV = c["B"], c["T"], c["Hv"], c["DK"], c["DV"]
-    cost = kernel_costs(B, T, H, DK, DV, Hk=c["Hk"])
+    segs = op.segments_for(B, T, H)
+    cost = kernel_costs(B, T, H, DK, DV, Hk=c["Hk"], segs=segs)
     kernels = {n: {"us": round(x * 1e6, 2), "GB/s": round(cost[n]["bytes"] / x / 1e9, 1),
                    "hbm_frac": round(cost[n]["bytes"] / x / HBM_PEAK, 4)} for n, x in t.items()}
     st = t["state_fwd_out"]
@@ -331,13 +338,13 @@ def bench_prefill(args):
             "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 4), "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
             "config": {"workload": "BASELINE config 3: long single-row prefill, forward only", "B": B, "T": T,
-                       "Hk": c["Hk"], "Hv": H, "DK": DK, "DV": DV, "chunk": C,
-                       "value_split": op.split_for(B * H, T, DV)},
+                       "Hk": c["Hk"], "Hv": H, "DK": DK, "DV": DV, "chunk": C, "segments": segs,
+                       "value_split": op.split_for(B * segs * H, T, DV)},
             "roofline": {"kernel": "state_fwd_out", "timing": "in-step HIP events", "bound": "hbm",
                          "achieved": round(cost["state_fwd_out"]["bytes"] / st / 1e9, 1), "peak": HBM_PEAK / 1e9,
                          "unit": "GB/s", "frac": round(cost["state_fwd_out"]["bytes"] / st / HBM_PEAK, 4),
                          "traffic": None},
-            "chain_us_per_chunk": round(st * 1e6 / math.ceil(T / C), 3),
+            "chain_us_per_chunk": round(st * 1e6 / math.ceil(math.ceil(T / C) / segs), 3),
             "kernels": kernels}
     print(json.dumps(line), flush=True)
 

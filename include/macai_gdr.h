@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define MACAI_GDR_ABI_VERSION 10
+#define MACAI_GDR_ABI_VERSION 11
 
 /* dtype codes (the rule takes F32 and BF16; the producers also F16) */
 #define MACAI_GDR_F32 0
@@ -110,6 +110,21 @@ int macai_gdr_state_pair(const void* W, const float* U, const void* Ke, const vo
                          const float* s0, const void* dO, const float* dsT, float* Sc, void* Vn, float* dSn, void* dVn,
                          float* ds0, int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV, int32_t dtype,
                          int32_t split, const int32_t* pack, int64_t NT, void* stream);
+
+/* Sequence parallelism for long rows (no counterpart in the reference, whose state pass walks a row's chunks in one
+ * chain): the state pass is affine in its starting state, S_end = A S_0 + B, so a row split into segments (packed-row
+ * sequences of one row) can run its segments side by side.  macai_gdr_state_map writes each sequence's map
+ * [A | B] (float32 [B, H, DK, DK + DV]: A = the pass from the identity with U taken as zero, B = the pass from zero),
+ * reading what macai_gdr_state_fwd reads for its states (W, U, Ke, GL).  macai_gdr_state_scan composes them in order
+ * along each row: starts[r, s] = the state entering segment s of row r, starts[r, 0] = s0[r] (NULL = zeros),
+ * starts[r, s + 1] = A_{r,s} starts[r, s] + B_{r,s} (maps and starts [rows * nseg, H, ...], s0 [rows, H, DK, DV]).
+ * macai_gdr_state_fwd over the segments from `starts` then gives the row's output and, for its last segment, the final
+ * state.  split as in macai_gdr_state_fwd over the DK + DV columns. */
+int macai_gdr_state_map(const void* W, const float* U, const void* Ke, const float* GL, float* maps, int64_t B,
+                        int64_t T, int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t split, const int32_t* pack,
+                        int64_t NT, void* stream);
+int macai_gdr_state_scan(const float* maps, const float* s0, float* starts, int64_t rows, int64_t nseg, int64_t H,
+                         int64_t DK, int64_t DV, void* stream);
 
 /* The per-chunk backward (north star (4)): dq, dk (w.r.t. the raw inputs when use_l2norm; per value head, [B, T, H,
  * DK]), dv in dtype; dg, dbeta in float32; one writer per element (bitwise deterministic).  Replaces

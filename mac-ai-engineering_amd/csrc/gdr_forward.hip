@@ -31,20 +31,21 @@ int64_t layout(int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV, int32_t 
   return total;
 }
 
-// The value split for `rows` head-rows when the caller passes 0: the smallest split that gives every CU a workgroup
-// (rows x split >= 256) with at most four column waves a workgroup, else the largest such split (the rule of the
-// Python host's op.split_for: eight waves plus the loader leave too few registers a wave).
+// The value split for `rows` head-rows when the caller passes 0: the largest split with at most four column waves a
+// workgroup whose workgroups all fit the 256 CUs at once (rows x split <= 256), else the smallest such split (the rule
+// of the Python host's op.split_for: eight waves plus the loader leave too few registers a wave, and a second round
+// of workgroups would double a sequential pass's time).
 int32_t auto_split(int64_t rows, int64_t DV) {
   const int ncb = (int)(DV / 16);
-  int32_t last = 0;
+  int32_t first = 0, best = 0;
   for (int s = 1; s <= ncb; ++s) {
     if (ncb % s) continue;
     const int nw = ncb / s;
     if (nw != 1 && nw != 2 && nw != 4) continue;
-    last = s;
-    if (rows * s >= 256) return s;
+    if (!first) first = s;
+    if (rows * s <= 256) best = s;
   }
-  return last;   // 0 when DV / 16 has no such split: the entry point's own choice
+  return best ? best : first;   // 0 when DV / 16 has no such split: the entry point's own choice
 }
 
 int forward_in(const char* what, const void* q, const void* k, const void* v, const float* g, const float* beta,

@@ -729,8 +729,13 @@ struct StateFwdLds {
 };
 
 // The pass of workgroup f of the launch (see state_map), with `lds` the workgroup's LDS (StateFwdLds::ELEMS elements).
-template <typename MT, int DK, int NW, bool OUT, bool STORE>
+// MAP (with neither OUT nor STORE): the chunk map of each sequence instead of its states.  A sequence's pass is affine
+// in its starting state, S_end = A S_0 + B, so it runs on DK + DV columns: the first DK start from the identity with U
+// taken as zero (they end as A, DK x DK), the other DV from zero with the real U (they end as B); sT receives
+// [A | B] per head-row, row pitch DK + DV.
+template <typename MT, int DK, int NW, bool OUT, bool STORE, bool MAP = false>
 __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, int f) {
+  static_assert(!MAP || (!OUT && !STORE), "the map pass writes only the maps");
   using L = StateFwdLds<MT, DK, OUT, STORE, NW>;
   using GW = typename L::GW;
   using GM = typename L::GM;
@@ -792,9 +797,16 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
 
   const int v0 = (slice * NW + w) * 16;
   const int col = v0 + (l & 15);
+  const int DVt = MAP ? DV + DK : DV;      // the pass's columns (the map pass: A's DK, then B's DV)
+  const bool ident = MAP && v0 < DK;       // a map column of A: identity start, no U (uniform across the wave)
   const size_t o_base = ((size_t)tb * T * H + h) * DV, o_pitch = (size_t)H * DV;
   auto loadU = [&](int c, f4* U) {
-    const float* Uc = a.U + (crow * NT + c) * C * DV + (size_t)(4 * j) * DV + col;
+    if (ident) {
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) U[mi] = f4{0.f, 0.f, 0.f, 0.f};
+      return;
+    }
+    const float* Uc = a.U + (crow * NT + c) * C * DV + (size_t)(4 * j) * DV + (MAP ? col - DK : col);
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
@@ -833,7 +845,14 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
   };
 
   f4 S[ND];
-  load_state(S, a.s0, (size_t)hr * DK * DV, DV, col);
+  if constexpr (MAP) {
+#pragma unroll
+    for (int di = 0; di < ND; ++di)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) S[di][r] = (ident && 16 * di + 4 * j + r == col) ? 1.f : 0.f;
+  } else {
+    load_state(S, a.s0, (size_t)hr * DK * DV, DV, col);
+  }
 
   f4 Un[4];
   float gln = 0.f;
@@ -952,14 +971,71 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
 #pragma unroll
     for (int di = 0; di < ND; ++di)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) a.sT[(size_t)hr * DK * DV + (16 * di + 4 * j + r) * DV + col] = S[di][r];
+      for (int r = 0; r < 4; ++r) a.sT[(size_t)hr * DK * DVt + (16 * di + 4 * j + r) * DVt + col] = S[di][r];
   }
 }
 
-template <typename MT, int DK, int NW, bool OUT, bool STORE>
+template <typename MT, int DK, int NW, bool OUT, bool STORE, bool MAP = false>
 __global__ void __launch_bounds__(64 * (NW + 1)) state_fwd_kernel(StateFwdArgs a) {
   __shared__ __attribute__((aligned(1024))) MT lds[StateFwdLds<MT, DK, OUT, STORE, NW>::ELEMS];
-  state_fwd_body<MT, DK, NW, OUT, STORE>(a, lds, blockIdx.x);
+  state_fwd_body<MT, DK, NW, OUT, STORE, MAP>(a, lds, blockIdx.x);
+}
+
+// The sequential composition of the segment maps of a row: starts[s] = the state entering segment s, starts[0] = s0
+// (zeros when null), starts[s + 1] = A_s starts[s] + B_s, maps[s] = [A_s | B_s] as the map pass writes them.  A
+// workgroup takes 16 value columns of a (row, head); the state slice [DK x 16] sits in LDS, and each step a lane forms
+// 8 columns of one state row, A's row read with 16-byte loads all in flight: the chain of steps is short (one per
+// segment) and latency-bound, so it is spread over a workgroup's lanes rather than one wave's MFMAs.
+template <int DK>
+__global__ void __launch_bounds__(256) state_scan_kernel(const float* maps, const float* s0, float* starts, int nseg,
+                                                         int H, int DV) {
+  __shared__ __attribute__((aligned(16))) float Sl[DK * 16];
+  const int h = blockIdx.y, r = blockIdx.z, c0 = blockIdx.x * 16;
+  const int DVt = DK + DV;
+  for (int i = threadIdx.x; i < DK * 16; i += 256) {
+    const int d = i / 16, c = i % 16;
+    Sl[i] = s0 ? s0[((size_t)r * H + h) * DK * DV + (size_t)d * DV + c0 + c] : 0.f;
+  }
+  __syncthreads();
+  for (int sg = 0; sg < nseg; ++sg) {
+    const size_t seg = (size_t)r * nseg + sg;
+    float* out = starts + (seg * H + h) * DK * DV;
+    for (int i = threadIdx.x; i < DK * 16; i += 256) out[(size_t)(i / 16) * DV + c0 + i % 16] = Sl[i];
+    if (sg + 1 == nseg) break;
+    const float* Mp = maps + (seg * H + h) * DK * DVt;
+    float acc[(2 * DK + 255) / 256][8];
+#pragma unroll
+    for (int u = 0; u < (2 * DK + 255) / 256; ++u) {
+      const int pr = threadIdx.x + 256 * u, d = pr / 2, cg = (pr % 2) * 8;
+      if (pr >= 2 * DK) break;
+      const float* Ar = Mp + (size_t)d * DVt;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[u][i] = Ar[DK + c0 + cg + i];           // B_s
+#pragma unroll 8
+      for (int k4 = 0; k4 < DK; k4 += 4) {
+        const f4 a = *reinterpret_cast<const f4*>(Ar + k4);                  // A_s[d][k4 .. k4 + 3]
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const f4 s_lo = *reinterpret_cast<const f4*>(Sl + (k4 + kk) * 16 + cg);
+          const f4 s_hi = *reinterpret_cast<const f4*>(Sl + (k4 + kk) * 16 + cg + 4);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            acc[u][i] = fmaf(a[kk], s_lo[i], acc[u][i]);
+            acc[u][4 + i] = fmaf(a[kk], s_hi[i], acc[u][4 + i]);
+          }
+        }
+      }
+    }
+    __syncthreads();                       // every lane has read this step's state
+#pragma unroll
+    for (int u = 0; u < (2 * DK + 255) / 256; ++u) {
+      const int pr = threadIdx.x + 256 * u, d = pr / 2, cg = (pr % 2) * 8;
+      if (pr >= 2 * DK) break;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) Sl[d * 16 + cg + i] = acc[u][i];
+    }
+    __syncthreads();
+  }
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
@@ -2809,6 +2885,56 @@ int macai_gdr_state_pair(const void* W, const float* U, const void* Ke, const vo
     DISPATCH_DK(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_pair_kernel<bf16, DKC, NWC>), grid, block, 0, st, af, ab,
                                                        nfwd)));
   }
+  return launched(what);
+}
+
+int macai_gdr_state_map(const void* W, const float* U, const void* Ke, const float* GL, float* maps, int64_t B,
+                        int64_t T, int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t split, const int32_t* pack,
+                        int64_t NT_packed, void* stream) {
+  const char* what = "macai_gdr_state_map";
+  int64_t NT = 0;
+  int rc = check_common(what, pack ? 1 : B, T, H, DK, DV, dtype);
+  if (!rc) rc = pack_chunks(what, pack, NT_packed, B, T, &NT);
+  if (rc) return rc;
+  if (!W || !U || !Ke || !GL || !maps) return fail(MACAI_GDR_EINVAL, "%s: null pointer", what);
+  const void* ps[] = {W, U, Ke, maps};
+  for (const void* p : ps)
+    if (!aligned16(p)) return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
+  int nw, nslice;
+  if ((rc = pick_waves(DK + DV, split, what, &nw, &nslice))) return rc;
+  StateFwdArgs a{W, U, Ke, GL, nullptr, nullptr, nullptr, nullptr, maps, nullptr, nullptr, (int)B, (int)T, (int)H,
+                 (int)DV, (int)NT, nslice, pack};
+  const int HR = (int)(B * H);
+  dim3 grid((unsigned)(8 * nslice * ((HR + 7) / 8)));
+  dim3 block(64 * (nw + 1));
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == MACAI_GDR_F32) {
+    DISPATCH_DK_F32(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_fwd_kernel<float, DKC, NWC, false, false, true>), grid,
+                                                           block, 0, st, a)));
+  } else {
+    DISPATCH_DK(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_fwd_kernel<bf16, DKC, NWC, false, false, true>), grid,
+                                                       block, 0, st, a)));
+  }
+  return launched(what);
+}
+
+int macai_gdr_state_scan(const float* maps, const float* s0, float* starts, int64_t rows, int64_t nseg, int64_t H,
+                         int64_t DK, int64_t DV, void* stream) {
+  const char* what = "macai_gdr_state_scan";
+  if (rows < 1 || nseg < 1 || H < 1 || rows > 65535 || H > 65535)
+    return fail(MACAI_GDR_EINVAL, "%s: rows, segments and heads must be >= 1 (and rows, heads <= 65535)", what);
+  if (DK != 32 && DK != 64 && DK != 128 && DK != 256)
+    return fail(MACAI_GDR_EUNSUP, "%s: key head width must be 32, 64, 128 or 256 (got %lld)", what, (long long)DK);
+  if (DV < 16 || DV % 16 != 0 || DV > 512)
+    return fail(MACAI_GDR_EUNSUP, "%s: value head width must be a multiple of 16 in [16, 512] (got %lld)", what,
+                (long long)DV);
+  if (!maps || !starts) return fail(MACAI_GDR_EINVAL, "%s: null pointer", what);
+  if (!aligned16(maps) || !aligned16(s0) || !aligned16(starts))
+    return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
+  const dim3 grid((unsigned)(DV / 16), (unsigned)H, (unsigned)rows);
+  hipStream_t st = (hipStream_t)stream;
+  DISPATCH_DK_F32(DK, hipLaunchKernelGGL((state_scan_kernel<DKC>), grid, dim3(256), 0, st, maps, s0, starts, (int)nseg,
+                                         (int)H, (int)DV));
   return launched(what);
 }
 

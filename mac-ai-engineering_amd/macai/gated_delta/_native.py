@@ -15,7 +15,7 @@ F32, BF16, F16 = 0, 1, 2
 OK, EINVAL, EUNSUP, ELAUNCH = 0, 1, 2, 3
 STORE_STATES, NO_OUTPUT = 1, 8
 NOALLOC_SCRATCH_BYTES = 128 << 20     # MACAI_GDR_NOALLOC_SCRATCH_BYTES
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _p, _i64, _i32, _f = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 # name -> argument types (the order of include/macai_gdr.h)
@@ -24,6 +24,8 @@ SIGNATURES = {
     "macai_gdr_state_fwd": [_p] * 11 + [_i64] * 5 + [_i32, _i32, _i32, _p, _i64, _p],
     "macai_gdr_state_bwd": [_p] * 10 + [_i64] * 5 + [_i32, _i32, _p, _i64, _p],
     "macai_gdr_state_pair": [_p] * 14 + [_i64] * 5 + [_i32, _i32, _p, _i64, _p],
+    "macai_gdr_state_map": [_p] * 5 + [_i64] * 5 + [_i32, _i32, _p, _i64, _p],
+    "macai_gdr_state_scan": [_p] * 3 + [_i64] * 5 + [_p],
     "macai_gdr_chunk_bwd": [_p] * 16 + [_i64] * 6 + [_i32, _i32, _f, _p, _i64, _p],
     "macai_gdr_decode": [_p] * 8 + [_i64] * 5 + [_i32, _i32, _f, _p],
     "macai_gdr_group_sum": [_p] * 2 + [_i64] * 5 + [_i32, _p],

@@ -44,6 +44,13 @@ OVERLAP = True
 # q's (176 MiB a layer at B = 4, T = 1024, H = 16), in one allocation saved with save_for_backward (so saved-tensor
 # hooks, activation checkpointing and offload see it and it goes with the graph).
 RECOMPUTE_STATES = True
+# SEQUENCE_SPLIT: segments a long row's forward without gradients runs side by side.  A state pass is a chain over
+# the row's chunks; with few head-rows (one long prefill) it fills few CUs and its length is the row's.  The pass is
+# affine in its starting state, so the row splits into segments: each segment's map [A | B] (macai_gdr_state_map,
+# from the identity and from zero), their composition in order (macai_gdr_state_scan) for each segment's starting
+# state, and the output pass over all segments at once.  "auto": for a single row (B = 1, no cu_seqlens), the largest
+# power of two P with P x H <= 64 head-rows and at least 32 chunks a segment (P = 1 otherwise); an int forces P.
+SEQUENCE_SPLIT = "auto"
 
 
 def _launch(name: str, entry: str, *args):
@@ -79,17 +86,17 @@ def split_for(rows: int, T: int, dv: int, share: int = 1) -> int:
 
 def _split_for(rows: int, T: int, dv: int, share: int = 1) -> int:
     """VALUE_SPLIT's choice for `rows` head-rows (B x H) of value width dv, for a pass that gets 1 / share of the
-    chip: "auto" takes the smallest valid split that gives at least 256 / share workgroups (one per CU), else the
-    largest; an int setting is rounded down to a valid split.  "auto" leaves out the splits with 8 waves of columns
-    per workgroup where another exists: with the loader wave that is 9 waves, 3 on one SIMD, which caps a wave at 168
-    VGPRs: the 128-wide state kernels spill there (the backward's pair pass ran 2.1-2.8x slower than at 4 waves)."""
+    chip: "auto" takes the largest valid split whose workgroups fit the pass's share of the CUs at once (rows x split
+    <= 256 / share: a state pass's workgroup holds its CU's LDS, and a second round of a sequential pass would double
+    its time), else the smallest; an int setting is rounded down to a valid split.  "auto" leaves out the splits with
+    8 waves of columns per workgroup where another exists: with the loader wave that is 9 waves, 3 on one SIMD, which
+    caps a wave at 168 VGPRs: the 128-wide state kernels spill there (the backward's pair pass ran 2.1-2.8x slower
+    than at 4 waves)."""
     valid = valid_splits(dv)
     if VALUE_SPLIT == "auto":
         valid = [s for s in valid if (dv // 16) // s <= 4] or valid
-        for s in valid:
-            if rows * s * share >= 256:
-                return s
-        return valid[-1]
+        fits = [s for s in valid if rows * s * share <= 256]
+        return fits[-1] if fits else valid[0]
     want = int(VALUE_SPLIT)
     below = [s for s in valid if s <= want]
     return below[-1] if below else valid[0]
@@ -230,10 +237,73 @@ def _prep(q, k, v, g, beta, l2norm: bool, q_scale: float, r, stream, pack=None, 
             r["A"], B, T, H, Hk, DK, DV, N.dtype_code(q.dtype), int(l2norm), q_scale, *_pack_args(pack), stream)
 
 
-def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, pack=None, keep=False):
+def segments_for(B: int, T: int, H: int, pack=None, save: bool = False) -> int:
+    """SEQUENCE_SPLIT's number of segments for a forward of B rows of T tokens over H value heads (1: no split).  A
+    forward that saves for a backward never splits: the training step keeps the bits of the unsplit pass."""
+    if save or pack is not None or B != 1:
+        return 1
+    NT = math.ceil(T / CHUNK)
+    if SEQUENCE_SPLIT != "auto":
+        return max(1, min(int(SEQUENCE_SPLIT), NT))
+    P = 1
+    while 2 * P * H <= 64 and NT // (2 * P) >= 32:
+        P *= 2
+    return P
+
+
+_SEGS = {}       # (T, P, device) -> the packed-row table of a row split into P segments of whole chunks
+
+
+def _segment_table(T: int, P: int, device):
+    """The packed-row table (include/macai_gdr.h) of one row of T tokens as P sequences of consecutive whole chunks:
+    chunk c spans tokens 64 c .. 64 c + 63 (the row's end bounds its last chunk), segment s owns chunks
+    ceil(NT / P) s .. (the last one the rest).  Returns (table, NT)."""
+    key = (T, P, str(device))
+    hit = _SEGS.get(key)
+    if hit is None:
+        NT = math.ceil(T / CHUNK)
+        L = math.ceil(NT / P)
+        c0 = [min(s * L, NT) for s in range(P)] + [NT]
+        table = torch.tensor([c * CHUNK for c in range(NT)] + [T] * NT + c0, dtype=torch.int32, device=device)
+        hit = _SEGS[key] = (table, NT)
+    return hit
+
+
+def _forward_segments(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, nseg: int):
+    """The forward of one row split into nseg segments (SEQUENCE_SPLIT): prep, the segments' maps, their composition
+    into each segment's starting state, then the output pass over the segments side by side."""
+    _, T, H, Hk, DK, DV, NT = _dims(q, v)
+    dev, dt = q.device, q.dtype
+    code, stream = N.dtype_code(dt), N.stream_of(q)
+    f32 = torch.float32
+    P = N.ptr
+    r = _carve(dev, (1, H, NT, DK, DV, q.element_size(), True, False, False, False))
+    _prep(q, k, v, g, beta, l2norm, q_scale, r, stream, None, "prep_fwd")
+    table, NT = _segment_table(T, nseg, dev)
+    # the maps of all segments but the last (its map composes into no later start): the first nseg - 1 sequences of
+    # the table
+    maps = torch.empty(nseg - 1, H, DK, DK + DV, device=dev, dtype=f32)
+    _launch("state_map", "macai_gdr_state_map", r["W"], r["U"], r["Ke"], r["GL"], P(maps), nseg - 1, T, H, DK, DV,
+            code, split_for((nseg - 1) * H, T, DK + DV), P(table), NT, stream)
+    starts = torch.empty(nseg, H, DK, DV, device=dev, dtype=f32)
+    _launch("state_scan", "macai_gdr_state_scan", P(maps), P(s0), P(starts), 1, nseg, H, DK, DV, stream)
+    o = torch.empty(1, T, H, DV, device=dev, dtype=dt)
+    sTs = torch.empty(nseg, H, DK, DV, device=dev, dtype=f32) if want_sT else None
+    split = split_for(nseg * H, T, DV)
+    _launch("state_fwd_out", "macai_gdr_state_fwd", r["W"], r["U"], r["Ke"], r["GL"], r["Qg"], r["M"], P(starts), P(o),
+            P(sTs), None, None, nseg, T, H, DK, DV, code, 0, split, P(table), NT, stream)
+    CALLS[f"fwd seg{nseg} s{split}"] += 1
+    return o, (None if sTs is None else sTs[nseg - 1:]), None
+
+
+def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, pack=None, keep=False, save=True):
     """prep, then the state pass with the output: returns (o in q's dtype, sT or None, and when keep -- for the
-    backward -- prep's operands with A and the chunk states Sc, Vn, else None)."""
+    backward -- prep's operands with A and the chunk states Sc, Vn, else None).  A single long row whose forward saves
+    nothing for a backward may run as segments side by side (SEQUENCE_SPLIT)."""
     B, T, H, Hk, DK, DV, NT = _dims(q, v, pack)
+    nseg = segments_for(B, T, H, pack, save or keep)
+    if nseg > 1:
+        return _forward_segments(q, k, v, g, beta, s0, l2norm, q_scale, want_sT, nseg)
     Bc = q.shape[0]
     dev, dt = q.device, q.dtype
     code, stream = N.dtype_code(dt), N.stream_of(q)
@@ -329,7 +399,7 @@ class GatedDeltaRule(torch.autograd.Function):
         q, k, v, g, beta, s0 = (t.contiguous() for t in (q, k, v, g, beta, s0))
         keep = save and not RECOMPUTE_STATES
         with _on(q.device):
-            o, sT, r = _forward(q, k, v, g, beta, s0, False, 1.0, True, keep=keep)
+            o, sT, r = _forward(q, k, v, g, beta, s0, False, 1.0, True, keep=keep, save=save)
         if save:
             _save(ctx, (q, k, v, g, beta, s0), r)
         return o.to(ctx.io_dtype), sT
@@ -356,7 +426,7 @@ class _DropIn(torch.autograd.Function):
                 pack=None):
         keep = save and not RECOMPUTE_STATES
         with _on(query.device):
-            o, sT, r = _forward(query, key, value, g, beta, s0, l2norm, q_scale, want_sT, pack, keep)
+            o, sT, r = _forward(query, key, value, g, beta, s0, l2norm, q_scale, want_sT, pack, keep, save)
         if save:
             _save(ctx, (query, key, value, g, beta, s0), r)
             ctx.cfg = (l2norm, q_scale, s0 is not None)

@@ -129,6 +129,24 @@ def chunked_forward_segments(q, k, v, g, beta, s0, C=64, seg=4096):
     return torch.cat(outs, 1), S
 
 
+def segment_map(q, k, v, g, beta, C=64):
+    """The chunked state pass (F3-F4) as an affine map of its starting state: (A [B,H,DK,DK], Bm [B,H,DK,DV]) with
+    S_end = A S_0 + Bm, composed chunk by chunk: S <- (gamma_last I - K^T diag(e) W) S + K^T diag(e) U.  The product's
+    sequence-parallel forward splits a row into segments by this map (no reference counterpart: the reference walks
+    a row in one chain); pinned in tests/test_oracle.py against chunked_forward."""
+    P = chunk_prep(k, v, g, beta, None, C)
+    B, H, nt = P["G"].shape[:3]
+    DK, DV = k.shape[-1], v.shape[-1]
+    eye = torch.eye(DK, dtype=k.dtype)
+    A = eye.expand(B, H, DK, DK).clone()
+    Bm = torch.zeros(B, H, DK, DV, dtype=k.dtype)
+    for c in range(nt):
+        KeT = (P["e"][:, :, c, :, None] * P["K"][:, :, c]).transpose(-1, -2)
+        Ac = P["gam"][:, :, c, -1, None, None] * eye - KeT @ P["W"][:, :, c]
+        A, Bm = Ac @ A, Ac @ Bm + KeT @ P["U"][:, :, c]
+    return A, Bm
+
+
 def chunked_backward(q, k, v, g, beta, s0, do, dsT, C=64, P=None):
     """B1-B6 (q already normalised and scaled), dg in the reference's no-cancellation form (_chunked.py:1138-1176).
     Returns (dq, dk, dv, dg, dbeta, ds0) and the intermediates dict (adds dSn = dS_{c+1} per chunk and dVn)."""

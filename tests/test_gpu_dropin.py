@@ -122,16 +122,27 @@ def test_config_bf16_fwd_bwd(cfg, recompute):
         assert ran == ({"fwd s4": 1, "bwd pair s2": 1} if recompute else {"fwd s4": 1, "bwd reverse s4": 1}), ran
 
 
+@pytest.mark.parametrize("split", ["auto", 1])
 @pytest.mark.parametrize("Hv", [16, 32])
-def test_config3_long_prefill_forward(Hv):
-    """Config 3: one row of 32,768 tokens (512 sequential chunks), bf16, forward only, the final state returned."""
-    _say(f"case config3 Hv={Hv}")
+def test_config3_long_prefill_forward(Hv, split):
+    """Config 3: one row of 32,768 tokens (512 sequential chunks), bf16, forward only, the final state returned; as
+    segments side by side (the default: 4 at Hv = 16, 2 at Hv = 32) and as one chain (SEQUENCE_SPLIT = 1)."""
+    _say(f"case config3 Hv={Hv} split={split}")
     inp = gdr.config_inputs(3, Hv=Hv)
     names = ("query", "key", "value", "g", "beta")
-    with torch.no_grad():
-        o, sT = chunk_gated_delta_rule(*(inp[n].to(DEV) for n in names), output_final_state=True,
-                                       use_qk_l2norm_in_kernel=True)
-        torch.cuda.synchronize()
+    old = op.SEQUENCE_SPLIT
+    before = dict(op.CALLS)
+    try:
+        op.SEQUENCE_SPLIT = split
+        with torch.no_grad():
+            o, sT = chunk_gated_delta_rule(*(inp[n].to(DEV) for n in names), output_final_state=True,
+                                           use_qk_l2norm_in_kernel=True)
+            torch.cuda.synchronize()
+    finally:
+        op.SEQUENCE_SPLIT = old
+    ran = [k_ for k_, v_ in op.CALLS.items() if v_ != before.get(k_, 0)]
+    want = f"fwd seg{64 // Hv} " if split == "auto" else "fwd s"
+    assert len(ran) == 1 and ran[0].startswith(want), ran
     q, k = gdr.prologue(inp["query"].double(), inp["key"].double())
     ro, rsT = gdr.chunked_forward_segments(q, k, inp["value"].double(), inp["g"].double(), inp["beta"].double(),
                                            torch.zeros(1, Hv, 128, 128, dtype=torch.float64))

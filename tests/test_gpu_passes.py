@@ -98,3 +98,82 @@ def test_one_call_forward_equals_the_two_passes(shape, dtype, split):
         op.VALUE_SPLIT = old
     torch.cuda.synchronize()
     assert torch.equal(o, ro) and torch.equal(sT, rsT)
+
+
+# ---- sequence parallelism: segment maps, their composition, the segmented forward -------------------------------------
+@pytest.mark.parametrize("dtype,T,P", [(torch.float32, 64 * 13 + 5, 3), (torch.bfloat16, 64 * 9, 2),
+                                       (torch.float32, 64 * 8, 8)])
+def test_segment_maps_and_scan(dtype, T, P):
+    """macai_gdr_state_map on a row split into P segments of whole chunks (the last one ragged) against the oracle's
+    segment_map of each segment, and macai_gdr_state_scan's starting states against the oracle's chunk states at the
+    segment boundaries.  float32 at the harness bar 2e-4 (relative to the largest entry of each map), bf16 at 1e-2."""
+    from macai.gated_delta import _native as N
+    from macai.gated_delta import op
+    print(f"case segment maps {dtype} T={T} P={P}", flush=True)
+    H, DK, DV = 2, 128, 128
+    q, k, v, g, b, s0 = gdr.harness_inputs(1, T, H, DK, DV, seed=5)
+    g = g * 0.02          # weak decay: A stays O(1) over a segment (under the harness's g it underflows float32)
+    rd = (lambda x: x.to(torch.bfloat16).double()) if dtype == torch.bfloat16 else (lambda x: x.float().double())
+    q, k, v = rd(q), rd(k), rd(v)
+    g, b, s0 = g.float().double(), b.float().double(), s0.float().double()
+    _, _, Pr = gdr.chunked_forward(q, k, v, g, b, s0)
+    dev, f32 = "cuda", torch.float32
+    x = [t.to(dev, dtype).contiguous() for t in (q, k, v)] + [t.to(dev, f32).contiguous() for t in (g, b, s0)]
+    NT = -(-T // 64)
+    es = 2 if dtype == torch.bfloat16 else 4
+    e = lambda *s, d=dtype: torch.empty(*s, device=dev, dtype=d)
+    W, U, Ke, GL, Qg, M = e(1, H, NT, 64, DK), e(1, H, NT, 64, DV, d=f32), e(1, H, NT, 64, DK), e(1, H, NT, d=f32), \
+        e(1, H, NT, 64, DK), e(1, H, NT, 64, 64)
+    code, st, Pt = N.dtype_code(dtype), N.stream_of(x[0]), N.ptr
+    N.call("macai_gdr_prep", *map(Pt, x[:5]), Pt(W), Pt(U), Pt(Ke), Pt(GL), Pt(Qg), Pt(M), None, 1, T, H, H, DK, DV,
+           code, 0, 1.0, None, 0, st)
+    table, NT2 = op._segment_table(T, P, dev)
+    assert NT2 == NT
+    maps = e(P, H, DK, DK + DV, d=f32)
+    N.call("macai_gdr_state_map", Pt(W), Pt(U), Pt(Ke), Pt(GL), Pt(maps), P, T, H, DK, DV, code, 0, Pt(table), NT, st)
+    starts = e(P, H, DK, DV, d=f32)
+    N.call("macai_gdr_state_scan", Pt(maps), Pt(x[5]), Pt(starts), 1, P, H, DK, DV, st)
+    torch.cuda.synchronize()
+    maps, starts = maps.cpu(), starts.cpu()
+    c0 = table.cpu().tolist()[2 * NT:]
+    bar = 1e-2 if dtype == torch.bfloat16 else 2e-4
+    errs = {}
+    for s in range(P):
+        t0, t1 = 64 * c0[s], min(64 * c0[s + 1], T)
+        A, Bm = gdr.segment_map(q[:, t0:t1], k[:, t0:t1], v[:, t0:t1], g[:, t0:t1], b[:, t0:t1])
+        errs[f"A{s}"] = gdr.rel(maps[s:s + 1, :, :, :DK], A)
+        errs[f"B{s}"] = gdr.rel(maps[s:s + 1, :, :, DK:], Bm)
+        errs[f"start{s}"] = gdr.rel(starts[s:s + 1], Pr["Sc"][:, :, c0[s]])
+    print({n: f"{v_:.1e}" for n, v_ in errs.items()}, flush=True)
+    bad = {n: v_ for n, v_ in errs.items() if not v_ < bar}
+    assert not bad, bad
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("P", [2, 4])
+def test_segmented_forward(dtype, P):
+    """A single row's forward without gradients split into P segments (op.SEQUENCE_SPLIT, taken when nothing is saved
+    for a backward): output and final state against the float64 oracle, float32 at 2e-4 and bf16 at 1e-2; the passes
+    run are the segmented ones; with a starting state and a ragged length."""
+    from macai.gated_delta import chunk_gated_delta_rule, op
+    print(f"case segmented forward {dtype} P={P}", flush=True)
+    inp = gdr.make_inputs(1, 64 * 40 + 17, 4, 4, 128, 128, dtype, s0=True, seed=12)
+    names = ("query", "key", "value", "g", "beta")
+    old = op.SEQUENCE_SPLIT
+    before = dict(op.CALLS)
+    try:
+        op.SEQUENCE_SPLIT = P
+        with torch.no_grad():
+            o, sT = chunk_gated_delta_rule(*(inp[n].to("cuda") for n in names),
+                                           initial_state=inp["initial_state"].to("cuda"), output_final_state=True,
+                                           use_qk_l2norm_in_kernel=True)
+            torch.cuda.synchronize()
+    finally:
+        op.SEQUENCE_SPLIT = old
+    ran = [k_ for k_, v_ in op.CALLS.items() if v_ != before.get(k_, 0)]
+    assert len(ran) == 1 and ran[0].startswith(f"fwd seg{P} "), ran
+    ro, rsT, _ = gdr.dropin_f64(*(inp[n] for n in names + ("initial_state",)))
+    bar = 1e-2 if dtype == torch.bfloat16 else 2e-4
+    errs = {"o": gdr.rel(o.cpu(), ro), "sT": gdr.rel(sT.cpu(), rsT)}
+    print(errs, flush=True)
+    assert all(v_ < bar for v_ in errs.values()), errs

@@ -214,3 +214,24 @@ def test_segmented_forward_is_the_same_computation():
     o, sT, _ = gdr.chunked_forward(*xs, 64)
     o2, sT2 = gdr.chunked_forward_segments(*xs, 64, seg=128)
     assert gdr.rel(o2, o) < 1e-14 and gdr.rel(sT2, sT) < 1e-14
+
+
+def test_segment_map_composes_the_state_pass():
+    """segment_map: A S_0 + B is the final state of chunked_forward from any S_0 (< 1e-12), composing two halves' maps
+    in order gives the whole row's, and the composition in the wrong order does not (a planted mistake)."""
+    gen = torch.Generator().manual_seed(21)
+    B, T, H, DK, DV = 1, 200, 2, 32, 16
+    q = gdr.l2norm(torch.randn(B, T, H, DK, generator=gen, dtype=F64)) * DK ** -0.5
+    k = gdr.l2norm(torch.randn(B, T, H, DK, generator=gen, dtype=F64))
+    v = torch.randn(B, T, H, DV, generator=gen, dtype=F64)
+    g = -torch.rand(B, T, H, generator=gen, dtype=F64) * 0.1
+    b = torch.rand(B, T, H, generator=gen, dtype=F64)
+    s0 = torch.randn(B, H, DK, DV, generator=gen, dtype=F64)
+    A, Bm = gdr.segment_map(q, k, v, g, b)
+    _, sT, _ = gdr.chunked_forward(q, k, v, g, b, s0)
+    assert (A @ s0 + Bm - sT).abs().max() < 1e-12
+    h = 128                                  # two segments of whole chunks
+    A1, B1 = gdr.segment_map(q[:, :h], k[:, :h], v[:, :h], g[:, :h], b[:, :h])
+    A2, B2 = gdr.segment_map(q[:, h:], k[:, h:], v[:, h:], g[:, h:], b[:, h:])
+    assert (A2 @ (A1 @ s0 + B1) + B2 - sT).abs().max() < 1e-12
+    assert (A1 @ (A2 @ s0 + B2) + B1 - sT).abs().max() > 1e-3
