@@ -157,6 +157,14 @@ def test_transformers_restatement_matches_installed_transformers(T, s0, in_dtype
     mo, ms = gdr.torch_chunk_gated_delta_rule(*args, cast_first=False, **kw)
     assert mo.dtype == ro.dtype == in_dtype
     assert gdr.rel(mo, ro) < 1e-6 and gdr.rel(ms, rs) < 1e-6
+    if in_dtype == torch.float32:
+        # float32 inputs: the two cast orders are one computation (the cast is the identity), bit for bit; the 5.22.1
+        # form the GPU tests' 2x anchor uses (cast first, solve_triangular inverse) sits within float32 error of the
+        # installed row-loop function
+        co, cs = gdr.torch_chunk_gated_delta_rule(*args, cast_first=True, **kw)
+        assert torch.equal(co, mo) and torch.equal(cs, ms)
+        so, ss = gdr.torch_chunk_gated_delta_rule(*args, cast_first=True, inverse="solve", **kw)
+        assert gdr.rel(so, ro) < 1e-5 and gdr.rel(ss, rs) < 1e-5
 
 
 def test_transformers_algorithm_is_the_recurrence():
@@ -192,8 +200,8 @@ def test_dropin_oracle_against_golden_fixture():
 
 
 def test_planted_mistakes_are_caught():
-    """A dropped term or a transposed operand in the oracle's backward fails the recurrence check (the tests above
-    would catch such a slip): here planted into copies of the equations on the CPU."""
+    """A dropped term, a transposed operand or a wrong sign in the oracle's backward fails the recurrence check (the
+    tests above would catch such a slip): here planted into copies of the equations on the CPU."""
     q, k, v, g, b, s0 = gdr.harness_inputs(1, 21, 1, 6, 5, seed=1)
     gen = torch.Generator().manual_seed(5)
     do = torch.randn(1, 21, 1, 5, generator=gen, dtype=F64)
@@ -204,6 +212,9 @@ def test_planted_mistakes_are_caught():
     mine, _ = gdr.chunked_backward(q, k, v, g, b, s0, do, dsT, 8, bad)
     assert max(gdr.rel(a, r) for a, r in zip(mine, grads)) > 1e-3
     bad = dict(P, e=torch.ones_like(P["e"]))             # dropped decay term
+    mine, _ = gdr.chunked_backward(q, k, v, g, b, s0, do, dsT, 8, bad)
+    assert max(gdr.rel(a, r) for a, r in zip(mine, grads)) > 1e-3
+    bad = dict(P, W=-P["W"])                             # wrong sign (of W's term in B2 and of dW)
     mine, _ = gdr.chunked_backward(q, k, v, g, b, s0, do, dsT, 8, bad)
     assert max(gdr.rel(a, r) for a, r in zip(mine, grads)) > 1e-3
 
