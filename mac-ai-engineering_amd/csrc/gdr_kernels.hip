@@ -2450,37 +2450,6 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   }
   lds_barrier();
 
-  // ---- F: dbeta and dg (wave 0, lane = chunk row), fixed-order sums of the partials
-  if (w == 0) {
-    const int r = l, t = t0 + r;
-    auto sum = [&](int pi, int np) {
-      float x = part[pi][0][r];
-      for (int i = 1; i < np; ++i) x += part[pi][i][r];
-      return x;
-    };
-    const float kx = sum(P_KX, NBD), qd = sum(P_QD, NBD), E = sum(P_E, NBD), r1 = sum(P_R1, 4), r2 = sum(P_R2, 4),
-                vy = sum(P_VY, NBV);
-    const float gmr = cs.gam[r], bt = cs.beta[r];
-    const float db = fmaf(gmr, kx, vy) + r2;
-    float dG = qd + bt * gmr * kx + (r1 - (colp[0][0][r] + colp[0][1][r])) + (bt * r2 - (colp[1][0][r] + colp[1][1][r]));
-    if (r == C - 1) {
-      float ss = partS[0];
-      for (int i = 1; i < NBD; ++i) ss += partS[i];
-      dG += cs.gam[C - 1] * ss;
-    }
-    // dg_t = sum_{s >= t} dG_s + sum_{r < t} E_r; the exclusive prefix by a shift, not incl - E: E on the last valid
-    // row is O(1) while the earlier ones carry exp(G_last - G_r) and can be ~1e-9 of it
-    const float rev = __shfl(dG, C - 1 - r, 64);
-    const float suf = __shfl(wave_incl_scan(rev), C - 1 - r, 64);
-    float Esh = __shfl_up(E, 1, 64);
-    if (r == 0) Esh = 0.f;
-    const float pre = wave_incl_scan(Esh);
-    if (t < T) {
-      a.dg[s_base + (size_t)t * H] = suf + pre;
-      a.dbeta[s_base + (size_t)t * H] = db;
-    }
-  }
-
   // ---- G: the prologue's backward; dq and dk staged over q's and k's tiles
   f4 gq[4], gk[4];
   if (w < NBD) {
@@ -2517,20 +2486,54 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
     }
   }
   lds_barrier();
-  // whole rows out: 16 bytes per lane
-  {
-    constexpr int UK = DK / 8, UV = DV / 8;
+  // whole rows out, 16 bytes a lane, by waves 1..7 while wave 0 forms dbeta and dg (F): the partials F reads are not
+  // written after E, so F runs off the path of the workgroup's last barrier
+  if (w != 0) {
+    constexpr int UK = DK / 8, UV = DV / 8, NTH = 64 * (NW - 1);
+    const int tid = threadIdx.x - 64;
     MT* dq = (MT*)a.dq + dqk_base + (size_t)t0 * dqk_pitch;
     MT* dk = (MT*)a.dk + dqk_base + (size_t)t0 * dqk_pitch;
     MT* dv = (MT*)a.dv + v_base + (size_t)t0 * v_pitch;
-    for (int i = threadIdx.x; i < nrows * UK; i += blockDim.x) {
+    for (int i = tid; i < nrows * UK; i += NTH) {
       const int row = i / UK, u = i - row * UK;
       *reinterpret_cast<bf16x8*>(dq + row * dqk_pitch + 8 * u) = *reinterpret_cast<const bf16x8*>(tq + row * KP + 8 * u);
       *reinterpret_cast<bf16x8*>(dk + row * dqk_pitch + 8 * u) = *reinterpret_cast<const bf16x8*>(tk + row * KP + 8 * u);
     }
-    for (int i = threadIdx.x; i < nrows * UV; i += blockDim.x) {
+    for (int i = tid; i < nrows * UV; i += NTH) {
       const int row = i / UV, u = i - row * UV;
       *reinterpret_cast<bf16x8*>(dv + row * v_pitch + 8 * u) = *reinterpret_cast<const bf16x8*>(tVn + row * VP + 8 * u);
+    }
+    return;
+  }
+
+  // ---- F: dbeta and dg (wave 0, lane = chunk row), fixed-order sums of the partials
+  if (w == 0) {
+    const int r = l, t = t0 + r;
+    auto sum = [&](int pi, int np) {
+      float x = part[pi][0][r];
+      for (int i = 1; i < np; ++i) x += part[pi][i][r];
+      return x;
+    };
+    const float kx = sum(P_KX, NBD), qd = sum(P_QD, NBD), E = sum(P_E, NBD), r1 = sum(P_R1, 4), r2 = sum(P_R2, 4),
+                vy = sum(P_VY, NBV);
+    const float gmr = cs.gam[r], bt = cs.beta[r];
+    const float db = fmaf(gmr, kx, vy) + r2;
+    float dG = qd + bt * gmr * kx + (r1 - (colp[0][0][r] + colp[0][1][r])) + (bt * r2 - (colp[1][0][r] + colp[1][1][r]));
+    if (r == C - 1) {
+      float ss = partS[0];
+      for (int i = 1; i < NBD; ++i) ss += partS[i];
+      dG += cs.gam[C - 1] * ss;
+    }
+    // dg_t = sum_{s >= t} dG_s + sum_{r < t} E_r; the exclusive prefix by a shift, not incl - E: E on the last valid
+    // row is O(1) while the earlier ones carry exp(G_last - G_r) and can be ~1e-9 of it
+    const float rev = __shfl(dG, C - 1 - r, 64);
+    const float suf = __shfl(wave_incl_scan(rev), C - 1 - r, 64);
+    float Esh = __shfl_up(E, 1, 64);
+    if (r == 0) Esh = 0.f;
+    const float pre = wave_incl_scan(Esh);
+    if (t < T) {
+      a.dg[s_base + (size_t)t * H] = suf + pre;
+      a.dbeta[s_base + (size_t)t * H] = db;
     }
   }
 }
