@@ -328,7 +328,7 @@ def bench_prefill(args):
     op.EVENTS = None
     t = {name: sum(v) / len(v) for name, v in t.items()}
     B, T, H, DK, DV = c["B"], c["T"], c["Hv"], c["DK"], c["DV"]
-    segs = op.segments_for(B, T, H)
+    segs = op.segments_for(B, T, H, DV)
     cost = kernel_costs(B, T, H, DK, DV, Hk=c["Hk"], segs=segs)
     kernels = {n: {"us": round(x * 1e6, 2), "GB/s": round(cost[n]["bytes"] / x / 1e9, 1),
                    "hbm_frac": round(cost[n]["bytes"] / x / HBM_PEAK, 4)} for n, x in t.items()}
@@ -540,6 +540,9 @@ def main():
                          "lengths with the same total")
     ap.add_argument("--producers", action="store_true",
                     help="time the rule's producers (the convolution path and the gates) instead of the rule")
+    ap.add_argument("--f32-compute", action="store_true",
+                    help="run the bf16 inputs on the float32 kernels (op.BF16_OPERANDS = False, the reference's own "
+                         "precision) and report that step's time only")
     ap.add_argument("--no-alone", action="store_true",
                     help="skip timing each pass alone, so a kernel trace of the run holds the step's launches only")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -600,6 +603,23 @@ def main():
         return torch.autograd.grad(o, leaves, do)
 
     from macai.gated_delta import op
+    if args.f32_compute:
+        old = op.BF16_OPERANDS
+        try:
+            op.BF16_OPERANDS = False
+            sec, in_step = _time_step(step, args)
+        finally:
+            op.BF16_OPERANDS = old
+        line = {"metric": METRIC + ", bf16 inputs on the float32 kernels", "value": round(c["B"] * c["T"] / sec, 1),
+                "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                "ms_per_step": round(sec * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+                "dtype": "f32", "data": "synthetic",
+                "config": {"workload": f"gated-delta drop-in fwd+bwd, BASELINE config {args.config}, "
+                                       "op.BF16_OPERANDS = False", "B": c["B"], "T": c["T"], "Hv": c["Hv"],
+                           "DK": c["DK"], "DV": c["DV"], "recompute_prep_in_backward": op.RECOMPUTE_STATES},
+                "kernels": {n: {"us": round(t * 1e6, 2)} for n, t in in_step.items()}}
+        print(json.dumps(line), flush=True)
+        return
     default_mode = op.RECOMPUTE_STATES
     modes = [not args.stored, args.stored]           # headline first, then the other mode as a second field
     runs = []

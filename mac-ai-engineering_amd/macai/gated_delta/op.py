@@ -20,6 +20,11 @@ CHUNK = 64   # chunk length of the kernels; the drop-in's chunk_size is accepted
 # The widest key head the bf16 kernels take; wider ones (256, the reference's widest tested, tests/test_harness.py:214-230)
 # run the float32 kernels, with 2-byte inputs upcast exactly and the results cast back.
 BF16_MAX_DK = 128
+# BF16_OPERANDS: bfloat16 inputs run on bf16 MFMA operands with fp32 accumulation and an fp32 state (True, the
+# default: the fast path, outputs and gradients within ~5e-3 of float64).  False upcasts them exactly and runs the
+# float32 kernels, as the reference computes every input (op.py:276-285, 297): dg and dbeta then come within ~1e-5 of
+# float64 (the bf16 operands' rounding, not the fp32 state, sets the default's error), at the float32 kernels' speed.
+BF16_OPERANDS = True
 # VALUE_SPLIT: workgroups a head-row's value columns are split over in the state passes (each owns DV / VALUE_SPLIT
 # columns as DV / 16 / VALUE_SPLIT waves of 16 columns): "auto" (split_for) or 1, 2, 4, 8, ...
 VALUE_SPLIT = "auto"
@@ -48,8 +53,12 @@ RECOMPUTE_STATES = True
 # the row's chunks; with few head-rows (one long prefill) it fills few CUs and its length is the row's.  The pass is
 # affine in its starting state, so the row splits into segments: each segment's map [A | B] (macai_gdr_state_map,
 # from the identity and from zero), their composition in order (macai_gdr_state_scan) for each segment's starting
-# state, and the output pass over all segments at once.  "auto": for a single row (B = 1, no cu_seqlens), the largest
-# power of two P with P x H <= 64 head-rows and at least 32 chunks a segment (P = 1 otherwise); an int forces P.
+# state, and the output pass over all segments at once.  The maps cost a second chain over DK + DV columns, so the
+# split pays only where the plain pass leaves most CUs idle.  "auto": for a single row (B = 1, no cu_seqlens) whose
+# plain pass has at most 128 workgroups of 16 columns (H x DV / 16 <= 128), the largest power of two P with P x H <= 64
+# head-rows and at least 32 chunks a segment (P = 1 otherwise); an int forces P.  Measured at T = 32,768, D = 128:
+# H = 16 splits in 4 (state passes 435 against 566 us); at H = 32 the plain pass already fills the chip (256
+# workgroups) and a split in 2 took 810 against 637 us.
 SEQUENCE_SPLIT = "auto"
 
 
@@ -237,14 +246,16 @@ def _prep(q, k, v, g, beta, l2norm: bool, q_scale: float, r, stream, pack=None, 
             r["A"], B, T, H, Hk, DK, DV, N.dtype_code(q.dtype), int(l2norm), q_scale, *_pack_args(pack), stream)
 
 
-def segments_for(B: int, T: int, H: int, pack=None, save: bool = False) -> int:
-    """SEQUENCE_SPLIT's number of segments for a forward of B rows of T tokens over H value heads (1: no split).  A
-    forward that saves for a backward never splits: the training step keeps the bits of the unsplit pass."""
+def segments_for(B: int, T: int, H: int, DV: int, pack=None, save: bool = False) -> int:
+    """SEQUENCE_SPLIT's number of segments for a forward of B rows of T tokens over H value heads of DV columns (1: no
+    split).  A forward that saves for a backward never splits: the training step keeps the bits of the unsplit pass."""
     if save or pack is not None or B != 1:
         return 1
     NT = math.ceil(T / CHUNK)
     if SEQUENCE_SPLIT != "auto":
         return max(1, min(int(SEQUENCE_SPLIT), NT))
+    if H * (DV // 16) > 128:
+        return 1
     P = 1
     while 2 * P * H <= 64 and NT // (2 * P) >= 32:
         P *= 2
@@ -301,7 +312,7 @@ def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, 
     backward -- prep's operands with A and the chunk states Sc, Vn, else None).  A single long row whose forward saves
     nothing for a backward may run as segments side by side (SEQUENCE_SPLIT)."""
     B, T, H, Hk, DK, DV, NT = _dims(q, v, pack)
-    nseg = segments_for(B, T, H, pack, save or keep)
+    nseg = segments_for(B, T, H, DV, pack, save or keep)
     if nseg > 1:
         return _forward_segments(q, k, v, g, beta, s0, l2norm, q_scale, want_sT, nseg)
     Bc = q.shape[0]
@@ -394,7 +405,7 @@ class GatedDeltaRule(torch.autograd.Function):
     def forward(ctx, q, k, v, g, beta, s0, save: bool):
         _check(q, k, v, g, beta, s0)
         ctx.io_dtype = q.dtype             # o and the q, k, v gradients come back in it
-        if q.shape[-1] > BF16_MAX_DK and q.dtype != torch.float32:
+        if q.dtype != torch.float32 and (q.shape[-1] > BF16_MAX_DK or not BF16_OPERANDS):
             q, k, v = q.float(), k.float(), v.float()
         q, k, v, g, beta, s0 = (t.contiguous() for t in (q, k, v, g, beta, s0))
         keep = save and not RECOMPUTE_STATES
@@ -461,15 +472,18 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size: int = 64, ini
     kernels. Returns the output [B, T, H, DV] in the query's dtype and the final state (float32) when
     output_final_state, else None.  chunk_size is accepted and unused (the kernels use 64-token chunks).  bfloat16
     inputs run on bf16 MFMA with fp32 accumulation and an fp32 state; float32 inputs on fp32 MFMA; float16 inputs,
-    and bfloat16 ones with key heads wider than 128 (up to 256), are upcast exactly and computed as float32, the
+    and bfloat16 ones with key heads wider than 128 (up to 256) or with BF16_OPERANDS off, are upcast exactly and
+    computed as float32, the
     output cast back (the reference runs every input this way: its prologue and `value.float()` run the rule in
     float32, op.py:276-285, 297).  With use_qk_l2norm_in_kernel=False
     the query is only scaled by DK^-1/2 (op.py:279-283), inside the kernels."""
     cu = kwargs.get("cu_seqlens")
     pack = None if cu is None else _pack(cu, query.shape[1], query.device)
     dtype = query.dtype
-    # bf16 runs on bf16 MFMA up to key width 128; float16, float32 and wider keys on the float32 kernels
-    cdt = torch.bfloat16 if dtype == torch.bfloat16 and query.shape[-1] <= BF16_MAX_DK else torch.float32
+    # bf16 runs on bf16 MFMA up to key width 128 (unless BF16_OPERANDS is off); float16, float32 and wider keys on
+    # the float32 kernels
+    bf16 = dtype == torch.bfloat16 and query.shape[-1] <= BF16_MAX_DK and BF16_OPERANDS
+    cdt = torch.bfloat16 if bf16 else torch.float32
     q, k, v = _as(query, cdt), _as(key, cdt), _as(value, cdt)
     gf, bf = _as(g, torch.float32), _as(beta, torch.float32)
     s0 = None if initial_state is None else _as(initial_state, torch.float32)

@@ -175,9 +175,9 @@ def test_cpu_tensors_refused_loudly():
 
 
 def test_split_rule():
-    """VALUE_SPLIT 'auto': the smallest valid split (1, 2, 4 or 8 waves of 16 columns per workgroup; 8 only when
-    nothing else is valid) giving >= 256 workgroups, else the largest; an int setting rounds down to a valid split
-    (reference op.split_for semantics, test_chunking.py:176-199)."""
+    """VALUE_SPLIT 'auto': the largest valid split (1, 2, 4 or 8 waves of 16 columns per workgroup; 8 only when
+    nothing else is valid) whose workgroups fit the pass's share of the 256 CUs at once, else the smallest; an int
+    setting rounds down to a valid split (reference op.split_for semantics, test_chunking.py:176-199)."""
     assert op.valid_splits(128) == [1, 2, 4, 8] and op.valid_splits(96) == [3, 6] and op.valid_splits(32) == [1, 2]
     assert op.split_for(64, 1024, 128) == 4
     assert op.split_for(16, 32768, 128) == 8
@@ -199,6 +199,27 @@ def test_split_rule():
         assert op.split_for(64, 1024, 96) == 3
     finally:
         op.VALUE_SPLIT = old
+
+
+def test_segment_rule():
+    """SEQUENCE_SPLIT 'auto': only a single unpacked row whose forward saves nothing, and only when its plain pass
+    leaves CUs idle (H x DV / 16 <= 128 workgroups); then the largest power of two with P x H <= 64 and >= 32 chunks
+    a segment.  An int forces P (capped at the chunk count)."""
+    assert op.segments_for(1, 32768, 16, 128) == 4
+    assert op.segments_for(1, 32768, 32, 128) == 1       # 256 workgroups already: the maps would only add a chain
+    assert op.segments_for(1, 32768, 8, 128) == 8
+    assert op.segments_for(1, 4096, 16, 128) == 2        # 64 chunks: two segments of 32
+    assert op.segments_for(1, 2048, 16, 128) == 1
+    assert op.segments_for(2, 32768, 16, 128) == 1
+    assert op.segments_for(1, 32768, 16, 128, save=True) == 1
+    assert op.segments_for(1, 32768, 16, 128, pack=object()) == 1
+    old = op.SEQUENCE_SPLIT
+    try:
+        op.SEQUENCE_SPLIT = 3
+        assert op.segments_for(1, 32768, 32, 128) == 3
+        assert op.segments_for(1, 100, 32, 128) == 2
+    finally:
+        op.SEQUENCE_SPLIT = old
 
 
 def test_patch_swaps_the_name_and_restores_it():
