@@ -416,13 +416,26 @@ __global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
   float* const sL = reinterpret_cast<float*>(lw);
   MT* const stW = reinterpret_cast<MT*>(lw);        // L is consumed by then
 
-  // ---- 0: tiles in flight, the chunk scalars meanwhile; then the row norms from the tiles
-  GQ::dma(tq, q + (size_t)t0 * qk_pitch, qk_pitch, w, NW, nrows);
-  GQ::dma(tk, k + (size_t)t0 * qk_pitch, qk_pitch, w, NW, nrows);
-  GV::dma(tv, v + (size_t)t0 * v_pitch, v_pitch, w, NW, nrows);
-  if (w == 0) chunk_scalars(cs, a.g, a.beta, s_base, H, t0, T);
-  wait_dma();
-  __syncthreads();
+  // ---- 0: g and beta read, then the q and k tiles copied, then v's, which is read only from phase 4 on: the waves
+  // wait for q and k (a partial wait; copies retire in issue order) and v lands during phases 1a and 1b.  Until then
+  // the barriers order LDS only (a workgroup fence would wait for v's copy).  The row norms come from the tiles.
+  float gv = 0.f, bv = 0.f;
+  if (w == 0) {
+    const size_t o = s_base + (size_t)(t0 + l < T ? t0 + l : T - 1) * H;
+    gv = a.g[o];
+    bv = a.beta[o];
+  }
+  GQ::template dma_exact<NW>(tq, q + (size_t)t0 * qk_pitch, qk_pitch, w, nrows);
+  GQ::template dma_exact<NW>(tk, k + (size_t)t0 * qk_pitch, qk_pitch, w, nrows);
+  __builtin_amdgcn_sched_barrier(0);
+  GV::template dma_exact<NW>(tv, v + (size_t)t0 * v_pitch, v_pitch, w, nrows);
+  __builtin_amdgcn_sched_barrier(0);
+  wait_vmcnt<GV::per_wave(NW)>();          // g, beta, q and k have landed
+  if (w == 0) {
+    asm volatile("" : "+v"(gv), "+v"(bv));  // no arithmetic on g ahead of the copies (it would wait for the load)
+    chunk_scalars_from(cs, t0 + l < T ? gv : 0.f, t0 + l < T ? bv : 0.f, t0, T);
+  }
+  lds_barrier();
   if (a.l2norm) {
     if (w < 4) row_rnorms_lds<DK>(rq, tq, KP, nrows, 4, w);
     else row_rnorms_lds<DK>(rk, tk, KP, nrows, 4, w - 4);
@@ -430,16 +443,15 @@ __global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
     rk[threadIdx.x] = 1.f;
     rq[threadIdx.x] = 1.f;
   }
-  if (nrows < C) {                         // rows past the end: zeros in q, k and v
-    constexpr int UQ = KP / 8, UV = VP / 8;
+  if (nrows < C) {                         // rows past the end: zeros in q and k (v's once it has landed)
+    constexpr int UQ = KP / 8;
     const int nz = C - nrows;
-    for (int i = threadIdx.x; i < nz * (2 * UQ + UV); i += blockDim.x) {
+    for (int i = threadIdx.x; i < nz * 2 * UQ; i += blockDim.x) {
       const int row = nrows + i % nz, u = i / nz;
-      MT* p = u < UQ ? tq + row * KP + 8 * u : u < 2 * UQ ? tk + row * KP + 8 * (u - UQ) : tv + row * VP + 8 * (u - 2 * UQ);
-      *reinterpret_cast<bf16x8*>(p) = bf16x8{};
+      *reinterpret_cast<bf16x8*>(u < UQ ? tq + row * KP + 8 * u : tk + row * KP + 8 * (u - UQ)) = bf16x8{};
     }
   }
-  __syncthreads();
+  lds_barrier();
   if (threadIdx.x < C) {                   // read from phase 3 on, after several barriers
     const int s = threadIdx.x;
     fW[s] = cs.beta[s] * cs.gam[s] * rk[s];
@@ -512,7 +524,14 @@ __global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
       }
     }
   }
+  wait_dma();                              // v's tile has landed (this wave's part of it)
   __syncthreads();
+  if (nrows < C) {                         // v's rows past the end: zeros (read in phase 4, after several barriers)
+    constexpr int UV = VP / 8;
+    const int nz = C - nrows;
+    for (int i = threadIdx.x; i < nz * UV; i += blockDim.x)
+      *reinterpret_cast<bf16x8*>(tv + (nrows + i % nz) * VP + 8 * (i / nz)) = bf16x8{};
+  }
   // ---- 1c: M out; the diagonal 16 x 16 blocks of A = (I + L)^-1 by forward substitution (wave 0, lane = (block l / 16,
   // column l % 16), column form: the same fmaf sequence per element as the row form), zeros above the diagonal blocks
   {
