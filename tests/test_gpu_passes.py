@@ -101,16 +101,18 @@ def test_one_call_forward_equals_the_two_passes(shape, dtype, split):
 
 
 # ---- sequence parallelism: segment maps, their composition, the segmented forward -------------------------------------
-@pytest.mark.parametrize("dtype,T,P", [(torch.float32, 64 * 13 + 5, 3), (torch.bfloat16, 64 * 9, 2),
-                                       (torch.float32, 64 * 8, 8)])
-def test_segment_maps_and_scan(dtype, T, P):
+@pytest.mark.parametrize("dtype,T,P,DK,DV", [(torch.float32, 64 * 13 + 5, 3, 128, 128),
+                                             (torch.bfloat16, 64 * 9, 2, 128, 128), (torch.float32, 64 * 8, 8, 128, 128),
+                                             (torch.float32, 64 * 6 + 9, 3, 256, 128), (torch.bfloat16, 64 * 7, 2, 64, 64)])
+def test_segment_maps_and_scan(dtype, T, P, DK, DV):
     """macai_gdr_state_map on a row split into P segments of whole chunks (the last one ragged) against the oracle's
     segment_map of each segment, and macai_gdr_state_scan's starting states against the oracle's chunk states at the
-    segment boundaries.  float32 at the harness bar 2e-4 (relative to the largest entry of each map), bf16 at 1e-2."""
+    segment boundaries.  float32 at the harness bar 2e-4 (relative to the largest entry of each map), bf16 at 1e-2.
+    Key heads of 256 (float32) take the map pass's direct form (the chunk's tiles read from memory, not LDS)."""
     from macai.gated_delta import _native as N
     from macai.gated_delta import op
-    print(f"case segment maps {dtype} T={T} P={P}", flush=True)
-    H, DK, DV = 2, 128, 128
+    print(f"case segment maps {dtype} T={T} P={P} DK={DK} DV={DV}", flush=True)
+    H = 2
     q, k, v, g, b, s0 = gdr.harness_inputs(1, T, H, DK, DV, seed=5)
     g = g * 0.02          # weak decay: A stays O(1) over a segment (under the harness's g it underflows float32)
     rd = (lambda x: x.to(torch.bfloat16).double()) if dtype == torch.bfloat16 else (lambda x: x.float().double())
@@ -149,15 +151,19 @@ def test_segment_maps_and_scan(dtype, T, P):
     assert not bad, bad
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("P", [2, 4])
-def test_segmented_forward(dtype, P):
+@pytest.mark.parametrize("dtype,P,DK", [(torch.float32, 2, 128), (torch.float32, 4, 128), (torch.bfloat16, 2, 128),
+                                        (torch.bfloat16, 4, 128), (torch.bfloat16, 2, 256)])
+def test_segmented_forward(dtype, P, DK):
     """A single row's forward without gradients split into P segments (op.SEQUENCE_SPLIT, taken when nothing is saved
     for a backward): output and final state against the float64 oracle, float32 at 2e-4 and bf16 at 1e-2; the passes
-    run are the segmented ones; with a starting state and a ragged length."""
+    run are the segmented ones; with a starting state and a ragged length; key heads of 256 (bf16 inputs upcast to the
+    float32 kernels).  The decay is weak (g scaled by 0.02), so each segment's output depends on the state carried
+    into it: under the generator's own decay a state is forgotten within a chunk or two and a wrong starting state
+    would go unseen."""
     from macai.gated_delta import chunk_gated_delta_rule, op
-    print(f"case segmented forward {dtype} P={P}", flush=True)
-    inp = gdr.make_inputs(1, 64 * 40 + 17, 4, 4, 128, 128, dtype, s0=True, seed=12)
+    print(f"case segmented forward {dtype} P={P} DK={DK}", flush=True)
+    inp = gdr.make_inputs(1, 64 * 40 + 17, 4, 4, DK, 128, dtype, s0=True, seed=12)
+    inp["g"] = inp["g"] * 0.02
     names = ("query", "key", "value", "g", "beta")
     old = op.SEQUENCE_SPLIT
     before = dict(op.CALLS)

@@ -83,6 +83,23 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert pair(*([p] * 6), None, p, None, *([p] * 5), split=3) == N.EINVAL
     assert L.macai_gdr_decode(p, p, p, p, p, p, p, p, 1, 1, 1, 256, 128, 1, 1, 1.0, None) == N.EUNSUP
     assert L.macai_gdr_decode(p, p, p, p, p, p, p, p, 1, 4, 3, 128, 128, 1, 1, 1.0, None) == N.EINVAL
+    # the segment maps and their scan: null or misaligned buffers, a split giving no valid wave count over DK + DV
+    # columns, widths and counts out of range
+    sm = lambda *ptrs, split=0, DK=128, DV=128, dtype=1: L.macai_gdr_state_map(*ptrs, 2, 640, 2, DK, DV, dtype, split,
+                                                                               None, 0, None)
+    assert sm(p, p, p, p, None) == N.EINVAL and b"null" in L.macai_gdr_last_error()
+    assert sm(p, p, p + 4, p, p) == N.EINVAL and b"aligned" in L.macai_gdr_last_error()
+    assert sm(p, p, p, p, p, split=3) == N.EINVAL and b"split" in L.macai_gdr_last_error()
+    assert sm(p, p, p, p, p, DK=96) == N.EUNSUP
+    assert sm(p, p, p, p, p, DK=256) == N.EUNSUP                       # wide keys take float32 operands
+    sc = lambda maps, s0, starts, rows=1, nseg=4, DK=128, DV=128: L.macai_gdr_state_scan(maps, s0, starts, rows, nseg,
+                                                                                          2, DK, DV, None)
+    assert sc(p, None, None) == N.EINVAL and b"null" in L.macai_gdr_last_error()
+    assert sc(p, p + 8, p) == N.EINVAL and b"aligned" in L.macai_gdr_last_error()
+    assert sc(p, None, p, nseg=0) == N.EINVAL
+    assert sc(p, None, p, rows=70000) == N.EINVAL
+    assert sc(p, None, p, DK=96) == N.EUNSUP
+    assert sc(p, None, p, DV=24) == N.EUNSUP
     gs = lambda x, y, H=4, Hk=2, D=128, dtype=1: L.macai_gdr_group_sum(x, y, 1, 64, H, Hk, D, dtype, None)
     assert gs(p, None) == N.EINVAL and b"null" in L.macai_gdr_last_error()
     assert gs(p, p, Hk=3) == N.EINVAL
