@@ -54,6 +54,7 @@ struct PrepArgs {
   float q_scale;
   int Hk;        // key heads of q, k ([B,T,Hk,DK]); value head h reads key head h / (H / Hk)
   const int* pack;  // packed rows (see chunk_span) or null
+  int stagger;   // prep8: the first round's workgroups (two a CU) start staggered
 };
 
 struct StateFwdArgs {
@@ -399,6 +400,14 @@ __global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
   __shared__ ChunkScalars cs;
   __shared__ __attribute__((aligned(16))) float rk[C], rq[C], fW[C], fU[C];
 
+  // The first round of workgroups (a.stagger of them, two a CU) starts in three groups 6.4K cycles apart, as in
+  // chunk_bwd8: their loads then do not all hit the memory system at once, and the offsets carry into the later
+  // rounds.  Measured on the long prefill's 16 rounds: 2-3% off the kernel; neutral at two rounds.
+  if (a.stagger) {
+    const unsigned flat = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    if (flat < (unsigned)a.stagger)
+      for (int i = 0, n = (int)(flat % 3u) * 50; i < n; ++i) __builtin_amdgcn_s_sleep(2);   // 128 cycles each
+  }
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int H = a.H, DV = a.DV, NT = a.NT;
   int t0, T;                               // the chunk's first token; T: its sequence's end (the bound for its rows)
@@ -2788,8 +2797,12 @@ int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, 
   for (const void* p : ps)
     if (!aligned16(p)) return fail(MACAI_GDR_EINVAL, "%s: pointers must be 16-byte aligned", what);
   PrepArgs a{q, k, v, g, beta, W, U, Ke, GL, Qg, M, A, (int)B, (int)T, (int)H, (int)DV, (int)NT,
-             use_l2norm, q_scale, (int)Hk, pack};
+             use_l2norm, q_scale, (int)Hk, pack, 0};
   dim3 grid(a.NT, (unsigned)H, pack ? 1u : (unsigned)B);
+  if (dtype != MACAI_GDR_F32) {            // prep8 (two workgroups a CU): stagger its first round when more follow
+    const int cus = device_cus();
+    if (cus > 0 && (int64_t)grid.x * grid.y * grid.z >= 4 * (int64_t)cus) a.stagger = 2 * cus;
+  }
   hipStream_t st = (hipStream_t)stream;
   if (dtype == MACAI_GDR_F32) {
     DISPATCH_DK_F32(DK, hipLaunchKernelGGL((prep_kernel<float, float, DKC>), grid, dim3(256), 0, st, a));
