@@ -30,7 +30,7 @@ import torch  # noqa: E402
 METRIC = "gated-delta fwd+bwd tokens/s (B4×T1024,H16,d128 bf16); % HBM/MFMA roofline"
 HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
 MFMA_PEAK = {"bf16": 2.5e15, "f32": 157.3e12}
-PUBLISHED = 401.1e3        # reference's own fwd+bwd tokens/s at this config (M3 Max)
+PUBLISHED = 401.1e3        # the reference's own published fwd+bwd tokens/s at this config (M3 Max, recompute mode)
 C = 64
 # HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of `bench.py --no-alone --no-cpu`, each
 # counter scaled by what it reads for a plain device copy of known size (bench.py --copy-mib 256): FETCH_SIZE x 2.000,
