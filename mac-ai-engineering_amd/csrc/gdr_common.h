@@ -84,8 +84,9 @@ template <> __device__ __forceinline__ void store4<bf16>(bf16* p, const f4& x) {
 // Fragment of a k-contiguous ("row-major along k") matrix X: lane takes row `row0 + l % 16`, k-block at k0.  For an A
 // operand X = A ([m][k]); for a B operand X = B^T ([n][k]).  `scale` multiplies the values before rounding to MT.
 template <typename MT, typename ST>
-__device__ __forceinline__ Frag<MT> frag_k(const ST* base, int pitch, int row0, int k0, float scale = 1.0f) {
-  const int l = lane_id(), j = l >> 4;
+__device__ __forceinline__ Frag<MT> frag_k(const ST* base, int pitch, int row0, int k0, float scale = 1.0f,
+                                           int l = lane_id()) {
+  const int j = l >> 4;
   const ST* p = base + (size_t)(row0 + (l & 15)) * pitch + k0 + 4 * j;
   f4 lo = load4(p), hi = load4(p + 16);
   Frag<MT> f;
@@ -98,8 +99,8 @@ __device__ __forceinline__ Frag<MT> frag_k(const ST* base, int pitch, int row0, 
 }
 
 // Specialisation for bf16 LDS/global data feeding bf16 MFMA without a scale: plain 8-byte moves.
-__device__ __forceinline__ Frag<bf16> frag_k_raw(const bf16* base, int pitch, int row0, int k0) {
-  const int l = lane_id(), j = l >> 4;
+__device__ __forceinline__ Frag<bf16> frag_k_raw(const bf16* base, int pitch, int row0, int k0, int l = lane_id()) {
+  const int j = l >> 4;
   const bf16* p = base + (size_t)(row0 + (l & 15)) * pitch + k0 + 4 * j;
   bf16x4 lo = *reinterpret_cast<const bf16x4*>(p), hi = *reinterpret_cast<const bf16x4*>(p + 16);
   Frag<bf16> f;
@@ -135,13 +136,12 @@ __device__ __forceinline__ void frag_split(const Frag<float>& x, Frag<MT>& hi, F
 }
 
 // fp32 fragment of a k-contiguous fp32 matrix (no rounding), for split products
-__device__ __forceinline__ Frag<float> frag_k_f32(const float* base, int pitch, int row0, int k0) {
-  return frag_k<float, float>(base, pitch, row0, k0);
+__device__ __forceinline__ Frag<float> frag_k_f32(const float* base, int pitch, int row0, int k0, int l = lane_id()) {
+  return frag_k<float, float>(base, pitch, row0, k0, 1.0f, l);
 }
 
 // ---- wave-level scans and reductions -------------------------------------------------------------------------------
-__device__ __forceinline__ float wave_incl_scan(float x) {
-  const int l = lane_id();
+__device__ __forceinline__ float wave_incl_scan(float x, int l = lane_id()) {
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
     float y = __shfl_up(x, off, 64);
@@ -168,8 +168,8 @@ __device__ __forceinline__ float group16_sum(float x) {
 // Eight sums over the 16 lanes of a lane group at once, by a butterfly that halves the values at every exchange
 // (partners l ^ 15, l ^ 7, l ^ 2, l ^ 1 -- they span the group): lane l returns the group's sum of v[(l % 16) / 2];
 // lanes l and l ^ 1 hold the same bits.  30 VALU operations where eight group16_sum take 64.
-__device__ __forceinline__ float group16_sum8(const float (&v)[8]) {
-  const int i = lane_id() & 15;
+__device__ __forceinline__ float group16_sum8(const float (&v)[8], int l = lane_id()) {
+  const int i = l & 15;
   const bool b3 = i & 8, b2 = i & 4, b1 = i & 2;
   float u[4], w[2];
 #pragma unroll
@@ -186,11 +186,14 @@ __device__ __forceinline__ float group16_sum8(const float (&v)[8]) {
   const float x = keep + dpp<DPP_XOR2>(send);
   return x + dpp<DPP_XOR1>(x);
 }
-// sum over lanes with equal l % 16 (the 4 lane groups), result in every lane
+// sum over lanes with equal l % 16 (the 4 lane groups), result in every lane: x + x[l ^ 16], then the same with
+// l ^ 32, by gfx950's row swaps (v_permlane16_swap: odd 16-lane rows of one copy with even rows of the other;
+// v_permlane32_swap: the halves), which exchange lanes in registers where a shuffle goes through LDS
 __device__ __forceinline__ float across_groups_sum(float x) {
-  x += __shfl_xor(x, 16, 64);
-  x += __shfl_xor(x, 32, 64);
-  return x;
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
 }
 
 // ---- chunk scalars ------------------------------------------------------------------------------------------------
@@ -207,8 +210,7 @@ struct __attribute__((aligned(16))) ChunkScalars {   // 16-byte aligned: rows ar
   __device__ __forceinline__ float decay(int i, int j) const { return expf((float)(G[i] - G[j])); }
 };
 
-__device__ __forceinline__ double wave_incl_scan_d(double x) {
-  const int l = lane_id();
+__device__ __forceinline__ double wave_incl_scan_d(double x, int l = lane_id()) {
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
     double y = __shfl_up(x, off, 64);
@@ -218,10 +220,10 @@ __device__ __forceinline__ double wave_incl_scan_d(double x) {
 }
 
 // from this lane's g and beta (0 past the sequence end)
-__device__ __forceinline__ void chunk_scalars_from(ChunkScalars& cs, float gv, float bv, int t0, int T) {
-  const int l = lane_id();
+__device__ __forceinline__ void chunk_scalars_from(ChunkScalars& cs, float gv, float bv, int t0, int T,
+                                                   int l = lane_id()) {
   const int last = (T - t0 < C ? T - t0 : C) - 1;
-  double G = wave_incl_scan_d((double)gv);
+  double G = wave_incl_scan_d((double)gv, l);
   const double Gl = __shfl(G, last, 64);
   if (l > last) G = Gl;
   cs.G[l] = G;
@@ -270,8 +272,9 @@ __device__ __forceinline__ void row_rnorms(float* out, const IT* x, size_t row_b
 }
 // The same over a bf16 tile already in LDS (row pitch `pitch` elements; rows < nrows, 0 past them).
 template <int D>
-__device__ __forceinline__ void row_rnorms_lds(float* out, const bf16* tile, int pitch, int nrows, int nwaves, int w) {
-  const int l = lane_id(), part = l & 3;
+__device__ __forceinline__ void row_rnorms_lds(float* out, const bf16* tile, int pitch, int nrows, int nwaves, int w,
+                                               int l = lane_id()) {
+  const int part = l & 3;
   for (int r0 = 16 * w; r0 < C; r0 += 16 * nwaves) {
     const int r = r0 + (l >> 2);
     const bf16* p = tile + r * pitch + 8 * part;   // rows past nrows hold copies of a valid row: masked below

@@ -1991,9 +1991,68 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
 // transpose reads.  The prologue's row scales (q^ = q rq DK^-1/2, k^ = k rk) are applied to products and folded into
 // the stored dM and Z, so the raw inputs are the MFMA operands.  Wave w owns key block w and value block w (16
 // features each) of the [D x C] products, and column block w % 4, row tiles 2 (w / 4) and 2 (w / 4) + 1 of the [C x C]
-// ones.  dq, dk and dv are staged in LDS and written as whole rows.
-template <int DK, int DV>
-__global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
+// ones.  dq, dk and dv are staged in LDS and written as whole rows.  With DK = DV a workgroup runs two chunk-heads
+// (chunk_bwd8x2_kernel), the second one's reads issued while the first computes.
+// The workgroup's LDS, as pointers to its arrays (declared in the kernels by CB8_LDS).  The three value tiles and dW's
+// tile are four arrays of one size (R1, R2, R3, R7; dW's tile is a value tile's size when DK = DV), so that a workgroup
+// running two chunk-heads can take the second one's tiles into the arrays the first has finished with.  Roles, first
+// chunk-head (0) / second (1): dO then v: R1 / R7; Vn then dv: R2 / R1; dVn: R3 / R3; dW: R7 / R2.
+struct Cb8Lds {
+  bf16 *R1, *R2, *R3, *R7;
+  bf16* tiles2;                            // q, k, A
+  bf16 *sMkT, *sMqT, *sAZ;                 // [s][t] = dM[t][s] rk_s; [s][t] = dM[t][s] rq_t qs; dA^T, then Z rk
+  ChunkScalars* cs;
+  float *rk, *rq;
+  float (*part)[8][C];
+  float (*colp)[2][C];
+  float* partS;
+};
+#define CB8_LDS(DK, DV)                                                                                              \
+  constexpr int CB8_KP = (DK) + 8, CB8_CP = C + 8;                                                                   \
+  constexpr int CB8_VE = Tile<bf16, C, (DV)>::ELEMS > C * CB8_KP ? Tile<bf16, C, (DV)>::ELEMS : C * CB8_KP;          \
+  __shared__ __attribute__((aligned(16))) bf16 cb8_R1[Tile<bf16, C, (DV)>::ELEMS];                                   \
+  __shared__ __attribute__((aligned(16))) bf16 cb8_R2[Tile<bf16, C, (DV)>::ELEMS];                                   \
+  __shared__ __attribute__((aligned(16))) bf16 cb8_R3[Tile<bf16, C, (DV)>::ELEMS];                                   \
+  __shared__ __attribute__((aligned(16))) bf16 cb8_R7[CB8_VE];                                                       \
+  __shared__ __attribute__((aligned(16))) bf16 cb8_t2[2 * Tile<bf16, C, (DK)>::ELEMS + Tile<bf16, C, C>::ELEMS];     \
+  __shared__ __attribute__((aligned(16))) bf16 cb8_mk[C * CB8_CP];                                                   \
+  __shared__ __attribute__((aligned(16))) bf16 cb8_mq[C * CB8_CP];                                                   \
+  __shared__ __attribute__((aligned(16))) bf16 cb8_az[C * CB8_CP];                                                   \
+  __shared__ ChunkScalars cb8_cs;                                                                                    \
+  __shared__ __attribute__((aligned(16))) float cb8_rk[C], cb8_rq[C];                                                \
+  __shared__ float cb8_part[NPART][8][C];                                                                            \
+  __shared__ float cb8_colp[2][2][C];                                                                                \
+  __shared__ float cb8_partS[8];                                                                                     \
+  const Cb8Lds L{cb8_R1, cb8_R2, cb8_R3, cb8_R7, cb8_t2, cb8_mk, cb8_mq, cb8_az, &cb8_cs, cb8_rk, cb8_rq, cb8_part,   \
+                 cb8_colp, cb8_partS};
+
+// A chunk-head's place in a flat order of (chunk, head, batch row), chunks fastest
+__device__ __forceinline__ void cb8_unit(int u, int NT, int H, int& c, int& h, int& b) {
+  c = u % NT;
+  h = (u / NT) % H;
+  b = u / (NT * H);
+}
+
+// The first round of workgroups (a.stagger of them, one a CU) starts in three groups 6.4K cycles apart.  Launched
+// together, every CU issues its block's 233 KB of reads at once and waits on the memory system's backpressure, and
+// the later rounds keep that lockstep (each CU's next workgroup starts when its last one ends); staggered, a third
+// of the CUs load while the rest compute, and the offsets carry into the later rounds.  Measured at 4 rounds with
+// the inputs out of the caches: 2.5-4% off the kernel (2 groups or 4 groups, and other offsets, gained less); in
+// the training step, whose chunk states are still in the Infinity Cache, 0.4 us of its 111.
+__device__ __forceinline__ void cb8_stagger(int stagger, unsigned flat) {
+  if (stagger && flat < (unsigned)stagger)
+    for (int i = 0, n = (int)(flat % 3u) * 50; i < n; ++i) __builtin_amdgcn_s_sleep(2);   // 128 cycles each
+}
+
+// One chunk-head (c, h, b).  FIRST: its global reads are issued here; otherwise the previous chunk-head of the
+// workgroup issued them (its tiles into this role's arrays, its chunk states into s32 / sD, its g and beta into gv,
+// bv).  next >= 0 (role 0 only): the chunk-head this workgroup runs after this one, whose reads are issued here while
+// this one computes: dO's tile once dW's tile is consumed (after C), the chunk states into s32 / sD (dead after the
+// state products) a value block at a time in T1, dL and D, Vn's tile after E, dVn's tile and g, beta in G.
+template <int DK, int DV, int ROLE, bool FIRST>
+__device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8Lds& L, int c, int h, int b, int next,
+                                                Frag<float> (&s32)[DV / 32], Frag<float> (&sD)[DV / 32], float& gv,
+                                                float& bv) {
   using MT = bf16;
   constexpr int NW = 8;
   constexpr int NBD = DK / 16, NBV = DV / 16;   // feature blocks (<= NW)
@@ -2002,37 +2061,29 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   using GV = Tile<MT, C, DV>;
   using GA = Tile<MT, C, C>;
   static_assert(GQ::PITCH == KP && GA::PITCH == CP && NBD <= NW && NBV <= NW, "chunk_bwd8 tiling");
+  static_assert(ROLE == 0 || (DK == DV && !FIRST), "the second role takes dW's tile into a value tile's array");
   constexpr int VP = GV::PITCH;
-  // two arrays: the compiler then knows that reads of the first do not depend on copies still in flight into the second
-  __shared__ __attribute__((aligned(16))) MT tiles1[3 * GV::ELEMS];                 // dO (then v), Vn (then dv), dVn
-  __shared__ __attribute__((aligned(16))) MT tiles2[2 * GQ::ELEMS + GA::ELEMS];     // q, k, A
-  __shared__ __attribute__((aligned(16))) MT sdW[C * KP];    // dW = -dVn S_c^T, [t][d]
-  __shared__ __attribute__((aligned(16))) MT sMkT[C * CP];   // [s][t] = dM[t][s] rk_s
-  __shared__ __attribute__((aligned(16))) MT sMqT[C * CP];   // [s][t] = dM[t][s] rq_t qs
-  __shared__ __attribute__((aligned(16))) MT sAZ[C * CP];    // dA^T: [s][t] = dA[t][s]; then [s][t] = Z[t][s] rk_t
-  __shared__ ChunkScalars cs;
-  __shared__ __attribute__((aligned(16))) float rk[C], rq[C];
-  __shared__ float part[NPART][NW][C];
-  __shared__ float colp[2][2][C];
-  __shared__ float partS[NW];
-
-  // The first round of workgroups (a.stagger of them, one a CU) starts in three groups 6.4K cycles apart.  Launched
-  // together, every CU issues its block's 233 KB of reads at once and waits on the memory system's backpressure, and
-  // the later rounds keep that lockstep (each CU's next workgroup starts when its last one ends); staggered, a third
-  // of the CUs load while the rest compute, and the offsets carry into the later rounds.  Measured at 4 rounds with
-  // the inputs out of the caches: 2.5-4% off the kernel (2 groups or 4 groups, and other offsets, gained less); in
-  // the training step, whose chunk states are still in the Infinity Cache, 0.4 us of its 111.
-  if (a.stagger) {
-    const unsigned flat = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-    if (flat < (unsigned)a.stagger)
-      for (int i = 0, n = (int)(flat % 3u) * 50; i < n; ++i) __builtin_amdgcn_s_sleep(2);   // 128 cycles each
-  }
-  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  MT* const tiles2 = L.tiles2;
+  MT* const sMkT = L.sMkT;
+  MT* const sMqT = L.sMqT;
+  MT* const sAZ = L.sAZ;
+  MT* const sdW = ROLE == 0 ? L.R7 : L.R2;   // dW = -dVn S_c^T, [t][d]
+  ChunkScalars& cs = *L.cs;
+  float* const rk = L.rk;
+  float* const rq = L.rq;
+  float(*const part)[8][C] = L.part;
+  float(*const colp)[2][C] = L.colp;
+  float* const partS = L.partS;
   const int H = a.H, NT = a.NT;
   int t0, T;                               // the chunk's first token; T: its sequence's end (the bound for its rows)
-  chunk_span(a.pack, NT, c, a.T, t0, T);
+  chunk_span<!FIRST>(a.pack, NT, c, a.T, t0, T);   // (FIRST: no copies in flight yet; else through the scalar cache)
   const int nrows = (T - t0 < C) ? T - t0 : C;
-  const int l = lane_id(), w = wave_id(), j = l >> 4, n = l & 15;
+  // The lane and wave numbers pass through empty assembly: a workgroup running two chunk-heads then forms the second
+  // one's lane-dependent offsets afresh instead of keeping the first one's live across it (which spills).
+  int l = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
+  asm volatile("" : "+v"(l));
+  asm volatile("" : "+s"(w));
+  const int j = l >> 4, n = l & 15, tid = 64 * w + l;
   const size_t qk_base = ((size_t)b * a.T * a.Hk + h / (H / a.Hk)) * DK, qk_pitch = (size_t)a.Hk * DK;
   const size_t dqk_base = ((size_t)b * a.T * H + h) * DK, dqk_pitch = (size_t)H * DK;   // dq, dk: value heads
   const size_t v_base = ((size_t)b * a.T * H + h) * DV, v_pitch = (size_t)H * DV;
@@ -2051,10 +2102,13 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   MT* const tq = tiles2;
   MT* const tk = tiles2 + GQ::ELEMS;
   MT* const tA = tiles2 + 2 * GQ::ELEMS;
-  MT* const tO = tiles1;
-  MT* const tVn = tiles1 + GV::ELEMS;
-  MT* const tdV = tiles1 + 2 * GV::ELEMS;
+  MT* const tO = ROLE == 0 ? L.R1 : L.R7;   // dO, then v
+  MT* const tVn = ROLE == 0 ? L.R2 : L.R1;  // Vn, then dv
+  MT* const tdV = L.R3;
   const int cb = w & 3, hh = w >> 2;       // [C x C] column block and row half
+  constexpr int NSTATE = 4 * (DV / 32);   // state loads a wave issues: two 16-byte loads a fragment
+  constexpr bool HOLDS_STATES = NBD == NW;  // every wave holds a key block of the states (else waves w < NBD)
+  const bool holds = HOLDS_STATES || w < NBD;
 
   // ---- 0: global reads in two groups.  Group 1 is what the state products of B consume: the dO, Vn, dVn tiles and
   // the chunk states (into registers), issued in that order.  Loads retire in issue order, so once at most the state
@@ -2062,29 +2116,31 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   // first use, so the tail of group 1 (the states are 128 of its 176 KiB) overlaps the first stages.  Group 2 -- the v
   // fragments and the q, k, A tiles -- lands while B runs.  Every read is unconditional (rows past the end re-read the
   // last row and are masked later).
-  float gv, bv;                            // this lane's g and beta (used by wave 0)
-  {
-    const size_t o = s_base + (size_t)(t0 + l < T ? t0 + l : T - 1) * H;
-    gv = a.g[o];
-    bv = a.beta[o];
-  }
-  GV::template dma_exact<NW>(tO, dO + (size_t)t0 * v_pitch, v_pitch, w, nrows);
-  GV::template dma_exact<NW>(tVn, Vnc, DV, w);
-  GV::template dma_exact<NW>(tdV, dVc, DV, w);
-  __builtin_amdgcn_sched_barrier(0);      // the state loads stay behind the copies (the partial wait below counts on it)
-  Frag<float> s32[DV / 32];               // S_c rows of key block w (A operand, k = value features)
-  Frag<float> sD[DV / 32];                // dS_{c+1} rows of key block w
-  constexpr int NSTATE = 4 * (DV / 32);   // state loads a wave issues: two 16-byte loads a fragment
-  if (NBD == NW || w < NBD) {
-#pragma unroll
-    for (int kb = 0; kb < DV / 32; ++kb) {
-      s32[kb] = frag_k_f32(Scc, DV, 16 * w, 32 * kb);
-      sD[kb] = frag_k_f32(dSc, DV, 16 * w, 32 * kb);
+  // (gv, bv: this lane's g and beta, used by wave 0; s32, sD: S_c and dS_{c+1} rows of key block w, A operands with
+  // k = value features)
+  if constexpr (FIRST) {
+    {
+      const size_t o = s_base + (size_t)(t0 + l < T ? t0 + l : T - 1) * H;
+      gv = a.g[o];
+      bv = a.beta[o];
     }
-    __builtin_amdgcn_sched_barrier(0);
-    wait_vmcnt<NSTATE>();                  // g, beta and the tiles have landed; the states may still be in flight
+    GV::template dma_exact<NW>(tO, dO + (size_t)t0 * v_pitch, v_pitch, w, nrows, l);
+    GV::template dma_exact<NW>(tVn, Vnc, DV, w, C, l);
+    GV::template dma_exact<NW>(tdV, dVc, DV, w, C, l);
+    __builtin_amdgcn_sched_barrier(0);    // the state loads stay behind the copies (the partial wait below counts on it)
+    if (holds) {
+#pragma unroll
+      for (int kb = 0; kb < DV / 32; ++kb) {
+        s32[kb] = frag_k_f32(Scc, DV, 16 * w, 32 * kb, l);
+        sD[kb] = frag_k_f32(dSc, DV, 16 * w, 32 * kb, l);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vmcnt<NSTATE>();                // g, beta and the tiles have landed; the states may still be in flight
+    } else {
+      wait_dma();
+    }
   } else {
-    wait_dma();
+    wait_dma();                            // issued by the previous chunk-head (and its global stores)
   }
   // Group 2 -- the v fragments and the q, k, A tile units -- goes through registers. Its loads are spread over the
   // state products' stages below: an issue stalls while the memory system is saturated, so issuing them all here
@@ -2100,14 +2156,14 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
       const bf16x4 lo = *reinterpret_cast<const bf16x4*>(pv + 32 * sl), hi = *reinterpret_cast<const bf16x4*>(pv + 32 * sl + 16);
       vf[sl].v = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     } else if (sl < DV / 32 + NQ) {
-      uq[sl - DV / 32] = GQ::template load_unit<NW>(q + (size_t)t0 * qk_pitch, qk_pitch, w, sl - DV / 32, nrows);
+      uq[sl - DV / 32] = GQ::template load_unit<NW>(q + (size_t)t0 * qk_pitch, qk_pitch, w, sl - DV / 32, nrows, l);
     } else if (sl < DV / 32 + 2 * NQ) {
-      uk[sl - DV / 32 - NQ] = GQ::template load_unit<NW>(k + (size_t)t0 * qk_pitch, qk_pitch, w, sl - DV / 32 - NQ, nrows);
+      uk[sl - DV / 32 - NQ] = GQ::template load_unit<NW>(k + (size_t)t0 * qk_pitch, qk_pitch, w, sl - DV / 32 - NQ, nrows, l);
     } else if (sl < NG2) {
-      ua[sl - DV / 32 - 2 * NQ] = GA::template load_unit<NW>(Ac, C, w, sl - DV / 32 - 2 * NQ);
+      ua[sl - DV / 32 - 2 * NQ] = GA::template load_unit<NW>(Ac, C, w, sl - DV / 32 - 2 * NQ, C, l);
     }
   };
-  if (w == 0) chunk_scalars_from(cs, t0 + l < T ? gv : 0.f, t0 + l < T ? bv : 0.f, t0, T);
+  if (w == 0) chunk_scalars_from(cs, t0 + l < T ? gv : 0.f, t0 + l < T ? bv : 0.f, t0, T, l);
   // the chunk states in their MFMA forms, value block by value block at its first stage (S_c in bf16; dS_{c+1} as
   // hi + lo bf16: the e k . (Vn dS^T) terms of dg sum 64 rows of it), and the last-row dg term <S_c, dS_{c+1}> from
   // the fp32 values, in value-block order
@@ -2123,7 +2179,7 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   if (nrows < C) {                         // rows past the end: zeros in dO
     constexpr int UV = VP / 8;
     const int nz = C - nrows;
-    for (int i = threadIdx.x; i < nz * UV; i += blockDim.x)
+    for (int i = tid; i < nz * UV; i += 64 * NW)
       *reinterpret_cast<bf16x8*>(tO + (nrows + i % nz) * VP + 8 * (i / nz)) = bf16x8{};
     lds_barrier();
   }
@@ -2133,7 +2189,7 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   f4 dQt[4], dKt[4];
   f4 aO[4], aV[4], aD[4];
   constexpr int NS = 2 * (DV / 32), PER = (NG2 + NS - 1) / NS;   // stages; group-2 loads issued per stage
-  if (NBD == NW || w < NBD) {
+  if (holds) {
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) aO[ti] = aV[ti] = aD[ti] = f4{0.f, 0.f, 0.f, 0.f};
     // stage sg = (value block kb = sg / 2, token tiles 2 (sg % 2) and 2 (sg % 2) + 1): its dO, Vn, dVn fragments are
@@ -2173,11 +2229,11 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   wait_dma();                              // group 2 is in registers
 #pragma unroll
   for (int u = 0; u < NQ; ++u) {
-    GQ::template store_unit<NW>(tq, w, u, uq[u]);
-    GQ::template store_unit<NW>(tk, w, u, uk[u]);
+    GQ::template store_unit<NW>(tq, w, u, uq[u], l);
+    GQ::template store_unit<NW>(tk, w, u, uk[u], l);
   }
 #pragma unroll
-  for (int u = 0; u < NA; ++u) GA::template store_unit<NW>(tA, w, u, ua[u]);
+  for (int u = 0; u < NA; ++u) GA::template store_unit<NW>(tA, w, u, ua[u], l);
   lds_barrier();                         // group 2 visible
   if (tv >= T) {                           // v rows past the end
 #pragma unroll
@@ -2186,17 +2242,17 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   if (nrows < C) {                         // rows past the end: zeros in q and k (the norms read rows < nrows only)
     constexpr int UQ = KP / 8;
     const int nz = C - nrows;
-    for (int i = threadIdx.x; i < nz * 2 * UQ; i += blockDim.x) {
+    for (int i = tid; i < nz * 2 * UQ; i += 64 * NW) {
       const int row = nrows + i % nz, u = i / nz;
       *reinterpret_cast<bf16x8*>(u < UQ ? tq + row * KP + 8 * u : tk + row * KP + 8 * (u - UQ)) = bf16x8{};
     }
   }
   if (a.l2norm) {                          // the row norms from the tiles (rows past the end: 0)
-    if (w < 4) row_rnorms_lds<DK>(rq, tq, KP, nrows, 4, w);
-    else row_rnorms_lds<DK>(rk, tk, KP, nrows, 4, w - 4);
-  } else if (threadIdx.x < C) {
-    rk[threadIdx.x] = (int)threadIdx.x < nrows ? 1.f : 0.f;
-    rq[threadIdx.x] = (int)threadIdx.x < nrows ? 1.f : 0.f;
+    if (w < 4) row_rnorms_lds<DK>(rq, tq, KP, nrows, 4, w, l);
+    else row_rnorms_lds<DK>(rk, tk, KP, nrows, 4, w - 4, l);
+  } else if (tid < C) {
+    rk[tid] = tid < nrows ? 1.f : 0.f;
+    rq[tid] = tid < nrows ? 1.f : 0.f;
   }
   lds_barrier();                         // norms visible
   if (w < NBD) {
@@ -2217,12 +2273,12 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
     Frag<MT> fW[2];
     Frag<MT> fx[4][2];                     // A's nonzero blocks, all read before the products
 #pragma unroll
-    for (int p = 0; p < 2; ++p) fW[p] = frag_tr(sdW, KP, 32 * p, 16 * w);
+    for (int p = 0; p < 2; ++p) fW[p] = frag_tr(sdW, KP, 32 * p, 16 * w, l);
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
       for (int p = 0; p < 2; ++p)
-        if (32 * p + 31 >= 16 * ti) fx[ti][p] = frag_tr(tA, CP, 32 * p, 16 * ti);
+        if (32 * p + 31 >= 16 * ti) fx[ti][p] = frag_tr(tA, CP, 32 * p, 16 * ti, l);
     float pKX[4];
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
@@ -2263,22 +2319,22 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
     Frag<MT> st[2][7];
     auto load = [&](int sg, Frag<MT>(&f)[7]) {
       if (sg < NP) {
-        f[0] = frag_tile<MT, GQ>(tk, 16 * cb, 32 * sg);
+        f[0] = frag_tile<MT, GQ>(tk, 16 * cb, 32 * sg, l);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           const int mi = 2 * hh + i;
-          f[1 + 3 * i] = frag_tile<MT, GQ>(tq, 16 * mi, 32 * sg);
-          f[2 + 3 * i] = frag_tile<MT, GQ>(tk, 16 * mi, 32 * sg);
-          f[3 + 3 * i] = frag_k_raw(sdW, KP, 16 * mi, 32 * sg);
+          f[1 + 3 * i] = frag_tile<MT, GQ>(tq, 16 * mi, 32 * sg, l);
+          f[2 + 3 * i] = frag_tile<MT, GQ>(tk, 16 * mi, 32 * sg, l);
+          f[3 + 3 * i] = frag_k_raw(sdW, KP, 16 * mi, 32 * sg, l);
         }
       } else {
         const int kb = sg - NP;
-        f[0] = frag_tile<MT, GV>(tVn, 16 * cb, 32 * kb);
+        f[0] = frag_tile<MT, GV>(tVn, 16 * cb, 32 * kb, l);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           const int mi = 2 * hh + i;
-          f[1 + 2 * i] = frag_tile<MT, GV>(tO, 16 * mi, 32 * kb);
-          f[2 + 2 * i] = frag_tile<MT, GV>(tdV, 16 * mi, 32 * kb);
+          f[1 + 2 * i] = frag_tile<MT, GV>(tO, 16 * mi, 32 * kb, l);
+          f[2 + 2 * i] = frag_tile<MT, GV>(tdV, 16 * mi, 32 * kb, l);
         }
       }
     };
@@ -2330,7 +2386,7 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
       *reinterpret_cast<bf16x4*>(sMqT + s * CP + r0) = bf16x4{(bf16)mq[0], (bf16)mq[1], (bf16)mq[2], (bf16)mq[3]};
       *reinterpret_cast<bf16x4*>(sAZ + s * CP + r0) = bf16x4{(bf16)da[0], (bf16)da[1], (bf16)da[2], (bf16)da[3]};
     }
-    const float rs = group16_sum8(pR1);            // row (l % 16) / 2 of the 8: tile i = idx / 4, r = idx % 4
+    const float rs = group16_sum8(pR1, l);            // row (l % 16) / 2 of the 8: tile i = idx / 4, r = idx % 4
     if ((n & 1) == 0) {
       const int idx = n >> 1;
       part[P_R1][cb][16 * (2 * hh + (idx >> 2)) + 4 * j + (idx & 3)] = rs;
@@ -2339,8 +2395,39 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
     if (j == 0) colp[0][hh][s] = cR1;
   }
   lds_barrier();
-  // dO is consumed: v takes its tile (needed from E on)
-  GV::template dma_exact<NW>(tO, v + (size_t)t0 * v_pitch, v_pitch, w, nrows);
+  // dO is consumed: v takes its tile (needed from E on).  The copies are hidden from the compiler (dma_exact_opaque), so
+  // it does not make the LDS reads of the next phases wait for them; the waits below are explicit.
+  GV::template dma_exact_opaque<NW>(tO, v + (size_t)t0 * v_pitch, v_pitch, w, nrows, l);
+  // The next chunk-head's reads, spread over the phases up to G: a wave's vector-memory issue stalls while the memory
+  // system is saturated, so issued at once they would hold this chunk-head's compute back.  Its dO goes into dW's
+  // array (consumed by C) now, its chunk states into s32 / sD (dead since B) a value block at a time in T1, dL and D,
+  // its Vn and dVn into v's and dVn's arrays after E and in G.
+  int nt0 = 0, nT = 0, nrows_n = 0;
+  size_t nv_base = 0, nbhc = 0, ns_base = 0;
+  const float *nS = nullptr, *ndS = nullptr;
+  const bool pf = ROLE == 0 && next >= 0;
+  auto pf_state = [&](int kb) {
+    if (ROLE == 0 && pf && holds) {
+      s32[kb] = frag_k_f32(nS, DV, 16 * w, 32 * kb, l);
+      sD[kb] = frag_k_f32(ndS, DV, 16 * w, 32 * kb, l);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  if constexpr (ROLE == 0) {
+    if (next >= 0) {
+      int nc, nh, nb;
+      cb8_unit(next, NT, H, nc, nh, nb);
+      chunk_span<true>(a.pack, NT, nc, a.T, nt0, nT);   // through the scalar cache: no wait on the copies above
+      nrows_n = (nT - nt0 < C) ? nT - nt0 : C;
+      nv_base = ((size_t)nb * a.T * H + nh) * DV;
+      ns_base = (size_t)nb * a.T * H + nh;
+      nbhc = ((size_t)nb * H + nh) * NT + nc;
+      GV::template dma_exact_opaque<NW>(L.R7, (const MT*)a.dO + nv_base + (size_t)nt0 * v_pitch, v_pitch, w, nrows_n, l);
+      nS = a.Sc + nbhc * DK * DV;
+      ndS = a.dSn + nbhc * DK * DV;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
 
   // ---- T1 = dA A^T (column block cb, all four row tiles), then dL = strictLower(-A^T T1) on this wave's tiles
   {
@@ -2350,15 +2437,16 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
     // every operand read first; blocks of A above the diagonal are zero, so no wave-dependent skip is needed
     Frag<MT> bA[2], fz[6];
 #pragma unroll
-    for (int p = 0; p < 2; ++p) bA[p] = frag_tile<MT, GA>(tA, 16 * cb, 32 * p);   // B[s][t'] = A[t'][s]
+    for (int p = 0; p < 2; ++p) bA[p] = frag_tile<MT, GA>(tA, 16 * cb, 32 * p, l);   // B[s][t'] = A[t'][s]
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) fz[mi] = frag_tr(sAZ, CP, 0, 16 * mi);
-    fz[4] = frag_tr(sAZ, CP, 32, 32);
-    fz[5] = frag_tr(sAZ, CP, 32, 48);
+    for (int mi = 0; mi < 4; ++mi) fz[mi] = frag_tr(sAZ, CP, 0, 16 * mi, l);
+    fz[4] = frag_tr(sAZ, CP, 32, 32, l);
+    fz[5] = frag_tr(sAZ, CP, 32, 48, l);
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) mma(T1[mi], fz[mi], bA[0]);
     mma(T1[2], fz[4], bA[1]);              // dA is strictly lower: rows 0-31 have no terms at t' >= 32
     mma(T1[3], fz[5], bA[1]);
+    pf_state(0);
     lds_barrier();                       // every wave has read dA^T: Z may overwrite it
     Frag<MT> T1f[2];
 #pragma unroll
@@ -2402,7 +2490,8 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
       if (mi > cb)
         *reinterpret_cast<bf16x4*>(sAZ + s * CP + r0) = bf16x4{(bf16)zt[0], (bf16)zt[1], (bf16)zt[2], (bf16)zt[3]};
     }
-    const float rs = group16_sum8(pR2);
+    pf_state(1);
+    const float rs = group16_sum8(pR2, l);
     if ((n & 1) == 0) {
       const int idx = n >> 1;
       part[P_R2][cb][16 * (2 * hh + (idx >> 2)) + 4 * j + (idx & 3)] = rs;
@@ -2417,17 +2506,17 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
     Frag<MT> kT[2], qT[2];
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-      kT[p] = frag_tr(tk, KP, 32 * p, 16 * w);
-      qT[p] = frag_tr(tq, KP, 32 * p, 16 * w);
+      kT[p] = frag_tr(tk, KP, 32 * p, 16 * w, l);
+      qT[p] = frag_tr(tq, KP, 32 * p, 16 * w, l);
     }
     // token tile ti is one stage: its dM and Z fragments are read one stage ahead of its products
     Frag<MT> st[2][6];
     auto load = [&](int ti, Frag<MT>(&f)[6]) {
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        if (32 * p <= 16 * ti + 15) f[3 * p] = frag_tr(sMkT, CP, 32 * p, 16 * ti);
-        if (32 * p + 31 >= 16 * ti) f[3 * p + 1] = frag_k_raw(sMqT, CP, 16 * ti, 32 * p);
-        f[3 * p + 2] = frag_k_raw(sAZ, CP, 16 * ti, 32 * p);
+        if (32 * p <= 16 * ti + 15) f[3 * p] = frag_tr(sMkT, CP, 32 * p, 16 * ti, l);
+        if (32 * p + 31 >= 16 * ti) f[3 * p + 1] = frag_k_raw(sMqT, CP, 16 * ti, 32 * p, l);
+        f[3 * p + 2] = frag_k_raw(sAZ, CP, 16 * ti, 32 * p, l);
       }
     };
     load(0, st[0]);
@@ -2441,7 +2530,9 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
         if (32 * p + 31 >= 16 * ti) mma(dKt[ti], qT[p], f[3 * p + 1]);
         mma(dKt[ti], kT[p], f[3 * p + 2]);
       }
+      if (ti == 1) pf_state(2);
     }
+    pf_state(3);
     if (a.l2norm) {
       const int d0 = 16 * w + 4 * j;
 #pragma unroll
@@ -2459,7 +2550,12 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
       }
     }
   }
-  wait_dma();                              // v
+  if (pf) {                                // v (the next chunk-head's dO copies and states may be in flight)
+    if (holds) wait_vmcnt<GV::per_wave(NW) + NSTATE>();
+    else wait_vmcnt<GV::per_wave(NW)>();
+  } else {
+    wait_dma();                            // v
+  }
   lds_barrier();
 
   // ---- E: Y^T = dVn^T A (value block w), dv = beta Y staged in Vn's tile, v . Y row sums
@@ -2468,12 +2564,12 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
     Frag<MT> fdv[2];
     Frag<MT> fy[4][2];
 #pragma unroll
-    for (int p = 0; p < 2; ++p) fdv[p] = frag_tr(tdV, VP, 32 * p, 16 * w);
+    for (int p = 0; p < 2; ++p) fdv[p] = frag_tr(tdV, VP, 32 * p, 16 * w, l);
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
       for (int p = 0; p < 2; ++p)
-        if (32 * p + 31 >= 16 * ti) fy[ti][p] = frag_tr(tA, CP, 32 * p, 16 * ti);
+        if (32 * p + 31 >= 16 * ti) fy[ti][p] = frag_tr(tA, CP, 32 * p, 16 * ti, l);
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
       f4 y = {0.f, 0.f, 0.f, 0.f};
@@ -2490,6 +2586,8 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
     }
   }
   lds_barrier();
+  if (ROLE == 0 && pf)                     // v's array is free: the next chunk-head's Vn
+    GV::template dma_exact_opaque<NW>(L.R1, (const MT*)a.Vn + nbhc * C * DV, DV, w, C, l);
 
   // ---- G: the prologue's backward; dq and dk staged over q's and k's tiles
   f4 gq[4], gk[4];
@@ -2515,6 +2613,12 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
     }
   }
   lds_barrier();                         // q and k tiles are read: they become the dq and dk staging
+  if (ROLE == 0 && pf) {                   // the next chunk-head's dVn into dVn's array (free since E), its g and beta
+    GV::template dma_exact_opaque<NW>(L.R3, (const MT*)a.dVn + nbhc * C * DV, DV, w, C, l);
+    const size_t o = ns_base + (size_t)(nt0 + l < nT ? nt0 + l : nT - 1) * H;
+    gv = a.g[o];
+    bv = a.beta[o];
+  }
   if (w < NBD) {
     const int d0 = 16 * w + 4 * j;
 #pragma unroll
@@ -2531,20 +2635,19 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   // written after E, so F runs off the path of the workgroup's last barrier
   if (w != 0) {
     constexpr int UK = DK / 8, UV = DV / 8, NTH = 64 * (NW - 1);
-    const int tid = threadIdx.x - 64;
+    const int wt = tid - 64;
     MT* dq = (MT*)a.dq + dqk_base + (size_t)t0 * dqk_pitch;
     MT* dk = (MT*)a.dk + dqk_base + (size_t)t0 * dqk_pitch;
     MT* dv = (MT*)a.dv + v_base + (size_t)t0 * v_pitch;
-    for (int i = tid; i < nrows * UK; i += NTH) {
+    for (int i = wt; i < nrows * UK; i += NTH) {
       const int row = i / UK, u = i - row * UK;
       *reinterpret_cast<bf16x8*>(dq + row * dqk_pitch + 8 * u) = *reinterpret_cast<const bf16x8*>(tq + row * KP + 8 * u);
       *reinterpret_cast<bf16x8*>(dk + row * dqk_pitch + 8 * u) = *reinterpret_cast<const bf16x8*>(tk + row * KP + 8 * u);
     }
-    for (int i = tid; i < nrows * UV; i += NTH) {
+    for (int i = wt; i < nrows * UV; i += NTH) {
       const int row = i / UV, u = i - row * UV;
       *reinterpret_cast<bf16x8*>(dv + row * v_pitch + 8 * u) = *reinterpret_cast<const bf16x8*>(tVn + row * VP + 8 * u);
     }
-    return;
   }
 
   // ---- F: dbeta and dg (wave 0, lane = chunk row), fixed-order sums of the partials
@@ -2568,14 +2671,43 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
     // dg_t = sum_{s >= t} dG_s + sum_{r < t} E_r; the exclusive prefix by a shift, not incl - E: E on the last valid
     // row is O(1) while the earlier ones carry exp(G_last - G_r) and can be ~1e-9 of it
     const float rev = __shfl(dG, C - 1 - r, 64);
-    const float suf = __shfl(wave_incl_scan(rev), C - 1 - r, 64);
+    const float suf = __shfl(wave_incl_scan(rev, l), C - 1 - r, 64);
     float Esh = __shfl_up(E, 1, 64);
     if (r == 0) Esh = 0.f;
-    const float pre = wave_incl_scan(Esh);
+    const float pre = wave_incl_scan(Esh, l);
     if (t < T) {
       a.dg[s_base + (size_t)t * H] = suf + pre;
       a.dbeta[s_base + (size_t)t * H] = db;
     }
+  }
+}
+
+template <int DK, int DV>
+__global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
+  CB8_LDS(DK, DV)
+  cb8_stagger(a.stagger, blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
+  Frag<float> s32[DV / 32], sD[DV / 32];
+  float gv, bv;
+  chunk_bwd8_body<DK, DV, 0, true>(a, L, blockIdx.x, blockIdx.y, blockIdx.z, -1, s32, sD, gv, bv);
+}
+
+// Two chunk-heads a workgroup (DK = DV): units blockIdx.x and blockIdx.x + half of the flat (chunk, head, batch row)
+// order.  The second one's reads are issued while the first one computes (its chunk states after the first one's
+// state products, its tiles into the arrays the first one has finished with), so only the first one's load phase is
+// exposed.
+template <int D>
+__global__ void __launch_bounds__(512) chunk_bwd8x2_kernel(ChunkBwdArgs a, int units, int half) {
+  CB8_LDS(D, D)
+  cb8_stagger(a.stagger, blockIdx.x);
+  Frag<float> s32[D / 32], sD[D / 32];
+  float gv, bv;
+  const int u0 = blockIdx.x, u1 = u0 + half;
+  int c, h, b;
+  cb8_unit(u0, a.NT, a.H, c, h, b);
+  chunk_bwd8_body<D, D, 0, true>(a, L, c, h, b, u1 < units ? u1 : -1, s32, sD, gv, bv);
+  if (u1 < units) {
+    cb8_unit(u1, a.NT, a.H, c, h, b);
+    chunk_bwd8_body<D, D, 1, false>(a, L, c, h, b, -1, s32, sD, gv, bv);
   }
 }
 
@@ -3022,9 +3154,13 @@ int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float
   ChunkBwdArgs a{q, k, v, g, beta, dO, A, Sc, dSn, Vn, dVn, dq, dk, dv, dg, dbeta, (int)B, (int)T, (int)H,
                  (int)DV, (int)NT, use_l2norm, q_scale, (int)Hk, pack, 0};
   dim3 grid(a.NT, (unsigned)H, pack ? 1u : (unsigned)B);
+  const int64_t units = (int64_t)grid.x * grid.y * grid.z;
+  bool x2 = false;                         // two chunk-heads a workgroup (DK = DV, more than one round of workgroups)
   if (dtype != MACAI_GDR_F32) {            // chunk_bwd8 (one workgroup a CU): stagger its first round when more follow
     const int cus = device_cus();
-    if (cus > 0 && (int64_t)grid.x * grid.y * grid.z >= 2 * (int64_t)cus) a.stagger = cus;
+    x2 = DK == DV && cus > 0 && units > cus && units < (int64_t)1 << 30;
+    const int64_t wgs = x2 ? (units + 1) / 2 : units;
+    if (cus > 0 && wgs >= 2 * (int64_t)cus) a.stagger = cus;
   }
   hipStream_t st = (hipStream_t)stream;
 #define LAUNCH_CB(MT)                                                                                               \
@@ -3036,6 +3172,10 @@ int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float
   })
   if (dtype == MACAI_GDR_F32) {
     LAUNCH_CB(float);
+  } else if (x2) {
+    const int half = (int)((units + 1) / 2);
+    DISPATCH_DK(DK, hipLaunchKernelGGL((chunk_bwd8x2_kernel<DKC>), dim3((unsigned)half), dim3(512), 0, st, a,
+                                       (int)units, half));
   } else {
     DISPATCH_DK(DK, switch (DV) {
       case 32: hipLaunchKernelGGL((chunk_bwd8_kernel<DKC, 32>), grid, dim3(512), 0, st, a); break;

@@ -54,8 +54,8 @@ struct Tile {
   // compiler can no longer order the vector-memory counter and waits for zero before every use of a loaded register.
   // Byte offsets within the tile must fit 31 bits.
   template <int NW>
-  __device__ static __forceinline__ void dma_exact(T* base, const T* g, size_t gpitch, int w, int nrows = R) {
-    const int l = lane_id();
+  __device__ static __forceinline__ void dma_exact(T* base, const T* g, size_t gpitch, int w, int nrows = R,
+                                                   int l = lane_id()) {
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)g, 0, 0x7fffffff, 0x00020000);
 #pragma unroll
     for (int k = 0; k < per_wave(NW); ++k) {
@@ -67,23 +67,46 @@ struct Tile {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(base + i * 64 * EPU), 16, off, 0, 0, 0);
     }
   }
+  // dma_exact() issued through inline assembly, unseen by the compiler: it then does not make every later LDS read
+  // wait for the copy (which it does for a copy into LDS it knows of).  The caller waits for it explicitly (wait_dma,
+  // wait_vmcnt) before the barrier that publishes the tile.  The buffer resource is dma_exact's (base g, no stride,
+  // 2^31 - 1 bytes, the same flags word); M0 holds the LDS address of the instruction's 64 x 16 bytes.
+  template <int NW>
+  __device__ static __forceinline__ void dma_exact_opaque(T* base, const T* g, size_t gpitch, int w, int nrows = R,
+                                                          int l = lane_id()) {
+    const unsigned long long ga = (unsigned long long)(const void*)g;
+    const u32x4 rs = {(unsigned)__builtin_amdgcn_readfirstlane((unsigned)ga),
+                      (unsigned)__builtin_amdgcn_readfirstlane((unsigned)(ga >> 32) & 0xffffu), 0x7fffffffu, 0x00020000u};
+#pragma unroll
+    for (int k = 0; k < per_wave(NW); ++k) {
+      const int i = w + k * NW < NI ? w + k * NW : NI - 1;
+      const int u = i * 64 + l;
+      const int row = u / RU, cu = u - row * RU;
+      int off = 0;
+      if (row < R && cu < PU) off = (int)(((size_t)(row < nrows ? row : nrows - 1) * gpitch + cu * EPU) * sizeof(T));
+      const unsigned lds = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(lds_void*)(base + i * 64 * EPU));
+      // s_nop: one wait state between an SALU write of M0 and an LDS-DMA read of it
+      asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(off), "s"(rs), "{m0}"(lds) : "memory");
+    }
+  }
   // The same copy through registers, one instruction's unit at a time: load_unit(k) reads the 16 bytes that
   // dma_exact's k-th instruction of wave w would move for this lane, store_unit(k) writes them to the same LDS place.
   // Loads issued this way are ordinary register loads, so they can be spread between other work without the compiler
   // treating every LDS read as dependent on them (which it does for copies into LDS in flight).
   template <int NW>
-  __device__ static __forceinline__ u32x4 load_unit(const T* g, size_t gpitch, int w, int k, int nrows = R) {
+  __device__ static __forceinline__ u32x4 load_unit(const T* g, size_t gpitch, int w, int k, int nrows = R,
+                                                    int l = lane_id()) {
     const int i = w + k * NW < NI ? w + k * NW : NI - 1;
-    const int u = i * 64 + lane_id();
+    const int u = i * 64 + l;
     const int row = u / RU, cu = u - row * RU;
     const T* src = g;
     if (row < R && cu < PU) src = g + (size_t)(row < nrows ? row : nrows - 1) * gpitch + cu * EPU;
     return *reinterpret_cast<const u32x4*>(src);
   }
   template <int NW>
-  __device__ static __forceinline__ void store_unit(T* base, int w, int k, u32x4 x) {
+  __device__ static __forceinline__ void store_unit(T* base, int w, int k, u32x4 x, int l = lane_id()) {
     const int i = w + k * NW < NI ? w + k * NW : NI - 1;
-    *reinterpret_cast<u32x4*>(base + i * 64 * EPU + lane_id() * EPU) = x;
+    *reinterpret_cast<u32x4*>(base + i * 64 * EPU + l * EPU) = x;
   }
   // Copy a global tile (row r at g + r * gpitch; rows >= nrows re-read row nrows - 1, to be masked by the reader) into
   // LDS `base`; waves w, w + nw, ... share the wave instructions.
@@ -108,8 +131,8 @@ struct Dense {
 
 // Fragment (A operand rows, or B operand columns = rows of B^T) of a k-contiguous tile.
 template <typename MT, typename G>
-__device__ __forceinline__ Frag<MT> frag_tile(const MT* base, int row0, int k0) {
-  const int l = lane_id(), j = l >> 4;
+__device__ __forceinline__ Frag<MT> frag_tile(const MT* base, int row0, int k0, int l = lane_id()) {
+  const int j = l >> 4;
   const MT* p = base + (row0 + (l & 15)) * G::PITCH + k0 + 4 * j;
   Frag<MT> f;
   if constexpr (sizeof(MT) == 2) {
@@ -159,8 +182,8 @@ __device__ __forceinline__ bf16x4 read_tr(const bf16* p) {
 }
 // Fragment whose k runs over the ROWS of a row-major bf16 matrix X[k][n] (B operand with k = row, or A operand of X^T):
 // lane l (j = l / 16) takes column n0 + l % 16 and rows k0 + kmap(j, 0..7).  Two transpose reads.
-__device__ __forceinline__ Frag<bf16> frag_tr(const bf16* X, int pitch, int k0, int n0) {
-  const int l = lane_id(), j = l >> 4, s = l & 15;
+__device__ __forceinline__ Frag<bf16> frag_tr(const bf16* X, int pitch, int k0, int n0, int l = lane_id()) {
+  const int j = l >> 4, s = l & 15;
   const bf16* p = X + (k0 + 4 * j + (s >> 2)) * pitch + n0 + 4 * (s & 3);
   const bf16x4 lo = read_tr(p), hi = read_tr(p + 16 * pitch);
   Frag<bf16> f;
