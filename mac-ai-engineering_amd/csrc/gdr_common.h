@@ -141,14 +141,35 @@ __device__ __forceinline__ Frag<float> frag_k_f32(const float* base, int pitch, 
 }
 
 // ---- wave-level scans and reductions -------------------------------------------------------------------------------
-__device__ __forceinline__ float wave_incl_scan(float x, int l = lane_id()) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    float y = __shfl_up(x, off, 64);
-    if (l >= off) x += y;
-  }
+// Inclusive scans over the wave's 64 lanes by DPP (GFX9), with no LDS round trip: in-row shifts by 1, 2, 4, 8 (a lane
+// whose source falls before its 16-lane row adds 0), then lane 15's sum into rows 1 and 3 (row_bcast:15) and lane
+// 31's into rows 2 and 3 (row_bcast:31) -- the published GCN cross-lane scan (AMD GPUOpen, "AMD GCN Assembly:
+// Cross-Lane Operations").  Rows a mask leaves out receive 0.
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ int dpp_z(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, ROWS, 0xF, true);
+}
+enum : int { DPP_ROW_SHR1 = 0x111, DPP_ROW_SHR2 = 0x112, DPP_ROW_SHR4 = 0x114, DPP_ROW_SHR8 = 0x118,
+             DPP_ROW_BCAST15 = 0x142, DPP_ROW_BCAST31 = 0x143, DPP_WAVE_SHR1 = 0x138 };
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ float dpp_zf(float x) { return __int_as_float(dpp_z<CTRL, ROWS>(__float_as_int(x))); }
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ double dpp_zd(double x) {
+  const long long b = __double_as_longlong(x);
+  const int lo = dpp_z<CTRL, ROWS>((int)b), hi = dpp_z<CTRL, ROWS>((int)(b >> 32));
+  return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
+__device__ __forceinline__ float wave_incl_scan(float x, int = 0) {
+  x += dpp_zf<DPP_ROW_SHR1>(x);
+  x += dpp_zf<DPP_ROW_SHR2>(x);
+  x += dpp_zf<DPP_ROW_SHR4>(x);
+  x += dpp_zf<DPP_ROW_SHR8>(x);
+  x += dpp_zf<DPP_ROW_BCAST15, 0xA>(x);
+  x += dpp_zf<DPP_ROW_BCAST31, 0xC>(x);
   return x;
 }
+// x of lane l - 1 (0 in lane 0)
+__device__ __forceinline__ float wave_shift_up1(float x) { return dpp_zf<DPP_WAVE_SHR1>(x); }
 // lane permutations inside each 16-lane DPP row (no LDS round trip): quad_perm [1,0,3,2] and [2,3,0,1], row_half_mirror
 // (lane i <-> 7 - i within each 8), row_mirror (i <-> 15 - i)
 enum : int { DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140 };
@@ -210,12 +231,13 @@ struct __attribute__((aligned(16))) ChunkScalars {   // 16-byte aligned: rows ar
   __device__ __forceinline__ float decay(int i, int j) const { return expf((float)(G[i] - G[j])); }
 };
 
-__device__ __forceinline__ double wave_incl_scan_d(double x, int l = lane_id()) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    double y = __shfl_up(x, off, 64);
-    if (l >= off) x += y;
-  }
+__device__ __forceinline__ double wave_incl_scan_d(double x) {
+  x += dpp_zd<DPP_ROW_SHR1>(x);
+  x += dpp_zd<DPP_ROW_SHR2>(x);
+  x += dpp_zd<DPP_ROW_SHR4>(x);
+  x += dpp_zd<DPP_ROW_SHR8>(x);
+  x += dpp_zd<DPP_ROW_BCAST15, 0xA>(x);
+  x += dpp_zd<DPP_ROW_BCAST31, 0xC>(x);
   return x;
 }
 
@@ -223,8 +245,10 @@ __device__ __forceinline__ double wave_incl_scan_d(double x, int l = lane_id()) 
 __device__ __forceinline__ void chunk_scalars_from(ChunkScalars& cs, float gv, float bv, int t0, int T,
                                                    int l = lane_id()) {
   const int last = (T - t0 < C ? T - t0 : C) - 1;
-  double G = wave_incl_scan_d((double)gv, l);
-  const double Gl = __shfl(G, last, 64);
+  double G = wave_incl_scan_d((double)gv);
+  const long long gb = __double_as_longlong(G);   // G of the last valid row, read from its lane (last is uniform)
+  const double Gl = __longlong_as_double(((long long)__builtin_amdgcn_readlane((int)(gb >> 32), last) << 32) |
+                                         (unsigned)__builtin_amdgcn_readlane((int)gb, last));
   if (l > last) G = Gl;
   cs.G[l] = G;
   cs.gam[l] = (float)exp(G);

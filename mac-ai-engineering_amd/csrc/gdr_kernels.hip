@@ -1944,7 +1944,7 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
     // row is O(1) while the earlier ones carry exp(G_last - G_r) and can be ~1e-9 of it
     const float rev = __shfl(dG, C - 1 - r, 64);
     const float suf = __shfl(wave_incl_scan(rev), C - 1 - r, 64);
-    float Esh = __shfl_up(E, 1, 64);
+    float Esh = wave_shift_up1(E);
     if (r == 0) Esh = 0.f;
     const float pre = wave_incl_scan(Esh);
     if (t < T) {
@@ -2006,6 +2006,7 @@ struct Cb8Lds {
   float (*part)[8][C];
   float (*colp)[2][C];
   float* partS;
+  float (*rowdot)[C];                      // the prologue's row dots of dq and dk, summed over key blocks
 };
 #define CB8_LDS(DK, DV)                                                                                              \
   constexpr int CB8_KP = (DK) + 8, CB8_CP = C + 8;                                                                   \
@@ -2023,8 +2024,9 @@ struct Cb8Lds {
   __shared__ float cb8_part[NPART][8][C];                                                                            \
   __shared__ float cb8_colp[2][2][C];                                                                                \
   __shared__ float cb8_partS[8];                                                                                     \
+  __shared__ __attribute__((aligned(16))) float cb8_rowdot[2][C];                                                    \
   const Cb8Lds L{cb8_R1, cb8_R2, cb8_R3, cb8_R7, cb8_t2, cb8_mk, cb8_mq, cb8_az, &cb8_cs, cb8_rk, cb8_rq, cb8_part,   \
-                 cb8_colp, cb8_partS};
+                 cb8_colp, cb8_partS, cb8_rowdot};
 
 // A chunk-head's place in a flat order of (chunk, head, batch row), chunks fastest
 __device__ __forceinline__ void cb8_unit(int u, int NT, int H, int& c, int& h, int& b) {
@@ -2044,15 +2046,17 @@ __device__ __forceinline__ void cb8_stagger(int stagger, unsigned flat) {
     for (int i = 0, n = (int)(flat % 3u) * 50; i < n; ++i) __builtin_amdgcn_s_sleep(2);   // 128 cycles each
 }
 
-// One chunk-head (c, h, b).  FIRST: its global reads are issued here; otherwise the previous chunk-head of the
+// One chunk-head (unit: its place in the flat (chunk, head, batch row) order).  FIRST: its global reads are issued here; otherwise the previous chunk-head of the
 // workgroup issued them (its tiles into this role's arrays, its chunk states into s32 / sD, its g and beta into gv,
 // bv).  next >= 0 (role 0 only): the chunk-head this workgroup runs after this one, whose reads are issued here while
 // this one computes: dO's tile once dW's tile is consumed (after C), the chunk states into s32 / sD (dead after the
-// state products) a value block at a time in T1, dL and D, Vn's tile after E, dVn's tile and g, beta in G.
+// state products) a value block at a time in T1, dL and D, Vn's, dVn's tiles and g, beta in G.
 template <int DK, int DV, int ROLE, bool FIRST>
-__device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8Lds& L, int c, int h, int b, int next,
+__device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8Lds& L, int unit, int next,
                                                 Frag<float> (&s32)[DV / 32], Frag<float> (&sD)[DV / 32], float& gv,
                                                 float& bv) {
+  int c, h, b;
+  cb8_unit(unit, a.NT, a.H, c, h, b);
   using MT = bf16;
   constexpr int NW = 8;
   constexpr int NBD = DK / 16, NBV = DV / 16;   // feature blocks (<= NW)
@@ -2074,6 +2078,7 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
   float(*const part)[8][C] = L.part;
   float(*const colp)[2][C] = L.colp;
   float* const partS = L.partS;
+  float(*const rowdot)[C] = L.rowdot;
   const int H = a.H, NT = a.NT;
   int t0, T;                               // the chunk's first token; T: its sequence's end (the bound for its rows)
   chunk_span<!FIRST>(a.pack, NT, c, a.T, t0, T);   // (FIRST: no copies in flight yet; else through the scalar cache)
@@ -2557,6 +2562,12 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
     wait_dma();                            // v
   }
   lds_barrier();
+  if (a.l2norm && tid < 2 * C) {           // G's row dots, each summed once, in key-block order
+    const int kind = tid >> 6, row = tid & (C - 1);
+    float x = part[P_DQ + kind][0][row];
+    for (int i = 1; i < NBD; ++i) x += part[P_DQ + kind][i][row];
+    rowdot[kind][row] = x;
+  }
 
   // ---- E: Y^T = dVn^T A (value block w), dv = beta Y staged in Vn's tile, v . Y row sums
   if (w < NBV) {
@@ -2586,8 +2597,6 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
     }
   }
   lds_barrier();
-  if (ROLE == 0 && pf)                     // v's array is free: the next chunk-head's Vn
-    GV::template dma_exact_opaque<NW>(L.R1, (const MT*)a.Vn + nbhc * C * DV, DV, w, C, l);
 
   // ---- G: the prologue's backward; dq and dk staged over q's and k's tiles
   f4 gq[4], gk[4];
@@ -2597,11 +2606,7 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
     for (int ti = 0; ti < 4; ++ti) {
       const int t = 16 * ti + n;
       if (a.l2norm) {
-        float dq_dot = part[P_DQ][0][t], dk_dot = part[P_DK][0][t];
-        for (int i = 1; i < NBD; ++i) {
-          dq_dot += part[P_DQ][i][t];
-          dk_dot += part[P_DK][i][t];
-        }
+        const float dq_dot = rowdot[0][t], dk_dot = rowdot[1][t];
         const float rqt = rq[t], rkt = rk[t];
         const f4 xq = load4(tq + t * KP + d0) * rqt, xk = load4(tk + t * KP + d0) * rkt;
         gq[ti] = (qs * rqt) * (dQt[ti] - xq * dq_dot);
@@ -2612,6 +2617,8 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
       }
     }
   }
+  if (ROLE == 0 && pf)                     // v's array is free since E: the next chunk-head's Vn
+    GV::template dma_exact_opaque<NW>(L.R1, (const MT*)a.Vn + nbhc * C * DV, DV, w, C, l);
   lds_barrier();                         // q and k tiles are read: they become the dq and dk staging
   if (ROLE == 0 && pf) {                   // the next chunk-head's dVn into dVn's array (free since E), its g and beta
     GV::template dma_exact_opaque<NW>(L.R3, (const MT*)a.dVn + nbhc * C * DV, DV, w, C, l);
@@ -2672,7 +2679,7 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
     // row is O(1) while the earlier ones carry exp(G_last - G_r) and can be ~1e-9 of it
     const float rev = __shfl(dG, C - 1 - r, 64);
     const float suf = __shfl(wave_incl_scan(rev, l), C - 1 - r, 64);
-    float Esh = __shfl_up(E, 1, 64);
+    float Esh = wave_shift_up1(E);
     if (r == 0) Esh = 0.f;
     const float pre = wave_incl_scan(Esh, l);
     if (t < T) {
@@ -2688,7 +2695,8 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   cb8_stagger(a.stagger, blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
   Frag<float> s32[DV / 32], sD[DV / 32];
   float gv, bv;
-  chunk_bwd8_body<DK, DV, 0, true>(a, L, blockIdx.x, blockIdx.y, blockIdx.z, -1, s32, sD, gv, bv);
+  chunk_bwd8_body<DK, DV, 0, true>(a, L, blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), -1, s32, sD,
+                                   gv, bv);
 }
 
 // Two chunk-heads a workgroup (DK = DV): units blockIdx.x and blockIdx.x + half of the flat (chunk, head, batch row)
@@ -2702,13 +2710,8 @@ __global__ void __launch_bounds__(512) chunk_bwd8x2_kernel(ChunkBwdArgs a, int u
   Frag<float> s32[D / 32], sD[D / 32];
   float gv, bv;
   const int u0 = blockIdx.x, u1 = u0 + half;
-  int c, h, b;
-  cb8_unit(u0, a.NT, a.H, c, h, b);
-  chunk_bwd8_body<D, D, 0, true>(a, L, c, h, b, u1 < units ? u1 : -1, s32, sD, gv, bv);
-  if (u1 < units) {
-    cb8_unit(u1, a.NT, a.H, c, h, b);
-    chunk_bwd8_body<D, D, 1, false>(a, L, c, h, b, -1, s32, sD, gv, bv);
-  }
+  chunk_bwd8_body<D, D, 0, true>(a, L, u0, u1 < units ? u1 : -1, s32, sD, gv, bv);
+  if (u1 < units) chunk_bwd8_body<D, D, 1, false>(a, L, u1, -1, s32, sD, gv, bv);
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
