@@ -1991,12 +1991,13 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
 // transpose reads.  The prologue's row scales (q^ = q rq DK^-1/2, k^ = k rk) are applied to products and folded into
 // the stored dM and Z, so the raw inputs are the MFMA operands.  Wave w owns key block w and value block w (16
 // features each) of the [D x C] products, and column block w % 4, row tiles 2 (w / 4) and 2 (w / 4) + 1 of the [C x C]
-// ones.  dq, dk and dv are staged in LDS and written as whole rows.  With DK = DV a workgroup runs two chunk-heads
-// (chunk_bwd8x2_kernel), the second one's reads issued while the first computes.
+// ones.  dq, dk and dv are staged in LDS and written as whole rows.  With DK = DV the workgroups are persistent
+// (chunk_bwd8xn_kernel, one a CU), each running a strided run of chunk-heads, the next one's reads issued while the
+// current one computes.
 // The workgroup's LDS, as pointers to its arrays (declared in the kernels by CB8_LDS).  The three value tiles and dW's
 // tile are four arrays of one size (R1, R2, R3, R7; dW's tile is a value tile's size when DK = DV), so that a workgroup
-// running two chunk-heads can take the second one's tiles into the arrays the first has finished with.  Roles, first
-// chunk-head (0) / second (1): dO then v: R1 / R7; Vn then dv: R2 / R1; dVn: R3 / R3; dW: R7 / R2.
+// running a sequence of chunk-heads can take the next one's tiles into arrays the current one has finished with: dVn
+// always in R3, while dO (then v), Vn (then dv) and dW rotate over R1, R2, R7 (chunk_bwd8xn_kernel).
 struct Cb8Lds {
   bf16 *R1, *R2, *R3, *R7;
   bf16* tiles2;                            // q, k, A
@@ -2046,13 +2047,17 @@ __device__ __forceinline__ void cb8_stagger(int stagger, unsigned flat) {
     for (int i = 0, n = (int)(flat % 3u) * 50; i < n; ++i) __builtin_amdgcn_s_sleep(2);   // 128 cycles each
 }
 
-// One chunk-head (unit: its place in the flat (chunk, head, batch row) order).  FIRST: its global reads are issued here; otherwise the previous chunk-head of the
-// workgroup issued them (its tiles into this role's arrays, its chunk states into s32 / sD, its g and beta into gv,
-// bv).  next >= 0 (role 0 only): the chunk-head this workgroup runs after this one, whose reads are issued here while
-// this one computes: dO's tile once dW's tile is consumed (after C), the chunk states into s32 / sD (dead after the
-// state products) a value block at a time in T1, dL and D, Vn's, dVn's tiles and g, beta in G.
-template <int DK, int DV, int ROLE, bool FIRST>
-__device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8Lds& L, int unit, int next,
+// One chunk-head (unit: its place in the flat (chunk, head, batch row) order), its dO / v, Vn / dv and dW tiles in
+// the arrays tO, tVn, sdW (dVn's in R3).  first: its global reads are issued here; otherwise the previous chunk-head of
+// the workgroup issued them (its tiles into these arrays, its chunk states into s32 / sD, its g and beta into gv, bv).
+// next >= 0 (DK = DV): the chunk-head this workgroup runs after this one, whose reads are issued here while this one
+// computes: its dO into sdW once dW is consumed (after C), its chunk states into s32 / sD (dead after the state
+// products) a value block at a time in T1, dL and D, its Vn into tO and its dVn, g and beta in G.  The copies into
+// LDS are issued unseen by the compiler (dma_exact_opaque), so the arrays may be chosen at run time, and each is
+// waited for explicitly.
+template <int DK, int DV>
+__device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8Lds& L, int unit, int next, bool first,
+                                                bf16* const tO, bf16* const tVn, bf16* const sdW,
                                                 Frag<float> (&s32)[DV / 32], Frag<float> (&sD)[DV / 32], float& gv,
                                                 float& bv) {
   int c, h, b;
@@ -2065,13 +2070,11 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
   using GV = Tile<MT, C, DV>;
   using GA = Tile<MT, C, C>;
   static_assert(GQ::PITCH == KP && GA::PITCH == CP && NBD <= NW && NBV <= NW, "chunk_bwd8 tiling");
-  static_assert(ROLE == 0 || (DK == DV && !FIRST), "the second role takes dW's tile into a value tile's array");
   constexpr int VP = GV::PITCH;
   MT* const tiles2 = L.tiles2;
   MT* const sMkT = L.sMkT;
   MT* const sMqT = L.sMqT;
   MT* const sAZ = L.sAZ;
-  MT* const sdW = ROLE == 0 ? L.R7 : L.R2;   // dW = -dVn S_c^T, [t][d]
   ChunkScalars& cs = *L.cs;
   float* const rk = L.rk;
   float* const rq = L.rq;
@@ -2081,7 +2084,7 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
   float(*const rowdot)[C] = L.rowdot;
   const int H = a.H, NT = a.NT;
   int t0, T;                               // the chunk's first token; T: its sequence's end (the bound for its rows)
-  chunk_span<!FIRST>(a.pack, NT, c, a.T, t0, T);   // (FIRST: no copies in flight yet; else through the scalar cache)
+  chunk_span<true>(a.pack, NT, c, a.T, t0, T);   // through the scalar cache: no wait on copies in flight
   const int nrows = (T - t0 < C) ? T - t0 : C;
   // The lane and wave numbers pass through empty assembly: a workgroup running two chunk-heads then forms the second
   // one's lane-dependent offsets afresh instead of keeping the first one's live across it (which spills).
@@ -2107,8 +2110,6 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
   MT* const tq = tiles2;
   MT* const tk = tiles2 + GQ::ELEMS;
   MT* const tA = tiles2 + 2 * GQ::ELEMS;
-  MT* const tO = ROLE == 0 ? L.R1 : L.R7;   // dO, then v
-  MT* const tVn = ROLE == 0 ? L.R2 : L.R1;  // Vn, then dv
   MT* const tdV = L.R3;
   const int cb = w & 3, hh = w >> 2;       // [C x C] column block and row half
   constexpr int NSTATE = 4 * (DV / 32);   // state loads a wave issues: two 16-byte loads a fragment
@@ -2123,15 +2124,15 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
   // last row and are masked later).
   // (gv, bv: this lane's g and beta, used by wave 0; s32, sD: S_c and dS_{c+1} rows of key block w, A operands with
   // k = value features)
-  if constexpr (FIRST) {
+  if (first) {
     {
       const size_t o = s_base + (size_t)(t0 + l < T ? t0 + l : T - 1) * H;
       gv = a.g[o];
       bv = a.beta[o];
     }
-    GV::template dma_exact<NW>(tO, dO + (size_t)t0 * v_pitch, v_pitch, w, nrows, l);
-    GV::template dma_exact<NW>(tVn, Vnc, DV, w, C, l);
-    GV::template dma_exact<NW>(tdV, dVc, DV, w, C, l);
+    GV::template dma_exact_opaque<NW>(tO, dO + (size_t)t0 * v_pitch, v_pitch, w, nrows, l);
+    GV::template dma_exact_opaque<NW>(tVn, Vnc, DV, w, C, l);
+    GV::template dma_exact_opaque<NW>(tdV, dVc, DV, w, C, l);
     __builtin_amdgcn_sched_barrier(0);    // the state loads stay behind the copies (the partial wait below counts on it)
     if (holds) {
 #pragma unroll
@@ -2410,16 +2411,16 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
   int nt0 = 0, nT = 0, nrows_n = 0;
   size_t nv_base = 0, nbhc = 0, ns_base = 0;
   const float *nS = nullptr, *ndS = nullptr;
-  const bool pf = ROLE == 0 && next >= 0;
+  const bool pf = next >= 0;
   auto pf_state = [&](int kb) {
-    if (ROLE == 0 && pf && holds) {
+    if (pf && holds) {
       s32[kb] = frag_k_f32(nS, DV, 16 * w, 32 * kb, l);
       sD[kb] = frag_k_f32(ndS, DV, 16 * w, 32 * kb, l);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
-  if constexpr (ROLE == 0) {
-    if (next >= 0) {
+  {
+    if (pf) {
       int nc, nh, nb;
       cb8_unit(next, NT, H, nc, nh, nb);
       chunk_span<true>(a.pack, NT, nc, a.T, nt0, nT);   // through the scalar cache: no wait on the copies above
@@ -2427,7 +2428,7 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
       nv_base = ((size_t)nb * a.T * H + nh) * DV;
       ns_base = (size_t)nb * a.T * H + nh;
       nbhc = ((size_t)nb * H + nh) * NT + nc;
-      GV::template dma_exact_opaque<NW>(L.R7, (const MT*)a.dO + nv_base + (size_t)nt0 * v_pitch, v_pitch, w, nrows_n, l);
+      GV::template dma_exact_opaque<NW>(sdW, (const MT*)a.dO + nv_base + (size_t)nt0 * v_pitch, v_pitch, w, nrows_n, l);
       nS = a.Sc + nbhc * DK * DV;
       ndS = a.dSn + nbhc * DK * DV;
       __builtin_amdgcn_sched_barrier(0);
@@ -2617,10 +2618,10 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
       }
     }
   }
-  if (ROLE == 0 && pf)                     // v's array is free since E: the next chunk-head's Vn
-    GV::template dma_exact_opaque<NW>(L.R1, (const MT*)a.Vn + nbhc * C * DV, DV, w, C, l);
+  if (pf)                                  // v's array is free since E: the next chunk-head's Vn
+    GV::template dma_exact_opaque<NW>(tO, (const MT*)a.Vn + nbhc * C * DV, DV, w, C, l);
   lds_barrier();                         // q and k tiles are read: they become the dq and dk staging
-  if (ROLE == 0 && pf) {                   // the next chunk-head's dVn into dVn's array (free since E), its g and beta
+  if (pf) {                                // the next chunk-head's dVn into dVn's array (free since E), its g and beta
     GV::template dma_exact_opaque<NW>(L.R3, (const MT*)a.dVn + nbhc * C * DV, DV, w, C, l);
     const size_t o = ns_base + (size_t)(nt0 + l < nT ? nt0 + l : nT - 1) * H;
     gv = a.g[o];
@@ -2695,23 +2696,32 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
   cb8_stagger(a.stagger, blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z));
   Frag<float> s32[DV / 32], sD[DV / 32];
   float gv, bv;
-  chunk_bwd8_body<DK, DV, 0, true>(a, L, blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), -1, s32, sD,
-                                   gv, bv);
+  chunk_bwd8_body<DK, DV>(a, L, blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), -1, true, L.R1,
+                          L.R2, L.R7, s32, sD, gv, bv);
 }
 
-// Two chunk-heads a workgroup (DK = DV): units blockIdx.x and blockIdx.x + half of the flat (chunk, head, batch row)
-// order.  The second one's reads are issued while the first one computes (its chunk states after the first one's
-// state products, its tiles into the arrays the first one has finished with), so only the first one's load phase is
-// exposed.
+// Persistent form (DK = DV): workgroup i runs units i, i + stride, ... of the flat (chunk, head, batch row) order,
+// each one's reads issued while the one before it computes, so only the first one's load phase is exposed.  The value
+// tiles' arrays rotate: the next unit's dO goes into this one's dW array, its Vn into this one's dO/v array, and its
+// dW array is this one's Vn/dv array.
 template <int D>
-__global__ void __launch_bounds__(512) chunk_bwd8x2_kernel(ChunkBwdArgs a, int units, int half) {
+__global__ void __launch_bounds__(512) chunk_bwd8xn_kernel(ChunkBwdArgs a, int units) {
   CB8_LDS(D, D)
   cb8_stagger(a.stagger, blockIdx.x);
   Frag<float> s32[D / 32], sD[D / 32];
   float gv, bv;
-  const int u0 = blockIdx.x, u1 = u0 + half;
-  chunk_bwd8_body<D, D, 0, true>(a, L, u0, u1 < units ? u1 : -1, s32, sD, gv, bv);
-  if (u1 < units) chunk_bwd8_body<D, D, 1, false>(a, L, u1, -1, s32, sD, gv, bv);
+  bf16 *tO = L.R1, *tVn = L.R2, *sdW = L.R7;
+  const int stride = gridDim.x;
+  bool first = true;
+  for (int u = blockIdx.x; u < units; u += stride) {
+    const int next = u + stride < units ? u + stride : -1;
+    chunk_bwd8_body<D, D>(a, L, u, next, first, tO, tVn, sdW, s32, sD, gv, bv);
+    bf16* const t = sdW;
+    sdW = tVn;
+    tVn = tO;
+    tO = t;
+    first = false;
+  }
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
@@ -3158,12 +3168,11 @@ int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float
                  (int)DV, (int)NT, use_l2norm, q_scale, (int)Hk, pack, 0};
   dim3 grid(a.NT, (unsigned)H, pack ? 1u : (unsigned)B);
   const int64_t units = (int64_t)grid.x * grid.y * grid.z;
-  bool x2 = false;                         // two chunk-heads a workgroup (DK = DV, more than one round of workgroups)
+  bool xn = false;                         // persistent workgroups, one a CU (DK = DV, more chunk-heads than CUs)
   if (dtype != MACAI_GDR_F32) {            // chunk_bwd8 (one workgroup a CU): stagger its first round when more follow
     const int cus = device_cus();
-    x2 = DK == DV && cus > 0 && units > cus && units < (int64_t)1 << 30;
-    const int64_t wgs = x2 ? (units + 1) / 2 : units;
-    if (cus > 0 && wgs >= 2 * (int64_t)cus) a.stagger = cus;
+    xn = DK == DV && cus > 0 && units > cus && units < (int64_t)1 << 30;
+    if (!xn && cus > 0 && units >= 2 * (int64_t)cus) a.stagger = cus;   // (the persistent form measured slower with it)
   }
   hipStream_t st = (hipStream_t)stream;
 #define LAUNCH_CB(MT)                                                                                               \
@@ -3175,10 +3184,11 @@ int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float
   })
   if (dtype == MACAI_GDR_F32) {
     LAUNCH_CB(float);
-  } else if (x2) {
-    const int half = (int)((units + 1) / 2);
-    DISPATCH_DK(DK, hipLaunchKernelGGL((chunk_bwd8x2_kernel<DKC>), dim3((unsigned)half), dim3(512), 0, st, a,
-                                       (int)units, half));
+  } else if (xn) {
+    const int cus = device_cus();
+    const int wgs = (int)(units < cus ? units : cus);
+    DISPATCH_DK(DK, hipLaunchKernelGGL((chunk_bwd8xn_kernel<DKC>), dim3((unsigned)wgs), dim3(512), 0, st, a,
+                                       (int)units));
   } else {
     DISPATCH_DK(DK, switch (DV) {
       case 32: hipLaunchKernelGGL((chunk_bwd8_kernel<DKC, 32>), grid, dim3(512), 0, st, a); break;
