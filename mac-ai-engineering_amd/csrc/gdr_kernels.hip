@@ -2376,7 +2376,8 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = r0 + r;
-        const float gm = (row >= s) ? expf((float)(cs.G[row] - Gs)) : 0.f;
+        // the decay by the hardware exp2 (a bf16 kernel: its ~1e-6 relative error is far below the operands')
+        const float gm = (row >= s) ? __builtin_amdgcn_exp2f((float)(cs.G[row] - Gs) * 1.4426950408889634f) : 0.f;
         gmv[i][r] = gm;
         const float Mv = QK[i][r] * (rq4[r] * qs * rks) * gm;
         const float dMv = dOV[i][r] * gm;
