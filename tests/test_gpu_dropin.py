@@ -404,6 +404,24 @@ def test_backward_is_bitwise_deterministic():
     assert all(torch.equal(a, b) for r in runs[1:] for a, b in zip(runs[0], r))
 
 
+@pytest.mark.parametrize("B,T,Hk,Hv,D", [(8, 1000, 16, 16, 128), (8, 1000, 16, 16, 64), (4, 700, 8, 16, 128)])
+def test_persistent_chunk_backward_equals_per_row_runs(B, T, Hk, Hv, D):
+    """With more chunk-heads than CUs the bf16 chunk backward runs persistent workgroups, each over a strided run of
+    chunk-heads whose reads are issued during the previous one's compute (rotating LDS arrays, the state registers
+    refilled early); one batch row alone has at most 256 chunk-heads and runs one chunk-head a workgroup.  Every row
+    is independent, so the batch run must equal the rows run one at a time bit for bit (ragged last chunks, grouped
+    value heads, D = 64 and 128)."""
+    _say(f"case persistent chunk backward B={B} T={T} Hk={Hk} Hv={Hv} D={D}")
+    inp = gdr.make_inputs(B, T, Hk, Hv, D, D, torch.bfloat16, s0=True, seed=21)
+    o, sT, g = run_dropin(inp, dsT=None)
+    for b in range(B):
+        row = {n: (None if x is None else x[b:b + 1]) for n, x in inp.items()}
+        ob, sTb, gb = run_dropin(row, dsT=None)
+        assert torch.equal(o[b:b + 1], ob) and torch.equal(sT[b:b + 1], sTb), b
+        for n in NAMES:
+            assert torch.equal(g[n][b:b + 1], gb[n]), (b, n)
+
+
 def test_value_split_changes_no_bits():
     """Splitting a head-row's value columns over 1, 2, 4 or 8 workgroups changes no arithmetic: identical bits
     (reference test_chunking.py:108-128)."""
