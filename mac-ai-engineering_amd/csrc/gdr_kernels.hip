@@ -2086,8 +2086,8 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
   int t0, T;                               // the chunk's first token; T: its sequence's end (the bound for its rows)
   chunk_span<true>(a.pack, NT, c, a.T, t0, T);   // through the scalar cache: no wait on copies in flight
   const int nrows = (T - t0 < C) ? T - t0 : C;
-  // The lane and wave numbers pass through empty assembly: a workgroup running two chunk-heads then forms the second
-  // one's lane-dependent offsets afresh instead of keeping the first one's live across it (which spills).
+  // The lane and wave numbers pass through empty assembly: a workgroup running several chunk-heads then forms each
+  // one's lane-dependent offsets afresh instead of keeping the previous one's live across it (which spills).
   int l = lane_id(), w = __builtin_amdgcn_readfirstlane(wave_id());
   asm volatile("" : "+v"(l));
   asm volatile("" : "+s"(w));
@@ -2708,7 +2708,6 @@ __global__ void __launch_bounds__(512) chunk_bwd8_kernel(ChunkBwdArgs a) {
 template <int D>
 __global__ void __launch_bounds__(512) chunk_bwd8xn_kernel(ChunkBwdArgs a, int units) {
   CB8_LDS(D, D)
-  cb8_stagger(a.stagger, blockIdx.x);
   Frag<float> s32[D / 32], sD[D / 32];
   float gv, bv;
   bf16 *tO = L.R1, *tVn = L.R2, *sdW = L.R7;
