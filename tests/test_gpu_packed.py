@@ -50,6 +50,8 @@ def _run(row, s0, dsT, cu=None):
     ([1, 63, 65, 128], 1, 3, 64, 64, torch.bfloat16),
     ([77, 150], 2, 4, 128, 64, torch.bfloat16),
     ([40, 0, 90], 2, 2, 64, 128, torch.float32),
+    # 51 chunks x 16 heads: more chunk-heads than CUs, so the persistent chunk backward runs over packed chunks
+    ([1000, 0, 700, 65, 1300, 3], 16, 16, 128, 128, torch.bfloat16),
 ])
 def test_packed_rows_equal_separate_sequences(lens, Hk, Hv, DK, DV, dtype):
     _say("case", lens, Hk, Hv, DK, DV, dtype)
