@@ -305,10 +305,11 @@ __device__ __forceinline__ void row_rnorms_lds(float* out, const bf16* tile, int
     float ss = 0.f;
 #pragma unroll
     for (int st = 0; st < D / 32; ++st) {
-      const bf16x8 x8 = *reinterpret_cast<const bf16x8*>(p + 32 * st);
+      // two 8-byte reads (rows need only be 8-byte aligned), the same summation order
+      const bf16x4 x0 = *reinterpret_cast<const bf16x4*>(p + 32 * st), x1 = *reinterpret_cast<const bf16x4*>(p + 32 * st + 4);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float v = (float)x8[i];
+        const float v = (float)(i < 4 ? x0[i] : x1[i - 4]);
         ss = fmaf(v, v, ss);
       }
     }

@@ -2010,24 +2010,24 @@ struct Cb8Lds {
   float (*rowdot)[C];                      // the prologue's row dots of dq and dk, summed over key blocks
 };
 #define CB8_LDS(DK, DV)                                                                                              \
-  constexpr int CB8_KP = (DK) + 8, CB8_CP = C + 8;                                                                   \
-  constexpr int CB8_VE = Tile<bf16, C, (DV)>::ELEMS > C * CB8_KP ? Tile<bf16, C, (DV)>::ELEMS : C * CB8_KP;          \
-  __shared__ __attribute__((aligned(16))) bf16 cb8_R1[Tile<bf16, C, (DV)>::ELEMS];                                   \
-  __shared__ __attribute__((aligned(16))) bf16 cb8_R2[Tile<bf16, C, (DV)>::ELEMS];                                   \
-  __shared__ __attribute__((aligned(16))) bf16 cb8_R3[Tile<bf16, C, (DV)>::ELEMS];                                   \
+  constexpr int CB8_KP = (DK) + 12, CB8_CP = C + 8;                                                                  \
+  constexpr int CB8_VE = RowTile<C, (DV)>::ELEMS > C * CB8_KP ? RowTile<C, (DV)>::ELEMS : C * CB8_KP;              \
+  __shared__ __attribute__((aligned(16))) bf16 cb8_R1[CB8_VE];                                                       \
+  __shared__ __attribute__((aligned(16))) bf16 cb8_R2[CB8_VE];                                                       \
+  __shared__ __attribute__((aligned(16))) bf16 cb8_R3[RowTile<C, (DV)>::ELEMS];                                      \
   __shared__ __attribute__((aligned(16))) bf16 cb8_R7[CB8_VE];                                                       \
-  __shared__ __attribute__((aligned(16))) bf16 cb8_t2[2 * Tile<bf16, C, (DK)>::ELEMS + Tile<bf16, C, C>::ELEMS];     \
+  __shared__ __attribute__((aligned(16))) bf16 cb8_t2[2 * RegRowTile<C, (DK)>::ELEMS + Tile<bf16, C, C>::ELEMS];    \
   __shared__ __attribute__((aligned(16))) bf16 cb8_mk[C * CB8_CP];                                                   \
   __shared__ __attribute__((aligned(16))) bf16 cb8_mq[C * CB8_CP];                                                   \
   __shared__ __attribute__((aligned(16))) bf16 cb8_az[C * CB8_CP];                                                   \
   __shared__ ChunkScalars cb8_cs;                                                                                    \
   __shared__ __attribute__((aligned(16))) float cb8_rk[C], cb8_rq[C];                                                \
   __shared__ float cb8_part[NPART][8][C];                                                                            \
-  __shared__ float cb8_colp[2][2][C];                                                                                \
   __shared__ float cb8_partS[8];                                                                                     \
-  __shared__ __attribute__((aligned(16))) float cb8_rowdot[2][C];                                                    \
+  /* colp and rowdot live in the partial rows that P_R1 and P_R2 leave unused (those take column blocks 0-3) */     \
   const Cb8Lds L{cb8_R1, cb8_R2, cb8_R3, cb8_R7, cb8_t2, cb8_mk, cb8_mq, cb8_az, &cb8_cs, cb8_rk, cb8_rq, cb8_part,   \
-                 cb8_colp, cb8_partS, cb8_rowdot};
+                 reinterpret_cast<float(*)[2][C]>(&cb8_part[P_R1][4][0]), cb8_partS,                                 \
+                 reinterpret_cast<float(*)[C]>(&cb8_part[P_R2][4][0])};
 
 // A chunk-head's place in a flat order of (chunk, head, batch row), chunks fastest
 __device__ __forceinline__ void cb8_unit(int u, int NT, int H, int& c, int& h, int& b) {
@@ -2065,9 +2065,9 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
   using MT = bf16;
   constexpr int NW = 8;
   constexpr int NBD = DK / 16, NBV = DV / 16;   // feature blocks (<= NW)
-  constexpr int KP = DK + 8, CP = C + 8;
-  using GQ = Tile<MT, C, DK>;
-  using GV = Tile<MT, C, DV>;
+  constexpr int KP = DK + 12, CP = C + 8;
+  using GQ = RegRowTile<C, DK>;            // q, k: through registers at a conflict-free pitch
+  using GV = RowTile<C, DV>;               // dO (then v), Vn (then dv), dVn: row copies at a conflict-free pitch
   using GA = Tile<MT, C, C>;
   static_assert(GQ::PITCH == KP && GA::PITCH == CP && NBD <= NW && NBV <= NW, "chunk_bwd8 tiling");
   constexpr int VP = GV::PITCH;
@@ -2130,9 +2130,9 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
       gv = a.g[o];
       bv = a.beta[o];
     }
-    GV::template dma_exact_opaque<NW>(tO, dO + (size_t)t0 * v_pitch, v_pitch, w, nrows, l);
-    GV::template dma_exact_opaque<NW>(tVn, Vnc, DV, w, C, l);
-    GV::template dma_exact_opaque<NW>(tdV, dVc, DV, w, C, l);
+    GV::template dma_rows_opaque<NW>(tO, dO + (size_t)t0 * v_pitch, v_pitch, w, nrows, l);
+    GV::template dma_rows_opaque<NW>(tVn, Vnc, DV, w, C, l);
+    GV::template dma_rows_opaque<NW>(tdV, dVc, DV, w, C, l);
     __builtin_amdgcn_sched_barrier(0);    // the state loads stay behind the copies (the partial wait below counts on it)
     if (holds) {
 #pragma unroll
@@ -2151,7 +2151,7 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
   // Group 2 -- the v fragments and the q, k, A tile units -- goes through registers. Its loads are spread over the
   // state products' stages below: an issue stalls while the memory system is saturated, so issuing them all here
   // would hold the products back. The tile units are written to LDS after the products.
-  constexpr int NQ = GQ::per_wave(NW), NA = GA::per_wave(NW);
+  constexpr int NQ = GQ::rows_per_wave(NW), NA = GA::per_wave(NW);
   constexpr int NG2 = DV / 32 + 2 * NQ + NA;                   // load slots: v fragments, q units, k units, A units
   Frag<MT> vf[DV / 32];                   // v rows of column block cb (B operand of dVn V^T)
   u32x4 uq[NQ], uk[NQ], ua[NA];
@@ -2162,9 +2162,10 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
       const bf16x4 lo = *reinterpret_cast<const bf16x4*>(pv + 32 * sl), hi = *reinterpret_cast<const bf16x4*>(pv + 32 * sl + 16);
       vf[sl].v = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     } else if (sl < DV / 32 + NQ) {
-      uq[sl - DV / 32] = GQ::template load_unit<NW>(q + (size_t)t0 * qk_pitch, qk_pitch, w, sl - DV / 32, nrows, l);
+      uq[sl - DV / 32] = GQ::template load_row_unit<NW>(q + (size_t)t0 * qk_pitch, qk_pitch, w, sl - DV / 32, nrows, l);
     } else if (sl < DV / 32 + 2 * NQ) {
-      uk[sl - DV / 32 - NQ] = GQ::template load_unit<NW>(k + (size_t)t0 * qk_pitch, qk_pitch, w, sl - DV / 32 - NQ, nrows, l);
+      uk[sl - DV / 32 - NQ] = GQ::template load_row_unit<NW>(k + (size_t)t0 * qk_pitch, qk_pitch, w, sl - DV / 32 - NQ, nrows,
+                                                             l);
     } else if (sl < NG2) {
       ua[sl - DV / 32 - 2 * NQ] = GA::template load_unit<NW>(Ac, C, w, sl - DV / 32 - 2 * NQ, C, l);
     }
@@ -2183,10 +2184,10 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
   };
   lds_barrier();                         // the group-1 tiles and the chunk scalars visible
   if (nrows < C) {                         // rows past the end: zeros in dO
-    constexpr int UV = VP / 8;
+    constexpr int UV = VP / 4;             // 8-byte units (rows are 8-byte aligned)
     const int nz = C - nrows;
     for (int i = tid; i < nz * UV; i += 64 * NW)
-      *reinterpret_cast<bf16x8*>(tO + (nrows + i % nz) * VP + 8 * (i / nz)) = bf16x8{};
+      *reinterpret_cast<bf16x4*>(tO + (nrows + i % nz) * VP + 4 * (i / nz)) = bf16x4{};
     lds_barrier();
   }
 
@@ -2235,8 +2236,8 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
   wait_dma();                              // group 2 is in registers
 #pragma unroll
   for (int u = 0; u < NQ; ++u) {
-    GQ::template store_unit<NW>(tq, w, u, uq[u], l);
-    GQ::template store_unit<NW>(tk, w, u, uk[u], l);
+    GQ::template store_row_unit<NW>(tq, w, u, uq[u], l);
+    GQ::template store_row_unit<NW>(tk, w, u, uk[u], l);
   }
 #pragma unroll
   for (int u = 0; u < NA; ++u) GA::template store_unit<NW>(tA, w, u, ua[u], l);
@@ -2246,11 +2247,11 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
     for (int kb = 0; kb < DV / 32; ++kb) vf[kb].v = bf16x8{};
   }
   if (nrows < C) {                         // rows past the end: zeros in q and k (the norms read rows < nrows only)
-    constexpr int UQ = KP / 8;
+    constexpr int UQ = KP / 4;             // 8-byte units (rows are 8-byte aligned)
     const int nz = C - nrows;
     for (int i = tid; i < nz * 2 * UQ; i += 64 * NW) {
       const int row = nrows + i % nz, u = i / nz;
-      *reinterpret_cast<bf16x8*>(u < UQ ? tq + row * KP + 8 * u : tk + row * KP + 8 * (u - UQ)) = bf16x8{};
+      *reinterpret_cast<bf16x4*>(u < UQ ? tq + row * KP + 4 * u : tk + row * KP + 4 * (u - UQ)) = bf16x4{};
     }
   }
   if (a.l2norm) {                          // the row norms from the tiles (rows past the end: 0)
@@ -2404,7 +2405,7 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
   lds_barrier();
   // dO is consumed: v takes its tile (needed from E on).  The copies are hidden from the compiler (dma_exact_opaque), so
   // it does not make the LDS reads of the next phases wait for them; the waits below are explicit.
-  GV::template dma_exact_opaque<NW>(tO, v + (size_t)t0 * v_pitch, v_pitch, w, nrows, l);
+  GV::template dma_rows_opaque<NW>(tO, v + (size_t)t0 * v_pitch, v_pitch, w, nrows, l);
   // The next chunk-head's reads, spread over the phases up to G: a wave's vector-memory issue stalls while the memory
   // system is saturated, so issued at once they would hold this chunk-head's compute back.  Its dO goes into dW's
   // array (consumed by C) now, its chunk states into s32 / sD (dead since B) a value block at a time in T1, dL and D,
@@ -2429,7 +2430,7 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
       nv_base = ((size_t)nb * a.T * H + nh) * DV;
       ns_base = (size_t)nb * a.T * H + nh;
       nbhc = ((size_t)nb * H + nh) * NT + nc;
-      GV::template dma_exact_opaque<NW>(sdW, (const MT*)a.dO + nv_base + (size_t)nt0 * v_pitch, v_pitch, w, nrows_n, l);
+      GV::template dma_rows_opaque<NW>(sdW, (const MT*)a.dO + nv_base + (size_t)nt0 * v_pitch, v_pitch, w, nrows_n, l);
       nS = a.Sc + nbhc * DK * DV;
       ndS = a.dSn + nbhc * DK * DV;
       __builtin_amdgcn_sched_barrier(0);
@@ -2558,8 +2559,8 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
     }
   }
   if (pf) {                                // v (the next chunk-head's dO copies and states may be in flight)
-    if (holds) wait_vmcnt<GV::per_wave(NW) + NSTATE>();
-    else wait_vmcnt<GV::per_wave(NW)>();
+    if (holds) wait_vmcnt<GV::rows_per_wave(NW) + NSTATE>();
+    else wait_vmcnt<GV::rows_per_wave(NW)>();
   } else {
     wait_dma();                            // v
   }
@@ -2620,10 +2621,10 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
     }
   }
   if (pf)                                  // v's array is free since E: the next chunk-head's Vn
-    GV::template dma_exact_opaque<NW>(tO, (const MT*)a.Vn + nbhc * C * DV, DV, w, C, l);
+    GV::template dma_rows_opaque<NW>(tO, (const MT*)a.Vn + nbhc * C * DV, DV, w, C, l);
   lds_barrier();                         // q and k tiles are read: they become the dq and dk staging
   if (pf) {                                // the next chunk-head's dVn into dVn's array (free since E), its g and beta
-    GV::template dma_exact_opaque<NW>(L.R3, (const MT*)a.dVn + nbhc * C * DV, DV, w, C, l);
+    GV::template dma_rows_opaque<NW>(L.R3, (const MT*)a.dVn + nbhc * C * DV, DV, w, C, l);
     const size_t o = ns_base + (size_t)(nt0 + l < nT ? nt0 + l : nT - 1) * H;
     gv = a.g[o];
     bv = a.beta[o];
@@ -2650,12 +2651,18 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
     MT* dv = (MT*)a.dv + v_base + (size_t)t0 * v_pitch;
     for (int i = wt; i < nrows * UK; i += NTH) {
       const int row = i / UK, u = i - row * UK;
-      *reinterpret_cast<bf16x8*>(dq + row * dqk_pitch + 8 * u) = *reinterpret_cast<const bf16x8*>(tq + row * KP + 8 * u);
-      *reinterpret_cast<bf16x8*>(dk + row * dqk_pitch + 8 * u) = *reinterpret_cast<const bf16x8*>(tk + row * KP + 8 * u);
+      const bf16x4 q0 = *reinterpret_cast<const bf16x4*>(tq + row * KP + 8 * u),   // rows are 8-byte aligned
+                   q1 = *reinterpret_cast<const bf16x4*>(tq + row * KP + 8 * u + 4),
+                   k0 = *reinterpret_cast<const bf16x4*>(tk + row * KP + 8 * u),
+                   k1 = *reinterpret_cast<const bf16x4*>(tk + row * KP + 8 * u + 4);
+      *reinterpret_cast<bf16x8*>(dq + row * dqk_pitch + 8 * u) = bf16x8{q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
+      *reinterpret_cast<bf16x8*>(dk + row * dqk_pitch + 8 * u) = bf16x8{k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
     }
     for (int i = wt; i < nrows * UV; i += NTH) {
       const int row = i / UV, u = i - row * UV;
-      *reinterpret_cast<bf16x8*>(dv + row * v_pitch + 8 * u) = *reinterpret_cast<const bf16x8*>(tVn + row * VP + 8 * u);
+      const bf16x4 lo = *reinterpret_cast<const bf16x4*>(tVn + row * VP + 8 * u),   // rows are 8-byte aligned
+                   hi = *reinterpret_cast<const bf16x4*>(tVn + row * VP + 8 * u + 4);
+      *reinterpret_cast<bf16x8*>(dv + row * v_pitch + 8 * u) = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
   }
 

@@ -171,6 +171,65 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// A bf16 tile of R rows copied one row per wave instruction, 4 bytes a lane (buffer_load_dword ... lds, lane l
+// writes dword l of the row), so its row pitch need only be a multiple of 4 bytes: COLS + 12 elements, an odd
+// number of 8-byte units.  At that pitch both the fragment reads (16 rows at one column, 8 bytes a lane) and the
+// transpose reads are free of bank conflicts; a pitch of whole 16-byte units (what a 16-byte copy needs) halves the
+// fragment reads (measured on gfx950 at 128 columns: 135 B/clk a CU at pitch 140, 72 at 136, 36 at 144).  The copies
+// are issued through inline assembly, unseen by the compiler (see Tile::dma_exact_opaque): the caller waits.
+template <int R, int COLS>
+struct RowTile {
+  static constexpr int PITCH = COLS + 12;
+  static constexpr int ELEMS = R * PITCH;
+  static constexpr int rows_per_wave(int nw) { return (R + nw - 1) / nw; }
+  template <int NW>
+  __device__ static __forceinline__ void dma_rows_opaque(bf16* base, const bf16* g, size_t gpitch, int w, int nrows,
+                                                         int l) {
+    static_assert(COLS % 2 == 0 && COLS / 2 <= 64 && R % NW == 0, "one row of at most 64 dwords a wave instruction");
+    const unsigned long long ga = (unsigned long long)(const void*)g;
+    const u32x4 rs = {(unsigned)__builtin_amdgcn_readfirstlane((unsigned)ga),
+                      (unsigned)__builtin_amdgcn_readfirstlane((unsigned)(ga >> 32) & 0xffffu), 0x7fffffffu, 0x00020000u};
+    const unsigned lds0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(lds_void*)base);
+    const bool active = COLS / 2 == 64 || l < COLS / 2;
+#pragma unroll
+    for (int k = 0; k < R / NW; ++k) {
+      const int row = w + k * NW;
+      const int off = (int)(((size_t)(row < nrows ? row : nrows - 1) * gpitch + 2 * l) * sizeof(bf16));
+      const unsigned lds = lds0 + (unsigned)(row * PITCH * (int)sizeof(bf16));
+      if (active)
+        asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds" : : "v"(off), "s"(rs), "{m0}"(lds) : "memory");
+    }
+  }
+};
+
+// A bf16 tile staged through registers at the same conflict-free pitch as RowTile (COLS + 12): lane l of a wave
+// instruction takes 16-byte unit l % PU (PU = COLS / 8) of row l / PU of its 64 / PU rows, and writes it to LDS as two
+// 8-byte halves (rows are 8-byte aligned).  Rows past nrows re-read row nrows - 1 (masked by the reader).
+template <int R, int COLS>
+struct RegRowTile {
+  static constexpr int PITCH = COLS + 12;
+  static constexpr int ELEMS = R * PITCH;
+  static constexpr int PU = COLS / 8;
+  static constexpr int RI = 64 / PU;
+  static constexpr int NRI = R / RI;
+  static constexpr int rows_per_wave(int nw) { return (NRI + nw - 1) / nw; }
+  template <int NW>
+  __device__ static __forceinline__ u32x4 load_row_unit(const bf16* g, size_t gpitch, int w, int k, int nrows, int l) {
+    static_assert((PU & (PU - 1)) == 0 && PU <= 64 && R % RI == 0, "row units: PU a power of two");
+    const int i = w + k * NW < NRI ? w + k * NW : NRI - 1;
+    const int row = i * RI + l / PU, cu = l % PU;
+    return *reinterpret_cast<const u32x4*>(g + (size_t)(row < nrows ? row : nrows - 1) * gpitch + cu * 8);
+  }
+  template <int NW>
+  __device__ static __forceinline__ void store_row_unit(bf16* base, int w, int k, u32x4 x, int l) {
+    const int i = w + k * NW < NRI ? w + k * NW : NRI - 1;
+    unsigned* p = reinterpret_cast<unsigned*>(base + (i * RI + l / PU) * PITCH + (l % PU) * 8);
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    reinterpret_cast<u32x2*>(p)[0] = u32x2{x[0], x[1]};
+    reinterpret_cast<u32x2*>(p)[1] = u32x2{x[2], x[3]};
+  }
+};
+
 // ---- gfx950 LDS transpose reads (ds_read_b64_tr_b16) ---------------------------------------------------------------
 // In each 16-lane group, lane s supplies the address of 4 consecutive 16-bit elements; lane i receives element i % 4 of
 // the 4 elements supplied by lanes 4e + i / 4, e = 0..3 (its result element e).  So if lane s points at
