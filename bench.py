@@ -37,11 +37,11 @@ C = 64
 # WRITE_SIZE x 1.000.  Keyed by the config and the mode the profile ran, and stamped with the fingerprint of the
 # kernel sources it was taken on: measured_traffic() reports the figures only while the sources still match.
 TRAFFIC = {
-    (1, "recompute"): {"sources": "e70d110566989112", "bytes": {
-        "prep_fwd": 143406401, "state_fwd_out": 110201201, "prep_bwd": 151793070, "state_pair": 313866055,
-        "chunk_bwd": 295324012}},
-    (1, "stored"): {"sources": "e70d110566989112", "bytes": {
-        "prep_fwd": 151804877, "state_fwd_out": 193149279, "state_bwd": 164420144, "chunk_bwd": 295242414}},
+    (1, "recompute"): {"sources": "de213cd85adaf271", "bytes": {
+        "prep_fwd": 143415355, "state_fwd_out": 110180466, "prep_bwd": 151793468, "state_pair": 314072649,
+        "chunk_bwd": 295093771}},
+    (1, "stored"): {"sources": "de213cd85adaf271", "bytes": {
+        "prep_fwd": 151803701, "state_fwd_out": 193183656, "state_bwd": 164437271, "chunk_bwd": 295094526}},
 }
 KERNEL_SOURCES = ("gdr_kernels.hip", "gdr_common.h", "gdr_lds.h", "gdr_stage.h")
 
