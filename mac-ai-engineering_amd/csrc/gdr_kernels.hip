@@ -2010,7 +2010,7 @@ struct Cb8Lds {
   float (*rowdot)[C];                      // the prologue's row dots of dq and dk, summed over key blocks
 };
 #define CB8_LDS(DK, DV)                                                                                              \
-  constexpr int CB8_KP = (DK) + 12, CB8_CP = C + 8;                                                                  \
+  constexpr int CB8_KP = (DK) + 12, CB8_CP = C + 4;                                                                  \
   constexpr int CB8_VE = RowTile<C, (DV)>::ELEMS > C * CB8_KP ? RowTile<C, (DV)>::ELEMS : C * CB8_KP;              \
   __shared__ __attribute__((aligned(16))) bf16 cb8_R1[CB8_VE];                                                       \
   __shared__ __attribute__((aligned(16))) bf16 cb8_R2[CB8_VE];                                                       \
@@ -2065,7 +2065,9 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
   using MT = bf16;
   constexpr int NW = 8;
   constexpr int NBD = DK / 16, NBV = DV / 16;   // feature blocks (<= NW)
-  constexpr int KP = DK + 12, CP = C + 8;
+  // CQ: the C x C tiles formed here (8-byte stores, any pitch) at 136 bytes a row, where both their fragment and
+  // their transpose reads are free of LDS bank conflicts (at 144, A's pitch, fragment reads run at half rate)
+  constexpr int KP = DK + 12, CP = C + 8, CQ = C + 4;
   using GQ = RegRowTile<C, DK>;            // q, k: through registers at a conflict-free pitch
   using GV = RowTile<C, DV>;               // dO (then v), Vn (then dv), dVn: row copies at a conflict-free pitch
   using GA = Tile<MT, C, C>;
@@ -2390,9 +2392,9 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
         da[r] = (row > s) ? fmaf(Ta[i][r] * rks, bgs, Tb[i][r] * bs) : 0.f;
         KG[i][r] = (row > s) ? KK[i][r] * (rk4[r] * rks) * gm : 0.f;
       }
-      *reinterpret_cast<bf16x4*>(sMkT + s * CP + r0) = bf16x4{(bf16)mk[0], (bf16)mk[1], (bf16)mk[2], (bf16)mk[3]};
-      *reinterpret_cast<bf16x4*>(sMqT + s * CP + r0) = bf16x4{(bf16)mq[0], (bf16)mq[1], (bf16)mq[2], (bf16)mq[3]};
-      *reinterpret_cast<bf16x4*>(sAZ + s * CP + r0) = bf16x4{(bf16)da[0], (bf16)da[1], (bf16)da[2], (bf16)da[3]};
+      *reinterpret_cast<bf16x4*>(sMkT + s * CQ + r0) = bf16x4{(bf16)mk[0], (bf16)mk[1], (bf16)mk[2], (bf16)mk[3]};
+      *reinterpret_cast<bf16x4*>(sMqT + s * CQ + r0) = bf16x4{(bf16)mq[0], (bf16)mq[1], (bf16)mq[2], (bf16)mq[3]};
+      *reinterpret_cast<bf16x4*>(sAZ + s * CQ + r0) = bf16x4{(bf16)da[0], (bf16)da[1], (bf16)da[2], (bf16)da[3]};
     }
     const float rs = group16_sum8(pR1, l);            // row (l % 16) / 2 of the 8: tile i = idx / 4, r = idx % 4
     if ((n & 1) == 0) {
@@ -2447,9 +2449,9 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
 #pragma unroll
     for (int p = 0; p < 2; ++p) bA[p] = frag_tile<MT, GA>(tA, 16 * cb, 32 * p, l);   // B[s][t'] = A[t'][s]
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) fz[mi] = frag_tr(sAZ, CP, 0, 16 * mi, l);
-    fz[4] = frag_tr(sAZ, CP, 32, 32, l);
-    fz[5] = frag_tr(sAZ, CP, 32, 48, l);
+    for (int mi = 0; mi < 4; ++mi) fz[mi] = frag_tr(sAZ, CQ, 0, 16 * mi, l);
+    fz[4] = frag_tr(sAZ, CQ, 32, 32, l);
+    fz[5] = frag_tr(sAZ, CQ, 32, 48, l);
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) mma(T1[mi], fz[mi], bA[0]);
     mma(T1[2], fz[4], bA[1]);              // dA is strictly lower: rows 0-31 have no terms at t' >= 32
@@ -2486,17 +2488,17 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
         zt[r] = z * rk4[r];
         if (mi == cb) {                              // diagonal tile: element by element
           if (row > s) {
-            sAZ[s * CP + row] = (bf16)zt[r];
-            sAZ[row * CP + s] = (bf16)(z * rks);
+            sAZ[s * CQ + row] = (bf16)zt[r];
+            sAZ[row * CQ + s] = (bf16)(z * rks);
           } else if (row == s) {
-            sAZ[s * CP + row] = (bf16)0.f;
+            sAZ[s * CQ + row] = (bf16)0.f;
           }
         } else if (mi > cb) {
-          sAZ[row * CP + s] = (bf16)(z * rks);
+          sAZ[row * CQ + s] = (bf16)(z * rks);
         }
       }
       if (mi > cb)
-        *reinterpret_cast<bf16x4*>(sAZ + s * CP + r0) = bf16x4{(bf16)zt[0], (bf16)zt[1], (bf16)zt[2], (bf16)zt[3]};
+        *reinterpret_cast<bf16x4*>(sAZ + s * CQ + r0) = bf16x4{(bf16)zt[0], (bf16)zt[1], (bf16)zt[2], (bf16)zt[3]};
     }
     pf_state(1);
     const float rs = group16_sum8(pR2, l);
@@ -2522,9 +2524,9 @@ __device__ __forceinline__ void chunk_bwd8_body(const ChunkBwdArgs& a, const Cb8
     auto load = [&](int ti, Frag<MT>(&f)[6]) {
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        if (32 * p <= 16 * ti + 15) f[3 * p] = frag_tr(sMkT, CP, 32 * p, 16 * ti, l);
-        if (32 * p + 31 >= 16 * ti) f[3 * p + 1] = frag_k_raw(sMqT, CP, 16 * ti, 32 * p, l);
-        f[3 * p + 2] = frag_k_raw(sAZ, CP, 16 * ti, 32 * p, l);
+        if (32 * p <= 16 * ti + 15) f[3 * p] = frag_tr(sMkT, CQ, 32 * p, 16 * ti, l);
+        if (32 * p + 31 >= 16 * ti) f[3 * p + 1] = frag_k_raw(sMqT, CQ, 16 * ti, 32 * p, l);
+        f[3 * p + 2] = frag_k_raw(sAZ, CQ, 16 * ti, 32 * p, l);
       }
     };
     load(0, st[0]);
