@@ -13,7 +13,13 @@ namespace gdr {
 typedef __attribute__((address_space(3))) void lds_void;
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
-template <typename T, int R, int COLS>
+// SW (bf16 tiles of whole 128-byte row blocks): odd rows hold the two 64-byte halves of every 128-byte block swapped --
+// LDS unit u of row r holds the row's unit u ^ (4 (r & 1)).  A row pitch of whole 16-byte units puts the 16 rows of a
+// fragment read two to a bank group; with the swap the 8-byte fragment reads run conflict-free (measured on gfx950:
+// 142-144 against 70-72 bytes a clock a CU at 272- and 144-byte pitches; transpose reads 126-128 against 131-134).
+// Swapping single 16-byte units instead measured as fast in LDS but made the copies slow: each 64-byte run of the
+// copy's lanes must stay in address order.  The readers (frag_tile, frag_tile_tr) take the swap from the layout.
+template <typename T, int R, int COLS, bool SW = false>
 struct Tile {
   static constexpr int EPU = 16 / (int)sizeof(T);        // elements per 16-byte unit
   static constexpr int PU = COLS / EPU;                   // data units per row
@@ -21,9 +27,16 @@ struct Tile {
   static constexpr int PITCH = RU * EPU;                  // row pitch in elements
   static constexpr int NI = (R * RU + 63) / 64;           // wave instructions to copy the tile
   static constexpr int ELEMS = NI * 64 * EPU;             // LDS footprint in elements
+  static constexpr bool SWZ = SW;
   static_assert(COLS % EPU == 0, "tile rows must be whole 16-byte units");
+  static constexpr int SWK = SW ? 4 : 0;                 // odd rows: LDS unit u holds the row's unit u ^ SWK
+  static_assert(!SW || (sizeof(T) == 2 && PU % 8 == 0), "unit swap: bf16 rows of whole 128-byte blocks");
 
-  __device__ static __forceinline__ int offset(int row, int col) { return row * PITCH + col; }
+  // the row's data unit that LDS unit cu (< PU) of row `row` holds
+  __device__ static __forceinline__ int src_unit(int row, int cu) { return cu ^ (SWK * (row & 1)); }
+  __device__ static __forceinline__ int offset(int row, int col) {
+    return row * PITCH + src_unit(row, col / EPU) * EPU + col % EPU;
+  }
   static constexpr int per_wave(int nw) { return (NI + nw - 1) / nw; }
 
   // The element offsets (from the tile's global base, row pitch gpitch) that this lane copies in the wave's
@@ -35,7 +48,7 @@ struct Tile {
     for (int k = 0; k < per_wave(NW); ++k) {
       const int i = w + k * NW;
       const int u = i * 64 + l, row = u / RU, cu = u - row * RU;
-      off[k] = (i < NI && row < R && cu < PU) ? row * gpitch + cu * EPU : 0;
+      off[k] = (i < NI && row < R && cu < PU) ? row * gpitch + src_unit(row, cu) * EPU : 0;
     }
   }
   template <int NW>
@@ -63,7 +76,7 @@ struct Tile {
       const int u = i * 64 + l;
       const int row = u / RU, cu = u - row * RU;
       int off = 0;
-      if (row < R && cu < PU) off = (int)(((size_t)(row < nrows ? row : nrows - 1) * gpitch + cu * EPU) * sizeof(T));
+      if (row < R && cu < PU) off = (int)(((size_t)(row < nrows ? row : nrows - 1) * gpitch + src_unit(row, cu) * EPU) * sizeof(T));
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(base + i * 64 * EPU), 16, off, 0, 0, 0);
     }
   }
@@ -83,7 +96,7 @@ struct Tile {
       const int u = i * 64 + l;
       const int row = u / RU, cu = u - row * RU;
       int off = 0;
-      if (row < R && cu < PU) off = (int)(((size_t)(row < nrows ? row : nrows - 1) * gpitch + cu * EPU) * sizeof(T));
+      if (row < R && cu < PU) off = (int)(((size_t)(row < nrows ? row : nrows - 1) * gpitch + src_unit(row, cu) * EPU) * sizeof(T));
       const unsigned lds = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(lds_void*)(base + i * 64 * EPU));
       // s_nop: one wait state between an SALU write of M0 and an LDS-DMA read of it
       asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(off), "s"(rs), "{m0}"(lds) : "memory");
@@ -100,7 +113,7 @@ struct Tile {
     const int u = i * 64 + l;
     const int row = u / RU, cu = u - row * RU;
     const T* src = g;
-    if (row < R && cu < PU) src = g + (size_t)(row < nrows ? row : nrows - 1) * gpitch + cu * EPU;
+    if (row < R && cu < PU) src = g + (size_t)(row < nrows ? row : nrows - 1) * gpitch + src_unit(row, cu) * EPU;
     return *reinterpret_cast<const u32x4*>(src);
   }
   template <int NW>
@@ -116,7 +129,7 @@ struct Tile {
       const int u = i * 64 + l;
       const int row = u / RU, cu = u - row * RU;
       const T* src = g;
-      if (row < R && cu < PU) src = g + (size_t)(row < nrows ? row : nrows - 1) * gpitch + cu * EPU;
+      if (row < R && cu < PU) src = g + (size_t)(row < nrows ? row : nrows - 1) * gpitch + src_unit(row, cu) * EPU;
       __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(base + i * 64 * EPU), 16, 0, 0);
     }
   }
@@ -127,6 +140,7 @@ struct Tile {
 template <typename T, int R, int COLS>
 struct Dense {
   static constexpr int PITCH = COLS;
+  static constexpr bool SWZ = false;
 };
 
 // Fragment (A operand rows, or B operand columns = rows of B^T) of a k-contiguous tile.
@@ -134,6 +148,14 @@ template <typename MT, typename G>
 __device__ __forceinline__ Frag<MT> frag_tile(const MT* base, int row0, int k0, int l = lane_id()) {
   const int j = l >> 4;
   const MT* p = base + (row0 + (l & 15)) * G::PITCH + k0 + 4 * j;
+  if constexpr (G::SWZ) {                  // the two 8-byte pieces from their swapped units
+    const int r = row0 + (l & 15);
+    Frag<MT> f;
+    const bf16x4 a = *reinterpret_cast<const bf16x4*>(base + G::offset(r, k0 + 4 * j)),
+                 b = *reinterpret_cast<const bf16x4*>(base + G::offset(r, k0 + 16 + 4 * j));
+    f.v = bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    return f;
+  }
   Frag<MT> f;
   if constexpr (sizeof(MT) == 2) {
     bf16x4 a = *reinterpret_cast<const bf16x4*>(p), b = *reinterpret_cast<const bf16x4*>(p + 16);
@@ -181,6 +203,7 @@ template <int R, int COLS>
 struct RowTile {
   static constexpr int PITCH = COLS + 12;
   static constexpr int ELEMS = R * PITCH;
+  static constexpr bool SWZ = false;
   static constexpr int rows_per_wave(int nw) { return (R + nw - 1) / nw; }
   template <int NW>
   __device__ static __forceinline__ void dma_rows_opaque(bf16* base, const bf16* g, size_t gpitch, int w, int nrows,
@@ -209,6 +232,7 @@ template <int R, int COLS>
 struct RegRowTile {
   static constexpr int PITCH = COLS + 12;
   static constexpr int ELEMS = R * PITCH;
+  static constexpr bool SWZ = false;
   static constexpr int PU = COLS / 8;
   static constexpr int RI = 64 / PU;
   static constexpr int NRI = R / RI;
@@ -249,11 +273,23 @@ __device__ __forceinline__ Frag<bf16> frag_tr(const bf16* X, int pitch, int k0, 
   f.v = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   return f;
 }
+// frag_tr over a tile with swapped units (Tile with SW; k0 even): rows k0 + 4 j + s / 4 and 16 below it have the
+// same parity, so both reads take the same swap
+template <typename G>
+__device__ __forceinline__ Frag<bf16> frag_tr_sw(const bf16* X, int k0, int n0, int l = lane_id()) {
+  const int j = l >> 4, s = l & 15;
+  const bf16* p = X + G::offset(k0 + 4 * j + (s >> 2), n0 + 4 * (s & 3));
+  const bf16x4 lo = read_tr(p), hi = read_tr(p + 16 * G::PITCH);
+  Frag<bf16> f;
+  f.v = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return f;
+}
 // The fragment of X^T for a row-major tile X of layout G: k over X's rows k0.., the lane's column n0 + l % 16.  LDS
 // transpose reads for bf16; element gathers for fp32 (no transpose read exists for 32-bit data).
 template <typename MT, typename G>
 __device__ __forceinline__ Frag<MT> frag_tile_tr(const MT* base, int k0, int n0) {
-  if constexpr (sizeof(MT) == 2) return frag_tr(base, G::PITCH, k0, n0);
+  if constexpr (G::SWZ) return frag_tr_sw<G>(base, k0, n0);
+  else if constexpr (sizeof(MT) == 2) return frag_tr(base, G::PITCH, k0, n0);
   else return frag_tile_rows<MT, G>(base, k0, n0 + (lane_id() & 15));
 }
 // The accumulator layout of a 16 x 16 block of a row-major bf16 matrix X: lane l gets X[r0 + 4j + e][c0 + l % 16],
