@@ -1011,60 +1011,138 @@ __global__ void __launch_bounds__(64 * (NW + 1)) state_fwd_kernel(StateFwdArgs a
   state_fwd_body<MT, DK, NW, OUT, STORE, MAP>(a, lds, blockIdx.x);
 }
 
-// The sequential composition of the segment maps of a row: starts[s] = the state entering segment s, starts[0] = s0
-// (zeros when null), starts[s + 1] = A_s starts[s] + B_s, maps[s] = [A_s | B_s] as the map pass writes them.  A
-// workgroup takes 16 value columns of a (row, head); the state slice [DK x 16] sits in LDS, and each step a lane forms
-// 8 columns of one state row, A's row read with 16-byte loads all in flight: the chain of steps is short (one per
-// segment) and latency-bound, so it is spread over a workgroup's lanes rather than one wave's MFMAs.
+// state_scan_kernel for DK <= 128 (see above).  A step is A_s [DK x DK] times the state slice [DK x 16] on fp32 MFMAs
+// (16x16x4): wave w forms row tiles w, w + 4 of the new slice, A's fragments from the LDS stage, the slice's from LDS
+// in fragment order (Sf[q][g][j][r] = S[16 q + 4 g + r][c0 + j], which is also where each row tile's accumulators go),
+// B_s's columns as the accumulators' start.  The products' k order: instruction (q, r) sums k = 16 q + 4 g + r over the
+// lane groups g.
 template <int DK>
-__global__ void __launch_bounds__(256) state_scan_kernel(const float* maps, const float* s0, float* starts, int nseg,
-                                                         int H, int DV) {
-  __shared__ __attribute__((aligned(16))) float Sl[DK * 16];
+__device__ __forceinline__ void state_scan_staged(const float* maps, const float* s0, float* starts, int nseg, int H,
+                                                  int DV) {
+  using GA = Tile<float, DK, DK>;          // A_s rows at a padded pitch (DK + 4 floats)
+  constexpr int NW = 4, NRT = DK / 16, TPW = (NRT + NW - 1) / NW;   // row tiles, per wave
+  __shared__ __attribute__((aligned(16))) float Sf[DK * 16];
+  __shared__ __attribute__((aligned(16))) float As[2][GA::ELEMS];
   const int h = blockIdx.y, r = blockIdx.z, c0 = blockIdx.x * 16;
   const int DVt = DK + DV;
+  const int l = lane_id(), w = wave_id(), g = l >> 4, j = l & 15;
+  auto sf_index = [](int d, int c) { return ((((d >> 4) * 4 + ((d & 15) >> 2)) * 16 + c) << 2) + (d & 3); };
+  auto map_of = [&](int sg) { return maps + (((size_t)r * nseg + sg) * H + h) * DK * DVt; };
+  f4 bn[TPW];                              // the next step's B_s[16 t + 4 g + 0..3][c0 + j] of this lane's row tiles
+  auto prefetch = [&](int sg) {            // A_sg into stage sg & 1 (asynchronous) and its B columns into bn
+    GA::template dma_exact_opaque<NW>(As[sg & 1], map_of(sg), DVt, w, DK, l);
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) {
+      const int t = min(w + NW * u, NRT - 1);
+      const float* Bc = map_of(sg) + (size_t)(16 * t + 4 * g) * DVt + DK + c0 + j;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bn[u][e] = Bc[(size_t)e * DVt];
+    }
+  };
   for (int i = threadIdx.x; i < DK * 16; i += 256) {
     const int d = i / 16, c = i % 16;
-    Sl[i] = s0 ? s0[((size_t)r * H + h) * DK * DV + (size_t)d * DV + c0 + c] : 0.f;
+    Sf[sf_index(d, c)] = s0 ? s0[((size_t)r * H + h) * DK * DV + (size_t)d * DV + c0 + c] : 0.f;
   }
+  if (nseg > 1) prefetch(0);
   __syncthreads();
   for (int sg = 0; sg < nseg; ++sg) {
     const size_t seg = (size_t)r * nseg + sg;
     float* out = starts + (seg * H + h) * DK * DV;
-    for (int i = threadIdx.x; i < DK * 16; i += 256) out[(size_t)(i / 16) * DV + c0 + i % 16] = Sl[i];
+    for (int i = threadIdx.x; i < DK * 16; i += 256) out[(size_t)(i / 16) * DV + c0 + i % 16] = Sf[sf_index(i / 16, i % 16)];
     if (sg + 1 == nseg) break;
-    const float* Mp = maps + (seg * H + h) * DK * DVt;
-    float acc[(2 * DK + 255) / 256][8];
+    f4 acc[TPW];
+    wait_vmcnt<0>();                       // A_sg and B_sg have landed (and this step's stores are out)
 #pragma unroll
-    for (int u = 0; u < (2 * DK + 255) / 256; ++u) {
-      const int pr = threadIdx.x + 256 * u, d = pr / 2, cg = (pr % 2) * 8;
-      if (pr >= 2 * DK) break;
-      const float* Ar = Mp + (size_t)d * DVt;
+    for (int u = 0; u < TPW; ++u) acc[u] = bn[u];
+    lds_barrier();                         // A_sg visible; every wave is past step sg - 1's reads of stage (sg + 1) & 1
+    if (sg + 2 < nseg) prefetch(sg + 1);   // A_{sg+1} lands while this step computes
+    const float* A = As[sg & 1];
+    f4 sfr[NRT];                           // the slice as B fragments: S[16 q + 4 g + e][c0 + j]
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[u][i] = Ar[DK + c0 + cg + i];           // B_s
-#pragma unroll 8
-      for (int k4 = 0; k4 < DK; k4 += 4) {
-        const f4 a = *reinterpret_cast<const f4*>(Ar + k4);                  // A_s[d][k4 .. k4 + 3]
+    for (int q = 0; q < NRT; ++q) sfr[q] = *reinterpret_cast<const f4*>(Sf + ((q * 4 + g) * 16 + j) * 4);
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          const f4 s_lo = *reinterpret_cast<const f4*>(Sl + (k4 + kk) * 16 + cg);
-          const f4 s_hi = *reinterpret_cast<const f4*>(Sl + (k4 + kk) * 16 + cg + 4);
+    for (int u = 0; u < TPW; ++u) {
+      const int t = w + NW * u;
+      if (t < NRT) {
+        const float* Ar = A + GA::offset(16 * t + j, 4 * g);   // A[16 t + j][16 q + 4 g + e] at Ar + 16 q + e
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            acc[u][i] = fmaf(a[kk], s_lo[i], acc[u][i]);
-            acc[u][4 + i] = fmaf(a[kk], s_hi[i], acc[u][4 + i]);
-          }
+        for (int q = 0; q < NRT; ++q) {
+          const f4 a = *reinterpret_cast<const f4*>(Ar + 16 * q);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], sfr[q][e], acc[u], 0, 0, 0);
         }
       }
     }
-    __syncthreads();                       // every lane has read this step's state
+    lds_barrier();                         // every lane has read this step's slice
 #pragma unroll
-    for (int u = 0; u < (2 * DK + 255) / 256; ++u) {
-      const int pr = threadIdx.x + 256 * u, d = pr / 2, cg = (pr % 2) * 8;
-      if (pr >= 2 * DK) break;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) Sl[d * 16 + cg + i] = acc[u][i];
+    for (int u = 0; u < TPW; ++u) {
+      const int t = w + NW * u;
+      if (t < NRT) *reinterpret_cast<f4*>(Sf + ((t * 4 + g) * 16 + j) * 4) = acc[u];
+    }
+    lds_barrier();
+  }
+}
+
+// The sequential composition of the segment maps of a row: starts[s] = the state entering segment s, starts[0] = s0
+// (zeros when null), starts[s + 1] = A_s starts[s] + B_s, maps[s] = [A_s | B_s] as the map pass writes them.  A
+// workgroup takes 16 value columns of a (row, head); the state slice [DK x 16] sits in LDS, and each step a lane forms
+// 8 columns of one state row.  The maps do not depend on the chain, so for DK <= 128 the next step's A (DK x DK fp32,
+// 64 KiB at 128) is copied into LDS (two stages, asynchronous, unseen by the compiler and waited for explicitly) and its
+// B columns into registers while this step computes: a step is then its FMAs only, not a 64 KiB read from memory
+// (10 us a step at config 3 before).  Wider keys read A's rows from memory, 16-byte loads all in flight.
+template <int DK>
+__global__ void __launch_bounds__(256) state_scan_kernel(const float* maps, const float* s0, float* starts, int nseg,
+                                                         int H, int DV) {
+  if constexpr (DK <= 128) {
+    state_scan_staged<DK>(maps, s0, starts, nseg, H, DV);
+  } else {
+    __shared__ __attribute__((aligned(16))) float Sl[DK * 16];
+    const int h = blockIdx.y, r = blockIdx.z, c0 = blockIdx.x * 16;
+    const int DVt = DK + DV;
+    for (int i = threadIdx.x; i < DK * 16; i += 256) {
+      const int d = i / 16, c = i % 16;
+      Sl[i] = s0 ? s0[((size_t)r * H + h) * DK * DV + (size_t)d * DV + c0 + c] : 0.f;
     }
     __syncthreads();
+    for (int sg = 0; sg < nseg; ++sg) {
+      const size_t seg = (size_t)r * nseg + sg;
+      float* out = starts + (seg * H + h) * DK * DV;
+      for (int i = threadIdx.x; i < DK * 16; i += 256) out[(size_t)(i / 16) * DV + c0 + i % 16] = Sl[i];
+      if (sg + 1 == nseg) break;
+      const float* Mp = maps + (seg * H + h) * DK * DVt;
+      float acc[(2 * DK + 255) / 256][8];
+#pragma unroll
+      for (int u = 0; u < (2 * DK + 255) / 256; ++u) {
+        const int pr = threadIdx.x + 256 * u, d = pr / 2, cg = (pr % 2) * 8;
+        if (pr >= 2 * DK) break;
+        const float* Ar = Mp + (size_t)d * DVt;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[u][i] = Ar[DK + c0 + cg + i];           // B_s
+#pragma unroll 8
+        for (int k4 = 0; k4 < DK; k4 += 4) {
+          const f4 a = *reinterpret_cast<const f4*>(Ar + k4);                  // A_s[d][k4 .. k4 + 3]
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) {
+            const f4 s_lo = *reinterpret_cast<const f4*>(Sl + (k4 + kk) * 16 + cg);
+            const f4 s_hi = *reinterpret_cast<const f4*>(Sl + (k4 + kk) * 16 + cg + 4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              acc[u][i] = fmaf(a[kk], s_lo[i], acc[u][i]);
+              acc[u][4 + i] = fmaf(a[kk], s_hi[i], acc[u][4 + i]);
+            }
+          }
+        }
+      }
+      __syncthreads();                       // every lane has read this step's state
+#pragma unroll
+      for (int u = 0; u < (2 * DK + 255) / 256; ++u) {
+        const int pr = threadIdx.x + 256 * u, d = pr / 2, cg = (pr % 2) * 8;
+        if (pr >= 2 * DK) break;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) Sl[d * 16 + cg + i] = acc[u][i];
+      }
+      __syncthreads();
+    }
   }
 }
 

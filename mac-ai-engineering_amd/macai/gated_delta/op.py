@@ -55,10 +55,12 @@ RECOMPUTE_STATES = True
 # from the identity and from zero), their composition in order (macai_gdr_state_scan) for each segment's starting
 # state, and the output pass over all segments at once.  The maps cost a second chain over DK + DV columns, so the
 # split pays only where the plain pass leaves most CUs idle.  "auto": for a single row (B = 1, no cu_seqlens) whose
-# plain pass has at most 128 workgroups of 16 columns (H x DV / 16 <= 128), the largest power of two P with P x H <= 64
-# head-rows and at least 32 chunks a segment (P = 1 otherwise); an int forces P.  Measured at T = 32,768, D = 128:
-# H = 16 splits in 4 (state passes 435 against 566 us); at H = 32 the plain pass already fills the chip (256
-# workgroups) and a split in 2 took 810 against 637 us.
+# plain pass has at most 128 workgroups of 16 columns (H x DV / 16 <= 128), the largest power of two P with P x H <= 128
+# head-rows and at least 32 chunks a segment (P = 1 otherwise); an int forces P.  The map pass then runs 8 waves of
+# columns a workgroup where that keeps its workgroups to one a CU (split_for's waves=8).  Measured at T = 32,768,
+# D = 128, H = 16: P = 8 (maps 143 us, scan 26, output 195) against P = 4 (maps 178, scan 15, output 205) and the
+# plain pass's 566 us; at H = 32 the plain pass already fills the chip (256 workgroups) and a split in 2 took 810
+# against 637 us.
 SEQUENCE_SPLIT = "auto"
 
 
@@ -84,26 +86,27 @@ def valid_splits(dv: int) -> list:
 _SPLITS = {}     # (rows, T, dv, share, VALUE_SPLIT) -> split: the launch path asks on every call
 
 
-def split_for(rows: int, T: int, dv: int, share: int = 1) -> int:
+def split_for(rows: int, T: int, dv: int, share: int = 1, waves: int = 4) -> int:
     """The value split for a pass (_split_for's rule), remembered per shape and VALUE_SPLIT setting."""
-    key = (rows, T, dv, share, VALUE_SPLIT)
+    key = (rows, T, dv, share, waves, VALUE_SPLIT)
     s = _SPLITS.get(key)
     if s is None:
-        s = _SPLITS[key] = _split_for(rows, T, dv, share)
+        s = _SPLITS[key] = _split_for(rows, T, dv, share, waves)
     return s
 
 
-def _split_for(rows: int, T: int, dv: int, share: int = 1) -> int:
+def _split_for(rows: int, T: int, dv: int, share: int = 1, waves: int = 4) -> int:
     """VALUE_SPLIT's choice for `rows` head-rows (B x H) of value width dv, for a pass that gets 1 / share of the
     chip: "auto" takes the largest valid split whose workgroups fit the pass's share of the CUs at once (rows x split
     <= 256 / share: a state pass's workgroup holds its CU's LDS, and a second round of a sequential pass would double
     its time), else the smallest; an int setting is rounded down to a valid split.  "auto" leaves out the splits with
     8 waves of columns per workgroup where another exists: with the loader wave that is 9 waves, 3 on one SIMD, which
     caps a wave at 168 VGPRs: the 128-wide state kernels spill there (the backward's pair pass ran 2.1-2.8x slower
-    than at 4 waves)."""
+    than at 4 waves); waves=8 admits them (the segment map pass at key heads up to 128, whose kernel holds 118-151
+    VGPRs at 8 waves; at 256 it spills)."""
     valid = valid_splits(dv)
     if VALUE_SPLIT == "auto":
-        valid = [s for s in valid if (dv // 16) // s <= 4] or valid
+        valid = [s for s in valid if (dv // 16) // s <= waves] or valid
         fits = [s for s in valid if rows * s * share <= 256]
         return fits[-1] if fits else valid[0]
     want = int(VALUE_SPLIT)
@@ -257,7 +260,7 @@ def segments_for(B: int, T: int, H: int, DV: int, pack=None, save: bool = False)
     if H * (DV // 16) > 128:
         return 1
     P = 1
-    while 2 * P * H <= 64 and NT // (2 * P) >= 32:
+    while 2 * P * H <= 128 and NT // (2 * P) >= 32:
         P *= 2
     return P
 
@@ -295,7 +298,7 @@ def _forward_segments(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_s
     # the table
     maps = torch.empty(nseg - 1, H, DK, DK + DV, device=dev, dtype=f32)
     _launch("state_map", "macai_gdr_state_map", r["W"], r["U"], r["Ke"], r["GL"], P(maps), nseg - 1, T, H, DK, DV,
-            code, split_for((nseg - 1) * H, T, DK + DV), P(table), NT, stream)
+            code, split_for((nseg - 1) * H, T, DK + DV, waves=8 if DK <= 128 else 4), P(table), NT, stream)
     starts = torch.empty(nseg, H, DK, DV, device=dev, dtype=f32)
     _launch("state_scan", "macai_gdr_state_scan", P(maps), P(s0), P(starts), 1, nseg, H, DK, DV, stream)
     o = torch.empty(1, T, H, DV, device=dev, dtype=dt)

@@ -126,7 +126,7 @@ def test_config_bf16_fwd_bwd(cfg, recompute):
 @pytest.mark.parametrize("Hv", [16, 32])
 def test_config3_long_prefill_forward(Hv, split):
     """Config 3: one row of 32,768 tokens (512 sequential chunks), bf16, forward only, the final state returned; as
-    segments side by side (the default at Hv = 16: 4 of them) and as one chain (SEQUENCE_SPLIT = 1, and the default
+    segments side by side (the default at Hv = 16: 8 of them) and as one chain (SEQUENCE_SPLIT = 1, and the default
     at Hv = 32, whose plain pass already fills the chip)."""
     _say(f"case config3 Hv={Hv} split={split}")
     inp = gdr.config_inputs(3, Hv=Hv)
@@ -143,7 +143,7 @@ def test_config3_long_prefill_forward(Hv, split):
         op.SEQUENCE_SPLIT = old
     ran = [k_ for k_, v_ in op.CALLS.items() if v_ != before.get(k_, 0)]
     seg = split == "auto" and Hv == 16
-    assert len(ran) == 1 and ran[0].startswith("fwd seg4 " if seg else "fwd s"), ran
+    assert len(ran) == 1 and ran[0].startswith("fwd seg8 " if seg else "fwd s"), ran
     assert seg or not ran[0].startswith("fwd seg"), ran
     q, k = gdr.prologue(inp["query"].double(), inp["key"].double())
     ro, rsT = gdr.chunked_forward_segments(q, k, inp["value"].double(), inp["g"].double(), inp["beta"].double(),

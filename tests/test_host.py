@@ -220,16 +220,20 @@ def test_split_rule():
 
 def test_segment_rule():
     """SEQUENCE_SPLIT 'auto': only a single unpacked row whose forward saves nothing, and only when its plain pass
-    leaves CUs idle (H x DV / 16 <= 128 workgroups); then the largest power of two with P x H <= 64 and >= 32 chunks
-    a segment.  An int forces P (capped at the chunk count)."""
-    assert op.segments_for(1, 32768, 16, 128) == 4
+    leaves CUs idle (H x DV / 16 <= 128 workgroups); then the largest power of two with P x H <= 128 and >= 32 chunks
+    a segment.  An int forces P (capped at the chunk count).  The map pass may take 8 waves of columns a workgroup
+    (key heads up to 128): at H = 16, P = 8 its 7 x 16 head-rows of 256 columns take two slices each, one round."""
+    assert op.segments_for(1, 32768, 16, 128) == 8
     assert op.segments_for(1, 32768, 32, 128) == 1       # 256 workgroups already: the maps would only add a chain
-    assert op.segments_for(1, 32768, 8, 128) == 8
+    assert op.segments_for(1, 32768, 8, 128) == 16
     assert op.segments_for(1, 4096, 16, 128) == 2        # 64 chunks: two segments of 32
     assert op.segments_for(1, 2048, 16, 128) == 1
     assert op.segments_for(2, 32768, 16, 128) == 1
     assert op.segments_for(1, 32768, 16, 128, save=True) == 1
     assert op.segments_for(1, 32768, 16, 128, pack=object()) == 1
+    assert op.split_for(7 * 16, 32768, 256, waves=8) == 2
+    assert op.split_for(3 * 16, 32768, 256, waves=8) == 4
+    assert op.split_for(7 * 16, 32768, 256) == 4        # 4 waves at most: two rounds
     old = op.SEQUENCE_SPLIT
     try:
         op.SEQUENCE_SPLIT = 3
