@@ -103,12 +103,14 @@ def test_one_call_forward_equals_the_two_passes(shape, dtype, split):
 # ---- sequence parallelism: segment maps, their composition, the segmented forward -------------------------------------
 @pytest.mark.parametrize("dtype,T,P,DK,DV", [(torch.float32, 64 * 13 + 5, 3, 128, 128),
                                              (torch.bfloat16, 64 * 9, 2, 128, 128), (torch.float32, 64 * 8, 8, 128, 128),
-                                             (torch.float32, 64 * 6 + 9, 3, 256, 128), (torch.bfloat16, 64 * 7, 2, 64, 64)])
+                                             (torch.float32, 64 * 6 + 9, 3, 256, 128), (torch.bfloat16, 64 * 7, 2, 64, 64),
+                                             (torch.float32, 64 * 12 + 3, 5, 32, 64), (torch.bfloat16, 64 * 8, 4, 64, 128)])
 def test_segment_maps_and_scan(dtype, T, P, DK, DV):
     """macai_gdr_state_map on a row split into P segments of whole chunks (the last one ragged) against the oracle's
     segment_map of each segment, and macai_gdr_state_scan's starting states against the oracle's chunk states at the
     segment boundaries.  float32 at the harness bar 2e-4 (relative to the largest entry of each map), bf16 at 1e-2.
-    Key heads of 256 (float32) take the map pass's direct form (the chunk's tiles read from memory, not LDS)."""
+    Key heads of 256 (float32) take the map pass's direct form (the chunk's tiles read from memory, not LDS) and the
+    scan's form that reads each map from memory; below 256 the scan's MFMA steps run on 2, 4 or 8 row tiles."""
     from macai.gated_delta import _native as N
     from macai.gated_delta import op
     print(f"case segment maps {dtype} T={T} P={P} DK={DK} DV={DV}", flush=True)
