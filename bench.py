@@ -43,7 +43,7 @@ TRAFFIC = {
     (1, "stored"): {"sources": "47dd3058cef71e86", "bytes": {
         "prep_fwd": 151801532, "state_fwd_out": 193206699, "state_bwd": 164489638, "chunk_bwd": 295096317}},
 }
-KERNEL_SOURCES = ("gdr_kernels.hip", "gdr_common.h", "gdr_lds.h", "gdr_stage.h")
+KERNEL_SOURCES = ("gdr_kernels.hip", "gdr_common.h", "gdr_lds.h", "gdr_stage.h", "gdr_chunk_bwd8.hip")
 
 
 def kernel_fingerprint():

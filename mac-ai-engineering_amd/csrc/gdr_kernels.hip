@@ -2891,8 +2891,15 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeArgs a) {
   }
 }
 
+// chunk_bwd8's launches (bf16 inputs): defined in gdr_chunk_bwd8.hip, a translation unit of their own that includes
+// this file's device code and is compiled with LLVM's max-memory-clause scheduling strategy (chunk_bwd8 2.5% faster
+// with it; applied to the whole library it slowed state_bwd by 4% and grew the spills of the float32 state kernels).
+// xn: the persistent form (wgs workgroups over `units` chunk-heads); else one chunk-head a workgroup over `grid`.
+void cb8_launch(const ChunkBwdArgs& a, int DK, int DV, bool xn, int wgs, int units, dim3 grid, hipStream_t st);
+
 }  // namespace gdr
 
+#ifndef GDR_CB8_ONLY   // gdr_chunk_bwd8.hip takes the device code above and nothing below
 // =====================================================================================================================
 // C ABI
 // =====================================================================================================================
@@ -3273,18 +3280,9 @@ int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float
   })
   if (dtype == MACAI_GDR_F32) {
     LAUNCH_CB(float);
-  } else if (xn) {
-    const int cus = device_cus();
-    const int wgs = (int)(units < cus ? units : cus);
-    DISPATCH_DK(DK, hipLaunchKernelGGL((chunk_bwd8xn_kernel<DKC>), dim3((unsigned)wgs), dim3(512), 0, st, a,
-                                       (int)units));
   } else {
-    DISPATCH_DK(DK, switch (DV) {
-      case 32: hipLaunchKernelGGL((chunk_bwd8_kernel<DKC, 32>), grid, dim3(512), 0, st, a); break;
-      case 64: hipLaunchKernelGGL((chunk_bwd8_kernel<DKC, 64>), grid, dim3(512), 0, st, a); break;
-      case 96: hipLaunchKernelGGL((chunk_bwd8_kernel<DKC, 96>), grid, dim3(512), 0, st, a); break;
-      default: hipLaunchKernelGGL((chunk_bwd8_kernel<DKC, 128>), grid, dim3(512), 0, st, a); break;
-    })
+    const int cus = xn ? device_cus() : 0;
+    cb8_launch(a, (int)DK, (int)DV, xn, (int)(xn && units > cus ? cus : units), (int)units, grid, st);
   }
 #undef LAUNCH_CB
   return launched(what);
@@ -3345,3 +3343,4 @@ int macai_gdr_group_sum(const void* x, void* y, int64_t B, int64_t T, int64_t H,
 }
 
 }  // extern "C"
+#endif  // GDR_CB8_ONLY
