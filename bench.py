@@ -37,11 +37,11 @@ C = 64
 # WRITE_SIZE x 1.000.  Keyed by the config and the mode the profile ran, and stamped with the fingerprint of the
 # kernel sources it was taken on: measured_traffic() reports the figures only while the sources still match.
 TRAFFIC = {
-    (1, "recompute"): {"sources": "47dd3058cef71e86", "bytes": {
-        "prep_fwd": 143410556, "state_fwd_out": 110335524, "prep_bwd": 151794423, "state_pair": 313766458,
-        "chunk_bwd": 295101168}},
-    (1, "stored"): {"sources": "47dd3058cef71e86", "bytes": {
-        "prep_fwd": 151801532, "state_fwd_out": 193206699, "state_bwd": 164489638, "chunk_bwd": 295096317}},
+    (1, "recompute"): {"sources": "f82054d34fecd5f7", "bytes": {
+        "prep_fwd": 143415658, "state_fwd_out": 110221300, "prep_bwd": 151799665, "state_pair": 313949588,
+        "chunk_bwd": 295105665}},
+    (1, "stored"): {"sources": "f82054d34fecd5f7", "bytes": {
+        "prep_fwd": 151810377, "state_fwd_out": 193172100, "state_bwd": 164412853, "chunk_bwd": 295099227}},
 }
 KERNEL_SOURCES = ("gdr_kernels.hip", "gdr_common.h", "gdr_lds.h", "gdr_stage.h", "gdr_chunk_bwd8.hip")
 
