@@ -26,8 +26,9 @@ def cb8_command(obj):
 
 
 def command(out=OUT, cb8_obj=None):
-    # the object first: hipcc marks every file after a .hip source as HIP source
-    return _common() + ["-shared", *([cb8_obj] if cb8_obj else []), *SRCS, "-o", out]
+    """The link of the library: with cb8_obj, chunk_bwd8's separately compiled object (placed first: hipcc marks every
+    file after a .hip source as HIP source); without it, its source compiled like the others (no scheduler flag)."""
+    return _common() + ["-shared", *([cb8_obj] if cb8_obj else []), *SRCS, *([] if cb8_obj else [CB8_SRC]), "-o", out]
 
 
 def _run(cmd, verbose):
