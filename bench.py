@@ -43,15 +43,17 @@ TRAFFIC = {
     (1, "stored"): {"sources": "f82054d34fecd5f7", "bytes": {
         "prep_fwd": 151810377, "state_fwd_out": 193172100, "state_bwd": 164412853, "chunk_bwd": 295099227}},
 }
-KERNEL_SOURCES = ("gdr_kernels.hip", "gdr_common.h", "gdr_lds.h", "gdr_stage.h", "gdr_chunk_bwd8.hip")
+# the rule's kernel sources and the build script that sets their compile flags (paths under mac-ai-engineering_amd/)
+KERNEL_SOURCES = ("csrc/gdr_kernels.hip", "csrc/gdr_common.h", "csrc/gdr_lds.h", "csrc/gdr_stage.h",
+                  "csrc/gdr_chunk_bwd8.hip", "build.py")
 
 
 def kernel_fingerprint():
-    """sha256 (first 16 hex digits) of the rule's kernel sources, in KERNEL_SOURCES order."""
+    """sha256 (first 16 hex digits) of the rule's kernel sources and build script, in KERNEL_SOURCES order."""
     import hashlib
     h = hashlib.sha256()
     for f in KERNEL_SOURCES:
-        with open(os.path.join(ROOT, "mac-ai-engineering_amd", "csrc", f), "rb") as fh:
+        with open(os.path.join(ROOT, "mac-ai-engineering_amd", f), "rb") as fh:
             h.update(fh.read())
     return h.hexdigest()[:16]
 
@@ -75,24 +77,27 @@ CONFIGS = {
 }
 
 
-def make_inputs(cfg, seed, dev, **over):
+def make_inputs(cfg, seed, dev, on_device=False, **over):
     """The measurement plan's synthetic inputs (q, k, v, u_g, x_g, x_beta, s0, dO drawn in that order in float64);
-    keyword overrides replace config fields."""
+    keyword overrides replace config fields.  on_device: the same distributions drawn in float32 by the device's own
+    generator (seconds faster for config 3's 32,768-token rows; other values, the same workload)."""
     c = dict(CONFIGS[cfg], **over)
-    gen = torch.Generator().manual_seed(seed)
     B, T, Hk, Hv, DK, DV = c["B"], c["T"], c["Hk"], c["Hv"], c["DK"], c["DV"]
     rep = Hv // Hk
-    f64 = torch.float64
-    q = torch.randn(B, T, Hk, DK, generator=gen, dtype=f64).repeat_interleave(rep, 2)
-    k = torch.randn(B, T, Hk, DK, generator=gen, dtype=f64).repeat_interleave(rep, 2)
-    v = torch.randn(B, T, Hv, DV, generator=gen, dtype=f64)
-    u = torch.rand(Hv, generator=gen, dtype=f64) * math.log(16.0)
-    xg = torch.randn(B, T, Hv, generator=gen, dtype=f64)
-    xb = torch.randn(B, T, Hv, generator=gen, dtype=f64)
+    where = dev if on_device else "cpu"
+    gen = torch.Generator(device=where).manual_seed(seed)
+    fdt = torch.float32 if on_device else torch.float64
+    randn = lambda *shape: torch.randn(*shape, generator=gen, dtype=fdt, device=where)
+    q = randn(B, T, Hk, DK).repeat_interleave(rep, 2)
+    k = randn(B, T, Hk, DK).repeat_interleave(rep, 2)
+    v = randn(B, T, Hv, DV)
+    u = torch.rand(Hv, generator=gen, dtype=fdt, device=where) * math.log(16.0)
+    xg = randn(B, T, Hv)
+    xb = randn(B, T, Hv)
     g = -torch.exp(u) * torch.nn.functional.softplus(xg)
     beta = torch.sigmoid(xb)
-    s0 = torch.randn(B, Hv, DK, DV, generator=gen, dtype=f64) * 0.02 if c["s0"] else None
-    do = torch.randn(B, T, Hv, DV, generator=gen, dtype=f64)
+    s0 = randn(B, Hv, DK, DV) * 0.02 if c["s0"] else None
+    do = randn(B, T, Hv, DV)
     bf = torch.bfloat16
     out = dict(query=q.to(dev, bf), key=k.to(dev, bf), value=v.to(dev, bf), g=g.to(dev, torch.float32),
                beta=beta.to(dev, torch.float32), initial_state=None if s0 is None else s0.to(dev, torch.float32),
@@ -307,13 +312,17 @@ def _events_time(fn, reps):
 
 
 def bench_prefill(args):
+    print(json.dumps(prefill_line(args.hv, args.steps, args.warmup)), flush=True)
+
+
+def prefill_line(hv, steps, warmup, on_device=False):
     """one row of 32,768 tokens, forward only (no_grad: no per-chunk states kept), the final state
     returned; Hv value heads over 16 key heads (q and k unrepeated).  The bound is the 512-chunk chain of the state
     pass; the line reports the value split it ran with and each pass's in-step time."""
     from macai.gated_delta import chunk_gated_delta_rule, op
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    inp, c = make_inputs(3, 1003, dev, Hv=args.hv)
+    inp, c = make_inputs(3, 1003, dev, on_device=on_device, Hv=hv)
     rep = c["Hv"] // c["Hk"]
     q, k = (inp[n][:, :, ::rep].contiguous() for n in ("query", "key"))
     v, g, beta = inp["value"], inp["g"], inp["beta"]
@@ -321,11 +330,11 @@ def bench_prefill(args):
     def fwd():
         with torch.no_grad():
             return chunk_gated_delta_rule(q, k, v, g, beta, output_final_state=True, use_qk_l2norm_in_kernel=True)
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         fwd()
-    sec = _events_time(fwd, args.steps)
+    sec = _events_time(fwd, steps)
     op.EVENTS = []
-    for _ in range(min(args.steps, 10)):
+    for _ in range(min(steps, 10)):
         fwd()
     torch.cuda.synchronize()
     t = {}
@@ -340,8 +349,8 @@ def bench_prefill(args):
                    "hbm_frac": round(cost[n]["bytes"] / x / HBM_PEAK, 4)} for n, x in t.items()}
     st = t["state_fwd_out"]
     line = {"metric": f"gated-delta forward tokens/s (B1xT32768, Hv{H}, Hk16, d128 bf16, forward only)",
-            "value": round(B * T / sec, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
-            "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+            "value": round(B * T / sec, 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps,
+            "warmup": warmup, "ms_per_step": round(sec * 1e3, 4), "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
             "config": {"workload": "BASELINE config 3: long single-row prefill, forward only", "B": B, "T": T,
                        "Hk": c["Hk"], "Hv": H, "DK": DK, "DV": DV, "chunk": C, "segments": segs,
@@ -352,7 +361,7 @@ def bench_prefill(args):
                          "traffic": None},
             "chain_us_per_chunk": round(st * 1e6 / math.ceil(math.ceil(T / C) / segs), 3),
             "kernels": kernels}
-    print(json.dumps(line), flush=True)
+    return line
 
 
 def decode_bytes(B, H, Hk, DK, DV, es=2):
@@ -362,6 +371,10 @@ def decode_bytes(B, H, Hk, DK, DV, es=2):
 
 
 def bench_decode(args):
+    print(json.dumps(decode_line(args.steps, args.warmup)), flush=True)
+
+
+def decode_line(steps, warmup):
     """one decode step per sequence (B = 64, Hv = 32 over Hk = 16, fp32 state [64, 32, 128, 128]),
     through the drop-in (transformers' torch_recurrent_gated_delta_rule signature) and as the bare C-ABI launch on
     preallocated buffers.  The step reads and writes the whole fp32 state once: HBM-bound, reported against peak."""
@@ -385,14 +398,14 @@ def bench_decode(args):
     st = N.stream_of(q)
     args_k = ("macai_gdr_decode", P(q), P(k), P(v), P(g), P(beta), P(s0), P(o), P(s1), B, H, Hk, DK, DV,
               N.dtype_code(v.dtype), 1, DK ** -0.5, st)
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         dropin()
-    sec_dropin = _events_time(dropin, args.steps)
-    sec = _events_time(lambda: N.call(*args_k), args.steps)
+    sec_dropin = _events_time(dropin, steps)
+    sec = _events_time(lambda: N.call(*args_k), steps)
     nbytes = decode_bytes(B, H, Hk, DK, DV)
     line = {"metric": "gated-delta decode step GB/s (B64, Hv32, Hk16, d128; fp32 state read + write)",
-            "value": round(nbytes / sec / 1e9, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
-            "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+            "value": round(nbytes / sec / 1e9, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps,
+            "warmup": warmup, "ms_per_step": round(sec * 1e3, 4), "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "f32", "data": "synthetic",
             "config": {"workload": "BASELINE config 4: one recurrent decode step per sequence", "B": B, "T": 1,
                        "Hk": Hk, "Hv": H, "DK": DK, "DV": DV},
@@ -401,7 +414,7 @@ def bench_decode(args):
                          "unit": "GB/s", "frac": round(nbytes / sec / HBM_PEAK, 4), "traffic": None},
             "bytes_per_step": nbytes, "tokens_per_s": round(B / sec, 1),
             "dropin_ms_per_step": round(sec_dropin * 1e3, 4), "dropin_tokens_per_s": round(B / sec_dropin, 1)}
-    print(json.dumps(line), flush=True)
+    return line
 
 
 def bench_producers(cfg, reps=20):
@@ -519,6 +532,88 @@ def bench_ceilings(args, mib=1024, reps=10):
     print(json.dumps(line), flush=True)
 
 
+def make_step(cfg, dev, grouped=False, packed=None):
+    """A training step of config cfg: the drop-in's forward (use_qk_l2norm_in_kernel=True) and torch.autograd.grad
+    for the seeded dO over every leaf (q and k at the model's key heads, v, g, beta and the initial state when the
+    config has one).  grouped: with Hk < Hv, q and k go to the rule unrepeated; otherwise the step repeats them first,
+    as the model does.  packed: "uniform" / "ragged" runs the B rows as one packed row (cu_seqlens).  Returns (step,
+    config, the drop-in's extra keywords, the inputs)."""
+    from macai.gated_delta import chunk_gated_delta_rule
+    inp, c = make_inputs(cfg, 1000 + cfg, dev)
+    rep = c["Hv"] // c["Hk"]
+    # q, k leaves at the model's key heads (make_inputs draws them per key head and repeats)
+    kq = {n: inp[n][:, :, ::rep].contiguous() for n in ("query", "key")}
+    leaves = [kq["query"], kq["key"]] + [inp[n] for n in ("value", "g", "beta")]
+    kw = {}
+    if packed:                                # the B rows as one row of B * T tokens
+        Bp, Tp = c["B"], c["T"]
+        leaves = [x.reshape(1, Bp * Tp, *x.shape[2:]) for x in leaves]
+        inp["do"] = inp["do"].reshape(1, Bp * Tp, *inp["do"].shape[2:])
+        if packed == "uniform":
+            lens = [Tp] * Bp
+        else:                                 # 4 B seeded lengths summing to B * T
+            gen = torch.Generator().manual_seed(7)
+            w = torch.rand(4 * Bp, generator=gen) + 0.01
+            lens = (w / w.sum() * Bp * Tp).long().clamp_min(1).tolist()
+            lens[-1] += Bp * Tp - sum(lens)
+        kw["cu_seqlens"] = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32, device=dev)
+        if inp["initial_state"] is not None:
+            inp["initial_state"] = None       # one state per sequence would be needed; the packed runs start at zero
+    leaves = [x.requires_grad_(True) for x in leaves]
+    s0 = inp["initial_state"]
+    if s0 is not None:
+        s0.requires_grad_(True)
+        leaves.append(s0)
+    do = inp["do"]
+
+    def step():
+        q, k = leaves[0], leaves[1]
+        if rep > 1 and not grouped:               # the model's layout: repeat over each group first
+            q, k = q.repeat_interleave(rep, 2), k.repeat_interleave(rep, 2)
+        o, _ = chunk_gated_delta_rule(q, k, *leaves[2:5], initial_state=s0, output_final_state=False,
+                                      use_qk_l2norm_in_kernel=True, **kw)
+        return torch.autograd.grad(o, leaves, do)
+    return step, c, kw, inp
+
+
+def other_configs(step1, steps=20, warmup=3):
+    """The default line's compact figures beside the headline: config 1's step on the float32 kernels
+    (op.BF16_OPERANDS = False, the reference's own precision), config 2's training step (q, k repeated by the step as
+    the model does, and grouped), config 3's forward at Hv 16 and 32 (inputs drawn on the device) and config 4's
+    decode step, each timed the way its own --config line times it, with fewer steps."""
+    from macai.gated_delta import op
+    dev = torch.device("cuda", 0)
+    ns = argparse.Namespace(steps=steps, warmup=warmup)
+    out = {}
+    old = op.BF16_OPERANDS
+    try:
+        op.BF16_OPERANDS = False
+        sec, in_step = _time_step(step1, ns)
+    finally:
+        op.BF16_OPERANDS = old
+    B1, T1 = CONFIGS[1]["B"], CONFIGS[1]["T"]
+    out["config1_f32_compute"] = {"ms_per_step": round(sec * 1e3, 4), "tokens_per_s": round(B1 * T1 / sec, 1),
+                                  "kernels_us": {n: round(t * 1e6, 2) for n, t in in_step.items()}}
+    for grouped in (False, True):
+        step, c, _, _ = make_step(2, dev, grouped)
+        sec, _ = _time_step(step, ns)
+        out["config2_" + ("grouped" if grouped else "repeated")] = {
+            "ms_per_step": round(sec * 1e3, 4), "tokens_per_s": round(c["B"] * c["T"] / sec, 1)}
+        del step
+    for hv in (16, 32):
+        ln = prefill_line(hv, steps, warmup, on_device=True)
+        out[f"config3_hv{hv}"] = {"ms_fwd": ln["ms_per_step"], "tokens_per_s": ln["value"],
+                                  "segments": ln["config"]["segments"], "value_split": ln["config"]["value_split"],
+                                  "state_pass_us": ln["kernels"]["state_fwd_out"]["us"],
+                                  "state_pass_hbm_frac": ln["roofline"]["frac"]}
+        torch.cuda.empty_cache()
+    ln = decode_line(steps, warmup)
+    out["config4_decode"] = {"us": round(ln["ms_per_step"] * 1e3, 2), "GB/s": ln["value"],
+                             "hbm_frac": ln["roofline"]["frac"], "tokens_per_s": ln["tokens_per_s"],
+                             "dropin_us": round(ln["dropin_ms_per_step"] * 1e3, 2)}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -549,6 +644,9 @@ def main():
     ap.add_argument("--f32-compute", action="store_true",
                     help="run the bf16 inputs on the float32 kernels (op.BF16_OPERANDS = False, the reference's own "
                          "precision) and report that step's time only")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="leave out the default line's compact figures of configs 2-4 and of config 1 on the float32 "
+                         "kernels")
     ap.add_argument("--no-alone", action="store_true",
                     help="skip timing each pass alone, so a kernel trace of the run holds the step's launches only")
     ap.add_argument("--copy-mib", type=int, default=0,
@@ -570,43 +668,9 @@ def main():
     if args.config == 4:
         bench_decode(args)
         return
-    from macai.gated_delta import chunk_gated_delta_rule
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    inp, c = make_inputs(args.config, 1000 + args.config, dev)
-    rep = c["Hv"] // c["Hk"]
-    # q, k leaves at the model's key heads (make_inputs draws them per key head and repeats)
-    kq = {n: inp[n][:, :, ::rep].contiguous() for n in ("query", "key")}
-    leaves = [kq["query"], kq["key"]] + [inp[n] for n in ("value", "g", "beta")]
-    kw = {}
-    if args.packed:                           # the B rows as one row of B * T tokens
-        Bp, Tp = c["B"], c["T"]
-        leaves = [x.reshape(1, Bp * Tp, *x.shape[2:]) for x in leaves]
-        inp["do"] = inp["do"].reshape(1, Bp * Tp, *inp["do"].shape[2:])
-        if args.packed == "uniform":
-            lens = [Tp] * Bp
-        else:                                 # 4 B seeded lengths summing to B * T
-            gen = torch.Generator().manual_seed(7)
-            w = torch.rand(4 * Bp, generator=gen) + 0.01
-            lens = (w / w.sum() * Bp * Tp).long().clamp_min(1).tolist()
-            lens[-1] += Bp * Tp - sum(lens)
-        kw["cu_seqlens"] = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32, device=dev)
-        if inp["initial_state"] is not None:
-            inp["initial_state"] = None       # one state per sequence would be needed; the packed runs start at zero
-    leaves = [x.requires_grad_(True) for x in leaves]
-    s0 = inp["initial_state"]
-    if s0 is not None:
-        s0.requires_grad_(True)
-        leaves.append(s0)
-    do = inp["do"]
-
-    def step():
-        q, k = leaves[0], leaves[1]
-        if rep > 1 and not args.grouped:          # the model's layout: repeat over each group first
-            q, k = q.repeat_interleave(rep, 2), k.repeat_interleave(rep, 2)
-        o, _ = chunk_gated_delta_rule(q, k, *leaves[2:5], initial_state=s0, output_final_state=False,
-                                      use_qk_l2norm_in_kernel=True, **kw)
-        return torch.autograd.grad(o, leaves, do)
+    step, c, kw, inp = make_step(args.config, dev, args.grouped, args.packed)
 
     from macai.gated_delta import op
     if args.f32_compute:
@@ -693,6 +757,8 @@ def main():
                        "overlapped_state_passes": (not keep) and op.OVERLAP, "recompute_prep_in_backward": not keep},
             "roofline": roof, "kernels": kernels,
             "stored_states" if not keep else "recompute_states": other}
+    if args.config == 1 and not (args.no_configs or args.packed or args.grouped or args.stored):
+        line["configs"] = other_configs(step, min(args.steps, 20), min(args.warmup, 3))
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.config, args.cpu_threads)
     print(json.dumps(line), flush=True)

@@ -2900,6 +2900,12 @@ void cb8_launch(const ChunkBwdArgs& a, int DK, int DV, bool xn, int wgs, int uni
 }  // namespace gdr
 
 #ifndef GDR_CB8_ONLY   // gdr_chunk_bwd8.hip takes the device code above and nothing below
+// The entry points fall into five parts by the kernels they instantiate; build.py compiles this file once per part
+// (-DGDR_PART=1..5) in parallel, each object holding only its part's kernels.  Without GDR_PART every part is built.
+#ifndef GDR_PART
+#define GDR_PART 0
+#endif
+#define GDR_IN_PART(n) (GDR_PART == 0 || GDR_PART == (n))
 // =====================================================================================================================
 // C ABI
 // =====================================================================================================================
@@ -2930,7 +2936,8 @@ __global__ void __launch_bounds__(256) group_sum_kernel(const T* x, T* y, int64_
 }
 
 
-static int check_common(const char* what, int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV, int dtype) {
+[[maybe_unused]] static int check_common(const char* what, int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV,
+                                         int dtype) {
   if (B < 1 || T < 1 || H < 1) return fail(MACAI_GDR_EINVAL, "%s: B, T, H must be >= 1 (got %lld, %lld, %lld)", what,
                                            (long long)B, (long long)T, (long long)H);
   if (DK != 32 && DK != 64 && DK != 128 && DK != 256)
@@ -2949,7 +2956,8 @@ static int check_common(const char* what, int64_t B, int64_t T, int64_t H, int64
 
 // Packed rows: `pack` (NULL = each batch row is one sequence) with its chunk count; sets NT.  The table's contents
 // (built by the caller from cu_seqlens) are on the device and are not checked here.
-static int pack_chunks(const char* what, const int32_t* pack, int64_t NT_packed, int64_t B, int64_t T, int64_t* NT) {
+[[maybe_unused]] static int pack_chunks(const char* what, const int32_t* pack, int64_t NT_packed, int64_t B, int64_t T,
+                                        int64_t* NT) {
   if (!pack) {
     *NT = (T + C - 1) / C;
     return MACAI_GDR_OK;
@@ -2962,7 +2970,7 @@ static int pack_chunks(const char* what, const int32_t* pack, int64_t NT_packed,
   return MACAI_GDR_OK;
 }
 
-static int check_heads(const char* what, int64_t H, int64_t Hk) {
+[[maybe_unused]] static int check_heads(const char* what, int64_t H, int64_t Hk) {
   if (Hk < 1 || H % Hk != 0)
     return fail(MACAI_GDR_EINVAL, "%s: key heads must divide value heads (got Hk = %lld, H = %lld)", what,
                 (long long)Hk, (long long)H);
@@ -2986,7 +2994,7 @@ static int check_heads(const char* what, int64_t H, int64_t Hk) {
   }
 
 // The current device's compute units (queried once per device), or 0 when the query fails.
-static int device_cus() {
+[[maybe_unused]] static int device_cus() {
   static std::atomic<int> cus[64];
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
@@ -2998,7 +3006,7 @@ static int device_cus() {
   return n;
 }
 
-static int pick_waves(int64_t DV, int split, const char* what, int* nw_out, int* nslice_out) {
+[[maybe_unused]] static int pick_waves(int64_t DV, int split, const char* what, int* nw_out, int* nslice_out) {
   // a workgroup holds NW in {1, 2, 4, 8} waves of 16 value columns; split = workgroups per head-row
   const int ncb = (int)(DV / 16);
   int nw;
@@ -3018,6 +3026,7 @@ static int pick_waves(int64_t DV, int split, const char* what, int* nw_out, int*
 
 extern "C" {
 
+#if GDR_IN_PART(1)
 const char* macai_gdr_last_error(void) { return g_err; }
 
 int macai_gdr_abi_version(void) { return MACAI_GDR_ABI_VERSION; }
@@ -3060,6 +3069,8 @@ int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, 
   return launched(what);
 }
 
+#endif
+
 #define DISPATCH_NW(NW, ...)                                  \
   switch (NW) {                                               \
     case 1: { constexpr int NWC = 1; __VA_ARGS__; } break;    \
@@ -3068,6 +3079,7 @@ int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, 
     default: { constexpr int NWC = 8; __VA_ARGS__; } break;   \
   }
 
+#if GDR_IN_PART(2)
 int macai_gdr_state_fwd(const void* W, const float* U, const void* Ke, const float* GL, const void* Qg, const void* M,
                         const float* s0, void* o, float* sT, float* Sc, void* Vn, int64_t B, int64_t T, int64_t H,
                         int64_t DK, int64_t DV, int32_t dtype, int32_t flags, int32_t split, const int32_t* pack,
@@ -3125,6 +3137,9 @@ int macai_gdr_state_fwd(const void* W, const float* U, const void* Ke, const flo
   return launched(what);
 }
 
+#endif
+
+#if GDR_IN_PART(3)
 int macai_gdr_state_bwd(const void* Ke, const void* Qg, const void* W, const void* M, const float* GL,
                         const void* dO, const float* dsT, float* dSn, void* dVn, float* ds0, int64_t B, int64_t T,
                         int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t split, const int32_t* pack,
@@ -3190,6 +3205,9 @@ int macai_gdr_state_pair(const void* W, const float* U, const void* Ke, const vo
   return launched(what);
 }
 
+#endif
+
+#if GDR_IN_PART(4)
 int macai_gdr_state_map(const void* W, const float* U, const void* Ke, const float* GL, float* maps, int64_t B,
                         int64_t T, int64_t H, int64_t DK, int64_t DV, int32_t dtype, int32_t split, const int32_t* pack,
                         int64_t NT_packed, void* stream) {
@@ -3240,6 +3258,9 @@ int macai_gdr_state_scan(const float* maps, const float* s0, float* starts, int6
   return launched(what);
 }
 
+#endif
+
+#if GDR_IN_PART(5)
 int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float* g, const float* beta, const void* dO,
                         const void* A, const float* Sc, const float* dSn, const void* Vn,
                         const void* dVn, void* dq, void* dk, void* dv, float* dg, float* dbeta, int64_t B, int64_t T,
@@ -3288,6 +3309,9 @@ int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float
   return launched(what);
 }
 
+#endif
+
+#if GDR_IN_PART(1)
 int macai_gdr_decode(const void* q, const void* k, const void* v, const float* g, const float* beta,
                      const float* s_in, void* o, float* s_out, int64_t B, int64_t H, int64_t Hk, int64_t DK,
                      int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, void* stream) {
@@ -3341,6 +3365,8 @@ int macai_gdr_group_sum(const void* x, void* y, int64_t B, int64_t T, int64_t H,
                        (int)(H / Hk), (int)D);
   return launched(what);
 }
+
+#endif
 
 }  // extern "C"
 #endif  // GDR_CB8_ONLY

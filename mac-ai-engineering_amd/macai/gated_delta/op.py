@@ -20,6 +20,11 @@ CHUNK = 64   # chunk length of the kernels; the drop-in's chunk_size is accepted
 # The widest key head the bf16 kernels take; wider ones (256, the reference's widest tested, tests/test_harness.py:214-230)
 # run the float32 kernels, with 2-byte inputs upcast exactly and the results cast back.
 BF16_MAX_DK = 128
+# FUSED_NORM (the reference's switch and default, op.py:19-21): with use_qk_l2norm_in_kernel=True the drop-in's
+# query / key prologue (l2 normalisation, the query's DK^-1/2 scale) runs inside the kernels, its backward inside the
+# per-chunk backward (True); False runs the normalisation as PyTorch operations in float32 (autograd takes its
+# backward), rounds the normalised query and key to the compute dtype and leaves the kernels only the scale.
+FUSED_NORM = True
 # BF16_OPERANDS: bfloat16 inputs run on bf16 MFMA operands with fp32 accumulation and an fp32 state (True, the
 # default: the fast path, outputs and gradients within ~5e-3 of float64).  False upcasts them exactly and runs the
 # float32 kernels, as the reference computes every input (op.py:276-285, 297): dg and dbeta then come within ~1e-5 of
@@ -235,8 +240,13 @@ def _scratch_sizes(Bc, H, NT, DK, DV, es, prep: bool, with_A: bool, states: bool
 
 
 def _as(x, dt):
-    """x in dtype dt, contiguous: x itself when it already is (skips two calls on the launch path)."""
-    return x if x.dtype == dt and x.is_contiguous() else x.to(dt).contiguous()
+    """x in dtype dt, contiguous and 16-byte aligned (the kernels' vector accesses): x itself when it already is
+    (skips two calls on the launch path), a copy when it is not -- also when only its start is misaligned, as a view
+    at an odd offset of a larger tensor is (the reference's _even, op.py:58-60, copies such a tensor too)."""
+    if x.dtype == dt and x.is_contiguous() and x.data_ptr() % 16 == 0:
+        return x
+    y = x.to(dt).contiguous()
+    return y if y.data_ptr() % 16 == 0 else y.clone()
 
 
 def _prep(q, k, v, g, beta, l2norm: bool, q_scale: float, r, stream, pack=None, name="prep_fwd"):
@@ -410,7 +420,8 @@ class GatedDeltaRule(torch.autograd.Function):
         ctx.io_dtype = q.dtype             # o and the q, k, v gradients come back in it
         if q.dtype != torch.float32 and (q.shape[-1] > BF16_MAX_DK or not BF16_OPERANDS):
             q, k, v = q.float(), k.float(), v.float()
-        q, k, v, g, beta, s0 = (t.contiguous() for t in (q, k, v, g, beta, s0))
+        q, k, v = (_as(t, t.dtype) for t in (q, k, v))
+        g, beta, s0 = (_as(t, torch.float32) for t in (g, beta, s0))
         keep = save and not RECOMPUTE_STATES
         with _on(q.device):
             o, sT, r = _forward(q, k, v, g, beta, s0, False, 1.0, True, keep=keep, save=save)
@@ -464,6 +475,52 @@ def l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     return x * torch.rsqrt((x * x).sum(dim=-1, keepdim=True) + eps)
 
 
+def compute_dtype(dtype, DK: int):
+    """The operand type the kernels compute a call in: bfloat16 inputs on bf16 MFMA up to key width 128 (unless
+    BF16_OPERANDS is off); float16, float32 and wider keys on the float32 kernels."""
+    bf16 = dtype == torch.bfloat16 and DK <= BF16_MAX_DK and BF16_OPERANDS
+    return torch.bfloat16 if bf16 else torch.float32
+
+
+def eager_prologue(query, key, cdt):
+    """FUSED_NORM = False: the l2 normalisation of query and key as PyTorch operations in float32 (the reference's
+    unfused prologue, op.py:279-283), rounded to the compute dtype cdt; the kernels then apply only the query's
+    DK^-1/2 scale (use_qk_l2norm_in_kernel=False).  Autograd takes the normalisation's backward."""
+    return l2norm(query.float()).to(cdt), l2norm(key.float()).to(cdt)
+
+
+def plan(B: int, T: int, H: int, DK: int, DV: int, save: bool, Hk: int = None, dtype=torch.bfloat16,
+         cus: int = 256) -> dict:
+    """What a drop-in call of these dimensions runs under the current settings (the reference's plan, op.py:105-113,
+    for this build's kernels): the chunk length (64 for every pass), the operand type, the forward's segments, value
+    split and state-pass kernel, and -- when the forward saves for a backward -- whether the backward recomputes
+    (RECOMPUTE_STATES), its state passes, their split and the per-chunk backward's kernel.  cus: the device's compute
+    units (the persistent per-chunk backward runs where there are more chunk-heads than CUs)."""
+    Hk = Hk or H
+    cdt = compute_dtype(dtype, DK)
+    bf = cdt == torch.bfloat16
+    NT = math.ceil(T / CHUNK)
+    recompute = save and RECOMPUTE_STATES
+    nseg = segments_for(B, T, H, DV, None, save)
+    out = {"fwd_chunk": CHUNK, "bwd_chunk": CHUNK, "operands": "bf16" if bf else "f32",
+           "prep": ("prep8" if bf and (DV <= 128 or DV % 128 == 0) else "prep"), "segments": nseg,
+           "fused_norm": FUSED_NORM, "recompute": recompute}
+    if nseg > 1:
+        out["map_split"] = split_for((nseg - 1) * H, T, DK + DV, waves=8 if DK <= 128 else 4)
+        out["fwd_split"] = split_for(nseg * H, T, DV)
+    else:
+        out["fwd_split"] = split_for(B * H, T, DV)
+    waves = DV // 16 // out["fwd_split"]
+    out["fwd_state_pass"] = "state_out" if bf and waves <= 2 else "state_fwd"
+    if save:
+        pair = recompute and OVERLAP
+        out["bwd_state_passes"] = "pair" if pair else "recompute+reverse" if recompute else "reverse"
+        out["bwd_split"] = split_for(B * H, T, DV, 2 if pair else 1)
+        units = B * H * NT
+        out["chunk_bwd"] = (("chunk_bwd8xn" if DK == DV and units > cus else "chunk_bwd8") if bf else "chunk_bwd")
+    return out
+
+
 def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size: int = 64, initial_state=None,
                            output_final_state: bool = False, use_qk_l2norm_in_kernel: bool = False, **kwargs):
     """Drop-in for transformers' torch_chunk_gated_delta_rule: query, key [B, T, H, DK]; value [B, T, H, DV]; g (log
@@ -483,10 +540,10 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size: int = 64, ini
     cu = kwargs.get("cu_seqlens")
     pack = None if cu is None else _pack(cu, query.shape[1], query.device)
     dtype = query.dtype
-    # bf16 runs on bf16 MFMA up to key width 128 (unless BF16_OPERANDS is off); float16, float32 and wider keys on
-    # the float32 kernels
-    bf16 = dtype == torch.bfloat16 and query.shape[-1] <= BF16_MAX_DK and BF16_OPERANDS
-    cdt = torch.bfloat16 if bf16 else torch.float32
+    cdt = compute_dtype(dtype, query.shape[-1])
+    if use_qk_l2norm_in_kernel and not FUSED_NORM:
+        query, key = eager_prologue(query, key, cdt)
+        use_qk_l2norm_in_kernel = False
     q, k, v = _as(query, cdt), _as(key, cdt), _as(value, cdt)
     gf, bf = _as(g, torch.float32), _as(beta, torch.float32)
     s0 = None if initial_state is None else _as(initial_state, torch.float32)
@@ -517,12 +574,12 @@ def recurrent_gated_delta_rule(query, key, value, g, beta, initial_state=None, o
                                       cu_seqlens=kwargs.get("cu_seqlens"))
     dtype = query.dtype
     cdt = torch.bfloat16 if dtype == torch.bfloat16 else torch.float32
-    q, k, v = (x.to(cdt).contiguous() for x in (query, key, value))
-    gf, bf = g.to(torch.float32).contiguous(), beta.to(torch.float32).contiguous()
+    q, k, v = (_as(x, cdt) for x in (query, key, value))
+    gf, bf = _as(g, torch.float32), _as(beta, torch.float32)
     B, _, Hk, DK = q.shape
     H, DV = v.shape[2], v.shape[-1]
     s_in = (torch.zeros(B, H, DK, DV, device=q.device, dtype=torch.float32) if initial_state is None
-            else initial_state.to(torch.float32).contiguous())
+            else _as(initial_state, torch.float32))
     _check(q, k, v, gf, bf, s_in)
     o = torch.empty(B, 1, H, DV, device=q.device, dtype=cdt)
     s_out = torch.empty_like(s_in)

@@ -50,11 +50,49 @@ def _upstream(grad, shape, dtype, device):
     return _dense(grad if grad.dtype == dtype else grad.to(dtype))
 
 
+DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def _unfit(x, w, kd: int, dk: int, rep: int, dv: int):
+    """Why the convolution path cannot take these arguments, or None: x [B, T, C] in one of DTYPES with C = 2 kd +
+    value_dim, w of C x 4 taps, kd a whole number of key heads of dk and value_dim of value heads of dv, each value head
+    group rep value heads a key head, every width a multiple of 8 (the kernels move 16-byte channel vectors)."""
+    if not isinstance(x, torch.Tensor) or not isinstance(w, torch.Tensor):
+        return "x and the weight must be tensors"
+    if x.dim() != 3:
+        return f"x must be [B, T, C] (got {tuple(x.shape)})"
+    if x.dtype not in DTYPES:
+        return f"x must be float32, bfloat16 or float16 (got {x.dtype})"
+    C = x.shape[-1]
+    vd = C - 2 * kd
+    if w.numel() != C * TAPS or w.shape[-1] != TAPS:
+        return f"the weight must hold {TAPS} taps a channel, [C, 1, {TAPS}] (got {tuple(w.shape)} for C = {C})"
+    if min(kd, dk, dv, rep) < 1 or vd < 1 or kd % dk or vd % dv or (kd // dk) * rep != vd // dv:
+        return (f"need C = 2 key_dim + value_dim with key_dim = key heads x {dk}, value_dim = key heads x rep x {dv} "
+                f"(got C {C}, key_dim {kd}, rep {rep})")
+    if C % 8 or kd % 8 or dk % 8 or dv % 8:
+        return f"C, key_dim and the head widths must be multiples of 8 (got {C}, {kd}, {dk}, {dv})"
+    if x.numel() >= 2 ** 31 or x.numel() // C * kd * rep >= 2 ** 31:
+        return "tensors past 2^31 elements are not supported"
+    if w.device != x.device:
+        return f"x and the weight must be on one device (got {x.device}, {w.device})"
+    return None
+
+
+def supported(x: torch.Tensor, w: torch.Tensor, kd: int, dk: int, rep: int, dv: int) -> bool:
+    """Whether the HIP convolution path takes these arguments (the reference's test of the same name and signature,
+    layer/_conv.py:178): x on a HIP device and the widths the kernels take."""
+    return isinstance(x, torch.Tensor) and x.is_cuda and _unfit(x, w, kd, dk, rep, dv) is None
+
+
 class ConvQKV(torch.autograd.Function):
     """(q, k, v) = the convolution path of x (see the module's docstring)."""
 
     @staticmethod
     def forward(ctx, x, weight, kd: int, dk: int, rep: int, dv: int, repeat: bool = True, v_dtype=torch.float32):
+        why = _unfit(x, weight, kd, dk, rep, dv)
+        if why is not None:
+            raise ValueError("macai conv_qkv: " + why)
         if not x.is_cuda:
             raise RuntimeError("macai's convolution path runs on a HIP device (MI355X); got " + str(x.device))
         sp = _Split(x.shape, kd, dk, rep, dv, repeat)

@@ -25,11 +25,47 @@ def _f32(t):
     return _dense(t if t.dtype == torch.float32 else t.to(torch.float32))
 
 
+DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def _unfit(b, a, A_log, dt_bias):
+    """Why the gates cannot take these arguments, or None.  The kernels index b and a by one count n = b.numel() and
+    take the head of element i as i mod H, so b and a must agree in shape and dtype and end in the H heads of A_log
+    and dt_bias."""
+    if not all(isinstance(t, torch.Tensor) for t in (b, a, A_log, dt_bias)):
+        return "b, a, A_log and dt_bias must be tensors"
+    if b.dtype not in DTYPES or a.dtype != b.dtype:
+        return f"b and a must share a dtype among float32, bfloat16, float16 (got {b.dtype}, {a.dtype})"
+    if A_log.dtype not in DTYPES or dt_bias.dtype not in DTYPES:
+        return f"A_log and dt_bias must be float32, bfloat16 or float16 (got {A_log.dtype}, {dt_bias.dtype})"
+    if b.shape != a.shape or b.dim() < 1:
+        return f"b and a must have one shape [..., H] (got {tuple(b.shape)}, {tuple(a.shape)})"
+    if A_log.dim() != 1 or dt_bias.shape != A_log.shape or b.shape[-1] != A_log.shape[0]:
+        return (f"A_log and dt_bias must be [H] with H = b.shape[-1] (got {tuple(A_log.shape)}, "
+                f"{tuple(dt_bias.shape)} for b {tuple(b.shape)})")
+    if b.numel() >= 2 ** 31:
+        return "b and a past 2^31 elements are not supported"
+    devs = {t.device for t in (b, a, A_log, dt_bias)}
+    if len(devs) != 1:
+        return f"b, a, A_log and dt_bias must be on one device (got {sorted(map(str, devs))})"
+    return None
+
+
+def supported(b, a, A_log, dt_bias) -> bool:
+    """Whether the HIP gates take these arguments (the reference's test of the same name and signature,
+    layer/_gates.py:75): on a HIP device, b and a of one shape [..., H] and dtype, A_log and dt_bias [H]."""
+    return isinstance(b, torch.Tensor) and b.is_cuda and _unfit(b, a, A_log, dt_bias) is None
+
+
 class Gates(torch.autograd.Function):
-    """(beta, g) = (sigmoid(b), -exp(A_log) softplus(a + dt_bias)), both float32."""
+    """The layer's two gates in one launch: the write strength beta = sigmoid(b) and the log decay
+    g = -exp(A_log) softplus(a + dt_bias), both returned in float32."""
 
     @staticmethod
     def forward(ctx, b, a, A_log, dt_bias):
+        why = _unfit(b, a, A_log, dt_bias)
+        if why is not None:
+            raise ValueError("macai gates: " + why)
         if not b.is_cuda:
             raise RuntimeError("macai's gates run on a HIP device (MI355X); got " + str(b.device))
         heads = A_log.shape[0]

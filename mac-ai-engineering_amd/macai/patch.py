@@ -44,10 +44,11 @@ def _warn_absent(asked):
                       "silence this)", RuntimeWarning, stacklevel=3)
 
 
-def install(layer: bool = True, training: bool = True, lora: bool = True, decode: bool = False) -> list:
+def install(layer: bool = True, training: bool = True, lora: bool = True, *, decode: bool = False) -> list:
     """Rebind the rule's name (and with decode the recurrent step's) in every module above that can be imported;
-    returns the (module, name) pairs changed by this call.  layer / training / lora ask for parts this build does not
-    have: nothing is installed for them and a RuntimeWarning says so once per part."""
+    returns the paths of the modules changed by this call, as the reference's install() does (patch.py:33-56).
+    layer / training / lora keep the reference's positions and ask for parts this build does not have: nothing is
+    installed for them and a RuntimeWarning says so once per part.  decode is keyword-only."""
     _warn_absent([p for p, on in zip(ABSENT_PARTS, (layer, training, lora)) if on])
     swaps = [(NAME, chunk_gated_delta_rule)] + ([(DECODE_NAME, recurrent_gated_delta_rule)] if decode else [])
     changed = []
@@ -60,8 +61,14 @@ def install(layer: bool = True, training: bool = True, lora: bool = True, decode
             if hasattr(mod, name) and getattr(mod, name) is not fn:
                 _saved.setdefault((path, name), getattr(mod, name))
                 setattr(mod, name, fn)
-                changed.append((path, name))
+                if path not in changed:
+                    changed.append(path)
     return changed
+
+
+def swapped() -> list:
+    """The (module path, name) pairs currently rebound by install()."""
+    return list(_saved)
 
 
 def layer_patches() -> list:
@@ -87,7 +94,7 @@ def uninstall() -> None:
 
 
 @contextlib.contextmanager
-def installed(layer: bool = True, training: bool = True, lora: bool = True, decode: bool = False):
+def installed(layer: bool = True, training: bool = True, lora: bool = True, *, decode: bool = False):
     """install() for the duration of a with-block, then uninstall()."""
     install(layer=layer, training=training, lora=lora, decode=decode)
     try:

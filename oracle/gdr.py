@@ -97,9 +97,47 @@ def chunk_prep(k, v, g, beta, q=None, C=64):
     return out
 
 
-def chunked_forward(q, k, v, g, beta, s0, C=64):
+# Planted mistakes (test infrastructure: tests/test_oracle.py checks that the GPU chain tests' inputs and bars catch
+# each one).  "fwd_gamma_sq" / "bwd_gamma_sq": the carried state (forward) or state gradient (reverse pass) decays by
+# gamma_last^2 instead of gamma_last; "fwd_glast_off" / "bwd_glast_off": the chain takes G_last from the row before the
+# chunk's last (both the carried decay gamma_last and e_r = exp(G_last - G_r)).
+PLANTS = ("fwd_gamma_sq", "fwd_glast_off", "bwd_gamma_sq", "bwd_glast_off")
+# Operand classes that the bf16 kernels feed to bf16 MFMA products (the rest is fp32): prep's stored W, Ke = diag(e) K,
+# Qg = diag(gamma) Q, M and A; the state S and its gradient dS as product operands; Vn and dVn; the per-chunk
+# backward's chunk state Sc and its normalised q, k ("QK").  `rnd` rounds the named classes to bf16 where they enter a
+# product (the precision model of the bf16 path; no rounding by default).
+ROUNDABLE = ("W", "Ke", "Qg", "M", "A", "S", "dS", "Vn", "dVn", "Sc", "QK")
+
+
+def bf16(x):
+    """x rounded to bfloat16 (round to nearest even) and back to its dtype."""
+    return x.to(torch.bfloat16).to(x.dtype)
+
+
+def _rounder(rnd):
+    bad = set(rnd) - set(ROUNDABLE)
+    assert not bad, bad
+    return lambda name, x: bf16(x) if name in rnd else x
+
+
+def _chain_decays(P, c, plant, side):
+    """(gamma_last [B,H,1,1], e [B,H,C,1]) the forward (side "fwd") or reverse ("bwd") chain uses at chunk c."""
+    G = P["G"][:, :, c]
+    gl, e = P["gam"][:, :, c, -1], P["e"][:, :, c]
+    if plant == side + "_glast_off":
+        gl, e = torch.exp(G[..., -2]), torch.exp(G[..., -2:-1] - G)
+    if plant == side + "_gamma_sq":
+        gl = gl * gl
+    return gl[..., None, None], e[..., :, None]
+
+
+def chunked_forward(q, k, v, g, beta, s0, C=64, plant=None, rnd=()):
     """F1-F5 (q already normalised and scaled).  Returns (o [B,T,H,DV], sT [B,H,DK,DV], P) where P holds the per-chunk
-    intermediates: everything of chunk_prep plus Sc [B,H,NT,DK,DV] (state entering each chunk) and Vn [B,H,NT,C,DV]."""
+    intermediates: everything of chunk_prep plus Sc [B,H,NT,DK,DV] (state entering each chunk) and Vn [B,H,NT,C,DV].
+    plant: one of PLANTS (a deliberate mistake, for the tests' teeth); rnd: operand classes of ROUNDABLE rounded to
+    bf16 where they enter a product."""
+    assert plant is None or plant in PLANTS, plant
+    R = _rounder(rnd)
     T = q.shape[1]
     P = chunk_prep(k, v, g, beta, q, C)
     nt = P["G"].shape[2]
@@ -107,24 +145,33 @@ def chunked_forward(q, k, v, g, beta, s0, C=64):
     Sc, Vn, O = [], [], []
     for c in range(nt):
         Sc.append(S)
-        vn = P["U"][:, :, c] - P["W"][:, :, c] @ S                           # F4
-        O.append(P["gam"][:, :, c, :, None] * (P["Q"][:, :, c] @ S) + P["M"][:, :, c] @ vn)   # F5
+        Sop = R("S", S)
+        vn = P["U"][:, :, c] - R("W", P["W"][:, :, c]) @ Sop                   # F4
+        vop = R("Vn", vn)
+        if "Qg" in rnd:
+            qs = R("Qg", P["gam"][:, :, c, :, None] * P["Q"][:, :, c]) @ Sop
+        else:
+            qs = P["gam"][:, :, c, :, None] * (P["Q"][:, :, c] @ Sop)
+        O.append(qs + R("M", P["M"][:, :, c]) @ vop)                             # F5
         Vn.append(vn)
-        S = (P["gam"][:, :, c, -1, None, None] * S
-             + P["K"][:, :, c].transpose(-1, -2) @ (P["e"][:, :, c, :, None] * vn))
+        gl, e = _chain_decays(P, c, plant, "fwd")
+        if "Ke" in rnd:
+            S = gl * S + R("Ke", e * P["K"][:, :, c]).transpose(-1, -2) @ vop
+        else:
+            S = gl * S + P["K"][:, :, c].transpose(-1, -2) @ (e * vop)
     P["Sc"] = torch.stack(Sc, 2)
     P["Vn"] = torch.stack(Vn, 2)
     return _unchunk(torch.stack(O, 2), T), S, P
 
 
-def chunked_forward_segments(q, k, v, g, beta, s0, C=64, seg=4096):
+def chunked_forward_segments(q, k, v, g, beta, s0, C=64, seg=4096, plant=None):
     """chunked_forward over segments of `seg` tokens (a multiple of C), the state carried between them: the same
-    arithmetic chunk by chunk with bounded memory, for long sequences.  Returns (o, sT)."""
+    arithmetic chunk by chunk with bounded memory, for long sequences.  Returns (o, sT).  plant: as chunked_forward."""
     assert seg % C == 0
     S, outs = s0, []
     for t0 in range(0, q.shape[1], seg):
         sl = slice(t0, t0 + seg)
-        o, S, _ = chunked_forward(q[:, sl], k[:, sl], v[:, sl], g[:, sl], beta[:, sl], S, C)
+        o, S, _ = chunked_forward(q[:, sl], k[:, sl], v[:, sl], g[:, sl], beta[:, sl], S, C, plant=plant)
         outs.append(o)
     return torch.cat(outs, 1), S
 
@@ -147,12 +194,15 @@ def segment_map(q, k, v, g, beta, C=64):
     return A, Bm
 
 
-def chunked_backward(q, k, v, g, beta, s0, do, dsT, C=64, P=None):
+def chunked_backward(q, k, v, g, beta, s0, do, dsT, C=64, P=None, plant=None, rnd=()):
     """B1-B6 (q already normalised and scaled), dg in the reference's no-cancellation form (_chunked.py:1138-1176).
-    Returns (dq, dk, dv, dg, dbeta, ds0) and the intermediates dict (adds dSn = dS_{c+1} per chunk and dVn)."""
+    Returns (dq, dk, dv, dg, dbeta, ds0) and the intermediates dict (adds dSn = dS_{c+1} per chunk and dVn).  plant and
+    rnd as for chunked_forward (a forward plant or rounding applies to the forward that P comes from)."""
+    assert plant is None or plant in PLANTS, plant
+    R = _rounder(rnd)
     T = q.shape[1]
     if P is None:
-        _, _, P = chunked_forward(q, k, v, g, beta, s0, C)
+        _, _, P = chunked_forward(q, k, v, g, beta, s0, C, plant=plant, rnd=rnd)
     dO = _chunks(do, C)
     nt = P["G"].shape[2]
     gam, e, Gam, A, W, M, K, V, Q, bc = (P[n] for n in ("gam", "e", "Gam", "A", "W", "M", "K", "V", "Q", "beta"))
@@ -161,29 +211,39 @@ def chunked_backward(q, k, v, g, beta, s0, do, dsT, C=64, P=None):
     dSn, dVn = [None] * nt, [None] * nt
     for c in reversed(range(nt)):
         dSn[c] = dS
-        dvn = M[:, :, c].transpose(-1, -2) @ dO[:, :, c] + e[:, :, c, :, None] * (K[:, :, c] @ dS)        # B1
-        dS = (gam[:, :, c, -1, None, None] * dS + (gam[:, :, c, :, None] * Q[:, :, c]).transpose(-1, -2) @ dO[:, :, c]
-              - W[:, :, c].transpose(-1, -2) @ dvn)                                                          # B2
+        gl, ec = _chain_decays(P, c, plant, "bwd")
+        dop = R("dS", dS)
+        if "Ke" in rnd:
+            kds = R("Ke", ec * K[:, :, c]) @ dop
+        else:
+            kds = ec * (K[:, :, c] @ dop)
+        dvn = R("M", M[:, :, c]).transpose(-1, -2) @ dO[:, :, c] + kds                                    # B1
+        if "Qg" in rnd:
+            qdo = R("Qg", gam[:, :, c, :, None] * Q[:, :, c]).transpose(-1, -2) @ dO[:, :, c]
+        else:
+            qdo = (gam[:, :, c, :, None] * Q[:, :, c]).transpose(-1, -2) @ dO[:, :, c]
+        dS = gl * dS + qdo - R("W", W[:, :, c]).transpose(-1, -2) @ R("dVn", dvn)                           # B2
         dVn[c] = dvn
     dSn = torch.stack(dSn, 2)
     dVn = torch.stack(dVn, 2)
     Sc, Vn = P["Sc"], P["Vn"]
     tr = lambda x: x.transpose(-1, -2)
-    dOVt = dO @ tr(Vn)                                                     # B3
+    Ar, Scr, Vnr, dVnr, Kr, Qr = R("A", A), R("Sc", Sc), R("Vn", Vn), R("dVn", dVn), R("QK", K), R("QK", Q)
+    dOVt = dO @ tr(Vnr)                                                    # B3
     dM = Gam * dOVt
-    dOSt = dO @ tr(Sc)
-    dQ = gam[..., None] * dOSt + dM @ K
-    VndSt = Vn @ tr(dSn)
-    dK = tr(dM) @ Q + e[..., None] * VndSt
-    dW = -dVn @ tr(Sc)
-    X, Y = tr(A) @ dW, tr(A) @ dVn                                         # B5
+    dOSt = dO @ tr(Scr)
+    dQ = gam[..., None] * dOSt + dM @ Kr
+    VndSt = Vnr @ tr(dSn)
+    dK = tr(dM) @ Qr + e[..., None] * VndSt
+    dW = -dVnr @ tr(Scr)
+    X, Y = tr(Ar) @ dW, tr(Ar) @ dVnr                                      # B5
     bg = bc * gam
     dK = dK + bg[..., None] * X
     dV = bc[..., None] * Y
-    dA = torch.where(low, dW @ tr(bg[..., None] * K) + dVn @ tr(bc[..., None] * V), torch.zeros_like(A))
-    dL = torch.where(low, -tr(A) @ dA @ tr(A), torch.zeros_like(A))
+    dA = torch.where(low, dW @ tr(bg[..., None] * Kr) + dVnr @ tr(bc[..., None] * V), torch.zeros_like(A))
+    dL = torch.where(low, -tr(Ar) @ dA @ tr(Ar), torch.zeros_like(A))
     Pm = dL * Gam
-    dK = dK + bc[..., None] * (Pm @ K) + tr(Pm) @ (bc[..., None] * K)
+    dK = dK + bc[..., None] * (Pm @ Kr) + tr(Pm) @ (bc[..., None] * Kr)
     KG = P["KK"] * Gam
     R2 = dL * KG
     kx = (K * X).sum(-1)
@@ -216,10 +276,10 @@ def prologue(query, key, use_qk_l2norm_in_kernel=True):
 
 
 def dropin_f64(query, key, value, g, beta, initial_state=None, do=None, dsT=None, use_qk_l2norm_in_kernel=True,
-               C=64):
+               C=64, plant=None, rnd=()):
     """The drop-in in float64 from the given (dtype-representable) values: returns (o, sT, grads) with grads a dict of
     dquery, dkey, dvalue, dg, dbeta, dstate (None without do / dsT).  Chunked F/B equations; the prologue's gradient by
-    autograd.  Every tensor is upcast to float64 first."""
+    autograd.  Every tensor is upcast to float64 first.  plant, rnd: as for chunked_forward (test infrastructure)."""
     query, key, value, g, beta = (x.detach().to(F64) for x in (query, key, value, g, beta))
     B, T, H, DK = query.shape
     DV = value.shape[-1]
@@ -227,12 +287,13 @@ def dropin_f64(query, key, value, g, beta, initial_state=None, do=None, dsT=None
     qr = query.clone().requires_grad_(True)
     kr = key.clone().requires_grad_(True)
     q, k = prologue(qr, kr, use_qk_l2norm_in_kernel)
-    o, sT, P = chunked_forward(q.detach(), k.detach(), value, g, beta, s0, C)
+    o, sT, P = chunked_forward(q.detach(), k.detach(), value, g, beta, s0, C, plant=plant, rnd=rnd)
     if do is None and dsT is None:
         return o, sT, None
     do = torch.zeros_like(o) if do is None else do.detach().to(F64)
     dsT = torch.zeros_like(sT) if dsT is None else dsT.detach().to(F64)
-    (dq, dk, dv, dg, db, ds0), _ = chunked_backward(q.detach(), k.detach(), value, g, beta, s0, do, dsT, C, P)
+    (dq, dk, dv, dg, db, ds0), _ = chunked_backward(q.detach(), k.detach(), value, g, beta, s0, do, dsT, C, P,
+                                                    plant=plant, rnd=rnd)
     torch.autograd.backward([q, k], [dq, dk])
     grads = dict(dquery=qr.grad, dkey=kr.grad, dvalue=dv, dg=dg, dbeta=db, dstate=ds0)
     return o, sT, grads

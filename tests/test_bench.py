@@ -5,6 +5,7 @@ import subprocess
 import sys
 
 import pytest
+import torch
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 sys.path.insert(0, ROOT)
@@ -82,3 +83,19 @@ def test_traffic_only_while_the_kernels_match(monkeypatch):
 def test_cpu_info():
     model, physical, allowed, share = bench.cpu_info()
     assert physical >= 1 and allowed >= 1 and share >= 1 and isinstance(model, str)
+
+
+def test_traffic_fingerprint_covers_the_build_flags():
+    """The traffic stamp's fingerprint includes build.py, whose compile flags (chunk_bwd8's scheduler strategy) change
+    the generated code and so its traffic."""
+    assert "build.py" in bench.KERNEL_SOURCES and len(bench.kernel_fingerprint()) == 16
+
+
+def test_bench_draws_the_oracle_generators_inputs():
+    """The bench's seeded CPU draw is the oracle's generator (same order, same seed, same values), so the driver's
+    bench runs on the inputs the parity tests check."""
+    from oracle import gdr
+    mine, _ = bench.make_inputs(1, 1001, "cpu")
+    ref = gdr.config_inputs(1)
+    for n in ("query", "key", "value", "g", "beta", "do"):
+        assert torch.equal(mine[n], ref[n]), n

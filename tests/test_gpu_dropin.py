@@ -470,3 +470,49 @@ def test_kept_prep_operands_change_no_bits(dtype):
     finally:
         op.RECOMPUTE_STATES = old
     assert all(torch.equal(a, b) for a, b in zip(*outs))
+
+
+def test_unfused_prologue_switch():
+    """op.FUSED_NORM = False (the reference's switch, op.py:19-21): the query / key normalisation runs as float32
+    PyTorch operations (autograd through them) and the kernels apply only the scale; outputs and gradients within the
+    bf16 bar of float64."""
+    _say("case fused_norm off")
+    inp = gdr.make_inputs(2, 150, 3, 3, 128, 128, torch.bfloat16, s0=True, seed=31)
+    dsT = torch.randn(2, 3, 128, 128, generator=torch.Generator().manual_seed(32))
+    old = op.FUSED_NORM
+    try:
+        op.FUSED_NORM = False
+        check_dropin(inp, bar=BF16_BAR, dsT=dsT)
+    finally:
+        op.FUSED_NORM = old
+
+
+def test_misaligned_inputs_give_the_aligned_bits():
+    """q, k, v, g, beta, the initial state and dO as contiguous views whose start is not 16-byte aligned (one element
+    into a larger buffer): the drop-in copies them to aligned buffers and returns the bits of aligned inputs, gradients
+    included (the reference's _even, op.py:58-60)."""
+    _say("case misaligned inputs")
+    inp = gdr.make_inputs(1, 100, 2, 2, 128, 128, torch.bfloat16, s0=True, seed=33)
+    dsT = torch.randn(1, 2, 128, 128, generator=torch.Generator().manual_seed(34))
+    names = ("query", "key", "value", "g", "beta", "initial_state")
+
+    def run(shift):
+        bases, leaves = [], []
+        for n in names:
+            x = inp[n].to(DEV)
+            base = torch.zeros(x.numel() + shift, device=DEV, dtype=x.dtype)
+            base[shift:] = x.reshape(-1)
+            base.requires_grad_(True)
+            bases.append(base)
+            leaves.append(base[shift:].view(x.shape))
+        assert shift == 0 or all(t.data_ptr() % 16 for t in leaves)
+        do = torch.zeros(inp["do"].numel() + shift, device=DEV, dtype=inp["do"].dtype)
+        do[shift:] = inp["do"].to(DEV).reshape(-1)
+        o, sT = chunk_gated_delta_rule(*leaves[:5], initial_state=leaves[5], output_final_state=True,
+                                       use_qk_l2norm_in_kernel=True)
+        torch.autograd.backward([o, sT], [do[shift:].view(inp["do"].shape), dsT.to(DEV)])
+        torch.cuda.synchronize()
+        return [o.detach().cpu(), sT.detach().cpu()] + [b.grad[shift:].cpu() for b in bases]
+
+    ref, got = run(0), run(1)
+    assert all(torch.equal(a, b) for a, b in zip(ref, got))

@@ -11,6 +11,8 @@ same q, k values either way.
 import pytest
 import torch
 
+import _parity
+
 from macai.gated_delta import chunk_gated_delta_rule, recurrent_gated_delta_rule
 from oracle import gdr
 
@@ -60,9 +62,7 @@ def test_grouped_heads_fwd_bwd(shape, dtype):
     errs = {"o": gdr.rel(o, ro), "sT": gdr.rel(sT, rsT)}
     errs.update({n: gdr.rel(g[n], rg[n]) for n in NAMES})
     _say("errors:", {k: f"{v:.2e}" for k, v in errs.items()})
-    bar = 1e-2 if dtype == torch.bfloat16 else 2e-4
-    bad = {n: e for n, e in errs.items() if not e <= bar}
-    assert not bad, f"over {bar}: {bad}"
+    _parity.check(errs, 1e-2 if dtype == torch.bfloat16 else 2e-4)
     # the forward reads the same q, k values as the repeated layout: the same bits
     o_rep, sT_rep, _ = _run(inp, dsT)
     assert torch.equal(o, o_rep) and torch.equal(sT, sT_rep)

@@ -10,6 +10,8 @@ the float64 oracle by test_gpu_dropin.py; one fp32 case is also checked against 
 import pytest
 import torch
 
+import _parity
+
 from macai.gated_delta import chunk_gated_delta_rule
 from oracle import gdr
 
@@ -78,17 +80,16 @@ def test_packed_rows_against_the_oracle():
     lens = [100, 37, 64]
     row, s0, dsT, cu = _inputs(lens, 2, 2, 64, 64, torch.float32, seed=50)
     o, sT, g = _run(row, s0, dsT, cu)
-    t, errs = 0, []
+    t, errs = 0, {}
     for n, L in enumerate(lens):
         ro, rsT, rg = gdr.dropin_f64(*(row[k][:, t:t + L] for k in ("query", "key", "value", "g", "beta")),
                                      initial_state=s0[n:n + 1], do=row["do"][:, t:t + L], dsT=dsT[n:n + 1])
-        errs += [gdr.rel(o[:, t:t + L], ro), gdr.rel(sT[n:n + 1], rsT)]
+        errs[f"o{n}"], errs[f"sT{n}"] = gdr.rel(o[:, t:t + L], ro), gdr.rel(sT[n:n + 1], rsT)
         for i, name in enumerate(("dquery", "dkey", "dvalue", "dg", "dbeta")):
-            errs.append(gdr.rel(g[i][:, t:t + L], rg[name]))
-        errs.append(gdr.rel(g[5][n:n + 1], rg["dstate"]))
+            errs[f"{name}{n}"] = gdr.rel(g[i][:, t:t + L], rg[name])
+        errs[f"dstate{n}"] = gdr.rel(g[5][n:n + 1], rg["dstate"])
         t += L
-    _say("max error", max(errs))
-    assert max(errs) <= 2e-4
+    _parity.check(errs, 2e-4)
 
 
 @pytest.mark.parametrize("lens,Hk,Hv,dtype", [([130, 0, 64, 6, 200], 2, 2, torch.bfloat16),

@@ -3,6 +3,8 @@ inputs already normalised (the GatedDeltaRule contract), ragged lengths."""
 import pytest
 import torch
 
+import _parity
+
 from oracle import gdr
 
 from _gpu import passes
@@ -30,10 +32,7 @@ def test_passes_fp32(shape):
     ref.update(dict(zip(NAMES, grads)))
     assert r["W2_equal"], "the forward- and backward-mode preps must give the same bits"
     assert r["store_equal"], "the output pass storing the states must give the output and recompute passes' bits"
-    errs = {n: gdr.rel(r[n], ref[n]) for n in ref}
-    print(errs)
-    bad = {n: e for n, e in errs.items() if not e < 2e-4}
-    assert not bad, bad
+    _parity.check({n: gdr.rel(r[n], ref[n]) for n in ref}, 2e-4)
 
 
 @pytest.mark.parametrize("shape", [(1, 64, 1, 128, 128), (2, 100, 3, 64, 64), (1, 37, 2, 128, 64), (1, 130, 2, 32, 96),
@@ -60,10 +59,7 @@ def test_passes_bf16(shape):
     r = passes(bf(q), bf(k), bf(v), f32(g), f32(b), f32(s0), bf(do), f32(dsT))
     assert r["W2_equal"] and r["store_equal"]
     ref = dict(o=o, sT=sT, **dict(zip(NAMES, grads)))
-    errs = {n: gdr.rel(r[n].double(), ref[n]) for n in ref}
-    print(errs)
-    bad = {n: e for n, e in errs.items() if not e < 1e-2}
-    assert not bad, bad
+    _parity.check({n: gdr.rel(r[n].double(), ref[n]) for n in ref}, 1e-2)
 
 
 @pytest.mark.parametrize("shape,dtype,split", [((2, 150, 3, 3, 128, 128), torch.bfloat16, 0),
@@ -148,9 +144,7 @@ def test_segment_maps_and_scan(dtype, T, P, DK, DV):
         errs[f"A{s}"] = gdr.rel(maps[s:s + 1, :, :, :DK], A)
         errs[f"B{s}"] = gdr.rel(maps[s:s + 1, :, :, DK:], Bm)
         errs[f"start{s}"] = gdr.rel(starts[s:s + 1], Pr["Sc"][:, :, c0[s]])
-    print({n: f"{v_:.1e}" for n, v_ in errs.items()}, flush=True)
-    bad = {n: v_ for n, v_ in errs.items() if not v_ < bar}
-    assert not bad, bad
+    _parity.check(errs, bar)
 
 
 @pytest.mark.parametrize("dtype,P,DK", [(torch.float32, 2, 128), (torch.float32, 4, 128), (torch.bfloat16, 2, 128),
@@ -182,6 +176,4 @@ def test_segmented_forward(dtype, P, DK):
     assert len(ran) == 1 and ran[0].startswith(f"fwd seg{P} "), ran
     ro, rsT, _ = gdr.dropin_f64(*(inp[n] for n in names + ("initial_state",)))
     bar = 1e-2 if dtype == torch.bfloat16 else 2e-4
-    errs = {"o": gdr.rel(o.cpu(), ro), "sT": gdr.rel(sT.cpu(), rsT)}
-    print(errs, flush=True)
-    assert all(v_ < bar for v_ in errs.values()), errs
+    _parity.check({"o": gdr.rel(o.cpu(), ro), "sT": gdr.rel(sT.cpu(), rsT)}, bar)

@@ -254,12 +254,19 @@ def test_patch_swaps_the_name_and_restores_it():
     assert mod.torch_chunk_gated_delta_rule is orig and mod.torch_recurrent_gated_delta_rule is orig_dec
     done = patch.install(layer=False, training=False, lora=False)
     try:
-        assert ("transformers.models.qwen3_5.modeling_qwen3_5", patch.NAME) in done
+        # the reference's return value: the paths of the modules patched (patch.py:33-56)
+        assert "transformers.models.qwen3_5.modeling_qwen3_5" in done and all(isinstance(p, str) for p in done)
+        assert ("transformers.models.qwen3_5.modeling_qwen3_5", patch.NAME) in patch.swapped()
         assert mod.torch_recurrent_gated_delta_rule is orig_dec
         assert patch.install(layer=False, training=False, lora=False) == []           # idempotent
+        assert patch.install(False, False, False, decode=True) == done                # adds the decode name
+        assert mod.torch_recurrent_gated_delta_rule is recurrent_gated_delta_rule
     finally:
         patch.uninstall()
-    assert mod.torch_chunk_gated_delta_rule is orig
+    assert mod.torch_chunk_gated_delta_rule is orig and mod.torch_recurrent_gated_delta_rule is orig_dec
+    assert patch.swapped() == []
+    with pytest.raises(TypeError):
+        patch.install(False, False, False, True)       # decode is keyword-only: the fourth position is not taken
 
 
 def test_patch_takes_the_reference_keywords():
@@ -300,3 +307,103 @@ def test_noalloc_forward_refuses_oversized_shapes_before_any_launch():
     rc = L.macai_gdr_forward_noalloc(*([p] * 8), 8, 4096, 32, 32, 128, 128, 1, 1, 1.0, 0, None, 0, None)
     assert rc == N.EINVAL and b"fixed" in L.macai_gdr_last_error()
     assert L.macai_gdr_forward_workspace(4, 1024, 16, 128, 128, 1, 0) <= N.NOALLOC_SCRATCH_BYTES
+
+
+def test_plan_reports_the_launch_choices():
+    """op.plan (the reference's op.py:105-113, here this build's choices), consistent with what the GPU tests see run:
+    config 1's forward at split 4 on the chain-and-output kernel, its recompute backward's pair pass at split 2 and
+    the persistent per-chunk backward; the stored mode's reverse pass; config 3's 8 segments; the float32 path."""
+    p = op.plan(4, 1024, 16, 128, 128, save=True)
+    assert p["fwd_chunk"] == p["bwd_chunk"] == 64 and p["operands"] == "bf16" and p["prep"] == "prep8"
+    assert (p["fwd_split"], p["fwd_state_pass"], p["segments"]) == (4, "state_out", 1)
+    assert (p["recompute"], p["bwd_state_passes"], p["bwd_split"], p["chunk_bwd"]) == (True, "pair", 2, "chunk_bwd8xn")
+    old = op.RECOMPUTE_STATES
+    try:
+        op.RECOMPUTE_STATES = False
+        p = op.plan(4, 1024, 16, 128, 128, save=True)
+        assert (p["recompute"], p["bwd_state_passes"], p["bwd_split"]) == (False, "reverse", 4)
+    finally:
+        op.RECOMPUTE_STATES = old
+    p = op.plan(1, 32768, 16, 128, 128, save=False)
+    assert p["segments"] == 8 and "bwd_state_passes" not in p and p["map_split"] >= 1
+    assert op.plan(1, 32768, 16, 128, 128, save=True)["segments"] == 1     # a training forward never splits
+    p = op.plan(2, 100, 4, 64, 64, save=True, dtype=torch.float32)
+    assert (p["operands"], p["prep"], p["fwd_state_pass"], p["chunk_bwd"]) == ("f32", "prep", "state_fwd", "chunk_bwd")
+    assert op.plan(1, 100, 2, 256, 128, save=True)["operands"] == "f32"      # wide keys run the float32 kernels
+    assert op.plan(4, 100, 2, 128, 128, save=True)["chunk_bwd"] == "chunk_bwd8"   # fewer chunk-heads than CUs
+
+
+def test_misaligned_inputs_are_copied_not_refused():
+    """A contiguous tensor whose start is not 16-byte aligned (a view at an odd offset) reaches the kernels as an
+    aligned copy with the same values (the reference's _even, op.py:58-60); an aligned one passes as it is."""
+    base = torch.arange(40, dtype=torch.float32)
+    x = base[1:33]
+    assert x.is_contiguous() and x.data_ptr() % 16 == 4
+    y = op._as(x, torch.float32)
+    assert y.data_ptr() % 16 == 0 and torch.equal(y, x)
+    z = base[4:36]
+    assert op._as(z, torch.float32) is z
+    h = torch.arange(40, dtype=torch.bfloat16)[3:35]
+    assert op._as(h, torch.bfloat16).data_ptr() % 16 == 0 and torch.equal(op._as(h, torch.bfloat16), h)
+
+
+def test_fused_norm_switch(monkeypatch):
+    """op.FUSED_NORM (the reference's switch, op.py:19-21): True hands the raw query and key to the kernels with the
+    normalisation fused (use_l2norm 1); False normalises them as float32 PyTorch operations (autograd records them),
+    rounds them to the compute dtype and asks the kernels for the scale only (use_l2norm 0)."""
+    seen = {}
+
+    def fake_apply(q, k, v, g, beta, s0, l2norm, q_scale, want_sT, save, pack):
+        seen.update(q=q, k=k, l2norm=l2norm, q_scale=q_scale)
+        return v.new_zeros(v.shape)
+
+    monkeypatch.setattr(op, "_check", lambda *a, **kw: None)
+    monkeypatch.setattr(op._DropIn, "apply", staticmethod(fake_apply))
+    gen = torch.Generator().manual_seed(1)
+    q, k, v = (torch.randn(1, 5, 2, 64, generator=gen).to(torch.bfloat16) for _ in range(3))
+    g, b = -torch.rand(1, 5, 2, generator=gen), torch.rand(1, 5, 2, generator=gen)
+    chunk_gated_delta_rule(q, k, v, g, b, use_qk_l2norm_in_kernel=True)
+    assert seen["l2norm"] is True and seen["q"] is q and seen["q_scale"] == 64 ** -0.5
+    monkeypatch.setattr(op, "FUSED_NORM", False)
+    qr = q.clone().requires_grad_(True)
+    chunk_gated_delta_rule(qr, k, v, g, b, use_qk_l2norm_in_kernel=True)
+    assert seen["l2norm"] is False and seen["q_scale"] == 64 ** -0.5
+    assert seen["q"].dtype == torch.bfloat16 and seen["q"].requires_grad
+    assert torch.equal(seen["q"], op.l2norm(q.float()).to(torch.bfloat16))
+    assert torch.equal(seen["k"], op.l2norm(k.float()).to(torch.bfloat16))
+    chunk_gated_delta_rule(q, k, v, g, b, use_qk_l2norm_in_kernel=False)      # nothing to normalise either way
+    assert seen["l2norm"] is False and seen["q"] is q
+
+
+def test_gates_and_conv_check_their_arguments():
+    """supported() with the reference's signatures (layer/_gates.py:75, layer/_conv.py:178), and the autograd
+    functions refusing shapes that would make the kernels read past a tensor or mix up heads, before any launch."""
+    from macai.layer import _conv, _gates, conv_qkv, gates
+    H = 4
+    b, a = torch.randn(2, 3, H), torch.randn(2, 3, H)
+    A_log, dt = torch.zeros(H), torch.zeros(H)
+    assert not _gates.supported(b, a, A_log, dt)                 # CPU tensors: the kernels run on a HIP device
+    assert _gates._unfit(b, a, A_log, dt) is None
+    with pytest.raises(RuntimeError, match="HIP device"):
+        gates(b, a, A_log, dt)
+    bad = [((b, a[:, :2], A_log, dt), "one shape"), ((b, a.double(), A_log, dt), "dtype"),
+           ((b, a, A_log[None], dt), r"\[H\]"), ((b, a, A_log, dt[:3]), r"\[H\]"),
+           ((torch.randn(2, 3, 5), torch.randn(2, 3, 5), A_log, dt), r"\[H\]"),
+           ((b.to(torch.int32), a.to(torch.int32), A_log, dt), "dtype")]
+    for args, msg in bad:
+        assert _gates._unfit(*args) is not None
+        with pytest.raises(ValueError, match=msg):
+            gates(*args)
+    kd, dk, dv, rep = 32, 16, 16, 2                              # 2 key heads, 4 value heads
+    C = 2 * kd + 4 * dv
+    x, w = torch.randn(2, 9, C), torch.randn(C, 1, 4)
+    assert not _conv.supported(x, w, kd, dk, rep, dv) and _conv._unfit(x, w, kd, dk, rep, dv) is None
+    with pytest.raises(RuntimeError, match="HIP device"):
+        conv_qkv(x, w, kd, dk, rep, dv)
+    bad = [((x[0], w, kd, dk, rep, dv), r"\[B, T, C\]"), ((x, w[:-1], kd, dk, rep, dv), "taps"),
+           ((x, w, kd, dk, 3, dv), "key_dim"), ((x, w, 24, 12, rep, dv), "key_dim"),
+           ((x.to(torch.int32), w, kd, dk, rep, dv), "float32")]
+    for args, msg in bad:
+        assert _conv._unfit(*args) is not None
+        with pytest.raises(ValueError, match=msg):
+            conv_qkv(*args)

@@ -7,6 +7,7 @@ import numpy as np
 import pytest
 import torch
 
+import _chain
 from oracle import gdr
 
 F64 = torch.float64
@@ -246,3 +247,37 @@ def test_segment_map_composes_the_state_pass():
     A2, B2 = gdr.segment_map(q[:, h:], k[:, h:], v[:, h:], g[:, h:], b[:, h:])
     assert (A2 @ (A1 @ s0 + B1) + B2 - sT).abs().max() < 1e-12
     assert (A1 @ (A2 @ s0 + B2) + B1 - sT).abs().max() > 1e-3
+
+
+@pytest.mark.parametrize("name", list(_chain.CASES))
+def test_chain_cases_catch_planted_mistakes(name):
+    """The many-chunk chain cases of tests/test_gpu_chain.py have teeth: on exactly their inputs, a carried decay of
+    gamma_last^2 instead of gamma_last, and G_last taken from the row before the chunk's last, each planted in the
+    forward chain and (for the cases with a backward) in the reverse chain, move some output or gradient by more than
+    twice the largest bar those tests apply (1e-2 for bf16; the float32 bars are 2x a float32 error, far smaller).  So
+    a kernel with such a mistake fails them even with its own rounding (a few 1e-3) on top."""
+    plants = gdr.PLANTS if _chain.CASES[name]["kind"] != "prefill" else ("fwd_gamma_sq", "fwd_glast_off")
+    for seed in _chain.seeds(name):
+        inp = _chain.inputs(name, seed)
+        ref = _chain.oracle(name, inp)
+        for plant in plants:
+            errs = _chain.errors(_chain.oracle(name, inp, plant), ref)
+            worst = max(errs, key=errs.get)
+            print(name, seed, plant, worst, f"{errs[worst]:.2e}", flush=True)
+            assert errs[worst] > 2 * _chain.BF16_BAR, (name, seed, plant, errs)
+
+
+def test_bf16_rounding_model_is_off_by_default():
+    """The precision model (rnd) rounds nothing unless asked, and rounding to bf16 is torch's round-to-nearest-even:
+    with rnd=() the forward and backward are the pinned equations bit for bit."""
+    xs = gdr.harness_inputs(1, 90, 2, 16, 8, seed=3)
+    gen = torch.Generator().manual_seed(4)
+    do = torch.randn(1, 90, 2, 8, generator=gen, dtype=F64)
+    dsT = torch.randn(1, 2, 16, 8, generator=gen, dtype=F64)
+    a, _ = gdr.chunked_backward(*xs, do, dsT, 64)
+    b, _ = gdr.chunked_backward(*xs, do, dsT, 64, rnd=())
+    assert all(torch.equal(x, y) for x, y in zip(a, b))
+    x = torch.tensor([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -3.14159], dtype=F64)
+    assert torch.equal(gdr.bf16(x), torch.tensor([1.0, 1.0 + 2 ** -6, -3.140625], dtype=F64))
+    c, _ = gdr.chunked_backward(*xs, do, dsT, 64, rnd=gdr.ROUNDABLE)
+    assert 1e-5 < max(gdr.rel(u, v) for u, v in zip(c, a)) < 3e-2
