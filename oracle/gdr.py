@@ -104,9 +104,10 @@ def chunk_prep(k, v, g, beta, q=None, C=64):
 PLANTS = ("fwd_gamma_sq", "fwd_glast_off", "bwd_gamma_sq", "bwd_glast_off")
 # Operand classes that the bf16 kernels feed to bf16 MFMA products (the rest is fp32): prep's stored W, Ke = diag(e) K,
 # Qg = diag(gamma) Q, M and A; the state S and its gradient dS as product operands; Vn and dVn; the per-chunk
-# backward's chunk state Sc and its normalised q, k ("QK").  `rnd` rounds the named classes to bf16 where they enter a
-# product (the precision model of the bf16 path; no rounding by default).
-ROUNDABLE = ("W", "Ke", "Qg", "M", "A", "S", "dS", "Vn", "dVn", "Sc", "QK")
+# backward's chunk state Sc, its normalised q, k ("QK") and the intermediates it forms and feeds to further products
+# ("CC": dM, dW, dA, dA A^T and the decayed dL).  `rnd` rounds the named classes to bf16 where they enter a product (the
+# precision model of the bf16 path; no rounding by default).
+ROUNDABLE = ("W", "Ke", "Qg", "M", "A", "S", "dS", "Vn", "dVn", "Sc", "QK", "CC")
 
 
 def bf16(x):
@@ -231,19 +232,22 @@ def chunked_backward(q, k, v, g, beta, s0, do, dsT, C=64, P=None, plant=None, rn
     Ar, Scr, Vnr, dVnr, Kr, Qr = R("A", A), R("Sc", Sc), R("Vn", Vn), R("dVn", dVn), R("QK", K), R("QK", Q)
     dOVt = dO @ tr(Vnr)                                                    # B3
     dM = Gam * dOVt
+    dMr = R("CC", dM)
     dOSt = dO @ tr(Scr)
-    dQ = gam[..., None] * dOSt + dM @ Kr
+    dQ = gam[..., None] * dOSt + dMr @ Kr
     VndSt = Vnr @ tr(dSn)
-    dK = tr(dM) @ Qr + e[..., None] * VndSt
+    dK = tr(dMr) @ Qr + e[..., None] * VndSt
     dW = -dVnr @ tr(Scr)
-    X, Y = tr(Ar) @ dW, tr(Ar) @ dVnr                                      # B5
+    dWr = R("CC", dW)
+    X, Y = tr(Ar) @ dWr, tr(Ar) @ dVnr                                     # B5
     bg = bc * gam
     dK = dK + bg[..., None] * X
     dV = bc[..., None] * Y
-    dA = torch.where(low, dW @ tr(bg[..., None] * Kr) + dVnr @ tr(bc[..., None] * V), torch.zeros_like(A))
-    dL = torch.where(low, -tr(Ar) @ dA @ tr(Ar), torch.zeros_like(A))
+    dA = torch.where(low, dWr @ tr(bg[..., None] * Kr) + dVnr @ tr(bc[..., None] * V), torch.zeros_like(A))
+    dL = torch.where(low, -tr(Ar) @ R("CC", R("CC", dA) @ tr(Ar)), torch.zeros_like(A))
     Pm = dL * Gam
-    dK = dK + bc[..., None] * (Pm @ Kr) + tr(Pm) @ (bc[..., None] * Kr)
+    Pr = R("CC", Pm)
+    dK = dK + bc[..., None] * (Pr @ Kr) + tr(Pr) @ (bc[..., None] * Kr)
     KG = P["KK"] * Gam
     R2 = dL * KG
     kx = (K * X).sum(-1)
