@@ -494,9 +494,11 @@ def bench_producers(cfg, reps=20):
 
 def bench_ceilings(args, mib=1024, reps=10):
     """The device's own streaming rates (macai_gdr_probe_stream: read-only, write-only and copy over `mib` MiB in
-    16-byte units, grid-stride; the best of a few workgroup counts, each timed with HIP events over `reps` launches)
-    and the floor they put under the config's training step: every kernel's algorithmic reads at the read rate plus
-    its writes at the write rate, summed over the step's launches (the recompute mode and the stored-states mode)."""
+    16-byte units, grid-stride; the best of a few workgroup counts, each timed with HIP events over `reps` launches),
+    its matrix cores' throughput (macai_gdr_probe_mfma: back-to-back MFMAs of the kernels' bf16 and fp32 shapes and
+    the larger bf16 one, the best of a few workgroup counts), and the floor the streams put under the config's
+    training step: every kernel's algorithmic reads at the read rate plus its writes at the write rate, summed over the
+    step's launches (the recompute mode and the stored-states mode)."""
     from macai.gated_delta import _native as N
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
@@ -513,6 +515,19 @@ def bench_ceilings(args, mib=1024, reps=10):
             if best is None or sec < best[0]:
                 best = (sec, blocks)
         rates[name] = {"GB/s": round(moved / best[0] / 1e9, 1), "blocks": best[1], "us": round(best[0] * 1e6, 2)}
+    mfma = {}
+    out = torch.empty(16384 * 256, device=dev)
+    for mode, name, peak in ((0, "bf16 16x16x32", MFMA_PEAK["bf16"]), (1, "f32 16x16x4", MFMA_PEAK["f32"]),
+                             (2, "bf16 32x32x16", MFMA_PEAK["bf16"])):
+        best = None
+        for blocks in (1024, 2048, 4096):
+            iters = 4096 if mode != 1 else 2048
+            sec = _events_time(lambda: N.call("macai_gdr_probe_mfma", mode, iters, N.ptr(out), blocks, st), 3)
+            fl = N.lib().macai_gdr_probe_mfma_flops(mode, iters, blocks) / sec
+            if best is None or fl > best[0]:
+                best = (fl, blocks, sec)
+        mfma[name] = {"TFLOP/s": round(best[0] / 1e12, 1), "of_peak": round(best[0] / peak, 4),
+                      "peak_TFLOP/s": peak / 1e12, "blocks": best[1], "us": round(best[2] * 1e6, 1)}
     c = CONFIGS[args.config]
     floors = {}
     for mode, keep in (("recompute", False), ("stored", True)):
@@ -528,7 +543,7 @@ def bench_ceilings(args, mib=1024, reps=10):
             "value": rates["copy"]["GB/s"], "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
             "data": "synthetic", "config": {"workload": f"{mib} MiB streams; step floor of BASELINE config "
                                                         f"{args.config}"},
-            "peak": HBM_PEAK / 1e9, "rates": rates, "step_floor": floors}
+            "peak": HBM_PEAK / 1e9, "rates": rates, "mfma": mfma, "step_floor": floors}
     print(json.dumps(line), flush=True)
 
 

@@ -51,7 +51,7 @@
 extern "C" {
 #endif
 
-#define MACAI_GDR_ABI_VERSION 11
+#define MACAI_GDR_ABI_VERSION 12
 
 /* dtype codes (the rule takes F32 and BF16; the producers also F16) */
 #define MACAI_GDR_F32 0
@@ -222,6 +222,14 @@ int macai_gdr_gates_bwd(const void* b, const void* a, const float* A_log, const 
  * reads `bytes` from src (dst: a 16-byte sink, written by practically no lane), 1 writes them to dst, 2 copies src to
  * dst; 16-byte units, grid-stride over `blocks` workgroups of 256 lanes. */
 int macai_gdr_probe_stream(int32_t mode, const void* src, void* dst, int64_t bytes, int32_t blocks, void* stream);
+
+/* A probe of the matrix cores' throughput (no counterpart in the reference; the MFMA half of its bench/hw_ceilings.py,
+ * bench.py --ceilings): `blocks` workgroups of 4 waves, each wave `iters` rounds of 8 independent chains of one MFMA,
+ * mode 0 v_mfma_f32_16x16x32_bf16 (the bf16 kernels' shape), 1 v_mfma_f32_16x16x4_f32 (the float32 kernels'), 2
+ * v_mfma_f32_32x32x16_bf16; out: blocks x 256 floats (the accumulators' sums).  macai_gdr_probe_mfma_flops gives the
+ * FLOP count of such a launch (2 per multiply-add), or -1 for bad arguments. */
+int macai_gdr_probe_mfma(int32_t mode, int32_t iters, void* out, int32_t blocks, void* stream);
+int64_t macai_gdr_probe_mfma_flops(int32_t mode, int32_t iters, int32_t blocks);
 
 #ifdef __cplusplus
 }

@@ -160,9 +160,11 @@ __device__ __forceinline__ Frag<MT> cvt(const Frag<float>& x, float s = 1.0f) {
 // ---------------------------------------------------------------------------------------------------------------------
 template <typename IT, typename MT, int DK>
 __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
-  // Key features are staged DKS at a time (DK = 256 in two passes), so the tiles fit LDS at every key width: the
-  // products over the key features accumulate across the passes, and W is formed a pass of columns at a time.
-  constexpr int DKS = DK > 128 ? 128 : DK;
+  // Key features are staged DKS at a time, so the tiles fit LDS at every key width: the products over the key features
+  // accumulate across the passes, and W is formed a pass of columns at a time.  float32 tiles of up to 192 columns
+  // fit in one pass (256: two of 128; 224: seven of 32).
+  constexpr int DKS = (DK <= 192 || sizeof(MT) == 2) ? DK : (DK % 128 == 0 ? 128 : 32);
+  static_assert(DK % DKS == 0 && DKS % 32 == 0, "prep key-column passes");
   constexpr int NPASS = DK / DKS;
   constexpr int KP = DKS + 8;  // pitch of [C][DKS] tiles (elements)
   constexpr int CP = C + 8;    // pitch of [*][C] MT tiles
@@ -529,7 +531,9 @@ __global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = r0 + r;
-        const float gm = (row >= s) ? expf((float)(cs.G[row] - Gs)) : 0.f;   // mask before the exponent
+        // mask before the exponent; the hardware exp2 (a bf16 kernel: its ~1e-6 relative error is far below the
+        // operands'; 2-3% off the kernel against the library expf)
+        const float gm = (row >= s) ? __builtin_amdgcn_exp2f((float)(cs.G[row] - Gs) * 1.4426950408889634f) : 0.f;
         sL[row * FP + s] = (row > s) ? b4[r] * (KK[i][r] * (rk4[r] * rks)) * gm : 0.f;
         sM[row * CP + s] = (bf16)((row >= s) ? QK[i][r] * (rq4[r] * qs * rks) * gm : 0.f);
       }
@@ -1642,9 +1646,10 @@ __device__ __forceinline__ Frag<MT> zero_frag() {
 // (q^ = q rq DK^-1/2, k^ = k rk) are applied to the products' rows and columns, and folded into the stored dM and Z, so
 // the raw inputs are the MFMA operands.  Wave w owns key-column blocks w, w + 4, ... of the [C x DK] products, column
 // block w of the [C x C] ones and value-column blocks w, w + 4, ...
-template <typename MT, int DK, int DV>
+template <typename MT, int DK, int DVT>
 __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
   static_assert(sizeof(MT) == 4, "bf16 operands take chunk_bwd8_kernel");
+  const int DV = DVT ? DVT : a.DV;        // DVT = 0: the value width at run time (a multiple of 32)
   constexpr int KP = DK + 8, CP = C + 8;
   constexpr int NBD = DK / 16;            // 16-column blocks of the key width
   constexpr int NBW = (NBD + 3) / 4;      // most blocks a wave owns
@@ -2936,14 +2941,19 @@ __global__ void __launch_bounds__(256) group_sum_kernel(const T* x, T* y, int64_
 }
 
 
+// Key head widths: every multiple of 32 up to 256 (float32 operands; bf16 operands take 32, 64 and 128).
+[[maybe_unused]] static bool key_width_ok(int64_t DK) { return DK >= 32 && DK <= 256 && DK % 32 == 0; }
+
 [[maybe_unused]] static int check_common(const char* what, int64_t B, int64_t T, int64_t H, int64_t DK, int64_t DV,
                                          int dtype) {
   if (B < 1 || T < 1 || H < 1) return fail(MACAI_GDR_EINVAL, "%s: B, T, H must be >= 1 (got %lld, %lld, %lld)", what,
                                            (long long)B, (long long)T, (long long)H);
-  if (DK != 32 && DK != 64 && DK != 128 && DK != 256)
-    return fail(MACAI_GDR_EUNSUP, "%s: key head width must be 32, 64, 128 or 256 (got %lld)", what, (long long)DK);
-  if (DK == 256 && dtype != MACAI_GDR_F32)
-    return fail(MACAI_GDR_EUNSUP, "%s: key head width 256 takes float32 operands (got dtype code %d)", what, dtype);
+  if (!key_width_ok(DK))
+    return fail(MACAI_GDR_EUNSUP, "%s: key head width must be a multiple of 32 in [32, 256] (got %lld)", what,
+                (long long)DK);
+  if (DK != 32 && DK != 64 && DK != 128 && dtype != MACAI_GDR_F32)
+    return fail(MACAI_GDR_EUNSUP, "%s: key head width %lld takes float32 operands (bf16: 32, 64, 128; got dtype code %d)",
+                what, (long long)DK, dtype);
   if (DV < 32 || DV % 32 != 0 || DV > 512)
     return fail(MACAI_GDR_EUNSUP, "%s: value head width must be a multiple of 32 in [32, 512] (got %lld)", what,
                 (long long)DV);
@@ -2983,12 +2993,16 @@ __global__ void __launch_bounds__(256) group_sum_kernel(const T* x, T* y, int64_
     case 64: { constexpr int DKC = 64; __VA_ARGS__; } break;   \
     default: { constexpr int DKC = 128; __VA_ARGS__; } break;  \
   }
-// float32 operands also take key width 256 (the fp32 kernels stage key columns in passes or read chunk tiles from
-// global memory where LDS is too small)
+// float32 operands take every multiple of 32 up to 256 (the fp32 kernels stage key columns in passes or read chunk
+// tiles from global memory where LDS is too small)
 #define DISPATCH_DK_F32(DK, ...)                               \
   switch (DK) {                                                \
     case 32: { constexpr int DKC = 32; __VA_ARGS__; } break;   \
     case 64: { constexpr int DKC = 64; __VA_ARGS__; } break;   \
+    case 96: { constexpr int DKC = 96; __VA_ARGS__; } break;   \
+    case 160: { constexpr int DKC = 160; __VA_ARGS__; } break; \
+    case 192: { constexpr int DKC = 192; __VA_ARGS__; } break; \
+    case 224: { constexpr int DKC = 224; __VA_ARGS__; } break; \
     case 256: { constexpr int DKC = 256; __VA_ARGS__; } break; \
     default: { constexpr int DKC = 128; __VA_ARGS__; } break;  \
   }
@@ -3243,8 +3257,9 @@ int macai_gdr_state_scan(const float* maps, const float* s0, float* starts, int6
   const char* what = "macai_gdr_state_scan";
   if (rows < 1 || nseg < 1 || H < 1 || rows > 65535 || H > 65535)
     return fail(MACAI_GDR_EINVAL, "%s: rows, segments and heads must be >= 1 (and rows, heads <= 65535)", what);
-  if (DK != 32 && DK != 64 && DK != 128 && DK != 256)
-    return fail(MACAI_GDR_EUNSUP, "%s: key head width must be 32, 64, 128 or 256 (got %lld)", what, (long long)DK);
+  if (!key_width_ok(DK))
+    return fail(MACAI_GDR_EUNSUP, "%s: key head width must be a multiple of 32 in [32, 256] (got %lld)", what,
+                (long long)DK);
   if (DV < 16 || DV % 16 != 0 || DV > 512)
     return fail(MACAI_GDR_EUNSUP, "%s: value head width must be a multiple of 16 in [16, 512] (got %lld)", what,
                 (long long)DV);
@@ -3272,9 +3287,11 @@ int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float
   if (!rc) rc = check_heads(what, H, Hk);
   if (!rc) rc = pack_chunks(what, pack, NT_packed, B, T, &NT);
   if (rc) return rc;
-  if (DV != 32 && DV != 64 && DV != 96 && DV != 128)
-    return fail(MACAI_GDR_EUNSUP, "%s: the backward takes value head widths 32, 64, 96 or 128 (got %lld)", what,
+  if (dtype != MACAI_GDR_F32 && DV != 32 && DV != 64 && DV != 96 && DV != 128)
+    return fail(MACAI_GDR_EUNSUP, "%s: the bf16 backward takes value head widths 32, 64, 96 or 128 (got %lld)", what,
                 (long long)DV);
+  if (DV > 256)
+    return fail(MACAI_GDR_EUNSUP, "%s: the backward takes value head widths up to 256 (got %lld)", what, (long long)DV);
   if (!q || !k || !v || !g || !beta || !dO || !A || !Sc || !dSn || !Vn || !dVn || !dq || !dk || !dv || !dg ||
       !dbeta)
     return fail(MACAI_GDR_EINVAL, "%s: null pointer", what);
@@ -3292,12 +3309,17 @@ int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float
     if (!xn && cus > 0 && units >= 2 * (int64_t)cus) a.stagger = cus;   // (the persistent form measured slower with it)
   }
   hipStream_t st = (hipStream_t)stream;
+// (the key widths 32, 64, 128 and 256 with value widths up to 128 have their value width as a template constant; every
+// other width pair takes it at run time, DV = 0 below)
 #define LAUNCH_CB(MT)                                                                                               \
-  DISPATCH_DK_F32(DK, switch (DV) {                                                                                    \
+  DISPATCH_DK_F32(DK, if constexpr (DKC != 32 && DKC != 64 && DKC != 128 && DKC != 256) {                             \
+    hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 0>), grid, dim3(256), 0, st, a);                                     \
+  } else switch (DV) {                                                                                                 \
     case 32: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 32>), grid, dim3(256), 0, st, a); break;                \
     case 64: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 64>), grid, dim3(256), 0, st, a); break;                \
     case 96: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 96>), grid, dim3(256), 0, st, a); break;                \
-    default: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 128>), grid, dim3(256), 0, st, a); break;               \
+    case 128: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 128>), grid, dim3(256), 0, st, a); break;              \
+    default: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 0>), grid, dim3(256), 0, st, a); break;                 \
   })
   if (dtype == MACAI_GDR_F32) {
     LAUNCH_CB(float);

@@ -15,7 +15,7 @@ F32, BF16, F16 = 0, 1, 2
 OK, EINVAL, EUNSUP, ELAUNCH = 0, 1, 2, 3
 STORE_STATES, NO_OUTPUT = 1, 8
 NOALLOC_SCRATCH_BYTES = 128 << 20     # MACAI_GDR_NOALLOC_SCRATCH_BYTES
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _p, _i64, _i32, _f = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 # name -> argument types (the order of include/macai_gdr.h)
@@ -38,9 +38,11 @@ SIGNATURES = {
     "macai_gdr_forward_workspace": [_i64] * 5 + [_i32, _i64],
     "macai_gdr_forward_noalloc": [_p] * 8 + [_i64] * 6 + [_i32, _i32, _f, _i32, _p, _i64, _p],
     "macai_gdr_probe_stream": [_i32, _p, _p, _i64, _i32, _p],
+    "macai_gdr_probe_mfma": [_i32, _i32, _p, _i32, _p],
+    "macai_gdr_probe_mfma_flops": [_i32, _i32, _i32],
 }
 # the rest return an int status
-RESTYPES = {"macai_gdr_conv_partials": _i64, "macai_gdr_forward_workspace": _i64}
+RESTYPES = {"macai_gdr_conv_partials": _i64, "macai_gdr_forward_workspace": _i64, "macai_gdr_probe_mfma_flops": _i64}
 
 _lib = None
 _fns = {}        # name -> the library's function object (a lookup per call costs host time on every launch)

@@ -17,9 +17,15 @@ import torch
 from . import _native as N
 
 CHUNK = 64   # chunk length of the kernels; the drop-in's chunk_size is accepted and not used (as op.py:266-269)
-# The widest key head the bf16 kernels take; wider ones (256, the reference's widest tested, tests/test_harness.py:214-230)
-# run the float32 kernels, with 2-byte inputs upcast exactly and the results cast back.
+# Head widths.  The float32 kernels take key heads of every multiple of 32 up to 256 and, in the backward, value heads
+# of every multiple of 32 up to 256 (the reference takes any multiple of 32: op.py:124-125, _chunked.py:1228-1229; its
+# tests reach 256, tests/test_harness.py:214-230).  The bf16 kernels take key heads of 32, 64 and 128 and, in the
+# backward, value heads up to 128: other widths run the float32 kernels, with 2-byte inputs upcast exactly and the
+# results cast back.
 BF16_MAX_DK = 128
+BF16_DK = (32, 64, 128)
+BF16_MAX_DV_BWD = 128
+MAX_DK = MAX_DV_BWD = 256
 # FUSED_NORM (the reference's switch and default, op.py:19-21): with use_qk_l2norm_in_kernel=True the drop-in's
 # query / key prologue (l2 normalisation, the query's DK^-1/2 scale) runs inside the kernels, its backward inside the
 # per-chunk backward (True); False runs the normalisation as PyTorch operations in float32 (autograd takes its
@@ -418,7 +424,8 @@ class GatedDeltaRule(torch.autograd.Function):
     def forward(ctx, q, k, v, g, beta, s0, save: bool):
         _check(q, k, v, g, beta, s0)
         ctx.io_dtype = q.dtype             # o and the q, k, v gradients come back in it
-        if q.dtype != torch.float32 and (q.shape[-1] > BF16_MAX_DK or not BF16_OPERANDS):
+        _widths(q.shape[-1], v.shape[-1], save)
+        if q.dtype != compute_dtype(q.dtype, q.shape[-1], v.shape[-1], save):
             q, k, v = q.float(), k.float(), v.float()
         q, k, v = (_as(t, t.dtype) for t in (q, k, v))
         g, beta, s0 = (_as(t, torch.float32) for t in (g, beta, s0))
@@ -475,11 +482,22 @@ def l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     return x * torch.rsqrt((x * x).sum(dim=-1, keepdim=True) + eps)
 
 
-def compute_dtype(dtype, DK: int):
-    """The operand type the kernels compute a call in: bfloat16 inputs on bf16 MFMA up to key width 128 (unless
-    BF16_OPERANDS is off); float16, float32 and wider keys on the float32 kernels."""
-    bf16 = dtype == torch.bfloat16 and DK <= BF16_MAX_DK and BF16_OPERANDS
+def compute_dtype(dtype, DK: int, DV: int = 0, save: bool = False):
+    """The operand type the kernels compute a call in: bfloat16 inputs on bf16 MFMA at key widths 32, 64, 128 and --
+    when the call saves for a backward -- value widths up to 128 (unless BF16_OPERANDS is off); float16, float32 and
+    other widths on the float32 kernels."""
+    bf16 = (dtype == torch.bfloat16 and DK in BF16_DK and BF16_OPERANDS and (not save or DV <= BF16_MAX_DV_BWD))
     return torch.bfloat16 if bf16 else torch.float32
+
+
+def _widths(DK: int, DV: int, save: bool):
+    """Refuse head widths no kernel takes, before any work (the C ABI refuses them too)."""
+    if DK % 32 or not 32 <= DK <= MAX_DK:
+        raise NotImplementedError(f"key head width must be a multiple of 32 in [32, {MAX_DK}], got {DK}")
+    if DV % 32 or not 32 <= DV <= 512:
+        raise NotImplementedError(f"value head width must be a multiple of 32 in [32, 512], got {DV}")
+    if save and DV > MAX_DV_BWD:
+        raise NotImplementedError(f"the backward takes value head widths up to {MAX_DV_BWD}, got {DV}")
 
 
 def eager_prologue(query, key, cdt):
@@ -497,7 +515,7 @@ def plan(B: int, T: int, H: int, DK: int, DV: int, save: bool, Hk: int = None, d
     (RECOMPUTE_STATES), its state passes, their split and the per-chunk backward's kernel.  cus: the device's compute
     units (the persistent per-chunk backward runs where there are more chunk-heads than CUs)."""
     Hk = Hk or H
-    cdt = compute_dtype(dtype, DK)
+    cdt = compute_dtype(dtype, DK, DV, save)
     bf = cdt == torch.bfloat16
     NT = math.ceil(T / CHUNK)
     recompute = save and RECOMPUTE_STATES
@@ -540,7 +558,10 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size: int = 64, ini
     cu = kwargs.get("cu_seqlens")
     pack = None if cu is None else _pack(cu, query.shape[1], query.device)
     dtype = query.dtype
-    cdt = compute_dtype(dtype, query.shape[-1])
+    grads = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (query, key, value, g, beta, initial_state))
+    _widths(query.shape[-1], value.shape[-1], grads)
+    cdt = compute_dtype(dtype, query.shape[-1], value.shape[-1], grads)
     if use_qk_l2norm_in_kernel and not FUSED_NORM:
         query, key = eager_prologue(query, key, cdt)
         use_qk_l2norm_in_kernel = False

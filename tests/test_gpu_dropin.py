@@ -516,3 +516,30 @@ def test_misaligned_inputs_give_the_aligned_bits():
 
     ref, got = run(0), run(1)
     assert all(torch.equal(a, b) for a, b in zip(ref, got))
+
+
+# ---- head widths beyond the bf16 kernels' (the reference takes any multiple of 32: op.py:124-125) --------------------
+@pytest.mark.parametrize("shape", [(1, 100, 2, 96, 64), (1, 77, 2, 160, 128), (2, 70, 2, 192, 96), (1, 130, 1, 224, 160),
+                                   (1, 90, 2, 128, 256), (1, 65, 2, 64, 192), (1, 100, 1, 256, 224), (1, 40, 2, 32, 256)])
+def test_rule_widths(shape):
+    """Key widths 96, 160, 192, 224 and value widths 160-256 through the backward, on the float32 kernels (key columns
+    staged in one pass up to 192, in passes of 32 at 224; the value width taken at run time by the per-chunk
+    backward): the contract at the harness bar 2e-4, ragged lengths, with a starting state."""
+    _say(f"case rule_widths {shape}")
+    check_rule(gdr.harness_inputs(*shape, seed=2), 2e-4)
+
+
+@pytest.mark.parametrize("DK,DV", [(96, 128), (128, 256), (160, 64)])
+def test_dropin_widths_bf16(DK, DV):
+    """bf16 drop-in at widths the bf16 kernels do not take in the backward: upcast exactly and computed by the float32
+    kernels (outputs and q, k, v gradients returned in bf16), within the 2-byte bar; the forward alone at a value width
+    of 256 stays on the bf16 kernels, within the bf16 bar."""
+    _say(f"case dropin_widths_bf16 DK={DK} DV={DV}")
+    inp = gdr.make_inputs(2, 80, 2, 2, DK, DV, torch.bfloat16, s0=True, seed=17)
+    dsT = torch.randn(2, 2, DK, DV, generator=torch.Generator().manual_seed(18))
+    check_dropin(inp, bar=5e-3, dsT=dsT)
+    if DV > 128:
+        ro, rsT, _ = gdr.dropin_f64(*(inp[n] for n in ("query", "key", "value", "g", "beta", "initial_state")))
+        with torch.no_grad():
+            o, sT, _ = run_dropin(inp, grads=False)
+        _parity.check({"o": gdr.rel(o, ro), "sT": gdr.rel(sT, rsT)}, BF16_BAR)

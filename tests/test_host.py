@@ -90,15 +90,17 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert sm(p, p, p, p, None) == N.EINVAL and b"null" in L.macai_gdr_last_error()
     assert sm(p, p, p + 4, p, p) == N.EINVAL and b"aligned" in L.macai_gdr_last_error()
     assert sm(p, p, p, p, p, split=3) == N.EINVAL and b"split" in L.macai_gdr_last_error()
-    assert sm(p, p, p, p, p, DK=96) == N.EUNSUP
+    assert sm(p, p, p, p, p, DK=96) == N.EUNSUP and b"float32" in L.macai_gdr_last_error()   # bf16: 32, 64, 128
     assert sm(p, p, p, p, p, DK=256) == N.EUNSUP                       # wide keys take float32 operands
+    assert sm(p, p, p, p, p, DK=80, dtype=0) == N.EUNSUP and b"multiple of 32" in L.macai_gdr_last_error()
+    assert sm(p, p, p, p, p, DK=288, dtype=0) == N.EUNSUP
     sc = lambda maps, s0, starts, rows=1, nseg=4, DK=128, DV=128: L.macai_gdr_state_scan(maps, s0, starts, rows, nseg,
                                                                                           2, DK, DV, None)
     assert sc(p, None, None) == N.EINVAL and b"null" in L.macai_gdr_last_error()
     assert sc(p, p + 8, p) == N.EINVAL and b"aligned" in L.macai_gdr_last_error()
     assert sc(p, None, p, nseg=0) == N.EINVAL
     assert sc(p, None, p, rows=70000) == N.EINVAL
-    assert sc(p, None, p, DK=96) == N.EUNSUP
+    assert sc(p, None, p, DK=80) == N.EUNSUP and sc(p, None, p, DK=288) == N.EUNSUP
     assert sc(p, None, p, DV=24) == N.EUNSUP
     gs = lambda x, y, H=4, Hk=2, D=128, dtype=1: L.macai_gdr_group_sum(x, y, 1, 64, H, Hk, D, dtype, None)
     assert gs(p, None) == N.EINVAL and b"null" in L.macai_gdr_last_error()
@@ -407,3 +409,44 @@ def test_gates_and_conv_check_their_arguments():
         assert _conv._unfit(*args) is not None
         with pytest.raises(ValueError, match=msg):
             conv_qkv(*args)
+
+
+def test_mfma_probe_checks_and_counts():
+    """The matrix-core probe's FLOP count (2 per multiply-add: 8 chains x iters x 4 waves a workgroup) and its
+    argument checks, before any launch."""
+    L = N.lib()
+    assert L.macai_gdr_probe_mfma_flops(0, 10, 3) == 16384 * 8 * 10 * 3 * 4
+    assert L.macai_gdr_probe_mfma_flops(1, 10, 3) == 2048 * 8 * 10 * 3 * 4
+    assert L.macai_gdr_probe_mfma_flops(2, 10, 3) == 32768 * 8 * 10 * 3 * 4
+    assert L.macai_gdr_probe_mfma_flops(3, 10, 3) == -1
+    p = 1 << 20
+    assert L.macai_gdr_probe_mfma(3, 10, p, 4, None) == N.EINVAL
+    assert L.macai_gdr_probe_mfma(0, 0, p, 4, None) == N.EINVAL
+    assert L.macai_gdr_probe_mfma(0, 10, p + 4, 4, None) == N.EINVAL and b"aligned" in L.macai_gdr_last_error()
+
+
+def test_head_widths():
+    """Key widths: every multiple of 32 up to 256 on the float32 kernels, 32 / 64 / 128 on the bf16 ones; value widths
+    in the backward: up to 256 on the float32 kernels, 128 on the bf16 ones (the reference takes any multiple of 32,
+    op.py:124-125).  bf16 inputs at other widths are computed as float32; widths no kernel takes are refused, on the
+    host and by the C ABI before any launch."""
+    bf, f32 = torch.bfloat16, torch.float32
+    assert op.compute_dtype(bf, 128, 128, True) == bf and op.compute_dtype(bf, 64, 96, True) == bf
+    assert op.compute_dtype(bf, 96, 128, True) == f32 and op.compute_dtype(bf, 256, 128, False) == f32
+    assert op.compute_dtype(bf, 128, 256, True) == f32          # the bf16 backward stops at value width 128
+    assert op.compute_dtype(bf, 128, 256, False) == bf          # a forward alone keeps bf16 operands
+    assert op.compute_dtype(torch.float16, 128, 128, True) == f32
+    for DK, DV, save in ((96, 256, True), (224, 160, True), (256, 512, False)):
+        op._widths(DK, DV, save)
+    for DK, DV, save, msg in ((80, 128, False, "key head"), (288, 128, False, "key head"), (128, 48, False, "value"),
+                              (128, 288, True, "backward")):
+        with pytest.raises(NotImplementedError, match=msg):
+            op._widths(DK, DV, save)
+    L, p = N.lib(), 1 << 20
+
+    def cb(DK=128, DV=128, dtype=0):
+        return L.macai_gdr_chunk_bwd(*([p] * 16), 1, 64, 2, 2, DK, DV, dtype, 1, 1.0, None, 0, None)
+    assert cb(DV=160, dtype=1) == N.EUNSUP and b"bf16 backward" in L.macai_gdr_last_error()
+    assert cb(DV=288) == N.EUNSUP and b"up to 256" in L.macai_gdr_last_error()
+    assert cb(DK=96, dtype=1) == N.EUNSUP and b"float32" in L.macai_gdr_last_error()
+    assert cb(DK=80) == N.EUNSUP and b"multiple of 32" in L.macai_gdr_last_error()

@@ -57,3 +57,31 @@ def test_noalloc_forward_refuses_shapes_over_its_scratch():
     p = 1 << 20
     with pytest.raises(ValueError, match="fixed"):
         N.call("macai_gdr_forward_noalloc", *([p] * 6), p, p, B, T, H, H, DK, DV, N.BF16, 1, 1.0, 0, None, 0, None)
+
+
+def test_noalloc_forward_under_graph_capture():
+    """The entry point for code under HIP graph capture: after one call on the device (which looks up the array's
+    address), the call is captured into a graph (torch.cuda.CUDAGraph) and replayed three times, with eager work on
+    the same buffers between the replays; every replay gives the bits of macai_gdr_forward with a workspace."""
+    shape, dtype = (2, 300, 4, 2, 128, 128), torch.bfloat16
+    print("case noalloc forward captured", shape, dtype, flush=True)
+    B, T, H, Hk, DK, DV = shape
+    xs = _inputs(*shape, dtype, seed=47)
+    ref_o, ref_s = _forward(False, xs, *shape, dtype)
+    q, k, v, g, beta, s0 = xs
+    o = torch.empty(B, T, H, DV, dtype=dtype, device="cuda")
+    sT = torch.empty(B, H, DK, DV, device="cuda")
+    P, code = N.ptr, N.dtype_code(dtype)
+    args = (P(q), P(k), P(v), P(g), P(beta), P(s0), P(o), P(sT), B, T, H, Hk, DK, DV, code, 1, DK ** -0.5, 0, None, 0)
+    N.call("macai_gdr_forward_noalloc", *args, N.stream_of(q))   # the first call on the device, outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        N.call("macai_gdr_forward_noalloc", *args, N.stream_of(q))
+    for _ in range(3):
+        o.fill_(float("nan"))
+        sT.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o, ref_o) and torch.equal(sT, ref_s)
