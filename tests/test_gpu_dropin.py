@@ -543,3 +543,50 @@ def test_dropin_widths_bf16(DK, DV):
         with torch.no_grad():
             o, sT, _ = run_dropin(inp, grads=False)
         _parity.check({"o": gdr.rel(o, ro), "sT": gdr.rel(sT, rsT)}, BF16_BAR)
+
+
+def test_recompute_keeps_only_inputs():
+    """What the training forward keeps for its backward (the reference's tests/test_memory.py:239-250): with
+    op.RECOMPUTE_STATES (the default) exactly the six inputs, nothing a chunk; with it off, the inputs and one buffer
+    holding prep's operands with A and the chunk states (2,816 bytes a token-head at D = 128 in bf16)."""
+    _say("case saved tensors")
+    B, T, H, D = 2, 650, 4, 128
+    xs = [x.to(DEV).requires_grad_(True) for x in gdr.harness_inputs(B, T, H, D, D, seed=3)]
+    xs = [x.to(torch.bfloat16 if i < 3 else torch.float32).detach().requires_grad_(True) for i, x in enumerate(xs)]
+    old = op.RECOMPUTE_STATES
+    try:
+        op.RECOMPUTE_STATES = True
+        o, sT = GatedDeltaRule.apply(*xs, True)
+        saved = [t for t in o.grad_fn.saved_tensors if t is not None]
+        assert len(saved) == 6 and all(s.data_ptr() == x.data_ptr() for s, x in zip(saved, xs))
+        op.RECOMPUTE_STATES = False
+        o, sT = GatedDeltaRule.apply(*xs, True)
+        saved = [t for t in o.grad_fn.saved_tensors if t is not None]
+        assert len(saved) == 7 and all(s.data_ptr() == x.data_ptr() for s, x in zip(saved, xs))
+        NT = -(-T // 64)
+        per_token_head = saved[6].numel() / (B * H * NT * 64)
+        assert 2816 <= per_token_head < 2816 + 64, per_token_head      # plus the parts' 256-byte alignment
+    finally:
+        op.RECOMPUTE_STATES = old
+
+
+def test_strided_views_give_contiguous_bits():
+    """q, k, v as strided views of one projection output (the model splits its conv output; the reference's layout
+    cases in tests/test_memory.py): the drop-in makes them contiguous itself and returns the bits of contiguous
+    inputs, gradients included."""
+    _say("case strided views")
+    inp = gdr.make_inputs(2, 90, 3, 3, 128, 128, torch.bfloat16, s0=True, seed=35)
+    dsT = torch.randn(2, 3, 128, 128, generator=torch.Generator().manual_seed(36))
+    ref = run_dropin(inp, dsT=dsT)
+    packed = torch.stack([inp["query"], inp["key"], inp["value"]], 2).to(DEV).requires_grad_(True)   # [B, T, 3, H, D]
+    q, k, v = packed[:, :, 0], packed[:, :, 1], packed[:, :, 2]
+    assert not q.is_contiguous()
+    rest = [inp[n].to(DEV).requires_grad_(True) for n in ("g", "beta", "initial_state")]
+    o, sT = chunk_gated_delta_rule(q, k, v, rest[0], rest[1], initial_state=rest[2], output_final_state=True,
+                                   use_qk_l2norm_in_kernel=True)
+    torch.autograd.backward([o, sT], [inp["do"].to(DEV), dsT.to(DEV)])
+    torch.cuda.synchronize()
+    assert torch.equal(o.detach().cpu(), ref[0]) and torch.equal(sT.detach().cpu(), ref[1])
+    grads = [packed.grad[:, :, i].cpu() for i in range(3)] + [x.grad.cpu() for x in rest]
+    for n, x in zip(NAMES, grads):
+        assert torch.equal(x, ref[2][n]), n
