@@ -27,8 +27,8 @@
  *   G_r = sum_{s<=r} g_s inside the chunk, gamma = exp(G), e = exp(G_last - G), q^ / k^ the prologue's outputs.
  * With use_l2norm = 1 the kernels apply the reference prologue (_norm.py:1-10) themselves: q^ = q * rsqrt(|q|^2 + 1e-6)
  * * q_scale, k^ = k * rsqrt(|k|^2 + 1e-6), and the backward returns gradients w.r.t. the raw q and k.
- * Supported widths: DK in {32, 64, 128}, and 256 with float32 operands; DV a multiple of 32 up to 512 (the backward:
- * 32, 64, 96 or 128).
+ * Supported widths: DK in {32, 64, 128}, and with float32 operands every multiple of 32 up to 256; DV a multiple of
+ * 32 up to 512 (the backward: up to 128 with bf16 operands, up to 256 with float32).
  * Pointers must be 16-byte aligned.
  *
  * Packed rows (several sequences in one row, transformers' cu_seqlens): pass `pack`, a device int32 table, and its

@@ -108,6 +108,9 @@ PLANTS = ("fwd_gamma_sq", "fwd_glast_off", "bwd_gamma_sq", "bwd_glast_off")
 # ("CC": dM, dW, dA, dA A^T and the decayed dL).  `rnd` rounds the named classes to bf16 where they enter a product (the
 # precision model of the bf16 path; no rounding by default).
 ROUNDABLE = ("W", "Ke", "Qg", "M", "A", "S", "dS", "Vn", "dVn", "Sc", "QK", "CC")
+# A class the bf16 kernels do NOT round, for design analysis: "ScDot" rounds Sc in the last-row dg term <Sc, dSn> too,
+# as storing the chunk states in bf16 would (tests/test_oracle.py::test_chunk_states_stay_float32 shows the cost).
+NOT_ROUNDED = ("ScDot",)
 
 
 def bf16(x):
@@ -116,7 +119,7 @@ def bf16(x):
 
 
 def _rounder(rnd):
-    bad = set(rnd) - set(ROUNDABLE)
+    bad = set(rnd) - set(ROUNDABLE) - set(NOT_ROUNDED)
     assert not bad, bad
     return lambda name, x: bf16(x) if name in rnd else x
 
@@ -258,7 +261,7 @@ def chunked_backward(q, k, v, g, beta, s0, do, dsT, C=64, P=None, plant=None, rn
     R1 = torch.where(low, dOVt * M, torch.zeros_like(M))
     dG = dG + R1.sum(-1) - R1.sum(-2)
     dG = dG + bc * R2.sum(-1) - (bc[..., :, None] * R2).sum(-2)
-    dG[..., -1] = dG[..., -1] + gam[..., -1] * (Sc * dSn).sum((-1, -2))
+    dG[..., -1] = dG[..., -1] + gam[..., -1] * (R("ScDot", Sc) * dSn).sum((-1, -2))
     E = e * (K * VndSt).sum(-1)
     # exclusive prefix by shifting first: cumsum(E) - E would cancel E_t (O(1) on the last row) against the O(e^g)
     # earlier terms under strong decay

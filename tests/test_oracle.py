@@ -281,3 +281,24 @@ def test_bf16_rounding_model_is_off_by_default():
     assert torch.equal(gdr.bf16(x), torch.tensor([1.0, 1.0 + 2 ** -6, -3.140625], dtype=F64))
     c, _ = gdr.chunked_backward(*xs, do, dsT, 64, rnd=gdr.ROUNDABLE)
     assert 1e-5 < max(gdr.rel(u, v) for u, v in zip(c, a)) < 3e-2
+
+
+def test_chunk_states_stay_float32():
+    """Why the chunk states S_c are stored in fp32 although the per-chunk backward feeds them to its products in bf16:
+    its last-row dg term <S_c, dS_{c+1}> is a dot over DK x DV products that can cancel.  On the inputs of
+    test_gpu_dropin.py::test_dropin_bf16_small's (1, 1, 2, 64) case the bf16 path's rounding model moves dg by 1.9e-3,
+    and S_c rounded in that dot as well ("ScDot", what bf16 storage would do) by 2.0e-2, twice the bf16 bar: a build
+    that stored S_c in bf16 failed that case on the GPU with exactly dg 2.00e-2.  Over 50 tokens the other terms of dg
+    dominate and the dot's rounding does not show."""
+    names = ("query", "key", "value", "g", "beta", "initial_state")
+    model = tuple(c for c in gdr.ROUNDABLE if c != "QK")
+    for shape, lo, hi in (((1, 1, 2, 64), 1.5e-2, 2.5e-2), ((2, 50, 3, 128), 0.0, 1e-2)):
+        B, T, H, D = shape
+        inp = gdr.make_inputs(B, T, H, H, D, D, torch.bfloat16, s0=True, seed=8)
+        dsT = torch.randn(B, H, D, D, generator=torch.Generator().manual_seed(9))
+        args = [inp[n] for n in names]
+        exact = gdr.dropin_f64(*args, do=inp["do"], dsT=dsT)[2]["dg"]
+        path = gdr.dropin_f64(*args, do=inp["do"], dsT=dsT, rnd=model)[2]["dg"]
+        dot = gdr.dropin_f64(*args, do=inp["do"], dsT=dsT, rnd=model + ("ScDot",))[2]["dg"]
+        assert gdr.rel(path, exact) < 2.5e-3, shape
+        assert lo <= gdr.rel(dot, exact) < hi, shape
