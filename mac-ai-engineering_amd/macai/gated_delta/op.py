@@ -36,6 +36,12 @@ FUSED_NORM = True
 # float32 kernels, as the reference computes every input (op.py:276-285, 297): dg and dbeta then come within ~1e-5 of
 # float64 (the bf16 operands' rounding, not the fp32 state, sets the default's error), at the float32 kernels' speed.
 BF16_OPERANDS = True
+# BF16_UNNORMALIZED: bf16 operands also for calls whose keys the kernels do not normalise (use_qk_l2norm_in_kernel=
+# False).  Off by default: those calls run on the float32 kernels, because the bf16 operands' rounding is amplified
+# as beta |k|^2 grows and only unit-norm keys keep it under the 1e-2 bar (the oracle's rounding model over N(0, 1)
+# keys, |k|^2 ~ DK: 6e-3 to 1.2e-1; the same keys normalised: 5-6e-3).  A caller whose keys already have unit norm can
+# turn it on, or pass use_qk_l2norm_in_kernel=True (normalising a unit vector again changes it by rounding only).
+BF16_UNNORMALIZED = False
 # VALUE_SPLIT: workgroups a head-row's value columns are split over in the state passes (each owns DV / VALUE_SPLIT
 # columns as DV / 16 / VALUE_SPLIT waves of 16 columns): "auto" (split_for) or 1, 2, 4, 8, ...
 VALUE_SPLIT = "auto"
@@ -482,11 +488,13 @@ def l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     return x * torch.rsqrt((x * x).sum(dim=-1, keepdim=True) + eps)
 
 
-def compute_dtype(dtype, DK: int, DV: int = 0, save: bool = False):
+def compute_dtype(dtype, DK: int, DV: int = 0, save: bool = False, normalized: bool = True):
     """The operand type the kernels compute a call in: bfloat16 inputs on bf16 MFMA at key widths 32, 64, 128 and --
-    when the call saves for a backward -- value widths up to 128 (unless BF16_OPERANDS is off); float16, float32 and
-    other widths on the float32 kernels."""
-    bf16 = (dtype == torch.bfloat16 and DK in BF16_DK and BF16_OPERANDS and (not save or DV <= BF16_MAX_DV_BWD))
+    when the call saves for a backward -- value widths up to 128 (unless BF16_OPERANDS is off), when the keys reach the
+    products with unit norm (normalized: the kernels' or the eager prologue's l2 normalisation; unless
+    BF16_UNNORMALIZED); float16, float32 and everything else on the float32 kernels."""
+    bf16 = (dtype == torch.bfloat16 and DK in BF16_DK and BF16_OPERANDS and (normalized or BF16_UNNORMALIZED)
+            and (not save or DV <= BF16_MAX_DV_BWD))
     return torch.bfloat16 if bf16 else torch.float32
 
 
@@ -508,14 +516,15 @@ def eager_prologue(query, key, cdt):
 
 
 def plan(B: int, T: int, H: int, DK: int, DV: int, save: bool, Hk: int = None, dtype=torch.bfloat16,
-         cus: int = 256) -> dict:
+         cus: int = 256, l2norm: bool = True) -> dict:
     """What a drop-in call of these dimensions runs under the current settings (the reference's plan, op.py:105-113,
     for this build's kernels): the chunk length (64 for every pass), the operand type, the forward's segments, value
     split and state-pass kernel, and -- when the forward saves for a backward -- whether the backward recomputes
     (RECOMPUTE_STATES), its state passes, their split and the per-chunk backward's kernel.  cus: the device's compute
-    units (the persistent per-chunk backward runs where there are more chunk-heads than CUs)."""
+    units (the persistent per-chunk backward runs where there are more chunk-heads than CUs); l2norm: the call's
+    use_qk_l2norm_in_kernel."""
     Hk = Hk or H
-    cdt = compute_dtype(dtype, DK, DV, save)
+    cdt = compute_dtype(dtype, DK, DV, save, l2norm)
     bf = cdt == torch.bfloat16
     NT = math.ceil(T / CHUNK)
     recompute = save and RECOMPUTE_STATES
@@ -550,18 +559,18 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size: int = 64, ini
     kernels. Returns the output [B, T, H, DV] in the query's dtype and the final state (float32) when
     output_final_state, else None.  chunk_size is accepted and unused (the kernels use 64-token chunks).  bfloat16
     inputs run on bf16 MFMA with fp32 accumulation and an fp32 state; float32 inputs on fp32 MFMA; float16 inputs,
-    and bfloat16 ones with key heads wider than 128 (up to 256) or with BF16_OPERANDS off, are upcast exactly and
-    computed as float32, the
-    output cast back (the reference runs every input this way: its prologue and `value.float()` run the rule in
-    float32, op.py:276-285, 297).  With use_qk_l2norm_in_kernel=False
-    the query is only scaled by DK^-1/2 (op.py:279-283), inside the kernels."""
+    and bfloat16 ones with key heads wider than 128 (up to 256), with BF16_OPERANDS off or with keys the kernels do
+    not normalise (use_qk_l2norm_in_kernel=False, unless BF16_UNNORMALIZED), are upcast exactly and computed as
+    float32, the output cast back (the reference runs every input this way: its prologue and `value.float()` run the
+    rule in float32, op.py:276-285, 297).  With use_qk_l2norm_in_kernel=False the query is only scaled by DK^-1/2
+    (op.py:279-283), inside the kernels."""
     cu = kwargs.get("cu_seqlens")
     pack = None if cu is None else _pack(cu, query.shape[1], query.device)
     dtype = query.dtype
     grads = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (query, key, value, g, beta, initial_state))
     _widths(query.shape[-1], value.shape[-1], grads)
-    cdt = compute_dtype(dtype, query.shape[-1], value.shape[-1], grads)
+    cdt = compute_dtype(dtype, query.shape[-1], value.shape[-1], grads, bool(use_qk_l2norm_in_kernel))
     if use_qk_l2norm_in_kernel and not FUSED_NORM:
         query, key = eager_prologue(query, key, cdt)
         use_qk_l2norm_in_kernel = False

@@ -206,6 +206,23 @@ def test_dropin_fp16(shape):
     assert errs["o"] < 1e-3        # float32 arithmetic: only the float16 output's rounding remains
 
 
+def test_unnormalized_keys_run_the_float32_kernels():
+    """bf16 inputs with use_qk_l2norm_in_kernel=False (keys the kernels do not normalise) run on the float32 kernels:
+    the output and every gradient are those of the same values given as float32, cast back, bit for bit, and within
+    1e-2 of float64 on a draw (raw N(0, 1) keys at DK = 32, 200 tokens, seed 501) on which the bf16 operands' rounding
+    model misses that bar twelvefold (tests/test_host.py::test_unnormalized_keys_take_the_float32_kernels)."""
+    _say("case unnormalized keys bf16 -> float32 kernels")
+    inp = gdr.make_inputs(2, 200, 1, 2, 32, 32, torch.bfloat16, s0=True, seed=501)
+    assert op.plan(2, 200, 2, 32, 32, True, l2norm=False)["operands"] == "f32"
+    check_dropin(inp, bar=BF16_BAR, l2norm=False)
+    f32 = {n: (x.float() if x is not None and x.dtype == torch.bfloat16 else x) for n, x in inp.items()}
+    o, sT, g = run_dropin(inp, l2norm=False)
+    o2, sT2, g2 = run_dropin(f32, l2norm=False)
+    assert torch.equal(o, o2.to(o.dtype)) and torch.equal(sT, sT2)
+    for n in g:
+        assert torch.equal(g[n], g2[n].to(g[n].dtype)), n
+
+
 def _prenormalised(inp):
     """The inputs with query and key already l2-normalised (in float64, then rounded to their dtype): what a caller
     that runs its own prologue passes with use_qk_l2norm_in_kernel=False."""
@@ -218,16 +235,24 @@ def _prenormalised(inp):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_dropin_unfused_prologue(dtype):
     """use_qk_l2norm_in_kernel=False: no normalisation, only the query's DK^-1/2 scale (reference op.py:279-283), on
-    pre-normalised inputs.  bf16: every output and gradient within 1e-2 on each of four seeds.  float32: within 2x the
-    torch path's own float32 error, both taken as the largest over the four seeds: one draw of that error varies up
-    to 6x between seeds of this shape (dbeta 1.3e-7 to 7.7e-7), too noisy a yardstick for a single case."""
+    pre-normalised inputs.  bf16: on the bf16 kernels (op.BF16_UNNORMALIZED, which such a caller may set; by default
+    these calls take the float32 kernels), every output and gradient within 1e-2 on each of four seeds.  float32:
+    within 2x the torch path's own float32 error, both taken as the largest over the four seeds: one draw of that
+    error varies up to 6x between seeds of this shape (dbeta 1.3e-7 to 7.7e-7), too noisy a yardstick for a single
+    case."""
     _say(f"case dropin_unfused {dtype}")
     worst, anchor = {}, {}
     for seed in range(4):
         inp = _prenormalised(gdr.make_inputs(2, 100, 3, 3, 128, 128, dtype, s0=True, seed=12 + seed))
         dsT = torch.randn(2, 3, 128, 128, generator=torch.Generator().manual_seed(9 + seed))
         if dtype == torch.bfloat16:
-            check_dropin(inp, bar=BF16_BAR, dsT=dsT, l2norm=False)
+            old = op.BF16_UNNORMALIZED
+            try:
+                op.BF16_UNNORMALIZED = True
+                assert op.plan(2, 100, 3, 128, 128, True, l2norm=False)["operands"] == "bf16"
+                check_dropin(inp, bar=BF16_BAR, dsT=dsT, l2norm=False)
+            finally:
+                op.BF16_UNNORMALIZED = old
             continue
         ro, rsT, rg = gdr.dropin_f64(*(inp[n] for n in ("query", "key", "value", "g", "beta", "initial_state")),
                                      do=inp["do"], dsT=dsT, use_qk_l2norm_in_kernel=False)

@@ -10,6 +10,7 @@ import torch
 
 from macai.gated_delta import _native as N
 from macai.gated_delta import chunk_gated_delta_rule, op
+from oracle import gdr
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "macai_gdr.h")
@@ -333,6 +334,29 @@ def test_plan_reports_the_launch_choices():
     assert (p["operands"], p["prep"], p["fwd_state_pass"], p["chunk_bwd"]) == ("f32", "prep", "state_fwd", "chunk_bwd")
     assert op.plan(1, 100, 2, 256, 128, save=True)["operands"] == "f32"      # wide keys run the float32 kernels
     assert op.plan(4, 100, 2, 128, 128, save=True)["chunk_bwd"] == "chunk_bwd8"   # fewer chunk-heads than CUs
+    assert op.plan(4, 1024, 16, 128, 128, save=True, l2norm=False)["operands"] == "f32"   # keys not normalised
+
+
+def test_unnormalized_keys_take_the_float32_kernels(monkeypatch):
+    """bf16 calls whose keys the kernels do not normalise (use_qk_l2norm_in_kernel=False) compute in float32 unless
+    op.BF16_UNNORMALIZED: the bf16 operands' rounding is amplified as beta |k|^2 grows.  The oracle's rounding model
+    (the bf16 path's operand classes) on N(0, 1) keys over 200 tokens at DK = 32 moves o by 1.2e-1 on one of six draws
+    (seed 501; the others 4e-3 to 9e-3); the same inputs normalised in the kernels stay under 1e-2.  FUSED_NORM = False
+    normalises in its eager prologue, so it keeps the bf16 kernels."""
+    bf, f32 = torch.bfloat16, torch.float32
+    assert op.compute_dtype(bf, 128, 128, True, normalized=False) == f32
+    assert op.compute_dtype(bf, 128, 128, True, normalized=True) == bf
+    monkeypatch.setattr(op, "BF16_UNNORMALIZED", True)
+    assert op.compute_dtype(bf, 128, 128, True, normalized=False) == bf
+    model = tuple(c for c in gdr.ROUNDABLE if c != "QK")
+    names = ("query", "key", "value", "g", "beta", "initial_state")
+    inp = gdr.make_inputs(2, 200, 1, 2, 32, 32, bf, s0=True, seed=501)
+    worst = {}
+    for l2 in (False, True):
+        o, sT, gr = gdr.dropin_f64(*(inp[n] for n in names), do=inp["do"], use_qk_l2norm_in_kernel=l2)
+        o2, sT2, gr2 = gdr.dropin_f64(*(inp[n] for n in names), do=inp["do"], use_qk_l2norm_in_kernel=l2, rnd=model)
+        worst[l2] = max([gdr.rel(o2, o), gdr.rel(sT2, sT)] + [gdr.rel(gr2[n], gr[n]) for n in gr])
+    assert worst[False] > 5e-2 and worst[True] < 1e-2, worst
 
 
 def test_misaligned_inputs_are_copied_not_refused():
@@ -373,7 +397,11 @@ def test_fused_norm_switch(monkeypatch):
     assert seen["q"].dtype == torch.bfloat16 and seen["q"].requires_grad
     assert torch.equal(seen["q"], op.l2norm(q.float()).to(torch.bfloat16))
     assert torch.equal(seen["k"], op.l2norm(k.float()).to(torch.bfloat16))
-    chunk_gated_delta_rule(q, k, v, g, b, use_qk_l2norm_in_kernel=False)      # nothing to normalise either way
+    chunk_gated_delta_rule(q, k, v, g, b, use_qk_l2norm_in_kernel=False)      # nothing to normalise either way;
+    assert seen["l2norm"] is False and seen["q"].dtype == torch.float32       # keys of unknown norm: float32 kernels
+    assert torch.equal(seen["q"], q.float())
+    monkeypatch.setattr(op, "BF16_UNNORMALIZED", True)
+    chunk_gated_delta_rule(q, k, v, g, b, use_qk_l2norm_in_kernel=False)
     assert seen["l2norm"] is False and seen["q"] is q
 
 
