@@ -42,6 +42,12 @@ BF16_OPERANDS = True
 # keys, |k|^2 ~ DK: 6e-3 to 1.2e-1; the same keys normalised: 5-6e-3).  A caller whose keys already have unit norm can
 # turn it on, or pass use_qk_l2norm_in_kernel=True (normalising a unit vector again changes it by rounding only).
 BF16_UNNORMALIZED = False
+# BF16_MIN_TOKENS: bf16 calls on rows shorter than this many tokens run on the float32 kernels.  With so few tokens the
+# bf16 operands' rounding is not averaged out -- dg and dq of a row of 1-3 tokens are sums of few, cancelling terms:
+# the oracle's rounding model puts 10% of random such rows over the 1e-2 bar (up to 0.2 on one token), none from 5
+# tokens up to 200 but one at 16 -- and the float32 kernels cost next to nothing at that size.  The default is one
+# chunk; 0 keeps every length on the bf16 kernels.
+BF16_MIN_TOKENS = 64
 # VALUE_SPLIT: workgroups a head-row's value columns are split over in the state passes (each owns DV / VALUE_SPLIT
 # columns as DV / 16 / VALUE_SPLIT waves of 16 columns): "auto" (split_for) or 1, 2, 4, 8, ...
 VALUE_SPLIT = "auto"
@@ -431,7 +437,7 @@ class GatedDeltaRule(torch.autograd.Function):
         _check(q, k, v, g, beta, s0)
         ctx.io_dtype = q.dtype             # o and the q, k, v gradients come back in it
         _widths(q.shape[-1], v.shape[-1], save)
-        if q.dtype != compute_dtype(q.dtype, q.shape[-1], v.shape[-1], save):
+        if q.dtype != compute_dtype(q.dtype, q.shape[-1], v.shape[-1], save, tokens=q.shape[1]):
             q, k, v = q.float(), k.float(), v.float()
         q, k, v = (_as(t, t.dtype) for t in (q, k, v))
         g, beta, s0 = (_as(t, torch.float32) for t in (g, beta, s0))
@@ -488,13 +494,14 @@ def l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     return x * torch.rsqrt((x * x).sum(dim=-1, keepdim=True) + eps)
 
 
-def compute_dtype(dtype, DK: int, DV: int = 0, save: bool = False, normalized: bool = True):
+def compute_dtype(dtype, DK: int, DV: int = 0, save: bool = False, normalized: bool = True, tokens: int = None):
     """The operand type the kernels compute a call in: bfloat16 inputs on bf16 MFMA at key widths 32, 64, 128 and --
     when the call saves for a backward -- value widths up to 128 (unless BF16_OPERANDS is off), when the keys reach the
     products with unit norm (normalized: the kernels' or the eager prologue's l2 normalisation; unless
-    BF16_UNNORMALIZED); float16, float32 and everything else on the float32 kernels."""
+    BF16_UNNORMALIZED) and the rows hold at least BF16_MIN_TOKENS tokens (tokens: the row length; None: not
+    checked); float16, float32 and everything else on the float32 kernels."""
     bf16 = (dtype == torch.bfloat16 and DK in BF16_DK and BF16_OPERANDS and (normalized or BF16_UNNORMALIZED)
-            and (not save or DV <= BF16_MAX_DV_BWD))
+            and (not save or DV <= BF16_MAX_DV_BWD) and (tokens is None or tokens >= BF16_MIN_TOKENS))
     return torch.bfloat16 if bf16 else torch.float32
 
 
@@ -524,7 +531,7 @@ def plan(B: int, T: int, H: int, DK: int, DV: int, save: bool, Hk: int = None, d
     units (the persistent per-chunk backward runs where there are more chunk-heads than CUs); l2norm: the call's
     use_qk_l2norm_in_kernel."""
     Hk = Hk or H
-    cdt = compute_dtype(dtype, DK, DV, save, l2norm)
+    cdt = compute_dtype(dtype, DK, DV, save, l2norm, T)
     bf = cdt == torch.bfloat16
     NT = math.ceil(T / CHUNK)
     recompute = save and RECOMPUTE_STATES
@@ -559,18 +566,18 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size: int = 64, ini
     kernels. Returns the output [B, T, H, DV] in the query's dtype and the final state (float32) when
     output_final_state, else None.  chunk_size is accepted and unused (the kernels use 64-token chunks).  bfloat16
     inputs run on bf16 MFMA with fp32 accumulation and an fp32 state; float32 inputs on fp32 MFMA; float16 inputs,
-    and bfloat16 ones with key heads wider than 128 (up to 256), with BF16_OPERANDS off or with keys the kernels do
-    not normalise (use_qk_l2norm_in_kernel=False, unless BF16_UNNORMALIZED), are upcast exactly and computed as
-    float32, the output cast back (the reference runs every input this way: its prologue and `value.float()` run the
-    rule in float32, op.py:276-285, 297).  With use_qk_l2norm_in_kernel=False the query is only scaled by DK^-1/2
-    (op.py:279-283), inside the kernels."""
+    and bfloat16 ones with key heads wider than 128 (up to 256), with BF16_OPERANDS off, with keys the kernels do not
+    normalise (use_qk_l2norm_in_kernel=False, unless BF16_UNNORMALIZED) or with rows shorter than BF16_MIN_TOKENS,
+    are upcast exactly and computed as float32, the output cast back (the reference runs every input this way: its
+    prologue and `value.float()` run the rule in float32, op.py:276-285, 297).  With use_qk_l2norm_in_kernel=False
+    the query is only scaled by DK^-1/2 (op.py:279-283), inside the kernels."""
     cu = kwargs.get("cu_seqlens")
     pack = None if cu is None else _pack(cu, query.shape[1], query.device)
     dtype = query.dtype
     grads = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (query, key, value, g, beta, initial_state))
     _widths(query.shape[-1], value.shape[-1], grads)
-    cdt = compute_dtype(dtype, query.shape[-1], value.shape[-1], grads, bool(use_qk_l2norm_in_kernel))
+    cdt = compute_dtype(dtype, query.shape[-1], value.shape[-1], grads, bool(use_qk_l2norm_in_kernel), query.shape[1])
     if use_qk_l2norm_in_kernel and not FUSED_NORM:
         query, key = eager_prologue(query, key, cdt)
         use_qk_l2norm_in_kernel = False

@@ -182,16 +182,26 @@ def test_dropin_fp32_within_twice_the_torch_path(shape, s0):
     check_dropin(inp, anchor=True, dsT=dsT)
 
 
+@pytest.mark.parametrize("kernels", ["default", "bf16"])
 @pytest.mark.parametrize("shape", [(2, 50, 3, 128), (2, 45, 3, 128), (1, 1, 2, 64), (3, 130, 2, 32), (1, 1, 2, 128),
                                    (1, 2, 2, 128), (2, 1, 3, 128), (2, 2, 3, 128), (1, 3, 1, 128)])
-def test_dropin_bf16_small(shape):
+def test_dropin_bf16_small(shape, kernels):
     """bf16 drop-in end to end with a starting state and the final state used (reference test_harness.py:139-166),
-    including one- to three-token rows at D = 128, where a chunk has a single valid row or two."""
+    including one- to three-token rows at D = 128, where a chunk has a single valid row or two.  "default": rows
+    shorter than a chunk run on the float32 kernels (op.BF16_MIN_TOKENS); "bf16": op.BF16_MIN_TOKENS = 0 keeps them on
+    the bf16 kernels, whose one- to three-row chunks these draws hold to the bar too."""
     B, T, H, D = shape
-    _say(f"case dropin_bf16 {shape}")
+    _say(f"case dropin_bf16 {shape} {kernels}")
     inp = gdr.make_inputs(B, T, H, H, D, D, torch.bfloat16, s0=True, seed=8)
     dsT = torch.randn(B, H, D, D, generator=torch.Generator().manual_seed(9))
-    check_dropin(inp, bar=BF16_BAR, dsT=dsT)
+    old = op.BF16_MIN_TOKENS
+    try:
+        if kernels == "bf16":
+            op.BF16_MIN_TOKENS = 0
+        assert op.plan(B, T, H, D, D, True)["operands"] == ("f32" if kernels == "default" and T < 64 else "bf16")
+        check_dropin(inp, bar=BF16_BAR, dsT=dsT)
+    finally:
+        op.BF16_MIN_TOKENS = old
 
 
 @pytest.mark.parametrize("shape", [(2, 50, 3, 128), (1, 130, 2, 64)])
@@ -206,18 +216,24 @@ def test_dropin_fp16(shape):
     assert errs["o"] < 1e-3        # float32 arithmetic: only the float16 output's rounding remains
 
 
-def test_unnormalized_keys_run_the_float32_kernels():
-    """bf16 inputs with use_qk_l2norm_in_kernel=False (keys the kernels do not normalise) run on the float32 kernels:
-    the output and every gradient are those of the same values given as float32, cast back, bit for bit, and within
-    1e-2 of float64 on a draw (raw N(0, 1) keys at DK = 32, 200 tokens, seed 501) on which the bf16 operands' rounding
-    model misses that bar twelvefold (tests/test_host.py::test_unnormalized_keys_take_the_float32_kernels)."""
-    _say("case unnormalized keys bf16 -> float32 kernels")
-    inp = gdr.make_inputs(2, 200, 1, 2, 32, 32, torch.bfloat16, s0=True, seed=501)
-    assert op.plan(2, 200, 2, 32, 32, True, l2norm=False)["operands"] == "f32"
-    check_dropin(inp, bar=BF16_BAR, l2norm=False)
+@pytest.mark.parametrize("why", ["unnormalized", "short"])
+def test_bf16_calls_on_the_float32_kernels(why):
+    """bf16 calls the bf16 operands do not serve run on the float32 kernels: keys the kernels do not normalise
+    (use_qk_l2norm_in_kernel=False; raw N(0, 1) keys at DK = 32, 200 tokens, seed 501, a draw on which the bf16
+    operands' rounding model misses the bar twelvefold) and rows shorter than a chunk (one token, seed 30130: the
+    model's dg 0.2; tests/test_host.py).  The output and every gradient are those of the same values given as float32,
+    cast back, bit for bit, and within 1e-2 of float64."""
+    _say(f"case bf16 on the float32 kernels: {why}")
+    if why == "unnormalized":
+        inp, l2 = gdr.make_inputs(2, 200, 1, 2, 32, 32, torch.bfloat16, s0=True, seed=501), False
+        assert op.plan(2, 200, 2, 32, 32, True, l2norm=False)["operands"] == "f32"
+    else:
+        inp, l2 = gdr.make_inputs(1, 1, 2, 2, 64, 32, torch.bfloat16, s0=True, seed=30130), True
+        assert op.plan(1, 1, 2, 64, 32, True)["operands"] == "f32"
+    check_dropin(inp, bar=BF16_BAR, l2norm=l2)
     f32 = {n: (x.float() if x is not None and x.dtype == torch.bfloat16 else x) for n, x in inp.items()}
-    o, sT, g = run_dropin(inp, l2norm=False)
-    o2, sT2, g2 = run_dropin(f32, l2norm=False)
+    o, sT, g = run_dropin(inp, l2norm=l2)
+    o2, sT2, g2 = run_dropin(f32, l2norm=l2)
     assert torch.equal(o, o2.to(o.dtype)) and torch.equal(sT, sT2)
     for n in g:
         assert torch.equal(g[n], g2[n].to(g[n].dtype)), n

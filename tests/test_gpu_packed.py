@@ -12,11 +12,18 @@ import torch
 
 import _parity
 
-from macai.gated_delta import chunk_gated_delta_rule
+from macai.gated_delta import chunk_gated_delta_rule, op
 from oracle import gdr
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
+
+
+@pytest.fixture(autouse=True)
+def _same_kernels_alone(monkeypatch):
+    """A packed row runs on the bf16 kernels whatever its sequences' lengths; a bf16 sequence shorter than a chunk run
+    alone would take the float32 kernels (op.BF16_MIN_TOKENS).  The comparisons here run it on the bf16 kernels too."""
+    monkeypatch.setattr(op, "BF16_MIN_TOKENS", 0)
 
 
 def _say(*a):

@@ -373,6 +373,26 @@ def test_misaligned_inputs_are_copied_not_refused():
     assert op._as(h, torch.bfloat16).data_ptr() % 16 == 0 and torch.equal(op._as(h, torch.bfloat16), h)
 
 
+def test_short_rows_take_the_float32_kernels(monkeypatch):
+    """bf16 calls on rows shorter than op.BF16_MIN_TOKENS (one chunk by default) compute in float32: dg, dq of a row of
+    1-3 tokens are sums of few, cancelling terms, and the bf16 operands' rounding is not averaged out.  The oracle's
+    rounding model on a single-token row (B=1, H=2, DK=64, DV=32, with a starting state, seed 30130) moves dg by 0.2;
+    the same model over 64 tokens of that draw's shape stays under 1e-2."""
+    bf, f32 = torch.bfloat16, torch.float32
+    assert op.compute_dtype(bf, 128, 128, True, tokens=63) == f32
+    assert op.compute_dtype(bf, 128, 128, True, tokens=64) == bf and op.compute_dtype(bf, 128, 128, True) == bf
+    assert op.plan(1, 3, 2, 128, 128, True)["operands"] == "f32" and op.plan(1, 64, 2, 128, 128, True)["operands"] == "bf16"
+    monkeypatch.setattr(op, "BF16_MIN_TOKENS", 0)
+    assert op.compute_dtype(bf, 128, 128, True, tokens=1) == bf
+    model = tuple(c for c in gdr.ROUNDABLE if c != "QK")
+    names = ("query", "key", "value", "g", "beta", "initial_state")
+    for T, seed, lo, hi in ((1, 30130, 5e-2, 1.0), (64, 30130, 0.0, 1e-2)):
+        inp = gdr.make_inputs(1, T, 2, 2, 64, 32, bf, s0=True, seed=seed)
+        exact = gdr.dropin_f64(*(inp[n] for n in names), do=inp["do"])[2]["dg"]
+        path = gdr.dropin_f64(*(inp[n] for n in names), do=inp["do"], rnd=model)[2]["dg"]
+        assert lo <= gdr.rel(path, exact) < hi, T
+
+
 def test_fused_norm_switch(monkeypatch):
     """op.FUSED_NORM (the reference's switch, op.py:19-21): True hands the raw query and key to the kernels with the
     normalisation fused (use_l2norm 1); False normalises them as float32 PyTorch operations (autograd records them),
@@ -386,8 +406,8 @@ def test_fused_norm_switch(monkeypatch):
     monkeypatch.setattr(op, "_check", lambda *a, **kw: None)
     monkeypatch.setattr(op._DropIn, "apply", staticmethod(fake_apply))
     gen = torch.Generator().manual_seed(1)
-    q, k, v = (torch.randn(1, 5, 2, 64, generator=gen).to(torch.bfloat16) for _ in range(3))
-    g, b = -torch.rand(1, 5, 2, generator=gen), torch.rand(1, 5, 2, generator=gen)
+    q, k, v = (torch.randn(1, 64, 2, 64, generator=gen).to(torch.bfloat16) for _ in range(3))
+    g, b = -torch.rand(1, 64, 2, generator=gen), torch.rand(1, 64, 2, generator=gen)
     chunk_gated_delta_rule(q, k, v, g, b, use_qk_l2norm_in_kernel=True)
     assert seen["l2norm"] is True and seen["q"] is q and seen["q_scale"] == 64 ** -0.5
     monkeypatch.setattr(op, "FUSED_NORM", False)
