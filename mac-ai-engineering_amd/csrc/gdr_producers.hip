@@ -406,10 +406,13 @@ __global__ void __launch_bounds__(256) sum_columns_kernel(const float* in, float
 }
 
 // ---- the gates -----------------------------------------------------------------------------------------------------
-// PyTorch's softplus with threshold 20: x above it, log1p(exp(x)) below.
-__device__ __forceinline__ float softplus_t20(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
-// its derivative with the same threshold: 1 above it, sigmoid(x) below
-__device__ __forceinline__ float softplus_t20_grad(float x) { return x > 20.0f ? 1.0f : 1.0f / (1.0f + expf(-x)); }
+// PyTorch's softplus with threshold 20: x above it, log1p(exp(x)) below; and its derivative with the same
+// threshold: 1 above it, sigmoid(x) below.  The gates compute in double, a + dt_bias included, and round each result
+// once: they are a few elements a token-head, so the kernels are bound by latency, and in float32 the sums', the
+// exponentials' and the quotients' roundings put the gradients at up to twice the PyTorch path's error on short
+// rows.
+__device__ __forceinline__ double softplus_t20(double x) { return x > 20.0 ? x : log1p(exp(x)); }
+__device__ __forceinline__ double softplus_t20_grad(double x) { return x > 20.0 ? 1.0 : 1.0 / (1.0 + exp(-x)); }
 
 // The gates move under a megabyte per layer, so they are bound by latency, not bandwidth: one element a lane, so
 // that a layer's elements spread over every lane of the chip and each lane runs one exponential chain.
@@ -421,9 +424,9 @@ __global__ void __launch_bounds__(GATE_THREADS) gates_fwd_kernel(const T* b, con
   const int64_t i = (int64_t)blockIdx.x * GATE_THREADS + threadIdx.x;
   if (i >= n) return;
   const int head = (int)(i % H);             // heads run fastest: element i is head i mod H
-  const float rate = -expf(alog[head]);
-  beta[i] = 1.0f / (1.0f + expf(-(float)b[i]));
-  g[i] = rate * softplus_t20((float)a[i] + dtb[head]);
+  const double rate = -exp((double)alog[head]);
+  beta[i] = (float)(1.0 / (1.0 + exp(-(double)(float)b[i])));
+  g[i] = (float)(rate * softplus_t20((double)(float)a[i] + (double)dtb[head]));
 }
 
 template <typename T>
@@ -433,42 +436,43 @@ __global__ void __launch_bounds__(GATE_THREADS) gates_bwd_kernel(const T* b, con
   const int64_t i = (int64_t)blockIdx.x * GATE_THREADS + threadIdx.x;
   if (i >= n) return;
   const int head = (int)(i % H);
-  const float rate = -expf(alog[head]);
-  const float sig = 1.0f / (1.0f + expf(-(float)b[i]));
-  db[i] = (T)(dbeta[i] * (sig - sig * sig));          // d sigmoid = s (1 - s)
-  da[i] = (T)(dg[i] * rate * softplus_t20_grad((float)a[i] + dtb[head]));
+  const double rate = -exp((double)alog[head]);
+  const double sig = 1.0 / (1.0 + exp(-(double)(float)b[i]));
+  db[i] = (T)(float)((double)dbeta[i] * (sig - sig * sig));          // d sigmoid = s (1 - s)
+  da[i] = (T)(float)((double)dg[i] * rate * softplus_t20_grad((double)(float)a[i] + (double)dtb[head]));
 }
 
 // dA_log[h] = sum over rows of dg g and ddt[h] = sum over rows of dg (-exp(A_log)) softplus'(a + dt_bias): one
 // workgroup a head; thread i takes rows i, i + 256, ... in order, then a wave sums its lanes by a fixed butterfly and
-// the four waves add in order.  Deterministic.
+// the four waves add in order.  Deterministic.  Terms and sums in double, rounded once: a head's rows of dg carry both
+// signs, so the sums can cancel.
 template <typename T>
 __global__ void __launch_bounds__(256) gates_params_kernel(const T* a, const float* alog, const float* dtb,
                                                            const float* dg, float* dA, float* ddt, int64_t rows,
                                                            int H) {
   const int h = blockIdx.x;
-  const float rate = -expf(alog[h]), bias = dtb[h];
-  float s_a = 0.f, s_d = 0.f;
+  const double rate = -exp((double)alog[h]), bias = (double)dtb[h];
+  double s_a = 0.0, s_d = 0.0;
   for (int64_t r = threadIdx.x; r < rows; r += 256) {
     const int64_t i = r * H + h;
-    const float x = (float)a[i] + bias, gv = dg[i];
-    s_a = fmaf(gv, rate * softplus_t20(x), s_a);
-    s_d = fmaf(gv, rate * softplus_t20_grad(x), s_d);
+    const double x = (double)(float)a[i] + bias, gv = (double)dg[i];
+    s_a = fma(gv, rate * softplus_t20(x), s_a);
+    s_d = fma(gv, rate * softplus_t20_grad(x), s_d);
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
     s_a += __shfl_xor(s_a, off, 64);
     s_d += __shfl_xor(s_d, off, 64);
   }
-  __shared__ float wa[4], wd[4];
+  __shared__ double wa[4], wd[4];
   if ((threadIdx.x & 63) == 0) {
     wa[threadIdx.x >> 6] = s_a;
     wd[threadIdx.x >> 6] = s_d;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    dA[h] = ((wa[0] + wa[1]) + wa[2]) + wa[3];
-    ddt[h] = ((wd[0] + wd[1]) + wd[2]) + wd[3];
+    dA[h] = (float)(((wa[0] + wa[1]) + wa[2]) + wa[3]);
+    ddt[h] = (float)(((wd[0] + wd[1]) + wd[2]) + wd[3]);
   }
 }
 
