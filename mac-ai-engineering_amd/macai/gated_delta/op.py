@@ -148,7 +148,7 @@ def _check(q, k, v, g, beta, s0, nseq=None):
                          f"{tuple(v.shape)}")
     B, T, Hk, DK = q.shape
     H = v.shape[2]
-    if H % Hk != 0:
+    if Hk == 0 or H % Hk != 0:
         raise ValueError(f"the key heads of q and k ({Hk}) must divide the value heads of v ({H})")
     if g.shape != (B, T, H) or beta.shape != (B, T, H):
         raise ValueError(f"g and beta must be [B, T, H] = {(B, T, H)}, got {tuple(g.shape)}, {tuple(beta.shape)}")
@@ -572,6 +572,8 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size: int = 64, ini
     prologue and `value.float()` run the rule in float32, op.py:276-285, 297).  With use_qk_l2norm_in_kernel=False
     the query is only scaled by DK^-1/2 (op.py:279-283), inside the kernels."""
     cu = kwargs.get("cu_seqlens")
+    if query.shape[0] == 0 or query.shape[1] == 0:
+        return _no_tokens((query, key, value, g, beta), initial_state, output_final_state, cu)
     pack = None if cu is None else _pack(cu, query.shape[1], query.device)
     dtype = query.dtype
     grads = torch.is_grad_enabled() and any(
@@ -593,6 +595,26 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size: int = 64, ini
     return (out if out.dtype == dtype else out.to(dtype)), sT
 
 
+def _no_tokens(inputs, initial_state, output_final_state, cu=None):
+    """A call without tokens (B = 0 or T = 0; inputs: query, key, value, g, beta): an empty output, and each starting
+    state passed through as the final one (zeros without one), as the reference's torch path returns when it loops
+    over no chunks (transformers modeling_qwen3_5.py:248-327); the inputs' gradients are empty and the state's is the
+    final state's."""
+    query, value = inputs[0], inputs[2]
+    if not query.is_cuda:
+        raise RuntimeError("macai's gated delta rule runs on a HIP device (MI355X); got tensors on " + str(query.device))
+    B, T, H, DV = value.shape
+    out = value.new_zeros(B, T, H, DV, dtype=query.dtype)
+    if torch.is_grad_enabled() and any(t.requires_grad for t in inputs):
+        out = out + sum(t.sum() for t in inputs) * 0      # empty: the output still hangs off the inputs
+    if not output_final_state:
+        return out, None
+    S = B if cu is None else cu.numel() - 1
+    if initial_state is None:
+        return out, torch.zeros(S, H, query.shape[-1], DV, device=value.device, dtype=torch.float32)
+    return out, initial_state.float().clone()
+
+
 def recurrent_gated_delta_rule(query, key, value, g, beta, initial_state=None, output_final_state: bool = False,
                                use_qk_l2norm_in_kernel: bool = False, **kwargs):
     """Drop-in for transformers' torch_recurrent_gated_delta_rule (modeling_qwen3_5.py:330-380), the decode path the
@@ -600,6 +622,8 @@ def recurrent_gated_delta_rule(query, key, value, g, beta, initial_state=None, o
     streaming pass over the fp32 state); longer inputs, or inputs that need gradients, run the chunked kernels, which
     compute the same recurrence."""
     T = query.shape[1]
+    if query.shape[0] == 0 or T == 0:
+        return _no_tokens((query, key, value, g, beta), initial_state, output_final_state, kwargs.get("cu_seqlens"))
     needs_grad = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (query, key, value, g, beta, initial_state))
     widths = (query.shape[-1], value.shape[-1])

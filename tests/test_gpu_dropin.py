@@ -239,6 +239,30 @@ def test_bf16_calls_on_the_float32_kernels(why):
         assert torch.equal(g[n], g2[n].to(g[n].dtype)), n
 
 
+def test_calls_without_tokens():
+    """B = 0 or T = 0: an empty output, the starting state passed through as the final one (zeros without one) and its
+    gradient the final state's, as the reference's torch path returns when it loops over no chunks (transformers
+    modeling_qwen3_5.py:248-327); the decode entry the same; no key heads is refused with a ValueError."""
+    for B, T in ((2, 0), (0, 5)):
+        q, k, v = (torch.randn(B, T, 2, 64, device=DEV, dtype=torch.bfloat16, requires_grad=True) for _ in range(3))
+        g = torch.zeros(B, T, 2, device=DEV, requires_grad=True)
+        s0 = torch.randn(B, 2, 64, 64, device=DEV, requires_grad=True)
+        o, sT = chunk_gated_delta_rule(q, k, v, g, g, initial_state=s0, output_final_state=True,
+                                       use_qk_l2norm_in_kernel=True)
+        assert o.shape == (B, T, 2, 64) and o.dtype == torch.bfloat16 and torch.equal(sT, s0)
+        dsT = torch.randn_like(sT)
+        torch.autograd.backward([o, sT], [torch.zeros_like(o), dsT])
+        assert torch.equal(s0.grad, dsT)
+        o, sT = chunk_gated_delta_rule(q, k, v, g, g, output_final_state=True)
+        assert sT.shape == (B, 2, 64, 64) and not sT.any()
+        o, sT = recurrent_gated_delta_rule(q, k, v, g, g, initial_state=s0, output_final_state=True)
+        assert o.shape == (B, T, 2, 64) and torch.equal(sT, s0)
+    q = torch.zeros(1, 3, 0, 64, device=DEV)
+    with pytest.raises(ValueError, match="key heads"):
+        chunk_gated_delta_rule(q, q, torch.zeros(1, 3, 2, 64, device=DEV), torch.zeros(1, 3, 2, device=DEV),
+                               torch.zeros(1, 3, 2, device=DEV))
+
+
 def _prenormalised(inp):
     """The inputs with query and key already l2-normalised (in float64, then rounded to their dtype): what a caller
     that runs its own prologue passes with use_qk_l2norm_in_kernel=False."""

@@ -194,6 +194,14 @@ def test_cpu_tensors_refused_loudly():
         chunk_gated_delta_rule(x, x, x, x[..., 0], x[..., 0])
 
 
+def test_calls_without_tokens_still_need_the_device():
+    """A call without tokens (B = 0 or T = 0) returns at once on the GPU (tests/test_gpu_dropin.py), but off a HIP
+    device it is refused like any other."""
+    for x in (torch.zeros(2, 0, 2, 64), torch.zeros(0, 3, 2, 64)):
+        with pytest.raises(RuntimeError, match="HIP device"):
+            chunk_gated_delta_rule(x, x, x, x[..., 0], x[..., 0], output_final_state=True)
+
+
 def test_split_rule():
     """VALUE_SPLIT 'auto': the largest valid split (1, 2, 4 or 8 waves of 16 columns per workgroup; 8 only when
     nothing else is valid) whose workgroups fit the pass's share of the 256 CUs at once, else the smallest; an int
