@@ -42,11 +42,13 @@ BF16_OPERANDS = True
 # keys, |k|^2 ~ DK: 6e-3 to 1.2e-1; the same keys normalised: 5-6e-3).  A caller whose keys already have unit norm can
 # turn it on, or pass use_qk_l2norm_in_kernel=True (normalising a unit vector again changes it by rounding only).
 BF16_UNNORMALIZED = False
-# BF16_MIN_TOKENS: bf16 calls on rows shorter than this many tokens run on the float32 kernels.  With so few tokens the
-# bf16 operands' rounding is not averaged out -- dg and dq of a row of 1-3 tokens are sums of few, cancelling terms:
-# the oracle's rounding model puts 10% of random such rows over the 1e-2 bar (up to 0.2 on one token), none from 5
-# tokens up to 200 but one at 16 -- and the float32 kernels cost next to nothing at that size.  The default is one
-# chunk; 0 keeps every length on the bf16 kernels.
+# BF16_MIN_TOKENS: bf16 calls that save for a backward, on rows shorter than this many tokens, run on the float32
+# kernels.  With so few tokens the bf16 operands' rounding is not averaged out -- dg and dq of a row of 1-3 tokens are
+# sums of few, cancelling terms: the oracle's rounding model puts 10% of random such rows over the 1e-2 bar (up to 0.2
+# on one token), none from 5 tokens up to 200 but one at 16 -- and the float32 kernels cost next to nothing at that
+# size.  The forward's outputs are not affected (the model's worst o and sT over 60 draws of 1-16 tokens: 8e-3, as on
+# long rows), so a forward without gradients keeps the bf16 kernels.  The default is one chunk; 0 keeps every length
+# on the bf16 kernels.
 BF16_MIN_TOKENS = 64
 # VALUE_SPLIT: workgroups a head-row's value columns are split over in the state passes (each owns DV / VALUE_SPLIT
 # columns as DV / 16 / VALUE_SPLIT waves of 16 columns): "auto" (split_for) or 1, 2, 4, 8, ...
@@ -498,10 +500,10 @@ def compute_dtype(dtype, DK: int, DV: int = 0, save: bool = False, normalized: b
     """The operand type the kernels compute a call in: bfloat16 inputs on bf16 MFMA at key widths 32, 64, 128 and --
     when the call saves for a backward -- value widths up to 128 (unless BF16_OPERANDS is off), when the keys reach the
     products with unit norm (normalized: the kernels' or the eager prologue's l2 normalisation; unless
-    BF16_UNNORMALIZED) and the rows hold at least BF16_MIN_TOKENS tokens (tokens: the row length; None: not
-    checked); float16, float32 and everything else on the float32 kernels."""
+    BF16_UNNORMALIZED) and, when the call saves for a backward, the rows hold at least BF16_MIN_TOKENS tokens (tokens:
+    the row length; None: not checked); float16, float32 and everything else on the float32 kernels."""
     bf16 = (dtype == torch.bfloat16 and DK in BF16_DK and BF16_OPERANDS and (normalized or BF16_UNNORMALIZED)
-            and (not save or DV <= BF16_MAX_DV_BWD) and (tokens is None or tokens >= BF16_MIN_TOKENS))
+            and (not save or (DV <= BF16_MAX_DV_BWD and (tokens is None or tokens >= BF16_MIN_TOKENS))))
     return torch.bfloat16 if bf16 else torch.float32
 
 
@@ -567,8 +569,8 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size: int = 64, ini
     output_final_state, else None.  chunk_size is accepted and unused (the kernels use 64-token chunks).  bfloat16
     inputs run on bf16 MFMA with fp32 accumulation and an fp32 state; float32 inputs on fp32 MFMA; float16 inputs,
     and bfloat16 ones with key heads wider than 128 (up to 256), with BF16_OPERANDS off, with keys the kernels do not
-    normalise (use_qk_l2norm_in_kernel=False, unless BF16_UNNORMALIZED) or with rows shorter than BF16_MIN_TOKENS,
-    are upcast exactly and computed as float32, the output cast back (the reference runs every input this way: its
+    normalise (use_qk_l2norm_in_kernel=False, unless BF16_UNNORMALIZED) or, with gradients, rows shorter than
+    BF16_MIN_TOKENS, are upcast exactly and computed as float32, the output cast back (the reference runs every input this way: its
     prologue and `value.float()` run the rule in float32, op.py:276-285, 297).  With use_qk_l2norm_in_kernel=False
     the query is only scaled by DK^-1/2 (op.py:279-283), inside the kernels."""
     cu = kwargs.get("cu_seqlens")

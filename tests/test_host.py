@@ -382,8 +382,9 @@ def test_misaligned_inputs_are_copied_not_refused():
 
 
 def test_short_rows_take_the_float32_kernels(monkeypatch):
-    """bf16 calls on rows shorter than op.BF16_MIN_TOKENS (one chunk by default) compute in float32: dg, dq of a row of
-    1-3 tokens are sums of few, cancelling terms, and the bf16 operands' rounding is not averaged out.  The oracle's
+    """bf16 calls with gradients on rows shorter than op.BF16_MIN_TOKENS (one chunk by default) compute in float32:
+    dg, dq of a row of 1-3 tokens are sums of few, cancelling terms, and the bf16 operands' rounding is not averaged
+    out (a forward without gradients keeps the bf16 kernels: its outputs are not affected).  The oracle's
     rounding model on a single-token row (B=1, H=2, DK=64, DV=32, with a starting state, seed 30130) moves dg by 0.2;
     the same model over 64 tokens of that draw's shape stays under 1e-2."""
     bf, f32 = torch.bfloat16, torch.float32
@@ -391,6 +392,7 @@ def test_short_rows_take_the_float32_kernels(monkeypatch):
     assert op.compute_dtype(bf, 128, 128, True, tokens=64) == bf and op.compute_dtype(bf, 128, 128, True) == bf
     assert op.plan(1, 3, 2, 128, 128, True)["operands"] == "f32"
     assert op.plan(1, 64, 2, 128, 128, True)["operands"] == "bf16"
+    assert op.plan(1, 3, 2, 128, 128, False)["operands"] == "bf16"   # a forward without gradients keeps bf16
     monkeypatch.setattr(op, "BF16_MIN_TOKENS", 0)
     assert op.compute_dtype(bf, 128, 128, True, tokens=1) == bf
     model = tuple(c for c in gdr.ROUNDABLE if c != "QK")
