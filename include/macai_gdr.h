@@ -154,8 +154,9 @@ int64_t macai_gdr_forward_workspace(int64_t B, int64_t T, int64_t H, int64_t DK,
 /* macai_gdr_forward without a workspace argument and without allocating: no counterpart in the reference; for callers
  * that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  The per-chunk operands live in a fixed device array of MACAI_GDR_NOALLOC_SCRATCH_BYTES, one per device,
- * held for the process's lifetime; a shape whose operands (macai_gdr_forward_workspace) exceed it is refused with
- * EINVAL before any launch.  Calls on one device share that array: calls that overlap on one device (different
+ * reserved by the first call on that device (the array sits alone in its code object, which the runtime loads on that
+ * call's address lookup, not when the library loads) and held for the process's lifetime; a shape whose operands
+ * (macai_gdr_forward_workspace) exceed it is refused with EINVAL before any launch.  Calls on one device share that array: calls that overlap on one device (different
  * streams, or threads) race and must be serialised by the caller.  Same arguments and bits as macai_gdr_forward.
  * Under graph capture: make one call on the device before capturing -- the first call there looks up the array's
  * address (hipGetSymbolAddress, not a stream operation); the captured launches then replay with the same bits. */

@@ -79,7 +79,9 @@ int forward_in(const char* what, const void* q, const void* k, const void* v, co
 // The workspace of macai_gdr_forward_noalloc: one copy per device, held for the process's lifetime.  Host code reaches
 // it only through the address hipGetSymbolAddress returns on the current device (device_scratch), never by its name:
 // in host code the name stands for a host-side shadow, not device memory.  Every call on a device shares its copy,
-// and prep rewrites every byte the state pass then reads, so nothing in it needs clearing between calls.
+// and prep rewrites every byte the state pass then reads, so nothing in it needs clearing between calls.  This file
+// defines no kernel, so its code object holds the array alone and is loaded (the array reserved) by the first
+// hipGetSymbolAddress on a device, not when the library loads.
 constexpr int64_t SCRATCH_BYTES = MACAI_GDR_NOALLOC_SCRATCH_BYTES;
 constexpr int MAX_DEVICES = 64;
 __device__ __align__(256) char scratch[SCRATCH_BYTES];
