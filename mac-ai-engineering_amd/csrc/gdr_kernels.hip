@@ -390,7 +390,7 @@ __global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
   constexpr int NBD = DK / 16, NBV = VB / 16;
   using GQ = Tile<MT, C, DK>;
   using GV = Tile<MT, C, VB>;
-  static_assert(GQ::PITCH == KP && NBD <= NW && NBV <= NW, "prep8 tiling");
+  static_assert(GQ::PITCH == KP && NW == 8 && NBD <= NW && NBV <= NW, "prep8 tiling");
   constexpr int VP = GV::PITCH;
   constexpr int QA = (GQ::ELEMS * 2 > C * FP * 4) ? GQ::ELEMS * 2 : C * FP * 4;   // bytes: q's tile, then A (fp32)
   constexpr int LW = (C * FP * 4 > C * KP * 2) ? C * FP * 4 : C * KP * 2;          // bytes: L (fp32), then W staged
@@ -605,31 +605,42 @@ __global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
     *reinterpret_cast<bf16x8*>(Ag + t * C + 8 * u) =
         bf16x8{(bf16)lo[0], (bf16)lo[1], (bf16)lo[2], (bf16)lo[3], (bf16)hi[0], (bf16)hi[1], (bf16)hi[2], (bf16)hi[3]};
   }
-  // B operand (A diag(f))^T, k = s: lane's token t = 16 ti + l % 16, slots s = 32 p + kmap(j, .)
-  auto fragAf = [&](int ti, int p, const float* f) -> Frag<MT> {
+  // B operand (A diag(f))^T, k = s: lane's token t = 16 ti + l % 16, slots s = 32 p + kmap(j, .), as a hi + lo pair of
+  // bf16 fragments (two products for one).  A diag(f) is fp32; rounded once to bf16 it put ~2^-9 relative error into
+  // every W and U (U is stored fp32 because Vn = U - W S cancels), which doubled the bf16 path's dg and dk against
+  // float64.  With the pair, W is the bf16 rounding of the fp32 product and U carries only fp32 error.  Wave w takes
+  // token tile ti = w % 4 and every other feature block from w / 4 on, so it splits only its own tile's two fragments
+  // (once for W's blocks, once for all of U's).
+  const int ti = w & 3, np = (16 * ti + 15) / 32 + 1;     // k-blocks p < np: the tokens s <= the tile's last row
+  auto fragAf = [&](int p, const float* f, Frag<MT>& hi, Frag<MT>& lo) {
     const int t = 16 * ti + n, s0 = 32 * p + 4 * j;
     const f4 a0 = *reinterpret_cast<const f4*>(sA + t * FP + s0), a1 = *reinterpret_cast<const f4*>(sA + t * FP + s0 + 16);
     const f4 f0 = *reinterpret_cast<const f4*>(f + s0), f1 = *reinterpret_cast<const f4*>(f + s0 + 16);
-    Frag<MT> fr;
+    Frag<float> x;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      fr.set(e, a0[e] * f0[e]);
-      fr.set(e + 4, a1[e] * f1[e]);
+      x.set(e, a0[e] * f0[e]);
+      x.set(e + 4, a1[e] * f1[e]);
     }
-    return fr;
+    frag_split(x, hi, lo);
   };
-  if (w < NBD) {
-    Frag<MT> kT[2];
+  {
+    Frag<MT> hi[2], lo[2];
 #pragma unroll
-    for (int p = 0; p < 2; ++p) kT[p] = frag_tr(tk, KP, 32 * p, 16 * w);
+    for (int p = 0; p < 2; ++p)
+      if (p < np) fragAf(p, fW, hi[p], lo[p]);
 #pragma unroll
-    for (int ti = 0; ti < 4; ++ti) {
+    for (int db = w >> 2; db < NBD; db += 2) {
       f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int p = 0; p < 2; ++p)
-        if (32 * p <= 16 * ti + 15) mma(acc, kT[p], fragAf(ti, p, fW));
+        if (p < np) {
+          const Frag<MT> kT = frag_tr(tk, KP, 32 * p, 16 * db);
+          mma(acc, kT, hi[p]);
+          mma(acc, kT, lo[p]);
+        }
       const int t = 16 * ti + n;
-      *reinterpret_cast<bf16x4*>(stW + t * KP + 16 * w + 4 * j) = bf16x4{(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
+      *reinterpret_cast<bf16x4*>(stW + t * KP + 16 * db + 4 * j) = bf16x4{(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
     }
   }
   __syncthreads();
@@ -643,6 +654,10 @@ __global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
   }
   // ---- 4: U^T = v^T (A diag(beta))^T, VB value columns per pass, written from the accumulators (4 fp32 columns a lane)
   float* Ug = a.U + bhc * C * DV;
+  Frag<MT> uhi[2], ulo[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+    if (p < np) fragAf(p, fU, uhi[p], ulo[p]);
   for (int vb = 0; vb < DV; vb += VB) {
     if (vb > 0) {                          // the next block of v, once every wave is done with this one
       __syncthreads();
@@ -656,18 +671,17 @@ __global__ void __launch_bounds__(512) prep8_kernel(PrepArgs a) {
         __syncthreads();
       }
     }
-    if (w < NBV) {
-      Frag<MT> vT[2];
 #pragma unroll
-      for (int p = 0; p < 2; ++p) vT[p] = frag_tr(tv, VP, 32 * p, 16 * w);
+    for (int vk = w >> 2; vk < NBV; vk += 2) {
+      f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ti = 0; ti < 4; ++ti) {
-        f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int p = 0; p < 2; ++p)
-          if (32 * p <= 16 * ti + 15) mma(acc, vT[p], fragAf(ti, p, fU));
-        *reinterpret_cast<f4*>(Ug + (size_t)(16 * ti + n) * DV + vb + 16 * w + 4 * j) = acc;
-      }
+      for (int p = 0; p < 2; ++p)
+        if (p < np) {
+          const Frag<MT> vT = frag_tr(tv, VP, 32 * p, 16 * vk);
+          mma(acc, vT, uhi[p]);
+          mma(acc, vT, ulo[p]);
+        }
+      *reinterpret_cast<f4*>(Ug + (size_t)(16 * ti + n) * DV + vb + 16 * vk + 4 * j) = acc;
     }
   }
 }

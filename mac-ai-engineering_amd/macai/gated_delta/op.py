@@ -29,7 +29,10 @@ MAX_DK = MAX_DV_BWD = 256
 # FUSED_NORM (the reference's switch and default, op.py:19-21): with use_qk_l2norm_in_kernel=True the drop-in's
 # query / key prologue (l2 normalisation, the query's DK^-1/2 scale) runs inside the kernels, its backward inside the
 # per-chunk backward (True); False runs the normalisation as PyTorch operations in float32 (autograd takes its
-# backward), rounds the normalised query and key to the compute dtype and leaves the kernels only the scale.
+# backward) and leaves the kernels only the scale.  The kernels then do not normalise the keys, so a bf16 call runs
+# on the float32 kernels with the normalised query and key kept in float32 (unless BF16_UNNORMALIZED, which rounds
+# them to bf16): rounding the normalised keys to bf16 adds their quantization to every product (dg 7.9e-3, o 7.5e-3
+# worst over 30 random draws of the oracle's rounding model, against 5-7e-3 with the kernels' own normalisation).
 FUSED_NORM = True
 # BF16_OPERANDS: bfloat16 inputs run on bf16 MFMA operands with fp32 accumulation and an fp32 state (True, the
 # default: the fast path, outputs and gradients within ~5e-3 of float64).  False upcasts them exactly and runs the
@@ -50,6 +53,15 @@ BF16_UNNORMALIZED = False
 # long rows), so a forward without gradients keeps the bf16 kernels.  The default is one chunk; 0 keeps every length
 # on the bf16 kernels.
 BF16_MIN_TOKENS = 64
+# BF16_STATE_GRAD: the backward of a bf16 call whose final state receives a gradient (sT in the loss, or passed on
+# to a later segment's backward) keeps the bf16 operands (True) or runs on the float32 kernels (False, the default:
+# the inputs upcast exactly, the states recomputed, dq, dk, dv cast back).  A final-state gradient of the size of the
+# output's feeds the last chunk's state gradient and, through it, dg's Vn dS^T terms and dbeta's dVn, whose bf16
+# rounding then no longer averages out: over random draws of 64-200 tokens with an N(0, 1) final-state gradient the
+# bf16 backward put dg or dbeta over the 1e-2 bar in about one draw in six (dg up to 3.0e-2, dbeta up to 1.7e-2; the
+# oracle's rounding model and the kernels agree to three digits), against at most 6.8e-3 over the same draws without
+# it.  A backward without a final-state gradient (output_final_state=False, or sT unused) keeps the bf16 kernels.
+BF16_STATE_GRAD = False
 # VALUE_SPLIT: workgroups a head-row's value columns are split over in the state passes (each owns DV / VALUE_SPLIT
 # columns as DV / 16 / VALUE_SPLIT waves of 16 columns): "auto" (split_for) or 1, 2, 4, 8, ...
 VALUE_SPLIT = "auto"
@@ -414,6 +426,19 @@ def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=
     return dq, dk, dv, dg, dbeta, ds0
 
 
+def _backward_routed(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=None, r=None):
+    """_backward, or -- for bf16 operands with a final-state gradient while BF16_STATE_GRAD is off -- _backward on the
+    float32 kernels: q, k, v and dO upcast exactly, the states recomputed (the forward's kept bf16 operands, if any,
+    are not used), dq, dk, dv cast back to bf16."""
+    if dsT is None or q.dtype != torch.bfloat16 or BF16_STATE_GRAD:
+        return _backward(q, k, v, g, beta, s0, do, dsT, l2norm, q_scale, pack, r)
+    CALLS["bwd f32 for a final-state gradient"] += 1
+    f32 = torch.float32
+    dq, dk, dv, dg, dbeta, ds0 = _backward(q.to(f32), k.to(f32), v.to(f32), g, beta, s0, do.to(f32), dsT, l2norm,
+                                           q_scale, pack)
+    return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg, dbeta, ds0
+
+
 def _save(ctx, inputs, r):
     """Save the inputs and, when the forward kept its per-chunk scratch (RECOMPUTE_STATES False), that allocation
     with them: save_for_backward hands both to saved-tensor hooks and frees them with the graph."""
@@ -448,6 +473,7 @@ class GatedDeltaRule(torch.autograd.Function):
             o, sT, r = _forward(q, k, v, g, beta, s0, False, 1.0, True, keep=keep, save=save)
         if save:
             _save(ctx, (q, k, v, g, beta, s0), r)
+        ctx.set_materialize_grads(False)   # an unused sT's gradient arrives as None, not as zeros (BF16_STATE_GRAD)
         return o.to(ctx.io_dtype), sT
 
     @staticmethod
@@ -456,7 +482,7 @@ class GatedDeltaRule(torch.autograd.Function):
         do = torch.zeros_like(v) if do is None else _as(do, v.dtype)
         dsT = None if dsT is None else _as(dsT, torch.float32)
         with _on(q.device):
-            dq, dk, dv, dg, dbeta, ds0 = _backward(q, k, v, g, beta, s0, do, dsT, False, 1.0, r=r)
+            dq, dk, dv, dg, dbeta, ds0 = _backward_routed(q, k, v, g, beta, s0, do, dsT, False, 1.0, None, r)
         dt = ctx.io_dtype
         return dq.to(dt), dk.to(dt), dv.to(dt), dg, dbeta, ds0, None
 
@@ -477,6 +503,7 @@ class _DropIn(torch.autograd.Function):
             _save(ctx, (query, key, value, g, beta, s0), r)
             ctx.cfg = (l2norm, q_scale, s0 is not None)
             ctx.pack = pack
+        ctx.set_materialize_grads(False)   # an unused sT's gradient arrives as None, not as zeros (BF16_STATE_GRAD)
         if sT is None:
             return o
         return o, sT
@@ -488,7 +515,8 @@ class _DropIn(torch.autograd.Function):
         do = torch.zeros_like(value) if do is None else _as(do, value.dtype)
         dsT = None if dsT is None else _as(dsT, torch.float32)
         with _on(query.device):
-            dq, dk, dv, dg, dbeta, ds0 = _backward(query, key, value, g, beta, s0, do, dsT, l2norm, q_scale, ctx.pack, r)
+            dq, dk, dv, dg, dbeta, ds0 = _backward_routed(query, key, value, g, beta, s0, do, dsT, l2norm, q_scale,
+                                                          ctx.pack, r)
         return dq, dk, dv, dg, dbeta, (ds0 if has_s0 else None), None, None, None, None, None
 
 
@@ -498,9 +526,9 @@ def l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
 
 def compute_dtype(dtype, DK: int, DV: int = 0, save: bool = False, normalized: bool = True, tokens: int = None):
     """The operand type the kernels compute a call in: bfloat16 inputs on bf16 MFMA at key widths 32, 64, 128 and --
-    when the call saves for a backward -- value widths up to 128 (unless BF16_OPERANDS is off), when the keys reach the
-    products with unit norm (normalized: the kernels' or the eager prologue's l2 normalisation; unless
-    BF16_UNNORMALIZED) and, when the call saves for a backward, the rows hold at least BF16_MIN_TOKENS tokens (tokens:
+    when the call saves for a backward -- value widths up to 128 (unless BF16_OPERANDS is off), when the kernels
+    normalise the keys (normalized: use_qk_l2norm_in_kernel with FUSED_NORM; unless BF16_UNNORMALIZED) and, when the
+    call saves for a backward, the rows hold at least BF16_MIN_TOKENS tokens (tokens:
     the row length; None: not checked); float16, float32 and everything else on the float32 kernels."""
     bf16 = (dtype == torch.bfloat16 and DK in BF16_DK and BF16_OPERANDS and (normalized or BF16_UNNORMALIZED)
             and (not save or (DV <= BF16_MAX_DV_BWD and (tokens is None or tokens >= BF16_MIN_TOKENS))))
@@ -529,11 +557,12 @@ def plan(B: int, T: int, H: int, DK: int, DV: int, save: bool, Hk: int = None, d
     """What a drop-in call of these dimensions runs under the current settings (the reference's plan, op.py:105-113,
     for this build's kernels): the chunk length (64 for every pass), the operand type, the forward's segments, value
     split and state-pass kernel, and -- when the forward saves for a backward -- whether the backward recomputes
-    (RECOMPUTE_STATES), its state passes, their split and the per-chunk backward's kernel.  cus: the device's compute
+    (RECOMPUTE_STATES), its state passes, their split, the per-chunk backward's kernel and the operands of a backward
+    that receives a gradient of the final state (BF16_STATE_GRAD).  cus: the device's compute
     units (the persistent per-chunk backward runs where there are more chunk-heads than CUs); l2norm: the call's
     use_qk_l2norm_in_kernel."""
     Hk = Hk or H
-    cdt = compute_dtype(dtype, DK, DV, save, l2norm, T)
+    cdt = compute_dtype(dtype, DK, DV, save, l2norm and FUSED_NORM, T)
     bf = cdt == torch.bfloat16
     NT = math.ceil(T / CHUNK)
     recompute = save and RECOMPUTE_STATES
@@ -554,6 +583,8 @@ def plan(B: int, T: int, H: int, DK: int, DV: int, save: bool, Hk: int = None, d
         out["bwd_split"] = split_for(B * H, T, DV, 2 if pair else 1)
         units = B * H * NT
         out["chunk_bwd"] = (("chunk_bwd8xn" if DK == DV and units > cus else "chunk_bwd8") if bf else "chunk_bwd")
+        # a backward that receives a gradient of the final state (BF16_STATE_GRAD)
+        out["state_grad_operands"] = "f32" if bf and not BF16_STATE_GRAD else out["operands"]
     return out
 
 
@@ -581,7 +612,8 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size: int = 64, ini
     grads = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (query, key, value, g, beta, initial_state))
     _widths(query.shape[-1], value.shape[-1], grads)
-    cdt = compute_dtype(dtype, query.shape[-1], value.shape[-1], grads, bool(use_qk_l2norm_in_kernel), query.shape[1])
+    cdt = compute_dtype(dtype, query.shape[-1], value.shape[-1], grads, bool(use_qk_l2norm_in_kernel) and FUSED_NORM,
+                        query.shape[1])
     if use_qk_l2norm_in_kernel and not FUSED_NORM:
         query, key = eager_prologue(query, key, cdt)
         use_qk_l2norm_in_kernel = False

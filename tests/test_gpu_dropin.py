@@ -100,13 +100,15 @@ def test_config0_fp32_forward():
 
 @pytest.mark.parametrize("recompute", [True, False], ids=["recompute", "stored"])
 @pytest.mark.parametrize("cfg", [1, 2])
-def test_config_bf16_fwd_bwd(cfg, recompute):
+def test_config_bf16_fwd_bwd(cfg, recompute, monkeypatch):
     """Configs 1 and 2 at full size: bf16 q/k/v/dO, fp32 g/beta (config 2: Hk=16 repeated to Hv=32, an initial state
-    and its gradient, the final state used): every output and gradient within 1e-2.  recompute: the backward reruns
+    and its gradient, the final state used, its backward kept on the bf16 kernels by op.BF16_STATE_GRAD): every output
+    and gradient within 1e-2.  recompute: the backward reruns
     prep and recomputes the chunk states beside its reverse pass in one launch (the reference's default and BASELINE
     config 1's form; at config 1's 64 head-rows that is macai_gdr_state_pair at split 2, four column waves a
     workgroup); stored: the forward keeps them."""
     _say(f"case config{cfg} recompute={recompute}")
+    monkeypatch.setattr(op, "BF16_STATE_GRAD", True)
     inp = gdr.config_inputs(cfg)
     dsT = torch.randn(inp["value"].shape[0], inp["value"].shape[2], 128, 128,
                       generator=torch.Generator().manual_seed(77)) if cfg == 2 else None
@@ -188,20 +190,23 @@ def test_dropin_fp32_within_twice_the_torch_path(shape, s0):
 def test_dropin_bf16_small(shape, kernels):
     """bf16 drop-in end to end with a starting state and the final state used (reference test_harness.py:139-166),
     including one- to three-token rows at D = 128, where a chunk has a single valid row or two.  "default": rows
-    shorter than a chunk run on the float32 kernels (op.BF16_MIN_TOKENS); "bf16": op.BF16_MIN_TOKENS = 0 keeps them on
-    the bf16 kernels, whose one- to three-row chunks these draws hold to the bar too."""
+    shorter than a chunk run on the float32 kernels (op.BF16_MIN_TOKENS), and the backward of the others, which gets
+    the final state's gradient, too (op.BF16_STATE_GRAD); "bf16": both switches keep every part on the bf16 kernels,
+    whose one- to three-row chunks these draws hold to the bar too."""
     B, T, H, D = shape
     _say(f"case dropin_bf16 {shape} {kernels}")
     inp = gdr.make_inputs(B, T, H, H, D, D, torch.bfloat16, s0=True, seed=8)
     dsT = torch.randn(B, H, D, D, generator=torch.Generator().manual_seed(9))
-    old = op.BF16_MIN_TOKENS
+    old = op.BF16_MIN_TOKENS, op.BF16_STATE_GRAD
     try:
         if kernels == "bf16":
-            op.BF16_MIN_TOKENS = 0
-        assert op.plan(B, T, H, D, D, True)["operands"] == ("f32" if kernels == "default" and T < 64 else "bf16")
+            op.BF16_MIN_TOKENS, op.BF16_STATE_GRAD = 0, True
+        p = op.plan(B, T, H, D, D, True)
+        assert p["operands"] == ("f32" if kernels == "default" and T < 64 else "bf16")
+        assert p["state_grad_operands"] == ("f32" if kernels == "default" else "bf16")
         check_dropin(inp, bar=BF16_BAR, dsT=dsT)
     finally:
-        op.BF16_MIN_TOKENS = old
+        op.BF16_MIN_TOKENS, op.BF16_STATE_GRAD = old
 
 
 @pytest.mark.parametrize("shape", [(2, 50, 3, 128), (1, 130, 2, 64)])
@@ -237,6 +242,39 @@ def test_bf16_calls_on_the_float32_kernels(why):
     assert torch.equal(o, o2.to(o.dtype)) and torch.equal(sT, sT2)
     for n in g:
         assert torch.equal(g[n], g2[n].to(g[n].dtype)), n
+
+
+def test_final_state_gradient_backward_on_the_float32_kernels():
+    """A bf16 call whose final state receives a gradient runs its backward on the float32 kernels (op.BF16_STATE_GRAD
+    off, the default): on a 150-token draw with an N(0, 1) final-state gradient (seed 209), where the bf16 backward's
+    dg is 2.4e-2 from float64 (the oracle's rounding model gives the same; tests/test_host.py), every output and
+    gradient is within 1e-2, and the gradients are those of the call run wholly on the float32 kernels
+    (op.BF16_OPERANDS off) bit for bit, cast to bf16 -- the backward recomputes from the inputs, so only the output o
+    keeps the bf16 forward's rounding.  With op.BF16_STATE_GRAD the bf16 backward runs and misses the bar on dg."""
+    _say("case final-state gradient backward")
+    inp = gdr.make_inputs(1, 150, 2, 2, 128, 128, torch.bfloat16, s0=True, seed=209)
+    dsT = torch.randn(1, 2, 128, 128, generator=torch.Generator().manual_seed(216))
+    key = "bwd f32 for a final-state gradient"
+    before = op.CALLS[key]
+    errs = check_dropin(inp, bar=BF16_BAR, dsT=dsT)
+    assert op.CALLS[key] == before + 1
+    o, sT, g = run_dropin(inp, dsT=dsT)
+    old = op.BF16_OPERANDS, op.BF16_STATE_GRAD
+    try:
+        op.BF16_OPERANDS = False
+        o32, sT32, g32 = run_dropin(inp, dsT=dsT)
+        op.BF16_OPERANDS, op.BF16_STATE_GRAD = True, True
+        before = op.CALLS[key]
+        ob, sTb, gb = run_dropin(inp, dsT=dsT)
+        assert op.CALLS[key] == before
+    finally:
+        op.BF16_OPERANDS, op.BF16_STATE_GRAD = old
+    for n in g:
+        assert torch.equal(g[n], g32[n].to(g[n].dtype)), n
+    rg = gdr.dropin_f64(*(inp[n] for n in ("query", "key", "value", "g", "beta", "initial_state")), do=inp["do"],
+                        dsT=dsT)[2]
+    _say(f"dg with the bf16 backward {gdr.rel(gb['dg'], rg['dg']):.2e}, rerouted {errs['dg']:.2e}")
+    assert gdr.rel(gb["dg"], rg["dg"]) > BF16_BAR and errs["dg"] < 1e-3
 
 
 def test_calls_without_tokens():
@@ -276,7 +314,8 @@ def _prenormalised(inp):
 def test_dropin_unfused_prologue(dtype):
     """use_qk_l2norm_in_kernel=False: no normalisation, only the query's DK^-1/2 scale (reference op.py:279-283), on
     pre-normalised inputs.  bf16: on the bf16 kernels (op.BF16_UNNORMALIZED, which such a caller may set; by default
-    these calls take the float32 kernels), every output and gradient within 1e-2 on each of four seeds.  float32:
+    these calls take the float32 kernels), the final-state gradient's backward too (op.BF16_STATE_GRAD), every output
+    and gradient within 1e-2 on each of four seeds.  float32:
     within 2x the torch path's own float32 error, both taken as the largest over the four seeds: one draw of that
     error varies up to 6x between seeds of this shape (dbeta 1.3e-7 to 7.7e-7), too noisy a yardstick for a single
     case."""
@@ -286,13 +325,13 @@ def test_dropin_unfused_prologue(dtype):
         inp = _prenormalised(gdr.make_inputs(2, 100, 3, 3, 128, 128, dtype, s0=True, seed=12 + seed))
         dsT = torch.randn(2, 3, 128, 128, generator=torch.Generator().manual_seed(9 + seed))
         if dtype == torch.bfloat16:
-            old = op.BF16_UNNORMALIZED
+            old = op.BF16_UNNORMALIZED, op.BF16_STATE_GRAD
             try:
-                op.BF16_UNNORMALIZED = True
+                op.BF16_UNNORMALIZED, op.BF16_STATE_GRAD = True, True
                 assert op.plan(2, 100, 3, 128, 128, True, l2norm=False)["operands"] == "bf16"
                 check_dropin(inp, bar=BF16_BAR, dsT=dsT, l2norm=False)
             finally:
-                op.BF16_UNNORMALIZED = old
+                op.BF16_UNNORMALIZED, op.BF16_STATE_GRAD = old
             continue
         ro, rsT, rg = gdr.dropin_f64(*(inp[n] for n in ("query", "key", "value", "g", "beta", "initial_state")),
                                      do=inp["do"], dsT=dsT, use_qk_l2norm_in_kernel=False)
@@ -415,12 +454,14 @@ def test_rule_bf16_operands():
     check_rule(gdr.harness_inputs(2, 100, 2, 128, 128, seed=4), BF16_BAR, dtype=torch.bfloat16)
 
 
-def test_bf16_inputs_on_the_float32_kernels():
+def test_bf16_inputs_on_the_float32_kernels(monkeypatch):
     """BF16_OPERANDS = False: bf16 inputs upcast exactly and run on the float32 kernels, the reference's own
     precision for every input (op.py:276-285, 297).  On the smoke's case the float32 outputs and gradients (sT, dg,
-    dbeta, ds0) come within 1e-4 of float64, at least 10x closer than the bf16-operand default, and the bf16 outputs
-    and gradients within their own rounding (1e-2)."""
+    dbeta, ds0) come within 1e-4 of float64, at least 10x closer than the bf16 operands (their backward with the final
+    state's gradient kept on them: op.BF16_STATE_GRAD), and the bf16 outputs and gradients within their own rounding
+    (1e-2)."""
     _say("case bf16 inputs on float32 kernels")
+    monkeypatch.setattr(op, "BF16_STATE_GRAD", True)
     inp = gdr.make_inputs(1, 100, 2, 2, 128, 128, torch.bfloat16, s0=True, seed=7)
     dsT = torch.randn(1, 2, 128, 128, generator=torch.Generator().manual_seed(11))
     ro, rsT, rg = gdr.dropin_f64(*(inp[n] for n in ("query", "key", "value", "g", "beta", "initial_state")),
@@ -461,7 +502,14 @@ def _grads_once(inp, split=None, dsT_width=128):
     return [o, sT] + [g[n] for n in sorted(g)]
 
 
-def test_backward_is_bitwise_deterministic():
+@pytest.fixture
+def bf16_state_grad(monkeypatch):
+    """op.BF16_STATE_GRAD on: a backward with a final-state gradient stays on the bf16 kernels, whose invariances the
+    tests below pin (by default such a backward runs the float32 kernels)."""
+    monkeypatch.setattr(op, "BF16_STATE_GRAD", True)
+
+
+def test_backward_is_bitwise_deterministic(bf16_state_grad):
     """One writer per gradient element, no atomics: three runs give identical bits (reference test_harness.py:196-211)."""
     _say("case determinism")
     inp = gdr.make_inputs(2, 100, 2, 2, 128, 128, torch.bfloat16, s0=True, seed=5)
@@ -487,7 +535,7 @@ def test_persistent_chunk_backward_equals_per_row_runs(B, T, Hk, Hv, D):
             assert torch.equal(g[n][b:b + 1], gb[n]), (b, n)
 
 
-def test_value_split_changes_no_bits():
+def test_value_split_changes_no_bits(bf16_state_grad):
     """Splitting a head-row's value columns over 1, 2, 4 or 8 workgroups changes no arithmetic: identical bits
     (reference test_chunking.py:108-128)."""
     _say("case split bits")
@@ -497,7 +545,7 @@ def test_value_split_changes_no_bits():
 
 
 @pytest.mark.parametrize("split", [2, 4])
-def test_overlapped_passes_change_no_bits(split):
+def test_overlapped_passes_change_no_bits(split, bf16_state_grad):
     """In the recompute mode (the default) the backward's recompute and reverse passes run in one launch
     (op.OVERLAP, macai_gdr_state_pair) or as two launches: identical bits, several times in a row.  split 2 gives
     four column waves a workgroup (config 1's pair pass), split 4 two."""
@@ -519,7 +567,7 @@ def test_overlapped_passes_change_no_bits(split):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_kept_prep_operands_change_no_bits(dtype):
+def test_kept_prep_operands_change_no_bits(dtype, bf16_state_grad):
     """The training forward keeping prep's operands (with A) for the backward (op.RECOMPUTE_STATES = False) or the
     backward recomputing them (True, the reference's default, op.py:27-33): the same output and gradient bits
     (the reference's claim for its switch, tests/test_memory.py)."""
@@ -539,14 +587,16 @@ def test_kept_prep_operands_change_no_bits(dtype):
 
 def test_unfused_prologue_switch():
     """op.FUSED_NORM = False (the reference's switch, op.py:19-21): the query / key normalisation runs as float32
-    PyTorch operations (autograd through them) and the kernels apply only the scale; outputs and gradients within the
-    bf16 bar of float64."""
+    PyTorch operations (autograd through them) and the kernels apply only the scale, on the float32 kernels with the
+    normalised values kept in float32; outputs and gradients within the bf16 bar of float64 (rounding the normalised
+    keys to bf16 for the bf16 kernels put dg at 9.4e-3 on this draw, and the oracle's model over 1e-2 on others)."""
     _say("case fused_norm off")
     inp = gdr.make_inputs(2, 150, 3, 3, 128, 128, torch.bfloat16, s0=True, seed=31)
     dsT = torch.randn(2, 3, 128, 128, generator=torch.Generator().manual_seed(32))
     old = op.FUSED_NORM
     try:
         op.FUSED_NORM = False
+        assert op.plan(2, 150, 3, 128, 128, True)["operands"] == "f32"
         check_dropin(inp, bar=BF16_BAR, dsT=dsT)
     finally:
         op.FUSED_NORM = old

@@ -13,12 +13,19 @@ import torch
 
 import _parity
 
-from macai.gated_delta import chunk_gated_delta_rule, recurrent_gated_delta_rule
+from macai.gated_delta import chunk_gated_delta_rule, op, recurrent_gated_delta_rule
 from oracle import gdr
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 NAMES = ("dquery", "dkey", "dvalue", "dg", "dbeta", "dstate")
+
+
+@pytest.fixture(autouse=True)
+def _bf16_backward(monkeypatch):
+    """The backward with the final state's gradient stays on the bf16 kernels (op.BF16_STATE_GRAD), whose grouped-head
+    forms these tests pin (by default it runs the float32 kernels)."""
+    monkeypatch.setattr(op, "BF16_STATE_GRAD", True)
 
 
 def _say(*a):

@@ -22,8 +22,11 @@ DEV = "cuda"
 @pytest.fixture(autouse=True)
 def _same_kernels_alone(monkeypatch):
     """A packed row runs on the bf16 kernels whatever its sequences' lengths; a bf16 sequence shorter than a chunk run
-    alone would take the float32 kernels (op.BF16_MIN_TOKENS).  The comparisons here run it on the bf16 kernels too."""
+    alone would take the float32 kernels (op.BF16_MIN_TOKENS).  The comparisons here run it on the bf16 kernels too,
+    and keep the backward with the final states' gradient on them (op.BF16_STATE_GRAD): these tests pin the bf16
+    kernels' packed-row forms."""
     monkeypatch.setattr(op, "BF16_MIN_TOKENS", 0)
+    monkeypatch.setattr(op, "BF16_STATE_GRAD", True)
 
 
 def _say(*a):

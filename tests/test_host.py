@@ -350,7 +350,8 @@ def test_unnormalized_keys_take_the_float32_kernels(monkeypatch):
     op.BF16_UNNORMALIZED: the bf16 operands' rounding is amplified as beta |k|^2 grows.  The oracle's rounding model
     (the bf16 path's operand classes) on N(0, 1) keys over 200 tokens at DK = 32 moves o by 1.2e-1 on one of six draws
     (seed 501; the others 4e-3 to 9e-3); the same inputs normalised in the kernels stay under 1e-2.  FUSED_NORM = False
-    normalises in its eager prologue, so it keeps the bf16 kernels."""
+    normalises in its eager prologue, not in the kernels, so it takes the float32 kernels too
+    (test_fused_norm_switch)."""
     bf, f32 = torch.bfloat16, torch.float32
     assert op.compute_dtype(bf, 128, 128, True, normalized=False) == f32
     assert op.compute_dtype(bf, 128, 128, True, normalized=True) == bf
@@ -365,6 +366,65 @@ def test_unnormalized_keys_take_the_float32_kernels(monkeypatch):
         o2, sT2, gr2 = gdr.dropin_f64(*(inp[n] for n in names), do=inp["do"], use_qk_l2norm_in_kernel=l2, rnd=model)
         worst[l2] = max([gdr.rel(o2, o), gdr.rel(sT2, sT)] + [gdr.rel(gr2[n], gr[n]) for n in gr])
     assert worst[False] > 5e-2 and worst[True] < 1e-2, worst
+
+
+def test_final_state_gradient_takes_the_float32_backward(monkeypatch):
+    """The backward of a bf16 call that receives a gradient of the final state runs on the float32 kernels (q, k, v
+    and dO upcast, dq, dk, dv cast back) unless op.BF16_STATE_GRAD; without one -- output_final_state=False, or sT
+    left out of the loss, whose gradient then arrives as None -- it keeps the bf16 operands.  Both autograd functions,
+    with the launches replaced by recorders.  Why: the oracle's rounding model of the bf16 path (which the kernels
+    follow to three digits on this draw) over 150 tokens with an N(0, 1) final-state gradient (seed 209) moves dg by
+    2.4e-2; the same draw without it stays under 5e-3."""
+    import contextlib
+    bf, f32 = torch.bfloat16, torch.float32
+    seen = []
+
+    def fake_forward(q, k, v, g, beta, s0, l2norm, q_scale, want_sT, pack=None, keep=False, save=True):
+        B, T, H, DV = v.shape
+        return v.new_zeros(v.shape), (torch.zeros(B, H, q.shape[-1], DV) if want_sT else None), None
+
+    def fake_backward(q, k, v, g, beta, s0, do, dsT, l2norm, q_scale, pack=None, r=None):
+        seen.append((q.dtype, k.dtype, v.dtype, do.dtype, dsT is not None))
+        z = torch.zeros_like
+        return z(q), z(k), z(v), z(g), z(beta), None if s0 is None else z(s0)
+
+    monkeypatch.setattr(op, "_forward", fake_forward)
+    monkeypatch.setattr(op, "_backward", fake_backward)
+    monkeypatch.setattr(op, "_on", lambda dev: contextlib.nullcontext())
+    monkeypatch.setattr(op, "_check", lambda *a, **kw: None)
+    gen = torch.Generator().manual_seed(2)
+    q, k, v = (torch.randn(1, 64, 2, 64, generator=gen).to(bf).requires_grad_(True) for _ in range(3))
+    g, b = -torch.rand(1, 64, 2, generator=gen), torch.rand(1, 64, 2, generator=gen)
+    s0 = torch.zeros(1, 2, 64, 64, requires_grad=True)
+
+    def run(fn, with_state_grad):
+        seen.clear()
+        if fn == "dropin":
+            o, sT = op._DropIn.apply(q, k, v, g, b, None, True, 0.125, True, True, None)
+        else:
+            o, sT = op.GatedDeltaRule.apply(q, k, v, g, b, s0, True)
+        outs = [o, sT] if with_state_grad else [o]
+        torch.autograd.backward(outs, [torch.ones_like(x) for x in outs])
+        assert q.grad.dtype == bf and v.grad.dtype == bf
+        q.grad = k.grad = v.grad = None
+        return seen[0]
+
+    for fn in ("dropin", "rule"):
+        assert run(fn, False) == (bf, bf, bf, bf, False)        # sT out of the loss: its gradient is None
+        assert run(fn, True) == (f32, f32, f32, f32, True)
+        monkeypatch.setattr(op, "BF16_STATE_GRAD", True)
+        assert run(fn, True) == (bf, bf, bf, bf, True)
+        monkeypatch.setattr(op, "BF16_STATE_GRAD", False)
+    assert op.plan(4, 1024, 16, 128, 128, True)["state_grad_operands"] == "f32"
+    assert op.plan(4, 1024, 16, 128, 128, True, dtype=f32)["state_grad_operands"] == "f32"
+    model = tuple(c for c in gdr.ROUNDABLE if c != "QK")
+    names = ("query", "key", "value", "g", "beta", "initial_state")
+    inp = gdr.make_inputs(1, 150, 2, 2, 128, 128, bf, s0=True, seed=209)
+    dsT = torch.randn(1, 2, 128, 128, generator=torch.Generator().manual_seed(216)).double()
+    for state_grad, lo, hi in ((dsT, 1e-2, 1.0), (None, 0.0, 5e-3)):
+        exact = gdr.dropin_f64(*(inp[n] for n in names), do=inp["do"], dsT=state_grad)[2]["dg"]
+        path = gdr.dropin_f64(*(inp[n] for n in names), do=inp["do"], dsT=state_grad, rnd=model)[2]["dg"]
+        assert lo <= gdr.rel(path, exact) < hi, state_grad is None
 
 
 def test_misaligned_inputs_are_copied_not_refused():
@@ -406,8 +466,9 @@ def test_short_rows_take_the_float32_kernels(monkeypatch):
 
 def test_fused_norm_switch(monkeypatch):
     """op.FUSED_NORM (the reference's switch, op.py:19-21): True hands the raw query and key to the kernels with the
-    normalisation fused (use_l2norm 1); False normalises them as float32 PyTorch operations (autograd records them),
-    rounds them to the compute dtype and asks the kernels for the scale only (use_l2norm 0)."""
+    normalisation fused (use_l2norm 1); False normalises them as float32 PyTorch operations (autograd records them)
+    and asks the kernels for the scale only (use_l2norm 0), on the float32 kernels with the normalised values kept in
+    float32 -- or, with op.BF16_UNNORMALIZED, rounded to bf16."""
     seen = {}
 
     def fake_apply(q, k, v, g, beta, s0, l2norm, q_scale, want_sT, save, pack):
@@ -425,9 +486,15 @@ def test_fused_norm_switch(monkeypatch):
     qr = q.clone().requires_grad_(True)
     chunk_gated_delta_rule(qr, k, v, g, b, use_qk_l2norm_in_kernel=True)
     assert seen["l2norm"] is False and seen["q_scale"] == 64 ** -0.5
+    assert seen["q"].dtype == torch.float32 and seen["q"].requires_grad
+    assert torch.equal(seen["q"], op.l2norm(q.float())) and torch.equal(seen["k"], op.l2norm(k.float()))
+    assert op.plan(1, 64, 2, 64, 64, True)["operands"] == "f32"
+    monkeypatch.setattr(op, "BF16_UNNORMALIZED", True)
+    chunk_gated_delta_rule(qr, k, v, g, b, use_qk_l2norm_in_kernel=True)
     assert seen["q"].dtype == torch.bfloat16 and seen["q"].requires_grad
     assert torch.equal(seen["q"], op.l2norm(q.float()).to(torch.bfloat16))
     assert torch.equal(seen["k"], op.l2norm(k.float()).to(torch.bfloat16))
+    monkeypatch.setattr(op, "BF16_UNNORMALIZED", False)
     chunk_gated_delta_rule(q, k, v, g, b, use_qk_l2norm_in_kernel=False)      # nothing to normalise either way;
     assert seen["l2norm"] is False and seen["q"].dtype == torch.float32       # keys of unknown norm: float32 kernels
     assert torch.equal(seen["q"], q.float())
