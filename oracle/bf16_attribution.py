@@ -1,12 +1,15 @@
 """Where the bf16 path's error comes from: the float64 oracle with one operand class at a time rounded to bf16 where
-the bf16 kernels feed it to an MFMA product (oracle.gdr.ROUNDABLE), then combinations of classes kept at full
-precision (the cost of hi + lo bf16 pairs for them), against float64 of the same inputs.  Test infrastructure / design
-analysis only (CPU): `python oracle/bf16_attribution.py` prints the table DESIGN.md section 4 quotes.
+a bf16 MFMA product would take it (oracle.gdr.ROUNDABLE), then the classes the kernels round (oracle.gdr.BF16_PATH)
+and combinations of them kept at full precision (the cost of hi + lo bf16 pairs for them), against float64 of the
+same inputs.  Test infrastructure / design analysis only (CPU): `python oracle/bf16_attribution.py` prints the table
+in markdown.
 
-Cases: the smoke case of __graft_entry__.smoke (B=1, T=100, H=2, D=128, bf16, s0 and dsT) and the same draw at 1024
-tokens with g x 0.005 (the many-chunk chain cases' decay).  Every run also rounds the bf16 outputs (o, dq, dk, dv)
-once, as the kernels do; "QK" (the normalised q, k as operands) is left out of the model's default, since the kernels
-take the raw bf16 q, k (exact) and apply the norms in fp32.
+Cases: the smoke's draw (B=1, T=100, H=2, D=128, bf16, a starting state) with an N(0, 1) gradient of the final state
+(on the bf16 kernels only with op.BF16_STATE_GRAD), and the same draw at 1024 tokens with g x 0.005 (the many-chunk
+chain cases' decay).  Every run also rounds the bf16 outputs (o, dq, dk, dv) once, as the kernels do.  "QK" (the
+normalised q, k as operands) is not in the path, since the kernels take the raw bf16 q, k (exact) and apply the norms
+in fp32, nor is "Sc" (the per-chunk backward takes the chunk state as a hi + lo pair); its row shows what rounding it
+once would add.
 """
 import os
 import sys
@@ -18,7 +21,8 @@ from oracle import gdr  # noqa: E402
 
 NAMES = ("query", "key", "value", "g", "beta", "initial_state")
 OUTS = ("o", "sT", "dquery", "dkey", "dvalue", "dg", "dbeta", "dstate")
-MODEL = tuple(c for c in gdr.ROUNDABLE if c != "QK")
+MODEL = gdr.BF16_PATH
+CLASSES = tuple(c for c in gdr.ROUNDABLE if c != "QK")   # one row each (Sc: what rounding S_c once would add)
 
 
 def case(T, scale):
@@ -48,7 +52,7 @@ def main():
         print(f"## {tag}")
         print("| rounded to bf16 | " + " | ".join(OUTS) + " |")
         print("|---" * (len(OUTS) + 1) + "|")
-        rows = [(f"only {c}", (c,)) for c in MODEL] + list(combos.items())
+        rows = [(f"only {c}", (c,)) for c in CLASSES] + list(combos.items())
         for name, rnd in rows:
             e = errors(inp, dsT, rnd, exact)
             print(f"| {name} | " + " | ".join(f"{e[n]:.1e}" for n in OUTS) + " |", flush=True)
