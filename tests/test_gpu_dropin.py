@@ -468,7 +468,8 @@ def test_rule_bf16_operands():
 
 def test_bf16_inputs_on_the_float32_kernels(monkeypatch):
     """BF16_OPERANDS = False: bf16 inputs upcast exactly and run on the float32 kernels, the reference's own
-    precision for every input (op.py:276-285, 297).  On the smoke's case the float32 outputs and gradients (sT, dg,
+    precision for every input (op.py:276-285, 297).  On the smoke's draw with a final-state gradient (the bf16
+    attribution case) the float32 outputs and gradients (sT, dg,
     dbeta, ds0) come within 1e-4 of float64, at least 10x closer than the bf16 operands (their backward with the final
     state's gradient kept on them: op.BF16_STATE_GRAD), and the bf16 outputs and gradients within their own rounding
     (1e-2)."""
