@@ -46,13 +46,14 @@ BF16_OPERANDS = True
 # turn it on, or pass use_qk_l2norm_in_kernel=True (normalising a unit vector again changes it by rounding only).
 BF16_UNNORMALIZED = False
 # BF16_MIN_TOKENS: bf16 calls that save for a backward, on rows shorter than this many tokens, run on the float32
-# kernels.  With so few tokens the bf16 operands' rounding is not averaged out -- dg and dq of a row of a few tokens are
-# sums of few, cancelling terms: the oracle's rounding model of the bf16 path puts 12 of 160 random rows of 2, 3, 5
-# and 8 tokens over the 1e-2 bar (dg up to 5.7e-2), none of 40 each at 1, 16, 32 and 63 tokens (the worst 9.2e-3, at
-# 16) -- and the float32 kernels cost next to nothing at that size.  The forward's outputs are not affected (the
-# model's worst o and sT over 60 draws of 1-16 tokens: 8e-3, as on long rows), so a forward without gradients keeps
-# the bf16 kernels.  The default is one chunk; 0 keeps every length on the bf16 kernels.
-BF16_MIN_TOKENS = 64
+# kernels.  With few tokens the bf16 operands' rounding is not averaged out -- dg and dq of a row of a few tokens are
+# sums of few, cancelling terms, and dg of a row of about one chunk is small against its terms: the oracle's rounding
+# model of the bf16 path puts 12 of 160 random rows of 2, 3, 5 and 8 tokens over the 1e-2 bar (dg up to 5.7e-2), 2
+# of 150 rows of 64 tokens and 1 of 150 of 65 (dg up to 1.7e-2, through Vn in the per-chunk backward's dO Vn^T), and
+# none of 150 each at 72, 80, 88, 96, 100, 112 and 128 tokens -- and the float32 kernels cost next to nothing at that
+# size.  The forward's outputs are not affected (the model's worst o and sT over 60 draws of 1-16 tokens: 8e-3, as on
+# long rows), so a forward without gradients keeps the bf16 kernels.  0 keeps every length on the bf16 kernels.
+BF16_MIN_TOKENS = 80
 # BF16_STATE_GRAD: the backward of a bf16 call whose final state receives a gradient (sT in the loss, or passed on
 # to a later segment's backward) keeps the bf16 operands (True) or runs on the float32 kernels (False, the default:
 # the inputs upcast exactly, the states recomputed, dq, dk, dv cast back).  A final-state gradient of the size of the

@@ -190,7 +190,7 @@ def test_dropin_fp32_within_twice_the_torch_path(shape, s0):
 def test_dropin_bf16_small(shape, kernels):
     """bf16 drop-in end to end with a starting state and the final state used (reference test_harness.py:139-166),
     including one- to three-token rows at D = 128, where a chunk has a single valid row or two.  "default": rows
-    shorter than a chunk run on the float32 kernels (op.BF16_MIN_TOKENS), and the backward of the others, which gets
+    shorter than op.BF16_MIN_TOKENS run on the float32 kernels, and the backward of the others, which gets
     the final state's gradient, too (op.BF16_STATE_GRAD); "bf16": both switches keep every part on the bf16 kernels,
     whose one- to three-row chunks these draws hold to the bar too."""
     B, T, H, D = shape
@@ -202,7 +202,7 @@ def test_dropin_bf16_small(shape, kernels):
         if kernels == "bf16":
             op.BF16_MIN_TOKENS, op.BF16_STATE_GRAD = 0, True
         p = op.plan(B, T, H, D, D, True)
-        assert p["operands"] == ("f32" if kernels == "default" and T < 64 else "bf16")
+        assert p["operands"] == ("f32" if kernels == "default" and T < op.BF16_MIN_TOKENS else "bf16")
         assert p["state_grad_operands"] == ("f32" if kernels == "default" else "bf16")
         check_dropin(inp, bar=BF16_BAR, dsT=dsT)
     finally:
@@ -221,20 +221,23 @@ def test_dropin_fp16(shape):
     assert errs["o"] < 1e-3        # float32 arithmetic: only the float16 output's rounding remains
 
 
-@pytest.mark.parametrize("why", ["unnormalized", "short"])
+@pytest.mark.parametrize("why", ["unnormalized", "short", "one_chunk"])
 def test_bf16_calls_on_the_float32_kernels(why):
     """bf16 calls the bf16 operands do not serve run on the float32 kernels: keys the kernels do not normalise
     (use_qk_l2norm_in_kernel=False; raw N(0, 1) keys at DK = 32, 200 tokens, seed 501, a draw on which the bf16
-    operands' rounding model misses the bar twelvefold) and rows shorter than a chunk (two tokens, seed 50217: the
-    model's dg 5.7e-2; tests/test_host.py).  The output and every gradient are those of the same values given as
-    float32, cast back, bit for bit, and within 1e-2 of float64."""
+    operands' rounding model misses the bar twelvefold) and rows shorter than op.BF16_MIN_TOKENS (two tokens, seed
+    50217: the model's dg 5.7e-2; one chunk, seed 134086: 1.7e-2; tests/test_host.py).  The output and every gradient
+    are those of the same values given as float32, cast back, bit for bit, and within 1e-2 of float64."""
     _say(f"case bf16 on the float32 kernels: {why}")
     if why == "unnormalized":
         inp, l2 = gdr.make_inputs(2, 200, 1, 2, 32, 32, torch.bfloat16, s0=True, seed=501), False
         assert op.plan(2, 200, 2, 32, 32, True, l2norm=False)["operands"] == "f32"
-    else:
+    elif why == "short":
         inp, l2 = gdr.make_inputs(1, 2, 1, 1, 32, 32, torch.bfloat16, s0=False, seed=50217), True
         assert op.plan(1, 2, 1, 32, 32, True)["operands"] == "f32"
+    else:
+        inp, l2 = gdr.make_inputs(1, 64, 2, 2, 64, 128, torch.bfloat16, s0=False, seed=134086), True
+        assert op.plan(1, 64, 2, 64, 128, True)["operands"] == "f32"
     check_dropin(inp, bar=BF16_BAR, l2norm=l2)
     f32 = {n: (x.float() if x is not None and x.dtype == torch.bfloat16 else x) for n, x in inp.items()}
     o, sT, g = run_dropin(inp, l2norm=l2)

@@ -23,9 +23,11 @@ NAMES = ("dquery", "dkey", "dvalue", "dg", "dbeta", "dstate")
 
 @pytest.fixture(autouse=True)
 def _bf16_backward(monkeypatch):
-    """The backward with the final state's gradient stays on the bf16 kernels (op.BF16_STATE_GRAD), whose grouped-head
-    forms these tests pin (by default it runs the float32 kernels)."""
+    """The backward with the final state's gradient stays on the bf16 kernels (op.BF16_STATE_GRAD), and so do rows
+    shorter than op.BF16_MIN_TOKENS: these tests pin the bf16 kernels' grouped-head forms (by default such calls run
+    the float32 kernels)."""
     monkeypatch.setattr(op, "BF16_STATE_GRAD", True)
+    monkeypatch.setattr(op, "BF16_MIN_TOKENS", 0)
 
 
 def _say(*a):

@@ -24,7 +24,8 @@ OUTS = ("o", "sT", "dkey", "dvalue", "dg", "dbeta", "dstate")
 ])
 def test_kernels_follow_the_rounding_model(T, DK, DV, seed, s0scale, dseed, monkeypatch):
     print(f"case rounding model T={T} DK={DK} DV={DV} seed={seed} s0x{s0scale} dsT={dseed}", flush=True)
-    monkeypatch.setattr(op, "BF16_STATE_GRAD", True)
+    monkeypatch.setattr(op, "BF16_STATE_GRAD", True)      # the bf16 kernels throughout, as the model
+    monkeypatch.setattr(op, "BF16_MIN_TOKENS", 0)
     inp = gdr.make_inputs(1, T, 2, 2, DK, DV, torch.bfloat16, s0=True, seed=seed)
     inp["initial_state"] = inp["initial_state"] * s0scale
     dsT = None if dseed is None else torch.randn(1, 2, DK, DV, generator=torch.Generator().manual_seed(dseed))
