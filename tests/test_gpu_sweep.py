@@ -7,7 +7,8 @@ reference's, tests/test_harness.py:100-117), fp32 2e-4 (the reference harness's 
 The reference's own tests are fixed shapes; this draws the combinations between them, with the library's routing as
 it is (bf16 calls it sends to the float32 kernels included).  Earlier draws of this sweep found two of the cases it
 routes there (bf16 keys the kernels do not normalise, bf16 rows shorter than a chunk); the oracle's rounding model of
-the bf16 path, swept on the CPU, found the others (a final-state gradient, rows of about one chunk)."""
+the bf16 path, swept on the CPU, found the others (a final-state gradient, rows of about one chunk).  A second set of
+40 bf16 training calls covers 300-2,300 tokens (test_random_long_case_against_the_oracle)."""
 import random
 
 import pytest
@@ -74,3 +75,39 @@ def test_random_case_against_the_oracle(c):
         op.RECOMPUTE_STATES = old
     errs = {"o": gdr.rel(o, ro), "sT": gdr.rel(sT, rsT), **{n: gdr.rel(x, rg[n]) for n, x in g.items()}}
     _parity.check(errs, BARS[dt], recompute=c["rec"])
+
+
+def _long_cases(n=40, seed=7):
+    """bf16 training calls of 300-2,300 tokens (at most 40,000 token-heads), batch rows 1-4, 2-16 value heads over
+    1-16 key heads, key and value widths 64 or 128, a starting state and a final-state gradient on or off, both
+    backward modes, the generator's decay or a twentieth of it: the sizes where the persistent per-chunk backward
+    and the value splits change."""
+    rng = random.Random(seed)
+    out = []
+    for i in range(n):
+        B, T, H = rng.choice([1, 2, 4]), rng.choice([300, 513, 1000, 1024, 1500, 2300]), rng.choice([2, 4, 8, 16])
+        Hk = rng.choice([d for d in (1, 2, 4, 8, 16) if H % d == 0 and d <= H])
+        c = dict(i=i, B=B, T=T, H=H, Hk=Hk, D=rng.choice([64, 128, 128]), s0=rng.random() < 0.5,
+                 dsT=rng.random() < 0.3, rec=rng.random() < 0.7, gs=rng.choice([1.0, 1.0, 0.05]))
+        if B * T * H > 40000:
+            c["T"] = 40000 // (B * H)
+        out.append(c)
+    return out
+
+
+@pytest.mark.parametrize("c", _long_cases(), ids=lambda c: f"{c['i']}-B{c['B']}-T{c['T']}-H{c['H']}-Hk{c['Hk']}")
+def test_random_long_case_against_the_oracle(c):
+    print("case", c, flush=True)
+    B, T, H, Hk, D = c["B"], c["T"], c["H"], c["Hk"], c["D"]
+    inp = gdr.make_inputs(B, T, Hk, H, D, D, torch.bfloat16, s0=c["s0"], seed=500 + c["i"], dsT=c["dsT"])
+    inp["g"] = inp["g"] * c["gs"]
+    dsT = inp.get("dsT")
+    ro, rsT, rg = gdr.dropin_f64(*(inp[n] for n in NAMES), do=inp["do"], dsT=dsT)
+    old = op.RECOMPUTE_STATES
+    try:
+        op.RECOMPUTE_STATES = c["rec"]
+        o, sT, g = run_dropin(inp, grads=True, dsT=dsT)
+    finally:
+        op.RECOMPUTE_STATES = old
+    errs = {"o": gdr.rel(o, ro), "sT": gdr.rel(sT, rsT), **{n: gdr.rel(x, rg[n]) for n, x in g.items()}}
+    _parity.check(errs, BARS[torch.bfloat16], recompute=c["rec"])
