@@ -593,7 +593,8 @@ def make_step(cfg, dev, grouped=False, packed=None):
 
 def other_configs(step1, steps=20, warmup=3):
     """The default line's compact figures beside the headline: config 1's step on the float32 kernels
-    (op.BF16_OPERANDS = False, the reference's own precision), config 2's training step (q, k repeated by the step as
+    (op.BF16_OPERANDS = False, the reference's own precision) and with the forward keeping prep's operands for the
+    backward, which then recomputes only the chunk states (op.KEEP_PREP), config 2's training step (q, k repeated by the step as
     the model does, and grouped), config 3's forward at Hv 16 and 32 (inputs drawn on the device) and config 4's
     decode step, each timed the way its own --config line times it, with fewer steps."""
     from macai.gated_delta import op
@@ -609,6 +610,14 @@ def other_configs(step1, steps=20, warmup=3):
     B1, T1 = CONFIGS[1]["B"], CONFIGS[1]["T"]
     out["config1_f32_compute"] = {"ms_per_step": round(sec * 1e3, 4), "tokens_per_s": round(B1 * T1 / sec, 1),
                                   "kernels_us": {n: round(t * 1e6, 2) for n, t in in_step.items()}}
+    old = op.KEEP_PREP, op.RECOMPUTE_STATES
+    try:
+        op.KEEP_PREP, op.RECOMPUTE_STATES = True, True
+        sec, in_step = _time_step(step1, ns)
+    finally:
+        op.KEEP_PREP, op.RECOMPUTE_STATES = old
+    out["config1_kept_prep"] = {"ms_per_step": round(sec * 1e3, 4), "tokens_per_s": round(B1 * T1 / sec, 1),
+                                "kernels_us": {n: round(t * 1e6, 2) for n, t in in_step.items()}}
     for grouped in (False, True):
         step, c, _, _ = make_step(2, dev, grouped)
         sec, _ = _time_step(step, ns)

@@ -87,6 +87,12 @@ OVERLAP = True
 # q's (176 MiB a layer at B = 4, T = 1024, H = 16), in one allocation saved with save_for_backward (so saved-tensor
 # hooks, activation checkpointing and offload see it and it goes with the graph).
 RECOMPUTE_STATES = True
+# KEEP_PREP (no counterpart in the reference, whose switch has two settings): with RECOMPUTE_STATES, the training
+# forward also keeps prep's per-chunk operands with A (W, U, Ke, Qg, M, A, GL: 1,536 bytes per token-head at D = 128
+# in bf16, 96 MiB a layer at B = 4, T = 1024, H = 16, a little over half of what RECOMPUTE_STATES = False keeps), and
+# the backward skips its prep but still recomputes the chunk states beside its reverse pass (macai_gdr_state_pair).
+# Outputs and gradients have the same bits in every mode.  False (the default) is the reference's form.
+KEEP_PREP = False
 # SEQUENCE_SPLIT: segments a long row's forward without gradients runs side by side.  A state pass is a chain over
 # the row's chunks; with few head-rows (one long prefill) it fills few CUs and its length is the row's.  The pass is
 # affine in its starting state, so the row splits into segments: each segment's map [A | B] (macai_gdr_state_map,
@@ -354,8 +360,9 @@ def _forward_segments(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_s
 
 
 def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, pack=None, keep=False, save=True):
-    """prep, then the state pass with the output: returns (o in q's dtype, sT or None, and when keep -- for the
-    backward -- prep's operands with A and the chunk states Sc, Vn, else None).  A single long row whose forward saves
+    """prep, then the state pass with the output: returns (o in q's dtype, sT or None, and for the backward, when
+    keep, prep's operands with A and the chunk states Sc, Vn, or, when the forward saves and KEEP_PREP, prep's
+    operands with A alone; else None).  A single long row whose forward saves
     nothing for a backward may run as segments side by side (SEQUENCE_SPLIT)."""
     B, T, H, Hk, DK, DV, NT = _dims(q, v, pack)
     nseg = segments_for(B, T, H, DV, pack, save or keep)
@@ -364,7 +371,8 @@ def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, 
     Bc = q.shape[0]
     dev, dt = q.device, q.dtype
     code, stream = N.dtype_code(dt), N.stream_of(q)
-    r = _carve(dev, (Bc, H, NT, DK, DV, q.element_size(), True, keep, keep, False))
+    keep_prep = save and KEEP_PREP and not keep       # prep's operands with A, without the chunk states
+    r = _carve(dev, (Bc, H, NT, DK, DV, q.element_size(), True, keep or keep_prep, keep, False))
     _prep(q, k, v, g, beta, l2norm, q_scale, r, stream, pack, "prep_fwd")
     o = torch.empty(Bc, T, H, DV, device=dev, dtype=dt)
     sT = torch.empty(B, H, DK, DV, device=dev, dtype=torch.float32) if want_sT else None
@@ -373,12 +381,12 @@ def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, 
     _launch("state_fwd_out", "macai_gdr_state_fwd", r["W"], r["U"], r["Ke"], r["GL"], r["Qg"], r["M"], P(s0), P(o), P(sT),
             r["Sc"], r["Vn"], B, T, H, DK, DV, code, N.STORE_STATES if keep else 0, split, *_pack_args(pack), stream)
     CALLS[f"fwd s{split}"] += 1
-    return o, sT, (r if keep else None)
+    return o, sT, (r if keep or keep_prep else None)
 
 
 def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=None, r=None):
-    """Recompute (prep and the state pass storing S_c and Vn, unless the forward kept them in `r`), the reverse state
-    pass, the per-chunk backward.  Returns (dq, dk, dv in q's dtype; dg, dbeta, ds0 float32).  With grouped heads (Hk < H) the per-chunk backward writes dq,
+    """Recompute (prep, unless the forward kept its operands in `r`, and the state pass storing S_c and Vn, unless the
+    forward kept them too), the reverse state pass, the per-chunk backward.  Returns (dq, dk, dv in q's dtype; dg, dbeta, ds0 float32).  With grouped heads (Hk < H) the per-chunk backward writes dq,
     dk per value head and macai_gdr_group_sum folds each group (the backward of the repeat the grouped layout
     replaces)."""
     B, T, H, Hk, DK, DV, NT = _dims(q, v, pack)
@@ -387,16 +395,19 @@ def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=
     code, stream = N.dtype_code(dt), N.stream_of(q)
     f32 = torch.float32
     es = q.element_size()
-    kept = r is not None                 # the forward kept prep's operands and the chunk states: only the reverse
-    if kept:                             # pass is left
+    kept = r is not None and r["Sc"] is not None   # the forward kept prep's operands and the chunk states: only the
+    if kept:                                       # reverse pass is left
         g2 = _carve(dev, (Bc, H, NT, DK, DV, es, False, False, False, True))
+    elif r is not None:                            # it kept prep's operands (KEEP_PREP): no prep here
+        g2 = _carve(dev, (Bc, H, NT, DK, DV, es, False, False, True, True))
     else:
         r = g2 = _carve(dev, (Bc, H, NT, DK, DV, es, True, True, True, True))
         _prep(q, k, v, g, beta, l2norm, q_scale, r, stream, pack, "prep_bwd")
     P = N.ptr
     pk = _pack_args(pack)
     split = split_for(B * H, T, DV, 2 if OVERLAP and not kept else 1)
-    Sc, Vn, dSn, dVn = r["Sc"], r["Vn"], g2["dSn"], g2["dVn"]
+    st = r if kept else g2
+    Sc, Vn, dSn, dVn = st["Sc"], st["Vn"], g2["dSn"], g2["dVn"]
     ds0 = torch.empty(B, H, DK, DV, device=dev, dtype=f32)
     if kept:
         _launch("state_bwd", "macai_gdr_state_bwd", r["Ke"], r["Qg"], r["W"], r["M"], r["GL"], P(do), P(dsT), dSn, dVn,
@@ -441,8 +452,8 @@ def _backward_routed(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float
 
 
 def _save(ctx, inputs, r):
-    """Save the inputs and, when the forward kept its per-chunk scratch (RECOMPUTE_STATES False), that allocation
-    with them: save_for_backward hands both to saved-tensor hooks and frees them with the graph."""
+    """Save the inputs and, when the forward kept its per-chunk scratch (RECOMPUTE_STATES False, or KEEP_PREP), that
+    allocation with them: save_for_backward hands both to saved-tensor hooks and frees them with the graph."""
     ctx.save_for_backward(*inputs, None if r is None else r["buf"])
     ctx.kept_shape = None if r is None else r["shape"]
 
@@ -558,9 +569,9 @@ def plan(B: int, T: int, H: int, DK: int, DV: int, save: bool, Hk: int = None, d
     """What a drop-in call of these dimensions runs under the current settings (the reference's plan, op.py:105-113,
     for this build's kernels): the chunk length (64 for every pass), the operand type, the forward's segments, value
     split and state-pass kernel, and -- when the forward saves for a backward -- whether the backward recomputes
-    (RECOMPUTE_STATES), its state passes, their split, the per-chunk backward's kernel and the operands of a backward
-    that receives a gradient of the final state (BF16_STATE_GRAD).  cus: the device's compute
-    units (the persistent per-chunk backward runs where there are more chunk-heads than CUs); l2norm: the call's
+    (RECOMPUTE_STATES) and reruns prep (KEEP_PREP), its state passes, their split, the per-chunk backward's kernel and
+    the operands of a backward that receives a gradient of the final state (BF16_STATE_GRAD).  cus: the device's
+    compute units (the persistent per-chunk backward runs where there are more chunk-heads than CUs); l2norm: the call's
     use_qk_l2norm_in_kernel."""
     Hk = Hk or H
     cdt = compute_dtype(dtype, DK, DV, save, l2norm and FUSED_NORM, T)
@@ -581,6 +592,7 @@ def plan(B: int, T: int, H: int, DK: int, DV: int, save: bool, Hk: int = None, d
     if save:
         pair = recompute and OVERLAP
         out["bwd_state_passes"] = "pair" if pair else "recompute+reverse" if recompute else "reverse"
+        out["bwd_prep"] = "rerun" if recompute and not KEEP_PREP else "kept"
         out["bwd_split"] = split_for(B * H, T, DV, 2 if pair else 1)
         units = B * H * NT
         out["chunk_bwd"] = (("chunk_bwd8xn" if DK == DV and units > cus else "chunk_bwd8") if bf else "chunk_bwd")

@@ -584,21 +584,33 @@ def test_overlapped_passes_change_no_bits(split, bf16_state_grad):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_kept_prep_operands_change_no_bits(dtype, bf16_state_grad):
-    """The training forward keeping prep's operands (with A) for the backward (op.RECOMPUTE_STATES = False) or the
-    backward recomputing them (True, the reference's default, op.py:27-33): the same output and gradient bits
-    (the reference's claim for its switch, tests/test_memory.py)."""
+    """The training forward keeping prep's operands (with A) and the chunk states for the backward
+    (op.RECOMPUTE_STATES = False), only prep's operands (op.KEEP_PREP: the backward recomputes the states), or nothing
+    (the reference's default, op.py:27-33, the backward rerunning prep): the same output and gradient bits (the
+    reference's claim for its switch, tests/test_memory.py), and each mode runs the passes it should."""
     _say("case recompute bits", dtype)
     inp = gdr.make_inputs(2, 150, 2, 4, 128, 128, dtype, s0=True, seed=9)
-    old = op.RECOMPUTE_STATES
+    old = op.RECOMPUTE_STATES, op.KEEP_PREP
     try:
         outs = []
-        for mode in (True, False):
-            op.RECOMPUTE_STATES = mode
-            o, sT, grads = run_dropin(inp, dsT=torch.ones(2, 4, 128, 128))
+        for recompute, keep_prep, state_pass in ((True, False, "pair"), (False, False, "reverse"),
+                                                 (True, True, "pair")):
+            op.RECOMPUTE_STATES, op.KEEP_PREP = recompute, keep_prep
+            p = op.plan(2, 150, 4, 128, 128, True, Hk=2, dtype=dtype)
+            assert (p["bwd_state_passes"], p["bwd_prep"]) == (state_pass, "rerun" if recompute and not keep_prep
+                                                              else "kept"), p
+            events, op.EVENTS = op.EVENTS, []
+            try:
+                o, sT, grads = run_dropin(inp, dsT=torch.ones(2, 4, 128, 128))
+                ran = [name for name, _, _ in op.EVENTS]
+            finally:
+                op.EVENTS = events
+            assert ran.count("prep_bwd") == (1 if recompute and not keep_prep else 0), ran
+            assert ("state_pair" in ran) == (state_pass == "pair") and ("state_bwd" in ran) == (state_pass == "reverse")
             outs.append([o, sT] + [grads[n] for n in sorted(grads)])
     finally:
-        op.RECOMPUTE_STATES = old
-    assert all(torch.equal(a, b) for a, b in zip(*outs))
+        op.RECOMPUTE_STATES, op.KEEP_PREP = old
+    assert all(torch.equal(a, b) for other in outs[1:] for a, b in zip(outs[0], other))
 
 
 def test_unfused_prologue_switch():
@@ -679,26 +691,28 @@ def test_dropin_widths_bf16(DK, DV):
 def test_recompute_keeps_only_inputs():
     """What the training forward keeps for its backward (the reference's tests/test_memory.py:239-250): with
     op.RECOMPUTE_STATES (the default) exactly the six inputs, nothing a chunk; with it off, the inputs and one buffer
-    holding prep's operands with A and the chunk states (2,816 bytes a token-head at D = 128 in bf16)."""
+    holding prep's operands with A and the chunk states (2,816 bytes a token-head at D = 128 in bf16); with
+    op.KEEP_PREP, the inputs and prep's operands with A alone (1,536 bytes a token-head)."""
     _say("case saved tensors")
     B, T, H, D = 2, 650, 4, 128
     xs = [x.to(DEV).requires_grad_(True) for x in gdr.harness_inputs(B, T, H, D, D, seed=3)]
     xs = [x.to(torch.bfloat16 if i < 3 else torch.float32).detach().requires_grad_(True) for i, x in enumerate(xs)]
-    old = op.RECOMPUTE_STATES
+    NT = -(-T // 64)
+    old = op.RECOMPUTE_STATES, op.KEEP_PREP
     try:
         op.RECOMPUTE_STATES = True
         o, sT = GatedDeltaRule.apply(*xs, True)
         saved = [t for t in o.grad_fn.saved_tensors if t is not None]
         assert len(saved) == 6 and all(s.data_ptr() == x.data_ptr() for s, x in zip(saved, xs))
-        op.RECOMPUTE_STATES = False
-        o, sT = GatedDeltaRule.apply(*xs, True)
-        saved = [t for t in o.grad_fn.saved_tensors if t is not None]
-        assert len(saved) == 7 and all(s.data_ptr() == x.data_ptr() for s, x in zip(saved, xs))
-        NT = -(-T // 64)
-        per_token_head = saved[6].numel() / (B * H * NT * 64)
-        assert 2816 <= per_token_head < 2816 + 64, per_token_head      # plus the parts' 256-byte alignment
+        for recompute, keep_prep, size in ((False, False, 2816), (True, True, 1536)):
+            op.RECOMPUTE_STATES, op.KEEP_PREP = recompute, keep_prep
+            o, sT = GatedDeltaRule.apply(*xs, True)
+            saved = [t for t in o.grad_fn.saved_tensors if t is not None]
+            assert len(saved) == 7 and all(s.data_ptr() == x.data_ptr() for s, x in zip(saved, xs))
+            per_token_head = saved[6].numel() / (B * H * NT * 64)
+            assert size <= per_token_head < size + 64, per_token_head    # plus the parts' 256-byte alignment
     finally:
-        op.RECOMPUTE_STATES = old
+        op.RECOMPUTE_STATES, op.KEEP_PREP = old
 
 
 def test_strided_views_give_contiguous_bits():

@@ -328,13 +328,17 @@ def test_plan_reports_the_launch_choices():
     assert p["fwd_chunk"] == p["bwd_chunk"] == 64 and p["operands"] == "bf16" and p["prep"] == "prep8"
     assert (p["fwd_split"], p["fwd_state_pass"], p["segments"]) == (4, "state_out", 1)
     assert (p["recompute"], p["bwd_state_passes"], p["bwd_split"], p["chunk_bwd"]) == (True, "pair", 2, "chunk_bwd8xn")
-    old = op.RECOMPUTE_STATES
+    assert p["bwd_prep"] == "rerun"
+    old = op.RECOMPUTE_STATES, op.KEEP_PREP
     try:
         op.RECOMPUTE_STATES = False
         p = op.plan(4, 1024, 16, 128, 128, save=True)
-        assert (p["recompute"], p["bwd_state_passes"], p["bwd_split"]) == (False, "reverse", 4)
+        assert (p["recompute"], p["bwd_state_passes"], p["bwd_split"], p["bwd_prep"]) == (False, "reverse", 4, "kept")
+        op.RECOMPUTE_STATES, op.KEEP_PREP = True, True
+        p = op.plan(4, 1024, 16, 128, 128, save=True)
+        assert (p["recompute"], p["bwd_state_passes"], p["bwd_split"], p["bwd_prep"]) == (True, "pair", 2, "kept")
     finally:
-        op.RECOMPUTE_STATES = old
+        op.RECOMPUTE_STATES, op.KEEP_PREP = old
     p = op.plan(1, 32768, 16, 128, 128, save=False)
     assert p["segments"] == 8 and "bwd_state_passes" not in p and p["map_split"] >= 1
     assert op.plan(1, 32768, 16, 128, 128, save=True)["segments"] == 1     # a training forward never splits
