@@ -1655,18 +1655,23 @@ __device__ __forceinline__ Frag<MT> zero_frag() {
   return o;
 }
 
-// The fp32 per-chunk backward (bf16 operands take chunk_bwd8_kernel): one workgroup (4 waves) per (chunk, head, batch
-// row), fragments read straight from global memory (fp32 tiles do not fit LDS).  The prologue's row scales
-// (q^ = q rq DK^-1/2, k^ = k rk) are applied to the products' rows and columns, and folded into the stored dM and Z, so
-// the raw inputs are the MFMA operands.  Wave w owns key-column blocks w, w + 4, ... of the [C x DK] products, column
-// block w of the [C x C] ones and value-column blocks w, w + 4, ...
+// The fp32 per-chunk backward (bf16 operands take chunk_bwd8_kernel): one workgroup of NW = cb32_waves(DK) waves per
+// (chunk, head, batch row), fragments read straight from global memory (fp32 tiles do not fit LDS).  The prologue's
+// row scales (q^ = q rq DK^-1/2, k^ = k rk) are applied to the products' rows and columns, and folded into the stored
+// dM and Z, so the raw inputs are the MFMA operands.  Wave w owns key-column blocks w, w + NW, ... of the [C x DK]
+// products and value-column blocks w, w + NW, ..., and of the [C x C] ones column block w % 4, row tiles
+// TPW (w / 4) .. TPW (w / 4) + TPW - 1 (TPW = 16 / NW: all four with 4 waves, two with 8).  8 waves (two a SIMD) hide
+// each other's global-load latency; at key widths above 128 the fp32 tiles leave LDS for 4 only.
+constexpr int cb32_waves(int DK) { return DK <= 128 ? 8 : 4; }
 template <typename MT, int DK, int DVT>
-__global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
+__global__ void __launch_bounds__(64 * cb32_waves(DK)) chunk_bwd_kernel(ChunkBwdArgs a) {
   static_assert(sizeof(MT) == 4, "bf16 operands take chunk_bwd8_kernel");
   const int DV = DVT ? DVT : a.DV;        // DVT = 0: the value width at run time (a multiple of 32)
   constexpr int KP = DK + 8, CP = C + 8;
+  constexpr int NW = cb32_waves(DK);
+  constexpr int RH = NW / 4, TPW = 4 / RH;   // row groups of the C x C tiles, row tiles a wave owns there
   constexpr int NBD = DK / 16;            // 16-column blocks of the key width
-  constexpr int NBW = (NBD + 3) / 4;      // most blocks a wave owns
+  constexpr int NBW = (NBD + NW - 1) / NW;   // most blocks a wave owns
   __shared__ __attribute__((aligned(16))) MT sdW[C * KP];   // dW = -dVn S_c^T
   __shared__ __attribute__((aligned(16))) MT sdMk[C * CP];  // dM diag(rk):            [t][s] = dM[t][s] rk_s
   __shared__ __attribute__((aligned(16))) MT sdMq[C * CP];  // dM^T diag(rq DK^-1/2):  [t][s] = dM[s][t] rq_s qs
@@ -1674,9 +1679,9 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
   __shared__ __attribute__((aligned(16))) MT sdA[C * CP];   // dA
   __shared__ ChunkScalars cs;
   __shared__ float rk[C], rq[C];
-  __shared__ float part[NPART][4][C];
-  __shared__ float partS[4];
-  __shared__ float colR1[C], colR2b[C];
+  __shared__ float part[NPART][NW][C];
+  __shared__ float partS[NW];
+  __shared__ float colR1[RH][C], colR2b[RH][C];
 
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int H = a.H, NT = a.NT;
@@ -1702,8 +1707,13 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
 
   if (w == 0) chunk_scalars(cs, a.g, a.beta, s_base, H, t0, T);
   if (a.l2norm) {
-    row_rnorms<MT, DK>(rk, (const MT*)a.k, qk_base, qk_pitch, t0, T, 4);
-    row_rnorms<MT, DK>(rq, (const MT*)a.q, qk_base, qk_pitch, t0, T, 4);
+    if constexpr (NW == 8) {               // k's norms on waves 0-3, q's on 4-7 (the same sums as on one wave set)
+      if (w < 4) row_rnorms<MT, DK>(rk, (const MT*)a.k, qk_base, qk_pitch, t0, T, 4, w);
+      else row_rnorms<MT, DK>(rq, (const MT*)a.q, qk_base, qk_pitch, t0, T, 4, w - 4);
+    } else {
+      row_rnorms<MT, DK>(rk, (const MT*)a.k, qk_base, qk_pitch, t0, T, 4);
+      row_rnorms<MT, DK>(rq, (const MT*)a.q, qk_base, qk_pitch, t0, T, 4);
+    }
   } else if (threadIdx.x < C) {
     rk[threadIdx.x] = (int)threadIdx.x < nrows ? 1.f : 0.f;
     rq[threadIdx.x] = (int)threadIdx.x < nrows ? 1.f : 0.f;
@@ -1729,7 +1739,7 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
     return (t0 + row < T) ? to_f(k[(size_t)(t0 + row) * qk_pitch + d]) * rk[row] : 0.f;
   };
 
-  // ---- B: products with the chunk states; wave w owns key-column blocks w, w + 4, ...
+  // ---- B: products with the chunk states; wave w owns key-column blocks w, w + NW, ...
   f4 dQ[NBW][4], dK[NBW][4];
   float pQD[4][4], pE[4][4], pKX[4][4];
 #pragma unroll
@@ -1739,7 +1749,7 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
   float sds = 0.f;
 #pragma unroll
   for (int ib = 0; ib < NBW; ++ib) {
-    const int nb = w + 4 * ib;
+    const int nb = w + NW * ib;
     if (nb >= NBD) break;
     const int d0 = 16 * nb, d = d0 + (l & 15);
     f4 aO[4], aV[4], aD[4];
@@ -1816,79 +1826,81 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
   if (l == 0) partS[w] = sds;
   __syncthreads();
 
-  // ---- C: the C x C products; wave w owns column block cb = w of every C x C matrix
-  const int cb = w, s = 16 * cb + (l & 15);
-  f4 QK[4], KK[4], dOV[4], Ta[4], Tb[4];
+  // ---- C: the C x C products; wave w owns column block cb = w % 4, row tiles mi = TPW hh + i (hh = w / 4)
+  const int cb = w & 3, hh = w >> 2, s = 16 * cb + (l & 15);
+  f4 QK[TPW], KK[TPW], dOV[TPW], Ta[TPW], Tb[TPW];
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi) QK[mi] = KK[mi] = dOV[mi] = Ta[mi] = Tb[mi] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < TPW; ++i) QK[i] = KK[i] = dOV[i] = Ta[i] = Tb[i] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int p = 0; p < DK / 32; ++p) {
     const Frag<MT> bk = fk(16 * cb, 32 * p);
-    Frag<MT> fa[4], fb[4], fw[4];
+    Frag<MT> fa[TPW], fb[TPW], fw[TPW];
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-      fa[mi] = fq(16 * mi, 32 * p);
-      fb[mi] = fk(16 * mi, 32 * p);
-      fw[mi] = frag_k_raw(sdW, KP, 16 * mi, 32 * p);
+    for (int i = 0; i < TPW; ++i) {
+      const int mi = TPW * hh + i;
+      fa[i] = fq(16 * mi, 32 * p);
+      fb[i] = fk(16 * mi, 32 * p);
+      fw[i] = frag_k_raw(sdW, KP, 16 * mi, 32 * p);
     }
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-      mma(QK[mi], fa[mi], bk);
-      mma(KK[mi], fb[mi], bk);
-      mma(Ta[mi], fw[mi], bk);
+    for (int i = 0; i < TPW; ++i) {
+      mma(QK[i], fa[i], bk);
+      mma(KK[i], fb[i], bk);
+      mma(Ta[i], fw[i], bk);
     }
   }
 #pragma unroll
   for (int kb = 0; kb < DV / 32; ++kb) {
     const Frag<MT> bvn = fVn(16 * cb, 32 * kb);
     const Frag<MT> bv = frag_k_seq<MT, MT>(v, v_pitch, t0, T, 16 * cb, 32 * kb, One());
-    Frag<MT> fo[4], fd[4];
+    Frag<MT> fo[TPW], fd[TPW];
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-      fo[mi] = fO(16 * mi, 32 * kb);
-      fd[mi] = fdVn(16 * mi, 32 * kb);
+    for (int i = 0; i < TPW; ++i) {
+      const int mi = TPW * hh + i;
+      fo[i] = fO(16 * mi, 32 * kb);
+      fd[i] = fdVn(16 * mi, 32 * kb);
     }
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-      mma(dOV[mi], fo[mi], bvn);
-      mma(Tb[mi], fd[mi], bv);
+    for (int i = 0; i < TPW; ++i) {
+      mma(dOV[i], fo[i], bvn);
+      mma(Tb[i], fd[i], bv);
     }
   }
-  float gm[4][4], KG[4][4];
+  float gm[TPW][4], KG[TPW][4];
   {
     float cR1 = 0.f;
-    float pR1[4][4];
-    const float bs = cs.beta[s], bgs = cs.beta[s] * cs.gam[s], rks = rk[s], rqs = rq[s] * qs;
+    float pR1[TPW][4];
+    const float bs = cs.beta[s], bgs = cs.beta[s] * cs.gam[s], rks = rk[s];
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+    for (int i = 0; i < TPW; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = 16 * mi + 4 * j + r;
-        gm[mi][r] = (row >= s) ? cs.decay(row, s) : 0.f;
-        const float Mv = QK[mi][r] * (rq[row] * qs * rks) * gm[mi][r];
-        const float dMv = dOV[mi][r] * gm[mi][r];
+        const int row = 16 * (TPW * hh + i) + 4 * j + r;
+        gm[i][r] = (row >= s) ? cs.decay(row, s) : 0.f;
+        const float Mv = QK[i][r] * (rq[row] * qs * rks) * gm[i][r];
+        const float dMv = dOV[i][r] * gm[i][r];
         sdMk[row * CP + s] = from_f<MT>(dMv * rks);
         sdMq[s * CP + row] = from_f<MT>(dMv * (rq[row] * qs));
-        const float r1 = (row > s) ? dOV[mi][r] * Mv : 0.f;
-        pR1[mi][r] = r1;
+        const float r1 = (row > s) ? dOV[i][r] * Mv : 0.f;
+        pR1[i][r] = r1;
         cR1 += r1;
-        sdA[row * CP + s] = from_f<MT>((row > s) ? fmaf(Ta[mi][r] * rks, bgs, Tb[mi][r] * bs) : 0.f);
-        KG[mi][r] = (row > s) ? KK[mi][r] * (rk[row] * rks) * gm[mi][r] : 0.f;
+        sdA[row * CP + s] = from_f<MT>((row > s) ? fmaf(Ta[i][r] * rks, bgs, Tb[i][r] * bs) : 0.f);
+        KG[i][r] = (row > s) ? KK[i][r] * (rk[row] * rks) * gm[i][r] : 0.f;
       }
-    (void)rqs;
     cR1 = across_groups_sum(cR1);
-    if (j == 0) colR1[s] = cR1;
+    if (j == 0) colR1[hh][s] = cR1;
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+    for (int i = 0; i < TPW; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float t = group16_sum(pR1[mi][r]);
-        if ((l & 15) == 0) part[P_R1][w][16 * mi + 4 * j + r] = t;
+        const float t = group16_sum(pR1[i][r]);
+        if ((l & 15) == 0) part[P_R1][w][16 * (TPW * hh + i) + 4 * j + r] = t;
       }
   }
   __syncthreads();
-  // T1 = dA A^T (column block cb of T1), then dL = strictLower(-A^T T1)
-  f4 T1[4], dL[4];
+  // T1 = dA A^T (column block cb of T1, all four row tiles: each wave of the column block forms it), then dL =
+  // strictLower(-A^T T1) on this wave's row tiles
+  f4 T1[4], dL[TPW];
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi) {
     T1[mi] = f4{0.f, 0.f, 0.f, 0.f};
@@ -1901,27 +1913,28 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
 #pragma unroll
   for (int p = 0; p < 2; ++p) T1f[p] = frag_acc<MT>(T1[2 * p], T1[2 * p + 1]);
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi) {
+  for (int i = 0; i < TPW; ++i) {
+    const int mi = TPW * hh + i;
     f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int p = 0; p < 2; ++p)
       if (32 * p + 31 >= 16 * mi) mma(acc, fAt(16 * mi, 32 * p), T1f[p]);
-    dL[mi] = acc;
+    dL[i] = acc;
   }
   {
     float cR2 = 0.f;
-    float pR2[4][4];
+    float pR2[TPW][4];
     const float rks = rk[s];
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+    for (int i = 0; i < TPW; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = 16 * mi + 4 * j + r;
-        const float dl = (row > s) ? -dL[mi][r] : 0.f;
-        const float r2 = dl * KG[mi][r];
-        pR2[mi][r] = r2;
+        const int row = 16 * (TPW * hh + i) + 4 * j + r;
+        const float dl = (row > s) ? -dL[i][r] : 0.f;
+        const float r2 = dl * KG[i][r];
+        pR2[i][r] = r2;
         cR2 = fmaf(cs.beta[row], r2, cR2);
-        const float z = cs.beta[row] * dl * gm[mi][r];    // Z[row][s] = Z[s][row] = beta_row P[row][s]
+        const float z = cs.beta[row] * dl * gm[i][r];    // Z[row][s] = Z[s][row] = beta_row P[row][s]
         if (row > s) {
           sZk[row * CP + s] = from_f<MT>(z * rks);
           sZk[s * CP + row] = from_f<MT>(z * rk[row]);
@@ -1930,13 +1943,13 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
         }
       }
     cR2 = across_groups_sum(cR2);
-    if (j == 0) colR2b[s] = cR2;
+    if (j == 0) colR2b[hh][s] = cR2;
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+    for (int i = 0; i < TPW; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float t = group16_sum(pR2[mi][r]);
-        if ((l & 15) == 0) part[P_R2][w][16 * mi + 4 * j + r] = t;
+        const float t = group16_sum(pR2[i][r]);
+        if ((l & 15) == 0) part[P_R2][w][16 * (TPW * hh + i) + 4 * j + r] = t;
       }
   }
   __syncthreads();
@@ -1949,7 +1962,7 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
     for (int r = 0; r < 4; ++r) pDQ[mi][r] = pDK[mi][r] = 0.f;
 #pragma unroll
   for (int ib = 0; ib < NBW; ++ib) {
-    const int nb = w + 4 * ib;
+    const int nb = w + NW * ib;
     if (nb >= NBD) break;
     const int d = 16 * nb + (l & 15);
 #pragma unroll
@@ -1992,14 +2005,14 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
       }
     }
 
-  // ---- E: Y = A^T dVn, dV = diag(beta) Y; v . Y row sums  (value-column blocks w, w + 4, ...)
+  // ---- E: Y = A^T dVn, dV = diag(beta) Y; v . Y row sums  (value-column blocks w, w + NW, ...)
   {
     float pVY[4][4];
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
       for (int r = 0; r < 4; ++r) pVY[mi][r] = 0.f;
-    for (int vb = w; vb < DV / 16; vb += 4) {
+    for (int vb = w; vb < DV / 16; vb += NW) {
       const int vc = 16 * vb + (l & 15);
       Frag<MT> bdv[2];
 #pragma unroll
@@ -2033,12 +2046,30 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
   // ---- F: dbeta and dg (wave 0, lane = chunk row), fixed-order sums of the per-wave partials
   if (w == 0) {
     const int r = l, t = t0 + r;
-    auto sum4 = [&](int pi) { return ((part[pi][0][r] + part[pi][1][r]) + part[pi][2][r]) + part[pi][3][r]; };
-    const float kx = sum4(P_KX), qd = sum4(P_QD), E = sum4(P_E), r1 = sum4(P_R1), r2 = sum4(P_R2), vy = sum4(P_VY);
+    auto sumw = [&](int pi) {              // over every wave, in wave order
+      float x = part[pi][0][r];
+#pragma unroll
+      for (int u = 1; u < NW; ++u) x += part[pi][u][r];
+      return x;
+    };
+    const int g0 = 4 * ((r >> 4) / TPW);   // the four waves whose C x C row tiles hold row r
+    auto sumc = [&](int pi) { return ((part[pi][g0][r] + part[pi][g0 + 1][r]) + part[pi][g0 + 2][r]) + part[pi][g0 + 3][r]; };
+    float cr1 = colR1[0][r], cr2 = colR2b[0][r];
+#pragma unroll
+    for (int u = 1; u < RH; ++u) {
+      cr1 += colR1[u][r];
+      cr2 += colR2b[u][r];
+    }
+    const float kx = sumw(P_KX), qd = sumw(P_QD), E = sumw(P_E), r1 = sumc(P_R1), r2 = sumc(P_R2), vy = sumw(P_VY);
     const float gmr = cs.gam[r], bt = cs.beta[r];
     const float db = fmaf(gmr, kx, vy) + r2;
-    float dG = qd + bt * gmr * kx + (r1 - colR1[r]) + (bt * r2 - colR2b[r]);
-    if (r == C - 1) dG += cs.gam[C - 1] * (((partS[0] + partS[1]) + partS[2]) + partS[3]);
+    float dG = qd + bt * gmr * kx + (r1 - cr1) + (bt * r2 - cr2);
+    if (r == C - 1) {
+      float ss = partS[0];
+#pragma unroll
+      for (int u = 1; u < NW; ++u) ss += partS[u];
+      dG += cs.gam[C - 1] * ss;
+    }
     // dg_t = sum_{s >= t} dG_s + sum_{r < t} E_r; the exclusive prefix by a shift, not incl - E: E on the last valid
     // row is O(1) while the earlier ones carry exp(G_last - G_r) and can be ~1e-9 of it
     const float rev = __shfl(dG, C - 1 - r, 64);
@@ -2055,7 +2086,7 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
   // ---- G: the prologue's backward, dq and dk out (own key-column blocks)
 #pragma unroll
   for (int ib = 0; ib < NBW; ++ib) {
-    const int nb = w + 4 * ib;
+    const int nb = w + NW * ib;
     if (nb >= NBD) break;
     const int d = 16 * nb + (l & 15);
 #pragma unroll
@@ -2066,8 +2097,12 @@ __global__ void __launch_bounds__(256) chunk_bwd_kernel(ChunkBwdArgs a) {
         if (t >= T) continue;
         float gq = dQ[ib][mi][r], gk = dK[ib][mi][r];
         if (a.l2norm) {
-          const float dq_dot = ((part[P_DQ][0][row] + part[P_DQ][1][row]) + part[P_DQ][2][row]) + part[P_DQ][3][row];
-          const float dk_dot = ((part[P_DK][0][row] + part[P_DK][1][row]) + part[P_DK][2][row]) + part[P_DK][3][row];
+          float dq_dot = part[P_DQ][0][row], dk_dot = part[P_DK][0][row];
+#pragma unroll
+          for (int u = 1; u < NW; ++u) {
+            dq_dot += part[P_DQ][u][row];
+            dk_dot += part[P_DK][u][row];
+          }
           gq = qs * rq[row] * fmaf(-xq(row, d), dq_dot, gq);
           gk = rk[row] * fmaf(-xk(row, d), dk_dot, gk);
         } else {
@@ -3331,13 +3366,13 @@ int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float
 // other width pair takes it at run time, DV = 0 below)
 #define LAUNCH_CB(MT)                                                                                               \
   DISPATCH_DK_F32(DK, if constexpr (DKC != 32 && DKC != 64 && DKC != 128 && DKC != 256) {                             \
-    hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 0>), grid, dim3(256), 0, st, a);                                     \
+    hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 0>), grid, dim3(64 * cb32_waves(DKC)), 0, st, a);                 \
   } else switch (DV) {                                                                                                 \
-    case 32: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 32>), grid, dim3(256), 0, st, a); break;                \
-    case 64: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 64>), grid, dim3(256), 0, st, a); break;                \
-    case 96: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 96>), grid, dim3(256), 0, st, a); break;                \
-    case 128: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 128>), grid, dim3(256), 0, st, a); break;              \
-    default: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 0>), grid, dim3(256), 0, st, a); break;                 \
+    case 32: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 32>), grid, dim3(64 * cb32_waves(DKC)), 0, st, a); break; \
+    case 64: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 64>), grid, dim3(64 * cb32_waves(DKC)), 0, st, a); break; \
+    case 96: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 96>), grid, dim3(64 * cb32_waves(DKC)), 0, st, a); break; \
+    case 128: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 128>), grid, dim3(64 * cb32_waves(DKC)), 0, st, a); break; \
+    default: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 0>), grid, dim3(64 * cb32_waves(DKC)), 0, st, a); break; \
   })
   if (dtype == MACAI_GDR_F32) {
     LAUNCH_CB(float);
