@@ -158,8 +158,10 @@ __device__ __forceinline__ Frag<MT> cvt(const Frag<float>& x, float s = 1.0f) {
 // ---------------------------------------------------------------------------------------------------------------------
 // prep: G, L, A = (I + L)^-1, W, U, M per chunk
 // ---------------------------------------------------------------------------------------------------------------------
+// 8 waves (two a SIMD, hiding each other's latencies): wave w owns row block w % 4 of the 16 x 16 tiles and every
+// other column block of it from w / 4 on.
 template <typename IT, typename MT, int DK>
-__global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
+__global__ void __launch_bounds__(512) prep_kernel(PrepArgs a) {
   // Key features are staged DKS at a time, so the tiles fit LDS at every key width: the products over the key features
   // accumulate across the passes, and W is formed a pass of columns at a time.  float32 tiles of up to 192 columns
   // fit in one pass (256: two of 128; 224: seven of 32).
@@ -191,10 +193,11 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
   const IT* k = (const IT*)a.k + qk_base;
   const IT* v = (const IT*)a.v + v_base;
 
+  const int rb = w & 3, half = w >> 2;       // row block; which column blocks (every other one from half)
   if (w == 0) chunk_scalars(cs, a.g, a.beta, s_base, H, t0, T);
-  if (a.l2norm) {
-    row_rnorms<IT, DK>(rk, (const IT*)a.k, qk_base, qk_pitch, t0, T, 4);
-    row_rnorms<IT, DK>(rq, (const IT*)a.q, qk_base, qk_pitch, t0, T, 4);
+  if (a.l2norm) {                          // k's norms on waves 0-3, q's on 4-7
+    if (w < 4) row_rnorms<IT, DK>(rk, (const IT*)a.k, qk_base, qk_pitch, t0, T, 4, w);
+    else row_rnorms<IT, DK>(rq, (const IT*)a.q, qk_base, qk_pitch, t0, T, 4, w - 4);
   } else if (threadIdx.x < C) {
     rk[threadIdx.x] = 1.f;
     rq[threadIdx.x] = 1.f;
@@ -203,7 +206,8 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
   if (threadIdx.x == 0) a.GL[bhc] = cs.gam[C - 1];
   const float qs = a.q_scale;
 
-  // K K^T and Q K^T on the lower 16 x 16 tiles (wave w owns row block w), accumulated over the passes of key columns.
+  // K K^T and Q K^T on the lower 16 x 16 tiles (wave w: row block rb, column blocks half, half + 2), accumulated over
+  // the passes of key columns.
   // Each pass stages K^ and Q^ rows of its columns into LDS and writes diag(e) K^ and diag(gamma) Q^ out.
   f4 kk[4], qk[4];
 #pragma unroll
@@ -241,10 +245,10 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
       store8(Qg + r * DK + c8, x);
     }
     __syncthreads();
-    const int mi = w;
+    const int mi = rb;
 #pragma unroll
     for (int ni = 0; ni < 4; ++ni) {
-      if (ni <= mi) {
+      if (ni <= mi && (ni & 1) == half) {
 #pragma unroll
         for (int p = 0; p < DKS / 32; ++p) {
           Frag<MT> bk = frag_k_raw(sK, KP, 16 * ni, 32 * p);
@@ -257,9 +261,10 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
   }
   // L (strictly lower, fp32) into LDS; M out
   {
-    const int mi = w;
+    const int mi = rb;
 #pragma unroll
     for (int ni = 0; ni < 4; ++ni) {
+      if ((ni & 1) != half) continue;
       const int col = 16 * ni + (l & 15);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -329,12 +334,13 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
     __syncthreads();
   }
 
-  // W = A (beta gamma K^): wave w owns row block w; A is lower triangular, so k-blocks above the row block are zero
+  // W = A (beta gamma K^): wave w owns row block rb, column blocks half, half + 2, ...; A is lower triangular, so
+  // k-blocks above the row block are zero
   {
     Frag<MT> af[2];
 #pragma unroll
-    for (int p = 0; p < 2; ++p) af[p] = cvt<MT>(frag_k_f32(sA, FP, 16 * w, 32 * p));
-    const int np = (16 * w + 15) / 32 + 1;
+    for (int p = 0; p < 2; ++p) af[p] = cvt<MT>(frag_k_f32(sA, FP, 16 * rb, 32 * p));
+    const int np = (16 * rb + 15) / 32 + 1;
     MT* Wc = (MT*)a.W + bhc * C * DK;
     for (int ps = 0; ps < NPASS; ++ps) {
       if (ps) {                            // the next pass of columns of (beta gamma K^)^T
@@ -342,11 +348,11 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
         stage_kT(ps * DKS);
         __syncthreads();
       }
-      for (int ni = 0; ni < DKS / 16; ++ni) {
+      for (int ni = half; ni < DKS / 16; ni += 2) {
         f4 acc = {0.f, 0.f, 0.f, 0.f};
         for (int p = 0; p < np; ++p) mma(acc, af[p], frag_k_raw(sQ, CP, 16 * ni, 32 * p));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) Wc[(16 * w + 4 * j + r) * DK + ps * DKS + 16 * ni + (l & 15)] = from_f<MT>(acc[r]);
+        for (int r = 0; r < 4; ++r) Wc[(16 * rb + 4 * j + r) * DK + ps * DKS + 16 * ni + (l & 15)] = from_f<MT>(acc[r]);
       }
     }
     // U = A (beta V), 64 value columns at a time staged transposed in sK
@@ -356,11 +362,11 @@ __global__ void __launch_bounds__(256) prep_kernel(PrepArgs a) {
       __syncthreads();
       stage_rows_T<MT, IT>(sK, CP, v + vb, v_pitch, t0, T, nv, [&](int r) { return cs.beta[r]; });
       __syncthreads();
-      for (int ni = 0; ni < nv / 16; ++ni) {
+      for (int ni = half; ni < nv / 16; ni += 2) {
         f4 acc = {0.f, 0.f, 0.f, 0.f};
         for (int p = 0; p < np; ++p) mma(acc, af[p], frag_k_raw(sK, CP, 16 * ni, 32 * p));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) Uc[(16 * w + 4 * j + r) * DV + vb + 16 * ni + (l & 15)] = acc[r];
+        for (int r = 0; r < 4; ++r) Uc[(16 * rb + 4 * j + r) * DV + vb + 16 * ni + (l & 15)] = acc[r];
       }
     }
   }
@@ -3122,7 +3128,7 @@ int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, 
   }
   hipStream_t st = (hipStream_t)stream;
   if (dtype == MACAI_GDR_F32) {
-    DISPATCH_DK_F32(DK, hipLaunchKernelGGL((prep_kernel<float, float, DKC>), grid, dim3(256), 0, st, a));
+    DISPATCH_DK_F32(DK, hipLaunchKernelGGL((prep_kernel<float, float, DKC>), grid, dim3(512), 0, st, a));
   } else if (DV <= 128 || DV % 128 == 0) {
     DISPATCH_DK(DK, switch (DV) {
       case 32: hipLaunchKernelGGL((prep8_kernel<DKC, 32>), grid, dim3(512), 0, st, a); break;
@@ -3131,7 +3137,7 @@ int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, 
       default: hipLaunchKernelGGL((prep8_kernel<DKC, 128>), grid, dim3(512), 0, st, a); break;
     })
   } else {
-    DISPATCH_DK(DK, hipLaunchKernelGGL((prep_kernel<bf16, bf16, DKC>), grid, dim3(256), 0, st, a));
+    DISPATCH_DK(DK, hipLaunchKernelGGL((prep_kernel<bf16, bf16, DKC>), grid, dim3(512), 0, st, a));
   }
   return launched(what);
 }
