@@ -778,7 +778,7 @@ def main():
                                                                      "chunks_per_head": chunks},
                        "initial_state": c["s0"], "value_split": split,
                        "pair_split": None if keep else op.split_for(rows, T, DV, 2),
-                       "overlapped_state_passes": (not keep) and op.OVERLAP, "recompute_prep_in_backward": not keep},
+                       "overlapped_state_passes": (not keep) and op.pairs_states(torch.bfloat16), "recompute_prep_in_backward": not keep},
             "roofline": roof, "kernels": kernels,
             "stored_states" if not keep else "recompute_states": other}
     if args.config == 1 and not (args.no_configs or args.packed or args.grouped or args.stored):

@@ -75,8 +75,16 @@ CALLS = collections.Counter()
 EVENTS = None
 # The backward's recompute pass (storing S_c, Vn) and its reverse pass need only prep's outputs, not each other: with
 # OVERLAP they run in one launch (macai_gdr_state_pair), each on about half the CUs.  Both are sequential chunk chains
-# whose speed hardly depends on how many CUs they get, so this nearly hides one of them.
-OVERLAP = True
+# whose speed hardly depends on how many CUs they get, so this nearly hides one of them -- with 2-byte operands.  On
+# float32 operands the pair is the slower choice (config 1: 311 us for the pair against 97 + 182 us as two launches,
+# the step 1.162 against 1.125 ms), so "auto" (the default) pairs the passes for bf16 and fp16 operands only; True
+# pairs them always, False never.  Same bits every way.
+OVERLAP = "auto"
+
+
+def pairs_states(dtype) -> bool:
+    """Whether the recompute backward runs its two state passes as one launch for operands of this dtype."""
+    return OVERLAP is True or (OVERLAP == "auto" and dtype != torch.float32)
 # RECOMPUTE_STATES (the reference's switch and default, op.py:27-33; outputs and gradients have the same bits either
 # way):
 # True (the default) -- the training forward keeps only its inputs; the backward reruns prep (with A) and recomputes
@@ -405,14 +413,15 @@ def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=
         _prep(q, k, v, g, beta, l2norm, q_scale, r, stream, pack, "prep_bwd")
     P = N.ptr
     pk = _pack_args(pack)
-    split = split_for(B * H, T, DV, 2 if OVERLAP and not kept else 1)
+    pair = pairs_states(dt) and not kept
+    split = split_for(B * H, T, DV, 2 if pair else 1)
     st = r if kept else g2
     Sc, Vn, dSn, dVn = st["Sc"], st["Vn"], g2["dSn"], g2["dVn"]
     ds0 = torch.empty(B, H, DK, DV, device=dev, dtype=f32)
     if kept:
         _launch("state_bwd", "macai_gdr_state_bwd", r["Ke"], r["Qg"], r["W"], r["M"], r["GL"], P(do), P(dsT), dSn, dVn,
                 P(ds0), B, T, H, DK, DV, code, split, *pk, stream)
-    elif OVERLAP:
+    elif pair:
         _launch("state_pair", "macai_gdr_state_pair", r["W"], r["U"], r["Ke"], r["Qg"], r["M"], r["GL"], P(s0), P(do),
                 P(dsT), Sc, Vn, dSn, dVn, P(ds0), B, T, H, DK, DV, code, split, *pk, stream)
     else:
@@ -420,7 +429,7 @@ def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=
                 None, Sc, Vn, B, T, H, DK, DV, code, N.STORE_STATES | N.NO_OUTPUT, split, *pk, stream)
         _launch("state_bwd", "macai_gdr_state_bwd", r["Ke"], r["Qg"], r["W"], r["M"], r["GL"], P(do), P(dsT), dSn, dVn,
                 P(ds0), B, T, H, DK, DV, code, split, *pk, stream)
-    CALLS[f"bwd {'reverse' if kept else 'pair' if OVERLAP else 'recompute+reverse'} s{split}"] += 1
+    CALLS[f"bwd {'reverse' if kept else 'pair' if pair else 'recompute+reverse'} s{split}"] += 1
     if Hk == H:
         dqh, dkh = torch.empty_like(q), torch.empty_like(k)
     else:
@@ -590,7 +599,7 @@ def plan(B: int, T: int, H: int, DK: int, DV: int, save: bool, Hk: int = None, d
     waves = DV // 16 // out["fwd_split"]
     out["fwd_state_pass"] = "state_out" if bf and waves <= 2 else "state_fwd"
     if save:
-        pair = recompute and OVERLAP
+        pair = recompute and pairs_states(cdt)
         out["bwd_state_passes"] = "pair" if pair else "recompute+reverse" if recompute else "reverse"
         out["bwd_prep"] = "rerun" if recompute and not KEEP_PREP else "kept"
         out["bwd_split"] = split_for(B * H, T, DV, 2 if pair else 1)

@@ -587,14 +587,15 @@ def test_kept_prep_operands_change_no_bits(dtype, bf16_state_grad):
     """The training forward keeping prep's operands (with A) and the chunk states for the backward
     (op.RECOMPUTE_STATES = False), only prep's operands (op.KEEP_PREP: the backward recomputes the states), or nothing
     (the reference's default, op.py:27-33, the backward rerunning prep): the same output and gradient bits (the
-    reference's claim for its switch, tests/test_memory.py), and each mode runs the passes it should."""
+    reference's claim for its switch, tests/test_memory.py), and each mode runs the passes it should (the recompute
+    modes pair their two state passes in one launch for bf16 operands, two launches for float32, op.OVERLAP)."""
     _say("case recompute bits", dtype)
     inp = gdr.make_inputs(2, 150, 2, 4, 128, 128, dtype, s0=True, seed=9)
     old = op.RECOMPUTE_STATES, op.KEEP_PREP
+    both = "pair" if dtype == torch.bfloat16 else "recompute+reverse"
     try:
         outs = []
-        for recompute, keep_prep, state_pass in ((True, False, "pair"), (False, False, "reverse"),
-                                                 (True, True, "pair")):
+        for recompute, keep_prep, state_pass in ((True, False, both), (False, False, "reverse"), (True, True, both)):
             op.RECOMPUTE_STATES, op.KEEP_PREP = recompute, keep_prep
             p = op.plan(2, 150, 4, 128, 128, True, Hk=2, dtype=dtype)
             assert (p["bwd_state_passes"], p["bwd_prep"]) == (state_pass, "rerun" if recompute and not keep_prep
@@ -606,7 +607,8 @@ def test_kept_prep_operands_change_no_bits(dtype, bf16_state_grad):
             finally:
                 op.EVENTS = events
             assert ran.count("prep_bwd") == (1 if recompute and not keep_prep else 0), ran
-            assert ("state_pair" in ran) == (state_pass == "pair") and ("state_bwd" in ran) == (state_pass == "reverse")
+            assert ("state_pair" in ran) == (state_pass == "pair") and ("state_bwd" in ran) == (state_pass != "pair")
+            assert ("state_fwd_store" in ran) == (state_pass == "recompute+reverse")
             outs.append([o, sT] + [grads[n] for n in sorted(grads)])
     finally:
         op.RECOMPUTE_STATES, op.KEEP_PREP = old

@@ -344,6 +344,18 @@ def test_plan_reports_the_launch_choices():
     assert op.plan(1, 32768, 16, 128, 128, save=True)["segments"] == 1     # a training forward never splits
     p = op.plan(2, 100, 4, 64, 64, save=True, dtype=torch.float32)
     assert (p["operands"], p["prep"], p["fwd_state_pass"], p["chunk_bwd"]) == ("f32", "prep", "state_fwd", "chunk_bwd")
+    # float32 operands run the recompute and reverse passes as two launches unless OVERLAP is True
+    p = op.plan(4, 1024, 16, 128, 128, save=True, dtype=torch.float32)
+    assert (p["bwd_state_passes"], p["bwd_split"]) == ("recompute+reverse", 4)
+    old = op.OVERLAP
+    try:
+        op.OVERLAP = True
+        assert op.plan(4, 1024, 16, 128, 128, save=True, dtype=torch.float32)["bwd_state_passes"] == "pair"
+        op.OVERLAP = False
+        assert op.plan(4, 1024, 16, 128, 128, save=True)["bwd_state_passes"] == "recompute+reverse"
+    finally:
+        op.OVERLAP = old
+    assert op.pairs_states(torch.float16) and op.pairs_states(torch.bfloat16) and not op.pairs_states(torch.float32)
     assert op.plan(1, 100, 2, 256, 128, save=True)["operands"] == "f32"      # wide keys run the float32 kernels
     assert op.plan(4, 100, 2, 128, 128, save=True)["chunk_bwd"] == "chunk_bwd8"   # fewer chunk-heads than CUs
     assert op.plan(4, 1024, 16, 128, 128, save=True, l2norm=False)["operands"] == "f32"   # keys not normalised
