@@ -766,7 +766,7 @@ __device__ __forceinline__ void touch_share(int lines, int parts, int part, int&
 // flight while this chunk's MFMAs run -- and each wave keeps its 16 columns of S in accumulators.  The barriers order
 // LDS only (lds_barrier): the loader waits for its copies itself, and no wave waits for its global stores.
 // ---------------------------------------------------------------------------------------------------------------------
-template <typename MT, int DK, bool OUT, bool STORE, int NW>
+template <typename MT, int DK, bool OUT, bool STORE, int NW, int KS = 1>
 struct StateFwdLds {
   using GW = Tile<MT, C, DK>;    // W, diag(e) K^, diag(gamma) Q^     [t][d]
   using GM = Tile<MT, C, C>;     // M                                  [t][s]
@@ -774,23 +774,189 @@ struct StateFwdLds {
   static constexpr int SZ = O_M + (OUT ? GM::ELEMS : 0);
   // bf16 Vn leaves through per-wave row staging (store mode)
   static constexpr int STG = (STORE && sizeof(MT) == 2) ? NW * ColStage::ELEMS : 0;
+  // KS = 2 (the key-split float32 pass): a slot per compute wave for its partial W S product (64 x 16) and, for the
+  // output, its half of S as fragments
+  static constexpr int XS = OUT ? (DK / 64) * 8 * 64 : 0, XW = XS + 16 * 64;
+  static constexpr int EX = KS == 2 ? 2 * NW * XW : 0;
   // DIRECT: one stage of the chunk's tiles does not fit LDS (fp32 at DK = 256); the compute waves then read their
   // fragments from global memory (L2) and the loader wave has nothing to do
-  static constexpr bool DIRECT = (SZ + STG) * (int)sizeof(MT) > LDS_BYTES;
-  static constexpr int NBUF = DIRECT ? 0 : Buffers<SZ * (int)sizeof(MT), STG * (int)sizeof(MT)>::N;
-  static constexpr int O_STG = NBUF * SZ;
-  static constexpr int ELEMS = (O_STG + STG) > 16 ? O_STG + STG : 16;
+  static constexpr bool DIRECT = (SZ + STG + EX) * (int)sizeof(MT) > LDS_BYTES;
+  static constexpr int NBUF = DIRECT ? 0 : Buffers<SZ * (int)sizeof(MT), (STG + EX) * (int)sizeof(MT)>::N;
+  static constexpr int O_STG = NBUF * SZ, O_EX = O_STG + STG;
+  static constexpr int ELEMS = (O_EX + EX) > 16 ? O_EX + EX : 16;
+  // whether the key-split form (this struct with KS = 2) serves the pass: float32 operands, key widths 64 and 128
+  // (whole 32-row fragments in each half), both halves' slots and a stage in LDS, and at most 5 waves (two column
+  // slices): at 9 waves a wave has 168 registers and the pass spills
+  static constexpr bool KS_OK = KS == 2 && sizeof(MT) == 4 && (DK == 64 || DK == 128) && !DIRECT && NW <= 2;
 };
+
+// The key-split float32 pass (the compute waves of state_fwd_body with KS = 2).  The 16x16x4 float32 MFMA takes a
+// SIMD 32 cycles, so a wave that carries a 16-column slice alone is bound by its matrix core: two waves (on two SIMDs)
+// carry each slice, wave 2 s + h holding rows [h DK / 2, (h + 1) DK / 2) of the slice's state.  Per chunk each forms
+// its half of W S, the pair exchanges the halves through LDS (one barrier) and both take Vn = U - (P_0 + P_1)
+// (the same bits in both waves: the sum is commutative), then each updates its own rows of S, and with the output
+// each forms the output's row blocks 2 h, 2 h + 1 from the whole S (the partner's half from LDS) and Vn.  Per wave
+// that is 208-224 MFMAs a chunk at DK = 128 against 432 for one wave.  The single-wave form sums the two halves of
+// W S the same way, so both give the same bits.
+template <int DK, int NW, bool OUT, bool STORE>
+__device__ __forceinline__ void state_fwd_ks(const StateFwdArgs& a, float* lds, int hr, int slice, int cb, int ce,
+                                             size_t crow, int tb) {
+  using MT = float;
+  using L = StateFwdLds<MT, DK, OUT, STORE, NW, 2>;
+  using GW = typename L::GW;
+  using GM = typename L::GM;
+  constexpr int ND = DK / 16, NH = ND / 2, PH = NH / 2;   // state tiles; a wave's tiles and its 32-row k-blocks
+  constexpr int O_KE = L::O_KE, O_Q = L::O_Q, O_M = L::O_M, SZ = L::SZ, NBUF = L::NBUF;
+  const int T = a.T, H = a.H, DV = a.DV, NT = a.NT;
+  const int h = hr % H;
+  const int l = lane_id(), w = wave_id(), j = l >> 4;
+  const int cw = w >> 1, kh = w & 1;       // the wave's column slice, and its half of the state's rows
+  const int v0 = (slice * NW + cw) * 16;
+  const int col = v0 + (l & 15);
+  const int r0 = kh * NH * 16;             // the wave's first state row
+  float* const xme = lds + L::O_EX + (2 * cw + kh) * L::XW;             // this wave's exchange slot
+  const float* const xpa = lds + L::O_EX + (2 * cw + (kh ^ 1)) * L::XW;  // its partner's
+  const size_t o_base = ((size_t)tb * T * H + h) * DV, o_pitch = (size_t)H * DV;
+  auto loadU = [&](int c, f4* U) {
+    const float* Uc = a.U + (crow * NT + c) * C * DV + (size_t)(4 * j) * DV + col;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) U[mi][r] = Uc[(16 * mi + r) * DV];
+  };
+
+  f4 S[NH];
+  load_state(S, a.s0, (size_t)hr * DK * DV + (size_t)r0 * DV, DV, col);
+  f4 Un[4];
+  float gln = 0.f;
+  if (cb < ce) {
+    loadU(cb, Un);
+    gln = a.GL[crow * NT + cb];
+    if (NBUF == 2) lds_barrier();        // the first chunk is in LDS
+  }
+  for (int c = cb; c < ce; ++c) {
+    const size_t bhc = crow * NT + c;
+    const int buf = (NBUF == 2) ? ((c - cb) & 1) : 0;
+    f4 U[4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) U[mi] = Un[mi];
+    const float gl = gln;
+    if (c + 1 < ce) {
+      loadU(c + 1, Un);
+      gln = a.GL[bhc + 1];
+    }
+    if constexpr (STORE) {                 // S_c: this wave's rows
+      float* Scc = a.Sc + bhc * DK * DV + (size_t)(r0 + 4 * j) * DV + col;
+#pragma unroll
+      for (int di = 0; di < NH; ++di)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) Scc[(16 * di + r) * DV] = S[di][r];
+    }
+    if (NBUF == 1) lds_barrier();        // chunk c is in LDS
+    const MT* st = lds + buf * SZ;
+    const MT* tW = st;
+    const MT* tK = st + O_KE;
+    // this wave's half of S as B fragments; the output needs the partner's too
+    Frag<MT> Sf[PH];
+#pragma unroll
+    for (int p = 0; p < PH; ++p) {
+      Sf[p] = frag_acc<MT>(S[2 * p], S[2 * p + 1]);
+      if constexpr (OUT) {
+        *reinterpret_cast<f4*>(xme + ((2 * p) * 64 + l) * 4) = f4{Sf[p].v[0], Sf[p].v[1], Sf[p].v[2], Sf[p].v[3]};
+        *reinterpret_cast<f4*>(xme + ((2 * p + 1) * 64 + l) * 4) = f4{Sf[p].v[4], Sf[p].v[5], Sf[p].v[6], Sf[p].v[7]};
+      }
+    }
+    // this wave's half of W S: k-blocks kh PH .. kh PH + PH - 1
+    f4 P[4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) P[mi] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < PH; ++p)
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) mma(P[mi], frag_tile<MT, GW>(tW, 16 * mi, 32 * (kh * PH + p)), Sf[p]);
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) *reinterpret_cast<f4*>(xme + L::XS + (mi * 64 + l) * 4) = P[mi];
+    lds_barrier();                         // the pair's halves are in LDS
+    f4 Vn[4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) Vn[mi] = U[mi] - (P[mi] + *reinterpret_cast<const f4*>(xpa + L::XS + (mi * 64 + l) * 4));
+    Frag<MT> Vf[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) Vf[p] = frag_acc<MT>(Vn[2 * p], Vn[2 * p + 1]);
+    if (STORE && kh == 0) {                // Vn (both waves hold it)
+      float* Vnc = (float*)a.Vn + bhc * C * DV + (size_t)(4 * j) * DV + col;
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) Vnc[(16 * mi + r) * DV] = Vn[mi][r];
+    }
+    // this wave's rows of S <- exp(G_last) S + (diag(e) K)^T Vn
+#pragma unroll
+    for (int di = 0; di < NH; ++di) {
+      S[di] = S[di] * gl;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) mma(S[di], frag_tile_tr<MT, GW>(tK, 32 * p, r0 + 16 * di), Vf[p]);
+    }
+    if constexpr (OUT) {
+      // rows 16 mi of O^T = S^T (diag(gamma) Q)^T + Vn^T M^T for mi = 2 kh, 2 kh + 1, from the whole S (fragments of
+      // rows 0 .. DK / 2 - 1 in S0, the rest in S1)
+      const MT* tQ = st + O_Q;
+      const MT* tM = st + O_M;
+      Frag<MT> S0[PH], S1[PH];
+#pragma unroll
+      for (int p = 0; p < PH; ++p) {
+        const f4 x = *reinterpret_cast<const f4*>(xpa + ((2 * p) * 64 + l) * 4);
+        const f4 y = *reinterpret_cast<const f4*>(xpa + ((2 * p + 1) * 64 + l) * 4);
+        Frag<MT> q;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          q.v[r] = x[r];
+          q.v[r + 4] = y[r];
+        }
+        S0[p] = kh ? q : Sf[p];
+        S1[p] = kh ? Sf[p] : q;
+      }
+      f4 pO[2];
+#pragma unroll
+      for (int m = 0; m < 2; ++m) pO[m] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p = 0; p < ND / 2; ++p)
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+          mma(pO[m], p < PH ? S0[p % PH] : S1[p % PH], frag_tile<MT, GW>(tQ, 16 * (2 * kh + m), 32 * p));
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+          if (32 * p <= 16 * (2 * kh + m) + 15) mma(pO[m], Vf[p], frag_tile<MT, GM>(tM, 16 * (2 * kh + m), 32 * p));
+      int t0, tend;
+      chunk_span(a.pack, NT, c, T, t0, tend);
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        const int t = t0 + 16 * (2 * kh + m) + (l & 15);
+        if (t < tend) store4<MT>((MT*)a.o + o_base + (size_t)t * o_pitch + v0 + 4 * j, pO[m]);
+      }
+    }
+    lds_barrier();                         // end of chunk c: the next chunk is in, this buffer and the slots are free
+  }
+  if (a.sT) {
+#pragma unroll
+    for (int di = 0; di < NH; ++di)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) a.sT[(size_t)hr * DK * DV + (r0 + 16 * di + 4 * j + r) * DV + col] = S[di][r];
+  }
+}
 
 // The pass of workgroup f of the launch (see state_map), with `lds` the workgroup's LDS (StateFwdLds::ELEMS elements).
 // MAP (with neither OUT nor STORE): the chunk map of each sequence instead of its states.  A sequence's pass is affine
 // in its starting state, S_end = A S_0 + B, so it runs on DK + DV columns: the first DK start from the identity with U
 // taken as zero (they end as A, DK x DK), the other DV from zero with the real U (they end as B); sT receives
 // [A | B] per head-row, row pitch DK + DV.
-template <typename MT, int DK, int NW, bool OUT, bool STORE, bool MAP = false>
+template <typename MT, int DK, int NW, bool OUT, bool STORE, bool MAP = false, int KS = 1>
 __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, int f) {
   static_assert(!MAP || (!OUT && !STORE), "the map pass writes only the maps");
-  using L = StateFwdLds<MT, DK, OUT, STORE, NW>;
+  static_assert(KS == 1 || (!MAP && StateFwdLds<MT, DK, OUT, STORE, NW, KS>::KS_OK), "the key-split pass");
+  using L = StateFwdLds<MT, DK, OUT, STORE, NW, KS>;
   using GW = typename L::GW;
   using GM = typename L::GM;
   constexpr int ND = DK / 16;
@@ -810,10 +976,11 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
   const size_t crow = a.pack ? (size_t)h : (size_t)hr;   // row of the per-chunk tensors [*, H, NT, ...]
   const int tb = a.pack ? 0 : b;           // batch row of the token tensors
 
-  if (w == NW) {
+  if (w == KS * NW) {
     if constexpr (DIRECT) return;          // no copies: the compute waves pass no barrier in this mode
     // the loader wave: every asynchronous copy of the chunk tiles, one chunk ahead of the compute waves, so that their
-    // issue (a CU's load path takes ~1K cycles for a chunk's tiles) never stalls the MFMA chain
+    // issue (a CU's load path takes ~1K cycles for a chunk's tiles) never stalls the MFMA chain.  With KS = 2 it also
+    // passes the compute waves' mid-chunk barrier (their exchange of halves), before waiting for its copies.
     int offW[GW::per_wave(1)], offM[GM::per_wave(1)];
     GW::template plan<1>(offW, 0, DK);
     if (OUT) GM::template plan<1>(offM, 0, C);
@@ -835,6 +1002,7 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
       }
       for (int c = cb; c < ce; ++c) {
         if (c + 1 < ce) issue(c + 1, (c + 1 - cb) & 1);
+        if constexpr (KS == 2) lds_barrier();
         wait_dma();
         lds_barrier();
       }
@@ -843,10 +1011,15 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
         issue(c, 0);
         wait_dma();
         lds_barrier();   // chunk c is in LDS
+        if constexpr (KS == 2) lds_barrier();
         lds_barrier();   // the compute waves are done with it
       }
     }
     return;                // the compute waves pass no barrier after their loop
+  }
+  if constexpr (KS == 2) {
+    state_fwd_ks<DK, NW, OUT, STORE>(a, lds, hr, slice, cb, ce, crow, tb);
+    return;
   }
 
   const int v0 = (slice * NW + w) * 16;
@@ -955,23 +1128,26 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
     Frag<MT> Sf[ND / 2];
 #pragma unroll
     for (int p = 0; p < ND / 2; ++p) Sf[p] = frag_acc<MT>(S[2 * p], S[2 * p + 1]);
-    // Vn = U - W S
-    f4 Vn[4];
+    // Vn = U - W S.  Float32 at key widths 64 and 128 sums the state's two row halves apart and then adds them, the
+    // key-split pass's order (state_fwd_ks), so the two forms give the same bits.
+    constexpr bool HALVES = sizeof(MT) == 4 && !MAP && (DK == 64 || DK == 128);
+    f4 Vn[4], Vh[4];
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) Vn[mi] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int mi = 0; mi < 4; ++mi) Vn[mi] = Vh[mi] = f4{0.f, 0.f, 0.f, 0.f};
     if constexpr (EARLY) {
 #pragma unroll
       for (int p = 0; p < ND / 2; ++p)
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi) mma(Vn[mi], fw[mi][p], Sf[p]);
+        for (int mi = 0; mi < 4; ++mi) mma((HALVES && p >= ND / 4) ? Vh[mi] : Vn[mi], fw[mi][p], Sf[p]);
     } else {
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-        for (int p = 0; p < ND / 2; ++p) mma(Vn[mi], frag_tile<MT, FW>(tW, 16 * mi, 32 * p), Sf[p]);
+        for (int p = 0; p < ND / 2; ++p)
+          mma((HALVES && p >= ND / 4) ? Vh[mi] : Vn[mi], frag_tile<MT, FW>(tW, 16 * mi, 32 * p), Sf[p]);
     }
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) Vn[mi] = U[mi] - Vn[mi];
+    for (int mi = 0; mi < 4; ++mi) Vn[mi] = U[mi] - (HALVES ? Vn[mi] + Vh[mi] : Vn[mi]);
     Frag<MT> Vf[2];
 #pragma unroll
     for (int p = 0; p < 2; ++p) Vf[p] = frag_acc<MT>(Vn[2 * p], Vn[2 * p + 1]);
@@ -1029,10 +1205,10 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
   }
 }
 
-template <typename MT, int DK, int NW, bool OUT, bool STORE, bool MAP = false>
-__global__ void __launch_bounds__(64 * (NW + 1)) state_fwd_kernel(StateFwdArgs a) {
-  __shared__ __attribute__((aligned(1024))) MT lds[StateFwdLds<MT, DK, OUT, STORE, NW>::ELEMS];
-  state_fwd_body<MT, DK, NW, OUT, STORE, MAP>(a, lds, blockIdx.x);
+template <typename MT, int DK, int NW, bool OUT, bool STORE, bool MAP = false, int KS = 1>
+__global__ void __launch_bounds__(64 * (KS * NW + 1)) state_fwd_kernel(StateFwdArgs a) {
+  __shared__ __attribute__((aligned(1024))) MT lds[StateFwdLds<MT, DK, OUT, STORE, NW, KS>::ELEMS];
+  state_fwd_body<MT, DK, NW, OUT, STORE, MAP, KS>(a, lds, blockIdx.x);
 }
 
 // state_scan_kernel for DK <= 128 (see above).  A step is A_s [DK x DK] times the state slice [DK x 16] on fp32 MFMAs
@@ -1416,7 +1592,7 @@ __global__ void __launch_bounds__(64 * (2 * NW + 1)) state_out_kernel(StateFwdAr
 // ---------------------------------------------------------------------------------------------------------------------
 // the reverse state pass: streams diag(e) K^, diag(gamma) Q^, W, M and the workgroup's dO columns per chunk
 // ---------------------------------------------------------------------------------------------------------------------
-template <typename MT, int DK, int NW>
+template <typename MT, int DK, int NW, int KS = 1>
 struct StateBwdLds {
   using GK = Tile<MT, C, DK>;        // diag(e) K^, diag(gamma) Q^, W    [t][d]
   using GM = Tile<MT, C, C>;         // M                                [t][s]
@@ -1425,16 +1601,134 @@ struct StateBwdLds {
   static constexpr int SZ = O_O + GO::ELEMS;
   static constexpr int STG = sizeof(MT) == 2 ? NW * ColStage::ELEMS : 0;   // bf16 dVn leaves through row staging
   static constexpr int SCAL = 32 / (int)sizeof(MT);   // per stage: the chunk's G_last (bits), t0, tend, as 4 ints
+  // KS = 2 (the key-split float32 pass): a slot per compute wave for its partial dVn (64 x 16)
+  static constexpr int XW = 16 * 64, EX = KS == 2 ? 2 * NW * XW : 0;
   // DIRECT: one stage does not fit LDS (fp32 at DK = 256): the compute waves read the tiles from global memory
-  static constexpr bool DIRECT = (SZ + STG + SCAL) * (int)sizeof(MT) + TOUCH_SINK > LDS_BYTES;
-  static constexpr int NBUF = DIRECT ? 0 : Buffers<SZ * (int)sizeof(MT), (STG + SCAL) * (int)sizeof(MT) + TOUCH_SINK>::N;
-  static constexpr int O_STG = NBUF * SZ, O_SCAL = O_STG + STG;
-  static constexpr int ELEMS = O_SCAL + SCAL;
+  static constexpr bool DIRECT = (SZ + STG + SCAL + EX) * (int)sizeof(MT) + TOUCH_SINK > LDS_BYTES;
+  static constexpr int NBUF =
+      DIRECT ? 0 : Buffers<SZ * (int)sizeof(MT), (STG + SCAL + EX) * (int)sizeof(MT) + TOUCH_SINK>::N;
+  static constexpr int O_STG = NBUF * SZ, O_SCAL = O_STG + STG, O_EX = O_SCAL + SCAL;
+  static constexpr int ELEMS = O_EX + EX;
+  // see StateFwdLds::KS_OK
+  static constexpr bool KS_OK = KS == 2 && sizeof(MT) == 4 && (DK == 64 || DK == 128) && !DIRECT && NW <= 2;
 };
 
-template <typename MT, int DK, int NW>
+// The key-split float32 reverse pass (the compute waves of state_bwd_body with KS = 2; see state_fwd_ks): wave
+// 2 s + h holds rows [h DK / 2, (h + 1) DK / 2) of its slice's dS.  Per chunk each forms its half of diag(e) K^ dS
+// (with M^T dO for row blocks 2 h, 2 h + 1), the pair exchanges the halves through LDS and both take dVn as their sum,
+// then each updates its own rows of dS.  Per wave 216 MFMAs a chunk at DK = 128 against 448 for one wave.
+template <int DK, int NW>
+__device__ __forceinline__ void state_bwd_ks(const StateBwdArgs& a, float* lds, int hr, int slice, int cb, int ce,
+                                             size_t crow, int tb) {
+  using MT = float;
+  using L = StateBwdLds<MT, DK, NW, 2>;
+  using GK = typename L::GK;
+  using GM = typename L::GM;
+  using GO = typename L::GO;
+  constexpr int ND = DK / 16, NH = ND / 2, PH = NH / 2;
+  constexpr int O_Q = L::O_Q, O_W = L::O_W, O_M = L::O_M, O_O = L::O_O, SZ = L::SZ, NBUF = L::NBUF;
+  const int DV = a.DV, NT = a.NT;
+  const int l = lane_id(), w = wave_id(), j = l >> 4;
+  const int cw = w >> 1, kh = w & 1;       // the wave's column slice, and its half of the state's rows
+  const int vg = slice * NW * 16;          // the workgroup's first value column
+  const int col = vg + cw * 16 + (l & 15);
+  const int r0 = kh * NH * 16;             // the wave's first state row
+  float* const xme = lds + L::O_EX + (2 * cw + kh) * L::XW;
+  const float* const xpa = lds + L::O_EX + (2 * cw + (kh ^ 1)) * L::XW;
+  (void)tb;
+
+  f4 dS[NH];
+  load_state(dS, a.dsT, (size_t)hr * DK * DV + (size_t)r0 * DV, DV, col);
+  if (cb < ce && NBUF == 2) lds_barrier();   // the last chunk is in LDS
+  for (int c = ce - 1, it = 0; c >= cb; --c, ++it) {
+    const int buf = (NBUF == 2) ? (it & 1) : 0;
+    const size_t bhc = crow * NT + c;
+    // the row pitch, opaque to the compiler here: otherwise it keeps the 32 store addresses of dSn and dVn (64-bit
+    // each) live across the loop, which spills at 5 waves' 256 registers
+    int dv = DV;
+    asm volatile("" : "+s"(dv));
+    {                                      // dS_{c+1}: this wave's rows
+      float* dSc = a.dSn + bhc * DK * dv + (size_t)(r0 + 4 * j) * dv + col;
+#pragma unroll
+      for (int di = 0; di < NH; ++di)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dSc[(16 * di + r) * dv] = dS[di][r];
+    }
+    if (NBUF == 1) lds_barrier();        // chunk c is in LDS
+    const int* sc = (const int*)(lds + L::O_SCAL) + 4 * buf;
+    const float gl = __int_as_float(sc[0]);
+    const int t0 = sc[1], tend = sc[2];
+    const MT* st = lds + buf * SZ;
+    const MT* tK = st;
+    const MT* tQ = st + O_Q;
+    const MT* tW = st + O_W;
+    const MT* tM = st + O_M;
+    Frag<MT> Of[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      Of[p] = frag_tile_rows<MT, GO>(st + O_O, 32 * p, cw * 16 + (l & 15));
+      if (t0 + C > tend)                   // rows past the sequence end hold copies of its last row: zero them
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (t0 + 32 * p + kmap(j, e) >= tend) Of[p].set(e, 0.f);
+    }
+    Frag<MT> Sf[PH];
+#pragma unroll
+    for (int p = 0; p < PH; ++p) Sf[p] = frag_acc<MT>(dS[2 * p], dS[2 * p + 1]);
+    // this wave's half of dVn
+    f4 P[4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p = 0; p < PH; ++p) mma(acc, frag_tile<MT, GK>(tK, 16 * mi, 32 * (kh * PH + p)), Sf[p]);
+      if ((mi >> 1) == kh)
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+          if (32 * p + 31 >= 16 * mi) mma(acc, frag_tile_tr<MT, GM>(tM, 32 * p, 16 * mi), Of[p]);
+      P[mi] = acc;
+      *reinterpret_cast<f4*>(xme + (mi * 64 + l) * 4) = acc;
+    }
+    lds_barrier();                         // the pair's halves are in LDS
+    f4 dV[4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) dV[mi] = P[mi] + *reinterpret_cast<const f4*>(xpa + (mi * 64 + l) * 4);
+    Frag<MT> Vf[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) Vf[p] = frag_acc<MT>(dV[2 * p], dV[2 * p + 1], -1.f);
+    if (kh == 0) {                         // dVn (both waves hold it)
+      float* dVc = (float*)a.dVn + bhc * C * dv + (size_t)(4 * j) * dv + col;
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dVc[(16 * mi + r) * dv] = dV[mi][r];
+    }
+    // this wave's rows of dS <- exp(G_last) dS + (diag(gamma) Q^)^T dO - W^T dVn, one row block at a time (the
+    // scheduling barrier keeps the next block's 32 gathered fragment values from being loaded early: 5 waves on 4
+    // SIMDs leave 256 registers a wave)
+#pragma unroll
+    for (int di = 0; di < NH; ++di) {
+      f4 acc = dS[di] * gl;
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        mma(acc, frag_tile_tr<MT, GK>(tW, 32 * p, r0 + 16 * di), Vf[p]);
+        mma(acc, frag_tile_tr<MT, GK>(tQ, 32 * p, r0 + 16 * di), Of[p]);
+      }
+      dS[di] = acc;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    lds_barrier();                         // end of chunk c
+  }
+#pragma unroll
+  for (int di = 0; di < NH; ++di)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) a.ds0[(size_t)hr * DK * DV + (r0 + 16 * di + 4 * j + r) * DV + col] = dS[di][r];
+}
+
+template <typename MT, int DK, int NW, int KS = 1>
 __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, int f) {
-  using L = StateBwdLds<MT, DK, NW>;
+  static_assert(KS == 1 || StateBwdLds<MT, DK, NW, KS>::KS_OK, "the key-split pass");
+  using L = StateBwdLds<MT, DK, NW, KS>;
   using GK = typename L::GK;
   using GM = typename L::GM;
   using GO = typename L::GO;
@@ -1456,7 +1750,7 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
   const int tb = a.pack ? 0 : b;             // batch row of the token tensors
   const size_t o_base = ((size_t)tb * T * H + h) * DV, o_pitch = (size_t)H * DV;
 
-  if (w == NW) {
+  if (w == KS * NW) {
     if constexpr (DIRECT) return;          // no copies: the compute waves pass no barrier in this mode
     // the loader wave (see state_fwd_kernel), walking the chunks backwards
     int offK[GK::per_wave(1)], offM[GM::per_wave(1)], offO[GO::per_wave(1)];
@@ -1468,13 +1762,21 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
       const size_t bhc = crow * NT + c;
       int t0, tend;
       chunk_span<true>(a.pack, NT, c, T, t0, tend);
-      GK::template dma_planned<1>(st, (const MT*)a.Ke + bhc * C * DK, offK, 0);
-      GK::template dma_planned<1>(st + O_Q, (const MT*)a.Qg + bhc * C * DK, offK, 0);
-      GK::template dma_planned<1>(st + O_W, (const MT*)a.W + bhc * C * DK, offK, 0);
-      GM::template dma_planned<1>(st + O_M, (const MT*)a.M + bhc * C * C, offM, 0);
       const MT* og = (const MT*)a.dO + o_base + (size_t)t0 * o_pitch + vg;
-      if (t0 + C <= tend) GO::template dma_planned<1>(st + O_O, og, offO, 0);
-      else GO::dma(st + O_O, og, o_pitch, 0, 1, tend - t0);   // a partial chunk: rows clamped to the sequence
+      if constexpr (KS == 2) {             // addresses formed per copy: the planned offsets (59 registers at DK = 128)
+        GK::dma(st, (const MT*)a.Ke + bhc * C * DK, DK, 0, 1);   // spill at 5 waves' 256 registers a wave
+        GK::dma(st + O_Q, (const MT*)a.Qg + bhc * C * DK, DK, 0, 1);
+        GK::dma(st + O_W, (const MT*)a.W + bhc * C * DK, DK, 0, 1);
+        GM::dma(st + O_M, (const MT*)a.M + bhc * C * C, C, 0, 1);
+        GO::dma(st + O_O, og, o_pitch, 0, 1, tend - t0);
+      } else {
+        GK::template dma_planned<1>(st, (const MT*)a.Ke + bhc * C * DK, offK, 0);
+        GK::template dma_planned<1>(st + O_Q, (const MT*)a.Qg + bhc * C * DK, offK, 0);
+        GK::template dma_planned<1>(st + O_W, (const MT*)a.W + bhc * C * DK, offK, 0);
+        GM::template dma_planned<1>(st + O_M, (const MT*)a.M + bhc * C * C, offM, 0);
+        if (t0 + C <= tend) GO::template dma_planned<1>(st + O_O, og, offO, 0);
+        else GO::dma(st + O_O, og, o_pitch, 0, 1, tend - t0);   // a partial chunk: rows clamped to the sequence
+      }
       if (l == 0) {                        // the chunk's scalars beside its stage (the compute waves load nothing)
         int* sc = (int*)(lds + L::O_SCAL) + 4 * buf;
         sc[0] = __float_as_int(ld_const(a.GL, bhc));
@@ -1506,6 +1808,7 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
       }
       for (int c = ce - 1, it = 0; c >= cb; --c, ++it) {
         if (c > cb) issue(c - 1, (it + 1) & 1);
+        if constexpr (KS == 2) lds_barrier();   // the compute waves' exchange of halves
         if (c - 2 >= cb) touch(c - 2);
         else wait_dma();
         lds_barrier();
@@ -1515,9 +1818,14 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
         issue(c, 0);
         wait_dma();
         lds_barrier();
+        if constexpr (KS == 2) lds_barrier();
         lds_barrier();
       }
     }
+    return;
+  }
+  if constexpr (KS == 2) {
+    state_bwd_ks<DK, NW>(a, lds, hr, slice, cb, ce, crow, tb);
     return;
   }
   const int col = vg + w * 16 + (l & 15);
@@ -1584,20 +1892,24 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
     Frag<MT> Sf[ND / 2];
 #pragma unroll
     for (int p = 0; p < ND / 2; ++p) Sf[p] = frag_acc<MT>(dS[2 * p], dS[2 * p + 1]);
-    // dVn = M^T dO + diag(e) K^ dS   (M^T upper triangular: k-blocks before the row block are zero)
+    // dVn = M^T dO + diag(e) K^ dS   (M^T upper triangular: k-blocks before the row block are zero).  Float32 at key
+    // widths 64 and 128 sums in the key-split pass's order (state_bwd_ks): the two row halves of dS apart, M^T dO
+    // with the first half for row blocks 0, 1 and with the second for 2, 3, then the halves added.
+    constexpr bool HALVES = sizeof(MT) == 4 && (DK == 64 || DK == 128);
     f4 dV[4];
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
       Frag<MT> fk[ND / 2];
 #pragma unroll
       for (int p = 0; p < ND / 2; ++p) fk[p] = frag_tile<MT, FK>(tK, 16 * mi, 32 * p);
-      f4 acc = {0.f, 0.f, 0.f, 0.f};
+      f4 acc = {0.f, 0.f, 0.f, 0.f}, acch = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int p = 0; p < ND / 2; ++p) mma(acc, fk[p], Sf[p]);
+      for (int p = 0; p < ND / 2; ++p) mma((HALVES && p >= ND / 4) ? acch : acc, fk[p], Sf[p]);
 #pragma unroll
       for (int p = 0; p < 2; ++p)
-        if (32 * p + 31 >= 16 * mi) mma(acc, frag_tile_tr<MT, FM>(tM, 32 * p, 16 * mi), Of[p]);
-      dV[mi] = acc;
+        if (32 * p + 31 >= 16 * mi)
+          mma((HALVES && mi >= 2) ? acch : acc, frag_tile_tr<MT, FM>(tM, 32 * p, 16 * mi), Of[p]);
+      dV[mi] = HALVES ? acc + acch : acc;
     }
     Frag<MT> Vf[2];
 #pragma unroll
@@ -1631,21 +1943,21 @@ __device__ __forceinline__ void state_bwd_body(const StateBwdArgs& a, MT* lds, i
     for (int r = 0; r < 4; ++r) a.ds0[(size_t)hr * DK * DV + (16 * di + 4 * j + r) * DV + col] = dS[di][r];
 }
 
-template <typename MT, int DK, int NW>
-__global__ void __launch_bounds__(64 * (NW + 1)) state_bwd_kernel(StateBwdArgs a) {
-  __shared__ __attribute__((aligned(1024))) MT lds[StateBwdLds<MT, DK, NW>::ELEMS];
-  state_bwd_body<MT, DK, NW>(a, lds, blockIdx.x);
+template <typename MT, int DK, int NW, int KS = 1>
+__global__ void __launch_bounds__(64 * (KS * NW + 1)) state_bwd_kernel(StateBwdArgs a) {
+  __shared__ __attribute__((aligned(1024))) MT lds[StateBwdLds<MT, DK, NW, KS>::ELEMS];
+  state_bwd_body<MT, DK, NW, KS>(a, lds, blockIdx.x);
 }
 
 // The backward's recompute pass (storing S_c, Vn) and its reverse pass in one launch: they read prep's outputs and
 // not each other's, so workgroups [0, nfwd) run the first and the rest the second, side by side on the CUs, with no
 // stream synchronisation between them.
-template <typename MT, int DK, int NW>
-__global__ void __launch_bounds__(64 * (NW + 1)) state_pair_kernel(StateFwdArgs af, StateBwdArgs ab, int nfwd) {
-  constexpr int EF = StateFwdLds<MT, DK, false, true, NW>::ELEMS, EB = StateBwdLds<MT, DK, NW>::ELEMS;
+template <typename MT, int DK, int NW, int KS = 1>
+__global__ void __launch_bounds__(64 * (KS * NW + 1)) state_pair_kernel(StateFwdArgs af, StateBwdArgs ab, int nfwd) {
+  constexpr int EF = StateFwdLds<MT, DK, false, true, NW, KS>::ELEMS, EB = StateBwdLds<MT, DK, NW, KS>::ELEMS;
   __shared__ __attribute__((aligned(1024))) MT lds[EF > EB ? EF : EB];
-  if ((int)blockIdx.x < nfwd) state_fwd_body<MT, DK, NW, false, true>(af, lds, blockIdx.x);
-  else state_bwd_body<MT, DK, NW>(ab, lds, blockIdx.x - nfwd);
+  if ((int)blockIdx.x < nfwd) state_fwd_body<MT, DK, NW, false, true, false, KS>(af, lds, blockIdx.x);
+  else state_bwd_body<MT, DK, NW, KS>(ab, lds, blockIdx.x - nfwd);
 }
 
 // ---------------------------------------------------------------------------------------------------------------------
@@ -3183,9 +3495,14 @@ int macai_gdr_state_fwd(const void* W, const float* U, const void* Ke, const flo
   hipStream_t st = (hipStream_t)stream;
 #define LAUNCH_SF(MT, O, S) \
   DISPATCH_DK(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_fwd_kernel<MT, DKC, NWC, O, S>), grid, block, 0, st, a)))
-#define LAUNCH_SF32(O, S)                                                                                      \
-  DISPATCH_DK_F32(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_fwd_kernel<float, DKC, NWC, O, S>), grid, block, 0, \
-                                                         st, a)))
+// float32: the key-split form (two waves a column slice) where it fits, else one wave a slice; the same bits
+#define LAUNCH_SF32(O, S)                                                                                              \
+  DISPATCH_DK_F32(DK, DISPATCH_NW(nw, {                                                                                \
+    if constexpr (StateFwdLds<float, DKC, O, S, NWC, 2>::KS_OK)                                                        \
+      hipLaunchKernelGGL((state_fwd_kernel<float, DKC, NWC, O, S, false, 2>), grid, dim3(64 * (2 * NWC + 1)), 0, st, a); \
+    else                                                                                                               \
+      hipLaunchKernelGGL((state_fwd_kernel<float, DKC, NWC, O, S>), grid, block, 0, st, a);                            \
+  }))
 #define LAUNCH_SO(S)                                                                                                  \
   {                                                                                                                   \
     const dim3 block2(64 * (2 * nw + 1));                                                                             \
@@ -3234,9 +3551,13 @@ int macai_gdr_state_bwd(const void* Ke, const void* Qg, const void* W, const voi
   dim3 grid((unsigned)(8 * nslice * ((HR + 7) / 8)));
   dim3 block(64 * (nw + 1));   // nw compute waves and the loader wave
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == MACAI_GDR_F32) {
-    DISPATCH_DK_F32(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_bwd_kernel<float, DKC, NWC>), grid, block, 0, st,
-                                                           a)));
+  if (dtype == MACAI_GDR_F32) {            // the key-split form where it fits (see macai_gdr_state_fwd)
+    DISPATCH_DK_F32(DK, DISPATCH_NW(nw, {
+      if constexpr (StateBwdLds<float, DKC, NWC, 2>::KS_OK)
+        hipLaunchKernelGGL((state_bwd_kernel<float, DKC, NWC, 2>), grid, dim3(64 * (2 * NWC + 1)), 0, st, a);
+      else
+        hipLaunchKernelGGL((state_bwd_kernel<float, DKC, NWC>), grid, block, 0, st, a);
+    }));
   } else {
     DISPATCH_DK(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_bwd_kernel<bf16, DKC, NWC>), grid, block, 0, st, a)));
   }
@@ -3268,9 +3589,14 @@ int macai_gdr_state_pair(const void* W, const float* U, const void* Ke, const vo
   dim3 grid((unsigned)(2 * nfwd));
   dim3 block(64 * (nw + 1));
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == MACAI_GDR_F32) {
-    DISPATCH_DK_F32(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_pair_kernel<float, DKC, NWC>), grid, block, 0, st, af,
-                                                           ab, nfwd)));
+  if (dtype == MACAI_GDR_F32) {            // the key-split form where both passes take it
+    DISPATCH_DK_F32(DK, DISPATCH_NW(nw, {
+      if constexpr (StateFwdLds<float, DKC, false, true, NWC, 2>::KS_OK && StateBwdLds<float, DKC, NWC, 2>::KS_OK)
+        hipLaunchKernelGGL((state_pair_kernel<float, DKC, NWC, 2>), grid, dim3(64 * (2 * NWC + 1)), 0, st, af, ab,
+                           nfwd);
+      else
+        hipLaunchKernelGGL((state_pair_kernel<float, DKC, NWC>), grid, block, 0, st, af, ab, nfwd);
+    }));
   } else {
     DISPATCH_DK(DK, DISPATCH_NW(nw, hipLaunchKernelGGL((state_pair_kernel<bf16, DKC, NWC>), grid, block, 0, st, af, ab,
                                                        nfwd)));

@@ -560,6 +560,26 @@ def test_value_split_changes_no_bits(bf16_state_grad):
     assert all(torch.equal(a, b) for r in runs[1:] for a, b in zip(runs[0], r))
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_float32_key_split_changes_no_bits(D):
+    """The float32 state passes carry a 16-column slice on two waves, each holding half the state's rows, where a
+    workgroup has at most two slices (value splits 4 and 8 at DV = 128), and on one wave a slice otherwise (splits 1,
+    2); both forms add the halves' products in the same order, so every split, both backward modes and the recompute
+    pair in one launch or two give identical bits."""
+    _say(f"case float32 key split bits D={D}")
+    inp = gdr.make_inputs(2, 150, 2, 2, D, 128, torch.float32, s0=True, seed=31)
+    ref = _grads_once(inp, 1, dsT_width=D)
+    old = op.RECOMPUTE_STATES, op.OVERLAP
+    try:
+        for split in (2, 4, 8):
+            for recompute, overlap in ((True, True), (True, False), (False, False)):
+                op.RECOMPUTE_STATES, op.OVERLAP = recompute, overlap
+                got = _grads_once(inp, split, dsT_width=D)
+                assert all(torch.equal(a, b) for a, b in zip(ref, got)), (split, recompute, overlap)
+    finally:
+        op.RECOMPUTE_STATES, op.OVERLAP = old
+
+
 @pytest.mark.parametrize("split", [2, 4])
 def test_overlapped_passes_change_no_bits(split, bf16_state_grad):
     """In the recompute mode (the default) the backward's recompute and reverse passes run in one launch
