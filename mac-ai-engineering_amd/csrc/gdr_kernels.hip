@@ -9,11 +9,12 @@
 //                     (/root/reference/src/macai/gated_delta/_chunked.py:220-313), which keeps A and forms no W/U.
 //   state_fwd_kernel  one wave per 16 value columns of a head-row, sequential over chunks, the fp32 state S in MFMA
 //                     accumulators: Vn = U - W S; O = diag(gamma) Q S + M Vn; S <- exp(G_last) S + K^T diag(e) Vn.
-//                     Optionally stores S_c and Vn for the backward (the recompute pass).  Replaces gdc_fwd
-//                     (_chunked.py:315-659, flags 1 / 8).
+//                     Optionally stores S_c and Vn for the backward (the recompute pass).  Float32 at key widths 64
+//                     and 128 with up to two column slices a workgroup carries each slice on two waves, each holding
+//                     half the state's rows (state_fwd_ks).  Replaces gdc_fwd (_chunked.py:315-659, flags 1 / 8).
 //   state_bwd_kernel  the reverse pass on the same grid, dS in accumulators: dVn = M^T dO + diag(e) K dS;
-//                     dS <- exp(G_last) dS + (diag(gamma) Q)^T dO - W^T dVn; stores dS_{c+1}, dVn; writes dS_0.
-//                     Replaces gdc_bwd_state (_chunked.py:661-903).
+//                     dS <- exp(G_last) dS + (diag(gamma) Q)^T dO - W^T dVn; stores dS_{c+1}, dVn; writes dS_0
+//                     (float32: the key split too, state_bwd_ks).  Replaces gdc_bwd_state (_chunked.py:661-903).
 //   chunk_bwd_kernel  one workgroup per (chunk, head, batch row): dq, dk, dv, dg, dbeta with one writer per element
 //                     (no atomics), dg in the no-cancellation form, the l2norm prologue's backward fused.  Replaces
 //                     gdc_bwd_chunk (_chunked.py:905-1177) and l2n_bwd (_norm.py:44-57).
