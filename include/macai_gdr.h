@@ -51,12 +51,17 @@
 extern "C" {
 #endif
 
-#define MACAI_GDR_ABI_VERSION 12
+#define MACAI_GDR_ABI_VERSION 13
 
 /* dtype codes (the rule takes F32 and BF16; the producers also F16) */
 #define MACAI_GDR_F32 0
 #define MACAI_GDR_BF16 1
 #define MACAI_GDR_F16 2
+/* bf16 tensors in memory with float32 arithmetic and float32 per-chunk operands: taken by macai_gdr_prep (q, k, v
+ * bf16), macai_gdr_state_fwd (o bf16) and macai_gdr_chunk_bwd (q, k, v, dq, dk, dv bf16, dO float32, Hk == H).  The
+ * same bits as the float32 call on the exactly upcast inputs with its bf16 results rounded to nearest even, without
+ * the casts' passes (the reference upcasts bf16 inputs and computes in float32, op.py:276-297). */
+#define MACAI_GDR_BF16_F32 3
 
 /* error codes */
 #define MACAI_GDR_OK 0

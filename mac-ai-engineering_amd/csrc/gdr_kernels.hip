@@ -72,6 +72,7 @@ struct StateFwdArgs {
   int B, T, H, DV, NT;
   int nslice;    // workgroups per head-row
   const int* pack;  // packed rows (see chunk_span) or null
+  int obf;       // o in bf16 from float32 operands (MACAI_GDR_BF16_F32); 0: o in MT
 };
 
 struct StateBwdArgs {
@@ -935,7 +936,11 @@ __device__ __forceinline__ void state_fwd_ks(const StateFwdArgs& a, float* lds, 
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
         const int t = t0 + 16 * (2 * kh + m) + (l & 15);
-        if (t < tend) store4<MT>((MT*)a.o + o_base + (size_t)t * o_pitch + v0 + 4 * j, pO[m]);
+        const size_t at = o_base + (size_t)t * o_pitch + v0 + 4 * j;
+        if (t < tend) {
+          if (a.obf) store4<bf16>((bf16*)a.o + at, pO[m]);
+          else store4<MT>((MT*)a.o + at, pO[m]);
+        }
       }
     }
     lds_barrier();                         // end of chunk c: the next chunk is in, this buffer and the slots are free
@@ -1050,7 +1055,11 @@ __device__ __forceinline__ void state_fwd_body(const StateFwdArgs& a, MT* lds, i
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
       const int t = t0 + 16 * mi + (l & 15);
-      if (t < tend) store4<MT>((MT*)a.o + o_base + (size_t)t * o_pitch + v0 + 4 * j, Ot[mi]);
+      const size_t at = o_base + (size_t)t * o_pitch + v0 + 4 * j;
+      if (t < tend) {
+        if (sizeof(MT) == 4 && a.obf) store4<bf16>((bf16*)a.o + at, Ot[mi]);
+        else store4<MT>((MT*)a.o + at, Ot[mi]);
+      }
     }
   };
   auto store_sc = [&](int c, const f4 (&X)[ND]) {
@@ -1982,7 +1991,9 @@ __device__ __forceinline__ Frag<MT> zero_frag() {
 // TPW (w / 4) .. TPW (w / 4) + TPW - 1 (TPW = 16 / NW: all four with 4 waves, two with 8).  8 waves (two a SIMD) hide
 // each other's global-load latency; at key widths above 128 the fp32 tiles leave LDS for 4 only.
 constexpr int cb32_waves(int DK) { return DK <= 128 ? 8 : 4; }
-template <typename MT, int DK, int DVT>
+// IT: the type of q, k, v and of dq, dk, dv in memory (bf16 with MACAI_GDR_BF16_F32: read exactly, the gradients
+// rounded once from float32); dO and the per-chunk operands are MT.
+template <typename MT, int DK, int DVT, typename IT = MT>
 __global__ void __launch_bounds__(64 * cb32_waves(DK)) chunk_bwd_kernel(ChunkBwdArgs a) {
   static_assert(sizeof(MT) == 4, "bf16 operands take chunk_bwd8_kernel");
   const int DV = DVT ? DVT : a.DV;        // DVT = 0: the value width at run time (a multiple of 32)
@@ -2013,9 +2024,9 @@ __global__ void __launch_bounds__(64 * cb32_waves(DK)) chunk_bwd_kernel(ChunkBwd
   const size_t v_base = ((size_t)b * a.T * H + h) * DV, v_pitch = (size_t)H * DV;
   const size_t s_base = (size_t)b * a.T * H + h;
   const size_t bhc = ((size_t)b * H + h) * NT + c;
-  const MT* q = (const MT*)a.q + qk_base;
-  const MT* k = (const MT*)a.k + qk_base;
-  const MT* v = (const MT*)a.v + v_base;
+  const IT* q = (const IT*)a.q + qk_base;
+  const IT* k = (const IT*)a.k + qk_base;
+  const IT* v = (const IT*)a.v + v_base;
   const MT* dO = (const MT*)a.dO + v_base;
   const float* Scc = a.Sc + bhc * DK * DV;
   const float* dSc = a.dSn + bhc * DK * DV;
@@ -2027,11 +2038,11 @@ __global__ void __launch_bounds__(64 * cb32_waves(DK)) chunk_bwd_kernel(ChunkBwd
   if (w == 0) chunk_scalars(cs, a.g, a.beta, s_base, H, t0, T);
   if (a.l2norm) {
     if constexpr (NW == 8) {               // k's norms on waves 0-3, q's on 4-7 (the same sums as on one wave set)
-      if (w < 4) row_rnorms<MT, DK>(rk, (const MT*)a.k, qk_base, qk_pitch, t0, T, 4, w);
-      else row_rnorms<MT, DK>(rq, (const MT*)a.q, qk_base, qk_pitch, t0, T, 4, w - 4);
+      if (w < 4) row_rnorms<IT, DK>(rk, (const IT*)a.k, qk_base, qk_pitch, t0, T, 4, w);
+      else row_rnorms<IT, DK>(rq, (const IT*)a.q, qk_base, qk_pitch, t0, T, 4, w - 4);
     } else {
-      row_rnorms<MT, DK>(rk, (const MT*)a.k, qk_base, qk_pitch, t0, T, 4);
-      row_rnorms<MT, DK>(rq, (const MT*)a.q, qk_base, qk_pitch, t0, T, 4);
+      row_rnorms<IT, DK>(rk, (const IT*)a.k, qk_base, qk_pitch, t0, T, 4);
+      row_rnorms<IT, DK>(rq, (const IT*)a.q, qk_base, qk_pitch, t0, T, 4);
     }
   } else if (threadIdx.x < C) {
     rk[threadIdx.x] = (int)threadIdx.x < nrows ? 1.f : 0.f;
@@ -2040,10 +2051,10 @@ __global__ void __launch_bounds__(64 * cb32_waves(DK)) chunk_bwd_kernel(ChunkBwd
   __syncthreads();
 
   // operand accessors: raw rows (zero past the sequence end)
-  auto fq = [&](int row0, int k0) { return frag_k_seq<MT, MT>(q, qk_pitch, t0, T, row0, k0, One()); };
-  auto fk = [&](int row0, int k0) { return frag_k_seq<MT, MT>(k, qk_pitch, t0, T, row0, k0, One()); };
-  auto fqrows = [&](int krow0, int col) { return frag_rows<MT, MT>(q, qk_pitch, t0, T, krow0, col, One()); };
-  auto fkrows = [&](int krow0, int col) { return frag_rows<MT, MT>(k, qk_pitch, t0, T, krow0, col, One()); };
+  auto fq = [&](int row0, int k0) { return frag_k_seq<MT, IT>(q, qk_pitch, t0, T, row0, k0, One()); };
+  auto fk = [&](int row0, int k0) { return frag_k_seq<MT, IT>(k, qk_pitch, t0, T, row0, k0, One()); };
+  auto fqrows = [&](int krow0, int col) { return frag_rows<MT, IT>(q, qk_pitch, t0, T, krow0, col, One()); };
+  auto fkrows = [&](int krow0, int col) { return frag_rows<MT, IT>(k, qk_pitch, t0, T, krow0, col, One()); };
   auto fO = [&](int row0, int k0) { return frag_k_seq<MT, MT>(dO, v_pitch, t0, T, row0, k0, One()); };
   auto fVn = [&](int row0, int k0) { return frag_k<MT, MT>(Vnc, DV, row0, k0); };
   auto fdVn = [&](int row0, int k0) { return frag_k<MT, MT>(dVc, DV, row0, k0); };
@@ -2171,7 +2182,7 @@ __global__ void __launch_bounds__(64 * cb32_waves(DK)) chunk_bwd_kernel(ChunkBwd
 #pragma unroll
   for (int kb = 0; kb < DV / 32; ++kb) {
     const Frag<MT> bvn = fVn(16 * cb, 32 * kb);
-    const Frag<MT> bv = frag_k_seq<MT, MT>(v, v_pitch, t0, T, 16 * cb, 32 * kb, One());
+    const Frag<MT> bv = frag_k_seq<MT, IT>(v, v_pitch, t0, T, 16 * cb, 32 * kb, One());
     Frag<MT> fo[TPW], fd[TPW];
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
@@ -2346,7 +2357,7 @@ __global__ void __launch_bounds__(64 * cb32_waves(DK)) chunk_bwd_kernel(ChunkBwd
         for (int r = 0; r < 4; ++r) {
           const int row = 16 * mi + 4 * j + r, t = t0 + row;
           if (t < T) {
-            ((MT*)a.dv)[v_base + (size_t)t * v_pitch + vc] = from_f<MT>(cs.beta[row] * y[r]);
+            ((IT*)a.dv)[v_base + (size_t)t * v_pitch + vc] = from_f<IT>(cs.beta[row] * y[r]);
             pVY[mi][r] = fmaf(to_f(v[(size_t)t * v_pitch + vc]), y[r], pVY[mi][r]);
           }
         }
@@ -2427,8 +2438,8 @@ __global__ void __launch_bounds__(64 * cb32_waves(DK)) chunk_bwd_kernel(ChunkBwd
         } else {
           gq = qs * gq;
         }
-        ((MT*)a.dq)[dqk_base + (size_t)t * dqk_pitch + d] = from_f<MT>(gq);
-        ((MT*)a.dk)[dqk_base + (size_t)t * dqk_pitch + d] = from_f<MT>(gk);
+        ((IT*)a.dq)[dqk_base + (size_t)t * dqk_pitch + d] = from_f<IT>(gq);
+        ((IT*)a.dk)[dqk_base + (size_t)t * dqk_pitch + d] = from_f<IT>(gk);
       }
   }
 }
@@ -3422,6 +3433,8 @@ int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, 
                    int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale, const int32_t* pack,
                    int64_t NT_packed, void* stream) {
   const char* what = "macai_gdr_prep";
+  const bool mixed = dtype == MACAI_GDR_BF16_F32;   // bf16 q, k, v; float32 arithmetic and outputs
+  if (mixed) dtype = MACAI_GDR_F32;
   int64_t NT = 0;
   int rc = check_common(what, pack ? 1 : B, T, H, DK, DV, dtype);
   if (!rc) rc = check_heads(what, H, Hk);
@@ -3440,7 +3453,9 @@ int macai_gdr_prep(const void* q, const void* k, const void* v, const float* g, 
     if (cus > 0 && (int64_t)grid.x * grid.y * grid.z >= 4 * (int64_t)cus) a.stagger = 2 * cus;
   }
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == MACAI_GDR_F32) {
+  if (mixed) {
+    DISPATCH_DK_F32(DK, hipLaunchKernelGGL((prep_kernel<bf16, float, DKC>), grid, dim3(512), 0, st, a));
+  } else if (dtype == MACAI_GDR_F32) {
     DISPATCH_DK_F32(DK, hipLaunchKernelGGL((prep_kernel<float, float, DKC>), grid, dim3(512), 0, st, a));
   } else if (DV <= 128 || DV % 128 == 0) {
     DISPATCH_DK(DK, switch (DV) {
@@ -3471,6 +3486,8 @@ int macai_gdr_state_fwd(const void* W, const float* U, const void* Ke, const flo
                         int64_t DK, int64_t DV, int32_t dtype, int32_t flags, int32_t split, const int32_t* pack,
                         int64_t NT_packed, void* stream) {
   const char* what = "macai_gdr_state_fwd";
+  const bool mixed = dtype == MACAI_GDR_BF16_F32;   // float32 operands, o in bf16
+  if (mixed) dtype = MACAI_GDR_F32;
   int64_t NT = 0;
   int rc = check_common(what, pack ? 1 : B, T, H, DK, DV, dtype);
   if (!rc) rc = pack_chunks(what, pack, NT_packed, B, T, &NT);
@@ -3489,7 +3506,7 @@ int macai_gdr_state_fwd(const void* W, const float* U, const void* Ke, const flo
   int nw, nslice;
   if ((rc = pick_waves(DV, split, what, &nw, &nslice))) return rc;
   StateFwdArgs a{W, U, Ke, GL, Qg, M, s0, o, out ? sT : nullptr, Sc, Vn, (int)B, (int)T, (int)H, (int)DV,
-                 (int)NT, nslice, pack};
+                 (int)NT, nslice, pack, mixed ? 1 : 0};
   const int HR = (int)(B * H);
   dim3 grid((unsigned)(8 * nslice * ((HR + 7) / 8)));
   dim3 block(64 * (nw + 1));   // nw compute waves and the loader wave
@@ -3668,9 +3685,14 @@ int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float
                         int64_t H, int64_t Hk, int64_t DK, int64_t DV, int32_t dtype, int32_t use_l2norm, float q_scale,
                         const int32_t* pack, int64_t NT_packed, void* stream) {
   const char* what = "macai_gdr_chunk_bwd";
+  const bool mixed = dtype == MACAI_GDR_BF16_F32;   // bf16 q, k, v and dq, dk, dv; float32 dO and operands
+  if (mixed) dtype = MACAI_GDR_F32;
   int64_t NT = 0;
   int rc = check_common(what, pack ? 1 : B, T, H, DK, DV, dtype);
   if (!rc) rc = check_heads(what, H, Hk);
+  if (!rc && mixed && Hk != H)
+    return fail(MACAI_GDR_EUNSUP, "%s: bf16 tensors with float32 operands take Hk == H (got Hk = %lld, H = %lld)", what,
+                (long long)Hk, (long long)H);
   if (!rc) rc = pack_chunks(what, pack, NT_packed, B, T, &NT);
   if (rc) return rc;
   if (dtype != MACAI_GDR_F32 && DV != 32 && DV != 64 && DV != 96 && DV != 128)
@@ -3707,7 +3729,13 @@ int macai_gdr_chunk_bwd(const void* q, const void* k, const void* v, const float
     case 128: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 128>), grid, dim3(64 * cb32_waves(DKC)), 0, st, a); break; \
     default: hipLaunchKernelGGL((chunk_bwd_kernel<MT, DKC, 0>), grid, dim3(64 * cb32_waves(DKC)), 0, st, a); break; \
   })
-  if (dtype == MACAI_GDR_F32) {
+  if (mixed) {                             // the value width a template constant at 128 only (fewer instances)
+    DISPATCH_DK_F32(DK, if (DV == 128 && (DKC == 32 || DKC == 64 || DKC == 128 || DKC == 256)) {
+      hipLaunchKernelGGL((chunk_bwd_kernel<float, DKC, 128, bf16>), grid, dim3(64 * cb32_waves(DKC)), 0, st, a);
+    } else {
+      hipLaunchKernelGGL((chunk_bwd_kernel<float, DKC, 0, bf16>), grid, dim3(64 * cb32_waves(DKC)), 0, st, a);
+    })
+  } else if (dtype == MACAI_GDR_F32) {
     LAUNCH_CB(float);
   } else {
     const int cus = xn ? device_cus() : 0;

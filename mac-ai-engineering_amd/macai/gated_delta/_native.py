@@ -12,10 +12,11 @@ LIB_NAME = "libmacai_gdr.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
 F32, BF16, F16 = 0, 1, 2
+BF16_F32 = 3                          # MACAI_GDR_BF16_F32: bf16 tensors, float32 arithmetic (prep, state_fwd, chunk_bwd)
 OK, EINVAL, EUNSUP, ELAUNCH = 0, 1, 2, 3
 STORE_STATES, NO_OUTPUT = 1, 8
 NOALLOC_SCRATCH_BYTES = 128 << 20     # MACAI_GDR_NOALLOC_SCRATCH_BYTES
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _p, _i64, _i32, _f = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
 # name -> argument types (the order of include/macai_gdr.h)

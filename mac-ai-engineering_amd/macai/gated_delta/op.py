@@ -80,6 +80,13 @@ EVENTS = None
 # the step 1.162 against 1.125 ms), so "auto" (the default) pairs the passes for bf16 and fp16 operands only; True
 # pairs them always, False never.  Same bits every way.
 OVERLAP = "auto"
+# MIXED_IO (no counterpart in the reference, which upcasts): a bf16 call computed on the float32 kernels (the routing
+# rules of compute_dtype) hands its bf16 q, k, v to the kernels as they are -- prep and the per-chunk backward read
+# them exactly into float32, the state pass writes o and the per-chunk backward dq, dk, dv in bf16, one rounding each
+# -- instead of upcasting them and casting the results back (8 passes over token tensors a training step, ~70 us at
+# config 1).  The same bits either way; dO is still upcast (the reverse pass reads it as a float32 tile).  Grouped
+# heads (Hk < H) upcast, as their dq, dk are summed over each group in float32 first.
+MIXED_IO = True
 
 
 def pairs_states(dtype) -> bool:
@@ -296,14 +303,16 @@ def _as(x, dt):
     return y if y.data_ptr() % 16 == 0 else y.clone()
 
 
-def _prep(q, k, v, g, beta, l2norm: bool, q_scale: float, r, stream, pack=None, name="prep_fwd"):
+def _prep(q, k, v, g, beta, l2norm: bool, q_scale: float, r, stream, pack=None, name="prep_fwd", mixed=False):
     """The per-chunk operands (row-major, tokens as rows) into the scratch r (addresses from _carve): W, U, diag(e) K^,
     exp(G_last), diag(gamma) Q^, M, and A when r has it (the backward's per-chunk pass needs it).  Per-chunk tensors
-    are [B, H, NT, ...] ([1, H, NT, ...] for packed rows)."""
+    are [B, H, NT, ...] ([1, H, NT, ...] for packed rows).  mixed: bf16 q, k, v read into float32 arithmetic and
+    float32 operands (macai_gdr_prep's MACAI_GDR_BF16_F32)."""
     B, T, H, Hk, DK, DV, NT = _dims(q, v, pack)
     P = N.ptr
+    code = N.BF16_F32 if mixed else N.dtype_code(q.dtype)
     _launch(name, "macai_gdr_prep", P(q), P(k), P(v), P(g), P(beta), r["W"], r["U"], r["Ke"], r["GL"], r["Qg"], r["M"],
-            r["A"], B, T, H, Hk, DK, DV, N.dtype_code(q.dtype), int(l2norm), q_scale, *_pack_args(pack), stream)
+            r["A"], B, T, H, Hk, DK, DV, code, int(l2norm), q_scale, *_pack_args(pack), stream)
 
 
 def segments_for(B: int, T: int, H: int, DV: int, pack=None, save: bool = False) -> int:
@@ -367,21 +376,28 @@ def _forward_segments(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_s
     return o, (None if sTs is None else sTs[nseg - 1:]), None
 
 
-def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, pack=None, keep=False, save=True):
+def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, pack=None, keep=False, save=True,
+             mixed=False):
     """prep, then the state pass with the output: returns (o in q's dtype, sT or None, and for the backward, when
     keep, prep's operands with A and the chunk states Sc, Vn, or, when the forward saves and KEEP_PREP, prep's
     operands with A alone; else None).  A single long row whose forward saves
-    nothing for a backward may run as segments side by side (SEQUENCE_SPLIT)."""
+    nothing for a backward may run as segments side by side (SEQUENCE_SPLIT).  mixed: bf16 q, k, v computed in
+    float32 (float32 per-chunk operands; o written in bf16)."""
     B, T, H, Hk, DK, DV, NT = _dims(q, v, pack)
     nseg = segments_for(B, T, H, DV, pack, save or keep)
     if nseg > 1:
+        if mixed:                          # the segmented passes take one operand type: upcast exactly
+            q, k, v = q.float(), k.float(), v.float()
+            o, sT, r = _forward_segments(q, k, v, g, beta, s0, l2norm, q_scale, want_sT, nseg)
+            return o.to(torch.bfloat16), sT, r
         return _forward_segments(q, k, v, g, beta, s0, l2norm, q_scale, want_sT, nseg)
     Bc = q.shape[0]
     dev, dt = q.device, q.dtype
-    code, stream = N.dtype_code(dt), N.stream_of(q)
+    code, stream = (N.BF16_F32 if mixed else N.dtype_code(dt)), N.stream_of(q)
     keep_prep = save and KEEP_PREP and not keep       # prep's operands with A, without the chunk states
-    r = _carve(dev, (Bc, H, NT, DK, DV, q.element_size(), True, keep or keep_prep, keep, False))
-    _prep(q, k, v, g, beta, l2norm, q_scale, r, stream, pack, "prep_fwd")
+    es = 4 if mixed else q.element_size()
+    r = _carve(dev, (Bc, H, NT, DK, DV, es, True, keep or keep_prep, keep, False))
+    _prep(q, k, v, g, beta, l2norm, q_scale, r, stream, pack, "prep_fwd", mixed)
     o = torch.empty(Bc, T, H, DV, device=dev, dtype=dt)
     sT = torch.empty(B, H, DK, DV, device=dev, dtype=torch.float32) if want_sT else None
     split = split_for(B * H, T, DV)
@@ -392,17 +408,21 @@ def _forward(q, k, v, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, 
     return o, sT, (r if keep or keep_prep else None)
 
 
-def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=None, r=None):
+def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=None, r=None, mixed=False):
     """Recompute (prep, unless the forward kept its operands in `r`, and the state pass storing S_c and Vn, unless the
-    forward kept them too), the reverse state pass, the per-chunk backward.  Returns (dq, dk, dv in q's dtype; dg, dbeta, ds0 float32).  With grouped heads (Hk < H) the per-chunk backward writes dq,
-    dk per value head and macai_gdr_group_sum folds each group (the backward of the repeat the grouped layout
-    replaces)."""
+    forward kept them too), the reverse state pass, the per-chunk backward.  Returns (dq, dk, dv in q's dtype; dg,
+    dbeta, ds0 float32).  With grouped heads (Hk < H) the per-chunk backward writes dq, dk per value head and
+    macai_gdr_group_sum folds each group (the backward of the repeat the grouped layout replaces).  mixed: bf16 q, k,
+    v (and dq, dk, dv) with float32 arithmetic, operands and dO (Hk == H)."""
     B, T, H, Hk, DK, DV, NT = _dims(q, v, pack)
     Bc = q.shape[0]
     dev, dt = q.device, q.dtype
-    code, stream = N.dtype_code(dt), N.stream_of(q)
     f32 = torch.float32
-    es = q.element_size()
+    assert not mixed or (Hk == H and do.dtype == f32), "mixed types: Hk == H and a float32 dO"
+    mt = f32 if mixed else dt              # the operands' type (the state passes run on it)
+    code, stream = N.dtype_code(mt), N.stream_of(q)
+    code_io = N.BF16_F32 if mixed else code   # prep and the per-chunk backward read (and write) q's dtype
+    es = 4 if mixed else q.element_size()
     kept = r is not None and r["Sc"] is not None   # the forward kept prep's operands and the chunk states: only the
     if kept:                                       # reverse pass is left
         g2 = _carve(dev, (Bc, H, NT, DK, DV, es, False, False, False, True))
@@ -410,10 +430,10 @@ def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=
         g2 = _carve(dev, (Bc, H, NT, DK, DV, es, False, False, True, True))
     else:
         r = g2 = _carve(dev, (Bc, H, NT, DK, DV, es, True, True, True, True))
-        _prep(q, k, v, g, beta, l2norm, q_scale, r, stream, pack, "prep_bwd")
+        _prep(q, k, v, g, beta, l2norm, q_scale, r, stream, pack, "prep_bwd", mixed)
     P = N.ptr
     pk = _pack_args(pack)
-    pair = pairs_states(dt) and not kept
+    pair = pairs_states(mt) and not kept
     split = split_for(B * H, T, DV, 2 if pair else 1)
     st = r if kept else g2
     Sc, Vn, dSn, dVn = st["Sc"], st["Vn"], g2["dSn"], g2["dVn"]
@@ -438,7 +458,7 @@ def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=
     dv = torch.empty_like(v)
     dg, dbeta = torch.empty_like(g), torch.empty_like(beta)
     _launch("chunk_bwd", "macai_gdr_chunk_bwd", P(q), P(k), P(v), P(g), P(beta), P(do), r["A"], Sc, dSn, Vn, dVn,
-            P(dqh), P(dkh), P(dv), P(dg), P(dbeta), B, T, H, Hk, DK, DV, code, int(l2norm), q_scale, *pk, stream)
+            P(dqh), P(dkh), P(dv), P(dg), P(dbeta), B, T, H, Hk, DK, DV, code_io, int(l2norm), q_scale, *pk, stream)
     if Hk == H:
         return dqh, dkh, dv, dg, dbeta, ds0
     dq, dk = torch.empty_like(q), torch.empty_like(k)
@@ -447,14 +467,16 @@ def _backward(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=
     return dq, dk, dv, dg, dbeta, ds0
 
 
-def _backward_routed(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=None, r=None):
+def _backward_routed(q, k, v, g, beta, s0, do, dsT, l2norm: bool, q_scale: float, pack=None, r=None, mixed=False):
     """_backward, or -- for bf16 operands with a final-state gradient while BF16_STATE_GRAD is off -- _backward on the
-    float32 kernels: q, k, v and dO upcast exactly, the states recomputed (the forward's kept bf16 operands, if any,
-    are not used), dq, dk, dv cast back to bf16."""
-    if dsT is None or q.dtype != torch.bfloat16 or BF16_STATE_GRAD:
-        return _backward(q, k, v, g, beta, s0, do, dsT, l2norm, q_scale, pack, r)
+    float32 kernels: q, k, v read exactly (mixed types where MIXED_IO and Hk == H, else upcast), dO upcast, the states
+    recomputed (the forward's kept bf16 operands, if any, are not used), dq, dk, dv rounded to bf16."""
+    if mixed or dsT is None or q.dtype != torch.bfloat16 or BF16_STATE_GRAD:
+        return _backward(q, k, v, g, beta, s0, do, dsT, l2norm, q_scale, pack, r, mixed)
     CALLS["bwd f32 for a final-state gradient"] += 1
     f32 = torch.float32
+    if MIXED_IO and k.shape[2] == v.shape[2]:
+        return _backward(q, k, v, g, beta, s0, do.to(f32), dsT, l2norm, q_scale, pack, None, True)
     dq, dk, dv, dg, dbeta, ds0 = _backward(q.to(f32), k.to(f32), v.to(f32), g, beta, s0, do.to(f32), dsT, l2norm,
                                            q_scale, pack)
     return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg, dbeta, ds0
@@ -516,14 +538,15 @@ class _DropIn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, query, key, value, g, beta, s0, l2norm: bool, q_scale: float, want_sT: bool, save: bool,
-                pack=None):
+                pack=None, mixed=False):
         keep = save and not RECOMPUTE_STATES
         with _on(query.device):
-            o, sT, r = _forward(query, key, value, g, beta, s0, l2norm, q_scale, want_sT, pack, keep, save)
+            o, sT, r = _forward(query, key, value, g, beta, s0, l2norm, q_scale, want_sT, pack, keep, save, mixed)
         if save:
             _save(ctx, (query, key, value, g, beta, s0), r)
             ctx.cfg = (l2norm, q_scale, s0 is not None)
             ctx.pack = pack
+            ctx.mixed = mixed
         ctx.set_materialize_grads(False)   # an unused sT's gradient arrives as None, not as zeros (BF16_STATE_GRAD)
         if sT is None:
             return o
@@ -533,12 +556,13 @@ class _DropIn(torch.autograd.Function):
     def backward(ctx, do, dsT=None):
         (query, key, value, g, beta, s0), r = _saved(ctx)
         l2norm, q_scale, has_s0 = ctx.cfg
-        do = torch.zeros_like(value) if do is None else _as(do, value.dtype)
+        ddt = torch.float32 if ctx.mixed else value.dtype
+        do = torch.zeros_like(value, dtype=ddt) if do is None else _as(do, ddt)
         dsT = None if dsT is None else _as(dsT, torch.float32)
         with _on(query.device):
             dq, dk, dv, dg, dbeta, ds0 = _backward_routed(query, key, value, g, beta, s0, do, dsT, l2norm, q_scale,
-                                                          ctx.pack, r)
-        return dq, dk, dv, dg, dbeta, (ds0 if has_s0 else None), None, None, None, None, None
+                                                          ctx.pack, r, ctx.mixed)
+        return dq, dk, dv, dg, dbeta, (ds0 if has_s0 else None), None, None, None, None, None, None
 
 
 def l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
@@ -589,6 +613,8 @@ def plan(B: int, T: int, H: int, DK: int, DV: int, save: bool, Hk: int = None, d
     recompute = save and RECOMPUTE_STATES
     nseg = segments_for(B, T, H, DV, None, save)
     out = {"fwd_chunk": CHUNK, "bwd_chunk": CHUNK, "operands": "bf16" if bf else "f32",
+           # bf16 tensors handed to the float32 kernels as they are (MIXED_IO), not upcast
+           "mixed_io": bool(dtype == torch.bfloat16 and not bf and MIXED_IO and Hk == H),
            "prep": ("prep8" if bf and (DV <= 128 or DV % 128 == 0) else "prep"), "segments": nseg,
            "fused_norm": FUSED_NORM, "recompute": recompute}
     if nseg > 1:
@@ -639,14 +665,18 @@ def chunk_gated_delta_rule(query, key, value, g, beta, chunk_size: int = 64, ini
     if use_qk_l2norm_in_kernel and not FUSED_NORM:
         query, key = eager_prologue(query, key, cdt)
         use_qk_l2norm_in_kernel = False
-    q, k, v = _as(query, cdt), _as(key, cdt), _as(value, cdt)
+    # bf16 tensors computed in float32: read as they are, not upcast (MIXED_IO)
+    mixed = (MIXED_IO and cdt == torch.float32 and query.dtype == key.dtype == value.dtype == torch.bfloat16
+             and key.shape[2] == value.shape[2])
+    tdt = torch.bfloat16 if mixed else cdt
+    q, k, v = _as(query, tdt), _as(key, tdt), _as(value, tdt)
     gf, bf = _as(g, torch.float32), _as(beta, torch.float32)
     s0 = None if initial_state is None else _as(initial_state, torch.float32)
     _check(q, k, v, gf, bf, s0, None if pack is None else pack[2])
     tensors = (q, k, v, gf, bf) + (() if s0 is None else (s0,))
     save = torch.is_grad_enabled() and any(t.requires_grad for t in tensors)
     res = _DropIn.apply(q, k, v, gf, bf, s0, bool(use_qk_l2norm_in_kernel), q.shape[-1] ** -0.5,
-                        bool(output_final_state), save, pack)
+                        bool(output_final_state), save, pack, mixed)
     out, sT = (res, None) if not output_final_state else res
     return (out if out.dtype == dtype else out.to(dtype)), sT
 

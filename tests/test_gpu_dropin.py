@@ -247,6 +247,49 @@ def test_bf16_calls_on_the_float32_kernels(why):
         assert torch.equal(g[n], g2[n].to(g[n].dtype)), n
 
 
+@pytest.mark.parametrize("case", ["f32_switch", "raw_keys", "wide_keys", "short_row", "state_grad", "stored",
+                                  "kept_prep", "segments"])
+def test_mixed_io_changes_no_bits(case, monkeypatch):
+    """A bf16 call computed on the float32 kernels hands its bf16 q, k, v to them as they are (op.MIXED_IO: prep and
+    the per-chunk backward read them exactly, the state pass writes o and the per-chunk backward dq, dk, dv in bf16,
+    one rounding each) instead of upcasting them and casting the results back: the same bits in each route that sends
+    a bf16 call to the float32 kernels (BF16_OPERANDS off, raw keys, key width 256, a short row, a final-state
+    gradient's backward), in both kept modes and through the segmented forward (which upcasts); packed rows in
+    tests/test_gpu_packed.py."""
+    _say(f"case mixed io bits {case}")
+    bf = torch.bfloat16
+    dsT, l2, grads = None, True, True
+    inp = gdr.make_inputs(2, 150, 2, 2, 128, 128, bf, s0=True, seed=41)
+    if case in ("f32_switch", "stored", "kept_prep"):
+        monkeypatch.setattr(op, "BF16_OPERANDS", False)
+        if case == "stored":
+            monkeypatch.setattr(op, "RECOMPUTE_STATES", False)
+        if case == "kept_prep":
+            monkeypatch.setattr(op, "KEEP_PREP", True)
+    elif case == "raw_keys":
+        l2 = False
+    elif case == "wide_keys":
+        inp = gdr.make_inputs(1, 100, 2, 2, 256, 64, bf, s0=True, seed=42)
+    elif case == "short_row":
+        inp = gdr.make_inputs(2, 40, 2, 2, 64, 64, bf, s0=True, seed=43)
+    elif case == "state_grad":
+        dsT = torch.randn(2, 2, 128, 128, generator=torch.Generator().manual_seed(44))
+    elif case == "segments":
+        monkeypatch.setattr(op, "BF16_OPERANDS", False)
+        monkeypatch.setattr(op, "SEQUENCE_SPLIT", 4)
+        inp = gdr.make_inputs(1, 64 * 12 + 5, 2, 2, 128, 128, bf, s0=True, seed=45)
+        grads = False
+    runs = []
+    for mixed in (True, False):
+        monkeypatch.setattr(op, "MIXED_IO", mixed)
+        runs.append(run_dropin(inp, grads=grads, dsT=dsT, l2norm=l2))
+    o, sT, g = runs[0]
+    o2, sT2, g2 = runs[1]
+    assert o.dtype == bf and torch.equal(o, o2) and torch.equal(sT, sT2)
+    for n in g:
+        assert g[n].dtype == g2[n].dtype and torch.equal(g[n], g2[n]), n
+
+
 def test_final_state_gradient_backward_on_the_float32_kernels():
     """A bf16 call whose final state receives a gradient runs its backward on the float32 kernels (op.BF16_STATE_GRAD
     off, the default): on a 150-token draw with an N(0, 1) final-state gradient (seed 209), where the bf16 backward's

@@ -84,6 +84,21 @@ def test_packed_rows_equal_separate_sequences(lens, Hk, Hv, DK, DV, dtype):
         t += L
 
 
+def test_packed_rows_mixed_io_changes_no_bits(monkeypatch):
+    """bf16 packed rows on the float32 kernels (op.BF16_OPERANDS off): the bf16 tensors handed to them as they are
+    (op.MIXED_IO: read exactly, o and dq, dk, dv rounded once) or upcast and the results cast back -- the same bits."""
+    _say("case packed mixed io")
+    monkeypatch.setattr(op, "BF16_OPERANDS", False)
+    row, s0, dsT, cu = _inputs([70, 0, 130, 5], 2, 2, 128, 128, torch.bfloat16, seed=46)
+    runs = []
+    for mixed in (True, False):
+        monkeypatch.setattr(op, "MIXED_IO", mixed)
+        runs.append(_run(row, s0, dsT, cu))
+    (o, sT, g), (o2, sT2, g2) = runs
+    assert o.dtype == torch.bfloat16 and torch.equal(o, o2) and torch.equal(sT, sT2)
+    assert all(a.dtype == b.dtype and torch.equal(a, b) for a, b in zip(g, g2))
+
+
 def test_packed_rows_against_the_oracle():
     """fp32, three sequences: outputs, final states and gradients within the fp32 harness bar of the float64 oracle
     run on each sequence."""

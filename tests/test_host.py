@@ -359,6 +359,11 @@ def test_plan_reports_the_launch_choices():
     assert op.plan(1, 100, 2, 256, 128, save=True)["operands"] == "f32"      # wide keys run the float32 kernels
     assert op.plan(4, 100, 2, 128, 128, save=True)["chunk_bwd"] == "chunk_bwd8"   # fewer chunk-heads than CUs
     assert op.plan(4, 1024, 16, 128, 128, save=True, l2norm=False)["operands"] == "f32"   # keys not normalised
+    # bf16 tensors on the float32 kernels go as they are (op.MIXED_IO) where the key heads are the value heads
+    assert op.plan(4, 1024, 16, 128, 128, save=True, l2norm=False)["mixed_io"]
+    assert not op.plan(4, 1024, 16, 128, 128, save=True, l2norm=False, Hk=4)["mixed_io"]
+    assert not op.plan(4, 1024, 16, 128, 128, save=True)["mixed_io"]                     # bf16 operands
+    assert not op.plan(4, 1024, 16, 128, 128, save=True, dtype=torch.float32)["mixed_io"]
 
 
 def test_unnormalized_keys_take_the_float32_kernels(monkeypatch):
@@ -385,22 +390,23 @@ def test_unnormalized_keys_take_the_float32_kernels(monkeypatch):
 
 
 def test_final_state_gradient_takes_the_float32_backward(monkeypatch):
-    """The backward of a bf16 call that receives a gradient of the final state runs on the float32 kernels (q, k, v
-    and dO upcast, dq, dk, dv cast back) unless op.BF16_STATE_GRAD; without one -- output_final_state=False, or sT
-    left out of the loss, whose gradient then arrives as None -- it keeps the bf16 operands.  Both autograd functions,
-    with the launches replaced by recorders.  Why: the oracle's rounding model of the bf16 path (which the kernels
+    """The backward of a bf16 call that receives a gradient of the final state runs on the float32 kernels unless
+    op.BF16_STATE_GRAD -- q, k, v handed over as bf16 with float32 arithmetic (op.MIXED_IO, key heads = value heads)
+    or upcast, dO upcast, dq, dk, dv in bf16 --; without one -- output_final_state=False, or sT left out of the loss,
+    whose gradient then arrives as None -- it keeps the bf16 operands.  Both autograd functions, with the launches
+    replaced by recorders.  Why: the oracle's rounding model of the bf16 path (which the kernels
     follow to three digits on this draw) over 150 tokens with an N(0, 1) final-state gradient (seed 209) moves dg by
     2.4e-2; the same draw without it stays under 5e-3."""
     import contextlib
     bf, f32 = torch.bfloat16, torch.float32
     seen = []
 
-    def fake_forward(q, k, v, g, beta, s0, l2norm, q_scale, want_sT, pack=None, keep=False, save=True):
+    def fake_forward(q, k, v, g, beta, s0, l2norm, q_scale, want_sT, pack=None, keep=False, save=True, mixed=False):
         B, T, H, DV = v.shape
         return v.new_zeros(v.shape), (torch.zeros(B, H, q.shape[-1], DV) if want_sT else None), None
 
-    def fake_backward(q, k, v, g, beta, s0, do, dsT, l2norm, q_scale, pack=None, r=None):
-        seen.append((q.dtype, k.dtype, v.dtype, do.dtype, dsT is not None))
+    def fake_backward(q, k, v, g, beta, s0, do, dsT, l2norm, q_scale, pack=None, r=None, mixed=False):
+        seen.append((q.dtype, k.dtype, v.dtype, do.dtype, dsT is not None, mixed))
         z = torch.zeros_like
         return z(q), z(k), z(v), z(g), z(beta), None if s0 is None else z(s0)
 
@@ -416,7 +422,7 @@ def test_final_state_gradient_takes_the_float32_backward(monkeypatch):
     def run(fn, with_state_grad):
         seen.clear()
         if fn == "dropin":
-            o, sT = op._DropIn.apply(q, k, v, g, b, None, True, 0.125, True, True, None)
+            o, sT = op._DropIn.apply(q, k, v, g, b, None, True, 0.125, True, True, None, False)
         else:
             o, sT = op.GatedDeltaRule.apply(q, k, v, g, b, s0, True)
         outs = [o, sT] if with_state_grad else [o]
@@ -426,10 +432,13 @@ def test_final_state_gradient_takes_the_float32_backward(monkeypatch):
         return seen[0]
 
     for fn in ("dropin", "rule"):
-        assert run(fn, False) == (bf, bf, bf, bf, False)        # sT out of the loss: its gradient is None
-        assert run(fn, True) == (f32, f32, f32, f32, True)
+        assert run(fn, False) == (bf, bf, bf, bf, False, False)        # sT out of the loss: its gradient is None
+        assert run(fn, True) == (bf, bf, bf, f32, True, True)          # bf16 tensors, float32 arithmetic
+        monkeypatch.setattr(op, "MIXED_IO", False)
+        assert run(fn, True) == (f32, f32, f32, f32, True, False)      # upcast
+        monkeypatch.setattr(op, "MIXED_IO", True)
         monkeypatch.setattr(op, "BF16_STATE_GRAD", True)
-        assert run(fn, True) == (bf, bf, bf, bf, True)
+        assert run(fn, True) == (bf, bf, bf, bf, True, False)
         monkeypatch.setattr(op, "BF16_STATE_GRAD", False)
     assert op.plan(4, 1024, 16, 128, 128, True)["state_grad_operands"] == "f32"
     assert op.plan(4, 1024, 16, 128, 128, True, dtype=f32)["state_grad_operands"] == "f32"
@@ -492,8 +501,8 @@ def test_fused_norm_switch(monkeypatch):
     float32 -- or, with op.BF16_UNNORMALIZED, rounded to bf16."""
     seen = {}
 
-    def fake_apply(q, k, v, g, beta, s0, l2norm, q_scale, want_sT, save, pack):
-        seen.update(q=q, k=k, l2norm=l2norm, q_scale=q_scale)
+    def fake_apply(q, k, v, g, beta, s0, l2norm, q_scale, want_sT, save, pack, mixed):
+        seen.update(q=q, k=k, v=v, l2norm=l2norm, q_scale=q_scale, mixed=mixed)
         return v.new_zeros(v.shape)
 
     monkeypatch.setattr(op, "_check", lambda *a, **kw: None)
@@ -507,8 +516,9 @@ def test_fused_norm_switch(monkeypatch):
     qr = q.clone().requires_grad_(True)
     chunk_gated_delta_rule(qr, k, v, g, b, use_qk_l2norm_in_kernel=True)
     assert seen["l2norm"] is False and seen["q_scale"] == 64 ** -0.5
-    assert seen["q"].dtype == torch.float32 and seen["q"].requires_grad
+    assert seen["q"].dtype == torch.float32 and seen["q"].requires_grad and seen["v"].dtype == torch.float32
     assert torch.equal(seen["q"], op.l2norm(q.float())) and torch.equal(seen["k"], op.l2norm(k.float()))
+    assert not seen["mixed"]                  # the normalised q, k are float32 tensors: v is upcast with them
     assert op.plan(1, 96, 2, 64, 64, True)["operands"] == "f32"
     monkeypatch.setattr(op, "BF16_UNNORMALIZED", True)
     chunk_gated_delta_rule(qr, k, v, g, b, use_qk_l2norm_in_kernel=True)
@@ -517,11 +527,14 @@ def test_fused_norm_switch(monkeypatch):
     assert torch.equal(seen["k"], op.l2norm(k.float()).to(torch.bfloat16))
     monkeypatch.setattr(op, "BF16_UNNORMALIZED", False)
     chunk_gated_delta_rule(q, k, v, g, b, use_qk_l2norm_in_kernel=False)      # nothing to normalise either way;
-    assert seen["l2norm"] is False and seen["q"].dtype == torch.float32       # keys of unknown norm: float32 kernels
-    assert torch.equal(seen["q"], q.float())
+    assert seen["l2norm"] is False and seen["mixed"] and seen["q"] is q       # keys of unknown norm: float32 kernels
+    monkeypatch.setattr(op, "MIXED_IO", False)                               # (bf16 tensors as they are, or upcast)
+    chunk_gated_delta_rule(q, k, v, g, b, use_qk_l2norm_in_kernel=False)
+    assert not seen["mixed"] and torch.equal(seen["q"], q.float()) and seen["q"].dtype == torch.float32
+    monkeypatch.setattr(op, "MIXED_IO", True)
     monkeypatch.setattr(op, "BF16_UNNORMALIZED", True)
     chunk_gated_delta_rule(q, k, v, g, b, use_qk_l2norm_in_kernel=False)
-    assert seen["l2norm"] is False and seen["q"] is q
+    assert seen["l2norm"] is False and seen["q"] is q and not seen["mixed"]
 
 
 def test_gates_and_conv_check_their_arguments():
