@@ -37,10 +37,10 @@ C = 64
 # WRITE_SIZE x 1.000.  Keyed by the config and the mode the profile ran, and stamped with the fingerprint of the
 # kernel sources it was taken on: measured_traffic() reports the figures only while the sources still match.
 TRAFFIC = {
-    (1, "recompute"): {"sources": "f1c7505bb2a12023", "bytes": {
+    (1, "recompute"): {"sources": "dd74fab67b094afc", "bytes": {
         "prep_fwd": 143435701, "state_fwd_out": 110185390, "prep_bwd": 151805154, "state_pair": 313846348,
         "chunk_bwd": 295139609}},
-    (1, "stored"): {"sources": "f1c7505bb2a12023", "bytes": {
+    (1, "stored"): {"sources": "dd74fab67b094afc", "bytes": {
         "prep_fwd": 151848942, "state_fwd_out": 193170556, "state_bwd": 164474805, "chunk_bwd": 295144959}},
 }
 # the rule's kernel sources and the build script that sets their compile flags (paths under mac-ai-engineering_amd/)
@@ -48,13 +48,24 @@ KERNEL_SOURCES = ("csrc/gdr_kernels.hip", "csrc/gdr_common.h", "csrc/gdr_lds.h",
                   "csrc/gdr_chunk_bwd8.hip", "build.py")
 
 
+def kernel_code(text: str) -> str:
+    """C++ source without its comments and blank lines, each line stripped: what the compiler sees, so that an edit
+    of comments or layout alone keeps the fingerprint (no string literal in these sources holds a comment marker)."""
+    import re
+    text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    return "\n".join(line.strip() for line in text.splitlines() if line.strip())
+
+
 def kernel_fingerprint():
-    """sha256 (first 16 hex digits) of the rule's kernel sources and build script, in KERNEL_SOURCES order."""
+    """sha256 (first 16 hex digits) of the rule's kernel sources (their code: kernel_code) and of the build script
+    (whole), in KERNEL_SOURCES order."""
     import hashlib
     h = hashlib.sha256()
     for f in KERNEL_SOURCES:
-        with open(os.path.join(ROOT, "mac-ai-engineering_amd", f), "rb") as fh:
-            h.update(fh.read())
+        with open(os.path.join(ROOT, "mac-ai-engineering_amd", f), encoding="utf-8") as fh:
+            text = fh.read()
+        h.update((text if f.endswith(".py") else kernel_code(text)).encode())
     return h.hexdigest()[:16]
 
 

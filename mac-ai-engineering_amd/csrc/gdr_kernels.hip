@@ -1626,7 +1626,7 @@ struct StateBwdLds {
 // The key-split float32 reverse pass (the compute waves of state_bwd_body with KS = 2; see state_fwd_ks): wave
 // 2 s + h holds rows [h DK / 2, (h + 1) DK / 2) of its slice's dS.  Per chunk each forms its half of diag(e) K^ dS
 // (with M^T dO for row blocks 2 h, 2 h + 1), the pair exchanges the halves through LDS and both take dVn as their sum,
-// then each updates its own rows of dS.  Per wave 216 MFMAs a chunk at DK = 128 against 448 for one wave.
+// then each updates its own rows of dS.  Per wave 208-224 MFMAs a chunk at DK = 128 against 432 for one wave.
 template <int DK, int NW>
 __device__ __forceinline__ void state_bwd_ks(const StateBwdArgs& a, float* lds, int hr, int slice, int cb, int ce,
                                              size_t crow, int tb) {

@@ -85,6 +85,15 @@ def test_cpu_info():
     assert physical >= 1 and allowed >= 1 and share >= 1 and isinstance(model, str)
 
 
+def test_traffic_fingerprint_reads_code_not_comments():
+    """The fingerprint hashes the kernel sources' code: comments, blank lines and indentation do not move it, a change
+    of code does."""
+    code = "int a = 1;  // one\n\n/* a block\n   comment */  int b = a;\n"
+    assert bench.kernel_code(code) == "int a = 1;\nint b = a;"
+    assert bench.kernel_code(code.replace("// one", "// uno")) == bench.kernel_code(code)
+    assert bench.kernel_code(code.replace("a = 1", "a = 2")) != bench.kernel_code(code)
+
+
 def test_traffic_fingerprint_covers_the_build_flags():
     """The traffic stamp's fingerprint includes build.py, whose compile flags (chunk_bwd8's scheduler strategy) change
     the generated code and so its traffic."""
