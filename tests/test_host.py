@@ -108,6 +108,21 @@ def test_abi_rejects_bad_arguments_before_launch():
     assert gs(p, p, Hk=3) == N.EINVAL
     assert gs(p, p, D=12) == N.EUNSUP
     assert gs(p + 4, p) == N.EINVAL and b"aligned" in L.macai_gdr_last_error()
+    # mixed types (bf16 tensors, float32 arithmetic): prep, the state pass and the per-chunk backward take the code --
+    # with it a key width of 256 is valid, so their next check (a null pointer) is what refuses; the per-chunk backward
+    # also refuses grouped heads with it; the other entry points refuse the code itself
+    B3 = N.BF16_F32
+    assert _prep(dtype=B3, DK=256, k=None) == N.EINVAL and b"null" in L.macai_gdr_last_error()
+    assert L.macai_gdr_state_fwd(p, p, p, p, p, None, None, p, None, None, None, 1, 64, 1, 256, 128, B3, 0, 0, None, 0,
+                                 None) == N.EINVAL
+    assert L.macai_gdr_chunk_bwd(*([p] * 15), None, 1, 64, 1, 1, 256, 128, B3, 1, 1.0, None, 0, None) == N.EINVAL
+    assert L.macai_gdr_chunk_bwd(*([p] * 16), 1, 64, 4, 2, 128, 128, B3, 1, 1.0, None, 0, None) == N.EUNSUP
+    assert b"Hk == H" in L.macai_gdr_last_error()
+    assert L.macai_gdr_state_bwd(p, p, p, p, p, p, None, p, p, p, 1, 64, 1, 128, 128, B3, 0, None, 0,
+                                 None) == N.EUNSUP
+    assert L.macai_gdr_state_pair(*([p] * 6), None, p, None, *([p] * 5), 1, 64, 1, 128, 128, B3, 0, None, 0,
+                                  None) == N.EUNSUP
+    assert gs(p, p, dtype=B3) == N.EUNSUP
 
 
 def test_forward_workspace_and_checks():
