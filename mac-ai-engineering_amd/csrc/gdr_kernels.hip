@@ -2053,20 +2053,47 @@ __global__ void __launch_bounds__(64 * cb32_waves(DK)) chunk_bwd_kernel(ChunkBwd
   // operand accessors: raw rows (zero past the sequence end)
   auto fq = [&](int row0, int k0) { return frag_k_seq<MT, IT>(q, qk_pitch, t0, T, row0, k0, One()); };
   auto fk = [&](int row0, int k0) { return frag_k_seq<MT, IT>(k, qk_pitch, t0, T, row0, k0, One()); };
-  auto fqrows = [&](int krow0, int col) { return frag_rows<MT, IT>(q, qk_pitch, t0, T, krow0, col, One()); };
-  auto fkrows = [&](int krow0, int col) { return frag_rows<MT, IT>(k, qk_pitch, t0, T, krow0, col, One()); };
+  // key widths up to 128: the row fragments' loads issued together (frag_rows_eager); 256 keeps frag_rows (it spills)
+  constexpr bool EAGER = DK <= 128;
+  auto fqrows = [&](int krow0, int col) {
+    if constexpr (EAGER) return frag_rows_eager<MT, IT>(q, qk_pitch, t0, T, krow0, col, One());
+    else return frag_rows<MT, IT>(q, qk_pitch, t0, T, krow0, col, One());
+  };
+  auto fkrows = [&](int krow0, int col) {
+    if constexpr (EAGER) return frag_rows_eager<MT, IT>(k, qk_pitch, t0, T, krow0, col, One());
+    else return frag_rows<MT, IT>(k, qk_pitch, t0, T, krow0, col, One());
+  };
   auto fO = [&](int row0, int k0) { return frag_k_seq<MT, MT>(dO, v_pitch, t0, T, row0, k0, One()); };
   auto fVn = [&](int row0, int k0) { return frag_k<MT, MT>(Vnc, DV, row0, k0); };
   auto fdVn = [&](int row0, int k0) { return frag_k<MT, MT>(dVc, DV, row0, k0); };
-  auto fdVnrows = [&](int krow0, int col) { return frag_rows<MT, MT>(dVc, DV, 0, C, krow0, col, One()); };
+  auto fdVnrows = [&](int krow0, int col) {
+    if constexpr (EAGER) return frag_rows_eager<MT, MT>(dVc, DV, 0, C, krow0, col, One());
+    else return frag_rows<MT, MT>(dVc, DV, 0, C, krow0, col, One());
+  };
   // A^T rows row0.. (A operand): column row0 + l % 16 of A, k over A's rows
-  auto fAt = [&](int row0, int k0) { return frag_rows<MT, MT>(Ac, C, 0, C, k0, row0 + (l & 15), One()); };
-  // raw q / k at (chunk row, key column) times the row's inverse norm: the unit-norm direction (0 past the end)
+  auto fAt = [&](int row0, int k0) {
+    if constexpr (EAGER) return frag_rows_eager<MT, MT>(Ac, C, 0, C, k0, row0 + (l & 15), One());
+    else return frag_rows<MT, MT>(Ac, C, 0, C, k0, row0 + (l & 15), One());
+  };
+  // raw q / k at (chunk row, key column) times the row's inverse norm: the unit-norm direction (zero past the end).
+  // EAGER: the load unconditional (a row past the end reads the last row) and the mask on the multiplier, so the
+  // compiler cannot sink the load into a per-row branch and wait for it there (rows past the end only ever feed
+  // their own masked partial sums).
   auto xq = [&](int row, int d) -> float {
-    return (t0 + row < T) ? to_f(q[(size_t)(t0 + row) * qk_pitch + d]) * rq[row] : 0.f;
+    if constexpr (EAGER) {
+      const float x = to_f(q[(size_t)(t0 + row < T ? t0 + row : T - 1) * qk_pitch + d]);
+      return x * ((t0 + row < T) ? rq[row] : 0.f);
+    } else {
+      return (t0 + row < T) ? to_f(q[(size_t)(t0 + row) * qk_pitch + d]) * rq[row] : 0.f;
+    }
   };
   auto xk = [&](int row, int d) -> float {
-    return (t0 + row < T) ? to_f(k[(size_t)(t0 + row) * qk_pitch + d]) * rk[row] : 0.f;
+    if constexpr (EAGER) {
+      const float x = to_f(k[(size_t)(t0 + row < T ? t0 + row : T - 1) * qk_pitch + d]);
+      return x * ((t0 + row < T) ? rk[row] : 0.f);
+    } else {
+      return (t0 + row < T) ? to_f(k[(size_t)(t0 + row) * qk_pitch + d]) * rk[row] : 0.f;
+    }
   };
 
   // ---- B: products with the chunk states; wave w owns key-column blocks w, w + NW, ...
@@ -2356,9 +2383,11 @@ __global__ void __launch_bounds__(64 * cb32_waves(DK)) chunk_bwd_kernel(ChunkBwd
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int row = 16 * mi + 4 * j + r, t = t0 + row;
+          // EAGER: loaded outside the branch (the last row past the end)
+          const float vv = EAGER ? to_f(v[(size_t)(t < T ? t : T - 1) * v_pitch + vc]) : 0.f;
           if (t < T) {
             ((IT*)a.dv)[v_base + (size_t)t * v_pitch + vc] = from_f<IT>(cs.beta[row] * y[r]);
-            pVY[mi][r] = fmaf(to_f(v[(size_t)t * v_pitch + vc]), y[r], pVY[mi][r]);
+            pVY[mi][r] = fmaf(EAGER ? vv : to_f(v[(size_t)t * v_pitch + vc]), y[r], pVY[mi][r]);
           }
         }
       }
