@@ -219,32 +219,43 @@ __global__ void __launch_bounds__(512) prep_kernel(PrepArgs a) {
     if (ps) __syncthreads();               // the previous pass's products are done with the tiles
     MT* Ke = (MT*)a.Ke + bhc * C * DK + cb;
     MT* Qg = (MT*)a.Qg + bhc * C * DK + cb;
-    constexpr int PR = DKS / 8;
-    for (int i = threadIdx.x; i < C * PR; i += blockDim.x) {
-      const int r = i / PR, c8 = (i - r * PR) * 8, t = t0 + r;
-      float x[8], y[8];
-      if (t < T) load8(k + (size_t)t * qk_pitch + cb + c8, x);
-      else
+    // A thread's (row, 8 columns) pieces of the pass: every load issued first, unconditionally (a row past the end
+    // reads row T - 1, the chunk having t0 < T) and masked on the row's multiplier after -- in a per-row branch each
+    // load was waited for alone.
+    constexpr int PR = DKS / 8, NIT = (C * PR + 511) / 512;   // 512 threads (the launch's)
+    float lk[NIT][8], lq[NIT][8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        y[e] = x[e] * rk[r];
-        x[e] = y[e] * cs.e[r];
+    for (int it = 0; it < NIT; ++it) {
+      const int i = (int)threadIdx.x + 512 * it;
+      if (i < C * PR) {
+        const int r = i / PR, c8 = (i - r * PR) * 8, t = (t0 + r < T) ? t0 + r : T - 1;
+        load8(k + (size_t)t * qk_pitch + cb + c8, lk[it]);
+        load8(q + (size_t)t * qk_pitch + cb + c8, lq[it]);
       }
-      store8(sK + r * KP + c8, y);
-      store8(Ke + r * DK + c8, x);
-      if (t < T) load8(q + (size_t)t * qk_pitch + cb + c8, x);
-      else
+    }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = 0.f;
+    for (int it = 0; it < NIT; ++it) {
+      const int i = (int)threadIdx.x + 512 * it;
+      if (i < C * PR) {
+        const int r = i / PR, c8 = (i - r * PR) * 8;
+        const bool in = t0 + r < T;
+        const float mk = in ? rk[r] : 0.f, mq = in ? rq[r] * qs : 0.f;
+        float x[8], y[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        y[e] = x[e] * (rq[r] * qs);
-        x[e] = y[e] * cs.gam[r];
+        for (int e = 0; e < 8; ++e) {
+          y[e] = lk[it][e] * mk;
+          x[e] = y[e] * cs.e[r];
+        }
+        store8(sK + r * KP + c8, y);
+        store8(Ke + r * DK + c8, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          y[e] = lq[it][e] * mq;
+          x[e] = y[e] * cs.gam[r];
+        }
+        store8(sQ + r * KP + c8, y);
+        store8(Qg + r * DK + c8, x);
       }
-      store8(sQ + r * KP + c8, y);
-      store8(Qg + r * DK + c8, x);
     }
     __syncthreads();
     const int mi = rb;
